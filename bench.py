@@ -1,0 +1,256 @@
+"""Benchmark of pico's MI355X backend (one JSON line on stdout).
+
+Workload: fp32 GEMM at M=N=K=4096, entries U[-1,1).
+One step = the three products of one matmul's forward and backward
+(C = A.B, dA = dC.B^T, dB = A^T.dC), i.e. 3 x 2n^3 FLOP, inputs resident in HBM.
+`value` is the achieved TFLOP/s over the timed steps.
+
+Also reported, outside the timed region:
+  roofline      the GEMM kernel's FLOP per launch / its mean launch time
+                (HIP events on the launch stream) against 157.3 TFLOP/s
+  sweep         TFLOP/s for n in {512..8192} and each layout
+  row_kernels   RMSNorm / SwiGLU / softmax-CE at the config-3 shapes: GB/s of
+                algorithmic traffic against 8 TB/s (buffer sets rotated past
+                the 256 MB last-level cache)
+  cpu_baseline  pico's own AVX+FMA matmul (threaded, 8 workers) on the host,
+                compiled from the reference's sources when present, else this
+                repo's restatement of it
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_FP32_PEAK = 157.3e12
+HBM_PEAK = 8.0e12
+
+
+def _events_time(fn, reps, warmup):
+    """mean ms per call of fn() measured with events on the current stream"""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(reps):
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    times.sort()
+    return sum(times) / len(times), times[len(times) // 2]
+
+
+def gemm_section(args, torch, K):
+    n = args.n
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(20261201)
+    A = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+    B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+    dC = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+    C = torch.empty(n, n, device=dev)
+    dA = torch.empty(n, n, device=dev)
+    dB = torch.empty(n, n, device=dev)
+
+    def step():
+        K.gemm("N", "N", A, B, C)
+        K.gemm("N", "T", dC, B, dA)
+        K.gemm("T", "N", A, dC, dB)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps, synchronised on both sides
+    t0 = time.perf_counter()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    for i in range(args.steps):
+        ev[i][0].record()
+        K.gemm("N", "N", A, B, C)
+        ev[i][1].record()
+        K.gemm("N", "T", dC, B, dA)
+        K.gemm("T", "N", A, dC, dB)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    nn_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+    flop_step = 3 * 2.0 * n ** 3
+    return {
+        "wall_s": wall,
+        "value": flop_step * args.steps / wall / 1e12,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "nn_kernel_ms": nn_ms,
+        "flop_per_launch": 2.0 * n ** 3,
+    }
+
+
+def sweep_section(torch, K, sizes):
+    dev = torch.device("cuda:0")
+    out = {}
+    for n in sizes:
+        gen = torch.Generator(device=dev).manual_seed(n)
+        A = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        C = torch.empty(n, n, device=dev)
+        reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
+        row = {}
+        for ta, tb in (("N", "N"), ("N", "T"), ("T", "N")):
+            mean_ms, _ = _events_time(lambda: K.gemm(ta, tb, A, B, C), reps, 2)
+            row[ta + tb] = round(2.0 * n ** 3 / (mean_ms * 1e-3) / 1e12, 2)
+        out[str(n)] = row
+        del A, B, C
+    return out
+
+
+def rows_section(torch, K):
+    """config-3 row kernels; 4 rotating buffer sets (> 256 MB MALL)"""
+    dev = torch.device("cuda:0")
+    res = {}
+    sets = 4
+
+    def bw(name, nbytes, fns):
+        i = [0]
+
+        def call():
+            fns[i[0] % len(fns)]()
+            i[0] += 1
+
+        mean_ms, med_ms = _events_time(call, 20, len(fns))
+        gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        res[name] = {"us": round(mean_ms * 1e3, 1), "GB/s": round(gbs, 1),
+                     "frac": round(gbs * 1e9 / HBM_PEAK, 3)}
+
+    # RMSNorm 8192 x 4096
+    R, Cc = 8192, 4096
+    xs = [torch.randn(R, Cc, device=dev) for _ in range(sets)]
+    ys = [torch.empty(R, Cc, device=dev) for _ in range(sets)]
+    g = 1 + 0.02 * torch.randn(Cc, device=dev)
+    rs = [torch.empty(R, device=dev) for _ in range(sets)]
+    bw("rmsnorm_fwd", 2 * R * Cc * 4,
+       [lambda j=j: K.rmsnorm_fwd(xs[j], g, ys[j], rs[j], 1e-6) for j in range(sets)])
+    dgs = torch.empty(Cc, device=dev)
+    ws = torch.empty(K.rmsnorm_bwd_workspace(R, Cc) // 4, device=dev)
+    bw("rmsnorm_bwd", 3 * R * Cc * 4,
+       [lambda j=j: K.rmsnorm_bwd(xs[j], g, rs[j], ys[(j + 1) % sets], ys[(j + 2) % sets], dgs, ws)
+        for j in range(sets)])
+    del xs, ys, rs
+    # SwiGLU 8192 x 11008
+    R, F = 8192, 11008
+    a = [torch.randn(R, F, device=dev) for _ in range(sets)]
+    u = [torch.randn(R, F, device=dev) for _ in range(sets)]
+    h = [torch.empty(R, F, device=dev) for _ in range(sets)]
+    bw("swiglu_fwd", 3 * R * F * 4,
+       [lambda j=j: K.swiglu_fwd(a[j], u[j], h[j]) for j in range(sets)])
+    da = [torch.empty(R, F, device=dev) for _ in range(2)]
+    bw("swiglu_bwd", 5 * R * F * 4,
+       [lambda j=j: K.swiglu_bwd(a[j], u[j], h[j], da[0], da[1]) for j in range(sets)])
+    del a, u, h, da
+    # softmax-CE 8192 x 32000, fused forward + backward
+    R, V = 8192, 32000
+    zs = [torch.randn(R, V, device=dev) * 2 for _ in range(2)]
+    lab = torch.randint(0, V, (R,), device=dev, dtype=torch.int32)
+    loss = torch.empty(R, device=dev)
+    dz = [torch.empty(R, V, device=dev) for _ in range(2)]
+    bw("xent_fwd_bwd", 2 * R * V * 4,
+       [lambda j=j: K.xent_fwd_bwd(zs[j], lab, loss, dz[j], scale=1.0 / R) for j in range(2)])
+    return res
+
+
+def cpu_baseline(n):
+    """pico's AVX matmul on the host: warmup 1, median of 3 (bench_matmul_large.c:16-18)"""
+    import ctypes
+
+    import numpy as np
+
+    from oracle import oracle as O
+
+    A = O.uniform(n * n, 1).reshape(n, n)
+    B = O.uniform(n * n, 2).reshape(n, n)
+    if O.ref_available():
+        kind = "reference"
+        R = O.ref()
+
+        def run():
+            C = np.zeros((n, n), np.float32)
+            R.picoref_matmul_avx(ctypes.c_int(n), ctypes.c_int(n), ctypes.c_int(n), O.p(A), O.p(B),
+                                 O.p(C))
+    else:
+        kind = "port"
+        O.set_threads(8)
+
+        def run():
+            O.matmul_avx(A, B)
+
+    run()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[1]
+    return {"value": round(2.0 * n ** 3 / t / 1e12, 4), "unit": "TFLOP/s", "cores": 8,
+            "kind": kind, "host_cpus": os.cpu_count(),
+            "sample": f"one fp32 matmul {n}^3 (forward A.B), pico's AVX+FMA kernel on its 8-worker "
+                      f"pool, median of 3 after 1 warmup, {t:.2f} s each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--n", type=int, default=4096)
+    ap.add_argument("--sections", default="sweep,rows,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU data-parallel path is design-only)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from pico_amd import kernels as K
+
+    sections = set(s for s in args.sections.split(",") if s)
+    info = K.device_info()
+    g = gemm_section(args, torch, K)
+    achieved = g["flop_per_launch"] / (g["nn_kernel_ms"] * 1e-3)
+    line = {
+        "metric": "fp32 GEMM TFLOP/s (matmul fwd + both bwd products, 4096^3)",
+        "value": round(g["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic U[-1,1) operands, resident in HBM",
+        "config": {"workload": f"fp32 GEMM sweep point M=N=K={args.n}: A.B, dC.B^T, A^T.dC",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2),
+                     "peak": MFMA_FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_FP32_PEAK, 4), "traffic": None,
+                     "kernel": "gemm_f32_kernel<N,N> (one launch = 2n^3 FLOP)",
+                     "kernel_ms": round(g["nn_kernel_ms"], 4)},
+        "device": info,
+    }
+    if "sweep" in sections:
+        line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
+    if "rows" in sections:
+        line["row_kernels"] = rows_section(torch, K)
+    if "cpu" in sections:
+        line["cpu_baseline"] = cpu_baseline(args.n)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

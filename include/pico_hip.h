@@ -1,0 +1,176 @@
+/*
+ * include/pico_hip.h -- the C-ABI launcher layer of pico's MI355X (gfx950) backend.
+ *
+ * Every entry point takes raw DEVICE pointers plus sizes and layout scalars,
+ * launches hand-written HIP kernels on the given stream, allocates nothing,
+ * and returns a status: 0 on success, PK_EINVAL (-1) for arguments it refuses
+ * (with a message available from pk_last_error()), otherwise the hipError_t
+ * value of the failed launch.  Nothing here synchronises the stream.
+ *
+ * These are the GPU twins of pico's CPU kernel seam (src/kernels/cpu_kernels.h
+ * :13-100) and of the commented-out pico_*_gpu stubs in src/ops.c:42-44,86-88,
+ * 130-132; pico's op layer and backward hooks call them when a tensor's
+ * backend is GPU.  Matrices are row-major, as pico's tensors are.
+ *
+ * "flags" arguments: bit 0 (PK_ACCUM) makes the first output accumulate
+ * (out += result, the += contract of pico's backward hooks, src/autograd.h
+ * :25-29); bit 1 (PK_ACCUM2) does the same for a second output.  Without the
+ * bit the output is overwritten and never read.
+ */
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* pk_stream_t; /* a hipStream_t; NULL is the null stream */
+
+#define PK_OK 0
+#define PK_EINVAL (-1)
+
+#define PK_ACCUM 1
+#define PK_ACCUM2 2
+
+/* ---- runtime ---------------------------------------------------------- */
+const char* pk_last_error(void);
+/* device properties of the current device: CU count, peak clock kHz, gcnArch name */
+int pk_device_info(int* cu_count, int* clock_khz, char* arch, int arch_len);
+
+/* ---- GEMM --------------------------------------------------------------
+ * C[M,N] = alpha * op(A) . op(B) + beta * C   (beta == 0: C is not read)
+ * op(A) is [M,K]: ta 'N' -> A stored [M,K] (lda >= K); ta 'T' -> A stored [K,M] (lda >= M)
+ * op(B) is [K,N]: tb 'N' -> B stored [K,N] (ldb >= N); tb 'T' -> B stored [N,K] (ldb >= K)
+ * Replaces pico_matmul_cpu (src/kernels/cpu_kernels.h:46-55, forward C = A.B with
+ * out zeroed, i.e. beta = 0) and both loops of pico_matmul_backward
+ * (src/autograd.h:96-130: dA += dC.B^T is ('N','T', beta 1), dB += A^T.dC is
+ * ('T','N', beta 1)); a pico_transpose_2d view (src/tensor.c:230-244) maps to 'T'. */
+int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                pk_stream_t stream);
+
+/* Batched form: batch index z = outer*inner_count + inner; operand X of batch z
+ * starts at X + outer*sX_outer + inner*sX_inner.  'causal' restricts work for
+ * attention-shaped products (no reference counterpart: pico's matmul is 2-D
+ * only, src/ops.c:150):
+ *   0 dense
+ *   1 only C[r,c] with c <= r is produced (tiles wholly above the diagonal are skipped)
+ *   2 op(A)[r,k] is zero for k > r (the k loop stops at the tile's last row)
+ *   3 op(A)[r,k] is zero for k < r (the k loop starts at the tile's first row) */
+int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                        const float* A, int64_t lda, int64_t sA_outer, int64_t sA_inner,
+                        const float* B, int64_t ldb, int64_t sB_outer, int64_t sB_inner,
+                        float beta, float* C, int64_t ldc, int64_t sC_outer, int64_t sC_inner,
+                        int64_t batch, int64_t inner_count, int causal, pk_stream_t stream);
+
+/* ---- elementwise (pico ops.c:12-142, autograd.h:53-94) -----------------
+ * op: 0 add, 1 sub, 2 mul.  ndim <= 8.  a_strides / b_strides are each
+ * operand's element strides mapped onto the output's dims (0 on a broadcast
+ * dim), the map pico's map_index computes (src/tensor.h:122-138).  out is
+ * contiguous with shape out_shape. */
+int pk_binary_f32(int op, int ndim, const int64_t* out_shape, const int64_t* a_strides,
+                  const int64_t* b_strides, const float* a, const float* b, float* out,
+                  pk_stream_t stream);
+/* gradient of one operand: gx[j] (+)= sum over output elements i that read
+ * x[j] of  g[i]            (add; or sub for operand a)
+ *          -g[i]           (sub, operand b: which = 1)
+ *          g[i] * other[i] (mul)
+ * x_shape/x_ndim are the operand's own shape (gx is contiguous in it),
+ * x_strides / other_strides are mapped onto the output dims as above. */
+int pk_binary_bwd_f32(int op, int which, int ndim, const int64_t* out_shape,
+                      const int64_t* x_strides, const int64_t* other_strides, int64_t x_numel,
+                      const float* gout, const float* other, float* gx, int flags,
+                      pk_stream_t stream);
+/* unary op: 0 sqrt, 1 sin, 2 cos, 3 tan, 4 tanh, 5 log (src/kernels/cpu/cpu_scalar.h:32-37) */
+int pk_unary_f32(int op, int64_t n, const float* x, float* y, pk_stream_t stream);
+/* gx (+)= local derivative x gy, with the reference's expressions
+ * (src/autograd.h:132-176, including its tanh form g - y*y) */
+int pk_unary_bwd_f32(int op, int64_t n, const float* x, const float* y, const float* gy,
+                     float* gx, int flags, pk_stream_t stream);
+/* y = max(x, 0) (NaN -> 0); gx (+)= gy * (y > 0)   (src/act/activations.c:16-18,
+ * src/act/autograd.h:9-17) */
+int pk_relu_f32(int64_t n, const float* x, float* y, pk_stream_t stream);
+int pk_relu_bwd_f32(int64_t n, const float* y, const float* gy, float* gx, int flags,
+                    pk_stream_t stream);
+int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream);
+/* y (+)= alpha * (*alpha_dev if non-NULL) * x */
+int pk_axpy_f32(int64_t n, float alpha, const float* alpha_dev, const float* x, float* y,
+                int flags, pk_stream_t stream);
+/* out[0] (+)= scale * sum(x) */
+int pk_reduce_sum_f32(int64_t n, const float* x, float scale, float* out, int flags,
+                      pk_stream_t stream);
+
+/* ---- optimizers ---------------------------------------------------------
+ * SGD: p -= lr*g, product rounded first (src/optim/SGD.c:29-37).
+ * AdamW: decoupled decay then bias-corrected Adam (no reference code; the
+ * reference's optim.h:19-23 only names Adam).  g == NULL means a zero gradient. */
+int pk_sgd_f32(int64_t n, float lr, float* p, const float* g, pk_stream_t stream);
+int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps, float weight_decay,
+                 int step, float* p, const float* g, float* m, float* v, pk_stream_t stream);
+
+/* ---- fused row kernels (no reference code; planned at todo.md:95) --------
+ * softmax cross-entropy, one pass over each row of logits [R,V] (row stride ldz):
+ *   loss_rows[r] = logsumexp(z_r) - z_r[labels[r]]        (if loss_rows != NULL)
+ *   dlogits[r,:] (+)= scale * (softmax(z_r) - onehot(y_r)) (if dlogits != NULL)
+ * A label outside [0,V) gives NaN loss and a zero gradient row. */
+int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, int64_t ldz,
+                        const int32_t* labels, float* loss_rows, float* dlogits, int64_t ldd,
+                        float scale, int flags, pk_stream_t stream);
+/* idx[r] = argmax_j x[r,j]: first maximum wins; a NaN is the maximum (first NaN wins) */
+int pk_argmax_f32(int64_t R, int64_t V, const float* x, int64_t ldx, int32_t* idx,
+                  pk_stream_t stream);
+/* RMSNorm over rows of x [R,C]: y = x * rstd * g, rstd = (mean(x^2) + eps)^-1/2 */
+int pk_rmsnorm_fwd_f32(int64_t R, int64_t C, float eps, const float* x, const float* g, float* y,
+                       float* rstd, pk_stream_t stream);
+/* dx (+)= rstd*(g*dy) - x*rstd^3*mean(g*dy*x)   (flags bit 0)
+ * dg (+)= sum_r dy*x*rstd                       (flags bit 1)
+ * needs pk_rmsnorm_bwd_workspace(R, C) bytes of device workspace */
+size_t pk_rmsnorm_bwd_workspace(int64_t R, int64_t C);
+int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const float* g, const float* rstd,
+                       const float* dy, float* dx, float* dg, int flags, void* workspace,
+                       size_t workspace_bytes, pk_stream_t stream);
+/* SwiGLU on [R,F] gate/up pairs (row strides lda, ldu, ldh): h = silu(a) * u */
+int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const float* u,
+                      int64_t ldu, float* h, int64_t ldh, pk_stream_t stream);
+/* da (+)= dh*u*s*(1 + a*(1-s)) (bit 0), du (+)= dh*a*s (bit 1), s = sigmoid(a);
+ * da and du share the row stride ldd */
+int pk_swiglu_bwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const float* u,
+                      int64_t ldu, const float* dh, int64_t ldh, float* da, float* du,
+                      int64_t ldd, int flags, pk_stream_t stream);
+
+/* ---- causal attention ----------------------------------------------------
+ * q, k, v, o are token-major [B*T, H*hd]; head h of batch b owns columns
+ * h*hd..h*hd+hd-1 of rows b*T..b*T+T-1.  lse is [B*H, T] (log-sum-exp of each
+ * score row, kept for the backward).  P is a [B*H, T, T] buffer the forward
+ * fills with the probabilities (zero above the diagonal) and the backward
+ * reads; dP_ws is a [B*H, T, T] scratch buffer for the backward.
+ * scale is normally 1/sqrt(hd). */
+int pk_attn_causal_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                           const float* q, const float* k, const float* v, float* o, float* lse,
+                           float* P, pk_stream_t stream);
+/* dq, dk, dv (+)= gradients; flags bit 0 accumulates all three */
+int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                           const float* q, const float* k, const float* v, const float* P,
+                           const float* dout, float* dq, float* dk, float* dv, float* dP_ws,
+                           int flags, pk_stream_t stream);
+/* the two row kernels inside the chain, exposed for tests:
+ * P = softmax(scale*S) over j <= i, zero for j > i, lse per row (P may alias S) */
+int pk_causal_softmax_fwd_f32(int64_t BH, int64_t T, float scale, const float* S, float* P,
+                              float* lse, pk_stream_t stream);
+/* dS = P * (dP - rowsum(dP*P)) for j <= i, zero above (dS may alias dP) */
+int pk_causal_softmax_bwd_f32(int64_t BH, int64_t T, const float* P, const float* dP, float* dS,
+                              pk_stream_t stream);
+
+/* ---- embedding -------------------------------------------------------------
+ * out[i,:] = table[ids[i],:]; dtable[ids[i],:] += dout[i,:] (order of the adds
+ * is unspecified).  An id outside [0,vocab) reads as a zero row and adds nothing. */
+int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids, const float* table,
+                     float* out, pk_stream_t stream);
+int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids, const float* dout,
+                     float* dtable, pk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,446 @@
+// pico_amd/csrc/elementwise.hip -- broadcast binary ops and their gradients,
+// unary math, relu, fill, axpy, sum, SGD, AdamW, embedding gather/scatter.
+//
+// Everything here is HBM-bound streaming: contiguous operands go through
+// 128-bit loads and stores, grid-stride loops sized to a few waves per CU.
+// Floating-point contraction is off in this file so each a*b+c rounds twice,
+// as pico's C11 build does (src/kernels/cpu/cpu_scalar.h, src/optim/SGD.c);
+// add/sub/mul, their gradients, relu and SGD are then bit-identical to the
+// reference's CPU results.
+#include <math.h>
+
+#include "pk_common.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kMaxDims = 8;
+constexpr int NT = 256;
+
+struct Strides {
+    int ndim;
+    int64_t shape[kMaxDims];
+    int64_t sa[kMaxDims];  // first operand's strides over the output dims
+    int64_t sb[kMaxDims];  // second operand's strides over the output dims
+};
+
+__device__ __forceinline__ float bin_apply(int op, float x, float y) {
+    return op == 0 ? x + y : op == 1 ? x - y : x * y;
+}
+
+// out[i] = a[ia] op b[ib], the broadcast index map of pico's map_index
+__global__ void binary_general(int op, Strides s, int64_t n, const float* __restrict__ a,
+                               const float* __restrict__ b, float* __restrict__ out) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t rem = i, ia = 0, ib = 0;
+        for(int d = s.ndim - 1; d >= 0; --d) {
+            const int64_t c = rem % s.shape[d];
+            rem /= s.shape[d];
+            ia += c * s.sa[d];
+            ib += c * s.sb[d];
+        }
+        out[i] = bin_apply(op, a[ia], b[ib]);
+    }
+}
+
+__global__ void binary_same4(int op, int64_t n4, const f32x4* __restrict__ a,
+                             const f32x4* __restrict__ b, f32x4* __restrict__ out) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const f32x4 x = a[i], y = b[i];
+        f32x4 r;
+        r[0] = bin_apply(op, x[0], y[0]);
+        r[1] = bin_apply(op, x[1], y[1]);
+        r[2] = bin_apply(op, x[2], y[2]);
+        r[3] = bin_apply(op, x[3], y[3]);
+        out[i] = r;
+    }
+}
+
+// Gradient of one operand x.  The output dims split into "kept" dims (x has
+// them) and "reduced" dims (x is broadcast there).  Thread j owns gx[j] and
+// walks the reduced dims in increasing flat order, adding one term at a time
+// to the running value -- the same order and rounding as the reference's
+// single pass (src/autograd.h:53-94).
+struct BwdDesc {
+    int nk, nr;
+    int64_t kshape[kMaxDims], kout[kMaxDims], koth[kMaxDims];
+    int64_t rshape[kMaxDims], rout[kMaxDims], roth[kMaxDims];
+    int64_t red_numel;
+};
+
+__device__ __forceinline__ float grad_term(int op, int which, float g, float other) {
+    if(op == 2) return g * other;
+    return (op == 1 && which == 1) ? -g : g;
+}
+
+__global__ void binary_bwd_reduce(int op, int which, BwdDesc d, int64_t xn,
+                                  const float* __restrict__ gout, const float* __restrict__ other,
+                                  float* __restrict__ gx, int accum) {
+    for(int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; j < xn;
+        j += (int64_t)gridDim.x * blockDim.x) {
+        int64_t rem = j, bo = 0, bt = 0;
+        for(int k = d.nk - 1; k >= 0; --k) {
+            const int64_t c = rem % d.kshape[k];
+            rem /= d.kshape[k];
+            bo += c * d.kout[k];
+            bt += c * d.koth[k];
+        }
+        float acc = accum ? gx[j] : 0.0f;
+        for(int64_t r = 0; r < d.red_numel; ++r) {
+            int64_t rr = r, oo = bo, ot = bt;
+            for(int k = d.nr - 1; k >= 0; --k) {
+                const int64_t c = rr % d.rshape[k];
+                rr /= d.rshape[k];
+                oo += c * d.rout[k];
+                ot += c * d.roth[k];
+            }
+            // sub's second operand: grad -= g, the reference's form
+            if(op == 1 && which == 1)
+                acc -= gout[oo];
+            else
+                acc += grad_term(op, which, gout[oo], op == 2 ? other[ot] : 0.0f);
+        }
+        gx[j] = acc;
+    }
+}
+
+// ---------------------------------------------------------------- unary
+__device__ __forceinline__ float un_apply(int op, float x) {
+    switch(op) {
+        case 0: return sqrtf(x);
+        case 1: return (float)sin((double)x);
+        case 2: return (float)cos((double)x);
+        case 3: return (float)tan((double)x);
+        case 4: return (float)tanh((double)x);
+        default: return logf(x);
+    }
+}
+
+__device__ __forceinline__ float un_bwd(int op, float gx, float x, float y, float g) {
+    switch(op) {
+        case 0: return gx + g * (1.0f / (2.0f * y));
+        case 1: return (float)((double)gx + (double)g * cos((double)x));
+        case 2: return (float)((double)gx - (double)g * sin((double)x));
+        case 3: {
+            const float sec = (float)(1.0 / cos((double)x));
+            return gx + g * (sec * sec);
+        }
+        case 4: return gx + (g * 1.0f - y * y);
+        default: return gx + g * 1.0f / x;
+    }
+}
+
+__global__ void unary_kernel(int op, int64_t n, const float* __restrict__ x, float* __restrict__ y) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = un_apply(op, x[i]);
+}
+
+__global__ void unary_bwd_kernel(int op, int64_t n, const float* __restrict__ x,
+                                 const float* __restrict__ y, const float* __restrict__ gy,
+                                 float* __restrict__ gx, int accum) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x)
+        gx[i] = un_bwd(op, accum ? gx[i] : 0.0f, x[i], y[i], gy[i]);
+}
+
+// ------------------------------------------------------------------ relu
+__device__ __forceinline__ float relu1(float x) { return x > 0.0f ? x : 0.0f; }
+
+__global__ void relu_kernel(int64_t n, const float* __restrict__ x, float* __restrict__ y) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = relu1(x[i]);
+}
+
+__global__ void relu_bwd_kernel(int64_t n, const float* __restrict__ y,
+                                const float* __restrict__ gy, float* __restrict__ gx, int accum) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const float gate = (float)(y[i] > 0.0f);
+        const float t = gy[i] * gate;
+        gx[i] = accum ? gx[i] + t : t;
+    }
+}
+
+// ------------------------------------------------------- fill, axpy, sum
+__global__ void fill_kernel(int64_t n, float v, float* __restrict__ x) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = v;
+}
+
+__global__ void axpy_kernel(int64_t n, float alpha, const float* __restrict__ alpha_dev,
+                            const float* __restrict__ x, float* __restrict__ y, int accum) {
+    const float a = alpha_dev ? alpha * *alpha_dev : alpha;
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const float t = a * x[i];
+        y[i] = accum ? y[i] + t : t;
+    }
+}
+
+// one 1024-thread block: fixed partition and tree, so the result is deterministic
+__global__ __launch_bounds__(1024) void sum_kernel(int64_t n, const float* __restrict__ x,
+                                                   float scale, float* __restrict__ out, int accum) {
+    __shared__ float red[16];
+    double s = 0.0;
+    for(int64_t i = threadIdx.x; i < n; i += 1024) s += (double)x[i];
+    float v = pk::block_sum<16>((float)s, red);
+    if(threadIdx.x == 0) {
+        const float t = scale * v;
+        out[0] = accum ? out[0] + t : t;
+    }
+}
+
+// ------------------------------------------------------------ optimizers
+__global__ void sgd_kernel(int64_t n, float lr, float* __restrict__ p, const float* __restrict__ g) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const float step = lr * g[i];
+        p[i] = p[i] - step;
+    }
+}
+
+__global__ void adamw_kernel(int64_t n, float lr, float b1, float b2, float eps, float decay,
+                             float step_size, float bc2_sqrt, float* __restrict__ p,
+                             const float* __restrict__ g, float* __restrict__ m,
+                             float* __restrict__ v) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const float gi = g ? g[i] : 0.0f;
+        const float pj = p[i] * decay;
+        const float mj = b1 * m[i] + (1.0f - b1) * gi;
+        const float vj = b2 * v[i] + (1.0f - b2) * gi * gi;
+        const float denom = sqrtf(vj) / bc2_sqrt + eps;
+        p[i] = pj - step_size * (mj / denom);
+        m[i] = mj;
+        v[i] = vj;
+    }
+}
+
+// ------------------------------------------------------------- embedding
+__global__ void embed_fwd_kernel(int64_t n, int64_t d, int64_t vocab, const int32_t* __restrict__ ids,
+                                 const float* __restrict__ table, float* __restrict__ out) {
+    const int64_t total = n * d;
+    for(int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+        t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = t / d, e = t % d;
+        const int32_t id = ids[i];
+        out[t] = (id >= 0 && id < vocab) ? table[(int64_t)id * d + e] : 0.0f;
+    }
+}
+
+__global__ void embed_fwd4_kernel(int64_t n, int64_t d4, int64_t vocab,
+                                  const int32_t* __restrict__ ids, const f32x4* __restrict__ table,
+                                  f32x4* __restrict__ out) {
+    const int64_t total = n * d4;
+    for(int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+        t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = t / d4, e = t % d4;
+        const int32_t id = ids[i];
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        out[t] = (id >= 0 && id < vocab) ? table[(int64_t)id * d4 + e] : z;
+    }
+}
+
+__global__ void embed_bwd_kernel(int64_t n, int64_t d, int64_t vocab, const int32_t* __restrict__ ids,
+                                 const float* __restrict__ dout, float* __restrict__ dtable) {
+    const int64_t total = n * d;
+    for(int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+        t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = t / d, e = t % d;
+        const int32_t id = ids[i];
+        if(id >= 0 && id < vocab) unsafeAtomicAdd(dtable + (int64_t)id * d + e, dout[t]);
+    }
+}
+
+bool valid_op(int op, int hi) { return op >= 0 && op <= hi; }
+
+}  // namespace
+
+// ======================================================================= C-ABI
+
+extern "C" int pk_binary_f32(int op, int ndim, const int64_t* out_shape, const int64_t* a_strides,
+                             const int64_t* b_strides, const float* a, const float* b, float* out,
+                             pk_stream_t stream) {
+    if(!valid_op(op, 2)) return pk::fail("pk_binary_f32: op %d not in 0..2", op);
+    if(ndim < 1 || ndim > kMaxDims) return pk::fail("pk_binary_f32: ndim %d not in 1..8", ndim);
+    if(!out_shape || !a_strides || !b_strides) return pk::fail("pk_binary_f32: NULL descriptor");
+    Strides s;
+    s.ndim = ndim;
+    int64_t n = 1;
+    bool same = true;
+    int64_t cs = 1;
+    for(int d = ndim - 1; d >= 0; --d) {
+        if(out_shape[d] < 0) return pk::fail("pk_binary_f32: negative dim");
+        s.shape[d] = out_shape[d];
+        s.sa[d] = a_strides[d];
+        s.sb[d] = b_strides[d];
+        if(out_shape[d] > 1 && (a_strides[d] != cs || b_strides[d] != cs)) same = false;
+        cs *= out_shape[d];
+        n *= out_shape[d];
+    }
+    if(n == 0) return PK_OK;
+    if(!a || !b || !out) return pk::fail("pk_binary_f32: NULL data pointer");
+    hipStream_t st = pk::as_stream(stream);
+    if(same && n % 4 == 0 && pk::aligned16(a) && pk::aligned16(b) && pk::aligned16(out))
+        binary_same4<<<pk::grid_for(n / 4, NT), NT, 0, st>>>(
+            op, n / 4, (const f32x4*)a, (const f32x4*)b, (f32x4*)out);
+    else
+        binary_general<<<pk::grid_for(n, NT), NT, 0, st>>>(op, s, n, a, b, out);
+    return pk::launch_status("pk_binary_f32");
+}
+
+extern "C" int pk_binary_bwd_f32(int op, int which, int ndim, const int64_t* out_shape,
+                                 const int64_t* x_strides, const int64_t* other_strides,
+                                 int64_t x_numel, const float* gout, const float* other, float* gx,
+                                 int flags, pk_stream_t stream) {
+    if(!valid_op(op, 2) || (which != 0 && which != 1))
+        return pk::fail("pk_binary_bwd_f32: op %d / operand %d invalid", op, which);
+    if(ndim < 1 || ndim > kMaxDims) return pk::fail("pk_binary_bwd_f32: ndim %d not in 1..8", ndim);
+    if(!out_shape || !x_strides || !other_strides)
+        return pk::fail("pk_binary_bwd_f32: NULL descriptor");
+    BwdDesc d;
+    d.nk = d.nr = 0;
+    d.red_numel = 1;
+    int64_t cs = 1, kept_numel = 1, out_n = 1;
+    int64_t out_stride[kMaxDims];
+    for(int k = ndim - 1; k >= 0; --k) {
+        out_stride[k] = cs;
+        cs *= out_shape[k];
+        out_n *= out_shape[k];
+    }
+    for(int k = 0; k < ndim; ++k) {
+        if(out_shape[k] == 1) continue;
+        if(x_strides[k] != 0) {
+            d.kshape[d.nk] = out_shape[k];
+            d.kout[d.nk] = out_stride[k];
+            d.koth[d.nk] = other_strides[k];
+            d.nk++;
+            kept_numel *= out_shape[k];
+        } else {
+            d.rshape[d.nr] = out_shape[k];
+            d.rout[d.nr] = out_stride[k];
+            d.roth[d.nr] = other_strides[k];
+            d.nr++;
+            d.red_numel *= out_shape[k];
+        }
+    }
+    if(x_numel != kept_numel)
+        return pk::fail("pk_binary_bwd_f32: x_numel %lld does not match its broadcast (%lld)",
+                        (long long)x_numel, (long long)kept_numel);
+    if(out_n == 0 || x_numel == 0) return PK_OK;
+    if(!gout || !gx || (op == 2 && !other)) return pk::fail("pk_binary_bwd_f32: NULL data pointer");
+    binary_bwd_reduce<<<pk::grid_for(x_numel, NT), NT, 0, pk::as_stream(stream)>>>(
+        op, which, d, x_numel, gout, other, gx, flags & PK_ACCUM);
+    return pk::launch_status("pk_binary_bwd_f32");
+}
+
+extern "C" int pk_unary_f32(int op, int64_t n, const float* x, float* y, pk_stream_t stream) {
+    if(!valid_op(op, 5)) return pk::fail("pk_unary_f32: op %d not in 0..5", op);
+    if(n <= 0) return n < 0 ? pk::fail("pk_unary_f32: negative n") : PK_OK;
+    if(!x || !y) return pk::fail("pk_unary_f32: NULL pointer");
+    unary_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(op, n, x, y);
+    return pk::launch_status("pk_unary_f32");
+}
+
+extern "C" int pk_unary_bwd_f32(int op, int64_t n, const float* x, const float* y, const float* gy,
+                                float* gx, int flags, pk_stream_t stream) {
+    if(!valid_op(op, 5)) return pk::fail("pk_unary_bwd_f32: op %d not in 0..5", op);
+    if(n <= 0) return n < 0 ? pk::fail("pk_unary_bwd_f32: negative n") : PK_OK;
+    if(!x || !y || !gy || !gx) return pk::fail("pk_unary_bwd_f32: NULL pointer");
+    unary_bwd_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(op, n, x, y, gy, gx,
+                                                                           flags & PK_ACCUM);
+    return pk::launch_status("pk_unary_bwd_f32");
+}
+
+extern "C" int pk_relu_f32(int64_t n, const float* x, float* y, pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_relu_f32: negative n") : PK_OK;
+    if(!x || !y) return pk::fail("pk_relu_f32: NULL pointer");
+    relu_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, x, y);
+    return pk::launch_status("pk_relu_f32");
+}
+
+extern "C" int pk_relu_bwd_f32(int64_t n, const float* y, const float* gy, float* gx, int flags,
+                               pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_relu_bwd_f32: negative n") : PK_OK;
+    if(!y || !gy || !gx) return pk::fail("pk_relu_bwd_f32: NULL pointer");
+    relu_bwd_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, y, gy, gx,
+                                                                          flags & PK_ACCUM);
+    return pk::launch_status("pk_relu_bwd_f32");
+}
+
+extern "C" int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_fill_f32: negative n") : PK_OK;
+    if(!x) return pk::fail("pk_fill_f32: NULL pointer");
+    fill_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, value, x);
+    return pk::launch_status("pk_fill_f32");
+}
+
+extern "C" int pk_axpy_f32(int64_t n, float alpha, const float* alpha_dev, const float* x, float* y,
+                           int flags, pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_axpy_f32: negative n") : PK_OK;
+    if(!x || !y) return pk::fail("pk_axpy_f32: NULL pointer");
+    axpy_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, alpha, alpha_dev, x, y,
+                                                                       flags & PK_ACCUM);
+    return pk::launch_status("pk_axpy_f32");
+}
+
+extern "C" int pk_reduce_sum_f32(int64_t n, const float* x, float scale, float* out, int flags,
+                                 pk_stream_t stream) {
+    if(n < 0) return pk::fail("pk_reduce_sum_f32: negative n");
+    if(!out || (n > 0 && !x)) return pk::fail("pk_reduce_sum_f32: NULL pointer");
+    sum_kernel<<<1, 1024, 0, pk::as_stream(stream)>>>(n, x, scale, out, flags & PK_ACCUM);
+    return pk::launch_status("pk_reduce_sum_f32");
+}
+
+extern "C" int pk_sgd_f32(int64_t n, float lr, float* p, const float* g, pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_sgd_f32: negative n") : PK_OK;
+    if(!p || !g) return pk::fail("pk_sgd_f32: NULL pointer");
+    sgd_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, lr, p, g);
+    return pk::launch_status("pk_sgd_f32");
+}
+
+extern "C" int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps,
+                            float weight_decay, int step, float* p, const float* g, float* m,
+                            float* v, pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_adamw_f32: negative n") : PK_OK;
+    if(step < 1) return pk::fail("pk_adamw_f32: step %d must be >= 1", step);
+    if(!p || !m || !v) return pk::fail("pk_adamw_f32: NULL pointer");
+    const double bc1 = 1.0 - pow((double)beta1, (double)step);
+    const double bc2 = 1.0 - pow((double)beta2, (double)step);
+    const float step_size = (float)((double)lr / bc1);
+    const float bc2_sqrt = (float)sqrt(bc2);
+    const float decay = 1.0f - lr * weight_decay;
+    adamw_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(
+        n, lr, beta1, beta2, eps, decay, step_size, bc2_sqrt, p, g, m, v);
+    return pk::launch_status("pk_adamw_f32");
+}
+
+extern "C" int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids,
+                                const float* table, float* out, pk_stream_t stream) {
+    if(n < 0 || d < 0 || vocab < 0) return pk::fail("pk_embed_fwd_f32: negative size");
+    if(n == 0 || d == 0) return PK_OK;
+    if(!ids || !table || !out) return pk::fail("pk_embed_fwd_f32: NULL pointer");
+    hipStream_t st = pk::as_stream(stream);
+    if(d % 4 == 0 && pk::aligned16(table) && pk::aligned16(out))
+        embed_fwd4_kernel<<<pk::grid_for(n * d / 4, NT), NT, 0, st>>>(
+            n, d / 4, vocab, ids, (const f32x4*)table, (f32x4*)out);
+    else
+        embed_fwd_kernel<<<pk::grid_for(n * d, NT), NT, 0, st>>>(n, d, vocab, ids, table, out);
+    return pk::launch_status("pk_embed_fwd_f32");
+}
+
+extern "C" int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids,
+                                const float* dout, float* dtable, pk_stream_t stream) {
+    if(n < 0 || d < 0 || vocab < 0) return pk::fail("pk_embed_bwd_f32: negative size");
+    if(n == 0 || d == 0) return PK_OK;
+    if(!ids || !dout || !dtable) return pk::fail("pk_embed_bwd_f32: NULL pointer");
+    embed_bwd_kernel<<<pk::grid_for(n * d, NT), NT, 0, pk::as_stream(stream)>>>(n, d, vocab, ids,
+                                                                               dout, dtable);
+    return pk::launch_status("pk_embed_bwd_f32");
+}

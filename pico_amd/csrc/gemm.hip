@@ -1,0 +1,298 @@
+// pico_amd/csrc/gemm.hip -- fp32 GEMM on gfx950 matrix cores.
+//
+// C = alpha * op(A) . op(B) + beta * C, row-major, the three layouts pico's
+// matmul and its backward need (A.B, A.B^T, A^T.B; src/ops.c:144-190 and
+// src/autograd.h:96-130), plus a two-level batch and the causal tile/k-range
+// restrictions attention uses.
+//
+// Design (one 256-thread workgroup per 128x128 C tile):
+//  * 4 waves in a 2x2 grid, each wave owns a 64x64 sub-tile = 2x2 blocks of
+//    v_mfma_f32_32x32x2f32 (4096 FLOP per instruction, 16 fp32 accumulators
+//    per lane per block).
+//  * K advances 32 at a time through LDS, double-buffered: the next slice is
+//    fetched into registers with 128-bit global loads while the current slice
+//    feeds the MFMAs, then written to the other LDS buffer; one barrier per slice.
+//  * LDS keeps each operand in its global orientation (no transposes on the
+//    store).  Within a 32-wide k slice, lanes 0-31 take k 0..15 and lanes 32-63
+//    take k 16..31, so a k-contiguous tile is read with 128-bit LDS loads and a
+//    row-contiguous tile with conflict-free 32-bit loads.  Row strides are
+//    padded by 4 floats.
+//  * Tile order is XCD-aware: the hardware deals consecutive workgroups to
+//    the 8 XCDs round-robin, so the launch index is remapped to give each XCD
+//    a contiguous run of tiles, walked in groups of 8 tile-rows so concurrently
+//    running tiles share A rows and B columns in that XCD's L2.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pk_common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
+constexpr int KF = BK + 4;     // row stride of a k-contiguous LDS tile [128][36]
+constexpr int RF = BM + 4;     // row stride of a row-contiguous LDS tile [32][132]
+constexpr int TILE = BM * KF;  // floats per LDS tile (>= BK * RF)
+constexpr int GROUP_M = 8;
+
+struct GemmParams {
+    const float* A;
+    const float* B;
+    float* C;
+    int64_t M, N, K, lda, ldb, ldc;
+    int64_t sAo, sAi, sBo, sBi, sCo, sCi, inner;
+    float alpha, beta;
+    int causal;
+    int tiles_m, tiles_n;
+};
+
+// One 128x32 operand slice -> 4 float4 per thread.  KFAST: element (r,k) at
+// base[r*ld + k]; otherwise at base[k*ld + r].  EDGE zero-fills outside [R) x [K).
+template <bool KFAST, bool EDGE>
+__device__ __forceinline__ void load_slice(const float* __restrict__ base, int64_t ld, int64_t r0,
+                                           int64_t k0, int64_t R, int64_t K, f32x4 (&v)[4]) {
+#pragma unroll
+    for(int i = 0; i < 4; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        int rr, kk;
+        if(KFAST) {
+            rr = idx >> 3;
+            kk = (idx & 7) * 4;
+        } else {
+            kk = idx >> 5;
+            rr = (idx & 31) * 4;
+        }
+        const int64_t r = r0 + rr, k = k0 + kk;
+        if(!EDGE) {
+            const float* p = KFAST ? base + r * ld + k : base + k * ld + r;
+            v[i] = *reinterpret_cast<const f32x4*>(p);
+        } else {
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if(KFAST) {
+                if(r < R) {
+                    const float* p = base + r * ld;
+#pragma unroll
+                    for(int e = 0; e < 4; ++e)
+                        if(k + e < K) x[e] = p[k + e];
+                }
+            } else {
+                if(k < K) {
+                    const float* p = base + k * ld;
+#pragma unroll
+                    for(int e = 0; e < 4; ++e)
+                        if(r + e < R) x[e] = p[r + e];
+                }
+            }
+            v[i] = x;
+        }
+    }
+}
+
+template <bool KFAST>
+__device__ __forceinline__ void store_slice(float* lds, const f32x4 (&v)[4]) {
+#pragma unroll
+    for(int i = 0; i < 4; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        if(KFAST)
+            *reinterpret_cast<f32x4*>(lds + (idx >> 3) * KF + (idx & 7) * 4) = v[i];
+        else
+            *reinterpret_cast<f32x4*>(lds + (idx >> 5) * RF + (idx & 31) * 4) = v[i];
+    }
+}
+
+// 16 k-values of LDS row r for this lane's k half
+template <bool KFAST>
+__device__ __forceinline__ void read_frag(const float* lds, int r, int h, float (&f)[16]) {
+    if(KFAST) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(lds + r * KF + h * 16);
+#pragma unroll
+        for(int q = 0; q < 4; ++q) {
+            f32x4 x = p[q];
+            f[4 * q + 0] = x[0];
+            f[4 * q + 1] = x[1];
+            f[4 * q + 2] = x[2];
+            f[4 * q + 3] = x[3];
+        }
+    } else {
+#pragma unroll
+        for(int s = 0; s < 16; ++s) f[s] = lds[(h * 16 + s) * RF + r];
+    }
+}
+
+template <bool TA, bool TB, bool EDGE>
+__global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float lds[2][2][TILE];
+
+    // ---- tile selection: XCD-contiguous runs, grouped by GROUP_M tile-rows
+    const int ntiles = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+    const int group_span = GROUP_M * p.tiles_n;
+    const int first_m = (bid / group_span) * GROUP_M;
+    const int gm = min(p.tiles_m - first_m, GROUP_M);
+    const int local = bid % group_span;
+    const int tm = first_m + local % gm;
+    const int tn = local / gm;
+
+    const int64_t z = blockIdx.y;
+    const int64_t zo = z / p.inner, zi = z % p.inner;
+    const float* __restrict__ A = p.A + zo * p.sAo + zi * p.sAi;
+    const float* __restrict__ B = p.B + zo * p.sBo + zi * p.sBi;
+    float* __restrict__ C = p.C + zo * p.sCo + zi * p.sCi;
+
+    const int64_t row0 = (int64_t)tm * BM, col0 = (int64_t)tn * BN;
+    int64_t kbeg = 0, kend = p.K;
+    if(p.causal == 1 && col0 > row0 + BM - 1) return;  // wholly above the diagonal
+    if(p.causal == 2) kend = min(p.K, row0 + BM);
+    if(p.causal == 3) kbeg = min(p.K, (row0 / BK) * BK);
+    const int nslices = (int)((kend - kbeg + BK - 1) / BK);
+
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    const int wm = w >> 1, wn = w & 1;
+    const int lr = l & 31, lh = l >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for(int i = 0; i < 2; ++i)
+#pragma unroll
+        for(int j = 0; j < 2; ++j)
+#pragma unroll
+            for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
+    // (indexed by n) are k-contiguous when B is transposed.
+    constexpr bool AK = !TA, BKF = TB;
+    f32x4 ra[4], rb[4];
+    if(nslices > 0) {
+        load_slice<AK, EDGE>(A, p.lda, row0, kbeg, p.M, kend, ra);
+        load_slice<BKF, EDGE>(B, p.ldb, col0, kbeg, p.N, kend, rb);
+        store_slice<AK>(lds[0][0], ra);
+        store_slice<BKF>(lds[0][1], rb);
+    }
+    __syncthreads();
+
+    for(int s = 0; s < nslices; ++s) {
+        const int cur = s & 1;
+        const bool more = s + 1 < nslices;
+        if(more) {
+            const int64_t k0 = kbeg + (int64_t)(s + 1) * BK;
+            load_slice<AK, EDGE>(A, p.lda, row0, k0, p.M, kend, ra);
+            load_slice<BKF, EDGE>(B, p.ldb, col0, k0, p.N, kend, rb);
+        }
+        float fa[2][16], fb[2][16];
+#pragma unroll
+        for(int i = 0; i < 2; ++i) read_frag<AK>(lds[cur][0], wm * 64 + i * 32 + lr, lh, fa[i]);
+#pragma unroll
+        for(int j = 0; j < 2; ++j) read_frag<BKF>(lds[cur][1], wn * 64 + j * 32 + lr, lh, fb[j]);
+#pragma unroll
+        for(int kk = 0; kk < 16; ++kk)
+#pragma unroll
+            for(int i = 0; i < 2; ++i)
+#pragma unroll
+                for(int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][kk], fb[j][kk],
+                                                                     acc[i][j], 0, 0, 0);
+        if(more) {
+            store_slice<AK>(lds[cur ^ 1][0], ra);
+            store_slice<BKF>(lds[cur ^ 1][1], rb);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: 32x32 block accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
+    // column l%32
+#pragma unroll
+    for(int i = 0; i < 2; ++i)
+#pragma unroll
+        for(int j = 0; j < 2; ++j) {
+            const int64_t col = col0 + wn * 64 + j * 32 + lr;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 64 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                if(EDGE && (row >= p.M || col >= p.N)) continue;
+                float v = p.alpha * acc[i][j][r];
+                float* c = C + row * p.ldc + col;
+                if(p.beta != 0.0f) v += p.beta * *c;
+                *c = v;
+            }
+        }
+}
+
+template <bool TA, bool TB>
+int launch(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
+    dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)batch);
+    if(edge)
+        gemm_f32_kernel<TA, TB, true><<<grid, NT, 0, st>>>(gp);
+    else
+        gemm_f32_kernel<TA, TB, false><<<grid, NT, 0, st>>>(gp);
+    return pk::launch_status("pk_gemm_f32");
+}
+
+}  // namespace
+
+extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                   const float* A, int64_t lda, int64_t sA_outer, int64_t sA_inner,
+                                   const float* B, int64_t ldb, int64_t sB_outer, int64_t sB_inner,
+                                   float beta, float* C, int64_t ldc, int64_t sC_outer,
+                                   int64_t sC_inner, int64_t batch, int64_t inner_count,
+                                   int causal, pk_stream_t stream) {
+    const bool TA = ta == 'T' || ta == 't', TB = tb == 'T' || tb == 't';
+    if(!(TA || ta == 'N' || ta == 'n') || !(TB || tb == 'N' || tb == 'n'))
+        return pk::fail("pk_gemm_f32: transpose flags must be 'N' or 'T' (got '%c','%c')", ta, tb);
+    if(M < 0 || N < 0 || K < 0 || batch < 0)
+        return pk::fail("pk_gemm_f32: negative size M=%lld N=%lld K=%lld batch=%lld",
+                        (long long)M, (long long)N, (long long)K, (long long)batch);
+    if(causal < 0 || causal > 3) return pk::fail("pk_gemm_f32: causal mode %d not in 0..3", causal);
+    if(inner_count < 1) return pk::fail("pk_gemm_f32: inner_count must be >= 1");
+    if(M == 0 || N == 0 || batch == 0) return PK_OK;
+    if(!C) return pk::fail("pk_gemm_f32: C is NULL");
+    if(K > 0 && (!A || !B)) return pk::fail("pk_gemm_f32: A or B is NULL");
+    const int64_t a_cols = TA ? M : K, b_cols = TB ? K : N;
+    if(K > 0 && (lda < a_cols || ldb < b_cols))
+        return pk::fail("pk_gemm_f32: leading dimension too small (lda=%lld needs >= %lld, "
+                        "ldb=%lld needs >= %lld)",
+                        (long long)lda, (long long)a_cols, (long long)ldb, (long long)b_cols);
+    if(ldc < N) return pk::fail("pk_gemm_f32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
+    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if(tiles_m * tiles_n > (int64_t)1 << 30 || batch > 65535)
+        return pk::fail("pk_gemm_f32: problem too large for one launch");
+
+    GemmParams gp;
+    gp.A = A;
+    gp.B = B;
+    gp.C = C;
+    gp.M = M;
+    gp.N = N;
+    gp.K = K;
+    gp.lda = lda;
+    gp.ldb = ldb;
+    gp.ldc = ldc;
+    gp.sAo = sA_outer;
+    gp.sAi = sA_inner;
+    gp.sBo = sB_outer;
+    gp.sBi = sB_inner;
+    gp.sCo = sC_outer;
+    gp.sCi = sC_inner;
+    gp.inner = inner_count;
+    gp.alpha = alpha;
+    gp.beta = beta;
+    gp.causal = causal;
+    gp.tiles_m = (int)tiles_m;
+    gp.tiles_n = (int)tiles_n;
+
+    // the unchecked path needs whole tiles and 16-byte aligned float4 loads
+    const bool edge = (M % BM) || (N % BN) || (K % BK) || (lda % 4) || (ldb % 4) ||
+                      (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
+                      !pk::aligned16(A) || !pk::aligned16(B);
+    hipStream_t st = pk::as_stream(stream);
+    if(!TA && !TB) return launch<false, false>(gp, batch, edge, st);
+    if(!TA && TB) return launch<false, true>(gp, batch, edge, st);
+    if(TA && !TB) return launch<true, false>(gp, batch, edge, st);
+    return launch<true, true>(gp, batch, edge, st);
+}
+
+extern "C" int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                           const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                           float* C, int64_t ldc, pk_stream_t stream) {
+    return pk_gemm_batched_f32(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc,
+                               0, 0, 1, 1, 0, stream);
+}

@@ -1,0 +1,271 @@
+"""Thin Python bindings of the pk_* C-ABI over torch device tensors.
+
+torch supplies device memory and the current stream; every computation runs
+in the hand-written HIP kernels of ``libpico_hip.so``.  Each function checks
+shapes on the host before launching (so a kernel never sees a shape its grid
+does not cover) and raises ``PkError`` on a non-zero status.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import check, hip_lib
+
+ACCUM = 1
+ACCUM2 = 2
+BINARY_OPS = {"add": 0, "sub": 1, "mul": 2}
+UNARY_OPS = {"sqrt": 0, "sin": 1, "cos": 2, "tan": 3, "tanh": 4, "log": 5}
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _f32(*ts):
+    for t in ts:
+        if t is not None:
+            if t.dtype != torch.float32 or not t.is_cuda:
+                raise TypeError("expected a float32 CUDA tensor")
+
+
+def _rowmajor(t, name):
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name} must be a 2-D tensor with unit column stride")
+    return max(t.stride(0), t.shape[1])
+
+
+def gemm(ta, tb, A, B, C, alpha=1.0, beta=0.0):
+    """C = alpha * op(A) @ op(B) + beta * C  (op = transpose for 'T')."""
+    _f32(A, B, C)
+    lda, ldb, ldc = _rowmajor(A, "A"), _rowmajor(B, "B"), _rowmajor(C, "C")
+    M = A.shape[1] if ta == "T" else A.shape[0]
+    K = A.shape[0] if ta == "T" else A.shape[1]
+    Kb = B.shape[1] if tb == "T" else B.shape[0]
+    N = B.shape[0] if tb == "T" else B.shape[1]
+    if K != Kb or tuple(C.shape) != (M, N):
+        raise ValueError(f"gemm shape mismatch: op(A) {M}x{K}, op(B) {Kb}x{N}, C {tuple(C.shape)}")
+    check("pk_gemm_f32", hip_lib().pk_gemm_f32(
+        ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc,
+        _stream()))
+    return C
+
+
+def gemm_batched(ta, tb, M, N, K, alpha, A, lda, sAo, sAi, B, ldb, sBo, sBi, beta, C, ldc, sCo,
+                 sCi, batch, inner, causal=0):
+    """Raw batched GEMM on flat tensors (strides in elements)."""
+    _f32(A, B, C)
+    check("pk_gemm_batched_f32", hip_lib().pk_gemm_batched_f32(
+        ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, sAo, sAi, _ptr(B), ldb, sBo, sBi,
+        beta, _ptr(C), ldc, sCo, sCi, batch, inner, causal, _stream()))
+    return C
+
+
+def _bcast_strides(shape, out_shape):
+    """Strides of a contiguous `shape` mapped onto `out_shape` (0 on broadcast dims)."""
+    nd = len(out_shape)
+    st = [0] * nd
+    s = 1
+    for d in range(len(shape) - 1, -1, -1):
+        od = d + nd - len(shape)
+        st[od] = 0 if shape[d] == 1 else s
+        s *= shape[d]
+    return st
+
+
+def _i64s(xs):
+    return (ctypes.c_int64 * len(xs))(*xs)
+
+
+def binary(op, a, b, out=None):
+    _f32(a, b)
+    out_shape = list(torch.broadcast_shapes(a.shape, b.shape))
+    if out is None:
+        out = torch.empty(out_shape, device=a.device, dtype=torch.float32)
+    nd = max(1, len(out_shape))
+    osh = out_shape or [1]
+    sa = _bcast_strides(list(a.shape) or [1], osh)
+    sb = _bcast_strides(list(b.shape) or [1], osh)
+    check("pk_binary_f32", hip_lib().pk_binary_f32(
+        BINARY_OPS[op], nd, _i64s(osh), _i64s(sa), _i64s(sb), _ptr(a.contiguous()),
+        _ptr(b.contiguous()), _ptr(out), _stream()))
+    return out
+
+
+def binary_bwd(op, which, out_shape, x_shape, other_shape, gout, other, gx, accumulate=False):
+    osh = list(out_shape) or [1]
+    sx = _bcast_strides(list(x_shape) or [1], osh)
+    so = _bcast_strides(list(other_shape) or [1], osh)
+    xn = 1
+    for s in x_shape:
+        xn *= s
+    check("pk_binary_bwd_f32", hip_lib().pk_binary_bwd_f32(
+        BINARY_OPS[op], which, len(osh), _i64s(osh), _i64s(sx), _i64s(so), xn, _ptr(gout),
+        _ptr(other), _ptr(gx), ACCUM if accumulate else 0, _stream()))
+    return gx
+
+
+def unary(op, x, y):
+    check("pk_unary_f32", hip_lib().pk_unary_f32(UNARY_OPS[op], x.numel(), _ptr(x), _ptr(y),
+                                                  _stream()))
+    return y
+
+
+def unary_bwd(op, x, y, gy, gx, accumulate=True):
+    check("pk_unary_bwd_f32", hip_lib().pk_unary_bwd_f32(
+        UNARY_OPS[op], x.numel(), _ptr(x), _ptr(y), _ptr(gy), _ptr(gx),
+        ACCUM if accumulate else 0, _stream()))
+    return gx
+
+
+def relu(x, y):
+    check("pk_relu_f32", hip_lib().pk_relu_f32(x.numel(), _ptr(x), _ptr(y), _stream()))
+    return y
+
+
+def relu_bwd(y, gy, gx, accumulate=True):
+    check("pk_relu_bwd_f32", hip_lib().pk_relu_bwd_f32(
+        y.numel(), _ptr(y), _ptr(gy), _ptr(gx), ACCUM if accumulate else 0, _stream()))
+    return gx
+
+
+def fill(x, value):
+    check("pk_fill_f32", hip_lib().pk_fill_f32(x.numel(), value, _ptr(x), _stream()))
+    return x
+
+
+def axpy(alpha, x, y, alpha_dev=None, accumulate=True):
+    check("pk_axpy_f32", hip_lib().pk_axpy_f32(x.numel(), alpha, _ptr(alpha_dev), _ptr(x),
+                                                _ptr(y), ACCUM if accumulate else 0, _stream()))
+    return y
+
+
+def reduce_sum(x, out, scale=1.0, accumulate=False):
+    check("pk_reduce_sum_f32", hip_lib().pk_reduce_sum_f32(
+        x.numel(), _ptr(x), scale, _ptr(out), ACCUM if accumulate else 0, _stream()))
+    return out
+
+
+def sgd(p, g, lr):
+    check("pk_sgd_f32", hip_lib().pk_sgd_f32(p.numel(), lr, _ptr(p), _ptr(g), _stream()))
+    return p
+
+
+def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step):
+    check("pk_adamw_f32", hip_lib().pk_adamw_f32(p.numel(), lr, beta1, beta2, eps, wd, step,
+                                                  _ptr(p), _ptr(g), _ptr(m), _ptr(v), _stream()))
+    return p
+
+
+def xent_fwd_bwd(logits, labels, loss_rows=None, dlogits=None, scale=1.0, accumulate=False):
+    R, V = logits.shape
+    if labels.dtype != torch.int32 or labels.numel() != R:
+        raise ValueError("labels must be int32 with one entry per row")
+    check("pk_xent_fwd_bwd_f32", hip_lib().pk_xent_fwd_bwd_f32(
+        R, V, _ptr(logits), _rowmajor(logits, "logits"), _ptr(labels), _ptr(loss_rows),
+        _ptr(dlogits), V if dlogits is None else _rowmajor(dlogits, "dlogits"), scale,
+        ACCUM if accumulate else 0, _stream()))
+
+
+def argmax(x, idx):
+    R, V = x.shape
+    check("pk_argmax_f32", hip_lib().pk_argmax_f32(R, V, _ptr(x), _rowmajor(x, "x"), _ptr(idx),
+                                                    _stream()))
+    return idx
+
+
+def rmsnorm_fwd(x, g, y, rstd, eps):
+    R, C = x.shape
+    if g.numel() != C or y.shape != x.shape or (rstd is not None and rstd.numel() != R):
+        raise ValueError("rmsnorm_fwd shape mismatch")
+    check("pk_rmsnorm_fwd_f32", hip_lib().pk_rmsnorm_fwd_f32(R, C, eps, _ptr(x), _ptr(g), _ptr(y),
+                                                              _ptr(rstd), _stream()))
+
+
+def rmsnorm_bwd_workspace(R, C):
+    return int(hip_lib().pk_rmsnorm_bwd_workspace(R, C))
+
+
+def rmsnorm_bwd(x, g, rstd, dy, dx, dg, ws=None, accum_dx=False, accum_dg=False):
+    R, C = x.shape
+    need = rmsnorm_bwd_workspace(R, C)
+    if ws is None and dg is not None:
+        ws = torch.empty(max(1, need // 4), device=x.device, dtype=torch.float32)
+    flags = (ACCUM if accum_dx else 0) | (ACCUM2 if accum_dg else 0)
+    check("pk_rmsnorm_bwd_f32", hip_lib().pk_rmsnorm_bwd_f32(
+        R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dg), flags, _ptr(ws),
+        0 if ws is None else ws.numel() * 4, _stream()))
+
+
+def swiglu_fwd(a, u, h):
+    R, F = a.shape
+    check("pk_swiglu_fwd_f32", hip_lib().pk_swiglu_fwd_f32(
+        R, F, _ptr(a), _rowmajor(a, "a"), _ptr(u), _rowmajor(u, "u"), _ptr(h), _rowmajor(h, "h"),
+        _stream()))
+    return h
+
+
+def swiglu_bwd(a, u, dh, da, du, accum_da=False, accum_du=False):
+    R, F = a.shape
+    ldd = _rowmajor(da if da is not None else du, "da")
+    flags = (ACCUM if accum_da else 0) | (ACCUM2 if accum_du else 0)
+    check("pk_swiglu_bwd_f32", hip_lib().pk_swiglu_bwd_f32(
+        R, F, _ptr(a), _rowmajor(a, "a"), _ptr(u), _rowmajor(u, "u"), _ptr(dh), _rowmajor(dh, "dh"),
+        _ptr(da), _ptr(du), ldd, flags, _stream()))
+
+
+def attn_fwd(B, H, q, k, v, o, lse, P, scale=None):
+    BT, D = q.shape
+    T, hd = BT // B, D // H
+    if B * T != BT or H * hd != D or P.numel() < B * H * T * T or lse.numel() < B * H * T:
+        raise ValueError("attention shape mismatch")
+    scale = hd ** -0.5 if scale is None else scale
+    check("pk_attn_causal_fwd_f32", hip_lib().pk_attn_causal_fwd_f32(
+        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(P), _stream()))
+
+
+def attn_bwd(B, H, q, k, v, P, dout, dq, dk, dv, dP_ws, accumulate=False, scale=None):
+    BT, D = q.shape
+    T, hd = BT // B, D // H
+    if dP_ws.numel() < B * H * T * T:
+        raise ValueError("attention backward workspace too small")
+    scale = hd ** -0.5 if scale is None else scale
+    check("pk_attn_causal_bwd_f32", hip_lib().pk_attn_causal_bwd_f32(
+        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(P), _ptr(dout), _ptr(dq), _ptr(dk),
+        _ptr(dv), _ptr(dP_ws), ACCUM if accumulate else 0, _stream()))
+
+
+def causal_softmax_fwd(BH, T, S, P, lse, scale=1.0):
+    check("pk_causal_softmax_fwd_f32", hip_lib().pk_causal_softmax_fwd_f32(
+        BH, T, scale, _ptr(S), _ptr(P), _ptr(lse), _stream()))
+
+
+def causal_softmax_bwd(BH, T, P, dP, dS):
+    check("pk_causal_softmax_bwd_f32", hip_lib().pk_causal_softmax_bwd_f32(
+        BH, T, _ptr(P), _ptr(dP), _ptr(dS), _stream()))
+
+
+def embed_fwd(ids, table, out):
+    n, d = out.shape
+    check("pk_embed_fwd_f32", hip_lib().pk_embed_fwd_f32(n, d, table.shape[0], _ptr(ids),
+                                                          _ptr(table), _ptr(out), _stream()))
+    return out
+
+
+def embed_bwd(ids, dout, dtable):
+    n, d = dout.shape
+    check("pk_embed_bwd_f32", hip_lib().pk_embed_bwd_f32(n, d, dtable.shape[0], _ptr(ids),
+                                                          _ptr(dout), _ptr(dtable), _stream()))
+    return dtable
+
+
+def device_info():
+    cu, clk = ctypes.c_int(0), ctypes.c_int(0)
+    arch = ctypes.create_string_buffer(64)
+    check("pk_device_info", hip_lib().pk_device_info(ctypes.byref(cu), ctypes.byref(clk), arch, 64))
+    return {"cu_count": cu.value, "clock_khz": clk.value, "arch": arch.value.decode()}

@@ -1,0 +1,369 @@
+"""GPU parity of every pk_* launcher against the CPU oracle (seeded inputs).
+
+Bar: bit-exact where the arithmetic is exact or order-free (integer-valued
+GEMMs, add/sub/mul and their gradients, relu, SGD, gathers, argmax); otherwise
+the north-star tolerance, max relative error <= 1e-4 (GEMM: the
+componentwise-normalised error of tests/_util.gemm_err).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from pico_amd import kernels as K
+from tests._util import gemm_err, max_rel, row_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_ops.npz"))
+
+
+def cu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _op(x, t):
+    return x.T if t == "T" else x
+
+
+def _operands(ta, tb, M, N, Kd, seed, integer=False):
+    if integer:
+        rng = np.random.default_rng(seed)
+        A = rng.integers(-8, 9, (M, Kd)).astype(np.float32)
+        B = rng.integers(-8, 9, (Kd, N)).astype(np.float32)
+    else:
+        A = O.uniform(M * Kd, seed).reshape(M, Kd)
+        B = O.uniform(Kd * N, seed + 1).reshape(Kd, N)
+    As = np.ascontiguousarray(A.T) if ta == "T" else A
+    Bs = np.ascontiguousarray(B.T) if tb == "T" else B
+    return A, B, As, Bs
+
+
+# ----------------------------------------------------------------- GEMM
+def test_gemm_reference_kats(dev):
+    A = cu(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
+    B = cu(np.array([[7, 8], [9, 10], [11, 12]], np.float32))
+    C = torch.zeros(2, 2, device=dev)
+    assert host(K.gemm("N", "N", A, B, C)).tolist() == [[58, 64], [139, 154]]
+    # pico_matmul_backward with dC = ones (tests/test_autograd.c:382)
+    dC = torch.ones(2, 2, device=dev)
+    dA = torch.zeros(2, 3, device=dev)
+    dB = torch.zeros(3, 2, device=dev)
+    K.gemm("N", "T", dC, B, dA, beta=1.0)
+    K.gemm("T", "N", A, dC, dB, beta=1.0)
+    assert host(dA).ravel().tolist() == [15, 19, 23, 15, 19, 23]
+    assert host(dB).ravel().tolist() == [5, 5, 7, 7, 9, 9]
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(64, 128, 784), (64, 10, 128), (130, 257, 70), (256, 256, 256),
+                                    (1, 1, 1), (3, 5, 0)])
+def test_gemm_integer_bitexact(dev, ta, tb, M, N, Kd):
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)  # beta = 0 must not read C
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N")])
+@pytest.mark.parametrize("n", [512, 1024, 2048])
+def test_gemm_uniform_vs_fp64(dev, ta, tb, n):
+    A, B, As, Bs = _operands(ta, tb, n, n, n, seed=100 + n)
+    C = torch.empty(n, n, device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    assert gemm_err(host(C), A, B) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N")])
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_gemm_large_sampled_rows(dev, ta, tb, n):
+    # full-size product on the GPU; 32 sampled rows checked against fp64
+    gen = torch.Generator(device="cpu").manual_seed(n)
+    As = (torch.rand(n, n, generator=gen) * 2 - 1)
+    Bs = (torch.rand(n, n, generator=gen) * 2 - 1)
+    C = torch.empty(n, n, device=dev)
+    K.gemm(ta, tb, As.cuda(), Bs.cuda(), C)
+    Cn = host(C)
+    A = As.numpy().T if ta == "T" else As.numpy()
+    B = Bs.numpy().T if tb == "T" else Bs.numpy()
+    rows = np.random.default_rng(n).choice(n, 32, replace=False)
+    assert gemm_err(Cn[rows], A[rows], B) <= TOL
+
+
+def test_gemm_alpha_beta_accumulate(dev):
+    M, N, Kd = 200, 136, 96
+    A, B, As, Bs = _operands("N", "N", M, N, Kd, seed=5)
+    C0 = O.uniform(M * N, 77).reshape(M, N)
+    C = cu(C0.copy())
+    K.gemm("N", "N", cu(As), cu(Bs), C, alpha=0.5, beta=1.0)
+    ref = 0.5 * (A.astype(np.float64) @ B) + C0
+    assert max_rel(host(C), ref) <= TOL
+    # a pico_transpose_2d view maps to 'T': A^T stored contiguously as [K, M]
+    C2 = torch.empty(M, N, device=dev)
+    K.gemm("T", "N", cu(np.ascontiguousarray(A.T)), cu(B), C2)
+    assert gemm_err(host(C2), A, B) <= TOL
+
+
+@pytest.mark.parametrize("causal", [0, 1, 2, 3])
+def test_gemm_batched_causal(dev, causal):
+    # two-level batch (2 sequences x 3 heads) addressed inside token-major buffers
+    Bn, H, T, hd = 2, 3, 256, 64
+    D = H * hd
+    q = O.uniform(Bn * T * D, 1).reshape(Bn * T, D)
+    k = O.uniform(Bn * T * D, 2).reshape(Bn * T, D)
+    S = torch.zeros(Bn * H * T * T, device=dev)
+    if causal in (0, 1):
+        K.gemm_batched("N", "T", T, T, hd, 0.5, cu(q), D, T * D, hd, cu(k), D, T * D, hd, 0.0, S,
+                       T, H * T * T, T * T, Bn * H, H, causal)
+        Sn = host(S).reshape(Bn, H, T, T)
+        for b in range(Bn):
+            for h in range(H):
+                Q = q[b * T:(b + 1) * T, h * hd:(h + 1) * hd].astype(np.float64)
+                Kh = k[b * T:(b + 1) * T, h * hd:(h + 1) * hd].astype(np.float64)
+                ref = 0.5 * Q @ Kh.T
+                got = Sn[b, h]
+                if causal == 1:
+                    keep = np.tril(np.ones((T, T), bool))
+                    got, ref = got[keep], ref[keep]
+                assert max_rel(got, ref) <= TOL
+    else:
+        # op(A) triangular: lower for mode 2 (stored as is), upper for mode 3 (stored
+        # transposed, read with 'T'); out = op(A) . V per head
+        X = O.uniform(T * T, 3).reshape(T, T)
+        Amat = np.tril(X) if causal == 2 else np.triu(X)
+        store = Amat if causal == 2 else np.ascontiguousarray(Amat.T)
+        Pb = np.broadcast_to(store, (Bn * H, T, T)).copy()
+        out = torch.zeros(Bn * T, D, device=dev)
+        ta = "N" if causal == 2 else "T"
+        K.gemm_batched(ta, "N", T, hd, T, 1.0, cu(Pb), T, H * T * T, T * T, cu(q), D, T * D,
+                       hd, 0.0, out, D, T * D, hd, Bn * H, H, causal)
+        on = host(out)
+        for b in range(Bn):
+            for h in range(H):
+                Vh = q[b * T:(b + 1) * T, h * hd:(h + 1) * hd].astype(np.float64)
+                ref = Amat @ Vh
+                assert max_rel(on[b * T:(b + 1) * T, h * hd:(h + 1) * hd], ref) <= TOL
+
+
+def test_gemm_rejects_bad_arguments(dev):
+    from pico_amd._lib import PkError
+
+    A = torch.zeros(4, 4, device=dev)
+    with pytest.raises(PkError):
+        K.gemm_batched("X", "N", 4, 4, 4, 1.0, A, 4, 0, 0, A, 4, 0, 0, 0.0, A, 4, 0, 0, 1, 1)
+    with pytest.raises(PkError):  # lda < K
+        K.gemm_batched("N", "N", 4, 4, 8, 1.0, A, 4, 0, 0, A, 4, 0, 0, 0.0, A, 4, 0, 0, 1, 1)
+
+
+# ---------------------------------------------------------- elementwise
+BCAST_CASES = [((3, 5), (3, 5)), ((4, 6), (6,)), ((4, 6), (4, 1)), ((2, 3, 4), (3, 1)),
+               ((7,), (1,)), ((5, 1, 3), (1, 4, 1)), ((16,), (16,)), ((19,), (19,))]
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+@pytest.mark.parametrize("sa,sb", BCAST_CASES)
+def test_binary_and_grad_bitexact(dev, op, sa, sb):
+    a = O.normal(int(np.prod(sa)), 1).reshape(sa)
+    b = O.normal(int(np.prod(sb)), 2).reshape(sb)
+    name = ["add", "sub", "mul"][op]
+    out = K.binary(name, cu(a), cu(b))
+    assert np.array_equal(host(out), O.binary(op, a, b))
+    g = O.normal(out.numel(), 3).reshape(out.shape)
+    ga0 = O.normal(a.size, 4).reshape(sa)  # += onto a nonzero grad
+    gb0 = O.normal(b.size, 5).reshape(sb)
+    ga_ref, gb_ref = O.binary_bwd(op, a, b, g, ga0.copy(), gb0.copy())
+    ga, gb = cu(ga0.copy()), cu(gb0.copy())
+    K.binary_bwd(name, 0, out.shape, sa, sb, cu(g), cu(b), ga, accumulate=True)
+    K.binary_bwd(name, 1, out.shape, sb, sa, cu(g), cu(a), gb, accumulate=True)
+    assert np.array_equal(host(ga), ga_ref)
+    assert np.array_equal(host(gb), gb_ref)
+
+
+@pytest.mark.parametrize("op", range(6))
+def test_unary_and_grad(dev, op):
+    n = 1000
+    x = O.uniform(n, 9, 0.05, 1.4)  # in every op's domain
+    y = K.unary(list(K.UNARY_OPS)[op], cu(x), torch.empty(n, device=dev))
+    assert row_err(host(y), O.unary(op, x)) <= 1e-6
+    gy = O.normal(n, 10)
+    gx0 = O.normal(n, 11)
+    yref = O.unary(op, x)
+    ref = O.unary_bwd(op, x, yref, gy, gx0.copy())
+    gx = cu(gx0.copy())
+    K.unary_bwd(list(K.UNARY_OPS)[op], cu(x), cu(yref), cu(gy), gx)
+    assert max_rel(host(gx), ref) <= 1e-6
+
+
+def test_relu_fill_sgd_bitexact(dev):
+    x = O.normal(5003, 1)
+    x[:4] = [np.nan, -0.0, 0.0, -1.0]
+    y = K.relu(cu(x), torch.empty(5003, device=dev))
+    assert np.array_equal(host(y), O.relu(x))
+    gy, gx0 = O.normal(5003, 2), O.normal(5003, 3)
+    gx = cu(gx0.copy())
+    K.relu_bwd(cu(O.relu(x)), cu(gy), gx)
+    assert np.array_equal(host(gx), O.relu_bwd(O.relu(x), gy, gx0.copy()))
+    f = K.fill(torch.empty(777, device=dev), 1.0)
+    assert np.all(host(f) == 1.0)
+    p, g = O.normal(4099, 4), O.normal(4099, 5)
+    pt = cu(p.copy())
+    K.sgd(pt, cu(g), 0.01)
+    assert np.array_equal(host(pt), O.sgd(p.copy(), g, 0.01))
+
+
+def test_axpy_and_sum(dev):
+    x, y0 = O.normal(3001, 1), O.normal(3001, 2)
+    s = cu(np.array([0.25], np.float32))
+    y = cu(y0.copy())
+    K.axpy(2.0, cu(x), y, alpha_dev=s)
+    assert max_rel(host(y), y0 + 0.5 * x) <= 1e-6
+    out = torch.zeros(1, device=dev)
+    K.reduce_sum(cu(x), out, scale=0.5)
+    assert abs(host(out)[0] - 0.5 * x.astype(np.float64).sum()) <= 1e-4 * np.abs(x).sum()
+
+
+def test_adamw_vs_oracle_and_golden(dev):
+    lr, b1, b2, eps, wd = (float(v) for v in GOLD["adamw_hparams"])
+    p = cu(GOLD["adamw_p0"].copy())
+    m, v = torch.zeros_like(p), torch.zeros_like(p)
+    for s in range(3):
+        K.adamw(p, cu(GOLD["adamw_g"][s]), m, v, lr, b1, b2, eps, wd, s + 1)
+        assert max_rel(host(p), GOLD["adamw_p"][s]) <= 1e-6
+    n = 10007
+    p0, g = O.normal(n, 1), O.normal(n, 2)
+    ref = O.adamw(p0.copy(), g, np.zeros(n, np.float32), np.zeros(n, np.float32), 1e-3, 0.9,
+                  0.999, 1e-8, 0.01, 1)
+    pt = cu(p0.copy())
+    K.adamw(pt, cu(g), torch.zeros_like(pt), torch.zeros_like(pt), 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+    assert np.array_equal(host(pt), ref)
+
+
+# ------------------------------------------------------------ row kernels
+@pytest.mark.parametrize("R,V", [(7, 37), (64, 10), (16, 8192), (8, 32000), (3, 40000),
+                                 (4, 33000)])
+def test_xent_vs_oracle(dev, R, V):
+    z = O.normal(R * V, R + V, 0.0, 2.0).reshape(R, V)
+    y = O.labels(R, 7, V)
+    loss_ref, dz_ref = O.xent(z, y, scale=1.0 / R)
+    rows = torch.empty(R, device=dev)
+    dz = torch.empty(R, V, device=dev)
+    K.xent_fwd_bwd(cu(z), cu(y), rows, dz, scale=1.0 / R)
+    assert row_err(host(rows), loss_ref) <= TOL
+    assert max_rel(host(dz), dz_ref) <= TOL
+    dz2 = cu(dz_ref.copy())  # accumulate mode adds onto the existing gradient
+    K.xent_fwd_bwd(cu(z), cu(y), None, dz2, scale=1.0 / R, accumulate=True)
+    assert max_rel(host(dz2), 2 * dz_ref) <= TOL
+
+
+def test_xent_golden_and_bad_labels(dev):
+    z, y = GOLD["xent_z"], GOLD["xent_y"]
+    rows = torch.empty(z.shape[0], device=dev)
+    dz = torch.empty(z.shape, device=dev)
+    K.xent_fwd_bwd(cu(z), cu(y), rows, dz, scale=1.0 / z.shape[0])
+    assert row_err(host(rows), GOLD["xent_rows"]) <= TOL
+    assert max_rel(host(dz), GOLD["xent_dz"]) <= TOL
+    bad = y.copy()
+    bad[0], bad[1] = -1, z.shape[1]
+    K.xent_fwd_bwd(cu(z), cu(bad), rows, dz)
+    r, d = host(rows), host(dz)
+    assert np.isnan(r[0]) and np.isnan(r[1]) and not np.any(d[:2])
+
+
+@pytest.mark.parametrize("R,V", [(6, 13), (100, 32000), (9, 7)])
+def test_argmax_bitexact(dev, R, V):
+    if (R, V) == (6, 13):
+        x = GOLD["argmax_x"]
+        ref = GOLD["argmax_idx"]
+    else:
+        x = O.normal(R * V, 5).reshape(R, V)
+        x[0, V // 2] = x[0, V // 3] = 100.0  # tie: first wins
+        ref = O.argmax(x)
+    idx = torch.empty(R, dtype=torch.int32, device=dev)
+    K.argmax(cu(x), idx)
+    assert np.array_equal(host(idx), ref)
+
+
+@pytest.mark.parametrize("R,C", [(5, 24), (64, 512), (33, 768), (16, 4096), (7, 10001), (3, 9000)])
+def test_rmsnorm_vs_oracle(dev, R, C):
+    x = O.normal(R * C, 1).reshape(R, C)
+    g = O.normal(C, 2, 1.0, 0.02)
+    dy = O.normal(R * C, 3).reshape(R, C)
+    y_ref, rstd_ref = O.rmsnorm_fwd(x, g, 1e-6)
+    y, rstd = torch.empty(R, C, device=dev), torch.empty(R, device=dev)
+    K.rmsnorm_fwd(cu(x), cu(g), y, rstd, 1e-6)
+    assert max_rel(host(y), y_ref) <= TOL and row_err(host(rstd), rstd_ref) <= TOL
+    dx0, dg0 = O.normal(R * C, 4).reshape(R, C), O.normal(C, 5)
+    dx_ref, dg_ref = O.rmsnorm_bwd(x, g, rstd_ref, dy, dx0.copy(), dg0.copy())
+    dx, dg = cu(dx0.copy()), cu(dg0.copy())
+    K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx, dg, accum_dx=True, accum_dg=True)
+    assert max_rel(host(dx), dx_ref) <= TOL and max_rel(host(dg), dg_ref) <= TOL
+    dx, dg = torch.empty(R, C, device=dev), torch.empty(C, device=dev)  # overwrite mode
+    K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx, dg)
+    dx_ref, dg_ref = O.rmsnorm_bwd(x, g, rstd_ref, dy)
+    assert max_rel(host(dx), dx_ref) <= TOL and max_rel(host(dg), dg_ref) <= TOL
+
+
+@pytest.mark.parametrize("R,F", [(4, 33), (64, 1376), (128, 2048)])
+def test_swiglu_vs_oracle(dev, R, F):
+    a, u, dh = (O.normal(R * F, s).reshape(R, F) for s in (1, 2, 3))
+    h = torch.empty(R, F, device=dev)
+    K.swiglu_fwd(cu(a), cu(u), h)
+    assert max_rel(host(h), O.swiglu_fwd(a, u)) <= TOL
+    da0, du0 = O.normal(R * F, 4).reshape(R, F), O.normal(R * F, 5).reshape(R, F)
+    da_ref, du_ref = O.swiglu_bwd(a, u, dh, da0.copy(), du0.copy())
+    da, du = cu(da0.copy()), cu(du0.copy())
+    K.swiglu_bwd(cu(a), cu(u), cu(dh), da, du, accum_da=True, accum_du=True)
+    assert max_rel(host(da), da_ref) <= TOL and max_rel(host(du), du_ref) <= TOL
+
+
+def _attn_case(dev, B, H, T, hd, q, k, v, do):
+    D = H * hd
+    o = torch.empty(B * T, D, device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    P = torch.empty(B * H * T * T, device=dev)
+    K.attn_fwd(B, H, cu(q), cu(k), cu(v), o, lse, P)
+    o_ref, lse_ref = O.attn_fwd(B, H, q, k, v)
+    assert max_rel(host(o), o_ref) <= TOL and max_rel(host(lse), lse_ref) <= TOL
+    dq, dk, dv = (torch.empty(B * T, D, device=dev) for _ in range(3))
+    ws = torch.empty(B * H * T * T, device=dev)
+    K.attn_bwd(B, H, cu(q), cu(k), cu(v), P, cu(do), dq, dk, dv, ws)
+    refs = O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)
+    for got, ref in zip((dq, dk, dv), refs):
+        assert max_rel(host(got), ref) <= TOL
+
+
+def test_attention_golden(dev):
+    B, H = int(GOLD["att_B"]), int(GOLD["att_H"])
+    _attn_case(dev, B, H, GOLD["att_q"].shape[0] // B, GOLD["att_q"].shape[1] // H,
+               GOLD["att_q"], GOLD["att_k"], GOLD["att_v"], GOLD["att_do"])
+
+
+@pytest.mark.parametrize("B,H,T,hd", [(2, 2, 128, 64), (1, 3, 256, 64), (1, 2, 200, 32)])
+def test_attention_vs_oracle(dev, B, H, T, hd):
+    D = H * hd
+    q, k, v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (1, 2, 3, 4))
+    _attn_case(dev, B, H, T, hd, q, k, v, do)
+
+
+def test_embedding(dev):
+    V, d, n = 1000, 64, 513
+    table = O.normal(V * d, 1).reshape(V, d)
+    ids = O.labels(n, 2, V)
+    out = torch.empty(n, d, device=dev)
+    K.embed_fwd(cu(ids), cu(table), out)
+    assert np.array_equal(host(out), O.embed_fwd(ids, table))
+    dout = O.normal(n * d, 3).reshape(n, d)
+    dt = torch.zeros(V, d, device=dev)
+    K.embed_bwd(cu(ids), cu(dout), dt)
+    assert max_rel(host(dt), O.embed_bwd(ids, dout, np.zeros((V, d), np.float32))) <= 1e-6
+    out = torch.empty(GOLD["emb_ids"].size, GOLD["emb_table"].shape[1], device=dev)
+    K.embed_fwd(cu(GOLD["emb_ids"]), cu(GOLD["emb_table"]), out)
+    assert np.array_equal(host(out), GOLD["emb_out"].astype(np.float32))
