@@ -35,6 +35,8 @@ def _f32(*ts):
 
 
 def _rowmajor(t, name):
+    if t.dim() == 2 and t.numel() == 0:
+        return max(1, t.shape[1])
     if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
         raise ValueError(f"{name} must be a 2-D tensor with unit column stride")
     return max(t.stride(0), t.shape[1])
