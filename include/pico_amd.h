@@ -1,0 +1,215 @@
+/*
+ * include/pico_amd.h -- pico's public C API over MI355X (gfx950) tensors.
+ *
+ * libpico_amd.so implements the operator, autograd, arena, module and
+ * optimizer API of pico (sijirama/pico) for tensors whose `backend` is GPU.
+ * Names, signatures, argument meaning and error behaviour follow the
+ * reference: an op validates its inputs, allocates its output in the calling
+ * thread's current arena, launches its kernel, wires `parents` and `_backward`,
+ * and returns the new tensor; a refused call prints "[Pico] Error: ..." on
+ * stderr and returns NULL (src/ops.c:12-54).  Backward hooks accumulate (+=)
+ * into their parents' grads (src/autograd.h:25-29).
+ *
+ * What differs, and why:
+ *  - `data` and `grad` of every tensor made here are DEVICE pointers.  Host
+ *    code must not dereference them; use pico_tensor_copy_from_host /
+ *    pico_tensor_copy_to_host / pico_tensor_grad_to_host.
+ *  - Every tensor made here is GPU-backed (pico_param, pico_create_tensor and
+ *    the ops all produce backend == GPU).  A CPU-backed tensor passed to an
+ *    op is refused with NULL: the CPU path is pico's own library, unchanged.
+ *  - Grad buffers are zero-initialised lazily: a grad that has received no
+ *    contribution reads as zeros (pico_tensor_grad_to_host) and the first
+ *    contribution overwrites instead of adding, which is bit-identical to
+ *    adding into zeros and saves one full write of every grad.
+ *  - An arena owns a device arena beside its host blocks: tensor structs,
+ *    shapes and parent lists live in host memory, tensor data in one device
+ *    block per arena block.  arena_reset rewinds both in O(#blocks) and keeps
+ *    the device blocks for the next step; an allocation larger than a block
+ *    gets a block of its own size (the reference's growth cannot serve it,
+ *    src/arena.h:78-116).
+ *  - Kernels run asynchronously on one HIP stream (pico_gpu_stream).  The
+ *    copy helpers synchronise it.  A failed launch inside a backward hook
+ *    prints "[Pico] Error: ..." and is kept for pico_gpu_last_error().
+ *
+ * Every declaration below cites the reference interface it replaces.
+ */
+#pragma once
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- core types: identical layout to src/tensor.h:9-23 and src/arena.h:20-29 ---- */
+typedef enum { CPU, GPU } PicoBackend;
+
+struct PicoTensor {
+    int64_t* shape;
+    int64_t* strides;
+    float* data; /* device memory */
+    float* grad; /* device memory */
+    void (*_backward)(struct PicoTensor*);
+    struct PicoTensor** parents;
+    int64_t numel;
+    PicoBackend backend;
+    uint8_t ndim;
+    uint8_t num_parents;
+    uint8_t is_persistent;
+};
+
+struct ArenaBlock {
+    struct ArenaBlock* next;
+    size_t capacity;
+    unsigned char* bottom;
+    unsigned char* curr;
+};
+
+struct PicoDeviceBlock;
+
+/* pico's two-pointer arena (src/arena.h:27-29) plus its device twin */
+struct Arena {
+    struct ArenaBlock *begin, *end;
+    struct PicoDeviceBlock *dev_begin, *dev_end;
+    size_t dev_block_bytes;
+};
+
+/* ---- init (src/global.c:29-75) ----
+ * pico_init brings up HIP on device 0 (or $PICO_DEVICE) and creates the
+ * library's stream; it is idempotent and called by every entry point that
+ * needs the device. */
+void pico_init(void);
+void pico_shutdown(void);
+
+/* ---- arena (src/arena.h:38-169; there they are static inline) ---- */
+struct Arena* arena_init(size_t bytes);
+void* arena_alloc(struct Arena* arena, size_t size);
+void arena_reset(struct Arena* arena);
+void arena_destroy(struct Arena* arena);
+void arena_ctx_push(struct Arena* arena);
+void arena_ctx_pop(void);
+struct Arena* arena_ctx_current(void);
+/* device memory from the arena's device twin, 256-byte aligned */
+void* arena_alloc_device(struct Arena* arena, size_t size);
+
+/* ---- tensors (src/tensor.h:25-57, src/tensor.c) ---- */
+void pico_backward(struct Arena* arena, struct PicoTensor* entry); /* tensor.c:15-42 */
+struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim);       /* tensor.c:44-84 */
+struct PicoTensor* pico_create_tensor(struct Arena* arena, int64_t* shape,
+                                      uint8_t ndim);               /* tensor.c:86-134 */
+struct PicoTensor* pico_tensor_from_scalar(float value);           /* tensor.c:173-188 */
+void pico_free(struct PicoTensor* tensor);                         /* tensor.c:136-168 */
+void pico_tensor_print(struct PicoTensor* t);                      /* tensor.c:210-228 */
+void pico_transpose_2d(struct PicoTensor* tensor);                 /* tensor.c:230-244 */
+/* uniform [0,1) from pico's xorshift32 stream (tensor.c:249-273), drawn on the
+ * host in the reference's order and copied to the device */
+struct PicoTensor* pico_rand(struct Arena* arena, int64_t* shape, uint8_t ndim);
+/* N(0,1) over all numel elements (flat Box-Muller, u1 in (0,1]).  The
+ * reference's pico_randn (tensor.c:348-367) halves the last dim and can take
+ * log(0); this one returns the requested shape. */
+struct PicoTensor* pico_randn(struct Arena* arena, int64_t* shape, uint8_t ndim);
+uint8_t pico_check_broadcast_compatibility(struct PicoTensor* a,
+                                           struct PicoTensor* b); /* tensor.c:371-397 */
+/* xorshift32 state of pico_rand (src/global.c:13) */
+extern uint32_t x_state;
+
+/* ---- ops (src/ops.h:5-18, src/act/activations.h:12) ---- */
+struct PicoTensor* pico_add(struct PicoTensor* a, struct PicoTensor* b);
+struct PicoTensor* pico_sub(struct PicoTensor* a, struct PicoTensor* b);
+struct PicoTensor* pico_mul(struct PicoTensor* a, struct PicoTensor* b);
+struct PicoTensor* pico_matmul(struct PicoTensor* a, struct PicoTensor* b);
+struct PicoTensor* pico_tensor_sqrt(struct PicoTensor* a);
+struct PicoTensor* pico_tensor_sin(struct PicoTensor* a);
+struct PicoTensor* pico_tensor_cos(struct PicoTensor* a);
+struct PicoTensor* pico_tensor_tan(struct PicoTensor* a);
+struct PicoTensor* pico_tensor_tanh(struct PicoTensor* a);
+struct PicoTensor* pico_tensor_log(struct PicoTensor* a);
+struct PicoTensor* pico_relu(struct PicoTensor* x);
+
+/* The GPU twins of the op seam the reference leaves commented out
+ * (src/ops.c:42-44, 86-88, 130-132): `out` is pre-allocated by the caller with
+ * the broadcast shape (matmul: [rows(a), cols(b)]), as pico's CPU kernels
+ * expect (src/kernels/cpu_kernels.h:13-55).  Return 0 or a pk_* status. */
+int pico_add_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out);
+int pico_sub_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out);
+int pico_mul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out);
+int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out);
+/* GPU twins of the backward hooks (src/autograd.h:53-130, act/autograd.h:9-17) */
+void pico_add_backward_gpu(struct PicoTensor* self);
+void pico_sub_backward_gpu(struct PicoTensor* self);
+void pico_mul_backward_gpu(struct PicoTensor* self);
+void pico_matmul_backward_gpu(struct PicoTensor* self);
+void pico_relu_backward_gpu(struct PicoTensor* self);
+
+/* ---- hot-path ops the reference lacks (no reference
+ * code: the softmax Jacobian comment at src/autograd.h:38-40 and the plan at
+ * todo.md:95 are the only traces).  Same op template as src/ops.c:12-54.
+ * `labels` / `ids` are int32 arrays in host or device memory; host arrays are
+ * staged into the current arena's device memory. ---- */
+/* loss [1] = mean_r (logsumexp(z_r) - z_r[labels[r]]) over logits [R, V] */
+struct PicoTensor* pico_softmax_xent(struct PicoTensor* logits, const int32_t* labels);
+/* y = x * rstd * gain over the last dim of x [R, C], rstd = (mean(x^2) + eps)^-1/2 */
+struct PicoTensor* pico_rmsnorm(struct PicoTensor* x, struct PicoTensor* gain, float eps);
+/* h = silu(a) * u, a and u of the same shape */
+struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u);
+/* causal softmax(q k^T / sqrt(hd)) v per head; q, k, v token-major
+ * [batch*T, n_heads*hd] */
+struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor* k,
+                                         struct PicoTensor* v, int batch, int n_heads);
+/* out [n, d] = table[ids] for table [vocab, d] */
+struct PicoTensor* pico_embedding(struct PicoTensor* table, const int32_t* ids, int64_t n);
+/* idx[r] = first argmax of row r of x [R, V]; idx is host memory (R int32) */
+int pico_argmax(struct PicoTensor* x, int32_t* idx);
+
+/* ---- nn (src/nn/linear.h:6-15) ---- */
+struct PicoLinear {
+    int in_features;
+    int out_features;
+    struct PicoTensor* weights; /* [in, out] */
+    struct PicoTensor* bias;    /* [out] */
+};
+struct PicoLinear* pico_nn_linear_init(int in_features, int out_features, bool bias);
+struct PicoTensor* pico_nn_linear_forward(struct PicoLinear* layer, struct PicoTensor* input);
+void pico_nn_linear_free(struct PicoLinear* linear);
+
+/* ---- optim (src/optim/optim.h:7-16) ---- */
+struct PicoOptimSGD;
+struct PicoOptimSGD* pico_optim_sgd_init(float lr);
+void pico_optim_sgd_add(struct PicoOptimSGD* optim, struct PicoTensor* param);
+void pico_optim_sgd_step(struct PicoOptimSGD* optim);
+void pico_optim_sgd_zero_grad(struct PicoOptimSGD* optim);
+void pico_optim_sgd_free(struct PicoOptimSGD* optim);
+
+/* AdamW with decoupled weight decay (the reference only names Adam,
+ * src/optim/optim.h:19-23):  p <- p(1 - lr wd);  m <- b1 m + (1-b1) g;
+ * v <- b2 v + (1-b2) g^2;  p <- p - lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps) */
+struct PicoOptimAdamW;
+struct PicoOptimAdamW* pico_optim_adamw_init(float lr, float beta1, float beta2, float eps,
+                                             float weight_decay);
+void pico_optim_adamw_add(struct PicoOptimAdamW* optim, struct PicoTensor* param);
+void pico_optim_adamw_step(struct PicoOptimAdamW* optim);
+void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* optim);
+void pico_optim_adamw_free(struct PicoOptimAdamW* optim);
+
+/* ---- host <-> device (no reference counterpart: pico's data is host memory) ----
+ * Each copies numel floats of the tensor's storage and synchronises the
+ * stream; 0 on success. */
+int pico_tensor_copy_from_host(struct PicoTensor* t, const float* src);
+int pico_tensor_copy_to_host(const struct PicoTensor* t, float* dst);
+int pico_tensor_grad_to_host(const struct PicoTensor* t, float* dst);
+int pico_tensor_grad_from_host(struct PicoTensor* t, const float* src);
+/* device copy of n int32 values in the current arena (NULL on failure) */
+int32_t* pico_ids_to_device(const int32_t* host_ids, int64_t n);
+
+/* ---- runtime ---- */
+int pico_gpu_synchronize(void);
+void* pico_gpu_stream(void);            /* the hipStream_t every launch uses */
+void pico_gpu_set_stream(void* stream); /* NULL restores the library's own */
+const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
+void pico_gpu_clear_error(void);
+
+#ifdef __cplusplus
+}
+#endif

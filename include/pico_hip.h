@@ -33,6 +33,7 @@ typedef void* pk_stream_t; /* a hipStream_t; NULL is the null stream */
 
 #define PK_ACCUM 1
 #define PK_ACCUM2 2
+#define PK_ACCUM3 4
 
 /* ---- runtime ---------------------------------------------------------- */
 const char* pk_last_error(void);
@@ -77,8 +78,10 @@ int pk_binary_f32(int op, int ndim, const int64_t* out_shape, const int64_t* a_s
  * x[j] of  g[i]            (add; or sub for operand a)
  *          -g[i]           (sub, operand b: which = 1)
  *          g[i] * other[i] (mul)
- * x_shape/x_ndim are the operand's own shape (gx is contiguous in it),
- * x_strides / other_strides are mapped onto the output dims as above. */
+ * x_strides / other_strides are each operand's element strides mapped onto
+ * the output dims as above (0 on a broadcast dim); gx is laid out with x's
+ * strides, as pico's grads share their tensor's strides (src/autograd.h:61-63),
+ * and x_numel is the number of elements x holds. */
 int pk_binary_bwd_f32(int op, int which, int ndim, const int64_t* out_shape,
                       const int64_t* x_strides, const int64_t* other_strides, int64_t x_numel,
                       const float* gout, const float* other, float* gx, int flags,
@@ -113,11 +116,13 @@ int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps, float
 /* ---- fused row kernels (no reference code; planned at todo.md:95) --------
  * softmax cross-entropy, one pass over each row of logits [R,V] (row stride ldz):
  *   loss_rows[r] = logsumexp(z_r) - z_r[labels[r]]        (if loss_rows != NULL)
- *   dlogits[r,:] (+)= scale * (softmax(z_r) - onehot(y_r)) (if dlogits != NULL)
+ *   dlogits[r,:] (+)= s * (softmax(z_r) - onehot(y_r))     (if dlogits != NULL)
+ * with s = scale * (*scale_dev) when scale_dev (a device float, e.g. the
+ * upstream gradient of the loss) is non-NULL, else s = scale.
  * A label outside [0,V) gives NaN loss and a zero gradient row. */
 int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, int64_t ldz,
                         const int32_t* labels, float* loss_rows, float* dlogits, int64_t ldd,
-                        float scale, int flags, pk_stream_t stream);
+                        float scale, const float* scale_dev, int flags, pk_stream_t stream);
 /* idx[r] = argmax_j x[r,j]: first maximum wins; a NaN is the maximum (first NaN wins) */
 int pk_argmax_f32(int64_t R, int64_t V, const float* x, int64_t ldx, int32_t* idx,
                   pk_stream_t stream);
@@ -150,7 +155,10 @@ int pk_swiglu_bwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const f
 int pk_attn_causal_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
                            const float* q, const float* k, const float* v, float* o, float* lse,
                            float* P, pk_stream_t stream);
-/* dq, dk, dv (+)= gradients; flags bit 0 accumulates all three */
+/* dq, dk, dv (+)= gradients: flags bit 0 (PK_ACCUM) accumulates dq, bit 1
+ * (PK_ACCUM2) dk, bit 2 (PK_ACCUM3) dv; a NULL gradient pointer is skipped.
+ * The writes happen in the order dv, dq, dk, so aliased outputs accumulate
+ * correctly when the later ones carry their accumulate bit. */
 int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
                            const float* q, const float* k, const float* v, const float* P,
                            const float* dout, float* dq, float* dk, float* dv, float* dP_ws,

@@ -48,7 +48,8 @@ PK_SIGNATURES = {
     "pk_reduce_sum_f32": [c_i64, c_p, c_f, c_p, c_int, c_p],
     "pk_sgd_f32": [c_i64, c_f, c_p, c_p, c_p],
     "pk_adamw_f32": [c_i64, c_f, c_f, c_f, c_f, c_f, c_int, c_p, c_p, c_p, c_p, c_p],
-    "pk_xent_fwd_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p, c_i64, c_f, c_int, c_p],
+    "pk_xent_fwd_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p, c_i64, c_f, c_p, c_int,
+                            c_p],
     "pk_argmax_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "pk_rmsnorm_fwd_f32": [c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p],
     "pk_rmsnorm_bwd_workspace": [c_i64, c_i64],

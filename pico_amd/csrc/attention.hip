@@ -45,25 +45,27 @@ extern "C" int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t h
     if(!q || !k || !v || !P || !dout || !dP_ws)
         return pk::fail("pk_attn_causal_bwd_f32: NULL input pointer");
     const int64_t D = H * hd, BH = B * H;
-    const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+    const float beta_q = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+    const float beta_k = (flags & PK_ACCUM2) ? 1.0f : 0.0f;
+    const float beta_v = (flags & PK_ACCUM3) ? 1.0f : 0.0f;
     int rc = pk_gemm_batched_f32('N', 'T', T, T, hd, 1.0f, dout, D, T * D, hd, v, D, T * D, hd,
                                  0.0f, dP_ws, T, H * T * T, T * T, BH, H, 1, stream);
     if(rc) return rc;
     if(dv) {
         rc = pk_gemm_batched_f32('T', 'N', T, hd, T, 1.0f, P, T, H * T * T, T * T, dout, D, T * D,
-                                 hd, beta, dv, D, T * D, hd, BH, H, 3, stream);
+                                 hd, beta_v, dv, D, T * D, hd, BH, H, 3, stream);
         if(rc) return rc;
     }
     rc = pk_causal_softmax_bwd_f32(BH, T, P, dP_ws, dP_ws, stream);
     if(rc) return rc;
     if(dq) {
         rc = pk_gemm_batched_f32('N', 'N', T, hd, T, scale, dP_ws, T, H * T * T, T * T, k, D,
-                                 T * D, hd, beta, dq, D, T * D, hd, BH, H, 2, stream);
+                                 T * D, hd, beta_q, dq, D, T * D, hd, BH, H, 2, stream);
         if(rc) return rc;
     }
     if(dk) {
         rc = pk_gemm_batched_f32('T', 'N', T, hd, T, scale, dP_ws, T, H * T * T, T * T, q, D,
-                                 T * D, hd, beta, dk, D, T * D, hd, BH, H, 3, stream);
+                                 T * D, hd, beta_k, dk, D, T * D, hd, BH, H, 3, stream);
         if(rc) return rc;
     }
     return PK_OK;

@@ -60,13 +60,15 @@ __global__ void binary_same4(int op, int64_t n4, const f32x4* __restrict__ a,
 }
 
 // Gradient of one operand x.  The output dims split into "kept" dims (x has
-// them) and "reduced" dims (x is broadcast there).  Thread j owns gx[j] and
+// them) and "reduced" dims (x is broadcast there).  Thread j owns the j-th
+// element of x in row-major order (stored at sum c_k * kx[k], x's own strides,
+// so a transposed view's grad lands where pico's map_index puts it) and
 // walks the reduced dims in increasing flat order, adding one term at a time
 // to the running value -- the same order and rounding as the reference's
 // single pass (src/autograd.h:53-94).
 struct BwdDesc {
     int nk, nr;
-    int64_t kshape[kMaxDims], kout[kMaxDims], koth[kMaxDims];
+    int64_t kshape[kMaxDims], kout[kMaxDims], koth[kMaxDims], kx[kMaxDims];
     int64_t rshape[kMaxDims], rout[kMaxDims], roth[kMaxDims];
     int64_t red_numel;
 };
@@ -81,14 +83,15 @@ __global__ void binary_bwd_reduce(int op, int which, BwdDesc d, int64_t xn,
                                   float* __restrict__ gx, int accum) {
     for(int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; j < xn;
         j += (int64_t)gridDim.x * blockDim.x) {
-        int64_t rem = j, bo = 0, bt = 0;
+        int64_t rem = j, bo = 0, bt = 0, bx = 0;
         for(int k = d.nk - 1; k >= 0; --k) {
             const int64_t c = rem % d.kshape[k];
             rem /= d.kshape[k];
             bo += c * d.kout[k];
             bt += c * d.koth[k];
+            bx += c * d.kx[k];
         }
-        float acc = accum ? gx[j] : 0.0f;
+        float acc = accum ? gx[bx] : 0.0f;
         for(int64_t r = 0; r < d.red_numel; ++r) {
             int64_t rr = r, oo = bo, ot = bt;
             for(int k = d.nr - 1; k >= 0; --k) {
@@ -103,7 +106,7 @@ __global__ void binary_bwd_reduce(int op, int which, BwdDesc d, int64_t xn,
             else
                 acc += grad_term(op, which, gout[oo], op == 2 ? other[ot] : 0.0f);
         }
-        gx[j] = acc;
+        gx[bx] = acc;
     }
 }
 
@@ -320,6 +323,7 @@ extern "C" int pk_binary_bwd_f32(int op, int which, int ndim, const int64_t* out
             d.kshape[d.nk] = out_shape[k];
             d.kout[d.nk] = out_stride[k];
             d.koth[d.nk] = other_strides[k];
+            d.kx[d.nk] = x_strides[k];
             d.nk++;
             kept_numel *= out_shape[k];
         } else {

@@ -22,8 +22,11 @@ __global__ __launch_bounds__(NT) void xent_reg_kernel(int64_t V, const float* __
                                                       int64_t ldz, const int32_t* __restrict__ labels,
                                                       float* __restrict__ loss_rows,
                                                       float* __restrict__ dlogits, int64_t ldd,
-                                                      float scale, int accum) {
+                                                      float scale_in,
+                                                      const float* __restrict__ scale_dev,
+                                                      int accum) {
     __shared__ float red[NT / 64];
+    const float scale = scale_dev ? scale_in * *scale_dev : scale_in;
     const int64_t r = blockIdx.x;
     const f32x4* z4 = reinterpret_cast<const f32x4*>(logits + r * ldz);
     const int64_t V4 = V / 4;
@@ -77,8 +80,11 @@ __global__ __launch_bounds__(NT) void xent_any_kernel(int64_t V, const float* __
                                                       int64_t ldz, const int32_t* __restrict__ labels,
                                                       float* __restrict__ loss_rows,
                                                       float* __restrict__ dlogits, int64_t ldd,
-                                                      float scale, int accum) {
+                                                      float scale_in,
+                                                      const float* __restrict__ scale_dev,
+                                                      int accum) {
     __shared__ float red[NT / 64];
+    const float scale = scale_dev ? scale_in * *scale_dev : scale_in;
     const int64_t r = blockIdx.x;
     const float* z = logits + r * ldz;
     float m = kNegInf, s = 0.0f;
@@ -545,7 +551,8 @@ int pick_nv(int64_t C) {
 
 extern "C" int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, int64_t ldz,
                                    const int32_t* labels, float* loss_rows, float* dlogits,
-                                   int64_t ldd, float scale, int flags, pk_stream_t stream) {
+                                   int64_t ldd, float scale, const float* scale_dev, int flags,
+                                   pk_stream_t stream) {
     if(R < 0 || V < 1) return pk::fail("pk_xent_fwd_bwd_f32: need R >= 0 and V >= 1");
     if(R == 0) return PK_OK;
     if(R > 0x7fffffff) return pk::fail("pk_xent_fwd_bwd_f32: too many rows");
@@ -558,17 +565,17 @@ extern "C" int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, in
     const int64_t V4 = V / 4;
     dim3 grid((unsigned)R);
     if(vec && V4 <= 256 * 1)
-        xent_reg_kernel<256, 1><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_reg_kernel<256, 1><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     else if(vec && V4 <= 256 * 2)
-        xent_reg_kernel<256, 2><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_reg_kernel<256, 2><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     else if(vec && V4 <= 256 * 4)
-        xent_reg_kernel<256, 4><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_reg_kernel<256, 4><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     else if(vec && V4 <= 256 * 8)
-        xent_reg_kernel<256, 8><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_reg_kernel<256, 8><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     else if(vec && V4 <= 1024 * 8)
-        xent_reg_kernel<1024, 8><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_reg_kernel<1024, 8><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     else
-        xent_any_kernel<1024><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, accum);
+        xent_any_kernel<1024><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
     return pk::launch_status("pk_xent_fwd_bwd_f32");
 }
 

@@ -1,0 +1,310 @@
+/*
+ * pico_amd/host/newops.c -- the hot-path ops pico does not have, in pico's op
+ * style (src/ops.c:12-54) over GPU tensors: fused softmax cross-entropy,
+ * RMSNorm, SwiGLU, causal attention, embedding, argmax.
+ *
+ * No reference code exists for these (the only traces are the softmax
+ * Jacobian comment at src/autograd.h:38-40 and the plan at todo.md:95).
+ * Their backward hooks keep the += contract of src/autograd.h:25-29.  Saved
+ * state (rstd, lse, probabilities, staged labels) lives in the node and in
+ * the arena's device memory, so it is released by arena_reset.
+ */
+#include <math.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+static int need_gpu(const char* op, const struct PicoTensor* t) {
+    if(!t) {
+        PKH_ERR("%s: NULL tensor!\n", op);
+        return 1;
+    }
+    if(!pkh_is_gpu(t)) {
+        PKH_ERR("%s: this library runs backend GPU; CPU tensors belong to pico's CPU library!\n",
+                op);
+        return 1;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------ softmax cross-entropy
+ * loss [1] = mean_r (logsumexp(z_r) - z_r[y_r]).  The forward pass reads the
+ * logits once and, when the logits' grad holds nothing yet, also writes the
+ * gradient of the mean, (softmax - onehot)/R, into that grad buffer.  If the
+ * backward then finds the upstream gradient is exactly pico_backward's seed
+ * of 1 and the buffer still untouched, it only marks it live: one pass over
+ * the logits instead of two.  Otherwise it recomputes, scaled by the upstream
+ * gradient on the device. */
+enum { XS_LABELS = 0, XS_ROWS = 1 };
+enum { XI_PRECOMPUTED = 0 };
+
+static void xent_backward(struct PicoTensor* self) {
+    struct PkNode* n = pkh_node(self);
+    struct PicoTensor* z = self->parents[0];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    int64_t R = z->shape[0], V = z->shape[1];
+    if(n->ival[XI_PRECOMPUTED] && n->seed_one && !pkh_grad_is_live(z)) {
+        n->ival[XI_PRECOMPUTED] = 0;
+        pkh_grad_mark(z);
+        return;
+    }
+    n->ival[XI_PRECOMPUTED] = 0;
+    int st = pk_xent_fwd_bwd_f32(R, V, z->data, V, (const int32_t*)n->saved[XS_LABELS], NULL,
+                                 z->grad, V, 1.0f / (float)R, g, pkh_grad_flag(z), pkh_stream());
+    if(pkh_status("pico_softmax_xent_backward", st)) return;
+    pkh_grad_mark(z);
+}
+
+struct PicoTensor* pico_softmax_xent(struct PicoTensor* logits, const int32_t* labels) {
+    if(need_gpu("pico_softmax_xent", logits)) return NULL;
+    if(logits->ndim != 2 || logits->strides[1] != 1 || logits->strides[0] != logits->shape[1]) {
+        PKH_ERR("softmax_xent expects contiguous 2-D logits [rows, classes]!\n");
+        return NULL;
+    }
+    if(!labels) {
+        PKH_ERR("softmax_xent: NULL labels!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    int64_t R = logits->shape[0], V = logits->shape[1];
+    const int32_t* dl = pkh_ids_on_device(labels, R);
+    if(!dl) return NULL;
+    int64_t one[1] = {1};
+    struct PicoTensor* out = pkh_new_tensor(arena, one, 1);
+    if(!out) return NULL;
+    struct PkNode* n = pkh_node(out);
+    float* rows = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(R > 0 ? R : 1));
+    if(!rows) return NULL;
+    n->saved[XS_LABELS] = (void*)dl;
+    n->saved[XS_ROWS] = rows;
+    int pre = !pkh_grad_is_live(logits);
+    int st = pk_xent_fwd_bwd_f32(R, V, logits->data, V, dl, rows, pre ? logits->grad : NULL, V,
+                                 1.0f / (float)(R > 0 ? R : 1), NULL, 0, pkh_stream());
+    if(pkh_status("pico_softmax_xent", st)) return NULL;
+    st = pk_reduce_sum_f32(R, rows, 1.0f / (float)(R > 0 ? R : 1), out->data, 0, pkh_stream());
+    if(pkh_status("pico_softmax_xent", st)) return NULL;
+    n->ival[XI_PRECOMPUTED] = pre;
+    pkh_set_parents(arena, out, 1, &logits, xent_backward);
+    return out;
+}
+
+/* ---------------------------------------------------------------- RMSNorm
+ * y = x * rstd * gain over the last dim; the backward reads the saved rstd */
+enum { RS_RSTD = 0 };
+
+static void rms_backward(struct PicoTensor* self) {
+    struct PkNode* n = pkh_node(self);
+    struct PicoTensor *x = self->parents[0], *gain = self->parents[1];
+    const float* dy = pkh_upstream(self);
+    if(!dy) return;
+    int64_t C = x->shape[x->ndim - 1], R = C ? x->numel / C : 0;
+    size_t ws_bytes = pk_rmsnorm_bwd_workspace(R, C);
+    void* ws = pkh_workspace(ws_bytes);
+    if(!ws && ws_bytes) return;
+    int flags = (pkh_grad_flag(x) ? PK_ACCUM : 0) | (pkh_grad_flag(gain) ? PK_ACCUM2 : 0);
+    int st = pk_rmsnorm_bwd_f32(R, C, x->data, gain->data, (const float*)n->saved[RS_RSTD], dy,
+                                x->grad, gain->grad, flags, ws, ws_bytes, pkh_stream());
+    if(pkh_status("pico_rmsnorm_backward", st)) return;
+    pkh_grad_mark(x);
+    pkh_grad_mark(gain);
+}
+
+struct PicoTensor* pico_rmsnorm(struct PicoTensor* x, struct PicoTensor* gain, float eps) {
+    if(need_gpu("pico_rmsnorm", x) || need_gpu("pico_rmsnorm", gain)) return NULL;
+    if(x->ndim < 1 || gain->numel != x->shape[x->ndim - 1] || x == gain) {
+        PKH_ERR("rmsnorm expects x [rows, C] and gain [C]!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    int64_t C = x->shape[x->ndim - 1], R = C ? x->numel / C : 0;
+    struct PicoTensor* out = pkh_new_tensor(arena, x->shape, x->ndim);
+    if(!out) return NULL;
+    struct PkNode* n = pkh_node(out);
+    float* rstd = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(R > 0 ? R : 1));
+    if(!rstd) return NULL;
+    n->saved[RS_RSTD] = rstd;
+    n->fval[0] = eps;
+    int st = pk_rmsnorm_fwd_f32(R, C, eps, x->data, gain->data, out->data, rstd, pkh_stream());
+    if(pkh_status("pico_rmsnorm", st)) return NULL;
+    struct PicoTensor* ps[2] = {x, gain};
+    pkh_set_parents(arena, out, 2, ps, rms_backward);
+    return out;
+}
+
+/* ----------------------------------------------------------------- SwiGLU */
+static void swiglu_backward(struct PicoTensor* self) {
+    struct PicoTensor *a = self->parents[0], *u = self->parents[1];
+    const float* dh = pkh_upstream(self);
+    if(!dh) return;
+    int64_t F = a->shape[a->ndim - 1], R = F ? a->numel / F : 0;
+    if(a == u) {
+        /* h = silu(a)*a: two passes so the second accumulates onto the first */
+        int st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, a->grad, NULL, F,
+                                   pkh_grad_flag(a), pkh_stream());
+        if(pkh_status("pico_swiglu_backward", st)) return;
+        pkh_grad_mark(a);
+        st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, NULL, u->grad, F, PK_ACCUM2,
+                               pkh_stream());
+        pkh_status("pico_swiglu_backward", st);
+        return;
+    }
+    int flags = (pkh_grad_flag(a) ? PK_ACCUM : 0) | (pkh_grad_flag(u) ? PK_ACCUM2 : 0);
+    int st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, a->grad, u->grad, F, flags,
+                               pkh_stream());
+    if(pkh_status("pico_swiglu_backward", st)) return;
+    pkh_grad_mark(a);
+    pkh_grad_mark(u);
+}
+
+struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
+    if(need_gpu("pico_swiglu", a) || need_gpu("pico_swiglu", u)) return NULL;
+    if(a->numel != u->numel || a->ndim != u->ndim ||
+       memcmp(a->shape, u->shape, sizeof(int64_t) * a->ndim) != 0) {
+        PKH_ERR("swiglu expects gate and up of the same shape!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    int64_t F = a->shape[a->ndim - 1], R = F ? a->numel / F : 0;
+    struct PicoTensor* out = pkh_new_tensor(arena, a->shape, a->ndim);
+    if(!out) return NULL;
+    int st = pk_swiglu_fwd_f32(R, F, a->data, F, u->data, F, out->data, F, pkh_stream());
+    if(pkh_status("pico_swiglu", st)) return NULL;
+    struct PicoTensor* ps[2] = {a, u};
+    pkh_set_parents(arena, out, 2, ps, swiglu_backward);
+    return out;
+}
+
+/* -------------------------------------------------------- causal attention
+ * q, k, v token-major [batch*T, heads*hd]; out the same.  Saved: lse [B*H*T]
+ * and the probabilities P [B*H, T, T] (arena device memory). */
+enum { AS_LSE = 0, AS_P = 1 };
+enum { AI_B = 0, AI_H = 1 };
+
+static void attn_backward(struct PicoTensor* self) {
+    struct PkNode* n = pkh_node(self);
+    struct PicoTensor *q = self->parents[0], *k = self->parents[1], *v = self->parents[2];
+    const float* dout = pkh_upstream(self);
+    if(!dout) return;
+    int64_t B = n->ival[AI_B], H = n->ival[AI_H];
+    int64_t T = q->shape[0] / B, hd = q->shape[1] / H;
+    void* ws = pkh_workspace(sizeof(float) * (size_t)(B * H * T * T));
+    if(!ws) return;
+    /* the launcher writes dv, then dq, then dk: aliased grads accumulate */
+    int flags = 0;
+    if(pkh_grad_flag(v)) flags |= PK_ACCUM3;
+    pkh_grad_mark(v);
+    if(pkh_grad_flag(q)) flags |= PK_ACCUM;
+    pkh_grad_mark(q);
+    if(pkh_grad_flag(k)) flags |= PK_ACCUM2;
+    pkh_grad_mark(k);
+    int st = pk_attn_causal_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+                                    (const float*)n->saved[AS_P], dout, q->grad, k->grad, v->grad,
+                                    (float*)ws, flags, pkh_stream());
+    pkh_status("pico_attention_causal_backward", st);
+}
+
+struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor* k,
+                                         struct PicoTensor* v, int batch, int n_heads) {
+    if(need_gpu("pico_attention_causal", q) || need_gpu("pico_attention_causal", k) ||
+       need_gpu("pico_attention_causal", v))
+        return NULL;
+    int contiguous = 1;
+    struct PicoTensor* xs[3] = {q, k, v};
+    for(int i = 0; i < 3; i++)
+        if(xs[i]->ndim != 2 || xs[i]->strides[1] != 1 || xs[i]->strides[0] != xs[i]->shape[1])
+            contiguous = 0;
+    if(!contiguous || q->shape[0] != k->shape[0] || q->shape[1] != k->shape[1] ||
+       q->shape[0] != v->shape[0] || q->shape[1] != v->shape[1] || batch <= 0 || n_heads <= 0 ||
+       q->shape[0] % batch || q->shape[1] % n_heads) {
+        PKH_ERR("attention expects q, k, v [batch*T, heads*hd]!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    int64_t B = batch, H = n_heads, T = q->shape[0] / batch, hd = q->shape[1] / n_heads;
+    struct PicoTensor* out = pkh_new_tensor(arena, q->shape, 2);
+    if(!out) return NULL;
+    struct PkNode* n = pkh_node(out);
+    float* lse = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T));
+    float* P = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T));
+    if(!lse || !P) return NULL;
+    n->saved[AS_LSE] = lse;
+    n->saved[AS_P] = P;
+    n->ival[AI_B] = B;
+    n->ival[AI_H] = H;
+    n->fval[0] = 1.0f / sqrtf((float)hd);
+    int st = pk_attn_causal_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data, out->data,
+                                    lse, P, pkh_stream());
+    if(pkh_status("pico_attention_causal", st)) return NULL;
+    pkh_set_parents(arena, out, 3, xs, attn_backward);
+    return out;
+}
+
+/* -------------------------------------------------------------- embedding
+ * out [n, d] = table[ids]; the backward scatter-adds rows into table.grad */
+enum { ES_IDS = 0 };
+
+static void emb_backward(struct PicoTensor* self) {
+    struct PkNode* n = pkh_node(self);
+    struct PicoTensor* tab = self->parents[0];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    int64_t V = tab->shape[0], d = tab->shape[1];
+    if(!pkh_grad_is_live(tab)) {
+        /* scatter-add needs a zeroed target */
+        if(pkh_status("pico_embedding_backward", pk_fill_f32(tab->numel, 0.0f, tab->grad,
+                                                               pkh_stream())))
+            return;
+        pkh_grad_mark(tab);
+    }
+    int st = pk_embed_bwd_f32(self->shape[0], d, V, (const int32_t*)n->saved[ES_IDS], g,
+                              tab->grad, pkh_stream());
+    pkh_status("pico_embedding_backward", st);
+}
+
+struct PicoTensor* pico_embedding(struct PicoTensor* table, const int32_t* ids, int64_t n_ids) {
+    if(need_gpu("pico_embedding", table)) return NULL;
+    if(table->ndim != 2 || table->strides[1] != 1 || table->strides[0] != table->shape[1]) {
+        PKH_ERR("embedding expects a contiguous 2-D table [vocab, d]!\n");
+        return NULL;
+    }
+    if(!ids || n_ids < 0) {
+        PKH_ERR("embedding: NULL ids or negative count!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    const int32_t* dids = pkh_ids_on_device(ids, n_ids);
+    if(!dids && n_ids) return NULL;
+    int64_t shape[2] = {n_ids, table->shape[1]};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    pkh_node(out)->saved[ES_IDS] = (void*)dids;
+    int st = pk_embed_fwd_f32(n_ids, table->shape[1], table->shape[0], dids, table->data, out->data,
+                              pkh_stream());
+    if(pkh_status("pico_embedding", st)) return NULL;
+    pkh_set_parents(arena, out, 1, &table, emb_backward);
+    return out;
+}
+
+/* ----------------------------------------------------------------- argmax */
+int pico_argmax(struct PicoTensor* x, int32_t* idx) {
+    if(need_gpu("pico_argmax", x)) return PK_EINVAL;
+    if(x->ndim != 2 || x->strides[1] != 1 || !idx) {
+        PKH_ERR("argmax expects 2-D x [rows, V] with contiguous rows and an output array!\n");
+        return PK_EINVAL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return PK_EINVAL;
+    int64_t R = x->shape[0], V = x->shape[1];
+    if(R == 0) return 0;
+    int32_t* d = (int32_t*)arena_alloc_device(arena, sizeof(int32_t) * (size_t)R);
+    if(!d) return PK_EINVAL;
+    int st = pk_argmax_f32(R, V, x->data, x->strides[0], d, pkh_stream());
+    if(pkh_status("pico_argmax", st)) return st;
+    return pkh_copy_d2h(idx, d, sizeof(int32_t) * (size_t)R);
+}

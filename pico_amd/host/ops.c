@@ -1,0 +1,310 @@
+/*
+ * pico_amd/host/ops.c -- pico's op layer for GPU tensors: add/sub/mul with
+ * broadcasting, 2-D matmul, unary math, relu, their backward hooks, and the
+ * GPU twins of the op seam the reference leaves as commented-out stubs
+ * (src/ops.c:42-44, 86-88, 130-132).
+ *
+ * Each op keeps the reference's template (src/ops.c:12-54): validate in the
+ * same order with the same messages, take the current arena, allocate the
+ * output there, launch, wire parents and _backward.  The launches go to the
+ * pk_* layer (include/pico_hip.h); nothing here touches device data.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+enum { OP_ADD = 0, OP_SUB = 1, OP_MUL = 2 };
+enum { U_SQRT = 0, U_SIN, U_COS, U_TAN, U_TANH, U_LOG };
+
+static int refuse_cpu(const char* op, const struct PicoTensor* a) {
+    if(pkh_is_gpu(a)) return 0;
+    PKH_ERR("%s: this library runs backend GPU; CPU tensors belong to pico's CPU library!\n", op);
+    return 1;
+}
+
+/* strides of t mapped onto an ndim-dim output (0 where t is broadcast), the
+ * map pico's map_index applies per element (src/tensor.h:122-138) */
+static void mapped_strides(const struct PicoTensor* t, int ndim, int64_t* out) {
+    int diff = ndim - t->ndim;
+    for(int d = 0; d < ndim; d++) {
+        int sd = d - diff;
+        out[d] = (sd >= 0 && t->shape[sd] > 1) ? t->strides[sd] : 0;
+    }
+}
+
+/* ---------------------------------------------------- binary: seam twins */
+static int binary_gpu(int op, struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    int64_t sa[256], sb[256];
+    int nd = out->ndim;
+    mapped_strides(a, nd, sa);
+    mapped_strides(b, nd, sb);
+    return pk_binary_f32(op, nd, out->shape, sa, sb, a->data, b->data, out->data, pkh_stream());
+}
+
+int pico_add_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    return pkh_status("pico_add", binary_gpu(OP_ADD, a, b, out));
+}
+int pico_sub_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    return pkh_status("pico_sub", binary_gpu(OP_SUB, a, b, out));
+}
+int pico_mul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    return pkh_status("pico_mul", binary_gpu(OP_MUL, a, b, out));
+}
+
+/* src/autograd.h:53-94: a.grad += g (or g*b), b.grad += g (-g, g*a), summed
+ * over each operand's broadcast dims */
+static void binary_backward(int op, struct PicoTensor* self) {
+    struct PicoTensor *a = self->parents[0], *b = self->parents[1];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    int64_t sa[256], sb[256];
+    int nd = self->ndim;
+    mapped_strides(a, nd, sa);
+    mapped_strides(b, nd, sb);
+    static const char* names[3] = {"pico_add_backward", "pico_sub_backward", "pico_mul_backward"};
+    int st = pk_binary_bwd_f32(op, 0, nd, self->shape, sa, sb, a->numel, g, b->data, a->grad,
+                               pkh_grad_flag(a), pkh_stream());
+    if(pkh_status(names[op], st)) return;
+    pkh_grad_mark(a);
+    st = pk_binary_bwd_f32(op, 1, nd, self->shape, sb, sa, b->numel, g, a->data, b->grad,
+                           pkh_grad_flag(b), pkh_stream());
+    if(pkh_status(names[op], st)) return;
+    pkh_grad_mark(b);
+}
+void pico_add_backward_gpu(struct PicoTensor* self) { binary_backward(OP_ADD, self); }
+void pico_sub_backward_gpu(struct PicoTensor* self) { binary_backward(OP_SUB, self); }
+void pico_mul_backward_gpu(struct PicoTensor* self) { binary_backward(OP_MUL, self); }
+
+/* src/ops.c:12-142 */
+static struct PicoTensor* binary_op(int op, const char* name, struct PicoTensor* a,
+                                    struct PicoTensor* b, void (*bw)(struct PicoTensor*)) {
+    if(!a || !b) {
+        PKH_ERR("%s: NULL tensor!\n", name);
+        return NULL;
+    }
+    if(!pico_check_broadcast_compatibility(a, b)) {
+        PKH_ERR("Shapes are not broadcastable!\n");
+        return NULL;
+    }
+    if(a->backend != b->backend) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu(name, a)) return NULL;
+    int ndim = a->ndim > b->ndim ? a->ndim : b->ndim;
+    int64_t shape[256];
+    for(int i = 0; i < ndim; i++) {
+        int ia = i - (ndim - a->ndim), ib = i - (ndim - b->ndim);
+        int64_t da = ia >= 0 ? a->shape[ia] : 1, db = ib >= 0 ? b->shape[ib] : 1;
+        shape[i] = da > db ? da : db;
+    }
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, ndim);
+    if(!out) return NULL;
+    if(pkh_status(name, binary_gpu(op, a, b, out))) return NULL;
+    struct PicoTensor* ps[2] = {a, b};
+    pkh_set_parents(arena, out, 2, ps, bw);
+    return out;
+}
+
+struct PicoTensor* pico_add(struct PicoTensor* a, struct PicoTensor* b) {
+    return binary_op(OP_ADD, "pico_add", a, b, pico_add_backward_gpu);
+}
+struct PicoTensor* pico_sub(struct PicoTensor* a, struct PicoTensor* b) {
+    return binary_op(OP_SUB, "pico_sub", a, b, pico_sub_backward_gpu);
+}
+struct PicoTensor* pico_mul(struct PicoTensor* a, struct PicoTensor* b) {
+    return binary_op(OP_MUL, "pico_mul", a, b, pico_mul_backward_gpu);
+}
+
+/* ------------------------------------------------------------------ GEMM */
+/* 'N' when rows are contiguous (strides[1] == 1, ld = strides[0]); 'T' when
+ * columns are (strides[0] == 1, ld = strides[1]).  With a single row (or
+ * column) the leading dimension is never stepped and only has to satisfy the
+ * launcher's minimum. */
+int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m) {
+    if(x->ndim != 2) return PK_EINVAL;
+    int64_t rows = x->shape[0], cols = x->shape[1], s0 = x->strides[0], s1 = x->strides[1];
+    m->p = base;
+    if(s1 == 1 && (rows <= 1 || s0 >= cols)) {
+        m->t = 'N';
+        m->ld = s0 > cols ? s0 : cols;
+    } else if(s0 == 1 && (cols <= 1 || s1 >= rows)) {
+        m->t = 'T';
+        m->ld = s1 > rows ? s1 : rows;
+    } else {
+        return PK_EINVAL;
+    }
+    if(m->ld < 1) m->ld = 1;
+    return 0;
+}
+
+static inline char flip(char t) { return t == 'N' ? 'T' : 'N'; }
+
+int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
+             int64_t ldc, int flags) {
+    const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+    if(tc == 'N')
+        return pk_gemm_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc,
+                           pkh_stream());
+    /* C stored transposed: produce C^T [N, M] = B^T . A^T */
+    return pk_gemm_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
+                       pkh_stream());
+}
+
+static int matmul_views(struct PicoTensor* a, struct PicoTensor* b, struct PkMat* va,
+                        struct PkMat* vb) {
+    if(pkh_mat_view(a, a->data, va) || pkh_mat_view(b, b->data, vb)) {
+        pkh_set_error("pico_matmul: operands must have a unit stride along one dimension");
+        PKH_ERR("pico_matmul: operands must have a unit stride along one dimension!\n");
+        return PK_EINVAL;
+    }
+    return 0;
+}
+
+/* out = a . b, out contiguous [rows(a), cols(b)] (pico's kernels += into a
+ * zeroed out, src/kernels/cpu/cpu_scalar.h:39-54; here it is overwritten) */
+int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return PK_EINVAL;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    return pkh_status("pico_matmul",
+                      pkh_gemm(va, vb, M, N, K, out->data, 'N', N > 0 ? N : 1, 0));
+}
+
+/* src/autograd.h:96-130: dA += dC . B^T, then dB += A^T . dC.  Each grad is
+ * laid out with its tensor's strides, so a transposed view's grad is
+ * produced transposed. */
+void pico_matmul_backward_gpu(struct PicoTensor* self) {
+    struct PicoTensor *a = self->parents[0], *b = self->parents[1];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    struct PkMat dC = {g, 'N', N > 0 ? N : 1};
+    struct PkMat BT = {b->data, flip(vb.t), vb.ld};
+    struct PkMat AT = {a->data, flip(va.t), va.ld};
+    int st = pkh_gemm(dC, BT, M, K, N, a->grad, va.t, va.ld, pkh_grad_flag(a));
+    if(pkh_status("pico_matmul_backward", st)) return;
+    pkh_grad_mark(a);
+    st = pkh_gemm(AT, dC, K, N, M, b->grad, vb.t, vb.ld, pkh_grad_flag(b));
+    if(pkh_status("pico_matmul_backward", st)) return;
+    pkh_grad_mark(b);
+}
+
+/* src/ops.c:144-190 (checks in the reference's order) */
+struct PicoTensor* pico_matmul(struct PicoTensor* a, struct PicoTensor* b) {
+    if(!a || !b) {
+        PKH_ERR("pico_matmul: NULL tensor!\n");
+        return NULL;
+    }
+    if(a->shape[a->ndim - 1] != b->shape[0]) {
+        PKH_ERR("2 matmuls matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->ndim != 2 || b->ndim != 2) {
+        PKH_ERR("2d matmul matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->backend != b->backend) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu("pico_matmul", a)) return NULL;
+    int64_t shape[2] = {a->shape[0], b->shape[1]};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    if(pico_matmul_gpu(a, b, out)) return NULL;
+    struct PicoTensor* ps[2] = {a, b};
+    pkh_set_parents(arena, out, 2, ps, pico_matmul_backward_gpu);
+    return out;
+}
+
+/* ----------------------------------------------------------------- unary */
+/* src/ops.c:198-328 / src/autograd.h:132-176: elementwise over the flat
+ * buffer, output contiguous in the input's shape */
+static void unary_backward(int op, struct PicoTensor* self) {
+    struct PicoTensor* a = self->parents[0];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    int st = pk_unary_bwd_f32(op, self->numel, a->data, self->data, g, a->grad, pkh_grad_flag(a),
+                              pkh_stream());
+    if(pkh_status("pico_tensor_unary_backward", st)) return;
+    pkh_grad_mark(a);
+}
+static void sqrt_bw(struct PicoTensor* s) { unary_backward(U_SQRT, s); }
+static void sin_bw(struct PicoTensor* s) { unary_backward(U_SIN, s); }
+static void cos_bw(struct PicoTensor* s) { unary_backward(U_COS, s); }
+static void tan_bw(struct PicoTensor* s) { unary_backward(U_TAN, s); }
+static void tanh_bw(struct PicoTensor* s) { unary_backward(U_TANH, s); }
+static void log_bw(struct PicoTensor* s) { unary_backward(U_LOG, s); }
+
+static struct PicoTensor* unary_op(int op, const char* name, struct PicoTensor* a,
+                                   void (*bw)(struct PicoTensor*)) {
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(!a) {
+        PKH_ERR("%s: NULL tensor!\n", name);
+        return NULL;
+    }
+    if(refuse_cpu(name, a)) return NULL;
+    struct PicoTensor* out = pkh_new_tensor(arena, a->shape, a->ndim);
+    if(!out) return NULL;
+    if(pkh_status(name, pk_unary_f32(op, a->numel, a->data, out->data, pkh_stream())))
+        return NULL;
+    pkh_set_parents(arena, out, 1, &a, bw);
+    return out;
+}
+
+struct PicoTensor* pico_tensor_sqrt(struct PicoTensor* a) {
+    return unary_op(U_SQRT, "pico_tensor_sqrt", a, sqrt_bw);
+}
+struct PicoTensor* pico_tensor_sin(struct PicoTensor* a) {
+    return unary_op(U_SIN, "pico_tensor_sin", a, sin_bw);
+}
+struct PicoTensor* pico_tensor_cos(struct PicoTensor* a) {
+    return unary_op(U_COS, "pico_tensor_cos", a, cos_bw);
+}
+struct PicoTensor* pico_tensor_tan(struct PicoTensor* a) {
+    return unary_op(U_TAN, "pico_tensor_tan", a, tan_bw);
+}
+struct PicoTensor* pico_tensor_tanh(struct PicoTensor* a) {
+    return unary_op(U_TANH, "pico_tensor_tanh", a, tanh_bw);
+}
+struct PicoTensor* pico_tensor_log(struct PicoTensor* a) {
+    return unary_op(U_LOG, "pico_tensor_log", a, log_bw);
+}
+
+/* ------------------------------------------------------------------ relu */
+/* src/act/autograd.h:9-17: parent.grad += g * (y > 0) */
+void pico_relu_backward_gpu(struct PicoTensor* self) {
+    struct PicoTensor* x = self->parents[0];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    int st = pk_relu_bwd_f32(x->numel, self->data, g, x->grad, pkh_grad_flag(x), pkh_stream());
+    if(pkh_status("pico_relu_backward", st)) return;
+    pkh_grad_mark(x);
+}
+
+/* src/act/activations.c:8-26 (the output is GPU-backed like its input; the
+ * reference leaves relu's output on the CPU backend) */
+struct PicoTensor* pico_relu(struct PicoTensor* x) {
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(!x) {
+        PKH_ERR("pico_relu: NULL tensor!\n");
+        return NULL;
+    }
+    if(refuse_cpu("pico_relu", x)) return NULL;
+    struct PicoTensor* out = pkh_new_tensor(arena, x->shape, x->ndim);
+    if(!out) return NULL;
+    if(pkh_status("pico_relu", pk_relu_f32(x->numel, x->data, out->data, pkh_stream())))
+        return NULL;
+    pkh_set_parents(arena, out, 1, &x, pico_relu_backward_gpu);
+    return out;
+}

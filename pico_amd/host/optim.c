@@ -1,0 +1,195 @@
+/*
+ * pico_amd/host/optim.c -- SGD (src/optim/SGD.c:16-52) and AdamW over GPU
+ * params, and pico's Linear layer (src/nn/linear.c:9-77).
+ *
+ * The optimizers mutate params in place, as the reference's contract says
+ * (docs/contracts/01-allocation-and-ownership.md:43-46).  zero_grad marks each
+ * grad as holding nothing (it then reads as zeros and the next contribution
+ * overwrites it), which is what the reference's zero-fill achieves, without
+ * a pass over memory.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+struct ParamList {
+    struct PicoTensor** v;
+    int n, cap;
+};
+
+static int pl_push(struct ParamList* l, struct PicoTensor* t) {
+    if(l->n == l->cap) {
+        int cap = l->cap ? 2 * l->cap : 16;
+        struct PicoTensor** nv = (struct PicoTensor**)realloc(l->v, sizeof(*nv) * cap);
+        if(!nv) return -1;
+        l->v = nv;
+        l->cap = cap;
+    }
+    l->v[l->n++] = t;
+    return 0;
+}
+
+static void zero_grads(struct ParamList* l) {
+    for(int i = 0; i < l->n; i++) {
+        struct PkNode* n = pkh_node(l->v[i]);
+        if(n) n->grad_live = 0;
+    }
+}
+
+/* ----------------------------------------------------------------- SGD */
+struct PicoOptimSGD {
+    struct ParamList params;
+    float lr;
+};
+
+struct PicoOptimSGD* pico_optim_sgd_init(float lr) {
+    struct PicoOptimSGD* o = (struct PicoOptimSGD*)calloc(1, sizeof(*o));
+    if(o) o->lr = lr;
+    return o;
+}
+
+void pico_optim_sgd_add(struct PicoOptimSGD* o, struct PicoTensor* p) {
+    if(!o || !p) return;
+    if(!pkh_node(p) || !pkh_is_gpu(p)) {
+        PKH_ERR("SGD: param is not a GPU tensor of this library!\n");
+        return;
+    }
+    pl_push(&o->params, p);
+}
+
+/* p -= lr * g (src/optim/SGD.c:29-37); a grad holding nothing is zero, and
+ * p - lr*0 == p, so such params are skipped */
+void pico_optim_sgd_step(struct PicoOptimSGD* o) {
+    for(int i = 0; i < o->params.n; i++) {
+        struct PicoTensor* p = o->params.v[i];
+        if(!pkh_grad_is_live(p)) continue;
+        pkh_status("pico_optim_sgd_step", pk_sgd_f32(p->numel, o->lr, p->data, p->grad,
+                                                     pkh_stream()));
+    }
+}
+
+void pico_optim_sgd_zero_grad(struct PicoOptimSGD* o) { zero_grads(&o->params); }
+
+void pico_optim_sgd_free(struct PicoOptimSGD* o) {
+    if(!o) return;
+    free(o->params.v);
+    free(o);
+}
+
+/* --------------------------------------------------------------- AdamW */
+struct PicoOptimAdamW {
+    struct ParamList params;
+    float** m; /* device moment buffers, one allocation per param (m then v) */
+    float lr, beta1, beta2, eps, wd;
+    int t;
+};
+
+struct PicoOptimAdamW* pico_optim_adamw_init(float lr, float beta1, float beta2, float eps,
+                                             float weight_decay) {
+    struct PicoOptimAdamW* o = (struct PicoOptimAdamW*)calloc(1, sizeof(*o));
+    if(!o) return NULL;
+    o->lr = lr;
+    o->beta1 = beta1;
+    o->beta2 = beta2;
+    o->eps = eps;
+    o->wd = weight_decay;
+    return o;
+}
+
+void pico_optim_adamw_add(struct PicoOptimAdamW* o, struct PicoTensor* p) {
+    if(!o || !p) return;
+    if(!pkh_node(p) || !pkh_is_gpu(p)) {
+        PKH_ERR("AdamW: param is not a GPU tensor of this library!\n");
+        return;
+    }
+    if(pl_push(&o->params, p)) return;
+    float** nm = (float**)realloc(o->m, sizeof(float*) * o->params.cap);
+    if(!nm) return;
+    o->m = nm;
+    size_t half = ((size_t)p->numel * sizeof(float) + 255) & ~(size_t)255;
+    float* buf = (float*)pkh_device_alloc(2 * (half ? half : 256));
+    o->m[o->params.n - 1] = buf;
+    if(buf)
+        pkh_status("pico_optim_adamw_add",
+                   pk_fill_f32((int64_t)(2 * half / sizeof(float)), 0.0f, buf, pkh_stream()));
+}
+
+void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
+    o->t++;
+    for(int i = 0; i < o->params.n; i++) {
+        struct PicoTensor* p = o->params.v[i];
+        float* m = o->m[i];
+        if(!m) continue;
+        size_t half = ((size_t)p->numel * sizeof(float) + 255) & ~(size_t)255;
+        float* v = (float*)((unsigned char*)m + half);
+        const float* g = pkh_grad_is_live(p) ? p->grad : NULL;
+        pkh_status("pico_optim_adamw_step",
+                   pk_adamw_f32(p->numel, o->lr, o->beta1, o->beta2, o->eps, o->wd, o->t, p->data,
+                                g, m, v, pkh_stream()));
+    }
+}
+
+void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* o) { zero_grads(&o->params); }
+
+void pico_optim_adamw_free(struct PicoOptimAdamW* o) {
+    if(!o) return;
+    pkh_sync();
+    for(int i = 0; i < o->params.n; i++) pkh_device_free(o->m[i]);
+    free(o->m);
+    free(o->params.v);
+    free(o);
+}
+
+/* -------------------------------------------------------------- Linear */
+/* src/nn/linear.c:9-38: W [in, out] and b [out], both zero-initialised */
+struct PicoLinear* pico_nn_linear_init(int in_features, int out_features, bool bias) {
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    int64_t wshape[2] = {in_features, out_features};
+    int64_t bshape[1] = {out_features};
+    struct PicoTensor* w = pico_param(wshape, 2);
+    struct PicoTensor* b = bias ? pico_param(bshape, 1) : NULL;
+    struct PicoLinear* l = (struct PicoLinear*)malloc(sizeof(*l));
+    if(!l || !w || (bias && !b)) {
+        pico_free(w);
+        pico_free(b);
+        free(l);
+        return NULL;
+    }
+    l->weights = w;
+    l->bias = b;
+    l->in_features = in_features;
+    l->out_features = out_features;
+    return l;
+}
+
+/* src/nn/linear.c:40-67: x . W, then + b broadcast over rows */
+struct PicoTensor* pico_nn_linear_forward(struct PicoLinear* layer, struct PicoTensor* input) {
+    if(!layer || !input) {
+        PKH_ERR("In Linear - NULL layer or input!\n");
+        return NULL;
+    }
+    if(input->shape[input->ndim - 1] != layer->weights->shape[0]) {
+        PKH_ERR(" In Linear - 2 matmuls matrices must be compatible\n");
+        return NULL;
+    }
+    if(layer->weights->backend != input->backend) {
+        PKH_ERR("In Linear - PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    if(!arena_ctx_current()) {
+        PKH_ERR("In Linear - No current arena in context!\n");
+        return NULL;
+    }
+    struct PicoTensor* out = pico_matmul(input, layer->weights);
+    if(out && layer->bias) out = pico_add(out, layer->bias);
+    return out;
+}
+
+void pico_nn_linear_free(struct PicoLinear* l) {
+    if(!l) return;
+    pico_free(l->weights);
+    pico_free(l->bias);
+    free(l);
+}

@@ -1,0 +1,102 @@
+/*
+ * pico_amd/host/pk_host.h -- internals shared by the C11 host side of the
+ * MI355X backend (libpico_amd.so): the node that carries every tensor this
+ * library makes, lazy-grad bookkeeping, error reporting, device workspace.
+ */
+#pragma once
+
+#include <stdint.h>
+#include <stdio.h>
+
+#include "pico_amd.h"
+#include "pico_hip.h"
+
+/* everything declared below is internal to libpico_amd.so */
+#pragma GCC visibility push(hidden)
+
+#define PKH_MAGIC 0x4E4B5050u /* "PPKN" */
+#define PKH_MAX_SAVED 4
+
+/* Every tensor made by this library is the first member of a node.  The node
+ * adds what pico's struct has no room for: whether the grad buffer holds
+ * values yet (lazy zeroing), a traversal mark for pico_backward, and the
+ * state an op's backward needs (saved device buffers and sizes). */
+struct PkNode {
+    struct PicoTensor t;
+    uint32_t magic;
+    uint32_t grad_live;
+    uint64_t visit;
+    uint32_t seed_one; /* this node is the entry pico_backward seeded with 1 */
+    uint32_t pad_;
+    void* saved[PKH_MAX_SAVED];
+    int64_t ival[PKH_MAX_SAVED];
+    float fval[PKH_MAX_SAVED];
+};
+
+static inline struct PkNode* pkh_node(const struct PicoTensor* t) {
+    struct PkNode* n = (struct PkNode*)t;
+    return (n && n->magic == PKH_MAGIC) ? n : NULL;
+}
+
+/* runtime (runtime.c) */
+int pkh_init(void);              /* 0 once the device and stream are up */
+pk_stream_t pkh_stream(void);
+void pkh_set_error(const char* fmt, ...);
+/* maps a launcher status to the pico convention: prints "[Pico] Error: op: msg"
+ * and records it; returns status */
+int pkh_status(const char* op, int status);
+int pkh_sync(void);
+void* pkh_device_alloc(size_t bytes); /* hipMalloc; NULL + message on failure */
+void pkh_device_free(void* p);
+/* a device scratch buffer of at least `bytes`, reused across calls (the
+ * previous contents are not preserved); valid until the next call */
+void* pkh_workspace(size_t bytes);
+int pkh_is_device_ptr(const void* p);
+int pkh_copy_h2d(void* dst, const void* src, size_t bytes);
+int pkh_copy_d2h(void* dst, const void* src, size_t bytes);
+
+/* tensors (tensor.c) */
+/* a GPU tensor node in `arena` with uninitialised device data and a
+ * not-yet-live grad; `node_bytes` >= sizeof(struct PkNode) */
+struct PicoTensor* pkh_new_tensor(struct Arena* arena, const int64_t* shape, int ndim);
+struct Arena* pkh_need_arena(void);
+int pkh_is_gpu(const struct PicoTensor* t);
+/* flags for a write into t->grad: PK_ACCUM if it already holds values; the
+ * caller marks it live after a successful launch */
+static inline int pkh_grad_flag(const struct PicoTensor* t) {
+    struct PkNode* n = pkh_node(t);
+    return (n && !n->grad_live) ? 0 : PK_ACCUM;
+}
+static inline void pkh_grad_mark(struct PicoTensor* t) {
+    struct PkNode* n = pkh_node(t);
+    if(n) n->grad_live = 1;
+}
+static inline int pkh_grad_is_live(const struct PicoTensor* t) {
+    struct PkNode* n = pkh_node(t);
+    return n ? (int)n->grad_live : 1;
+}
+void pkh_set_parents(struct Arena* arena, struct PicoTensor* out, int n,
+                     struct PicoTensor* const* ps, void (*bw)(struct PicoTensor*));
+/* the grad of `self` as the upstream gradient; NULL (nothing to propagate)
+ * when it holds no values */
+const float* pkh_upstream(struct PicoTensor* self);
+/* int32 ids/labels on the device: device pointers pass through, host arrays
+ * are copied into the current arena */
+const int32_t* pkh_ids_on_device(const int32_t* ids, int64_t n);
+
+/* matrix view of a 2-D tensor for the GEMM launcher: 'N' when rows are
+ * contiguous (strides[1] == 1), 'T' when columns are (strides[0] == 1) */
+struct PkMat {
+    const float* p;
+    char t;
+    int64_t ld;
+};
+int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m);
+/* C (+)= A . B for logical matrices A [M,K], B [K,N]; C is stored as the
+ * view `c` describes (a transposed C is produced as C^T = B^T A^T) */
+int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
+             int64_t ldc, int flags);
+
+#pragma GCC visibility pop
+
+#define PKH_ERR(...) fprintf(stderr, "[Pico] Error: " __VA_ARGS__)

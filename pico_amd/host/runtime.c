@@ -1,0 +1,156 @@
+/*
+ * pico_amd/host/runtime.c -- device bring-up, the library's stream, error
+ * reporting and device memory helpers for libpico_amd.so.
+ *
+ * pico's pico_init (src/global.c:29-69) selects a SIMD level, a GPU enum and
+ * starts its thread pool; here it selects the HIP device ($PICO_DEVICE, else
+ * 0) and creates one non-blocking stream at default priority that every
+ * launch of this library uses.
+ */
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+uint32_t x_state = 123456789u; /* src/global.c:13 */
+
+static int g_ready = 0;
+static int g_device = 0;
+static hipStream_t g_own_stream = NULL;
+static hipStream_t g_user_stream = NULL;
+static int g_user_stream_set = 0;
+static char g_err[512] = "";
+
+static void* g_ws = NULL;
+static size_t g_ws_bytes = 0;
+
+void pkh_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+int pkh_init(void) {
+    if(g_ready) return 0;
+    const char* env = getenv("PICO_DEVICE");
+    g_device = env ? atoi(env) : 0;
+    hipError_t e = hipSetDevice(g_device);
+    if(e == hipSuccess) e = hipStreamCreateWithFlags(&g_own_stream, hipStreamNonBlocking);
+    if(e != hipSuccess) {
+        pkh_set_error("pico_init: HIP device %d unavailable: %s", g_device, hipGetErrorString(e));
+        PKH_ERR("%s\n", g_err);
+        return (int)e;
+    }
+    g_ready = 1;
+    return 0;
+}
+
+void pico_init(void) { (void)pkh_init(); }
+
+void pico_shutdown(void) {
+    if(!g_ready) return;
+    hipStreamSynchronize(g_own_stream);
+    if(g_ws) hipFree(g_ws);
+    g_ws = NULL;
+    g_ws_bytes = 0;
+    hipStreamDestroy(g_own_stream);
+    g_own_stream = NULL;
+    g_ready = 0;
+}
+
+pk_stream_t pkh_stream(void) {
+    return (pk_stream_t)(g_user_stream_set ? g_user_stream : g_own_stream);
+}
+
+void* pico_gpu_stream(void) {
+    pkh_init();
+    return (void*)pkh_stream();
+}
+
+void pico_gpu_set_stream(void* stream) {
+    g_user_stream = (hipStream_t)stream;
+    g_user_stream_set = stream != NULL;
+}
+
+int pkh_status(const char* op, int status) {
+    if(status == 0) return 0;
+    const char* msg = pk_last_error();
+    if(status != PK_EINVAL || !msg || !*msg) msg = hipGetErrorString((hipError_t)status);
+    pkh_set_error("%s: %s (status %d)", op, msg, status);
+    PKH_ERR("%s\n", g_err);
+    return status;
+}
+
+int pkh_sync(void) {
+    if(pkh_init()) return -1;
+    hipError_t e = hipStreamSynchronize((hipStream_t)pkh_stream());
+    if(e != hipSuccess) return pkh_status("pico_gpu_synchronize", (int)e);
+    return 0;
+}
+
+int pico_gpu_synchronize(void) { return pkh_sync(); }
+const char* pico_gpu_last_error(void) { return g_err; }
+void pico_gpu_clear_error(void) { g_err[0] = 0; }
+
+void* pkh_device_alloc(size_t bytes) {
+    if(pkh_init()) return NULL;
+    void* p = NULL;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
+    if(e != hipSuccess) {
+        pkh_set_error("device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+        PKH_ERR("%s\n", g_err);
+        return NULL;
+    }
+    return p;
+}
+
+void pkh_device_free(void* p) {
+    if(p) hipFree(p);
+}
+
+void* pkh_workspace(size_t bytes) {
+    if(bytes <= g_ws_bytes) return g_ws;
+    /* grow: wait for work that may still read the old buffer */
+    if(g_ws) {
+        hipStreamSynchronize((hipStream_t)pkh_stream());
+        hipFree(g_ws);
+        g_ws = NULL;
+        g_ws_bytes = 0;
+    }
+    g_ws = pkh_device_alloc(bytes);
+    if(g_ws) g_ws_bytes = bytes;
+    return g_ws;
+}
+
+int pkh_is_device_ptr(const void* p) {
+    if(!p || pkh_init()) return 0;
+    hipPointerAttribute_t attr;
+    memset(&attr, 0, sizeof(attr));
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if(e != hipSuccess) {
+        (void)hipGetLastError(); /* plain host memory: clear the sticky status */
+        return 0;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+int pkh_copy_h2d(void* dst, const void* src, size_t bytes) {
+    if(pkh_init()) return -1;
+    if(bytes == 0) return 0;
+    hipStream_t st = (hipStream_t)pkh_stream();
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
+    if(e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : pkh_status("host-to-device copy", (int)e);
+}
+
+int pkh_copy_d2h(void* dst, const void* src, size_t bytes) {
+    if(pkh_init()) return -1;
+    if(bytes == 0) return 0;
+    hipStream_t st = (hipStream_t)pkh_stream();
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st);
+    if(e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : pkh_status("device-to-host copy", (int)e);
+}

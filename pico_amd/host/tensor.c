@@ -1,0 +1,551 @@
+/*
+ * pico_amd/host/tensor.c -- arenas, GPU tensor creation, the backward walk,
+ * seeded generators and host<->device copies for libpico_amd.so.
+ *
+ * Follows the reference's contracts (docs/contracts/01-allocation-and-
+ * ownership.md): params are persistent and freed by pico_free; everything
+ * else lives in the current arena until arena_reset / arena_destroy.  Here an
+ * arena has a device twin: struct metadata stays in host blocks (pico's
+ * layout, src/arena.h:20-29), tensor data goes to device blocks.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+#define DEV_ALIGN 256
+#define HOST_ALIGN 16
+#define MAX_ARENA_STACK 16
+
+/* ------------------------------------------------------------------ arena */
+struct PicoDeviceBlock {
+    struct PicoDeviceBlock* next;
+    size_t capacity;
+    size_t used;
+    unsigned char* bottom; /* device memory */
+};
+
+static _Thread_local struct Arena* g_arena_stack[MAX_ARENA_STACK];
+static _Thread_local int g_arena_top = -1;
+
+static struct ArenaBlock* host_block_new(size_t bytes) {
+    struct ArenaBlock* b = (struct ArenaBlock*)malloc(sizeof(*b));
+    if(!b) return NULL;
+    b->bottom = (unsigned char*)malloc(bytes);
+    if(!b->bottom) {
+        free(b);
+        return NULL;
+    }
+    b->curr = b->bottom;
+    b->capacity = bytes;
+    b->next = NULL;
+    return b;
+}
+
+/* src/arena.h:38-64.  `bytes` sizes both the first host block and each device
+ * block; host blocks hold only structs, shapes and parent lists, so they are
+ * capped at 4 MiB and grow on demand. */
+struct Arena* arena_init(size_t bytes) {
+    struct Arena* a = (struct Arena*)calloc(1, sizeof(*a));
+    if(!a) return NULL;
+    size_t hb = bytes < ((size_t)4 << 20) ? bytes : ((size_t)4 << 20);
+    if(hb < 4096) hb = 4096;
+    a->begin = host_block_new(hb);
+    if(!a->begin) {
+        free(a);
+        return NULL;
+    }
+    a->end = a->begin;
+    a->dev_block_bytes = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    return a;
+}
+
+/* src/arena.h:105-116; a request larger than the block size gets a block of
+ * its own size instead of failing */
+void* arena_alloc(struct Arena* a, size_t size) {
+    size = (size + HOST_ALIGN - 1) & ~(size_t)(HOST_ALIGN - 1);
+    struct ArenaBlock* b = a->end;
+    if((size_t)(b->curr - b->bottom) + size > b->capacity) {
+        size_t cap = a->begin->capacity > size ? a->begin->capacity : size;
+        struct ArenaBlock* nb = host_block_new(cap);
+        if(!nb) {
+            printf("Memory allocation failed!\n");
+            exit(1);
+        }
+        b->next = nb;
+        a->end = nb;
+        b = nb;
+    }
+    void* p = b->curr;
+    b->curr += size;
+    return p;
+}
+
+void* arena_alloc_device(struct Arena* a, size_t size) {
+    size = (size + DEV_ALIGN - 1) & ~(size_t)(DEV_ALIGN - 1);
+    if(size == 0) size = DEV_ALIGN;
+    struct PicoDeviceBlock* b = a->dev_end;
+    while(b && b->used + size > b->capacity) b = b->next;
+    if(!b) {
+        size_t cap = a->dev_block_bytes > size ? a->dev_block_bytes : size;
+        struct PicoDeviceBlock* nb = (struct PicoDeviceBlock*)calloc(1, sizeof(*nb));
+        if(!nb) return NULL;
+        nb->bottom = (unsigned char*)pkh_device_alloc(cap);
+        if(!nb->bottom) {
+            free(nb);
+            PKH_ERR("arena: device memory exhausted (%zu bytes requested)\n", size);
+            return NULL;
+        }
+        nb->capacity = cap;
+        if(!a->dev_begin) {
+            a->dev_begin = nb;
+        } else {
+            struct PicoDeviceBlock* last = a->dev_begin;
+            while(last->next) last = last->next;
+            last->next = nb;
+        }
+        b = nb;
+    }
+    a->dev_end = b;
+    void* p = b->bottom + b->used;
+    b->used += size;
+    return p;
+}
+
+/* src/arena.h:123-136: the host side frees its extra blocks as pico does; the
+ * device blocks are rewound and kept, so a training loop allocates device
+ * memory only in its first step */
+void arena_reset(struct Arena* a) {
+    struct ArenaBlock* c = a->begin->next;
+    while(c) {
+        struct ArenaBlock* n = c->next;
+        free(c->bottom);
+        free(c);
+        c = n;
+    }
+    a->begin->curr = a->begin->bottom;
+    a->begin->next = NULL;
+    a->end = a->begin;
+    for(struct PicoDeviceBlock* d = a->dev_begin; d; d = d->next) d->used = 0;
+    a->dev_end = a->dev_begin;
+}
+
+void arena_destroy(struct Arena* a) {
+    if(!a) return;
+    if(a->dev_begin) pkh_sync();
+    struct ArenaBlock* c = a->begin;
+    while(c) {
+        struct ArenaBlock* n = c->next;
+        free(c->bottom);
+        free(c);
+        c = n;
+    }
+    struct PicoDeviceBlock* d = a->dev_begin;
+    while(d) {
+        struct PicoDeviceBlock* n = d->next;
+        pkh_device_free(d->bottom);
+        free(d);
+        d = n;
+    }
+    free(a);
+}
+
+/* src/arena.h:155-169 */
+void arena_ctx_push(struct Arena* a) {
+    if(g_arena_top + 1 >= MAX_ARENA_STACK) {
+        PKH_ERR("arena context stack overflow (max %d)\n", MAX_ARENA_STACK);
+        return;
+    }
+    g_arena_stack[++g_arena_top] = a;
+}
+void arena_ctx_pop(void) {
+    if(g_arena_top >= 0) g_arena_top--;
+}
+struct Arena* arena_ctx_current(void) {
+    if(g_arena_top < 0 || g_arena_top >= MAX_ARENA_STACK) return NULL;
+    return g_arena_stack[g_arena_top];
+}
+
+struct Arena* pkh_need_arena(void) {
+    struct Arena* a = arena_ctx_current();
+    if(!a) PKH_ERR("No current arena in context!\n");
+    return a;
+}
+
+/* ---------------------------------------------------------------- tensors */
+static int64_t numel_of(const int64_t* shape, int ndim) {
+    int64_t n = 1;
+    for(int i = 0; i < ndim; i++) n *= shape[i];
+    return n;
+}
+
+static void contig_strides(const int64_t* shape, int ndim, int64_t* st) {
+    int64_t s = 1;
+    for(int i = ndim - 1; i >= 0; i--) {
+        st[i] = s;
+        s *= shape[i];
+    }
+}
+
+int pkh_is_gpu(const struct PicoTensor* t) { return t && t->backend == GPU; }
+
+struct PicoTensor* pkh_new_tensor(struct Arena* a, const int64_t* shape, int ndim) {
+    if(pkh_init()) return NULL;
+    if(ndim < 1 || ndim > 255) {
+        PKH_ERR("tensor rank %d not supported\n", ndim);
+        return NULL;
+    }
+    struct PkNode* n = (struct PkNode*)arena_alloc(a, sizeof(struct PkNode));
+    memset(n, 0, sizeof(*n));
+    n->magic = PKH_MAGIC;
+    struct PicoTensor* t = &n->t;
+    t->ndim = (uint8_t)ndim;
+    t->shape = (int64_t*)arena_alloc(a, sizeof(int64_t) * ndim);
+    t->strides = (int64_t*)arena_alloc(a, sizeof(int64_t) * ndim);
+    memcpy(t->shape, shape, sizeof(int64_t) * ndim);
+    contig_strides(t->shape, ndim, t->strides);
+    t->numel = numel_of(shape, ndim);
+    t->backend = GPU;
+    t->data = (float*)arena_alloc_device(a, sizeof(float) * (size_t)t->numel);
+    t->grad = (float*)arena_alloc_device(a, sizeof(float) * (size_t)t->numel);
+    if(!t->data || !t->grad) return NULL;
+    return t;
+}
+
+/* src/tensor.c:86-134: data zeroed (a fill kernel), grad lazily zero */
+struct PicoTensor* pico_create_tensor(struct Arena* arena, int64_t* shape, uint8_t ndim) {
+    if(!arena) {
+        PKH_ERR("No current arena in context!\n");
+        return NULL;
+    }
+    struct PicoTensor* t = pkh_new_tensor(arena, shape, ndim);
+    if(!t) return NULL;
+    if(pkh_status("pico_create_tensor", pk_fill_f32(t->numel, 0.0f, t->data, pkh_stream())))
+        return NULL;
+    return t;
+}
+
+/* src/tensor.c:44-84: persistent, zeroed; data and grad share one allocation */
+struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
+    if(pkh_init()) return NULL;
+    if(ndim < 1) {
+        PKH_ERR("pico_param needs ndim >= 1\n");
+        return NULL;
+    }
+    struct PkNode* n = (struct PkNode*)calloc(1, sizeof(struct PkNode));
+    if(!n) {
+        printf("Memory allocation failed!\n");
+        return NULL;
+    }
+    n->magic = PKH_MAGIC;
+    struct PicoTensor* t = &n->t;
+    t->ndim = ndim;
+    t->is_persistent = 1;
+    t->backend = GPU;
+    t->shape = (int64_t*)calloc(ndim, sizeof(int64_t));
+    t->strides = (int64_t*)calloc(ndim, sizeof(int64_t));
+    if(!t->shape || !t->strides) {
+        free(t->shape);
+        free(t->strides);
+        free(n);
+        return NULL;
+    }
+    memcpy(t->shape, shape, sizeof(int64_t) * ndim);
+    contig_strides(t->shape, ndim, t->strides);
+    t->numel = numel_of(shape, ndim);
+    size_t half = ((size_t)t->numel * sizeof(float) + DEV_ALIGN - 1) & ~(size_t)(DEV_ALIGN - 1);
+    if(half == 0) half = DEV_ALIGN;
+    unsigned char* base = (unsigned char*)pkh_device_alloc(2 * half);
+    if(!base) {
+        free(t->shape);
+        free(t->strides);
+        free(n);
+        return NULL;
+    }
+    t->data = (float*)base;
+    t->grad = (float*)(base + half);
+    if(pkh_status("pico_param", pk_fill_f32(t->numel, 0.0f, t->data, pkh_stream()))) {
+        pkh_device_free(base);
+        free(t->shape);
+        free(t->strides);
+        free(n);
+        return NULL;
+    }
+    return t;
+}
+
+/* src/tensor.c:136-168 */
+void pico_free(struct PicoTensor* t) {
+    if(!t || t->is_persistent == 0) return;
+    pkh_sync();
+    free(t->shape);
+    free(t->strides);
+    pkh_device_free(t->data); /* data and grad are one allocation */
+    free(t->parents);
+    free(t);
+}
+
+/* src/tensor.c:173-188 */
+struct PicoTensor* pico_tensor_from_scalar(float value) {
+    struct Arena* a = pkh_need_arena();
+    if(!a) return NULL;
+    int64_t shape[1] = {1};
+    struct PicoTensor* t = pkh_new_tensor(a, shape, 1);
+    if(!t) return NULL;
+    if(pkh_status("pico_tensor_from_scalar", pk_fill_f32(1, value, t->data, pkh_stream())))
+        return NULL;
+    return t;
+}
+
+/* src/tensor.c:230-244 */
+void pico_transpose_2d(struct PicoTensor* t) {
+    if(t->ndim != 2) {
+        fprintf(stderr, "Error: This is not a rank 2 tensor!\n");
+        return;
+    }
+    int64_t c = t->shape[1];
+    t->shape[1] = t->shape[0];
+    t->shape[0] = c;
+    int64_t sc = t->strides[1];
+    t->strides[1] = t->strides[0];
+    t->strides[0] = sc;
+}
+
+/* src/tensor.c:371-397 */
+uint8_t pico_check_broadcast_compatibility(struct PicoTensor* a, struct PicoTensor* b) {
+    for(int i = a->ndim - 1, j = b->ndim - 1; i >= 0 && j >= 0; i--, j--) {
+        int64_t da = a->shape[i], db = b->shape[j];
+        if(da != db && da != 1 && db != 1) return 0;
+    }
+    return 1;
+}
+
+void pkh_set_parents(struct Arena* a, struct PicoTensor* out, int n, struct PicoTensor* const* ps,
+                     void (*bw)(struct PicoTensor*)) {
+    out->parents = (struct PicoTensor**)arena_alloc(a, sizeof(struct PicoTensor*) * n);
+    for(int i = 0; i < n; i++) out->parents[i] = ps[i];
+    out->num_parents = (uint8_t)n;
+    out->_backward = bw;
+}
+
+const float* pkh_upstream(struct PicoTensor* self) {
+    return pkh_grad_is_live(self) ? self->grad : NULL;
+}
+
+/* ------------------------------------------------------------ pico_rand/n */
+static inline uint32_t xorshift32(void) {
+    uint32_t x = x_state;
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    return x_state = x;
+}
+
+static inline float unit_from_bits(uint32_t r) {
+    uint32_t bits = (r >> 9) | 0x3F800000u; /* [1, 2) */
+    float f;
+    memcpy(&f, &bits, sizeof(f));
+    return f - 1.0f;
+}
+
+static struct PicoTensor* tensor_from_host_values(struct Arena* a, const int64_t* shape, int ndim,
+                                                  float* host) {
+    struct PicoTensor* t = pkh_new_tensor(a, shape, ndim);
+    if(!t) return NULL;
+    if(pkh_copy_h2d(t->data, host, sizeof(float) * (size_t)t->numel)) return NULL;
+    return t;
+}
+
+/* src/tensor.c:249-273: the same xorshift32 stream and bit construction */
+struct PicoTensor* pico_rand(struct Arena* arena, int64_t* shape, uint8_t ndim) {
+    int64_t n = numel_of(shape, ndim);
+    float* h = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    if(!h) return NULL;
+    for(int64_t i = 0; i < n; i++) h[i] = unit_from_bits(xorshift32());
+    struct PicoTensor* t = tensor_from_host_values(arena, shape, ndim, h);
+    free(h);
+    return t;
+}
+
+struct PicoTensor* pico_randn(struct Arena* arena, int64_t* shape, uint8_t ndim) {
+    int64_t n = numel_of(shape, ndim);
+    float* h = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    if(!h) return NULL;
+    const double two_pi = 6.283185307179586;
+    for(int64_t i = 0; i < n; i += 2) {
+        double u1 = 1.0 - (double)unit_from_bits(xorshift32()); /* (0, 1] */
+        double u2 = (double)unit_from_bits(xorshift32());
+        double r = sqrt(-2.0 * log(u1));
+        h[i] = (float)(r * cos(two_pi * u2));
+        if(i + 1 < n) h[i + 1] = (float)(r * sin(two_pi * u2));
+    }
+    struct PicoTensor* t = tensor_from_host_values(arena, shape, ndim, h);
+    free(h);
+    return t;
+}
+
+/* ------------------------------------------------------------- backward */
+static uint64_t g_visit_epoch = 0;
+
+struct NodeVec {
+    struct PicoTensor** v;
+    int64_t n, cap;
+};
+static int nv_push(struct NodeVec* l, struct PicoTensor* t) {
+    if(l->n == l->cap) {
+        int64_t cap = l->cap ? 2 * l->cap : 64;
+        struct PicoTensor** nv = (struct PicoTensor**)realloc(l->v, sizeof(*nv) * cap);
+        if(!nv) return -1;
+        l->v = nv;
+        l->cap = cap;
+    }
+    l->v[l->n++] = t;
+    return 0;
+}
+
+/* src/tensor.c:15-42, 399-415.  The same post-order as the reference's
+ * recursive DFS (mark on entry, parents in order, append after them), walked
+ * with an explicit stack and an epoch mark per node instead of a linear
+ * visited scan. */
+void pico_backward(struct Arena* arena, struct PicoTensor* entry) {
+    (void)arena;
+    if(!entry) return;
+    if(!pkh_node(entry) || !pkh_is_gpu(entry)) {
+        PKH_ERR("pico_backward: entry is not a GPU tensor of this library!\n");
+        return;
+    }
+    uint64_t epoch = ++g_visit_epoch;
+    struct NodeVec order = {0}, stack = {0};
+    int64_t* next = NULL;
+    int64_t next_cap = 0;
+    pkh_node(entry)->visit = epoch;
+    nv_push(&stack, entry);
+    next_cap = 64;
+    next = (int64_t*)calloc(next_cap, sizeof(int64_t));
+    while(stack.n > 0) {
+        struct PicoTensor* top = stack.v[stack.n - 1];
+        int64_t* idx = &next[stack.n - 1];
+        if(*idx < top->num_parents) {
+            struct PicoTensor* p = top->parents[(*idx)++];
+            if(!p) continue;
+            struct PkNode* pn = pkh_node(p);
+            if(!pn) {
+                PKH_ERR("pico_backward: graph holds a tensor this library did not make!\n");
+                goto done;
+            }
+            if(pn->visit == epoch) continue;
+            pn->visit = epoch;
+            if(stack.n == next_cap) {
+                next_cap *= 2;
+                next = (int64_t*)realloc(next, sizeof(int64_t) * next_cap);
+            }
+            next[stack.n] = 0;
+            nv_push(&stack, p);
+        } else {
+            stack.n--;
+            nv_push(&order, top);
+        }
+    }
+    /* seed dL/dentry = 1 over every element (tensor.c:27-30) */
+    if(pkh_status("pico_backward", pk_fill_f32(entry->numel, 1.0f, entry->grad, pkh_stream())))
+        goto done;
+    pkh_grad_mark(entry);
+    pkh_node(entry)->seed_one = 1;
+    for(int64_t i = order.n - 1; i >= 0; i--) {
+        struct PicoTensor* t = order.v[i];
+        if(t->_backward) t->_backward(t);
+    }
+    pkh_node(entry)->seed_one = 0;
+done:
+    free(order.v);
+    free(stack.v);
+    free(next);
+}
+
+/* ----------------------------------------------------------------- copies */
+int pico_tensor_copy_from_host(struct PicoTensor* t, const float* src) {
+    if(!t || !pkh_is_gpu(t)) return PK_EINVAL;
+    return pkh_copy_h2d(t->data, src, sizeof(float) * (size_t)t->numel);
+}
+
+int pico_tensor_copy_to_host(const struct PicoTensor* t, float* dst) {
+    if(!t || !pkh_is_gpu(t)) return PK_EINVAL;
+    return pkh_copy_d2h(dst, t->data, sizeof(float) * (size_t)t->numel);
+}
+
+int pico_tensor_grad_to_host(const struct PicoTensor* t, float* dst) {
+    if(!t || !pkh_is_gpu(t)) return PK_EINVAL;
+    if(!pkh_grad_is_live(t)) {
+        memset(dst, 0, sizeof(float) * (size_t)t->numel);
+        return 0;
+    }
+    return pkh_copy_d2h(dst, t->grad, sizeof(float) * (size_t)t->numel);
+}
+
+int pico_tensor_grad_from_host(struct PicoTensor* t, const float* src) {
+    if(!t || !pkh_is_gpu(t)) return PK_EINVAL;
+    int rc = pkh_copy_h2d(t->grad, src, sizeof(float) * (size_t)t->numel);
+    if(rc == 0) pkh_grad_mark(t);
+    return rc;
+}
+
+int32_t* pico_ids_to_device(const int32_t* host_ids, int64_t n) {
+    struct Arena* a = pkh_need_arena();
+    if(!a || n < 0) return NULL;
+    int32_t* d = (int32_t*)arena_alloc_device(a, sizeof(int32_t) * (size_t)(n > 0 ? n : 1));
+    if(!d) return NULL;
+    if(n > 0 && pkh_copy_h2d(d, host_ids, sizeof(int32_t) * (size_t)n)) return NULL;
+    return d;
+}
+
+const int32_t* pkh_ids_on_device(const int32_t* ids, int64_t n) {
+    if(!ids) return NULL;
+    if(pkh_is_device_ptr(ids)) return ids;
+    return pico_ids_to_device(ids, n);
+}
+
+/* src/tensor.c:190-228, reading the device data back first */
+static void print_rec(const struct PicoTensor* t, const float* h, int dim, int64_t off) {
+    if(dim == t->ndim - 1) {
+        printf("[");
+        for(int64_t i = 0; i < t->shape[dim]; i++) {
+            printf("%g", h[off + i * t->strides[dim]]);
+            if(i != t->shape[dim] - 1) printf(", ");
+        }
+        printf("]");
+        return;
+    }
+    printf("[");
+    for(int64_t i = 0; i < t->shape[dim]; i++) {
+        print_rec(t, h, dim + 1, off + i * t->strides[dim]);
+        if(i != t->shape[dim] - 1) printf(",\n ");
+    }
+    printf("]");
+}
+
+void pico_tensor_print(struct PicoTensor* t) {
+    if(!t) {
+        printf("PicoTensor(NULL)\n");
+        return;
+    }
+    printf("PicoTensor(shape=[");
+    for(int i = 0; i < t->ndim; i++) {
+        printf("%ld", (long)t->shape[i]);
+        if(i != t->ndim - 1) printf(", ");
+    }
+    printf("], numel=%ld)\n", (long)t->numel);
+    if(t->ndim == 0 || !t->data) {
+        printf("(no data)\n");
+        return;
+    }
+    float* h = (float*)malloc(sizeof(float) * (size_t)(t->numel > 0 ? t->numel : 1));
+    if(!h || pico_tensor_copy_to_host(t, h)) {
+        free(h);
+        printf("(device read failed)\n");
+        return;
+    }
+    print_rec(t, h, 0, 0);
+    printf("\n");
+    free(h);
+}

@@ -164,14 +164,15 @@ def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step):
     return p
 
 
-def xent_fwd_bwd(logits, labels, loss_rows=None, dlogits=None, scale=1.0, accumulate=False):
+def xent_fwd_bwd(logits, labels, loss_rows=None, dlogits=None, scale=1.0, accumulate=False,
+                 scale_dev=None):
     R, V = logits.shape
     if labels.dtype != torch.int32 or labels.numel() != R:
         raise ValueError("labels must be int32 with one entry per row")
     check("pk_xent_fwd_bwd_f32", hip_lib().pk_xent_fwd_bwd_f32(
         R, V, _ptr(logits), _rowmajor(logits, "logits"), _ptr(labels), _ptr(loss_rows),
         _ptr(dlogits), V if dlogits is None else _rowmajor(dlogits, "dlogits"), scale,
-        ACCUM if accumulate else 0, _stream()))
+        _ptr(scale_dev), ACCUM if accumulate else 0, _stream()))
 
 
 def argmax(x, idx):
@@ -239,7 +240,7 @@ def attn_bwd(B, H, q, k, v, P, dout, dq, dk, dv, dP_ws, accumulate=False, scale=
     scale = hd ** -0.5 if scale is None else scale
     check("pk_attn_causal_bwd_f32", hip_lib().pk_attn_causal_bwd_f32(
         B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(P), _ptr(dout), _ptr(dq), _ptr(dk),
-        _ptr(dv), _ptr(dP_ws), ACCUM if accumulate else 0, _stream()))
+        _ptr(dv), _ptr(dP_ws), 7 if accumulate else 0, _stream()))
 
 
 def causal_softmax_fwd(BH, T, S, P, lse, scale=1.0):
