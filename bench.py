@@ -162,6 +162,90 @@ def rows_section(torch, K):
     return res
 
 
+TRAIN_CONFIGS = {
+    "config4": dict(vocab=8192, d_model=512, n_layers=1, n_heads=8, d_ff=1376, batch=16,
+                    seq_len=256),
+    "config5": dict(vocab=32000, d_model=768, n_layers=12, n_heads=12, d_ff=2048, batch=8,
+                    seq_len=1024),
+}
+ADAMW = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+
+
+def train_flop_per_step(cfg):
+    """6 x GEMM params x tokens, plus dense causal-attention products
+    (QK^T and PV forward, 2x that backward) counted over the full T x T"""
+    d, F, V, L = cfg["d_model"], cfg["d_ff"], cfg["vocab"], cfg["n_layers"]
+    tok = cfg["batch"] * cfg["seq_len"]
+    gemm_params = L * (4 * d * d + 3 * d * F) + d * V
+    attn = L * 3 * 2 * 2 * cfg["batch"] * cfg["seq_len"] ** 2 * d
+    return 6.0 * gemm_params * tok + attn
+
+
+def train_section(name, steps, warmup):
+    """one AdamW training step of the transformer per step, inputs resident"""
+    import numpy as np
+
+    from pico_amd.pico import Pico
+
+    cfg = TRAIN_CONFIGS[name]
+    P = Pico()
+    lib = P.lib
+    model = P.gpt_init(cfg, 20261201)
+    n = cfg["batch"] * cfg["seq_len"]
+    # synthetic token stream: inputs and next-token targets, uniform ids
+    rng = np.random.default_rng(20261201)
+    seq = rng.integers(0, cfg["vocab"], (cfg["batch"], cfg["seq_len"] + 1), dtype=np.int32)
+    data = lib.arena_init(1 << 20)
+    lib.arena_ctx_push(data)
+    tok = lib.pico_ids_to_device(P.ids(np.ascontiguousarray(seq[:, :-1])), n)
+    tgt = lib.pico_ids_to_device(P.ids(np.ascontiguousarray(seq[:, 1:])), n)
+    lib.arena_ctx_pop()
+    opt = lib.pico_optim_adamw_init(ADAMW["lr"], ADAMW["beta1"], ADAMW["beta2"], ADAMW["eps"],
+                                    ADAMW["weight_decay"])
+    for t in P.gpt_params(model):
+        lib.pico_optim_adamw_add(opt, t)
+    work = lib.arena_init(1 << 30)
+    lib.arena_ctx_push(work)
+    losses = []
+
+    def step(keep_loss):
+        loss = lib.pico_gpt_loss(model, tok, tgt)
+        if not loss:
+            raise RuntimeError("pico_gpt_loss failed")
+        lib.pico_optim_adamw_zero_grad(opt)
+        lib.pico_backward(work, loss)
+        lib.pico_optim_adamw_step(opt)
+        if keep_loss:
+            losses.append(float(P.data(loss)[0]))
+        lib.arena_reset(work)
+
+    for i in range(warmup):
+        step(keep_loss=(i == 0))
+    P.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(keep_loss=False)
+    P.sync()
+    wall = time.perf_counter() - t0
+    step(keep_loss=True)
+    err = lib.pico_gpu_last_error().decode()
+    lib.arena_ctx_pop()
+    lib.arena_destroy(work)
+    lib.arena_destroy(data)
+    lib.pico_optim_adamw_free(opt)
+    lib.pico_gpt_free(model)
+    if err:
+        raise RuntimeError(err)
+    flop = train_flop_per_step(cfg)
+    ms = wall * 1e3 / steps
+    return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
+            "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+            "mfu": round(flop / (ms * 1e-3) / MFMA_FP32_PEAK, 4),
+            "tokens_per_step": n, "steps": steps, "warmup": warmup,
+            "loss_first": round(losses[0], 5), "loss_after": round(losses[-1], 5),
+            "optimizer": dict(ADAMW, name="AdamW"), "config": cfg}
+
+
 def cpu_baseline(n):
     """pico's AVX matmul on the host: warmup 1, median of 3 (bench_matmul_large.c:16-18)"""
     import ctypes
@@ -206,7 +290,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4096)
-    ap.add_argument("--sections", default="sweep,rows,cpu")
+    ap.add_argument("--sections", default="train,sweep,rows,cpu")
+    ap.add_argument("--train-steps", type=int, default=10)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -222,7 +307,7 @@ def main():
     g = gemm_section(args, torch, K)
     achieved = g["flop_per_launch"] / (g["nn_kernel_ms"] * 1e-3)
     line = {
-        "metric": "fp32 GEMM TFLOP/s (matmul fwd + both bwd products, 4096^3)",
+        "metric": "train tokens/sec (fwd+bwd) + fp32 GEMM TFLOPS, % of MFMA/HBM roofline",
         "value": round(g["value"], 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -243,6 +328,8 @@ def main():
                      "kernel_ms": round(g["nn_kernel_ms"], 4)},
         "device": info,
     }
+    if "train" in sections:
+        line["train"] = {name: train_section(name, args.train_steps, 3) for name in TRAIN_CONFIGS}
     if "sweep" in sections:
         line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
     if "rows" in sections:

@@ -193,6 +193,38 @@ void pico_optim_adamw_step(struct PicoOptimAdamW* optim);
 void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* optim);
 void pico_optim_adamw_free(struct PicoOptimAdamW* optim);
 
+/* ---- decoder-only transformer built only from the ops above (no reference
+ * counterpart: pico has no sequence model; this is the training step of the
+ * benchmark configurations).  Pre-norm blocks without biases:
+ *   x = E[tokens]
+ *   per layer: x += attn_causal(rms(x) Wq, rms(x) Wk, rms(x) Wv) Wo
+ *              x += swiglu(rms(x) W1, rms(x) W3) W2
+ *   loss = softmax_xent(rms(x) Wlm, targets)
+ * Weights ~ N(0, init_std) from a seeded device generator, norm gains 1.
+ * Parameter order: E [V,d]; per layer g_attn [d], Wq, Wk, Wv, Wo [d,d],
+ * g_ffn [d], W1 [d,F], W3 [d,F], W2 [F,d]; g_final [d]; Wlm [d,V]. */
+struct PicoGPTConfig {
+    int vocab;
+    int d_model;
+    int n_layers;
+    int n_heads;
+    int d_ff;
+    int batch;
+    int seq_len;
+    float norm_eps;
+    float init_std;
+};
+struct PicoGPT;
+struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed);
+/* mean next-token cross-entropy over batch*seq_len positions; tokens and
+ * targets are int32 [batch*seq_len] (host or device).  Every intermediate is
+ * allocated in the current arena. */
+struct PicoTensor* pico_gpt_loss(struct PicoGPT* model, const int32_t* tokens,
+                                 const int32_t* targets);
+int pico_gpt_num_params(const struct PicoGPT* model);
+struct PicoTensor* pico_gpt_param(struct PicoGPT* model, int index);
+void pico_gpt_free(struct PicoGPT* model);
+
 /* ---- host <-> device (no reference counterpart: pico's data is host memory) ----
  * Each copies numel floats of the tensor's storage and synchronises the
  * stream; 0 on success. */

@@ -98,6 +98,13 @@ int pk_relu_f32(int64_t n, const float* x, float* y, pk_stream_t stream);
 int pk_relu_bwd_f32(int64_t n, const float* y, const float* gy, float* gx, int flags,
                     pk_stream_t stream);
 int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream);
+/* x[i] = mean + std * z_i, z_i ~ N(0,1) from a counter-based generator: element
+ * i draws two uniforms from the 64-bit mix of (seed, i) and applies Box-Muller
+ * (u1 in (0,1]), so the values do not depend on the launch shape.  Seeded
+ * parameter initialisation (no reference counterpart: pico_randn,
+ * src/tensor.c:348-367, builds normals from graph ops on the host). */
+int pk_fill_normal_f32(int64_t n, uint64_t seed, float mean, float std, float* x,
+                       pk_stream_t stream);
 /* y (+)= alpha * (*alpha_dev if non-NULL) * x */
 int pk_axpy_f32(int64_t n, float alpha, const float* alpha_dev, const float* x, float* y,
                 int flags, pk_stream_t stream);

@@ -44,6 +44,7 @@ PK_SIGNATURES = {
     "pk_relu_f32": [c_i64, c_p, c_p, c_p],
     "pk_relu_bwd_f32": [c_i64, c_p, c_p, c_p, c_int, c_p],
     "pk_fill_f32": [c_i64, c_f, c_p, c_p],
+    "pk_fill_normal_f32": [c_i64, ctypes.c_uint64, c_f, c_f, c_p, c_p],
     "pk_axpy_f32": [c_i64, c_f, c_p, c_p, c_p, c_int, c_p],
     "pk_reduce_sum_f32": [c_i64, c_p, c_f, c_p, c_int, c_p],
     "pk_sgd_f32": [c_i64, c_f, c_p, c_p, c_p],

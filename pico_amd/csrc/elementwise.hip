@@ -176,6 +176,27 @@ __global__ void fill_kernel(int64_t n, float v, float* __restrict__ x) {
         x[i] = v;
 }
 
+// splitmix64 finaliser: a bijective 64-bit mix (Steele, Lea & Flood 2014)
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_kernel(int64_t n, uint64_t seed, float mean, float std,
+                                   float* __restrict__ x) {
+    const uint64_t key = mix64(seed ^ 0x9e3779b97f4a7c15ull);
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = mix64(key + (uint64_t)i * 0x9e3779b97f4a7c15ull);
+        // two 24-bit uniforms: u1 in (0, 1], u2 in [0, 1)
+        const float u1 = ((float)(uint32_t)(r >> 40) + 1.0f) * (1.0f / 16777216.0f);
+        const float u2 = (float)(uint32_t)((r >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+        const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958648f * u2);
+        x[i] = mean + std * z;
+    }
+}
+
 __global__ void axpy_kernel(int64_t n, float alpha, const float* __restrict__ alpha_dev,
                             const float* __restrict__ x, float* __restrict__ y, int accum) {
     const float a = alpha_dev ? alpha * *alpha_dev : alpha;
@@ -383,6 +404,15 @@ extern "C" int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream)
     if(!x) return pk::fail("pk_fill_f32: NULL pointer");
     fill_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, value, x);
     return pk::launch_status("pk_fill_f32");
+}
+
+extern "C" int pk_fill_normal_f32(int64_t n, uint64_t seed, float mean, float std, float* x,
+                                  pk_stream_t stream) {
+    if(n <= 0) return n < 0 ? pk::fail("pk_fill_normal_f32: negative n") : PK_OK;
+    if(!x) return pk::fail("pk_fill_normal_f32: NULL pointer");
+    fill_normal_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, seed, mean, std,
+                                                                             x);
+    return pk::launch_status("pk_fill_normal_f32");
 }
 
 extern "C" int pk_axpy_f32(int64_t n, float alpha, const float* alpha_dev, const float* x, float* y,

@@ -1,0 +1,133 @@
+/*
+ * pico_amd/host/gpt.c -- a pre-norm decoder-only transformer written only
+ * with pico's public API (include/pico_amd.h), the way a pico user writes a
+ * model (compare examples/02_relu_mlp/main.c:64-130 for the MLP).  It is the
+ * training step of the benchmark configurations; the ops it calls are the
+ * hot path.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "pk_host.h"
+
+struct PicoGPTLayer {
+    struct PicoTensor *g_attn, *wq, *wk, *wv, *wo, *g_ffn, *w1, *w3, *w2;
+};
+
+struct PicoGPT {
+    struct PicoGPTConfig cfg;
+    struct PicoTensor* emb;
+    struct PicoGPTLayer* layers;
+    struct PicoTensor *g_final, *wlm;
+    struct PicoTensor** params;
+    int n_params;
+};
+
+static struct PicoTensor* new_param(struct PicoGPT* m, int64_t r, int64_t c, int is_gain,
+                                    uint64_t seed) {
+    int64_t shape[2] = {r, c};
+    struct PicoTensor* t = is_gain ? pico_param(&shape[1], 1) : pico_param(shape, 2);
+    if(!t) return NULL;
+    int st = is_gain ? pk_fill_f32(t->numel, 1.0f, t->data, pkh_stream())
+                     : pk_fill_normal_f32(t->numel, seed, 0.0f, m->cfg.init_std, t->data,
+                                          pkh_stream());
+    if(pkh_status("pico_gpt_init", st)) {
+        pico_free(t);
+        return NULL;
+    }
+    m->params[m->n_params++] = t;
+    return t;
+}
+
+struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed) {
+    if(!cfg || cfg->vocab < 1 || cfg->d_model < 1 || cfg->n_layers < 0 || cfg->n_heads < 1 ||
+       cfg->d_ff < 1 || cfg->batch < 1 || cfg->seq_len < 1 || cfg->d_model % cfg->n_heads) {
+        PKH_ERR("pico_gpt_init: invalid configuration!\n");
+        return NULL;
+    }
+    if(pkh_init()) return NULL;
+    struct PicoGPT* m = (struct PicoGPT*)calloc(1, sizeof(*m));
+    if(!m) return NULL;
+    m->cfg = *cfg;
+    int total = 3 + 9 * cfg->n_layers;
+    m->params = (struct PicoTensor**)calloc(total, sizeof(struct PicoTensor*));
+    m->layers = (struct PicoGPTLayer*)calloc(cfg->n_layers ? cfg->n_layers : 1, sizeof(*m->layers));
+    if(!m->params || !m->layers) {
+        pico_gpt_free(m);
+        return NULL;
+    }
+    const int64_t V = cfg->vocab, d = cfg->d_model, F = cfg->d_ff;
+    uint64_t s = seed * 1000003ull;
+    int ok = (m->emb = new_param(m, V, d, 0, s++)) != NULL;
+    for(int l = 0; ok && l < cfg->n_layers; l++) {
+        struct PicoGPTLayer* L = &m->layers[l];
+        ok = (L->g_attn = new_param(m, 1, d, 1, 0)) && (L->wq = new_param(m, d, d, 0, s++)) &&
+             (L->wk = new_param(m, d, d, 0, s++)) && (L->wv = new_param(m, d, d, 0, s++)) &&
+             (L->wo = new_param(m, d, d, 0, s++)) && (L->g_ffn = new_param(m, 1, d, 1, 0)) &&
+             (L->w1 = new_param(m, d, F, 0, s++)) && (L->w3 = new_param(m, d, F, 0, s++)) &&
+             (L->w2 = new_param(m, F, d, 0, s++));
+    }
+    ok = ok && (m->g_final = new_param(m, 1, d, 1, 0)) && (m->wlm = new_param(m, d, V, 0, s++));
+    if(!ok) {
+        pico_gpt_free(m);
+        return NULL;
+    }
+    return m;
+}
+
+struct PicoTensor* pico_gpt_loss(struct PicoGPT* m, const int32_t* tokens,
+                                 const int32_t* targets) {
+    if(!m || !tokens || !targets) {
+        PKH_ERR("pico_gpt_loss: NULL model or batch!\n");
+        return NULL;
+    }
+    const struct PicoGPTConfig* c = &m->cfg;
+    const int64_t n = (int64_t)c->batch * c->seq_len;
+    const float eps = c->norm_eps;
+    struct PicoTensor* x = pico_embedding(m->emb, tokens, n);
+    for(int l = 0; x && l < c->n_layers; l++) {
+        struct PicoGPTLayer* L = &m->layers[l];
+        struct PicoTensor* h = pico_rmsnorm(x, L->g_attn, eps);
+        if(!h) return NULL;
+        struct PicoTensor* q = pico_matmul(h, L->wq);
+        struct PicoTensor* k = pico_matmul(h, L->wk);
+        struct PicoTensor* v = pico_matmul(h, L->wv);
+        if(!q || !k || !v) return NULL;
+        struct PicoTensor* a = pico_attention_causal(q, k, v, c->batch, c->n_heads);
+        if(!a) return NULL;
+        struct PicoTensor* o = pico_matmul(a, L->wo);
+        if(!o) return NULL;
+        x = pico_add(x, o);
+        if(!x) return NULL;
+        h = pico_rmsnorm(x, L->g_ffn, eps);
+        if(!h) return NULL;
+        struct PicoTensor* gate = pico_matmul(h, L->w1);
+        struct PicoTensor* up = pico_matmul(h, L->w3);
+        if(!gate || !up) return NULL;
+        struct PicoTensor* act = pico_swiglu(gate, up);
+        if(!act) return NULL;
+        struct PicoTensor* down = pico_matmul(act, L->w2);
+        if(!down) return NULL;
+        x = pico_add(x, down);
+    }
+    if(!x) return NULL;
+    struct PicoTensor* hf = pico_rmsnorm(x, m->g_final, eps);
+    if(!hf) return NULL;
+    struct PicoTensor* logits = pico_matmul(hf, m->wlm);
+    if(!logits) return NULL;
+    return pico_softmax_xent(logits, targets);
+}
+
+int pico_gpt_num_params(const struct PicoGPT* m) { return m ? m->n_params : 0; }
+
+struct PicoTensor* pico_gpt_param(struct PicoGPT* m, int i) {
+    return (m && i >= 0 && i < m->n_params) ? m->params[i] : NULL;
+}
+
+void pico_gpt_free(struct PicoGPT* m) {
+    if(!m) return;
+    for(int i = 0; i < m->n_params; i++) pico_free(m->params[i]);
+    free(m->params);
+    free(m->layers);
+    free(m);
+}

@@ -41,6 +41,16 @@ PicoTensor._fields_ = [
 ]
 TP = ctypes.POINTER(PicoTensor)
 
+
+class PicoGPTConfig(ctypes.Structure):
+    """struct PicoGPTConfig (include/pico_amd.h)"""
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("vocab", "d_model", "n_layers", "n_heads", "d_ff", "batch", "seq_len")] + \
+               [("norm_eps", ctypes.c_float), ("init_std", ctypes.c_float)]
+
+
+GPT_KEYS = ("vocab", "d_model", "n_layers", "n_heads", "d_ff", "batch", "seq_len")
+
 _SIGS = {
     "pico_init": (None, []),
     "arena_init": (c_p, [ctypes.c_size_t]),
@@ -97,6 +107,11 @@ _GPU_SIGS = {
     "pico_gpu_last_error": (ctypes.c_char_p, []),
     "pico_gpu_clear_error": (None, []),
     "pico_randn": (TP, [c_p, ctypes.POINTER(c_i64), ctypes.c_uint8]),
+    "pico_gpt_init": (c_p, [ctypes.POINTER(PicoGPTConfig), ctypes.c_uint64]),
+    "pico_gpt_loss": (TP, [c_p, c_p, c_p]),
+    "pico_gpt_num_params": (ctypes.c_int, [c_p]),
+    "pico_gpt_param": (TP, [c_p, ctypes.c_int]),
+    "pico_gpt_free": (None, [c_p]),
 }
 
 _amd = None
@@ -276,6 +291,25 @@ class Pico:
     def embedding(self, table, ids):
         a = np.ascontiguousarray(ids, dtype=np.int32)
         return self._check(self.lib.pico_embedding(table, self.ids(a), a.size), "pico_embedding")
+
+    # ------------------------------------------------------------ the model
+    def gpt_init(self, cfg, seed, norm_eps=1e-6, init_std=0.02):
+        c = PicoGPTConfig(*[int(cfg[k]) for k in GPT_KEYS], norm_eps, init_std)
+        m = self.lib.pico_gpt_init(ctypes.byref(c), seed)
+        if not m:
+            raise PicoError("pico_gpt_init failed " +
+                            self.lib.pico_gpu_last_error().decode(errors="replace"))
+        return m
+
+    def gpt_params(self, model):
+        return [self.lib.pico_gpt_param(model, i)
+                for i in range(self.lib.pico_gpt_num_params(model))]
+
+    def gpt_loss(self, model, tokens, targets):
+        """tokens / targets: int32 numpy arrays (staged per call) or device pointers"""
+        tp = tokens if isinstance(tokens, int) else self.ids(tokens)
+        gp = targets if isinstance(targets, int) else self.ids(targets)
+        return self._check(self.lib.pico_gpt_loss(model, tp, gp), "pico_gpt_loss")
 
     def backward(self, loss):
         if self.device:

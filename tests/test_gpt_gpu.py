@@ -1,0 +1,154 @@
+"""The benchmark transformer (pico_amd/host/gpt.c, built from pico ops) on the
+GPU against the float64 reference oracle/gpt_ref.py, on the GPU model's own
+seeded weights (read back to the host).
+
+Bar (the north star's floating-point tolerance): max relative error <= 1e-4
+on the loss and on every parameter gradient (max|gpu - ref| / max|ref| per
+tensor), and the loss curve of AdamW steps within 1e-4.  Config 5's full
+12-layer step is checked at full size through properties (initial loss of a
+near-uniform model, loss falls when one batch is repeated, finite grads) and
+at its full widths and sequence length with two layers against the reference.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import gpt_ref as G
+from oracle import oracle as O
+from pico_amd.pico import Pico
+from tests._util import max_rel
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+ADAMW = dict(lr=1e-3, b1=0.9, b2=0.95, eps=1e-8, wd=0.1)
+CONFIG4 = dict(vocab=8192, d_model=512, n_layers=1, n_heads=8, d_ff=1376, batch=16, seq_len=256)
+CONFIG5 = dict(vocab=32000, d_model=768, n_layers=12, n_heads=12, d_ff=2048, batch=8,
+               seq_len=1024)
+
+
+@pytest.fixture(scope="module")
+def P():
+    return Pico()
+
+
+def _batch(cfg, seed):
+    n = cfg["batch"] * cfg["seq_len"]
+    seq = O.labels(cfg["batch"] * (cfg["seq_len"] + 1), seed, cfg["vocab"])
+    seq = seq.reshape(cfg["batch"], cfg["seq_len"] + 1)
+    return (np.ascontiguousarray(seq[:, :-1]).ravel(), np.ascontiguousarray(seq[:, 1:]).ravel(), n)
+
+
+def _gpu_step(P, model, tokens, targets, arena_bytes=1 << 28):
+    with P.arena(arena_bytes):
+        loss = P.gpt_loss(model, tokens, targets)
+        P.backward(loss)
+        params = P.gpt_params(model)
+        return float(P.data(loss)[0]), [P.grad(p) for p in params]
+
+
+def _host_params(P, model, cfg):
+    out = []
+    for t in P.gpt_params(model):
+        out.append(P.value(t).astype(np.float64))
+    return out
+
+
+def _check_step(P, cfg, seed):
+    model = P.gpt_init(cfg, seed)
+    try:
+        tokens, targets, _ = _batch(cfg, seed + 1)
+        params = _host_params(P, model, cfg)
+        loss, grads = _gpu_step(P, model, tokens, targets)
+        ref_loss, ref_grads = G.loss_and_grads(params, cfg, tokens, targets)
+        assert abs(loss - ref_loss) <= TOL * abs(ref_loss)
+        assert len(grads) == len(ref_grads)
+        for i, (g, r) in enumerate(zip(grads, ref_grads)):
+            assert max_rel(g, r.ravel()) <= TOL, (i, max_rel(g, r.ravel()))
+    finally:
+        P.gpt_free(model)
+
+
+def test_small_model_loss_and_grads(P):
+    _check_step(P, dict(vocab=96, d_model=64, n_layers=2, n_heads=2, d_ff=160, batch=2,
+                        seq_len=64), 11)
+
+
+def test_config4_one_step_loss_and_grads(P):
+    _check_step(P, CONFIG4, 21)
+
+
+def test_config5_widths_two_layers_loss_and_grads(P):
+    # config 5's d_model, heads, d_ff, vocab and sequence length; 2 layers, batch 2
+    _check_step(P, dict(CONFIG5, n_layers=2, batch=2), 31)
+
+
+def test_config4_adamw_loss_curve(P):
+    cfg, steps = CONFIG4, 8
+    model = P.gpt_init(cfg, 41)
+    try:
+        tokens, targets, _ = _batch(cfg, 42)
+        params = _host_params(P, model, cfg)
+        opt = P.optim_adamw_init(ADAMW["lr"], ADAMW["b1"], ADAMW["b2"], ADAMW["eps"], ADAMW["wd"])
+        tensors = P.gpt_params(model)
+        for t in tensors:
+            P.optim_adamw_add(opt, t)
+        gpu = []
+        with P.arena(1 << 28) as ar:
+            for _ in range(steps):
+                loss = P.gpt_loss(model, tokens, targets)
+                P.optim_adamw_zero_grad(opt)
+                P.backward(loss)
+                P.optim_adamw_step(opt)
+                gpu.append(float(P.data(loss)[0]))
+                P.reset(ar)
+        final_gpu = [P.value(t) for t in tensors]
+        P.optim_adamw_free(opt)
+        ref = []
+        m = [np.zeros_like(p) for p in params]
+        v = [np.zeros_like(p) for p in params]
+        for s in range(1, steps + 1):
+            loss, grads = G.loss_and_grads(params, cfg, tokens, targets)
+            ref.append(loss)
+            for i, g in enumerate(grads):
+                params[i], m[i], v[i] = G.adamw(params[i], g.reshape(params[i].shape), m[i], v[i],
+                                               s, ADAMW["lr"], ADAMW["b1"], ADAMW["b2"],
+                                               ADAMW["eps"], ADAMW["wd"])
+        assert gpu[-1] < gpu[0]
+        assert max_rel(np.array(gpu), np.array(ref)) <= TOL
+        # weights after 8 updates: AdamW's normalised step turns fp32-vs-fp64
+        # rounding in the sign of a near-zero gradient into a full +-lr move of that
+        # one element, so the weights are compared by their Frobenius-relative error
+        for i, (fg, fr) in enumerate(zip(final_gpu, params)):
+            fro = np.linalg.norm(fg.astype(np.float64) - fr) / np.linalg.norm(fr)
+            assert fro <= 1e-4, (i, fro)
+    finally:
+        P.gpt_free(model)
+
+
+def test_config5_full_step_properties(P):
+    cfg = CONFIG5
+    model = P.gpt_init(cfg, 51)
+    try:
+        tokens, targets, n = _batch(cfg, 52)
+        opt = P.optim_adamw_init(ADAMW["lr"], ADAMW["b1"], ADAMW["b2"], ADAMW["eps"], ADAMW["wd"])
+        for t in P.gpt_params(model):
+            P.optim_adamw_add(opt, t)
+        losses = []
+        with P.arena(1 << 30) as ar:
+            for step in range(3):
+                loss = P.gpt_loss(model, tokens, targets)
+                P.optim_adamw_zero_grad(opt)
+                P.backward(loss)
+                if step == 0:
+                    for t in P.gpt_params(model)[-3:]:
+                        assert np.all(np.isfinite(P.grad(t)))
+                P.optim_adamw_step(opt)
+                losses.append(float(P.data(loss)[0]))
+                P.reset(ar)
+        P.optim_adamw_free(opt)
+        # weights N(0, 0.02): logits are ~1e-2, so the first loss is ln V to ~1e-3
+        assert abs(losses[0] - math.log(cfg["vocab"])) < 2e-2 * math.log(cfg["vocab"])
+        assert losses[2] < losses[1] < losses[0]
+    finally:
+        P.gpt_free(model)
