@@ -292,6 +292,7 @@ def main():
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--sections", default="train,sweep,rows,cpu")
     ap.add_argument("--train-steps", type=int, default=10)
+    ap.add_argument("--train-configs", default=",".join(TRAIN_CONFIGS))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -329,7 +330,8 @@ def main():
         "device": info,
     }
     if "train" in sections:
-        line["train"] = {name: train_section(name, args.train_steps, 3) for name in TRAIN_CONFIGS}
+        line["train"] = {name: train_section(name, args.train_steps, 3)
+                         for name in args.train_configs.split(",") if name}
     if "sweep" in sections:
         line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
     if "rows" in sections:

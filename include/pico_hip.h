@@ -52,6 +52,18 @@ int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, 
                 int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                 pk_stream_t stream);
 
+/* pk_gemm_f32 with a caller-provided device workspace.  When C has too few
+ * 128x128 tiles to fill the chip (a linear layer's weight gradient: M, N of the
+ * order of d_model, K = tokens), K is split into slices whose partial products
+ * go to the workspace and are summed by a second kernel in slice order, so the
+ * result is deterministic.  pk_gemm_workspace_f32 returns the bytes a split
+ * needs (0 when the product runs unsplit); a NULL or smaller workspace runs it
+ * unsplit.  Same backward roles as pk_gemm_f32 (src/autograd.h:96-130). */
+size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K);
+int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                   int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                   void* workspace, size_t workspace_bytes, pk_stream_t stream);
+
 /* Batched form: batch index z = outer*inner_count + inner; operand X of batch z
  * starts at X + outer*sX_outer + inner*sX_inner.  'causal' restricts work for
  * attention-shaped products (no reference counterpart: pico's matmul is 2-D

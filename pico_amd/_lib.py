@@ -34,6 +34,9 @@ PK_SIGNATURES = {
     "pk_device_info": [ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.c_char_p, c_int],
     "pk_gemm_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f, c_p,
                     c_i64, c_p],
+    "pk_gemm_workspace_f32": [c_i64, c_i64, c_i64],
+    "pk_gemm_ex_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f, c_p,
+                       c_i64, c_p, c_size, c_p],
     "pk_gemm_batched_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_i64, c_i64,
                             c_p, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_i64, c_i64, c_i64,
                             c_i64, c_int, c_p],
@@ -68,7 +71,8 @@ PK_SIGNATURES = {
     "pk_embed_bwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p],
     "pk_last_error": [],
 }
-_RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size}
+_RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size,
+             "pk_gemm_workspace_f32": c_size}
 
 _hip = None
 

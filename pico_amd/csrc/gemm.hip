@@ -43,6 +43,9 @@ struct GemmParams {
     float alpha, beta;
     int causal;
     int tiles_m, tiles_n;
+    int splits;      // > 1: blockIdx.y is a K slice of kchunk, partials go to ws
+    int64_t kchunk;
+    float* ws;
 };
 
 // One 128x32 operand slice -> 4 float4 per thread.  KFAST: element (r,k) at
@@ -133,17 +136,29 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     const int tm = first_m + local % gm;
     const int tn = local / gm;
 
-    const int64_t z = blockIdx.y;
+    // blockIdx.y is the batch index, or the K slice of a split product
+    const int64_t z = p.splits > 1 ? 0 : blockIdx.y;
     const int64_t zo = z / p.inner, zi = z % p.inner;
     const float* __restrict__ A = p.A + zo * p.sAo + zi * p.sAi;
     const float* __restrict__ B = p.B + zo * p.sBo + zi * p.sBi;
     float* __restrict__ C = p.C + zo * p.sCo + zi * p.sCi;
+    int64_t ldc = p.ldc;
+    float alpha = p.alpha, beta = p.beta;
 
     const int64_t row0 = (int64_t)tm * BM, col0 = (int64_t)tn * BN;
     int64_t kbeg = 0, kend = p.K;
     if(p.causal == 1 && col0 > row0 + BM - 1) return;  // wholly above the diagonal
     if(p.causal == 2) kend = min(p.K, row0 + BM);
     if(p.causal == 3) kbeg = min(p.K, (row0 / BK) * BK);
+    if(p.splits > 1) {
+        // slice s of K; its partial product goes to workspace plane s
+        kbeg = (int64_t)blockIdx.y * p.kchunk;
+        kend = min(p.K, kbeg + p.kchunk);
+        C = p.ws + (int64_t)blockIdx.y * p.M * p.N;
+        ldc = p.N;
+        alpha = 1.0f;
+        beta = 0.0f;
+    }
     const int nslices = (int)((kend - kbeg + BK - 1) / BK);
 
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
@@ -209,17 +224,62 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
             for(int r = 0; r < 16; ++r) {
                 const int64_t row = row0 + wm * 64 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
                 if(EDGE && (row >= p.M || col >= p.N)) continue;
-                float v = p.alpha * acc[i][j][r];
-                float* c = C + row * p.ldc + col;
-                if(p.beta != 0.0f) v += p.beta * *c;
+                float v = alpha * acc[i][j][r];
+                float* c = C + row * ldc + col;
+                if(beta != 0.0f) v += beta * *c;
                 *c = v;
             }
         }
 }
 
+// C = alpha * sum_s ws[s] + beta * C, planes summed in order s = 0, 1, ...
+__global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restrict__ ws,
+                              float alpha, float beta, float* __restrict__ C, int64_t ldc) {
+    const int64_t plane = M * N;
+    if((N & 3) == 0 && (ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+        const int64_t n4 = plane / 4, N4 = N / 4;
+        for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
+            i += (int64_t)gridDim.x * blockDim.x) {
+            f32x4 acc = reinterpret_cast<const f32x4*>(ws)[i];
+            for(int s = 1; s < S; ++s) acc += reinterpret_cast<const f32x4*>(ws + s * plane)[i];
+            f32x4* c = reinterpret_cast<f32x4*>(C + (i / N4) * ldc) + (i % N4);
+            f32x4 v = alpha * acc;
+            if(beta != 0.0f) v += beta * *c;
+            *c = v;
+        }
+        return;
+    }
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < plane;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        float acc = ws[i];
+        for(int s = 1; s < S; ++s) acc += ws[s * plane + i];
+        float* c = C + (i / N) * ldc + (i % N);
+        float v = alpha * acc;
+        if(beta != 0.0f) v += beta * *c;
+        *c = v;
+    }
+}
+
+// K split for a product whose output has too few tiles to fill the chip: 2
+// resident workgroups per CU x 256 CUs want >= 512 workgroups; each slice keeps
+// at least 256 of K (8 LDS stages) so the pipeline stays long.
+constexpr int64_t kSplitTarget = 512, kMinSliceK = 256;
+
+int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
+    const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    *kchunk = K;
+    if(tiles <= 0 || tiles * 2 > kSplitTarget || K < 4 * kMinSliceK) return 1;
+    int64_t s = kSplitTarget / tiles;
+    if(s > K / kMinSliceK) s = K / kMinSliceK;
+    if(s < 2) return 1;
+    const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
+    *kchunk = chunk;
+    return (int)((K + chunk - 1) / chunk);
+}
+
 template <bool TA, bool TB>
 int launch(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
-    dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)batch);
+    dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)(gp.splits > 1 ? gp.splits : batch));
     if(edge)
         gemm_f32_kernel<TA, TB, true><<<grid, NT, 0, st>>>(gp);
     else
@@ -227,14 +287,11 @@ int launch(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
     return pk::launch_status("pk_gemm_f32");
 }
 
-}  // namespace
-
-extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
-                                   const float* A, int64_t lda, int64_t sA_outer, int64_t sA_inner,
-                                   const float* B, int64_t ldb, int64_t sB_outer, int64_t sB_inner,
-                                   float beta, float* C, int64_t ldc, int64_t sC_outer,
-                                   int64_t sC_inner, int64_t batch, int64_t inner_count,
-                                   int causal, pk_stream_t stream) {
+int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+              int64_t lda, int64_t sA_outer, int64_t sA_inner, const float* B, int64_t ldb,
+              int64_t sB_outer, int64_t sB_inner, float beta, float* C, int64_t ldc,
+              int64_t sC_outer, int64_t sC_inner, int64_t batch, int64_t inner_count, int causal,
+              float* ws, size_t ws_bytes, pk_stream_t stream) {
     const bool TA = ta == 'T' || ta == 't', TB = tb == 'T' || tb == 't';
     if(!(TA || ta == 'N' || ta == 'n') || !(TB || tb == 'N' || tb == 'n'))
         return pk::fail("pk_gemm_f32: transpose flags must be 'N' or 'T' (got '%c','%c')", ta, tb);
@@ -284,15 +341,64 @@ extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64
                       (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
                       !pk::aligned16(A) || !pk::aligned16(B);
     hipStream_t st = pk::as_stream(stream);
-    if(!TA && !TB) return launch<false, false>(gp, batch, edge, st);
-    if(!TA && TB) return launch<false, true>(gp, batch, edge, st);
-    if(TA && !TB) return launch<true, false>(gp, batch, edge, st);
-    return launch<true, true>(gp, batch, edge, st);
+    gp.splits = 1;
+    gp.kchunk = K;
+    gp.ws = nullptr;
+    if(batch == 1 && causal == 0 && ws && K > 0) {
+        int64_t kchunk;
+        const int S = choose_splits(M, N, K, &kchunk);
+        if(S > 1 && ws_bytes >= (size_t)S * (size_t)M * (size_t)N * sizeof(float)) {
+            gp.splits = S;
+            gp.kchunk = kchunk;
+            gp.ws = ws;
+        }
+    }
+    int rc;
+    if(!TA && !TB)
+        rc = launch<false, false>(gp, batch, edge, st);
+    else if(!TA && TB)
+        rc = launch<false, true>(gp, batch, edge, st);
+    else if(TA && !TB)
+        rc = launch<true, false>(gp, batch, edge, st);
+    else
+        rc = launch<true, true>(gp, batch, edge, st);
+    if(rc || gp.splits == 1) return rc;
+    splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(M, N, gp.splits, gp.ws, alpha,
+                                                                  beta, C, ldc);
+    return pk::launch_status("pk_gemm_ex_f32 (split-K reduction)");
+}
+
+}  // namespace
+
+extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                   const float* A, int64_t lda, int64_t sA_outer, int64_t sA_inner,
+                                   const float* B, int64_t ldb, int64_t sB_outer, int64_t sB_inner,
+                                   float beta, float* C, int64_t ldc, int64_t sC_outer,
+                                   int64_t sC_inner, int64_t batch, int64_t inner_count,
+                                   int causal, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, sA_outer, sA_inner, B, ldb, sB_outer,
+                     sB_inner, beta, C, ldc, sC_outer, sC_inner, batch, inner_count, causal,
+                     nullptr, 0, stream);
 }
 
 extern "C" int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                            const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                            float* C, int64_t ldc, pk_stream_t stream) {
-    return pk_gemm_batched_f32(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc,
-                               0, 0, 1, 1, 0, stream);
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, nullptr, 0, stream);
+}
+
+extern "C" size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K) {
+    if(M <= 0 || N <= 0 || K <= 0) return 0;
+    int64_t kchunk;
+    const int S = choose_splits(M, N, K, &kchunk);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+extern "C" int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                              const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                              float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                              pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, static_cast<float*>(workspace), workspace_bytes, stream);
 }

@@ -143,15 +143,20 @@ int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m)
 
 static inline char flip(char t) { return t == 'N' ? 'T' : 'N'; }
 
+/* products with too few output tiles (weight gradients) split K through the
+ * library workspace; see pk_gemm_ex_f32 */
 int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
              int64_t ldc, int flags) {
     const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+    size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
+    void* ws = ws_bytes ? pkh_workspace(ws_bytes) : NULL;
+    if(!ws) ws_bytes = 0;
     if(tc == 'N')
-        return pk_gemm_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc,
-                           pkh_stream());
+        return pk_gemm_ex_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws,
+                              ws_bytes, pkh_stream());
     /* C stored transposed: produce C^T [N, M] = B^T . A^T */
-    return pk_gemm_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
-                       pkh_stream());
+    return pk_gemm_ex_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
+                          ws, ws_bytes, pkh_stream());
 }
 
 static int matmul_views(struct PicoTensor* a, struct PicoTensor* b, struct PkMat* va,

@@ -58,6 +58,27 @@ def gemm(ta, tb, A, B, C, alpha=1.0, beta=0.0):
     return C
 
 
+def gemm_workspace(M, N, K):
+    return int(hip_lib().pk_gemm_workspace_f32(M, N, K))
+
+
+def gemm_ex(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
+    """gemm with a workspace: K is split when C has too few tiles (ws=None
+    allocates the size pk_gemm_workspace_f32 asks for)."""
+    _f32(A, B, C)
+    lda, ldb, ldc = _rowmajor(A, "A"), _rowmajor(B, "B"), _rowmajor(C, "C")
+    M = A.shape[1] if ta == "T" else A.shape[0]
+    K = A.shape[0] if ta == "T" else A.shape[1]
+    N = B.shape[0] if tb == "T" else B.shape[1]
+    if ws is None:
+        need = gemm_workspace(M, N, K)
+        ws = torch.empty(max(1, need // 4), device=C.device, dtype=torch.float32)
+    check("pk_gemm_ex_f32", hip_lib().pk_gemm_ex_f32(
+        ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc,
+        _ptr(ws), ws.numel() * 4, _stream()))
+    return C
+
+
 def gemm_batched(ta, tb, M, N, K, alpha, A, lda, sAo, sAi, B, ldb, sBo, sBi, beta, C, ldc, sCo,
                  sCi, batch, inner, causal=0):
     """Raw batched GEMM on flat tensors (strides in elements)."""

@@ -98,6 +98,35 @@ def test_gemm_large_sampled_rows(dev, ta, tb, n):
     assert gemm_err(Cn[rows], A[rows], B) <= TOL
 
 
+@pytest.mark.parametrize("ta,tb", [("T", "N"), ("N", "T"), ("N", "N")])
+@pytest.mark.parametrize("M,N,Kd", [(768, 768, 8192), (768, 2048, 8192), (200, 136, 4000),
+                                    (64, 10, 784)])
+def test_gemm_splitk(dev, ta, tb, M, N, Kd):
+    # weight-gradient shapes: K split into slices summed in a fixed order
+    need = K.gemm_workspace(M, N, Kd)
+    assert (need > 0) == (Kd >= 1024)  # short K (the MLP's 784) stays unsplit
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm_ex(ta, tb, cu(As), cu(Bs), C)
+    # |entries| <= 8 and K <= 8192 keep every partial sum below 2^19, exact in
+    # fp32 and in the float64 BLAS product used as the reference
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N + 1)
+    C0 = O.uniform(M * N, 3).reshape(M, N)
+    C = cu(C0.copy())
+    K.gemm_ex(ta, tb, cu(As), cu(Bs), C, alpha=0.5, beta=1.0)
+    Cn = host(C)
+    assert gemm_err(Cn - C0, 0.5 * A, B) <= TOL
+    C2 = cu(C0.copy())  # deterministic: the same call gives the same bits
+    K.gemm_ex(ta, tb, cu(As), cu(Bs), C2, alpha=0.5, beta=1.0)
+    assert np.array_equal(host(C2), Cn)
+    small = torch.empty(1, device=dev)  # a workspace too small runs the product unsplit
+    C3 = torch.empty(M, N, device=dev)
+    K.gemm_ex(ta, tb, cu(As), cu(Bs), C3, ws=small)
+    assert gemm_err(host(C3), A, B) <= TOL
+
+
 def test_gemm_alpha_beta_accumulate(dev):
     M, N, Kd = 200, 136, 96
     A, B, As, Bs = _operands("N", "N", M, N, Kd, seed=5)
