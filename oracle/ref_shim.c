@@ -73,3 +73,49 @@ void picoref_rand(uint32_t seed, int64_t n, float* out) {
     for(int64_t i = 0; i < n; i++) out[i] = t->data[i];
     arena_destroy(ar);
 }
+
+static struct PicoTensor view1(float* data, int64_t* shape, int64_t* strides, int64_t n) {
+    struct PicoTensor t = {0};
+    shape[0] = n;
+    strides[0] = 1;
+    t.shape = shape;
+    t.strides = strides;
+    t.data = data;
+    t.numel = n;
+    t.ndim = 1;
+    return t;
+}
+
+/* pico's unary kernels (src/kernels/cpu_kernels.h:60-100), op 0..5 =
+ * sqrt, sin, cos, tan, tanh, log */
+void picoref_unary(int op, int64_t n, float* x, float* y) {
+    int64_t s0[1], t0[1], s1[1], t1[1];
+    struct PicoTensor a = view1(x, s0, t0, n), out = view1(y, s1, t1, n);
+    switch(op) {
+        case 0: pico_sqrt_cpu(&a, &out); break;
+        case 1: pico_sin_cpu(&a, &out); break;
+        case 2: pico_cos_cpu(&a, &out); break;
+        case 3: pico_tan_cpu(&a, &out); break;
+        case 4: pico_tanh_cpu(&a, &out); break;
+        default: pico_log_cpu(&a, &out); break;
+    }
+}
+
+/* their backward hooks (src/autograd.h:132-176): gx += local derivative * gy */
+void picoref_unary_bwd(int op, int64_t n, float* x, float* y, float* gy, float* gx) {
+    int64_t s0[1], t0[1], s1[1], t1[1];
+    struct PicoTensor a = view1(x, s0, t0, n), self = view1(y, s1, t1, n);
+    a.grad = gx;
+    self.grad = gy;
+    struct PicoTensor* parents[1] = {&a};
+    self.parents = parents;
+    self.num_parents = 1;
+    switch(op) {
+        case 0: pico_tensor_sqrt_backward(&self); break;
+        case 1: pico_tensor_sin_backward(&self); break;
+        case 2: pico_tensor_cos_backward(&self); break;
+        case 3: pico_tensor_tan_backward(&self); break;
+        case 4: pico_tensor_tanh_backward(&self); break;
+        default: pico_tensor_log_backward(&self); break;
+    }
+}

@@ -104,6 +104,40 @@ def test_broadcast_kats():
     assert ga.ravel().tolist() == [10, 40, 30, 80] and gb.tolist() == [10, 20]
 
 
+def test_unary_kats():
+    # tests/test_unary.c:18-129 forward, :165-289 backward with upstream 2
+    pi = np.float32(np.pi)
+    assert O.unary(0, [0, 4, 9, 16]).tolist() == [0, 2, 3, 4]
+    near = lambda a, b: np.allclose(a, b, atol=1e-5)  # the reference's NEAR
+    assert near(O.unary(1, [0, pi / 2]), [0, 1]) and near(O.unary(2, [0, pi]), [1, -1])
+    assert near(O.unary(3, [0, pi / 4]), [0, 1]) and near(O.unary(4, [0, 20]), [0, 1])
+    assert O.unary(5, [1])[0] == 0 and near(O.unary(5, [np.e]), [1])
+    for op, x, want in ((0, 4.0, 0.5), (1, pi, -2.0), (2, pi / 2, -2.0), (3, 0.0, 2.0),
+                        (4, 0.0, 2.0), (5, 2.0, 1.0)):
+        xs = np.array([x], np.float32)
+        g = O.unary_bwd(op, xs, O.unary(op, xs), np.array([2.0], np.float32),
+                        np.zeros(1, np.float32))
+        assert near(g, [want]), op
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build absent")
+@pytest.mark.parametrize("op", range(6))
+def test_unary_bitexact_vs_reference(op):
+    # libm-dependent values and the backward expressions as the reference
+    # evaluates them (tanh's g*1 - y^2 precedence included), bit for bit
+    import ctypes
+
+    x = O.uniform(4099, 30 + op, 0.05, 1.4)
+    y = np.empty_like(x)
+    O.ref().picoref_unary(ctypes.c_int(op), ctypes.c_int64(x.size), O.p(x), O.p(y))
+    assert np.array_equal(O.unary(op, x), y)
+    gy, gx0 = O.normal(x.size, 40 + op), O.normal(x.size, 50 + op)
+    gref = gx0.copy()
+    O.ref().picoref_unary_bwd(ctypes.c_int(op), ctypes.c_int64(x.size), O.p(x), O.p(y), O.p(gy),
+                              O.p(gref))
+    assert np.array_equal(O.unary_bwd(op, x, y, gy, gx0.copy()), gref)
+
+
 def test_relu_kats():
     # tests/act/test_activations.c:12 (clamp), :75 (gate at 0 closed), NaN -> 0
     x = np.array([-2, -0.5, 0, 0.5, 3, np.nan, -0.0], np.float32)
