@@ -30,22 +30,22 @@ HBM_PEAK = 8.0e12
 
 
 def _events_time(fn, reps, warmup):
-    """mean ms per call of fn() measured with events on the current stream"""
+    """mean ms per call of fn(): `reps` back-to-back launches between two HIP
+    events on the launch stream (torch's current stream, which the pk_*
+    bindings launch on), so per-launch host gaps are not counted"""
     import torch
 
     for _ in range(warmup):
         fn()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
-    times = []
+    s.record()
     for _ in range(reps):
-        s.record()
         fn()
-        e.record()
-        e.synchronize()
-        times.append(s.elapsed_time(e))
-    times.sort()
-    return sum(times) / len(times), times[len(times) // 2]
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e) / reps
+    return ms, ms
 
 
 def gemm_section(args, torch, K):
@@ -126,6 +126,11 @@ def rows_section(torch, K):
         res[name] = {"us": round(mean_ms * 1e3, 1), "GB/s": round(gbs, 1),
                      "frac": round(gbs * 1e9 / HBM_PEAK, 3)}
 
+    # context: what a plain device copy (torch's kernel) reaches on this box
+    src = [torch.empty(1 << 28, device=dev) for _ in range(sets)]
+    dst = [torch.empty(1 << 28, device=dev) for _ in range(sets)]
+    bw("copy_1GiB_context", 2 * (1 << 30), [lambda j=j: dst[j].copy_(src[j]) for j in range(sets)])
+    del src, dst
     # RMSNorm 8192 x 4096
     R, Cc = 8192, 4096
     xs = [torch.randn(R, Cc, device=dev) for _ in range(sets)]

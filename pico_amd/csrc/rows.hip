@@ -16,7 +16,11 @@ namespace {
 constexpr float kNegInf = -INFINITY;
 
 // ============================================================ cross-entropy
-// one workgroup of NT threads per row; each thread caches NV float4 of the row
+// One workgroup of NT threads per row, each thread caching NV float4 of the row
+// in registers: max, one exponential per element (kept for the gradient), sum,
+// gradient, store.  Measured on MI355X at 8192 x 32000, 256 threads with the
+// row in registers beat 1024 threads walking rows with a prefetch (70 % vs
+// 61 % of HBM peak): more independent workgroups per CU, cheaper reductions.
 template <int NT, int NV>
 __global__ __launch_bounds__(NT) void xent_reg_kernel(int64_t V, const float* __restrict__ logits,
                                                       int64_t ldz, const int32_t* __restrict__ labels,
@@ -25,36 +29,37 @@ __global__ __launch_bounds__(NT) void xent_reg_kernel(int64_t V, const float* __
                                                       float scale_in,
                                                       const float* __restrict__ scale_dev,
                                                       int accum) {
-    __shared__ float red[NT / 64];
+    __shared__ float red[2][NT / 64];
     const float scale = scale_dev ? scale_in * *scale_dev : scale_in;
-    const int64_t r = blockIdx.x;
+    const int64_t r = blockIdx.x, V4 = V / 4;
     const f32x4* z4 = reinterpret_cast<const f32x4*>(logits + r * ldz);
-    const int64_t V4 = V / 4;
     f32x4 z[NV];
+#pragma unroll
+    for(int i = 0; i < NV; ++i) {
+        const int64_t c = threadIdx.x + (int64_t)i * NT;
+        z[i] = c < V4 ? pk::ld_stream(z4 + c) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    }
     float m = kNegInf;
 #pragma unroll
-    for(int v = 0; v < NV; ++v) {
-        const int64_t c = threadIdx.x + (int64_t)v * NT;
-        if(c < V4) {
-            z[v] = z4[c];
-            m = fmaxf(m, fmaxf(fmaxf(z[v][0], z[v][1]), fmaxf(z[v][2], z[v][3])));
-        } else {
-            z[v] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
-        }
-    }
-    m = pk::block_max<NT / 64>(m, red);
+    for(int v = 0; v < NV; ++v)
+        m = fmaxf(m, fmaxf(fmaxf(z[v][0], z[v][1]), fmaxf(z[v][2], z[v][3])));
+    m = pk::block_max<NT / 64>(m, red[0]);
     float s = 0.0f;
 #pragma unroll
     for(int v = 0; v < NV; ++v)
 #pragma unroll
-        for(int e = 0; e < 4; ++e) s += expf(z[v][e] - m);
-    s = pk::block_sum<NT / 64>(s, red);
+        for(int e = 0; e < 4; ++e) {
+            z[v][e] = __expf(z[v][e] - m);
+            s += z[v][e];
+        }
+    s = pk::block_sum<NT / 64>(s, red[1]);
     const float lse = m + logf(s);
     const int32_t y = labels[r];
     const bool ok = y >= 0 && y < V;
     if(loss_rows && threadIdx.x == 0) loss_rows[r] = ok ? lse - logits[r * ldz + y] : NAN;
     if(!dlogits) return;
     f32x4* d4 = reinterpret_cast<f32x4*>(dlogits + r * ldd);
+    const float ps = scale / s;
 #pragma unroll
     for(int v = 0; v < NV; ++v) {
         const int64_t c = threadIdx.x + (int64_t)v * NT;
@@ -63,14 +68,10 @@ __global__ __launch_bounds__(NT) void xent_reg_kernel(int64_t V, const float* __
 #pragma unroll
         for(int e = 0; e < 4; ++e) {
             const int64_t col = c * 4 + e;
-            const float p = expf(z[v][e] - lse);
-            g[e] = ok ? scale * (p - (col == y ? 1.0f : 0.0f)) : 0.0f;
+            g[e] = ok ? z[v][e] * ps - (col == y ? scale : 0.0f) : 0.0f;
         }
-        if(accum) {
-            const f32x4 o = d4[c];
-            g = g + o;
-        }
-        d4[c] = g;
+        if(accum) g = g + d4[c];
+        pk::st_stream(d4 + c, g);
     }
 }
 
@@ -169,38 +170,112 @@ __global__ __launch_bounds__(NT) void argmax_kernel(int64_t V, const float* __re
 }
 
 // ================================================================= RMSNorm
-// one wave per row, NV float4 per lane (row width C <= 256*NV, C % 4 == 0)
+// One wave per row, NV float4 per lane (row width C <= 256*NV, C % 4 == 0).
+// Each wave walks rows gridDim.x*4 apart and loads its next row while it
+// reduces and stores the current one, so loads and stores overlap.
+template <int NV>
+__device__ __forceinline__ void load_row4(const float* __restrict__ base, int64_t C4, int lane,
+                                          f32x4 (&v)[NV]) {
+    const f32x4* r = reinterpret_cast<const f32x4*>(base);
+#pragma unroll
+    for(int i = 0; i < NV; ++i) {
+        const int64_t c = lane + i * 64;
+        v[i] = c < C4 ? pk::ld_stream(r + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_reg(int64_t R, int64_t C, float eps,
                                                        const float* __restrict__ x,
                                                        const float* __restrict__ g,
                                                        float* __restrict__ y,
                                                        float* __restrict__ rstd) {
-    const int64_t row = blockIdx.x * 4 + threadIdx.x / 64;
     const int lane = threadIdx.x % 64;
+    const int64_t step = (int64_t)gridDim.x * 4;
+    int64_t row = blockIdx.x * 4 + threadIdx.x / 64;
     if(row >= R) return;
     const int64_t C4 = C / 4;
-    const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * C);
     const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
-    f32x4 xv[NV];
-    float ss = 0.0f;
+    f32x4 cur[NV], nxt[NV];
+    load_row4<NV>(x + row * C, C4, lane, cur);
+    for(; row < R; row += step) {
+        const bool more = row + step < R;
+        if(more) load_row4<NV>(x + (row + step) * C, C4, lane, nxt);
+        float ss = 0.0f;
 #pragma unroll
-    for(int v = 0; v < NV; ++v) {
-        const int64_t c = lane + v * 64;
-        if(c < C4) {
-            xv[v] = xr[c];
-            ss += xv[v][0] * xv[v][0] + xv[v][1] * xv[v][1] + xv[v][2] * xv[v][2] +
-                  xv[v][3] * xv[v][3];
+        for(int v = 0; v < NV; ++v)
+            ss += cur[v][0] * cur[v][0] + cur[v][1] * cur[v][1] + cur[v][2] * cur[v][2] +
+                  cur[v][3] * cur[v][3];
+        ss = pk::wave_sum(ss);
+        const float rs = 1.0f / sqrtf(ss / (float)C + eps);
+        if(lane == 0 && rstd) rstd[row] = rs;
+        f32x4* yr = reinterpret_cast<f32x4*>(y + row * C);
+#pragma unroll
+        for(int v = 0; v < NV; ++v) {
+            const int64_t c = lane + v * 64;
+            if(c < C4) pk::st_stream(yr + c, cur[v] * rs * g4[c]);
+        }
+        if(more) {
+#pragma unroll
+            for(int v = 0; v < NV; ++v) cur[v] = nxt[v];
         }
     }
-    ss = pk::wave_sum(ss);
-    const float rs = 1.0f / sqrtf(ss / (float)C + eps);
-    if(lane == 0 && rstd) rstd[row] = rs;
-    f32x4* yr = reinterpret_cast<f32x4*>(y + row * C);
+}
+
+// Wide rows (C4 = C/4 >= 512): the 4 waves of a workgroup share each row (wave
+// w owns float4 columns [w*Q, (w+1)*Q), Q = ceil(C4/4)), combine the sum of
+// squares through LDS (one barrier per row, double-buffered), and walk rows
+// gridDim.x apart with the next row prefetched.  Measured at 8192 x 4096: 76 %
+// of HBM peak, against 67-71 % for one wave per row.
+template <int NQ, bool EXACT>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_cols(int64_t R, int64_t C, float eps,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ g,
+                                                        float* __restrict__ y,
+                                                        float* __restrict__ rstd) {
+    __shared__ float red[2][4];
+    const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int64_t C4 = C / 4, Q = (C4 + 3) / 4, c0 = w * Q;
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(g) + c0;
+    // EXACT: C is a multiple of 1024, so every lane owns NQ whole float4s and
+    // the loads and stores need no predicates
+    bool on[NQ];
 #pragma unroll
-    for(int v = 0; v < NV; ++v) {
-        const int64_t c = lane + v * 64;
-        if(c < C4) yr[c] = xv[v] * rs * g4[c];
+    for(int v = 0; v < NQ; ++v) {
+        const int64_t q = lane + v * 64;
+        on[v] = EXACT || (q < Q && c0 + q < C4);
+    }
+    f32x4 xv[NQ], xn[NQ];
+    auto load = [&](int64_t r, f32x4 (&a)[NQ]) {
+        const f32x4* xr = reinterpret_cast<const f32x4*>(x + r * C) + c0;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v)
+            a[v] = on[v] ? pk::ld_stream(xr + lane + v * 64) : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    int64_t row = blockIdx.x;
+    if(row < R) load(row, xv);
+    for(int it = 0; row < R; row += gridDim.x, ++it) {
+        const bool more = row + gridDim.x < R;
+        if(more) load(row + gridDim.x, xn);
+        float ss = 0.0f;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v)
+            ss += xv[v][0] * xv[v][0] + xv[v][1] * xv[v][1] + xv[v][2] * xv[v][2] +
+                  xv[v][3] * xv[v][3];
+        ss = pk::wave_sum(ss);
+        if(lane == 0) red[it & 1][w] = ss;
+        __syncthreads();
+        ss = ((red[it & 1][0] + red[it & 1][1]) + red[it & 1][2]) + red[it & 1][3];
+        const float rs = 1.0f / sqrtf(ss / (float)C + eps);
+        if(threadIdx.x == 0 && rstd) rstd[row] = rs;
+        f32x4* yr = reinterpret_cast<f32x4*>(y + row * C) + c0;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v)
+            if(on[v]) pk::st_stream(yr + lane + v * 64, xv[v] * rs * g4[lane + v * 64]);
+        if(more) {
+#pragma unroll
+            for(int v = 0; v < NQ; ++v) xv[v] = xn[v];
+        }
     }
 }
 
@@ -221,7 +296,13 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_any(int64_t R, int64_t C, flo
     for(int64_t c = lane; c < C; c += 64) y[row * C + c] = xr[c] * rs * g[c];
 }
 
-// backward, stage 1: dx for each row; per-workgroup partial of dg into ws[block][C]
+// backward, stage 1: dx for each row, and this workgroup's partial of dg
+// (over the rows it walked) into ws[block][C].  Internal flags: 4 = write dx,
+// 8 = produce dg partials, bit 0 = accumulate dx.
+//
+// Narrow rows (C <= 256*NV): one wave per row, rows gridDim.x*4 apart, the
+// next row's x and dy prefetched while the current one is finished; the 4
+// waves' dg partials are combined in LDS in a fixed order.
 template <int NV>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
                                                        const float* __restrict__ x,
@@ -242,20 +323,24 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
         dg[v] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const float invC = 1.0f / (float)C;
-    for(int64_t row = (int64_t)blockIdx.x * 4 + w; row < R; row += (int64_t)gridDim.x * 4) {
-        const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * C);
-        const f32x4* dyr = reinterpret_cast<const f32x4*>(dy + row * C);
-        f32x4 xv[NV], dv[NV];
+    const int64_t step = (int64_t)gridDim.x * 4;
+    int64_t row = (int64_t)blockIdx.x * 4 + w;
+    f32x4 xv[NV], dv[NV], xn[NV], dn[NV];
+    if(row < R) {
+        load_row4<NV>(x + row * C, C4, lane, xv);
+        load_row4<NV>(dy + row * C, C4, lane, dv);
+    }
+    for(; row < R; row += step) {
+        const bool more = row + step < R;
+        if(more) {
+            load_row4<NV>(x + (row + step) * C, C4, lane, xn);
+            load_row4<NV>(dy + (row + step) * C, C4, lane, dn);
+        }
         float dot = 0.0f;
 #pragma unroll
         for(int v = 0; v < NV; ++v) {
-            const int64_t c = lane + v * 64;
-            if(c < C4) {
-                xv[v] = xr[c];
-                dv[v] = dyr[c];
-                const f32x4 t = gv[v] * dv[v] * xv[v];
-                dot += t[0] + t[1] + t[2] + t[3];
-            }
+            const f32x4 t = gv[v] * dv[v] * xv[v];
+            dot += t[0] + t[1] + t[2] + t[3];
         }
         dot = pk::wave_sum(dot);
         const float rs = rstd[row];
@@ -265,12 +350,19 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
         for(int v = 0; v < NV; ++v) {
             const int64_t c = lane + v * 64;
             if(c < C4) {
-                if(flags & 4) {  // dx requested
+                if(flags & 4) {
                     f32x4 o = rs * gv[v] * dv[v] - xv[v] * k;
                     if(flags & PK_ACCUM) o = o + dxr[c];
-                    dxr[c] = o;
+                    pk::st_stream(dxr + c, o);
                 }
                 dg[v] = dg[v] + dv[v] * xv[v] * rs;
+            }
+        }
+        if(more) {
+#pragma unroll
+            for(int v = 0; v < NV; ++v) {
+                xv[v] = xn[v];
+                dv[v] = dn[v];
             }
         }
     }
@@ -291,6 +383,89 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
     }
     f32x4* out = reinterpret_cast<f32x4*>(ws + (int64_t)blockIdx.x * C);
     for(int64_t c = threadIdx.x; c < C4; c += 256) out[c] = reinterpret_cast<f32x4*>(part)[c];
+}
+
+// Wide rows (C4 = C/4 >= 512): the 4 waves of a workgroup share each row, wave w
+// owning the float4 columns [w*Q, (w+1)*Q), Q = ceil(C4/4), NQ float4 per lane.
+// The row's dot product is combined across waves through LDS (one barrier per
+// row, double-buffered); each wave keeps dg for its own columns, so the
+// workgroup's partial needs no combine.  The next row is prefetched.
+template <int NQ, bool EXACT>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_cols(int64_t R, int64_t C,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ g,
+                                                        const float* __restrict__ rstd,
+                                                        const float* __restrict__ dy,
+                                                        float* __restrict__ dx,
+                                                        float* __restrict__ ws, int flags) {
+    __shared__ float red[2][4];
+    const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int64_t C4 = C / 4, Q = (C4 + 3) / 4;
+    const int64_t c0 = w * Q;
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+    f32x4 gv[NQ], dg[NQ];
+    bool on[NQ];
+#pragma unroll
+    for(int v = 0; v < NQ; ++v) {
+        const int64_t q = lane + v * 64, c = c0 + q;
+        on[v] = EXACT || (q < Q && c < C4);
+        gv[v] = on[v] ? g4[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+        dg[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float invC = 1.0f / (float)C;
+    f32x4 xv[NQ], dv[NQ], xn[NQ], dn[NQ];
+    auto load = [&](int64_t r, f32x4 (&a)[NQ], f32x4 (&b)[NQ]) {
+        const f32x4* xr = reinterpret_cast<const f32x4*>(x + r * C) + c0;
+        const f32x4* dr = reinterpret_cast<const f32x4*>(dy + r * C) + c0;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v) {
+            const int64_t q = lane + v * 64;
+            a[v] = on[v] ? pk::ld_stream(xr + q) : f32x4{0.f, 0.f, 0.f, 0.f};
+            b[v] = on[v] ? pk::ld_stream(dr + q) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    int64_t row = blockIdx.x;
+    if(row < R) load(row, xv, dv);
+    for(int it = 0; row < R; row += gridDim.x, ++it) {
+        const bool more = row + gridDim.x < R;
+        if(more) load(row + gridDim.x, xn, dn);
+        float dot = 0.0f;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v) {
+            const f32x4 t = gv[v] * dv[v] * xv[v];
+            dot += t[0] + t[1] + t[2] + t[3];
+        }
+        dot = pk::wave_sum(dot);
+        if(lane == 0) red[it & 1][w] = dot;
+        __syncthreads();
+        dot = ((red[it & 1][0] + red[it & 1][1]) + red[it & 1][2]) + red[it & 1][3];
+        const float rs = rstd[row];
+        const float k = rs * rs * rs * dot * invC;
+        f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * C) + c0;
+#pragma unroll
+        for(int v = 0; v < NQ; ++v) {
+            if(!on[v]) continue;
+            const int64_t q = lane + v * 64;
+            if(flags & 4) {
+                f32x4 o = rs * gv[v] * dv[v] - xv[v] * k;
+                if(flags & PK_ACCUM) o = o + dxr[q];
+                pk::st_stream(dxr + q, o);
+            }
+            dg[v] = dg[v] + dv[v] * xv[v] * rs;
+        }
+        if(more) {
+#pragma unroll
+            for(int v = 0; v < NQ; ++v) {
+                xv[v] = xn[v];
+                dv[v] = dn[v];
+            }
+        }
+    }
+    if(!(flags & 8)) return;
+    f32x4* out = reinterpret_cast<f32x4*>(ws + (int64_t)blockIdx.x * C) + c0;
+#pragma unroll
+    for(int v = 0; v < NQ; ++v)
+        if(on[v]) out[lane + v * 64] = dg[v];
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_bwd_any(int64_t R, int64_t C,
@@ -328,20 +503,28 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_any(int64_t R, int64_t C,
     }
 }
 
-// backward, stage 2: dg (+)= sum over the partial rows; 64 columns per block,
-// 4 waves split the partial rows, combined in a fixed order
-__global__ __launch_bounds__(256) void colsum_kernel(int64_t P, int64_t C, const float* __restrict__ ws,
-                                                     float* __restrict__ dg, int accum) {
-    __shared__ float part[4][64];
+// backward, stage 2: dg (+)= sum over the partial rows.  64 columns per
+// block; its 16 waves each sum every 16th partial row (independent loads, so
+// they are in flight together), then the 16 sums are combined in a fixed order.
+constexpr int kColsumWaves = 16;
+__global__ __launch_bounds__(64 * kColsumWaves) void colsum_kernel(int64_t P, int64_t C,
+                                                                 const float* __restrict__ ws,
+                                                                 float* __restrict__ dg,
+                                                                 int accum) {
+    __shared__ float part[kColsumWaves][64];
     const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int64_t c = (int64_t)blockIdx.x * 64 + lane;
     float acc = 0.0f;
-    if(c < C)
-        for(int64_t p = w; p < P; p += 4) acc += ws[p * C + c];
+    if(c < C) {
+#pragma unroll 8
+        for(int64_t p = w; p < P; p += kColsumWaves) acc += ws[p * C + c];
+    }
     part[w][lane] = acc;
     __syncthreads();
     if(w == 0 && c < C) {
-        const float s = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+        float s = part[0][lane];
+#pragma unroll
+        for(int i = 1; i < kColsumWaves; ++i) s += part[i][lane];
         dg[c] = accum ? dg[c] + s : s;
     }
 }
@@ -358,11 +541,11 @@ __global__ void swiglu_fwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
                             f32x4* __restrict__ h) {
     for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
         i += (int64_t)gridDim.x * blockDim.x) {
-        const f32x4 av = a[i], uv = u[i];
+        const f32x4 av = pk::ld_stream(a + i), uv = pk::ld_stream(u + i);
         f32x4 o;
 #pragma unroll
         for(int e = 0; e < 4; ++e) o[e] = av[e] * sigmoidf_(av[e]) * uv[e];
-        h[i] = o;
+        pk::st_stream(h + i, o);
     }
 }
 
@@ -383,7 +566,7 @@ __global__ void swiglu_bwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
                             f32x4* __restrict__ du, int flags) {
     for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
         i += (int64_t)gridDim.x * blockDim.x) {
-        const f32x4 av = a[i], uv = u[i], g = dh[i];
+        const f32x4 av = pk::ld_stream(a + i), uv = pk::ld_stream(u + i), g = pk::ld_stream(dh + i);
         f32x4 ga, gu;
 #pragma unroll
         for(int e = 0; e < 4; ++e) {
@@ -391,8 +574,8 @@ __global__ void swiglu_bwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
             ga[e] = g[e] * uv[e] * s * (1.0f + av[e] * (1.0f - s));
             gu[e] = g[e] * av[e] * s;
         }
-        if(flags & 4) da[i] = (flags & PK_ACCUM) ? da[i] + ga : ga;
-        if(flags & 8) du[i] = (flags & PK_ACCUM2) ? du[i] + gu : gu;
+        if(flags & 4) pk::st_stream(da + i, (flags & PK_ACCUM) ? da[i] + ga : ga);
+        if(flags & 8) pk::st_stream(du + i, (flags & PK_ACCUM2) ? du[i] + gu : gu);
     }
 }
 
@@ -564,18 +747,27 @@ extern "C" int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, in
                      (!dlogits || (ldd % 4 == 0 && pk::aligned16(dlogits)));
     const int64_t V4 = V / 4;
     dim3 grid((unsigned)R);
+#define PK_XENT(NT_, NV_)                                                                       \
+    xent_reg_kernel<NT_, NV_><<<grid, NT_, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, \
+                                                    ldd, scale, scale_dev, accum)
     if(vec && V4 <= 256 * 1)
-        xent_reg_kernel<256, 1><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
+        PK_XENT(256, 1);
     else if(vec && V4 <= 256 * 2)
-        xent_reg_kernel<256, 2><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
+        PK_XENT(256, 2);
     else if(vec && V4 <= 256 * 4)
-        xent_reg_kernel<256, 4><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
+        PK_XENT(256, 4);
     else if(vec && V4 <= 256 * 8)
-        xent_reg_kernel<256, 8><<<grid, 256, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
-    else if(vec && V4 <= 1024 * 8)
-        xent_reg_kernel<1024, 8><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
+        PK_XENT(256, 8);
+    else if(vec && V4 <= 256 * 16)
+        PK_XENT(256, 16);
+    else if(vec && V4 <= 256 * 32)
+        PK_XENT(256, 32);
+    else if(vec && V4 <= 1024 * 16)
+        PK_XENT(1024, 16);
     else
-        xent_any_kernel<1024><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, scale_dev, accum);
+        xent_any_kernel<1024><<<grid, 1024, 0, st>>>(V, logits, ldz, labels, loss_rows, dlogits, ldd,
+                                                     scale, scale_dev, accum);
+#undef PK_XENT
     return pk::launch_status("pk_xent_fwd_bwd_f32");
 }
 
@@ -594,9 +786,30 @@ extern "C" int pk_rmsnorm_fwd_f32(int64_t R, int64_t C, float eps, const float* 
     if(R == 0) return PK_OK;
     if(!x || !g || !y) return pk::fail("pk_rmsnorm_fwd_f32: NULL pointer");
     hipStream_t st = pk::as_stream(stream);
-    const unsigned grid = (unsigned)((R + 3) / 4);
     const bool vec = C % 4 == 0 && pk::aligned16(x) && pk::aligned16(g) && pk::aligned16(y);
     const int nv = vec ? pick_nv(C) : 0;
+    const int64_t blocks = (R + 3) / 4;
+    const unsigned grid = (unsigned)blocks;  // one row per wave
+    if(vec && C / 4 >= 512 && C <= 16384) {
+        const int64_t Q = (C / 4 + 3) / 4;
+        const unsigned cgrid = (unsigned)(R < 512 ? R : 512);
+#define PK_RMSF(NQ_)                                                                        \
+    if(C % 1024 == 0 && Q == NQ_ * 64)                                                       \
+        rmsnorm_fwd_cols<NQ_, true><<<cgrid, 256, 0, st>>>(R, C, eps, x, g, y, rstd);       \
+    else                                                                                     \
+        rmsnorm_fwd_cols<NQ_, false><<<cgrid, 256, 0, st>>>(R, C, eps, x, g, y, rstd)
+        if(Q <= 128) {
+            PK_RMSF(2);
+        } else if(Q <= 256) {
+            PK_RMSF(4);
+        } else if(Q <= 512) {
+            PK_RMSF(8);
+        } else {
+            PK_RMSF(16);
+        }
+#undef PK_RMSF
+        return pk::launch_status("pk_rmsnorm_fwd_f32");
+    }
     switch(nv) {
         case 1: rmsnorm_fwd_reg<1><<<grid, 256, 0, st>>>(R, C, eps, x, g, y, rstd); break;
         case 2: rmsnorm_fwd_reg<2><<<grid, 256, 0, st>>>(R, C, eps, x, g, y, rstd); break;
@@ -634,7 +847,25 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
                      (!dx || pk::aligned16(dx)) && (!ws || pk::aligned16(ws));
     const int nv = vec && C <= 8192 ? pick_nv(C) : 0;
     const size_t lds = (size_t)C * sizeof(float);
-    switch(nv) {
+    if(vec && C / 4 >= 512 && C <= 16384) {
+        const int64_t Q = (C / 4 + 3) / 4;
+        const unsigned grid = (unsigned)P;
+#define PK_RMSB(NQ_)                                                                           \
+    if(C % 1024 == 0 && Q == NQ_ * 64)                                                          \
+        rmsnorm_bwd_cols<NQ_, true><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dx, ws, kf);   \
+    else                                                                                        \
+        rmsnorm_bwd_cols<NQ_, false><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dx, ws, kf)
+        if(Q <= 128) {
+            PK_RMSB(2);
+        } else if(Q <= 256) {
+            PK_RMSB(4);
+        } else if(Q <= 512) {
+            PK_RMSB(8);
+        } else {
+            PK_RMSB(16);
+        }
+#undef PK_RMSB
+    } else switch(nv) {
         case 1: rmsnorm_bwd_reg<1><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
         case 2: rmsnorm_bwd_reg<2><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
         case 4: rmsnorm_bwd_reg<4><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
@@ -645,7 +876,8 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
     }
     int rc = pk::launch_status("pk_rmsnorm_bwd_f32");
     if(rc || !dg) return rc;
-    colsum_kernel<<<(unsigned)((C + 63) / 64), 256, 0, st>>>(P, C, ws, dg, (flags & PK_ACCUM2) ? 1 : 0);
+    colsum_kernel<<<(unsigned)((C + 63) / 64), 64 * kColsumWaves, 0, st>>>(
+        P, C, ws, dg, (flags & PK_ACCUM2) ? 1 : 0);
     return pk::launch_status("pk_rmsnorm_bwd_f32");
 }
 
@@ -659,7 +891,7 @@ extern "C" int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t l
     const int64_t n = R * F;
     if(lda == F && ldu == F && ldh == F && n % 4 == 0 && pk::aligned16(a) && pk::aligned16(u) &&
        pk::aligned16(h))
-        swiglu_fwd4<<<pk::grid_for(n / 4, 256, 256 * 8), 256, 0, st>>>(n / 4, (const f32x4*)a,
+        swiglu_fwd4<<<pk::grid_stream(n / 4, 256), 256, 0, st>>>(n / 4, (const f32x4*)a,
                                                                        (const f32x4*)u, (f32x4*)h);
     else
         swiglu_fwd_any<<<pk::grid_for(n, 256, 256 * 8), 256, 0, st>>>(R, F, a, lda, u, ldu, h, ldh);
@@ -679,7 +911,7 @@ extern "C" int pk_swiglu_bwd_f32(int64_t R, int64_t F, const float* a, int64_t l
     if(lda == F && ldu == F && ldh == F && ldd == F && n % 4 == 0 && pk::aligned16(a) &&
        pk::aligned16(u) && pk::aligned16(dh) && (!da || pk::aligned16(da)) &&
        (!du || pk::aligned16(du)))
-        swiglu_bwd4<<<pk::grid_for(n / 4, 256, 256 * 8), 256, 0, st>>>(
+        swiglu_bwd4<<<pk::grid_stream(n / 4, 256), 256, 0, st>>>(
             n / 4, (const f32x4*)a, (const f32x4*)u, (const f32x4*)dh, (f32x4*)da, (f32x4*)du, kf);
     else
         swiglu_bwd_any<<<pk::grid_for(n, 256, 256 * 8), 256, 0, st>>>(R, F, a, lda, u, ldu, dh, ldh,

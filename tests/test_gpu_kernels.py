@@ -320,7 +320,8 @@ def test_argmax_bitexact(dev, R, V):
     assert np.array_equal(host(idx), ref)
 
 
-@pytest.mark.parametrize("R,C", [(5, 24), (64, 512), (33, 768), (16, 4096), (7, 10001), (3, 9000)])
+@pytest.mark.parametrize("R,C", [(5, 24), (64, 512), (33, 768), (16, 4096), (7, 10001), (3, 9000),
+                                 (1030, 2048), (9, 2052), (5, 3072), (600, 8192)])
 def test_rmsnorm_vs_oracle(dev, R, C):
     x = O.normal(R * C, 1).reshape(R, C)
     g = O.normal(C, 2, 1.0, 0.02)
