@@ -7,7 +7,11 @@ One step = the three products of one matmul's forward and backward
 
 Also reported, outside the timed region:
   roofline      the GEMM kernel's FLOP per launch / its mean launch time
-                (HIP events on the launch stream) against 157.3 TFLOP/s
+                (HIP events on the launch stream) against 157.3 TFLOP/s; its
+                HBM bytes per launch come from the committed rocprofv3 PMC
+                summary (profiles/traffic.json)
+  train         configs 4 and 5: one AdamW training step of the transformer
+                built from pico ops (pico_amd/host/gpt.c) per step, tokens/s
   sweep         TFLOP/s for n in {512..8192} and each layout
   row_kernels   RMSNorm / SwiGLU / softmax-CE at the config-3 shapes: GB/s of
                 algorithmic traffic against 8 TB/s (buffer sets rotated past
@@ -27,6 +31,16 @@ sys.path.insert(0, ROOT)
 
 MFMA_FP32_PEAK = 157.3e12
 HBM_PEAK = 8.0e12
+
+
+def _measured_traffic(key):
+    """HBM bytes per launch of one kernel, from the committed rocprofv3 PMC
+    summary (profiles/traffic.json); None when it has no figure for it"""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)["bytes_per_launch"].get(key)
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def _events_time(fn, reps, warmup):
@@ -114,7 +128,7 @@ def rows_section(torch, K):
     res = {}
     sets = 4
 
-    def bw(name, nbytes, fns):
+    def bw(name, nbytes, fns, shape=""):
         i = [0]
 
         def call():
@@ -124,6 +138,7 @@ def rows_section(torch, K):
         mean_ms, med_ms = _events_time(call, 20, len(fns))
         gbs = nbytes / (mean_ms * 1e-3) / 1e9
         res[name] = {"us": round(mean_ms * 1e3, 1), "GB/s": round(gbs, 1),
+                     "traffic_bytes": _measured_traffic(f"{name} {shape}"),
                      "frac": round(gbs * 1e9 / HBM_PEAK, 3)}
 
     # context: what a plain device copy (torch's kernel) reaches on this box
@@ -138,12 +153,13 @@ def rows_section(torch, K):
     g = 1 + 0.02 * torch.randn(Cc, device=dev)
     rs = [torch.empty(R, device=dev) for _ in range(sets)]
     bw("rmsnorm_fwd", 2 * R * Cc * 4,
-       [lambda j=j: K.rmsnorm_fwd(xs[j], g, ys[j], rs[j], 1e-6) for j in range(sets)])
+       [lambda j=j: K.rmsnorm_fwd(xs[j], g, ys[j], rs[j], 1e-6) for j in range(sets)],
+       f"{R}x{Cc}")
     dgs = torch.empty(Cc, device=dev)
     ws = torch.empty(K.rmsnorm_bwd_workspace(R, Cc) // 4, device=dev)
     bw("rmsnorm_bwd", 3 * R * Cc * 4,
        [lambda j=j: K.rmsnorm_bwd(xs[j], g, rs[j], ys[(j + 1) % sets], ys[(j + 2) % sets], dgs, ws)
-        for j in range(sets)])
+        for j in range(sets)], f"{R}x{Cc}")
     del xs, ys, rs
     # SwiGLU 8192 x 11008
     R, F = 8192, 11008
@@ -151,10 +167,11 @@ def rows_section(torch, K):
     u = [torch.randn(R, F, device=dev) for _ in range(sets)]
     h = [torch.empty(R, F, device=dev) for _ in range(sets)]
     bw("swiglu_fwd", 3 * R * F * 4,
-       [lambda j=j: K.swiglu_fwd(a[j], u[j], h[j]) for j in range(sets)])
+       [lambda j=j: K.swiglu_fwd(a[j], u[j], h[j]) for j in range(sets)], f"{R}x{F}")
     da = [torch.empty(R, F, device=dev) for _ in range(2)]
     bw("swiglu_bwd", 5 * R * F * 4,
-       [lambda j=j: K.swiglu_bwd(a[j], u[j], h[j], da[0], da[1]) for j in range(sets)])
+       [lambda j=j: K.swiglu_bwd(a[j], u[j], h[j], da[0], da[1]) for j in range(sets)],
+       f"{R}x{F}")
     del a, u, h, da
     # softmax-CE 8192 x 32000, fused forward + backward
     R, V = 8192, 32000
@@ -163,7 +180,8 @@ def rows_section(torch, K):
     loss = torch.empty(R, device=dev)
     dz = [torch.empty(R, V, device=dev) for _ in range(2)]
     bw("xent_fwd_bwd", 2 * R * V * 4,
-       [lambda j=j: K.xent_fwd_bwd(zs[j], lab, loss, dz[j], scale=1.0 / R) for j in range(2)])
+       [lambda j=j: K.xent_fwd_bwd(zs[j], lab, loss, dz[j], scale=1.0 / R) for j in range(2)],
+       f"{R}x{V}")
     return res
 
 
@@ -329,11 +347,23 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2),
                      "peak": MFMA_FP32_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_FP32_PEAK, 4), "traffic": None,
+                     "frac": round(achieved / MFMA_FP32_PEAK, 4),
+                     "traffic": _measured_traffic(f"gemm_f32_kernel<N,N> {args.n}^3"),
+                     "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE x2.00 + "
+                                       "WRITE_SIZE x1.00, calibrated on a 256 MiB copy)",
                      "kernel": "gemm_f32_kernel<N,N> (one launch = 2n^3 FLOP)",
                      "kernel_ms": round(g["nn_kernel_ms"], 4)},
         "device": info,
     }
+    if "calib" in sections:
+        # a plain copy of known size (256 MiB read + 256 MiB written per launch):
+        # the yardstick that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes
+        src = torch.empty(1 << 26, device="cuda:0").uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if "train" in sections:
         line["train"] = {name: train_section(name, args.train_steps, 3)
                          for name in args.train_configs.split(",") if name}
