@@ -65,6 +65,11 @@ PK_SIGNATURES = {
                                c_p],
     "pk_attn_causal_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p,
                                c_p, c_p, c_p, c_int, c_p],
+    "pk_flash_attn_supported": [c_i64, c_i64],
+    "pk_flash_attn_fwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p],
+    "pk_flash_attn_bwd_workspace": [c_i64, c_i64, c_i64],
+    "pk_flash_attn_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+                              c_p, c_p, c_p, c_size, c_int, c_p],
     "pk_causal_softmax_fwd_f32": [c_i64, c_i64, c_f, c_p, c_p, c_p, c_p],
     "pk_causal_softmax_bwd_f32": [c_i64, c_i64, c_p, c_p, c_p, c_p],
     "pk_embed_fwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p],
@@ -72,7 +77,7 @@ PK_SIGNATURES = {
     "pk_last_error": [],
 }
 _RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size,
-             "pk_gemm_workspace_f32": c_size}
+             "pk_gemm_workspace_f32": c_size, "pk_flash_attn_bwd_workspace": c_size}
 
 _hip = None
 

@@ -179,10 +179,13 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
 }
 
 /* -------------------------------------------------------- causal attention
- * q, k, v token-major [batch*T, heads*hd]; out the same.  Saved: lse [B*H*T]
- * and the probabilities P [B*H, T, T] (arena device memory). */
+ * q, k, v token-major [batch*T, heads*hd]; out the same.  For head size 64 and
+ * T a multiple of 128 the fused kernels run (pk_flash_attn_*): only lse
+ * [B*H*T] is saved and the scores never reach memory.  Otherwise the chain of
+ * batched GEMMs and causal-softmax kernels runs and saves the probabilities
+ * P [B*H, T, T] (arena device memory). */
 enum { AS_LSE = 0, AS_P = 1 };
-enum { AI_B = 0, AI_H = 1 };
+enum { AI_B = 0, AI_H = 1, AI_FLASH = 2 };
 
 static void attn_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
@@ -191,17 +194,28 @@ static void attn_backward(struct PicoTensor* self) {
     if(!dout) return;
     int64_t B = n->ival[AI_B], H = n->ival[AI_H];
     int64_t T = q->shape[0] / B, hd = q->shape[1] / H;
-    void* ws = pkh_workspace(sizeof(float) * (size_t)(B * H * T * T));
+    const int flash = (int)n->ival[AI_FLASH];
+    size_t ws_bytes = flash ? pk_flash_attn_bwd_workspace(B, H, T)
+                            : sizeof(float) * (size_t)(B * H * T * T);
+    void* ws = pkh_workspace(ws_bytes);
     if(!ws) return;
-    /* the launcher writes dv, then dq, then dk: aliased grads accumulate */
+    /* aliased grads (q, k or v the same tensor) accumulate when each write
+     * after the first carries its accumulate bit; the write order is dv, dk,
+     * dq (fused) or dv, dq, dk (chain) */
+    struct PicoTensor* order[3] = {v, flash ? k : q, flash ? q : k};
+    const int bit[3] = {PK_ACCUM3, flash ? PK_ACCUM2 : PK_ACCUM, flash ? PK_ACCUM : PK_ACCUM2};
     int flags = 0;
-    if(pkh_grad_flag(v)) flags |= PK_ACCUM3;
-    pkh_grad_mark(v);
-    if(pkh_grad_flag(q)) flags |= PK_ACCUM;
-    pkh_grad_mark(q);
-    if(pkh_grad_flag(k)) flags |= PK_ACCUM2;
-    pkh_grad_mark(k);
-    int st = pk_attn_causal_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+    for(int i = 0; i < 3; i++) {
+        if(pkh_grad_flag(order[i])) flags |= bit[i];
+        pkh_grad_mark(order[i]);
+    }
+    int st;
+    if(flash)
+        st = pk_flash_attn_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data, self->data,
+                                   (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad,
+                                   ws, ws_bytes, flags, pkh_stream());
+    else
+        st = pk_attn_causal_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
                                     (const float*)n->saved[AS_P], dout, q->grad, k->grad, v->grad,
                                     (float*)ws, flags, pkh_stream());
     pkh_status("pico_attention_causal_backward", st);
@@ -229,16 +243,20 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     struct PicoTensor* out = pkh_new_tensor(arena, q->shape, 2);
     if(!out) return NULL;
     struct PkNode* n = pkh_node(out);
+    const int flash = pk_flash_attn_supported(T, hd);
     float* lse = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T));
-    float* P = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T));
-    if(!lse || !P) return NULL;
+    float* P = flash ? NULL : (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T));
+    if(!lse || (!flash && !P)) return NULL;
     n->saved[AS_LSE] = lse;
     n->saved[AS_P] = P;
     n->ival[AI_B] = B;
     n->ival[AI_H] = H;
+    n->ival[AI_FLASH] = flash;
     n->fval[0] = 1.0f / sqrtf((float)hd);
-    int st = pk_attn_causal_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data, out->data,
-                                    lse, P, pkh_stream());
+    int st = flash ? pk_flash_attn_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+                                           out->data, lse, pkh_stream())
+                   : pk_attn_causal_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+                                            out->data, lse, P, pkh_stream());
     if(pkh_status("pico_attention_causal", st)) return NULL;
     pkh_set_parents(arena, out, 3, xs, attn_backward);
     return out;

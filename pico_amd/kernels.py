@@ -264,6 +264,31 @@ def attn_bwd(B, H, q, k, v, P, dout, dq, dk, dv, dP_ws, accumulate=False, scale=
         _ptr(dv), _ptr(dP_ws), 7 if accumulate else 0, _stream()))
 
 
+def flash_supported(T, hd):
+    return bool(hip_lib().pk_flash_attn_supported(T, hd))
+
+
+def flash_fwd(B, H, q, k, v, o, lse, scale=None):
+    BT, D = q.shape
+    T, hd = BT // B, D // H
+    if B * T != BT or H * hd != D or lse.numel() < B * H * T or o.shape != q.shape:
+        raise ValueError("attention shape mismatch")
+    scale = hd ** -0.5 if scale is None else scale
+    check("pk_flash_attn_fwd_f32", hip_lib().pk_flash_attn_fwd_f32(
+        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
+
+
+def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None):
+    BT, D = q.shape
+    T, hd = BT // B, D // H
+    scale = hd ** -0.5 if scale is None else scale
+    need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
+    ws = torch.empty(max(1, need // 4), device=q.device, dtype=torch.float32)
+    check("pk_flash_attn_bwd_f32", hip_lib().pk_flash_attn_bwd_f32(
+        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout), _ptr(dq),
+        _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() * 4, flags, _stream()))
+
+
 def causal_softmax_fwd(BH, T, S, P, lse, scale=1.0):
     check("pk_causal_softmax_fwd_f32", hip_lib().pk_causal_softmax_fwd_f32(
         BH, T, scale, _ptr(S), _ptr(P), _ptr(lse), _stream()))

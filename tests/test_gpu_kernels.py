@@ -397,3 +397,44 @@ def test_embedding(dev):
     out = torch.empty(GOLD["emb_ids"].size, GOLD["emb_table"].shape[1], device=dev)
     K.embed_fwd(cu(GOLD["emb_ids"]), cu(GOLD["emb_table"]), out)
     assert np.array_equal(host(out), GOLD["emb_out"].astype(np.float32))
+
+
+# ------------------------------------------------------- fused attention (hd 64)
+@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (1, 2, 1024)])
+def test_flash_attention_vs_oracle(dev, B, H, T):
+    hd, D = 64, H * 64
+    assert K.flash_supported(T, hd) and not K.flash_supported(T + 64, hd)
+    q, k, v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (11, 12, 13, 14))
+    o = torch.empty(B * T, D, device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    K.flash_fwd(B, H, cu(q), cu(k), cu(v), o, lse)
+    o_ref, lse_ref = O.attn_fwd(B, H, q, k, v)
+    assert max_rel(host(o), o_ref) <= TOL and max_rel(host(lse), lse_ref) <= TOL
+    dq, dk, dv = (torch.full((B * T, D), float("nan"), device=dev) for _ in range(3))
+    K.flash_bwd(B, H, cu(q), cu(k), cu(v), cu(o_ref), cu(lse_ref), cu(do), dq, dk, dv)
+    refs = O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)
+    for got, ref in zip((dq, dk, dv), refs):
+        assert max_rel(host(got), ref) <= TOL
+    # accumulate bits: each output adds onto what it holds
+    base = [O.normal(B * T * D, 20 + i).reshape(B * T, D) for i in range(3)]
+    acc = [cu(b.copy()) for b in base]
+    K.flash_bwd(B, H, cu(q), cu(k), cu(v), cu(o_ref), cu(lse_ref), cu(do), *acc, flags=7)
+    for got, ref, b0 in zip(acc, refs, base):
+        assert max_rel(host(got) - b0, ref) <= TOL
+
+
+def test_flash_attention_causality(dev):
+    # a change to the last key/value of each sequence leaves every earlier
+    # query's output unchanged (bit for bit) and changes the last one
+    B, H, T, D = 2, 2, 256, 128
+    q, k, v = (O.normal(B * T * D, s).reshape(B * T, D) for s in (1, 2, 3))
+    o1, o2 = torch.empty(B * T, D, device=dev), torch.empty(B * T, D, device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    K.flash_fwd(B, H, cu(q), cu(k), cu(v), o1, lse)
+    k2, v2 = k.copy(), v.copy()
+    for b in range(B):
+        k2[b * T + T - 1] += 1.0
+        v2[b * T + T - 1] -= 1.0
+    K.flash_fwd(B, H, cu(q), cu(k2), cu(v2), o2, lse)
+    a, c = host(o1).reshape(B, T, D), host(o2).reshape(B, T, D)
+    assert np.array_equal(a[:, :-1], c[:, :-1]) and not np.array_equal(a[:, -1], c[:, -1])

@@ -376,3 +376,21 @@ def test_config1_mlp_loss_curve_matches_cpu(P, C):
     assert max_rel(gpu, cpu) <= TOL
     for g, c in zip(gp, cp):
         assert max_rel(g, c) <= TOL
+
+
+def test_self_attention_shared_parent_vs_oracle(P, C):
+    # attention(x, x, x) through the fused kernels (T 128, head size 64): the
+    # three gradient contributions land in one grad buffer
+    B, T, H, hd = 2, 128, 2, 64
+    D = H * hd
+    xv = O.normal(B * T * D, 5).reshape(B * T, D)
+    res = []
+    for L in (P, C):
+        with L.arena(1 << 24):
+            x = L.param([B * T, D], xv)
+            out = L.attention_causal(x, x, x, B, H)
+            L.backward(L.mul(out, out))
+            res.append((L.data(out), L.grad(x)))
+    assert max_rel(res[0][0], res[1][0]) <= TOL
+    assert max_rel(res[0][1], res[1][1]) <= TOL
+
