@@ -28,11 +28,19 @@
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
-constexpr int KF = BK + 4;     // row stride of a k-contiguous LDS tile [128][36]
-constexpr int RF = BM + 4;     // row stride of a row-contiguous LDS tile [32][132]
-constexpr int TILE = BM * KF;  // floats per LDS tile (>= BK * RF)
+constexpr int BM = 128, BK = 32, NT = 256;
+constexpr int KF = BK + 4;  // row stride of a k-contiguous LDS tile [rows][36]
 constexpr int GROUP_M = 8;
+
+// An R x BK operand slice (R = 128 or 96 rows): float4 per thread, the row
+// stride of its row-contiguous LDS form [BK][R+4], and the LDS floats it needs.
+template <int R>
+struct Slice {
+    static constexpr int V = R * BK / 4 / NT;
+    static constexpr int Q4 = R / 4;  // float4 per k-row of the row-contiguous form
+    static constexpr int RF = R + 4;
+    static constexpr int FLOATS = R * KF > BK * RF ? R * KF : BK * RF;
+};
 
 struct GemmParams {
     const float* A;
@@ -48,21 +56,23 @@ struct GemmParams {
     float* ws;
 };
 
-// One 128x32 operand slice -> 4 float4 per thread.  KFAST: element (r,k) at
-// base[r*ld + k]; otherwise at base[k*ld + r].  EDGE zero-fills outside [R) x [K).
-template <bool KFAST, bool EDGE>
+// One R x 32 operand slice -> Slice<R>::V float4 per thread.  KFAST: element
+// (r,k) at base[r*ld + k]; otherwise at base[k*ld + r].  EDGE zero-fills
+// outside [Rlim) x [K).
+template <bool KFAST, bool EDGE, int R>
 __device__ __forceinline__ void load_slice(const float* __restrict__ base, int64_t ld, int64_t r0,
-                                           int64_t k0, int64_t R, int64_t K, f32x4 (&v)[4]) {
+                                           int64_t k0, int64_t Rlim, int64_t K,
+                                           f32x4 (&v)[Slice<R>::V]) {
 #pragma unroll
-    for(int i = 0; i < 4; ++i) {
+    for(int i = 0; i < Slice<R>::V; ++i) {
         const int idx = threadIdx.x + i * NT;
         int rr, kk;
         if(KFAST) {
             rr = idx >> 3;
             kk = (idx & 7) * 4;
         } else {
-            kk = idx >> 5;
-            rr = (idx & 31) * 4;
+            kk = idx / Slice<R>::Q4;
+            rr = (idx % Slice<R>::Q4) * 4;
         }
         const int64_t r = r0 + rr, k = k0 + kk;
         if(!EDGE) {
@@ -71,7 +81,7 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int64
         } else {
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
             if(KFAST) {
-                if(r < R) {
+                if(r < Rlim) {
                     const float* p = base + r * ld;
 #pragma unroll
                     for(int e = 0; e < 4; ++e)
@@ -82,7 +92,7 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int64
                     const float* p = base + k * ld;
 #pragma unroll
                     for(int e = 0; e < 4; ++e)
-                        if(r + e < R) x[e] = p[r + e];
+                        if(r + e < Rlim) x[e] = p[r + e];
                 }
             }
             v[i] = x;
@@ -90,20 +100,21 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int64
     }
 }
 
-template <bool KFAST>
-__device__ __forceinline__ void store_slice(float* lds, const f32x4 (&v)[4]) {
+template <bool KFAST, int R>
+__device__ __forceinline__ void store_slice(float* lds, const f32x4 (&v)[Slice<R>::V]) {
 #pragma unroll
-    for(int i = 0; i < 4; ++i) {
+    for(int i = 0; i < Slice<R>::V; ++i) {
         const int idx = threadIdx.x + i * NT;
         if(KFAST)
             *reinterpret_cast<f32x4*>(lds + (idx >> 3) * KF + (idx & 7) * 4) = v[i];
         else
-            *reinterpret_cast<f32x4*>(lds + (idx >> 5) * RF + (idx & 31) * 4) = v[i];
+            *reinterpret_cast<f32x4*>(lds + (idx / Slice<R>::Q4) * Slice<R>::RF +
+                                      (idx % Slice<R>::Q4) * 4) = v[i];
     }
 }
 
 // 16 k-values of LDS row r for this lane's k half
-template <bool KFAST>
+template <bool KFAST, int R>
 __device__ __forceinline__ void read_frag(const float* lds, int r, int h, float (&f)[16]) {
     if(KFAST) {
         const f32x4* p = reinterpret_cast<const f32x4*>(lds + r * KF + h * 16);
@@ -117,13 +128,24 @@ __device__ __forceinline__ void read_frag(const float* lds, int r, int h, float 
         }
     } else {
 #pragma unroll
-        for(int s = 0; s < 16; ++s) f[s] = lds[(h * 16 + s) * RF + r];
+        for(int s = 0; s < 16; ++s) f[s] = lds[(h * 16 + s) * Slice<R>::RF + r];
     }
 }
 
-template <bool TA, bool TB, bool EDGE>
+// Wave layout of a BM x BN tile: BN = 128 -> 2 x 2 waves, each 64 x 64 = 2 x 2
+// blocks of 32 x 32; BN = 96 -> 4 x 1 waves, each 32 x 96 = 1 x 3 blocks.
+template <int BN>
+struct WaveGrid {
+    static constexpr int TN = BN == 128 ? 2 : 3;  // 32x32 blocks per wave along N
+    static constexpr int TM = BN == 128 ? 2 : 1;  // along M
+    static constexpr int WN = BN / (32 * TN);     // waves along N
+};
+
+template <bool TA, bool TB, bool EDGE, int BN>
 __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) float lds[2][2][TILE];
+    constexpr int TM = WaveGrid<BN>::TM, TN = WaveGrid<BN>::TN, WN = WaveGrid<BN>::WN;
+    __shared__ __attribute__((aligned(16))) float ldsA[2][Slice<BM>::FLOATS];
+    __shared__ __attribute__((aligned(16))) float ldsB[2][Slice<BN>::FLOATS];
 
     // ---- tile selection: XCD-contiguous runs, grouped by GROUP_M tile-rows
     const int ntiles = p.tiles_m * p.tiles_n;
@@ -162,26 +184,26 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     const int nslices = (int)((kend - kbeg + BK - 1) / BK);
 
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-    const int wm = w >> 1, wn = w & 1;
+    const int wm = w / WN, wn = w % WN;
     const int lr = l & 31, lh = l >> 5;
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for(int i = 0; i < 2; ++i)
+    for(int i = 0; i < TM; ++i)
 #pragma unroll
-        for(int j = 0; j < 2; ++j)
+        for(int j = 0; j < TN; ++j)
 #pragma unroll
             for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
     // (indexed by n) are k-contiguous when B is transposed.
     constexpr bool AK = !TA, BKF = TB;
-    f32x4 ra[4], rb[4];
+    f32x4 ra[Slice<BM>::V], rb[Slice<BN>::V];
     if(nslices > 0) {
-        load_slice<AK, EDGE>(A, p.lda, row0, kbeg, p.M, kend, ra);
-        load_slice<BKF, EDGE>(B, p.ldb, col0, kbeg, p.N, kend, rb);
-        store_slice<AK>(lds[0][0], ra);
-        store_slice<BKF>(lds[0][1], rb);
+        load_slice<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, ra);
+        load_slice<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, rb);
+        store_slice<AK, BM>(ldsA[0], ra);
+        store_slice<BKF, BN>(ldsB[0], rb);
     }
     __syncthreads();
 
@@ -190,25 +212,27 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
         const bool more = s + 1 < nslices;
         if(more) {
             const int64_t k0 = kbeg + (int64_t)(s + 1) * BK;
-            load_slice<AK, EDGE>(A, p.lda, row0, k0, p.M, kend, ra);
-            load_slice<BKF, EDGE>(B, p.ldb, col0, k0, p.N, kend, rb);
+            load_slice<AK, EDGE, BM>(A, p.lda, row0, k0, p.M, kend, ra);
+            load_slice<BKF, EDGE, BN>(B, p.ldb, col0, k0, p.N, kend, rb);
         }
-        float fa[2][16], fb[2][16];
+        float fa[TM][16], fb[TN][16];
 #pragma unroll
-        for(int i = 0; i < 2; ++i) read_frag<AK>(lds[cur][0], wm * 64 + i * 32 + lr, lh, fa[i]);
+        for(int i = 0; i < TM; ++i)
+            read_frag<AK, BM>(ldsA[cur], wm * TM * 32 + i * 32 + lr, lh, fa[i]);
 #pragma unroll
-        for(int j = 0; j < 2; ++j) read_frag<BKF>(lds[cur][1], wn * 64 + j * 32 + lr, lh, fb[j]);
+        for(int j = 0; j < TN; ++j)
+            read_frag<BKF, BN>(ldsB[cur], wn * TN * 32 + j * 32 + lr, lh, fb[j]);
 #pragma unroll
         for(int kk = 0; kk < 16; ++kk)
 #pragma unroll
-            for(int i = 0; i < 2; ++i)
+            for(int i = 0; i < TM; ++i)
 #pragma unroll
-                for(int j = 0; j < 2; ++j)
+                for(int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][kk], fb[j][kk],
                                                                      acc[i][j], 0, 0, 0);
         if(more) {
-            store_slice<AK>(lds[cur ^ 1][0], ra);
-            store_slice<BKF>(lds[cur ^ 1][1], rb);
+            store_slice<AK, BM>(ldsA[cur ^ 1], ra);
+            store_slice<BKF, BN>(ldsB[cur ^ 1], rb);
         }
         __syncthreads();
     }
@@ -216,13 +240,13 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     // ---- epilogue: 32x32 block accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
     // column l%32
 #pragma unroll
-    for(int i = 0; i < 2; ++i)
+    for(int i = 0; i < TM; ++i)
 #pragma unroll
-        for(int j = 0; j < 2; ++j) {
-            const int64_t col = col0 + wn * 64 + j * 32 + lr;
+        for(int j = 0; j < TN; ++j) {
+            const int64_t col = col0 + wn * TN * 32 + j * 32 + lr;
 #pragma unroll
             for(int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + wm * 64 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                const int64_t row = row0 + wm * TM * 32 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
                 if(EDGE && (row >= p.M || col >= p.N)) continue;
                 float v = alpha * acc[i][j][r];
                 float* c = C + row * ldc + col;
@@ -266,7 +290,7 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
 constexpr int64_t kSplitTarget = 512, kMinSliceK = 256;
 
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
-    const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int64_t tiles = ((M + BM - 1) / BM) * ((N + 127) / 128);
     *kchunk = K;
     if(tiles <= 0 || tiles * 2 > kSplitTarget || K < 4 * kMinSliceK) return 1;
     int64_t s = kSplitTarget / tiles;
@@ -277,14 +301,38 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     return (int)((K + chunk - 1) / chunk);
 }
 
-template <bool TA, bool TB>
-int launch(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
+// Tile width: 96-wide tiles when N is a multiple of 96 and they fill the 512
+// resident workgroup slots (2 per CU) clearly better than 128-wide ones.  An
+// [8192, 768] output, every projection of a d_model-768 transformer, makes 384
+// 128-wide tiles (75 % of the slots busy) but 512 96-wide ones.
+constexpr int64_t kSlots = 512;
+
+double slot_fill(int64_t tiles) {
+    const int64_t rounds = (tiles + kSlots - 1) / kSlots;
+    return rounds ? (double)tiles / (double)(rounds * kSlots) : 0.0;
+}
+
+int pick_bn(int64_t M, int64_t N, int64_t batch) {
+    if(N % 96) return 128;
+    const int64_t tm = (M + BM - 1) / BM;
+    const int64_t t128 = tm * ((N + 127) / 128) * batch, t96 = tm * (N / 96) * batch;
+    return slot_fill(t96) > slot_fill(t128) + 0.1 ? 96 : 128;
+}
+
+template <bool TA, bool TB, int BN>
+int launch_bn(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
     dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)(gp.splits > 1 ? gp.splits : batch));
     if(edge)
-        gemm_f32_kernel<TA, TB, true><<<grid, NT, 0, st>>>(gp);
+        gemm_f32_kernel<TA, TB, true, BN><<<grid, NT, 0, st>>>(gp);
     else
-        gemm_f32_kernel<TA, TB, false><<<grid, NT, 0, st>>>(gp);
+        gemm_f32_kernel<TA, TB, false, BN><<<grid, NT, 0, st>>>(gp);
     return pk::launch_status("pk_gemm_f32");
+}
+
+template <bool TA, bool TB>
+int launch(const GemmParams& gp, int64_t batch, bool edge, int bn, hipStream_t st) {
+    return bn == 96 ? launch_bn<TA, TB, 96>(gp, batch, edge, st)
+                    : launch_bn<TA, TB, 128>(gp, batch, edge, st);
 }
 
 int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
@@ -309,9 +357,7 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
                         "ldb=%lld needs >= %lld)",
                         (long long)lda, (long long)a_cols, (long long)ldb, (long long)b_cols);
     if(ldc < N) return pk::fail("pk_gemm_f32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
-    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    if(tiles_m * tiles_n > (int64_t)1 << 30 || batch > 65535)
-        return pk::fail("pk_gemm_f32: problem too large for one launch");
+    if(batch > 65535) return pk::fail("pk_gemm_f32: problem too large for one launch");
 
     GemmParams gp;
     gp.A = A;
@@ -333,13 +379,6 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     gp.alpha = alpha;
     gp.beta = beta;
     gp.causal = causal;
-    gp.tiles_m = (int)tiles_m;
-    gp.tiles_n = (int)tiles_n;
-
-    // the unchecked path needs whole tiles and 16-byte aligned float4 loads
-    const bool edge = (M % BM) || (N % BN) || (K % BK) || (lda % 4) || (ldb % 4) ||
-                      (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
-                      !pk::aligned16(A) || !pk::aligned16(B);
     hipStream_t st = pk::as_stream(stream);
     gp.splits = 1;
     gp.kchunk = K;
@@ -353,15 +392,25 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
             gp.ws = ws;
         }
     }
+    const int bn = gp.splits > 1 ? 128 : pick_bn(M, N, batch);
+    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + bn - 1) / bn;
+    if(tiles_m * tiles_n > (int64_t)1 << 30)
+        return pk::fail("pk_gemm_f32: problem too large for one launch");
+    gp.tiles_m = (int)tiles_m;
+    gp.tiles_n = (int)tiles_n;
+    // the unchecked path needs whole tiles and 16-byte aligned float4 loads
+    const bool edge = (M % BM) || (N % bn) || (K % BK) || (lda % 4) || (ldb % 4) ||
+                      (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
+                      !pk::aligned16(A) || !pk::aligned16(B);
     int rc;
     if(!TA && !TB)
-        rc = launch<false, false>(gp, batch, edge, st);
+        rc = launch<false, false>(gp, batch, edge, bn, st);
     else if(!TA && TB)
-        rc = launch<false, true>(gp, batch, edge, st);
+        rc = launch<false, true>(gp, batch, edge, bn, st);
     else if(TA && !TB)
-        rc = launch<true, false>(gp, batch, edge, st);
+        rc = launch<true, false>(gp, batch, edge, bn, st);
     else
-        rc = launch<true, true>(gp, batch, edge, st);
+        rc = launch<true, true>(gp, batch, edge, bn, st);
     if(rc || gp.splits == 1) return rc;
     splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(M, N, gp.splits, gp.ws, alpha,
                                                                   beta, C, ldc);

@@ -438,3 +438,21 @@ def test_flash_attention_causality(dev):
     K.flash_fwd(B, H, cu(q), cu(k2), cu(v2), o2, lse)
     a, c = host(o1).reshape(B, T, D), host(o2).reshape(B, T, D)
     assert np.array_equal(a[:, :-1], c[:, :-1]) and not np.array_equal(a[:, -1], c[:, -1])
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(8192, 768, 768), (1000, 768, 200), (4096, 2304, 256),
+                                    (8192, 768, 2048)])
+def test_gemm_96_wide_tiles(dev, ta, tb, M, N, Kd):
+    # N a multiple of 96: these shapes take the 128 x 96 tiles that fill the
+    # 512 resident workgroup slots (a d_model-768 transformer's projections)
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 3 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N + Kd + 1)
+    C0 = O.uniform(M * N, 9).reshape(M, N)
+    C = cu(C0.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=2.0, beta=1.0)
+    assert gemm_err(host(C) - C0, 2.0 * A, B) <= TOL
