@@ -251,6 +251,7 @@ def train_section(name, steps, warmup):
     P.sync()
     wall = time.perf_counter() - t0
     step(keep_loss=True)
+    _, peak_bytes = P.memory()
     err = lib.pico_gpu_last_error().decode()
     lib.arena_ctx_pop()
     lib.arena_destroy(work)
@@ -266,6 +267,7 @@ def train_section(name, steps, warmup):
             "mfu": round(flop / (ms * 1e-3) / MFMA_FP32_PEAK, 4),
             "tokens_per_step": n, "steps": steps, "warmup": warmup,
             "loss_first": round(losses[0], 5), "loss_after": round(losses[-1], 5),
+            "device_gib_peak": round(peak_bytes / 2 ** 30, 2),
             "optimizer": dict(ADAMW, name="AdamW"), "config": cfg}
 
 

@@ -240,6 +240,9 @@ int pico_gpu_synchronize(void);
 void* pico_gpu_stream(void);            /* the hipStream_t every launch uses */
 void pico_gpu_set_stream(void* stream); /* NULL restores the library's own */
 const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
+/* device bytes this library holds now, and the most it has held (params,
+ * arena blocks, optimizer moments, scratch) */
+void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
 
 #ifdef __cplusplus

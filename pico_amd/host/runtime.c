@@ -53,7 +53,7 @@ void pico_init(void) { (void)pkh_init(); }
 void pico_shutdown(void) {
     if(!g_ready) return;
     hipStreamSynchronize(g_own_stream);
-    if(g_ws) hipFree(g_ws);
+    if(g_ws) pkh_device_free(g_ws);
     g_ws = NULL;
     g_ws_bytes = 0;
     hipStreamDestroy(g_own_stream);
@@ -95,20 +95,33 @@ int pico_gpu_synchronize(void) { return pkh_sync(); }
 const char* pico_gpu_last_error(void) { return g_err; }
 void pico_gpu_clear_error(void) { g_err[0] = 0; }
 
+static size_t g_dev_bytes = 0, g_dev_peak = 0;
+
 void* pkh_device_alloc(size_t bytes) {
     if(pkh_init()) return NULL;
     void* p = NULL;
-    hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
+    if(!bytes) bytes = 256;
+    hipError_t e = hipMalloc(&p, bytes);
     if(e != hipSuccess) {
         pkh_set_error("device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
         PKH_ERR("%s\n", g_err);
         return NULL;
     }
+    g_dev_bytes += bytes;
+    if(g_dev_bytes > g_dev_peak) g_dev_peak = g_dev_bytes;
     return p;
 }
 
 void pkh_device_free(void* p) {
-    if(p) hipFree(p);
+    if(!p) return;
+    size_t sz = 0;
+    if(hipMemPtrGetInfo(p, &sz) == hipSuccess) g_dev_bytes -= sz < g_dev_bytes ? sz : g_dev_bytes;
+    hipFree(p);
+}
+
+void pico_gpu_memory(size_t* in_use, size_t* peak) {
+    if(in_use) *in_use = g_dev_bytes;
+    if(peak) *peak = g_dev_peak;
 }
 
 void* pkh_workspace(size_t bytes) {
@@ -116,7 +129,7 @@ void* pkh_workspace(size_t bytes) {
     /* grow: wait for work that may still read the old buffer */
     if(g_ws) {
         hipStreamSynchronize((hipStream_t)pkh_stream());
-        hipFree(g_ws);
+        pkh_device_free(g_ws);
         g_ws = NULL;
         g_ws_bytes = 0;
     }

@@ -106,6 +106,7 @@ _GPU_SIGS = {
     "pico_gpu_synchronize": (ctypes.c_int, []),
     "pico_gpu_last_error": (ctypes.c_char_p, []),
     "pico_gpu_clear_error": (None, []),
+    "pico_gpu_memory": (None, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "pico_randn": (TP, [c_p, ctypes.POINTER(c_i64), ctypes.c_uint8]),
     "pico_gpt_init": (c_p, [ctypes.POINTER(PicoGPTConfig), ctypes.c_uint64]),
     "pico_gpt_loss": (TP, [c_p, c_p, c_p]),
@@ -263,6 +264,12 @@ class Pico:
         a = np.ascontiguousarray(arr, dtype=np.int32)
         self._keep.append(a)
         return a.ctypes.data_as(c_p)
+
+    def memory(self):
+        """(bytes of device memory the library holds, its peak)"""
+        a, b = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        self.lib.pico_gpu_memory(ctypes.byref(a), ctypes.byref(b))
+        return a.value, b.value
 
     def sync(self):
         if self.device:
