@@ -5,22 +5,37 @@
 // src/autograd.h:96-130), plus a two-level batch and the causal tile/k-range
 // restrictions attention uses.
 //
-// Design (one 256-thread workgroup per 128x128 C tile):
-//  * 4 waves in a 2x2 grid, each wave owns a 64x64 sub-tile = 2x2 blocks of
-//    v_mfma_f32_32x32x2f32 (4096 FLOP per instruction, 16 fp32 accumulators
-//    per lane per block).
-//  * K advances 32 at a time through LDS, double-buffered: the next slice is
-//    fetched into registers with 128-bit global loads while the current slice
-//    feeds the MFMAs, then written to the other LDS buffer; one barrier per slice.
+// Design (one 256-thread workgroup = 4 waves per C tile):
+//  * Three tile shapes built from v_mfma_f32_32x32x2f32 blocks (4096 FLOP per
+//    instruction, 16 fp32 accumulators per lane per block):
+//      256x256  2x2 waves of 128x128 (4x4 blocks, 256 accumulators held in
+//               AGPRs), one workgroup per CU -- large products;
+//      128x128  2x2 waves of 64x64, two workgroups per CU;
+//      128x96   4x1 waves of 32x96, two per CU -- N a multiple of 96, where
+//               it fills the resident slots better (d_model 768).
+//  * K advances 32 at a time through a double-buffered LDS ring.  A 32-wide
+//    slice is consumed as four k-groups of 4; the fragments of group q+1 are
+//    read from LDS while the MFMAs of group q run (two register sets).  The
+//    next slice is staged into the other LDS buffer, and the slice after it
+//    fetched into registers with 128-bit global loads, spread over groups 0-2.
+//    Every memory instruction is interleaved with the MFMAs through
+//    sched_group_barrier, so the wave never issues a long run of loads or
+//    stores while the matrix pipe drains (measured: a block of 16 back-to-back
+//    stores + 16 loads per slice cost 13 % of the MFMA rate).  One barrier per
+//    slice sits before group 3, so group 0 of the next slice is read under
+//    group 3's MFMAs.
 //  * LDS keeps each operand in its global orientation (no transposes on the
-//    store).  Within a 32-wide k slice, lanes 0-31 take k 0..15 and lanes 32-63
-//    take k 16..31, so a k-contiguous tile is read with 128-bit LDS loads and a
-//    row-contiguous tile with conflict-free 32-bit loads.  Row strides are
-//    padded by 4 floats.
+//    store).  Within a 32-wide k slice, lanes 0-31 take k 0..15 and lanes
+//    32-63 take k 16..31, so a k-contiguous tile is read with 128-bit LDS loads
+//    and a row-contiguous tile with conflict-free 32-bit loads.  Row strides
+//    are padded by 4 floats.
 //  * Tile order is XCD-aware: the hardware deals consecutive workgroups to
 //    the 8 XCDs round-robin, so the launch index is remapped to give each XCD
 //    a contiguous run of tiles, walked in groups of 8 tile-rows so concurrently
 //    running tiles share A rows and B columns in that XCD's L2.
+//  * Each output element accumulates k in the same order (k, then k+16 within
+//    each pair of a slice) for every tile shape, so the shape choice never
+//    changes a result bit.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -28,12 +43,12 @@
 
 namespace {
 
-constexpr int BM = 128, BK = 32, NT = 256;
+constexpr int BK = 32, NT = 256;
 constexpr int KF = BK + 4;  // row stride of a k-contiguous LDS tile [rows][36]
 constexpr int GROUP_M = 8;
 
-// An R x BK operand slice (R = 128 or 96 rows): float4 per thread, the row
-// stride of its row-contiguous LDS form [BK][R+4], and the LDS floats it needs.
+// An R x BK operand slice: float4 per thread, the row stride of its
+// row-contiguous LDS form [BK][R+4], and the LDS floats it needs.
 template <int R>
 struct Slice {
     static constexpr int V = R * BK / 4 / NT;
@@ -41,6 +56,17 @@ struct Slice {
     static constexpr int RF = R + 4;
     static constexpr int FLOATS = R * KF > BK * RF ? R * KF : BK * RF;
 };
+
+// A tile shape: WGM x (4 / WGM) waves, each TM x TN blocks of 32 x 32.
+template <int BM_, int BN_, int WGM_, int TM_, int TN_, int OCC_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = 4 / WGM_, TM = TM_, TN = TN_;
+    static constexpr int OCC = OCC_;  // resident workgroups per CU
+    static_assert(WGM * TM * 32 == BM && WGN * TN * 32 == BN, "tile does not tile");
+};
+using Tile256 = Tile<256, 256, 2, 4, 4, 1>;
+using Tile128 = Tile<128, 128, 2, 2, 2, 2>;
+using Tile96 = Tile<128, 96, 4, 1, 3, 2>;
 
 struct GemmParams {
     const float* A;
@@ -56,94 +82,138 @@ struct GemmParams {
     float* ws;
 };
 
-// One R x 32 operand slice -> Slice<R>::V float4 per thread.  KFAST: element
-// (r,k) at base[r*ld + k]; otherwise at base[k*ld + r].  EDGE zero-fills
-// outside [Rlim) x [K).
+// Element i (0 <= i < Slice<R>::V) of this thread's share of an R x 32 operand
+// slice.  KFAST: element (r,k) at base[r*ld + k]; otherwise at base[k*ld + r].
+// EDGE zero-fills outside [Rlim) x [K).
 template <bool KFAST, bool EDGE, int R>
-__device__ __forceinline__ void load_slice(const float* __restrict__ base, int64_t ld, int64_t r0,
-                                           int64_t k0, int64_t Rlim, int64_t K,
-                                           f32x4 (&v)[Slice<R>::V]) {
-#pragma unroll
-    for(int i = 0; i < Slice<R>::V; ++i) {
-        const int idx = threadIdx.x + i * NT;
-        int rr, kk;
-        if(KFAST) {
-            rr = idx >> 3;
-            kk = (idx & 7) * 4;
-        } else {
-            kk = idx / Slice<R>::Q4;
-            rr = (idx % Slice<R>::Q4) * 4;
-        }
-        const int64_t r = r0 + rr, k = k0 + kk;
-        if(!EDGE) {
-            const float* p = KFAST ? base + r * ld + k : base + k * ld + r;
-            v[i] = *reinterpret_cast<const f32x4*>(p);
-        } else {
-            f32x4 x = {0.f, 0.f, 0.f, 0.f};
-            if(KFAST) {
-                if(r < Rlim) {
-                    const float* p = base + r * ld;
-#pragma unroll
-                    for(int e = 0; e < 4; ++e)
-                        if(k + e < K) x[e] = p[k + e];
-                }
-            } else {
-                if(k < K) {
-                    const float* p = base + k * ld;
-#pragma unroll
-                    for(int e = 0; e < 4; ++e)
-                        if(r + e < Rlim) x[e] = p[r + e];
-                }
-            }
-            v[i] = x;
-        }
-    }
-}
-
-template <bool KFAST, int R>
-__device__ __forceinline__ void store_slice(float* lds, const f32x4 (&v)[Slice<R>::V]) {
-#pragma unroll
-    for(int i = 0; i < Slice<R>::V; ++i) {
-        const int idx = threadIdx.x + i * NT;
-        if(KFAST)
-            *reinterpret_cast<f32x4*>(lds + (idx >> 3) * KF + (idx & 7) * 4) = v[i];
-        else
-            *reinterpret_cast<f32x4*>(lds + (idx / Slice<R>::Q4) * Slice<R>::RF +
-                                      (idx % Slice<R>::Q4) * 4) = v[i];
-    }
-}
-
-// 16 k-values of LDS row r for this lane's k half
-template <bool KFAST, int R>
-__device__ __forceinline__ void read_frag(const float* lds, int r, int h, float (&f)[16]) {
+__device__ __forceinline__ f32x4 load_one(const float* __restrict__ base, int64_t ld, int64_t r0,
+                                          int64_t k0, int64_t Rlim, int64_t K, int i) {
+    const int idx = threadIdx.x + i * NT;
+    int rr, kk;
     if(KFAST) {
-        const f32x4* p = reinterpret_cast<const f32x4*>(lds + r * KF + h * 16);
+        rr = idx >> 3;
+        kk = (idx & 7) * 4;
+    } else {
+        kk = idx / Slice<R>::Q4;
+        rr = (idx % Slice<R>::Q4) * 4;
+    }
+    const int64_t r = r0 + rr, k = k0 + kk;
+    if(!EDGE) {
+        const float* p = KFAST ? base + r * ld + k : base + k * ld + r;
+        return *reinterpret_cast<const f32x4*>(p);
+    }
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if(KFAST) {
+        if(r < Rlim) {
+            const float* p = base + r * ld;
 #pragma unroll
-        for(int q = 0; q < 4; ++q) {
-            f32x4 x = p[q];
-            f[4 * q + 0] = x[0];
-            f[4 * q + 1] = x[1];
-            f[4 * q + 2] = x[2];
-            f[4 * q + 3] = x[3];
+            for(int e = 0; e < 4; ++e)
+                if(k + e < K) x[e] = p[k + e];
         }
     } else {
+        if(k < K) {
+            const float* p = base + k * ld;
 #pragma unroll
-        for(int s = 0; s < 16; ++s) f[s] = lds[(h * 16 + s) * Slice<R>::RF + r];
+            for(int e = 0; e < 4; ++e)
+                if(r + e < Rlim) x[e] = p[r + e];
+        }
+    }
+    return x;
+}
+
+template <bool KFAST, int R>
+__device__ __forceinline__ void store_one(float* lds, int i, f32x4 v) {
+    const int idx = threadIdx.x + i * NT;
+    if(KFAST)
+        *reinterpret_cast<f32x4*>(lds + (idx >> 3) * KF + (idx & 7) * 4) = v;
+    else
+        *reinterpret_cast<f32x4*>(lds + (idx / Slice<R>::Q4) * Slice<R>::RF +
+                                  (idx % Slice<R>::Q4) * 4) = v;
+}
+
+// k-group q (k = 4q..4q+3 for lanes 0-31, 16+4q.. for lanes 32-63) of the
+// fragments of NB blocks starting at LDS row r0 (one row per lane).
+template <bool KFAST, int R, int NB>
+__device__ __forceinline__ void read_group(const float* lds, int r0, int lr, int lh, int q,
+                                           float (&f)[NB][4]) {
+#pragma unroll
+    for(int b = 0; b < NB; ++b) {
+        const int r = r0 + b * 32 + lr;
+        if(KFAST) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(lds + r * KF + lh * 16 + 4 * q);
+            f[b][0] = x[0];
+            f[b][1] = x[1];
+            f[b][2] = x[2];
+            f[b][3] = x[3];
+        } else {
+#pragma unroll
+            for(int t = 0; t < 4; ++t) f[b][t] = lds[(lh * 16 + 4 * q + t) * Slice<R>::RF + r];
+        }
     }
 }
 
-// Wave layout of a BM x BN tile: BN = 128 -> 2 x 2 waves, each 64 x 64 = 2 x 2
-// blocks of 32 x 32; BN = 96 -> 4 x 1 waves, each 32 x 96 = 1 x 3 blocks.
-template <int BN>
-struct WaveGrid {
-    static constexpr int TN = BN == 128 ? 2 : 3;  // 32x32 blocks per wave along N
-    static constexpr int TM = BN == 128 ? 2 : 1;  // along M
-    static constexpr int WN = BN / (32 * TN);     // waves along N
-};
+template <int TM, int TN>
+__device__ __forceinline__ void mfma_group(f32x16 (&acc)[TM][TN], const float (&fa)[TM][4],
+                                           const float (&fb)[TN][4]) {
+#pragma unroll
+    for(int t = 0; t < 4; ++t)
+#pragma unroll
+        for(int i = 0; i < TM; ++i)
+#pragma unroll
+            for(int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][t], fb[j][t], acc[i][j], 0,
+                                                                 0, 0);
+}
 
-template <bool TA, bool TB, bool EDGE, int BN>
-__global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
-    constexpr int TM = WaveGrid<BN>::TM, TN = WaveGrid<BN>::TN, WN = WaveGrid<BN>::WN;
+// Scheduling hints for one k-group: NMEM memory instructions (LDS or global)
+// spread evenly after the group's NMFMA matrix instructions.
+constexpr int kMaskMfma = 0x008, kMaskMem = 0x090;  // MFMA; all VMEM | all DS
+
+template <int NMFMA, int NMEM, int I = 0>
+__device__ __forceinline__ void interleave() {
+    if constexpr(I < NMFMA) {
+        constexpr int m = (I + 1) * NMEM / NMFMA - I * NMEM / NMFMA;
+        __builtin_amdgcn_sched_group_barrier(kMaskMfma, 1, 0);
+        if constexpr(m > 0) __builtin_amdgcn_sched_group_barrier(kMaskMem, m, 0);
+        interleave<NMFMA, NMEM, I + 1>();
+    }
+}
+
+// Staging of the next operand slice, spread over k-groups 0..2: group g moves
+// elements [lo(g), lo(g+1)) of the VA + VB float4 this thread holds (A's
+// first) from registers to LDS, then refetches them from k0.
+template <int TOT>
+constexpr int stage_lo(int g) {
+    return g >= 3 ? TOT : (g * TOT + 2) / 3;
+}
+
+template <bool AK, bool BKF, bool EDGE, class T, int G>
+__device__ __forceinline__ void stage(f32x4 (&ra)[Slice<T::BM>::V], f32x4 (&rb)[Slice<T::BN>::V],
+                                      float* sa, float* sb, const float* __restrict__ A,
+                                      const float* __restrict__ B, const GemmParams& p,
+                                      int64_t row0, int64_t col0, int64_t kn, int64_t kend) {
+    constexpr int VA = Slice<T::BM>::V, VB = Slice<T::BN>::V, TOT = VA + VB;
+    constexpr int lo = stage_lo<TOT>(G), hi = stage_lo<TOT>(G + 1);
+#pragma unroll
+    for(int e = lo; e < hi; ++e) {
+        if(e < VA)
+            store_one<AK, T::BM>(sa, e, ra[e]);
+        else
+            store_one<BKF, T::BN>(sb, e - VA, rb[e - VA]);
+    }
+#pragma unroll
+    for(int e = lo; e < hi; ++e) {
+        if(e < VA)
+            ra[e] = load_one<AK, EDGE, T::BM>(A, p.lda, row0, kn, p.M, kend, e);
+        else
+            rb[e - VA] = load_one<BKF, EDGE, T::BN>(B, p.ldb, col0, kn, p.N, kend, e - VA);
+    }
+}
+
+template <bool TA, bool TB, bool EDGE, class T>
+__global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
+    constexpr int VA = Slice<BM>::V, VB = Slice<BN>::V, TOT = VA + VB;
     __shared__ __attribute__((aligned(16))) float ldsA[2][Slice<BM>::FLOATS];
     __shared__ __attribute__((aligned(16))) float ldsB[2][Slice<BN>::FLOATS];
 
@@ -184,8 +254,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     const int nslices = (int)((kend - kbeg + BK - 1) / BK);
 
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-    const int wm = w / WN, wn = w % WN;
+    const int wm = w / WGN, wn = w % WGN;
     const int lr = l & 31, lh = l >> 5;
+    const int ar0 = wm * TM * 32, br0 = wn * TN * 32;
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -198,43 +269,75 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
     // (indexed by n) are k-contiguous when B is transposed.
     constexpr bool AK = !TA, BKF = TB;
-    f32x4 ra[Slice<BM>::V], rb[Slice<BN>::V];
-    if(nslices > 0) {
-        load_slice<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, ra);
-        load_slice<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, rb);
-        store_slice<AK, BM>(ldsA[0], ra);
-        store_slice<BKF, BN>(ldsB[0], rb);
-    }
-    __syncthreads();
+    // LDS reads per k-group: one 128-bit load per k-contiguous block, two
+    // paired 32-bit loads per row-contiguous block
+    constexpr int RD = (AK ? TM : 2 * TM) + (BKF ? TN : 2 * TN);
+    constexpr int NMFMA = TM * TN * 4;
 
-    for(int s = 0; s < nslices; ++s) {
-        const int cur = s & 1;
-        const bool more = s + 1 < nslices;
-        if(more) {
-            const int64_t k0 = kbeg + (int64_t)(s + 1) * BK;
-            load_slice<AK, EDGE, BM>(A, p.lda, row0, k0, p.M, kend, ra);
-            load_slice<BKF, EDGE, BN>(B, p.ldb, col0, k0, p.N, kend, rb);
-        }
-        float fa[TM][16], fb[TN][16];
+    if(nslices > 0) {
+        f32x4 ra[VA], rb[VB];
+        // prologue: slice 0 into LDS buffer 0, slice 1 into registers
 #pragma unroll
-        for(int i = 0; i < TM; ++i)
-            read_frag<AK, BM>(ldsA[cur], wm * TM * 32 + i * 32 + lr, lh, fa[i]);
+        for(int e = 0; e < VA; ++e) ra[e] = load_one<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, e);
 #pragma unroll
-        for(int j = 0; j < TN; ++j)
-            read_frag<BKF, BN>(ldsB[cur], wn * TN * 32 + j * 32 + lr, lh, fb[j]);
+        for(int e = 0; e < VB; ++e) rb[e] = load_one<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, e);
 #pragma unroll
-        for(int kk = 0; kk < 16; ++kk)
+        for(int e = 0; e < VA; ++e) store_one<AK, BM>(ldsA[0], e, ra[e]);
 #pragma unroll
-            for(int i = 0; i < TM; ++i)
+        for(int e = 0; e < VB; ++e) store_one<BKF, BN>(ldsB[0], e, rb[e]);
+        {
+            const int64_t k1 = kbeg + (nslices > 1 ? BK : 0);
 #pragma unroll
-                for(int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][kk], fb[j][kk],
-                                                                     acc[i][j], 0, 0, 0);
-        if(more) {
-            store_slice<AK, BM>(ldsA[cur ^ 1], ra);
-            store_slice<BKF, BN>(ldsB[cur ^ 1], rb);
+            for(int e = 0; e < VA; ++e) ra[e] = load_one<AK, EDGE, BM>(A, p.lda, row0, k1, p.M, kend, e);
+#pragma unroll
+            for(int e = 0; e < VB; ++e) rb[e] = load_one<BKF, EDGE, BN>(B, p.ldb, col0, k1, p.N, kend, e);
         }
         __syncthreads();
+
+        float fa0[TM][4], fb0[TN][4], fa1[TM][4], fb1[TN][4];
+        read_group<AK, BM, TM>(ldsA[0], ar0, lr, lh, 0, fa0);
+        read_group<BKF, BN, TN>(ldsB[0], br0, lr, lh, 0, fb0);
+        for(int s = 0; s < nslices; ++s) {
+            const int cur = s & 1;
+            const float* la = ldsA[cur];
+            const float* lb = ldsB[cur];
+            float* sa = ldsA[cur ^ 1];
+            float* sb = ldsB[cur ^ 1];
+            // the slice the staging registers fetch next; past the end it
+            // re-fetches the last slice, which keeps the loop free of branches
+            const int64_t kn = kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
+
+            // group 0: read group 1, stage part 0
+            read_group<AK, BM, TM>(la, ar0, lr, lh, 1, fa1);
+            read_group<BKF, BN, TN>(lb, br0, lr, lh, 1, fb1);
+            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            mfma_group<TM, TN>(acc, fa0, fb0);
+            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(1) - stage_lo<TOT>(0))>();
+            __builtin_amdgcn_sched_barrier(0);
+            // group 1: read group 2, stage part 1
+            read_group<AK, BM, TM>(la, ar0, lr, lh, 2, fa0);
+            read_group<BKF, BN, TN>(lb, br0, lr, lh, 2, fb0);
+            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            mfma_group<TM, TN>(acc, fa1, fb1);
+            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(2) - stage_lo<TOT>(1))>();
+            __builtin_amdgcn_sched_barrier(0);
+            // group 2: read group 3, stage part 2
+            read_group<AK, BM, TM>(la, ar0, lr, lh, 3, fa1);
+            read_group<BKF, BN, TN>(lb, br0, lr, lh, 3, fb1);
+            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            mfma_group<TM, TN>(acc, fa0, fb0);
+            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(3) - stage_lo<TOT>(2))>();
+            __builtin_amdgcn_sched_barrier(0);
+            // every wave has staged slice s+1 and finished reading slice s
+            __syncthreads();
+            // group 3, with group 0 of slice s+1 read underneath (on the last
+            // slice this reads the re-staged data and is discarded)
+            read_group<AK, BM, TM>(sa, ar0, lr, lh, 0, fa0);
+            read_group<BKF, BN, TN>(sb, br0, lr, lh, 0, fb0);
+            mfma_group<TM, TN>(acc, fa1, fb1);
+            interleave<NMFMA, RD>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
     // ---- epilogue: 32x32 block accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
@@ -243,10 +346,10 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_kernel(GemmParams p) {
     for(int i = 0; i < TM; ++i)
 #pragma unroll
         for(int j = 0; j < TN; ++j) {
-            const int64_t col = col0 + wn * TN * 32 + j * 32 + lr;
+            const int64_t col = col0 + br0 + j * 32 + lr;
 #pragma unroll
             for(int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + wm * TM * 32 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                const int64_t row = row0 + ar0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
                 if(EDGE && (row >= p.M || col >= p.N)) continue;
                 float v = alpha * acc[i][j][r];
                 float* c = C + row * ldc + col;
@@ -290,7 +393,7 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
 constexpr int64_t kSplitTarget = 512, kMinSliceK = 256;
 
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
-    const int64_t tiles = ((M + BM - 1) / BM) * ((N + 127) / 128);
+    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
     *kchunk = K;
     if(tiles <= 0 || tiles * 2 > kSplitTarget || K < 4 * kMinSliceK) return 1;
     int64_t s = kSplitTarget / tiles;
@@ -301,38 +404,54 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     return (int)((K + chunk - 1) / chunk);
 }
 
-// Tile width: 96-wide tiles when N is a multiple of 96 and they fill the 512
-// resident workgroup slots (2 per CU) clearly better than 128-wide ones.  An
-// [8192, 768] output, every projection of a d_model-768 transformer, makes 384
-// 128-wide tiles (75 % of the slots busy) but 512 96-wide ones.
-constexpr int64_t kSlots = 512;
+// Tile shape: the estimated time of a shape is its number of rounds over the
+// chip's resident slots times the work of one round per CU.  256 CUs hold 256
+// workgroups of 256x256 (work 4 per CU per round, in 128x128 units), 512 of
+// 128x128 (work 2) or 512 of 128x96 (work 1.5).  The 256x256 shape runs its
+// MFMAs about 5 % more efficiently, so it wins ties.  Examples: 4096^2 -> 256
+// tiles of 256x256 (one round); an [8192, 768] output (every projection of a
+// d_model-768 transformer) -> 512 tiles of 128x96 (one round) instead of 384
+// of 128x128 or 96 of 256x256.
+enum TileKind { kTile128 = 0, kTile96 = 1, kTile256 = 2 };
+constexpr int64_t kCUs = 256;
 
-double slot_fill(int64_t tiles) {
-    const int64_t rounds = (tiles + kSlots - 1) / kSlots;
-    return rounds ? (double)tiles / (double)(rounds * kSlots) : 0.0;
+TileKind pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_big) {
+    auto rounds = [](int64_t tiles, int64_t slots) { return (tiles + slots - 1) / slots; };
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    double best = 2.0 * (double)rounds(t128, 2 * kCUs);
+    TileKind kind = kTile128;
+    if(N % 96 == 0) {
+        const double c96 = 1.5 * (double)rounds(((M + 127) / 128) * (N / 96) * batch, 2 * kCUs);
+        if(c96 < best) {
+            best = c96;
+            kind = kTile96;
+        }
+    }
+    if(allow_big) {
+        const double c256 =
+            4.0 * (double)rounds(((M + 255) / 256) * ((N + 255) / 256) * batch, kCUs) / 1.05;
+        if(c256 <= best) kind = kTile256;
+    }
+    return kind;
 }
 
-int pick_bn(int64_t M, int64_t N, int64_t batch) {
-    if(N % 96) return 128;
-    const int64_t tm = (M + BM - 1) / BM;
-    const int64_t t128 = tm * ((N + 127) / 128) * batch, t96 = tm * (N / 96) * batch;
-    return slot_fill(t96) > slot_fill(t128) + 0.1 ? 96 : 128;
-}
-
-template <bool TA, bool TB, int BN>
-int launch_bn(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
+template <bool TA, bool TB, class T>
+int launch_tile(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
     dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)(gp.splits > 1 ? gp.splits : batch));
     if(edge)
-        gemm_f32_kernel<TA, TB, true, BN><<<grid, NT, 0, st>>>(gp);
+        gemm_f32_kernel<TA, TB, true, T><<<grid, NT, 0, st>>>(gp);
     else
-        gemm_f32_kernel<TA, TB, false, BN><<<grid, NT, 0, st>>>(gp);
+        gemm_f32_kernel<TA, TB, false, T><<<grid, NT, 0, st>>>(gp);
     return pk::launch_status("pk_gemm_f32");
 }
 
 template <bool TA, bool TB>
-int launch(const GemmParams& gp, int64_t batch, bool edge, int bn, hipStream_t st) {
-    return bn == 96 ? launch_bn<TA, TB, 96>(gp, batch, edge, st)
-                    : launch_bn<TA, TB, 128>(gp, batch, edge, st);
+int launch(const GemmParams& gp, int64_t batch, bool edge, TileKind kind, hipStream_t st) {
+    switch(kind) {
+    case kTile256: return launch_tile<TA, TB, Tile256>(gp, batch, edge, st);
+    case kTile96: return launch_tile<TA, TB, Tile96>(gp, batch, edge, st);
+    default: return launch_tile<TA, TB, Tile128>(gp, batch, edge, st);
+    }
 }
 
 int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
@@ -392,25 +511,31 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
             gp.ws = ws;
         }
     }
-    const int bn = gp.splits > 1 ? 128 : pick_bn(M, N, batch);
-    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + bn - 1) / bn;
+    // split products keep 128x128 tiles (the split count is sized for them);
+    // causal products keep 128-row tiles (the attention chain's diagonal logic
+    // is exercised at that size)
+    const TileKind kind =
+        gp.splits > 1 ? kTile128 : pick_tile(M, N, batch, causal == 0);
+    const int bm = kind == kTile256 ? 256 : 128;
+    const int bn = kind == kTile256 ? 256 : kind == kTile96 ? 96 : 128;
+    const int64_t tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
     if(tiles_m * tiles_n > (int64_t)1 << 30)
         return pk::fail("pk_gemm_f32: problem too large for one launch");
     gp.tiles_m = (int)tiles_m;
     gp.tiles_n = (int)tiles_n;
     // the unchecked path needs whole tiles and 16-byte aligned float4 loads
-    const bool edge = (M % BM) || (N % bn) || (K % BK) || (lda % 4) || (ldb % 4) ||
+    const bool edge = (M % bm) || (N % bn) || (K % BK) || (lda % 4) || (ldb % 4) ||
                       (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
                       !pk::aligned16(A) || !pk::aligned16(B);
     int rc;
     if(!TA && !TB)
-        rc = launch<false, false>(gp, batch, edge, bn, st);
+        rc = launch<false, false>(gp, batch, edge, kind, st);
     else if(!TA && TB)
-        rc = launch<false, true>(gp, batch, edge, bn, st);
+        rc = launch<false, true>(gp, batch, edge, kind, st);
     else if(TA && !TB)
-        rc = launch<true, false>(gp, batch, edge, bn, st);
+        rc = launch<true, false>(gp, batch, edge, kind, st);
     else
-        rc = launch<true, true>(gp, batch, edge, bn, st);
+        rc = launch<true, true>(gp, batch, edge, kind, st);
     if(rc || gp.splits == 1) return rc;
     splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(M, N, gp.splits, gp.ws, alpha,
                                                                   beta, C, ldc);

@@ -456,3 +456,20 @@ def test_gemm_96_wide_tiles(dev, ta, tb, M, N, Kd):
     C = cu(C0.copy())
     K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=2.0, beta=1.0)
     assert gemm_err(host(C) - C0, 2.0 * A, B) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(4096, 4096, 256), (4000, 4000, 200), (4096, 8192, 96),
+                                    (4352, 3840, 1)])
+def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
+    # outputs of >= 256 tiles of 256 x 256 take the one-workgroup-per-CU shape;
+    # 4000 and Kd = 200 / 1 exercise its edge path
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 5 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    C0 = ref.copy()
+    C = cu(C0)
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)  # C - A.B = 0 exactly
+    assert not np.any(host(C))
