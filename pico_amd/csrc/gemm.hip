@@ -6,13 +6,18 @@
 // restrictions attention uses.
 //
 // Design (one 256-thread workgroup = 4 waves per C tile):
-//  * Three tile shapes built from v_mfma_f32_32x32x2f32 blocks (4096 FLOP per
-//    instruction, 16 fp32 accumulators per lane per block):
+//  * Four tile shapes built from v_mfma_f32_32x32x2f32 blocks (4096 FLOP per
+//    instruction, 16 fp32 accumulators per lane per block), chosen per call by
+//    how evenly they spread over the 256 CUs:
 //      256x256  2x2 waves of 128x128 (4x4 blocks, 256 accumulators held in
 //               AGPRs), one workgroup per CU -- large products;
 //      128x128  2x2 waves of 64x64, two workgroups per CU;
-//      128x96   4x1 waves of 32x96, two per CU -- N a multiple of 96, where
-//               it fills the resident slots better (d_model 768).
+//      128x96   4x1 waves of 32x96, two per CU -- N a multiple of 96 (an
+//               [8192, 768] output, d_model 768, is 512 of them);
+//      64x64    2x2 waves of 32x32, four per CU -- small products.
+//  * Tiles on the edge of C are handled in the same kernel: with M, N, K and
+//    the strides multiples of 4 each 128-bit load is predicated as a whole;
+//    otherwise loads fall back to 32-bit elements.
 //  * K advances 32 at a time through a double-buffered LDS ring.  A 32-wide
 //    slice is consumed as four k-groups of 4; the fragments of group q+1 are
 //    read from LDS while the MFMAs of group q run (two register sets).  The
@@ -67,6 +72,7 @@ struct Tile {
 using Tile256 = Tile<256, 256, 2, 4, 4, 1>;
 using Tile128 = Tile<128, 128, 2, 2, 2, 2>;
 using Tile96 = Tile<128, 96, 4, 1, 3, 2>;
+using Tile64 = Tile<64, 64, 2, 1, 1, 4>;
 
 struct GemmParams {
     const float* A;
@@ -82,10 +88,15 @@ struct GemmParams {
     float* ws;
 };
 
+// Bounds handling of a tile's loads and stores: none (whole tiles), per float4
+// (M, N, K, the leading dimensions and batch strides multiples of 4, 16-byte
+// aligned operands: a float4 is wholly inside or wholly outside), or per element.
+constexpr int kEdgeNone = 0, kEdgeVec = 1, kEdgeScalar = 2;
+
 // Element i (0 <= i < Slice<R>::V) of this thread's share of an R x 32 operand
 // slice.  KFAST: element (r,k) at base[r*ld + k]; otherwise at base[k*ld + r].
-// EDGE zero-fills outside [Rlim) x [K).
-template <bool KFAST, bool EDGE, int R>
+// Edge modes zero-fill outside [Rlim) x [K).
+template <bool KFAST, int EDGE, int R>
 __device__ __forceinline__ f32x4 load_one(const float* __restrict__ base, int64_t ld, int64_t r0,
                                           int64_t k0, int64_t Rlim, int64_t K, int i) {
     const int idx = threadIdx.x + i * NT;
@@ -98,11 +109,16 @@ __device__ __forceinline__ f32x4 load_one(const float* __restrict__ base, int64_
         rr = (idx % Slice<R>::Q4) * 4;
     }
     const int64_t r = r0 + rr, k = k0 + kk;
-    if(!EDGE) {
+    if(EDGE == kEdgeNone) {
         const float* p = KFAST ? base + r * ld + k : base + k * ld + r;
         return *reinterpret_cast<const f32x4*>(p);
     }
     f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if(EDGE == kEdgeVec) {
+        if(r < Rlim && k < K)
+            x = *reinterpret_cast<const f32x4*>(KFAST ? base + r * ld + k : base + k * ld + r);
+        return x;
+    }
     if(KFAST) {
         if(r < Rlim) {
             const float* p = base + r * ld;
@@ -187,7 +203,7 @@ constexpr int stage_lo(int g) {
     return g >= 3 ? TOT : (g * TOT + 2) / 3;
 }
 
-template <bool AK, bool BKF, bool EDGE, class T, int G>
+template <bool AK, bool BKF, int EDGE, class T, int G>
 __device__ __forceinline__ void stage(f32x4 (&ra)[Slice<T::BM>::V], f32x4 (&rb)[Slice<T::BN>::V],
                                       float* sa, float* sb, const float* __restrict__ A,
                                       const float* __restrict__ B, const GemmParams& p,
@@ -210,7 +226,7 @@ __device__ __forceinline__ void stage(f32x4 (&ra)[Slice<T::BM>::V], f32x4 (&rb)[
     }
 }
 
-template <bool TA, bool TB, bool EDGE, class T>
+template <bool TA, bool TB, int EDGE, class T>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
     constexpr int VA = Slice<BM>::V, VB = Slice<BN>::V, TOT = VA + VB;
@@ -350,7 +366,7 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
 #pragma unroll
             for(int r = 0; r < 16; ++r) {
                 const int64_t row = row0 + ar0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                if(EDGE && (row >= p.M || col >= p.N)) continue;
+                if(EDGE != kEdgeNone && (row >= p.M || col >= p.N)) continue;
                 float v = alpha * acc[i][j][r];
                 float* c = C + row * ldc + col;
                 if(beta != 0.0f) v += beta * *c;
@@ -404,52 +420,63 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     return (int)((K + chunk - 1) / chunk);
 }
 
-// Tile shape: the estimated time of a shape is its number of rounds over the
-// chip's resident slots times the work of one round per CU.  256 CUs hold 256
-// workgroups of 256x256 (work 4 per CU per round, in 128x128 units), 512 of
-// 128x128 (work 2) or 512 of 128x96 (work 1.5).  The 256x256 shape runs its
-// MFMAs about 5 % more efficiently, so it wins ties.  Examples: 4096^2 -> 256
-// tiles of 256x256 (one round); an [8192, 768] output (every projection of a
-// d_model-768 transformer) -> 512 tiles of 128x96 (one round) instead of 384
-// of 128x128 or 96 of 256x256.
-enum TileKind { kTile128 = 0, kTile96 = 1, kTile256 = 2 };
+// Tile shape: the estimated time of a shape is the work of the busiest CU --
+// its share of the tiles, ceil(tiles / 256 CUs), times the work of one tile in
+// units of a 128x128 tile (256x256: 4, 128x96: 0.75, 64x64: 0.25).
+// Workgroups resident on one CU share its matrix pipes, and a CU with no tile
+// adds nothing.  The 256x256 shape (one workgroup per CU) runs its MFMAs
+// about 5 % more efficiently; 64x64 tiles move twice the operand bytes per
+// FLOP of 128x128 ones and are charged 20 % for it.  Examples: 4096^2 -> 256
+// tiles of 256x256; an [8192, 768] output (every projection of a d_model-768
+// transformer) -> 512 of 128x96; 2048^2 -> 256 of 128x128; 1024^2 -> 256 of
+// 64x64 rather than 64 of 128x128.
+enum TileKind { kTile128, kTile96, kTile256, kTile64 };
 constexpr int64_t kCUs = 256;
 
-TileKind pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_big) {
-    auto rounds = [](int64_t tiles, int64_t slots) { return (tiles + slots - 1) / slots; };
-    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
-    double best = 2.0 * (double)rounds(t128, 2 * kCUs);
-    TileKind kind = kTile128;
-    if(N % 96 == 0) {
-        const double c96 = 1.5 * (double)rounds(((M + 127) / 128) * (N / 96) * batch, 2 * kCUs);
-        if(c96 < best) {
-            best = c96;
-            kind = kTile96;
+struct TileChoice {
+    TileKind kind;
+    int bm, bn;
+};
+
+TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
+    auto cost = [&](int bm, int bn, double units) {
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
+        return units * (double)((tiles + kCUs - 1) / kCUs);
+    };
+    TileChoice best = {kTile128, 128, 128};
+    double c = cost(128, 128, 1.0);
+    auto consider = [&](TileKind k, int bm, int bn, double ck) {
+        if(ck < c) {
+            c = ck;
+            best = {k, bm, bn};
         }
+    };
+    if(N % 96 == 0) consider(kTile96, 128, 96, cost(128, 96, 0.75));
+    if(allow_all) {
+        consider(kTile64, 64, 64, cost(64, 64, 0.25) * 1.2);
+        if(cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
     }
-    if(allow_big) {
-        const double c256 =
-            4.0 * (double)rounds(((M + 255) / 256) * ((N + 255) / 256) * batch, kCUs) / 1.05;
-        if(c256 <= best) kind = kTile256;
-    }
-    return kind;
+    return best;
 }
 
 template <bool TA, bool TB, class T>
-int launch_tile(const GemmParams& gp, int64_t batch, bool edge, hipStream_t st) {
+int launch_tile(const GemmParams& gp, int64_t batch, int edge, hipStream_t st) {
     dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)(gp.splits > 1 ? gp.splits : batch));
-    if(edge)
-        gemm_f32_kernel<TA, TB, true, T><<<grid, NT, 0, st>>>(gp);
+    if(edge == kEdgeNone)
+        gemm_f32_kernel<TA, TB, kEdgeNone, T><<<grid, NT, 0, st>>>(gp);
+    else if(edge == kEdgeVec)
+        gemm_f32_kernel<TA, TB, kEdgeVec, T><<<grid, NT, 0, st>>>(gp);
     else
-        gemm_f32_kernel<TA, TB, false, T><<<grid, NT, 0, st>>>(gp);
+        gemm_f32_kernel<TA, TB, kEdgeScalar, T><<<grid, NT, 0, st>>>(gp);
     return pk::launch_status("pk_gemm_f32");
 }
 
 template <bool TA, bool TB>
-int launch(const GemmParams& gp, int64_t batch, bool edge, TileKind kind, hipStream_t st) {
+int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, hipStream_t st) {
     switch(kind) {
     case kTile256: return launch_tile<TA, TB, Tile256>(gp, batch, edge, st);
     case kTile96: return launch_tile<TA, TB, Tile96>(gp, batch, edge, st);
+    case kTile64: return launch_tile<TA, TB, Tile64>(gp, batch, edge, st);
     default: return launch_tile<TA, TB, Tile128>(gp, batch, edge, st);
     }
 }
@@ -514,19 +541,24 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     // split products keep 128x128 tiles (the split count is sized for them);
     // causal products keep 128-row tiles (the attention chain's diagonal logic
     // is exercised at that size)
-    const TileKind kind =
-        gp.splits > 1 ? kTile128 : pick_tile(M, N, batch, causal == 0);
-    const int bm = kind == kTile256 ? 256 : 128;
-    const int bn = kind == kTile256 ? 256 : kind == kTile96 ? 96 : 128;
-    const int64_t tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
+    const TileChoice tc = gp.splits > 1 ? TileChoice{kTile128, 128, 128}
+                                        : pick_tile(M, N, batch, causal == 0);
+    const int64_t tiles_m = (M + tc.bm - 1) / tc.bm, tiles_n = (N + tc.bn - 1) / tc.bn;
     if(tiles_m * tiles_n > (int64_t)1 << 30)
         return pk::fail("pk_gemm_f32: problem too large for one launch");
     gp.tiles_m = (int)tiles_m;
     gp.tiles_n = (int)tiles_n;
-    // the unchecked path needs whole tiles and 16-byte aligned float4 loads
-    const bool edge = (M % bm) || (N % bn) || (K % BK) || (lda % 4) || (ldb % 4) ||
-                      (sA_outer % 4) || (sA_inner % 4) || (sB_outer % 4) || (sB_inner % 4) ||
-                      !pk::aligned16(A) || !pk::aligned16(B);
+    // float4 loads need 16-byte aligned operands and leading dimensions and
+    // batch strides that are multiples of 4; the unchecked path also needs
+    // whole tiles
+    const bool vec = (lda % 4) == 0 && (ldb % 4) == 0 && (sA_outer % 4) == 0 &&
+                     (sA_inner % 4) == 0 && (sB_outer % 4) == 0 && (sB_inner % 4) == 0 &&
+                     pk::aligned16(A) && pk::aligned16(B);
+    const bool whole = (M % tc.bm) == 0 && (N % tc.bn) == 0 && (K % BK) == 0;
+    const int edge = vec && whole ? kEdgeNone
+                     : vec && (M % 4) == 0 && (N % 4) == 0 && (K % 4) == 0 ? kEdgeVec
+                                                                           : kEdgeScalar;
+    const TileKind kind = tc.kind;
     int rc;
     if(!TA && !TB)
         rc = launch<false, false>(gp, batch, edge, kind, st);

@@ -473,3 +473,20 @@ def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
     C = cu(C0)
     K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)  # C - A.B = 0 exactly
     assert not np.any(host(C))
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(4096, 1376, 512), (1000, 1376, 516), (516, 960, 100),
+                                    (8192, 768, 772), (1024, 1024, 1024), (200, 64, 36)])
+def test_gemm_vector_edge_tiles(dev, ta, tb, M, N, Kd):
+    # sizes that are multiples of 4 but not of the tile: partial tiles load
+    # whole float4 under a predicate (d_ff = 1376 in the 1-layer config);
+    # 8192 x 768 takes 128 x 96 tiles, 1024^2 and 200 x 64 the 64 x 64 ones
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 7 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    C = cu(ref.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)
+    assert not np.any(host(C))
