@@ -204,6 +204,109 @@ def train_flop_per_step(cfg):
     return 6.0 * gemm_params * tok + attn
 
 
+def _gpt_step_launches(lib, model, opt, tok, tgt, work):
+    loss = lib.pico_gpt_loss(model, tok, tgt)
+    if not loss:
+        raise RuntimeError("pico_gpt_loss failed")
+    lib.pico_optim_adamw_zero_grad(opt)
+    lib.pico_backward(work, loss)
+    lib.pico_optim_adamw_step(opt)
+    return loss
+
+
+def _graph_replay_ms(P, launch_step, steps):
+    """ms per step of a captured step replayed `steps` times (pico_graph_*);
+    the step has already run eagerly, so its memory exists"""
+    lib = P.lib
+    lib.arena_reset(lib.arena_ctx_current())
+    if lib.pico_graph_begin() != 0:
+        raise RuntimeError(lib.pico_gpu_last_error().decode())
+    launch_step()
+    graph = lib.pico_graph_end()
+    if not graph:
+        raise RuntimeError("graph capture failed: " + lib.pico_gpu_last_error().decode())
+    for _ in range(2):
+        lib.pico_graph_launch(graph)
+    P.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lib.pico_graph_launch(graph)
+    P.sync()
+    wall = time.perf_counter() - t0
+    lib.pico_graph_free(graph)
+    lib.arena_reset(lib.arena_ctx_current())
+    return wall * 1e3 / steps
+
+
+def mlp_section(steps, warmup):
+    """config 1: pico's 784 -> 128 -> 10 ReLU MLP (examples/02_relu_mlp shapes),
+    softmax cross-entropy, SGD lr 0.01, batch 64, inputs resident; eager steps
+    and a captured step replayed"""
+    import ctypes
+
+    import numpy as np
+
+    from oracle import oracle as O
+    from pico_amd.pico import TP, Pico
+
+    P = Pico()
+    lib = P.lib
+    data = lib.arena_init(1 << 20)
+    lib.arena_ctx_push(data)
+    labels = lib.pico_ids_to_device(P.ids(O.labels(64, 20261202, 10)), 64)
+    lib.arena_ctx_pop()
+    work = lib.arena_init(1 << 24)
+    lib.arena_ctx_push(work)
+    fc1 = lib.pico_nn_linear_init(784, 128, True)
+    fc2 = lib.pico_nn_linear_init(128, 10, True)
+    opt = lib.pico_optim_sgd_init(0.01)
+    for fc, (fan, seed) in ((fc1, (784, 3)), (fc2, (128, 4))):
+        w = ctypes.cast(fc + 8, ctypes.POINTER(TP)).contents
+        b = ctypes.cast(fc + 16, ctypes.POINTER(TP)).contents
+        P.set(w, O.uniform(w.contents.numel, 20261200 + seed, -fan ** -0.5, fan ** -0.5))
+        lib.pico_optim_sgd_add(opt, w)
+        lib.pico_optim_sgd_add(opt, b)
+    x = P.param([64, 784], O.normal(64 * 784, 20261201))
+
+    def launch_step():
+        lib.pico_optim_sgd_zero_grad(opt)
+        h = lib.pico_relu(lib.pico_nn_linear_forward(fc1, x))
+        loss = lib.pico_softmax_xent(lib.pico_nn_linear_forward(fc2, h), labels)
+        lib.pico_backward(work, loss)
+        lib.pico_optim_sgd_step(opt)
+        return loss
+
+    losses = []
+    for _ in range(warmup):
+        losses.append(float(P.data(launch_step())[0]))
+        lib.arena_reset(work)
+    P.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        launch_step()
+        lib.arena_reset(work)
+    P.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = _graph_replay_ms(P, launch_step, steps)
+    err = lib.pico_gpu_last_error().decode()
+    lib.arena_ctx_pop()
+    lib.pico_optim_sgd_free(opt)
+    lib.pico_free(x)
+    lib.pico_nn_linear_free(fc1)
+    lib.pico_nn_linear_free(fc2)
+    lib.arena_destroy(work)
+    lib.arena_destroy(data)
+    if err:
+        raise RuntimeError(err)
+    flop = 2 * 64 * (784 * 128 + 128 * 10) * 3
+    return {"samples_per_s": round(64 / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+            "graph_ms_per_step": round(graph_ms, 4),
+            "graph_samples_per_s": round(64 / (graph_ms * 1e-3), 1),
+            "flop_per_step": flop, "steps": steps, "warmup": warmup,
+            "loss_first": round(losses[0], 5), "loss_after_warmup": round(losses[-1], 5),
+            "config": {"model": "MLP 784-128-10 ReLU", "batch": 64, "optimizer": "SGD lr 0.01"}}
+
+
 def train_section(name, steps, warmup):
     """one AdamW training step of the transformer per step, inputs resident"""
     import numpy as np
@@ -251,6 +354,8 @@ def train_section(name, steps, warmup):
     P.sync()
     wall = time.perf_counter() - t0
     step(keep_loss=True)
+    graph_ms = _graph_replay_ms(P, lambda: _gpt_step_launches(lib, model, opt, tok, tgt, work),
+                                steps)
     _, peak_bytes = P.memory()
     err = lib.pico_gpu_last_error().decode()
     lib.arena_ctx_pop()
@@ -265,6 +370,8 @@ def train_section(name, steps, warmup):
     return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
             "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
             "mfu": round(flop / (ms * 1e-3) / MFMA_FP32_PEAK, 4),
+            "graph_ms_per_step": round(graph_ms, 3),
+            "graph_tokens_per_s": round(n / (graph_ms * 1e-3), 1),
             "tokens_per_step": n, "steps": steps, "warmup": warmup,
             "loss_first": round(losses[0], 5), "loss_after": round(losses[-1], 5),
             "device_gib_peak": round(peak_bytes / 2 ** 30, 2),
@@ -317,7 +424,7 @@ def main():
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--sections", default="train,sweep,rows,cpu")
     ap.add_argument("--train-steps", type=int, default=10)
-    ap.add_argument("--train-configs", default=",".join(TRAIN_CONFIGS))
+    ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -367,8 +474,12 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if "train" in sections:
-        line["train"] = {name: train_section(name, args.train_steps, 3)
-                         for name in args.train_configs.split(",") if name}
+        line["train"] = {}
+        for name in args.train_configs.split(","):
+            if name == "config1":
+                line["train"][name] = mlp_section(100, 3)
+            elif name:
+                line["train"][name] = train_section(name, args.train_steps, 3)
     if "sweep" in sections:
         line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
     if "rows" in sections:

@@ -234,6 +234,8 @@ int pico_tensor_grad_to_host(const struct PicoTensor* t, float* dst);
 int pico_tensor_grad_from_host(struct PicoTensor* t, const float* src);
 /* device copy of n int32 values in the current arena (NULL on failure) */
 int32_t* pico_ids_to_device(const int32_t* host_ids, int64_t n);
+/* overwrite n device ids (from pico_ids_to_device) with host values; 0 on success */
+int pico_ids_update(int32_t* device_ids, const int32_t* host_ids, int64_t n);
 
 /* ---- runtime ---- */
 int pico_gpu_synchronize(void);
@@ -244,6 +246,28 @@ const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
  * arena blocks, optimizer moments, scratch) */
 void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
+
+/* ---- device graphs (no reference counterpart) ----
+ * Record the launches of one training step once and replay them with a
+ * single call.  Between pico_graph_begin() and pico_graph_end() every op,
+ * pico_backward and optimizer step is recorded on the library's stream
+ * instead of running.  Nothing may allocate device memory, copy to or from
+ * the host, or wait on the device meanwhile, so:
+ *   - run the step once eagerly first (the arena's device blocks, the GEMM
+ *     workspace and the optimizer's tables then exist, and an arena_reset
+ *     before capturing makes the captured step reuse the same addresses);
+ *   - pass token ids as device pointers (pico_ids_to_device into an arena
+ *     that outlives the graph) and refresh them with pico_ids_update;
+ *   - read results (the loss tensor of the captured step) after
+ *     pico_graph_launch.
+ * A refused call fails the capture: pico_graph_end then returns NULL, with
+ * the reason in pico_gpu_last_error().  A replay repeats the captured work
+ * exactly (same kernels, same arguments, same addresses). */
+struct PicoGraph;
+int pico_graph_begin(void);
+struct PicoGraph* pico_graph_end(void);
+int pico_graph_launch(struct PicoGraph* graph);
+void pico_graph_free(struct PicoGraph* graph);
 
 #ifdef __cplusplus
 }

@@ -132,6 +132,28 @@ int pk_sgd_f32(int64_t n, float lr, float* p, const float* g, pk_stream_t stream
 int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps, float weight_decay,
                  int step, float* p, const float* g, float* m, float* v, pk_stream_t stream);
 
+/* AdamW over many tensors in one launch, with the step count kept on the
+ * device so a captured graph replays correctly (no reference counterpart; the
+ * multi-tensor form of pk_adamw_f32, same arithmetic per element).
+ *   pk_adamw_prep_f32: *step += 1, then coef[0] = lr / (1 - beta1^step) and
+ *     coef[1] = sqrt(1 - beta2^step) (both computed in double, rounded once).
+ *   pk_adamw_multi_f32: chunks is a device array of nchunks descriptors, each
+ *     at most PK_ADAMW_CHUNK elements of one tensor starting 16-byte aligned;
+ *     g == NULL in a descriptor means a zero gradient. */
+#define PK_ADAMW_CHUNK 65536
+typedef struct PkAdamwChunk {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    int64_t n;
+} PkAdamwChunk;
+int pk_adamw_prep_f32(int32_t* step, float lr, float beta1, float beta2, float* coef,
+                      pk_stream_t stream);
+int pk_adamw_multi_f32(int64_t nchunks, const PkAdamwChunk* chunks, float lr, float beta1,
+                       float beta2, float eps, float weight_decay, const float* coef,
+                       pk_stream_t stream);
+
 /* ---- fused row kernels (no reference code; planned at todo.md:95) --------
  * softmax cross-entropy, one pass over each row of logits [R,V] (row stride ldz):
  *   loss_rows[r] = logsumexp(z_r) - z_r[labels[r]]        (if loss_rows != NULL)
@@ -207,12 +229,16 @@ int pk_causal_softmax_bwd_f32(int64_t BH, int64_t T, const float* P, const float
                               pk_stream_t stream);
 
 /* ---- embedding -------------------------------------------------------------
- * out[i,:] = table[ids[i],:]; dtable[ids[i],:] += dout[i,:] (order of the adds
- * is unspecified).  An id outside [0,vocab) reads as a zero row and adds nothing. */
+ * out[i,:] = table[ids[i],:]; dtable[ids[i],:] += dout[i,:], the adds into
+ * one row made in increasing i (the sequential loop's order: deterministic).
+ * An id outside [0,vocab) reads as a zero row and adds nothing.  The backward
+ * needs pk_embed_bwd_workspace(n) bytes of device workspace; it groups equal
+ * ids with O(n^2) compares (microseconds at n ~ 10^4). */
 int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids, const float* table,
                      float* out, pk_stream_t stream);
+size_t pk_embed_bwd_workspace(int64_t n);
 int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids, const float* dout,
-                     float* dtable, pk_stream_t stream);
+                     float* dtable, void* workspace, size_t workspace_bytes, pk_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,8 @@ PK_SIGNATURES = {
     "pk_reduce_sum_f32": [c_i64, c_p, c_f, c_p, c_int, c_p],
     "pk_sgd_f32": [c_i64, c_f, c_p, c_p, c_p],
     "pk_adamw_f32": [c_i64, c_f, c_f, c_f, c_f, c_f, c_int, c_p, c_p, c_p, c_p, c_p],
+    "pk_adamw_prep_f32": [c_p, c_f, c_f, c_f, c_p, c_p],
+    "pk_adamw_multi_f32": [c_i64, c_p, c_f, c_f, c_f, c_f, c_f, c_p, c_p],
     "pk_xent_fwd_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p, c_i64, c_f, c_p, c_int,
                             c_p],
     "pk_argmax_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p],
@@ -73,11 +75,13 @@ PK_SIGNATURES = {
     "pk_causal_softmax_fwd_f32": [c_i64, c_i64, c_f, c_p, c_p, c_p, c_p],
     "pk_causal_softmax_bwd_f32": [c_i64, c_i64, c_p, c_p, c_p, c_p],
     "pk_embed_fwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p],
-    "pk_embed_bwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p],
+    "pk_embed_bwd_workspace": [c_i64],
+    "pk_embed_bwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_size, c_p],
     "pk_last_error": [],
 }
 _RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size,
-             "pk_gemm_workspace_f32": c_size, "pk_flash_attn_bwd_workspace": c_size}
+             "pk_gemm_workspace_f32": c_size, "pk_flash_attn_bwd_workspace": c_size,
+             "pk_embed_bwd_workspace": c_size}
 
 _hip = None
 

@@ -229,20 +229,75 @@ __global__ void sgd_kernel(int64_t n, float lr, float* __restrict__ p, const flo
     }
 }
 
-__global__ void adamw_kernel(int64_t n, float lr, float b1, float b2, float eps, float decay,
+// decoupled decay, then the bias-corrected Adam update of one element
+__device__ __forceinline__ float adamw_elem(float& p, float gi, float& m, float& v, float b1,
+                                            float b2, float eps, float decay, float step_size,
+                                            float bc2_sqrt) {
+    const float pj = p * decay;
+    const float mj = b1 * m + (1.0f - b1) * gi;
+    const float vj = b2 * v + (1.0f - b2) * gi * gi;
+    const float denom = sqrtf(vj) / bc2_sqrt + eps;
+    p = pj - step_size * (mj / denom);
+    m = mj;
+    v = vj;
+    return p;
+}
+
+__global__ void adamw_kernel(int64_t n, float b1, float b2, float eps, float decay,
                              float step_size, float bc2_sqrt, float* __restrict__ p,
                              const float* __restrict__ g, float* __restrict__ m,
                              float* __restrict__ v) {
     for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
         i += (int64_t)gridDim.x * blockDim.x) {
         const float gi = g ? g[i] : 0.0f;
-        const float pj = p[i] * decay;
-        const float mj = b1 * m[i] + (1.0f - b1) * gi;
-        const float vj = b2 * v[i] + (1.0f - b2) * gi * gi;
-        const float denom = sqrtf(vj) / bc2_sqrt + eps;
-        p[i] = pj - step_size * (mj / denom);
-        m[i] = mj;
-        v[i] = vj;
+        adamw_elem(p[i], gi, m[i], v[i], b1, b2, eps, decay, step_size, bc2_sqrt);
+    }
+}
+
+// One multi-tensor AdamW step: the step counter and the two bias corrections
+// live in device memory, so the launch parameters never change between steps.
+__global__ void adamw_prep_kernel(int32_t* step, float lr, float b1, float b2, float* coef) {
+    if(threadIdx.x != 0 || blockIdx.x != 0) return;
+    const int32_t t = *step + 1;
+    *step = t;
+    const double bc1 = 1.0 - pow((double)b1, (double)t);
+    const double bc2 = 1.0 - pow((double)b2, (double)t);
+    coef[0] = (float)((double)lr / bc1);
+    coef[1] = (float)sqrt(bc2);
+}
+
+// one workgroup per chunk (<= PK_ADAMW_CHUNK elements of one tensor)
+__global__ __launch_bounds__(256) void adamw_multi_kernel(const PkAdamwChunk* __restrict__ chunks,
+                                                          float b1, float b2, float eps,
+                                                          float decay,
+                                                          const float* __restrict__ coef) {
+    const PkAdamwChunk c = chunks[blockIdx.x];
+    const float step_size = coef[0], bc2_sqrt = coef[1];
+    const uintptr_t align = reinterpret_cast<uintptr_t>(c.p) | reinterpret_cast<uintptr_t>(c.g) |
+                            reinterpret_cast<uintptr_t>(c.m) | reinterpret_cast<uintptr_t>(c.v);
+    const int64_t n4 = (align & 15) ? 0 : c.n / 4;
+    f32x4* p4 = reinterpret_cast<f32x4*>(c.p);
+    f32x4* m4 = reinterpret_cast<f32x4*>(c.m);
+    f32x4* v4 = reinterpret_cast<f32x4*>(c.v);
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(c.g);
+    for(int64_t i = threadIdx.x; i < n4; i += blockDim.x) {
+        f32x4 p = p4[i], m = m4[i], v = v4[i];
+        const f32x4 g = c.g ? g4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            float pe = p[e], me = m[e], ve = v[e];
+            adamw_elem(pe, g[e], me, ve, b1, b2, eps, decay, step_size, bc2_sqrt);
+            p[e] = pe;
+            m[e] = me;
+            v[e] = ve;
+        }
+        p4[i] = p;
+        m4[i] = m;
+        v4[i] = v;
+    }
+    for(int64_t i = n4 * 4 + threadIdx.x; i < c.n; i += blockDim.x) {
+        const float gi = c.g ? c.g[i] : 0.0f;
+        adamw_elem(c.p[i], gi, c.m[i], c.v[i], b1, b2, eps, decay, step_size, bc2_sqrt);
     }
 }
 
@@ -271,14 +326,129 @@ __global__ void embed_fwd4_kernel(int64_t n, int64_t d4, int64_t vocab,
     }
 }
 
-__global__ void embed_bwd_kernel(int64_t n, int64_t d, int64_t vocab, const int32_t* __restrict__ ids,
-                                 const float* __restrict__ dout, float* __restrict__ dtable) {
-    const int64_t total = n * d;
-    for(int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
-        t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t i = t / d, e = t % d;
+// ---- deterministic embedding backward -------------------------------------
+// dtable[r,:] += dout[i,:] for every i with ids[i] == r, the adds of one row
+// made in increasing i -- the order of the sequential loop, so the result is
+// the same bits on every run and replay.  Four launches:
+//   group:  for each position i, rank_i = #{j < i : ids[j] == ids[i]},
+//           first_i = the smallest such j (i itself when rank_i == 0) and
+//           cnt_i = #{j : ids[j] == ids[i]}.  Each workgroup owns 64
+//           positions (one per lane) and its 8 waves split the j range, with
+//           the ids staged through LDS in tiles of 4096: O(n^2) compares, a
+//           few microseconds at the n = B*T of a training step.
+//   scan:   start_i = sum over j < i of (first occurrence of a valid id ?
+//           cnt_j : 0), one workgroup.
+//   place:  perm[start_{first_i} + rank_i] = i, so each id's positions are
+//           contiguous and in increasing order.
+//   sum:    one workgroup per first occurrence adds its rows in that order.
+constexpr int kGroupWaves = 8, kGroupTile = 4096, kScanThreads = 1024;
+
+struct EmbedWs {
+    int32_t *rank, *first, *cnt, *start, *perm;
+};
+
+__global__ __launch_bounds__(64 * kGroupWaves) void embed_group_kernel(
+    int64_t n, const int32_t* __restrict__ ids, EmbedWs ws) {
+    __shared__ int32_t tile[kGroupTile];
+    __shared__ int32_t part[3][kGroupWaves][64];
+    const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+    const int64_t i = blockIdx.x * 64 + lane;
+    const int32_t my = i < n ? ids[i] : 0;
+    int32_t r = 0, c = 0, f = 0x7fffffff;
+    constexpr int per_wave = kGroupTile / kGroupWaves;
+    for(int64_t j0 = 0; j0 < n; j0 += kGroupTile) {
+        __syncthreads();
+        for(int t = threadIdx.x; t < kGroupTile; t += blockDim.x)
+            tile[t] = j0 + t < n ? ids[j0 + t] : 0;
+        __syncthreads();
+        const int lim = (int)min((int64_t)kGroupTile, n - j0);
+        const int tb = w * per_wave, te = min(lim, tb + per_wave);
+        for(int t = tb; t < te; ++t) {
+            const int64_t j = j0 + t;
+            const bool eq = tile[t] == my;
+            const bool before = j < i;
+            c += eq;
+            r += eq && before;
+            if(eq && before) f = min(f, (int32_t)j);
+        }
+    }
+    part[0][w][lane] = r;
+    part[1][w][lane] = c;
+    part[2][w][lane] = f;
+    __syncthreads();
+    if(w == 0 && i < n) {
+        for(int k = 1; k < kGroupWaves; ++k) {
+            r += part[0][k][lane];
+            c += part[1][k][lane];
+            f = min(f, part[2][k][lane]);
+        }
+        ws.rank[i] = r;
+        ws.cnt[i] = c;
+        ws.first[i] = f == 0x7fffffff ? (int32_t)i : f;
+    }
+}
+
+__global__ __launch_bounds__(kScanThreads) void embed_scan_kernel(int64_t n, int64_t vocab,
+                                                                  const int32_t* __restrict__ ids,
+                                                                  EmbedWs ws) {
+    __shared__ int32_t sums[kScanThreads];
+    const int64_t chunk = (n + kScanThreads - 1) / kScanThreads;
+    const int64_t b = threadIdx.x * chunk, e = min(n, b + chunk);
+    auto weight = [&](int64_t i) {
         const int32_t id = ids[i];
-        if(id >= 0 && id < vocab) unsafeAtomicAdd(dtable + (int64_t)id * d + e, dout[t]);
+        return (ws.rank[i] == 0 && id >= 0 && id < vocab) ? ws.cnt[i] : 0;
+    };
+    int32_t local = 0;
+    for(int64_t i = b; i < e; ++i) local += weight(i);
+    sums[threadIdx.x] = local;
+    __syncthreads();
+    // inclusive scan of the per-thread sums (Hillis-Steele in LDS)
+    for(int o = 1; o < kScanThreads; o <<= 1) {
+        const int32_t add = threadIdx.x >= o ? sums[threadIdx.x - o] : 0;
+        __syncthreads();
+        sums[threadIdx.x] += add;
+        __syncthreads();
+    }
+    int32_t run = threadIdx.x ? sums[threadIdx.x - 1] : 0;
+    for(int64_t i = b; i < e; ++i) {
+        ws.start[i] = run;
+        run += weight(i);
+    }
+}
+
+__global__ void embed_place_kernel(int64_t n, int64_t vocab, const int32_t* __restrict__ ids,
+                                   EmbedWs ws) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t id = ids[i];
+        if(id < 0 || id >= vocab) continue;
+        ws.perm[ws.start[ws.first[i]] + ws.rank[i]] = (int32_t)i;
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_sum_kernel(int64_t d, int64_t vocab,
+                                                        const int32_t* __restrict__ ids,
+                                                        const float* __restrict__ dout,
+                                                        float* __restrict__ dtable, EmbedWs ws) {
+    const int64_t i = blockIdx.x;
+    const int32_t id = ids[i];
+    if(ws.rank[i] != 0 || id < 0 || id >= vocab) return;
+    const int32_t s = ws.start[i], c = ws.cnt[i];
+    float* row = dtable + (int64_t)id * d;
+    if((d & 3) == 0 && pk::aligned16(dout) && pk::aligned16(dtable)) {
+        const int64_t d4 = d / 4;
+        for(int64_t col = threadIdx.x; col < d4; col += blockDim.x) {
+            f32x4 acc = reinterpret_cast<f32x4*>(row)[col];
+            for(int32_t k = 0; k < c; ++k)
+                acc += reinterpret_cast<const f32x4*>(dout + (int64_t)ws.perm[s + k] * d)[col];
+            reinterpret_cast<f32x4*>(row)[col] = acc;
+        }
+        return;
+    }
+    for(int64_t col = threadIdx.x; col < d; col += blockDim.x) {
+        float acc = row[col];
+        for(int32_t k = 0; k < c; ++k) acc += dout[(int64_t)ws.perm[s + k] * d + col];
+        row[col] = acc;
     }
 }
 
@@ -451,8 +621,28 @@ extern "C" int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float
     const float bc2_sqrt = (float)sqrt(bc2);
     const float decay = 1.0f - lr * weight_decay;
     adamw_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(
-        n, lr, beta1, beta2, eps, decay, step_size, bc2_sqrt, p, g, m, v);
+        n, beta1, beta2, eps, decay, step_size, bc2_sqrt, p, g, m, v);
     return pk::launch_status("pk_adamw_f32");
+}
+
+extern "C" int pk_adamw_prep_f32(int32_t* step, float lr, float beta1, float beta2,
+                                 float* coef, pk_stream_t stream) {
+    if(!step || !coef) return pk::fail("pk_adamw_prep_f32: NULL pointer");
+    adamw_prep_kernel<<<1, 64, 0, pk::as_stream(stream)>>>(step, lr, beta1, beta2, coef);
+    return pk::launch_status("pk_adamw_prep_f32");
+}
+
+extern "C" int pk_adamw_multi_f32(int64_t nchunks, const PkAdamwChunk* chunks, float lr,
+                                  float beta1, float beta2, float eps, float weight_decay,
+                                  const float* coef, pk_stream_t stream) {
+    if(nchunks < 0) return pk::fail("pk_adamw_multi_f32: negative chunk count");
+    if(nchunks == 0) return PK_OK;
+    if(!chunks || !coef) return pk::fail("pk_adamw_multi_f32: NULL pointer");
+    if(nchunks > 0x7fffffff) return pk::fail("pk_adamw_multi_f32: too many chunks");
+    const float decay = 1.0f - lr * weight_decay;
+    adamw_multi_kernel<<<(unsigned)nchunks, 256, 0, pk::as_stream(stream)>>>(chunks, beta1, beta2,
+                                                                           eps, decay, coef);
+    return pk::launch_status("pk_adamw_multi_f32");
 }
 
 extern "C" int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids,
@@ -469,12 +659,26 @@ extern "C" int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32
     return pk::launch_status("pk_embed_fwd_f32");
 }
 
+extern "C" size_t pk_embed_bwd_workspace(int64_t n) {
+    return n > 0 ? (size_t)5 * (size_t)n * sizeof(int32_t) + 256 : 0;
+}
+
 extern "C" int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids,
-                                const float* dout, float* dtable, pk_stream_t stream) {
+                                const float* dout, float* dtable, void* workspace,
+                                size_t workspace_bytes, pk_stream_t stream) {
     if(n < 0 || d < 0 || vocab < 0) return pk::fail("pk_embed_bwd_f32: negative size");
     if(n == 0 || d == 0) return PK_OK;
     if(!ids || !dout || !dtable) return pk::fail("pk_embed_bwd_f32: NULL pointer");
-    embed_bwd_kernel<<<pk::grid_for(n * d, NT), NT, 0, pk::as_stream(stream)>>>(n, d, vocab, ids,
-                                                                               dout, dtable);
+    if(n > 0x7fffffff) return pk::fail("pk_embed_bwd_f32: more than 2^31 - 1 ids");
+    if(!workspace || workspace_bytes < pk_embed_bwd_workspace(n))
+        return pk::fail("pk_embed_bwd_f32: workspace of %zu bytes, %zu needed", workspace_bytes,
+                        pk_embed_bwd_workspace(n));
+    int32_t* base = static_cast<int32_t*>(workspace);
+    EmbedWs ws = {base, base + n, base + 2 * n, base + 3 * n, base + 4 * n};
+    hipStream_t st = pk::as_stream(stream);
+    embed_group_kernel<<<(unsigned)((n + 63) / 64), 64 * kGroupWaves, 0, st>>>(n, ids, ws);
+    embed_scan_kernel<<<1, kScanThreads, 0, st>>>(n, vocab, ids, ws);
+    embed_place_kernel<<<pk::grid_for(n, NT), NT, 0, st>>>(n, vocab, ids, ws);
+    embed_sum_kernel<<<(unsigned)n, 256, 0, st>>>(d, vocab, ids, dout, dtable, ws);
     return pk::launch_status("pk_embed_bwd_f32");
 }

@@ -21,7 +21,7 @@ int launch_status(const char* what);
 
 inline hipStream_t as_stream(pk_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---- wavefront reductions over all 64 lanes (DPP/permute via shfl_xor) ----
 __device__ __forceinline__ float wave_sum(float v) {

@@ -273,14 +273,17 @@ static void emb_backward(struct PicoTensor* self) {
     if(!g) return;
     int64_t V = tab->shape[0], d = tab->shape[1];
     if(!pkh_grad_is_live(tab)) {
-        /* scatter-add needs a zeroed target */
+        /* rows no id touches must read as zero */
         if(pkh_status("pico_embedding_backward", pk_fill_f32(tab->numel, 0.0f, tab->grad,
                                                                pkh_stream())))
             return;
         pkh_grad_mark(tab);
     }
+    const size_t need = pk_embed_bwd_workspace(self->shape[0]);
+    void* ws = pkh_workspace(need);
+    if(!ws) return;
     int st = pk_embed_bwd_f32(self->shape[0], d, V, (const int32_t*)n->saved[ES_IDS], g,
-                              tab->grad, pkh_stream());
+                              tab->grad, ws, need, pkh_stream());
     pkh_status("pico_embedding_backward", st);
 }
 

@@ -78,11 +78,26 @@ void pico_optim_sgd_free(struct PicoOptimSGD* o) {
 }
 
 /* --------------------------------------------------------------- AdamW */
+/*
+ * One step is two launches whatever the number of params: a one-thread
+ * kernel advances the step counter held in device memory and writes the two
+ * bias corrections, then one multi-tensor kernel updates every param, one
+ * workgroup per chunk of up to PK_ADAMW_CHUNK elements.  Nothing in the
+ * launches changes between steps, so a step can be captured in a graph and
+ * replayed.  The chunk table lives in device memory and is rebuilt (a
+ * synchronous upload) only when the params or the set of params holding a
+ * gradient change.
+ */
 struct PicoOptimAdamW {
     struct ParamList params;
     float** m; /* device moment buffers, one allocation per param (m then v) */
     float lr, beta1, beta2, eps, wd;
     int t;
+    void* state;          /* device: int32 step count, then 2 floats of coefficients */
+    PkAdamwChunk* table;  /* device chunk table */
+    int64_t nchunks, table_cap;
+    unsigned char* built; /* per param: 1 + grad_live when the table was built, 0 = stale */
+    int built_n;
 };
 
 struct PicoOptimAdamW* pico_optim_adamw_init(float lr, float beta1, float beta2, float eps,
@@ -94,6 +109,13 @@ struct PicoOptimAdamW* pico_optim_adamw_init(float lr, float beta1, float beta2,
     o->beta2 = beta2;
     o->eps = eps;
     o->wd = weight_decay;
+    o->state = pkh_device_alloc(256);
+    if(!o->state) {
+        free(o);
+        return NULL;
+    }
+    /* step count 0 and zero coefficients: all-zero bits */
+    pkh_status("pico_optim_adamw_init", pk_fill_f32(3, 0.0f, (float*)o->state, pkh_stream()));
     return o;
 }
 
@@ -115,19 +137,71 @@ void pico_optim_adamw_add(struct PicoOptimAdamW* o, struct PicoTensor* p) {
                    pk_fill_f32((int64_t)(2 * half / sizeof(float)), 0.0f, buf, pkh_stream()));
 }
 
-void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
-    o->t++;
-    for(int i = 0; i < o->params.n; i++) {
+/* the chunk table for the current params and their gradient state */
+static int adamw_table(struct PicoOptimAdamW* o) {
+    const int n = o->params.n;
+    int stale = o->built_n != n || !o->built;
+    for(int i = 0; i < n && !stale; i++)
+        stale = o->built[i] != (unsigned char)(1 + (pkh_grad_is_live(o->params.v[i]) ? 1 : 0));
+    if(!stale) return 0;
+    int64_t count = 0;
+    for(int i = 0; i < n; i++)
+        if(o->m[i]) count += (o->params.v[i]->numel + PK_ADAMW_CHUNK - 1) / PK_ADAMW_CHUNK;
+    PkAdamwChunk* h = (PkAdamwChunk*)malloc(sizeof(PkAdamwChunk) * (size_t)(count ? count : 1));
+    unsigned char* built = (unsigned char*)realloc(o->built, (size_t)(n > 0 ? n : 1));
+    if(!h || !built) {
+        free(h);
+        if(built) o->built = built;
+        pkh_set_error("AdamW: out of host memory");
+        return -1;
+    }
+    o->built = built;
+    int64_t c = 0;
+    for(int i = 0; i < n; i++) {
         struct PicoTensor* p = o->params.v[i];
+        const int live = pkh_grad_is_live(p);
+        built[i] = (unsigned char)(1 + (live ? 1 : 0));
         float* m = o->m[i];
         if(!m) continue;
         size_t half = ((size_t)p->numel * sizeof(float) + 255) & ~(size_t)255;
         float* v = (float*)((unsigned char*)m + half);
-        const float* g = pkh_grad_is_live(p) ? p->grad : NULL;
-        pkh_status("pico_optim_adamw_step",
-                   pk_adamw_f32(p->numel, o->lr, o->beta1, o->beta2, o->eps, o->wd, o->t, p->data,
-                                g, m, v, pkh_stream()));
+        for(int64_t off = 0; off < p->numel; off += PK_ADAMW_CHUNK, c++) {
+            h[c].p = p->data + off;
+            h[c].g = live ? p->grad + off : NULL;
+            h[c].m = m + off;
+            h[c].v = v + off;
+            h[c].n = p->numel - off < PK_ADAMW_CHUNK ? p->numel - off : PK_ADAMW_CHUNK;
+        }
     }
+    int rc = 0;
+    if(count > o->table_cap) {
+        if(o->table) {
+            pkh_sync();
+            pkh_device_free(o->table);
+        }
+        o->table = (PkAdamwChunk*)pkh_device_alloc(sizeof(PkAdamwChunk) * (size_t)count);
+        o->table_cap = o->table ? count : 0;
+        if(!o->table) rc = -1;
+    }
+    if(rc == 0 && count > 0) rc = pkh_copy_h2d(o->table, h, sizeof(PkAdamwChunk) * (size_t)count);
+    free(h);
+    o->nchunks = rc == 0 ? count : 0;
+    o->built_n = rc == 0 ? n : -1;
+    return rc;
+}
+
+void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
+    if(!o) return;
+    if(adamw_table(o)) return; /* the failing call recorded the error */
+    o->t++;
+    int32_t* step = (int32_t*)o->state;
+    float* coef = (float*)o->state + 1;
+    if(pkh_status("pico_optim_adamw_step",
+                  pk_adamw_prep_f32(step, o->lr, o->beta1, o->beta2, coef, pkh_stream())))
+        return;
+    pkh_status("pico_optim_adamw_step",
+               pk_adamw_multi_f32(o->nchunks, o->table, o->lr, o->beta1, o->beta2, o->eps, o->wd,
+                                  coef, pkh_stream()));
 }
 
 void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* o) { zero_grads(&o->params); }
@@ -136,6 +210,9 @@ void pico_optim_adamw_free(struct PicoOptimAdamW* o) {
     if(!o) return;
     pkh_sync();
     for(int i = 0; i < o->params.n; i++) pkh_device_free(o->m[i]);
+    pkh_device_free(o->table);
+    pkh_device_free(o->state);
+    free(o->built);
     free(o->m);
     free(o->params.v);
     free(o);

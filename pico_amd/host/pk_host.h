@@ -46,6 +46,7 @@ void pkh_set_error(const char* fmt, ...);
  * and records it; returns status */
 int pkh_status(const char* op, int status);
 int pkh_sync(void);
+int pkh_capturing(void); /* a graph capture is in progress */
 void* pkh_device_alloc(size_t bytes); /* hipMalloc; NULL + message on failure */
 void pkh_device_free(void* p);
 /* a device scratch buffer of at least `bytes`, reused across calls (the

@@ -23,6 +23,12 @@ static hipStream_t g_user_stream = NULL;
 static int g_user_stream_set = 0;
 static char g_err[512] = "";
 
+/* graph capture: while set, every launch is recorded on the library's stream,
+ * and anything that would allocate, free, copy synchronously or wait on the
+ * device fails the capture instead */
+static int g_capturing = 0;
+static int g_capture_failed = 0;
+
 static void* g_ws = NULL;
 static size_t g_ws_bytes = 0;
 
@@ -32,6 +38,19 @@ void pkh_set_error(const char* fmt, ...) {
     vsnprintf(g_err, sizeof(g_err), fmt, ap);
     va_end(ap);
 }
+
+/* refuses a call that cannot be recorded in a graph; returns nonzero then */
+static int capture_refuses(const char* what) {
+    if(!g_capturing) return 0;
+    g_capture_failed = 1;
+    pkh_set_error("%s during graph capture: run the step once before capturing, pass "
+                  "token ids as device pointers, and read results after pico_graph_launch",
+                  what);
+    PKH_ERR("%s\n", g_err);
+    return 1;
+}
+
+int pkh_capturing(void) { return g_capturing; }
 
 int pkh_init(void) {
     if(g_ready) return 0;
@@ -77,6 +96,7 @@ void pico_gpu_set_stream(void* stream) {
 
 int pkh_status(const char* op, int status) {
     if(status == 0) return 0;
+    if(g_capturing) g_capture_failed = 1;
     const char* msg = pk_last_error();
     if(status != PK_EINVAL || !msg || !*msg) msg = hipGetErrorString((hipError_t)status);
     pkh_set_error("%s: %s (status %d)", op, msg, status);
@@ -86,6 +106,7 @@ int pkh_status(const char* op, int status) {
 
 int pkh_sync(void) {
     if(pkh_init()) return -1;
+    if(capture_refuses("waiting on the device")) return -1;
     hipError_t e = hipStreamSynchronize((hipStream_t)pkh_stream());
     if(e != hipSuccess) return pkh_status("pico_gpu_synchronize", (int)e);
     return 0;
@@ -99,6 +120,7 @@ static size_t g_dev_bytes = 0, g_dev_peak = 0;
 
 void* pkh_device_alloc(size_t bytes) {
     if(pkh_init()) return NULL;
+    if(capture_refuses("device allocation")) return NULL;
     void* p = NULL;
     if(!bytes) bytes = 256;
     hipError_t e = hipMalloc(&p, bytes);
@@ -114,6 +136,7 @@ void* pkh_device_alloc(size_t bytes) {
 
 void pkh_device_free(void* p) {
     if(!p) return;
+    if(capture_refuses("freeing device memory")) return;
     size_t sz = 0;
     if(hipMemPtrGetInfo(p, &sz) == hipSuccess) g_dev_bytes -= sz < g_dev_bytes ? sz : g_dev_bytes;
     hipFree(p);
@@ -126,6 +149,7 @@ void pico_gpu_memory(size_t* in_use, size_t* peak) {
 
 void* pkh_workspace(size_t bytes) {
     if(bytes <= g_ws_bytes) return g_ws;
+    if(capture_refuses("growing the GEMM workspace")) return NULL;
     /* grow: wait for work that may still read the old buffer */
     if(g_ws) {
         hipStreamSynchronize((hipStream_t)pkh_stream());
@@ -152,6 +176,7 @@ int pkh_is_device_ptr(const void* p) {
 
 int pkh_copy_h2d(void* dst, const void* src, size_t bytes) {
     if(pkh_init()) return -1;
+    if(capture_refuses("a host-to-device copy")) return -1;
     if(bytes == 0) return 0;
     hipStream_t st = (hipStream_t)pkh_stream();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
@@ -161,9 +186,84 @@ int pkh_copy_h2d(void* dst, const void* src, size_t bytes) {
 
 int pkh_copy_d2h(void* dst, const void* src, size_t bytes) {
     if(pkh_init()) return -1;
+    if(capture_refuses("a device-to-host copy")) return -1;
     if(bytes == 0) return 0;
     hipStream_t st = (hipStream_t)pkh_stream();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st);
     if(e == hipSuccess) e = hipStreamSynchronize(st);
     return e == hipSuccess ? 0 : pkh_status("device-to-host copy", (int)e);
+}
+
+/* ------------------------------------------------------------ device graphs */
+struct PicoGraph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+int pico_graph_begin(void) {
+    if(pkh_init()) return -1;
+    if(g_capturing) {
+        pkh_set_error("pico_graph_begin: a capture is already in progress");
+        PKH_ERR("%s\n", g_err);
+        return PK_EINVAL;
+    }
+    /* relaxed: the library itself refuses every call that would break the
+     * graph (see capture_refuses) */
+    hipError_t e = hipStreamBeginCapture((hipStream_t)pkh_stream(), hipStreamCaptureModeRelaxed);
+    if(e != hipSuccess) return pkh_status("pico_graph_begin", (int)e);
+    g_capturing = 1;
+    g_capture_failed = 0;
+    return 0;
+}
+
+struct PicoGraph* pico_graph_end(void) {
+    if(!g_capturing) {
+        pkh_set_error("pico_graph_end: no capture in progress");
+        PKH_ERR("%s\n", g_err);
+        return NULL;
+    }
+    hipGraph_t graph = NULL;
+    hipError_t e = hipStreamEndCapture((hipStream_t)pkh_stream(), &graph);
+    g_capturing = 0;
+    if(e != hipSuccess || g_capture_failed) {
+        if(graph) hipGraphDestroy(graph);
+        if(e != hipSuccess) pkh_status("pico_graph_end", (int)e);
+        return NULL;
+    }
+    struct PicoGraph* g = (struct PicoGraph*)calloc(1, sizeof(*g));
+    if(!g) {
+        hipGraphDestroy(graph);
+        pkh_set_error("pico_graph_end: out of host memory");
+        return NULL;
+    }
+    g->graph = graph;
+    e = hipGraphInstantiate(&g->exec, graph, NULL, NULL, 0);
+    if(e != hipSuccess) {
+        hipGraphDestroy(graph);
+        free(g);
+        pkh_status("pico_graph_end (instantiate)", (int)e);
+        return NULL;
+    }
+    return g;
+}
+
+int pico_graph_launch(struct PicoGraph* g) {
+    if(!g) {
+        pkh_set_error("pico_graph_launch: NULL graph");
+        return PK_EINVAL;
+    }
+    if(g_capturing) {
+        pkh_set_error("pico_graph_launch: cannot launch a graph while capturing");
+        return PK_EINVAL;
+    }
+    hipError_t e = hipGraphLaunch(g->exec, (hipStream_t)pkh_stream());
+    return e == hipSuccess ? 0 : pkh_status("pico_graph_launch", (int)e);
+}
+
+void pico_graph_free(struct PicoGraph* g) {
+    if(!g) return;
+    hipStreamSynchronize((hipStream_t)pkh_stream());
+    hipGraphExecDestroy(g->exec);
+    hipGraphDestroy(g->graph);
+    free(g);
 }

@@ -499,6 +499,14 @@ int32_t* pico_ids_to_device(const int32_t* host_ids, int64_t n) {
     return d;
 }
 
+int pico_ids_update(int32_t* device_ids, const int32_t* host_ids, int64_t n) {
+    if(n < 0 || (n > 0 && (!device_ids || !host_ids))) {
+        pkh_set_error("pico_ids_update: bad arguments");
+        return PK_EINVAL;
+    }
+    return pkh_copy_h2d(device_ids, host_ids, sizeof(int32_t) * (size_t)n);
+}
+
 const int32_t* pkh_ids_on_device(const int32_t* ids, int64_t n) {
     if(!ids) return NULL;
     if(pkh_is_device_ptr(ids)) return ids;

@@ -185,6 +185,43 @@ def adamw(p, g, m, v, lr, beta1, beta2, eps, wd, step):
     return p
 
 
+class PkAdamwChunk(ctypes.Structure):
+    """struct PkAdamwChunk (include/pico_hip.h)"""
+    _fields_ = [("p", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p),
+                ("v", ctypes.c_void_p), ("n", ctypes.c_int64)]
+
+
+ADAMW_CHUNK = 65536
+
+
+def adamw_multi(groups, lr, beta1, beta2, eps, wd, state):
+    """One multi-tensor AdamW step over groups of (p, g or None, m, v).  state:
+    a device int32 tensor of >= 3 elements -- the step count (advanced here)
+    and the two bias corrections, as floats, in elements 1 and 2.  Returns the
+    device chunk table, which must stay alive until the launch has run."""
+    _f32(*[t for grp in groups for t in grp])
+    if state.dtype != torch.int32 or state.numel() < 3 or not state.is_cuda:
+        raise ValueError("state must be a device int32 tensor of >= 3 elements")
+    chunks = []
+    for p, g, m, v in groups:
+        n = p.numel()
+        if any(t is not None and t.numel() != n for t in (g, m, v)):
+            raise ValueError("p, g, m, v must have the same size")
+        for off in range(0, n, ADAMW_CHUNK):
+            chunks.append(PkAdamwChunk(p.data_ptr() + 4 * off,
+                                       None if g is None else g.data_ptr() + 4 * off,
+                                       m.data_ptr() + 4 * off, v.data_ptr() + 4 * off,
+                                       min(ADAMW_CHUNK, n - off)))
+    arr = (PkAdamwChunk * max(1, len(chunks)))(*chunks)
+    table = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(state.device)
+    coef = ctypes.c_void_p(state.data_ptr() + 4)
+    check("pk_adamw_prep_f32", hip_lib().pk_adamw_prep_f32(_ptr(state), lr, beta1, beta2, coef,
+                                                            _stream()))
+    check("pk_adamw_multi_f32", hip_lib().pk_adamw_multi_f32(
+        len(chunks), _ptr(table), lr, beta1, beta2, eps, wd, coef, _stream()))
+    return table
+
+
 def xent_fwd_bwd(logits, labels, loss_rows=None, dlogits=None, scale=1.0, accumulate=False,
                  scale_dev=None):
     R, V = logits.shape
@@ -307,9 +344,13 @@ def embed_fwd(ids, table, out):
 
 
 def embed_bwd(ids, dout, dtable):
+    """dtable[ids[i]] += dout[i], each row's adds in increasing i"""
     n, d = dout.shape
+    need = hip_lib().pk_embed_bwd_workspace(n)
+    ws = torch.empty(max(1, need), dtype=torch.uint8, device=dout.device)
     check("pk_embed_bwd_f32", hip_lib().pk_embed_bwd_f32(n, d, dtable.shape[0], _ptr(ids),
-                                                          _ptr(dout), _ptr(dtable), _stream()))
+                                                          _ptr(dout), _ptr(dtable), _ptr(ws),
+                                                          need, _stream()))
     return dtable
 
 

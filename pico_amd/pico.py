@@ -102,6 +102,11 @@ _GPU_SIGS = {
     "pico_tensor_grad_to_host": (ctypes.c_int, [TP, c_p]),
     "pico_tensor_grad_from_host": (ctypes.c_int, [TP, c_p]),
     "pico_ids_to_device": (c_p, [c_p, c_i64]),
+    "pico_ids_update": (ctypes.c_int, [c_p, c_p, c_i64]),
+    "pico_graph_begin": (ctypes.c_int, []),
+    "pico_graph_end": (c_p, []),
+    "pico_graph_launch": (ctypes.c_int, [c_p]),
+    "pico_graph_free": (None, [c_p]),
     "pico_argmax": (ctypes.c_int, [TP, c_p]),
     "pico_gpu_synchronize": (ctypes.c_int, []),
     "pico_gpu_last_error": (ctypes.c_char_p, []),
