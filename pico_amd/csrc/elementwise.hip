@@ -110,6 +110,42 @@ __global__ void binary_bwd_reduce(int op, int which, BwdDesc d, int64_t xn,
     }
 }
 
+// Fast paths of the same gradient, with the same order and rounding:
+//  * x has the output's shape and layout (a residual add): one float4 per thread;
+//  * x is broadcast over leading rows only (a bias): out viewed as [R, C], one
+//    thread per column j adds the R rows in increasing order.
+__device__ __forceinline__ float grad_add(int op, int which, float acc, float g, float other) {
+    // sub's second operand: grad -= g, the reference's form
+    if(op == 1 && which == 1) return acc - g;
+    return acc + grad_term(op, which, g, other);
+}
+
+__global__ void binary_bwd_same4(int op, int which, int64_t n4, const f32x4* __restrict__ gout,
+                                 const f32x4* __restrict__ other, f32x4* __restrict__ gx,
+                                 int accum) {
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const f32x4 g = pk::ld_stream(gout + i);
+        const f32x4 o = op == 2 ? pk::ld_stream(other + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 acc = accum ? gx[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for(int e = 0; e < 4; ++e) acc[e] = grad_add(op, which, acc[e], g[e], o[e]);
+        pk::st_stream(gx + i, acc);
+    }
+}
+
+__global__ void binary_bwd_rows(int op, int which, int64_t R, int64_t C,
+                                const float* __restrict__ gout, const float* __restrict__ other,
+                                float* __restrict__ gx, int accum) {
+    for(int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; j < C;
+        j += (int64_t)gridDim.x * blockDim.x) {
+        float acc = accum ? gx[j] : 0.0f;
+        for(int64_t r = 0; r < R; ++r)
+            acc = grad_add(op, which, acc, gout[r * C + j], op == 2 ? other[r * C + j] : 0.0f);
+        gx[j] = acc;
+    }
+}
+
 // ---------------------------------------------------------------- unary
 __device__ __forceinline__ float un_apply(int op, float x) {
     switch(op) {
@@ -348,28 +384,44 @@ struct EmbedWs {
 };
 
 __global__ __launch_bounds__(64 * kGroupWaves) void embed_group_kernel(
-    int64_t n, const int32_t* __restrict__ ids, EmbedWs ws) {
-    __shared__ int32_t tile[kGroupTile];
+    int64_t n64, const int32_t* __restrict__ ids, EmbedWs ws) {
+    __shared__ __attribute__((aligned(16))) int32_t tile[kGroupTile];
     __shared__ int32_t part[3][kGroupWaves][64];
+    const int n = (int)n64;  // the launcher refuses n >= 2^31
     const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
-    const int64_t i = blockIdx.x * 64 + lane;
+    const int i = blockIdx.x * 64 + lane;
     const int32_t my = i < n ? ids[i] : 0;
+    // r counts matches before i; the first occurrence is the smallest match
+    // over all j (i itself when nothing earlier matches)
     int32_t r = 0, c = 0, f = 0x7fffffff;
     constexpr int per_wave = kGroupTile / kGroupWaves;
-    for(int64_t j0 = 0; j0 < n; j0 += kGroupTile) {
+    for(int j0 = 0; j0 < n; j0 += kGroupTile) {
         __syncthreads();
         for(int t = threadIdx.x; t < kGroupTile; t += blockDim.x)
             tile[t] = j0 + t < n ? ids[j0 + t] : 0;
         __syncthreads();
-        const int lim = (int)min((int64_t)kGroupTile, n - j0);
+        const int lim = min(kGroupTile, n - j0);
         const int tb = w * per_wave, te = min(lim, tb + per_wave);
-        for(int t = tb; t < te; ++t) {
-            const int64_t j = j0 + t;
+        const int4* t4 = reinterpret_cast<const int4*>(tile);
+        int t = tb;
+        for(; t + 4 <= te; t += 4) {
+            const int4 x = t4[t >> 2];
+            const int32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for(int e = 0; e < 4; ++e) {
+                const int j = j0 + t + e;
+                const bool eq = xs[e] == my;
+                c += eq;
+                r += eq && j < i;
+                f = eq ? min(f, j) : f;
+            }
+        }
+        for(; t < te; ++t) {
+            const int j = j0 + t;
             const bool eq = tile[t] == my;
-            const bool before = j < i;
             c += eq;
-            r += eq && before;
-            if(eq && before) f = min(f, (int32_t)j);
+            r += eq && j < i;
+            f = eq ? min(f, j) : f;
         }
     }
     part[0][w][lane] = r;
@@ -384,35 +436,52 @@ __global__ __launch_bounds__(64 * kGroupWaves) void embed_group_kernel(
         }
         ws.rank[i] = r;
         ws.cnt[i] = c;
-        ws.first[i] = f == 0x7fffffff ? (int32_t)i : f;
+        ws.first[i] = f;  // i matches itself, so f <= i
     }
 }
+
+// start_i = sum over j < i of the group sizes of first occurrences of valid
+// ids: each thread owns kScanPer consecutive positions, loaded up front
+constexpr int kScanPer = 8;
 
 __global__ __launch_bounds__(kScanThreads) void embed_scan_kernel(int64_t n, int64_t vocab,
                                                                   const int32_t* __restrict__ ids,
                                                                   EmbedWs ws) {
     __shared__ int32_t sums[kScanThreads];
-    const int64_t chunk = (n + kScanThreads - 1) / kScanThreads;
-    const int64_t b = threadIdx.x * chunk, e = min(n, b + chunk);
-    auto weight = [&](int64_t i) {
-        const int32_t id = ids[i];
-        return (ws.rank[i] == 0 && id >= 0 && id < vocab) ? ws.cnt[i] : 0;
-    };
-    int32_t local = 0;
-    for(int64_t i = b; i < e; ++i) local += weight(i);
-    sums[threadIdx.x] = local;
-    __syncthreads();
-    // inclusive scan of the per-thread sums (Hillis-Steele in LDS)
-    for(int o = 1; o < kScanThreads; o <<= 1) {
-        const int32_t add = threadIdx.x >= o ? sums[threadIdx.x - o] : 0;
+    __shared__ int32_t carry;
+    if(threadIdx.x == 0) carry = 0;
+    for(int64_t base = 0; base < n; base += (int64_t)kScanThreads * kScanPer) {
+        const int64_t b = base + (int64_t)threadIdx.x * kScanPer;
+        int32_t wgt[kScanPer];
+#pragma unroll
+        for(int e = 0; e < kScanPer; ++e) {
+            const int64_t i = b + e;
+            const bool in = i < n;
+            const int32_t id = in ? ids[i] : -1;
+            const int32_t rk = in ? ws.rank[i] : 1;
+            const int32_t ct = in ? ws.cnt[i] : 0;
+            wgt[e] = (rk == 0 && id >= 0 && id < vocab) ? ct : 0;
+        }
+        int32_t local = 0;
+#pragma unroll
+        for(int e = 0; e < kScanPer; ++e) local += wgt[e];
         __syncthreads();
-        sums[threadIdx.x] += add;
+        sums[threadIdx.x] = local;
         __syncthreads();
-    }
-    int32_t run = threadIdx.x ? sums[threadIdx.x - 1] : 0;
-    for(int64_t i = b; i < e; ++i) {
-        ws.start[i] = run;
-        run += weight(i);
+        for(int o = 1; o < kScanThreads; o <<= 1) {
+            const int32_t add = threadIdx.x >= o ? sums[threadIdx.x - o] : 0;
+            __syncthreads();
+            sums[threadIdx.x] += add;
+            __syncthreads();
+        }
+        int32_t run = carry + (threadIdx.x ? sums[threadIdx.x - 1] : 0);
+#pragma unroll
+        for(int e = 0; e < kScanPer; ++e) {
+            if(b + e < n) ws.start[b + e] = run;
+            run += wgt[e];
+        }
+        __syncthreads();
+        if(threadIdx.x == kScanThreads - 1) carry = run;
     }
 }
 
@@ -530,8 +599,29 @@ extern "C" int pk_binary_bwd_f32(int op, int which, int ndim, const int64_t* out
                         (long long)x_numel, (long long)kept_numel);
     if(out_n == 0 || x_numel == 0) return PK_OK;
     if(!gout || !gx || (op == 2 && !other)) return pk::fail("pk_binary_bwd_f32: NULL data pointer");
-    binary_bwd_reduce<<<pk::grid_for(x_numel, NT), NT, 0, pk::as_stream(stream)>>>(
-        op, which, d, x_numel, gout, other, gx, flags & PK_ACCUM);
+    hipStream_t st = pk::as_stream(stream);
+    const int accum = flags & PK_ACCUM;
+    // x and (for mul) the other operand laid out exactly like the output
+    // over the kept dims, and every reduced dim ahead of every kept dim
+    bool kept_like_out = true, reduced_first = true;
+    for(int k = 0; k < d.nk; ++k)
+        if(d.kx[k] != d.kout[k] || (op == 2 && d.koth[k] != d.kout[k])) kept_like_out = false;
+    for(int k = 0; k < d.nr; ++k)
+        if(op == 2 && d.roth[k] != d.rout[k]) kept_like_out = false;
+    if(d.nk > 0 && d.nr > 0 && d.rout[d.nr - 1] < d.kout[0]) reduced_first = false;
+    if(kept_like_out && reduced_first && d.nr == 0 && x_numel % 4 == 0 && pk::aligned16(gout) &&
+       pk::aligned16(gx) && (op != 2 || pk::aligned16(other))) {
+        binary_bwd_same4<<<pk::grid_stream(x_numel / 4, NT), NT, 0, st>>>(
+            op, which, x_numel / 4, (const f32x4*)gout, (const f32x4*)other, (f32x4*)gx, accum);
+        return pk::launch_status("pk_binary_bwd_f32");
+    }
+    if(kept_like_out && reduced_first) {  // R = 1 when nothing is reduced
+        binary_bwd_rows<<<pk::grid_for(x_numel, NT), NT, 0, st>>>(op, which, d.red_numel, x_numel,
+                                                                  gout, other, gx, accum);
+        return pk::launch_status("pk_binary_bwd_f32");
+    }
+    binary_bwd_reduce<<<pk::grid_for(x_numel, NT), NT, 0, st>>>(op, which, d, x_numel, gout,
+                                                                  other, gx, accum);
     return pk::launch_status("pk_binary_bwd_f32");
 }
 

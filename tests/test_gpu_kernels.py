@@ -193,25 +193,35 @@ def test_gemm_rejects_bad_arguments(dev):
 
 
 # ---------------------------------------------------------- elementwise
+# same shapes (float4 and per-element paths), biases broadcast over leading rows,
+# broadcasts over trailing or interleaved dims (the general path), config-sized ones
 BCAST_CASES = [((3, 5), (3, 5)), ((4, 6), (6,)), ((4, 6), (4, 1)), ((2, 3, 4), (3, 1)),
-               ((7,), (1,)), ((5, 1, 3), (1, 4, 1)), ((16,), (16,)), ((19,), (19,))]
+               ((7,), (1,)), ((5, 1, 3), (1, 4, 1)), ((16,), (16,)), ((19,), (19,)),
+               ((64, 128), (128,)), ((3, 64, 10), (1, 10)), ((256, 768), (256, 768))]
 
 
+@pytest.mark.parametrize("accumulate", [True, False])
 @pytest.mark.parametrize("op", [0, 1, 2])
 @pytest.mark.parametrize("sa,sb", BCAST_CASES)
-def test_binary_and_grad_bitexact(dev, op, sa, sb):
+def test_binary_and_grad_bitexact(dev, op, sa, sb, accumulate):
     a = O.normal(int(np.prod(sa)), 1).reshape(sa)
     b = O.normal(int(np.prod(sb)), 2).reshape(sb)
     name = ["add", "sub", "mul"][op]
     out = K.binary(name, cu(a), cu(b))
     assert np.array_equal(host(out), O.binary(op, a, b))
     g = O.normal(out.numel(), 3).reshape(out.shape)
-    ga0 = O.normal(a.size, 4).reshape(sa)  # += onto a nonzero grad
-    gb0 = O.normal(b.size, 5).reshape(sb)
+    g.ravel()[::5] = -0.0  # a fresh grad is 0 + g: -0.0 becomes +0.0, as in pico
+    if accumulate:  # += onto a nonzero grad
+        ga0 = O.normal(a.size, 4).reshape(sa)
+        gb0 = O.normal(b.size, 5).reshape(sb)
+    else:
+        ga0, gb0 = np.zeros(sa, np.float32), np.zeros(sb, np.float32)
     ga_ref, gb_ref = O.binary_bwd(op, a, b, g, ga0.copy(), gb0.copy())
-    ga, gb = cu(ga0.copy()), cu(gb0.copy())
-    K.binary_bwd(name, 0, out.shape, sa, sb, cu(g), cu(b), ga, accumulate=True)
-    K.binary_bwd(name, 1, out.shape, sb, sa, cu(g), cu(a), gb, accumulate=True)
+    ga = cu(ga0.copy()) if accumulate else torch.full(sa, float("nan"), device=dev)
+    gb = cu(gb0.copy()) if accumulate else torch.full(sb, float("nan"), device=dev)
+    K.binary_bwd(name, 0, out.shape, sa, sb, cu(g), cu(b), ga, accumulate=accumulate)
+    K.binary_bwd(name, 1, out.shape, sb, sa, cu(g), cu(a), gb, accumulate=accumulate)
+    assert np.array_equal(np.signbit(host(ga)), np.signbit(ga_ref))
     assert np.array_equal(host(ga), ga_ref)
     assert np.array_equal(host(gb), gb_ref)
 
