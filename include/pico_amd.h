@@ -223,6 +223,9 @@ struct PicoTensor* pico_gpt_loss(struct PicoGPT* model, const int32_t* tokens,
                                  const int32_t* targets);
 int pico_gpt_num_params(const struct PicoGPT* model);
 struct PicoTensor* pico_gpt_param(struct PicoGPT* model, int index);
+/* name of param `index`: "emb", "layers.<l>.{attn_norm,wq,wk,wv,wo,ffn_norm,w1,w3,w2}",
+ * "final_norm", "lm_head" (NULL when out of range) */
+const char* pico_gpt_param_name(const struct PicoGPT* model, int index);
 void pico_gpt_free(struct PicoGPT* model);
 
 /* ---- host <-> device (no reference counterpart: pico's data is host memory) ----
@@ -246,6 +249,23 @@ const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
  * arena blocks, optimizer moments, scratch) */
 void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
+
+/* ---- checkpoints (no reference counterpart: the reference's params are plain
+ * float arrays, src/tensor.h:14-15, and nothing is ever saved) ----
+ * A safetensors file: 8-byte little-endian header length, a JSON header mapping
+ * each name to {"dtype", "shape", "data_offsets"}, then the raw little-endian
+ * bytes; any safetensors reader opens it.  tensors[i] is saved as F32 under
+ * names[i] (or "param.<i>" when names is NULL).  With an AdamW optimizer, each
+ * of its params also saves "<name>.adam_m" and "<name>.adam_v", plus
+ * "adamw.step" (I32), and the hyper-parameters go to the header's metadata.
+ * pico_checkpoint_load checks every name, dtype and shape before writing
+ * anything, then restores the tensors and the optimizer's moments and step
+ * count (its params must already be added), so a resumed run continues exactly
+ * as the saved one.  Both return 0, or nonzero with pico_gpu_last_error() set. */
+int pico_checkpoint_save(const char* path, int n, struct PicoTensor* const* tensors,
+                         const char* const* names, const struct PicoOptimAdamW* adamw);
+int pico_checkpoint_load(const char* path, int n, struct PicoTensor* const* tensors,
+                         const char* const* names, struct PicoOptimAdamW* adamw);
 
 /* ---- device graphs (no reference counterpart) ----
  * Record the launches of one training step once and replay them with a

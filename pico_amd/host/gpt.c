@@ -5,6 +5,7 @@
  * training step of the benchmark configurations; the ops it calls are the
  * hot path.
  */
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -20,6 +21,7 @@ struct PicoGPT {
     struct PicoGPTLayer* layers;
     struct PicoTensor *g_final, *wlm;
     struct PicoTensor** params;
+    char** names;
     int n_params;
 };
 
@@ -38,6 +40,8 @@ static struct PicoTensor* new_param(struct PicoGPT* m, int64_t r, int64_t c, int
     m->params[m->n_params++] = t;
     return t;
 }
+
+static int name_params(struct PicoGPT* m);
 
 struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed) {
     if(!cfg || cfg->vocab < 1 || cfg->d_model < 1 || cfg->n_layers < 0 || cfg->n_heads < 1 ||
@@ -68,6 +72,7 @@ struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed) {
              (L->w2 = new_param(m, F, d, 0, s++));
     }
     ok = ok && (m->g_final = new_param(m, 1, d, 1, 0)) && (m->wlm = new_param(m, d, V, 0, s++));
+    ok = ok && name_params(m) == 0;
     if(!ok) {
         pico_gpt_free(m);
         return NULL;
@@ -124,9 +129,39 @@ struct PicoTensor* pico_gpt_param(struct PicoGPT* m, int i) {
     return (m && i >= 0 && i < m->n_params) ? m->params[i] : NULL;
 }
 
+const char* pico_gpt_param_name(const struct PicoGPT* m, int i) {
+    return (m && m->names && i >= 0 && i < m->n_params) ? m->names[i] : NULL;
+}
+
+/* "emb", "layers.<l>.<part>", "final_norm", "lm_head", in param order */
+static int name_params(struct PicoGPT* m) {
+    static const char* const parts[9] = {"attn_norm", "wq", "wk", "wv", "wo",
+                                         "ffn_norm", "w1", "w3", "w2"};
+    m->names = (char**)calloc((size_t)m->n_params, sizeof(char*));
+    if(!m->names) return -1;
+    for(int i = 0; i < m->n_params; i++) {
+        char buf[48];
+        if(i == 0)
+            snprintf(buf, sizeof(buf), "emb");
+        else if(i == m->n_params - 2)
+            snprintf(buf, sizeof(buf), "final_norm");
+        else if(i == m->n_params - 1)
+            snprintf(buf, sizeof(buf), "lm_head");
+        else
+            snprintf(buf, sizeof(buf), "layers.%d.%s", (i - 1) / 9, parts[(i - 1) % 9]);
+        m->names[i] = (char*)malloc(strlen(buf) + 1);
+        if(!m->names[i]) return -1;
+        memcpy(m->names[i], buf, strlen(buf) + 1);
+    }
+    return 0;
+}
+
 void pico_gpt_free(struct PicoGPT* m) {
     if(!m) return;
     for(int i = 0; i < m->n_params; i++) pico_free(m->params[i]);
+    if(m->names)
+        for(int i = 0; i < m->n_params; i++) free(m->names[i]);
+    free(m->names);
     free(m->params);
     free(m->layers);
     free(m);

@@ -206,6 +206,49 @@ void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
 
 void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* o) { zero_grads(&o->params); }
 
+/* ---- state access for checkpoints ---- */
+int pkh_adamw_moments(const struct PicoOptimAdamW* o, const struct PicoTensor* p, float** m,
+                      float** v) {
+    for(int i = 0; i < o->params.n; i++) {
+        if(o->params.v[i] != p || !o->m[i]) continue;
+        size_t half = ((size_t)p->numel * sizeof(float) + 255) & ~(size_t)255;
+        *m = o->m[i];
+        *v = (float*)((unsigned char*)o->m[i] + half);
+        return 1;
+    }
+    return 0;
+}
+
+/* the device's step count is authoritative (graph replays advance only it) */
+int pkh_adamw_sync_step(struct PicoOptimAdamW* o) {
+    int32_t t = 0;
+    if(pkh_copy_d2h(&t, o->state, sizeof(t))) return -1;
+    o->t = t;
+    return 0;
+}
+
+int pkh_adamw_step(const struct PicoOptimAdamW* o) { return o->t; }
+
+int pkh_adamw_set_step(struct PicoOptimAdamW* o, int step) {
+    int32_t t = step;
+    if(step < 0) {
+        pkh_set_error("AdamW: negative step count %d", step);
+        return PK_EINVAL;
+    }
+    if(pkh_copy_h2d(o->state, &t, sizeof(t))) return PK_EINVAL;
+    o->t = step;
+    return 0;
+}
+
+void pkh_adamw_hparams(const struct PicoOptimAdamW* o, float* lr, float* b1, float* b2,
+                       float* eps, float* wd) {
+    *lr = o->lr;
+    *b1 = o->beta1;
+    *b2 = o->beta2;
+    *eps = o->eps;
+    *wd = o->wd;
+}
+
 void pico_optim_adamw_free(struct PicoOptimAdamW* o) {
     if(!o) return;
     pkh_sync();

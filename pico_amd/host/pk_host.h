@@ -47,6 +47,15 @@ void pkh_set_error(const char* fmt, ...);
 int pkh_status(const char* op, int status);
 int pkh_sync(void);
 int pkh_capturing(void); /* a graph capture is in progress */
+
+/* AdamW state, for checkpoints (optim.c) */
+int pkh_adamw_moments(const struct PicoOptimAdamW* o, const struct PicoTensor* p, float** m,
+                      float** v);
+int pkh_adamw_sync_step(struct PicoOptimAdamW* o);
+int pkh_adamw_step(const struct PicoOptimAdamW* o);
+int pkh_adamw_set_step(struct PicoOptimAdamW* o, int step);
+void pkh_adamw_hparams(const struct PicoOptimAdamW* o, float* lr, float* b1, float* b2,
+                       float* eps, float* wd);
 void* pkh_device_alloc(size_t bytes); /* hipMalloc; NULL + message on failure */
 void pkh_device_free(void* p);
 /* a device scratch buffer of at least `bytes`, reused across calls (the

@@ -118,6 +118,11 @@ _GPU_SIGS = {
     "pico_gpt_num_params": (ctypes.c_int, [c_p]),
     "pico_gpt_param": (TP, [c_p, ctypes.c_int]),
     "pico_gpt_free": (None, [c_p]),
+    "pico_gpt_param_name": (ctypes.c_char_p, [c_p, ctypes.c_int]),
+    "pico_checkpoint_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),
+                                            ctypes.POINTER(ctypes.c_char_p), c_p]),
+    "pico_checkpoint_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),
+                                            ctypes.POINTER(ctypes.c_char_p), c_p]),
 }
 
 _amd = None
