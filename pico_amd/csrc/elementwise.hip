@@ -140,6 +140,8 @@ __global__ void binary_bwd_rows(int op, int which, int64_t R, int64_t C,
     for(int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; j < C;
         j += (int64_t)gridDim.x * blockDim.x) {
         float acc = accum ? gx[j] : 0.0f;
+        // the adds stay in row order; unrolling lets the loads run ahead of them
+#pragma unroll 8
         for(int64_t r = 0; r < R; ++r)
             acc = grad_add(op, which, acc, gout[r * C + j], op == 2 ? other[r * C + j] : 0.0f);
         gx[j] = acc;

@@ -29,11 +29,12 @@
 //    stores + 16 loads per slice cost 13 % of the MFMA rate).  One barrier per
 //    slice sits before group 3, so group 0 of the next slice is read under
 //    group 3's MFMAs.
-//  * LDS keeps each operand in its global orientation (no transposes on the
-//    store).  Within a 32-wide k slice, lanes 0-31 take k 0..15 and lanes
-//    32-63 take k 16..31, so a k-contiguous tile is read with 128-bit LDS loads
-//    and a row-contiguous tile with conflict-free 32-bit loads.  Row strides
-//    are padded by 4 floats.
+//  * LDS holds every operand k-contiguous, [rows][32 + 4 pad]: an operand that
+//    is row-contiguous in memory is fetched as 4 x 4 blocks and transposed in
+//    registers on its way to LDS.  Within a 32-wide k slice, lanes 0-31 take
+//    k 0..15 and lanes 32-63 take k 16..31, so every fragment read is a 128-bit
+//    LDS load, for all four layouts (measured: paired 32-bit reads of a
+//    row-contiguous tile held NN and TN 5 % below NT).
 //  * Tile order is XCD-aware: the hardware deals consecutive workgroups to
 //    the 8 XCDs round-robin, so the launch index is remapped to give each XCD
 //    a contiguous run of tiles, walked in groups of 8 tile-rows so concurrently
@@ -52,14 +53,26 @@ constexpr int BK = 32, NT = 256;
 constexpr int KF = BK + 4;  // row stride of a k-contiguous LDS tile [rows][36]
 constexpr int GROUP_M = 8;
 
-// An R x BK operand slice: float4 per thread, the row stride of its
-// row-contiguous LDS form [BK][R+4], and the LDS floats it needs.
-template <int R>
-struct Slice {
-    static constexpr int V = R * BK / 4 / NT;
-    static constexpr int Q4 = R / 4;  // float4 per k-row of the row-contiguous form
-    static constexpr int RF = R + 4;
-    static constexpr int FLOATS = R * KF > BK * RF ? R * KF : BK * RF;
+// One operand's R x BK slice, staged into a k-contiguous LDS tile [R][KF].
+//  * k-contiguous in memory (KFAST: op(A) when A is not transposed, op(B)^T
+//    when B is): each staging item is one float4 of 4 consecutive k in a row;
+//    R/32 items per thread.
+//  * row-contiguous in memory: each item is a 4 x 4 block -- 4 consecutive
+//    rows at 4 consecutive k, fetched as 4 float4 along the rows and
+//    transposed in registers -- so LDS holds the same k-contiguous form and
+//    every fragment read is a 128-bit load.  The slice has 2R such blocks:
+//    one per thread (two at R = 256; at R = 96 some threads repeat one; at
+//    R = 64 the blocks are 4 rows x 2 k, one per thread).
+template <bool KFAST, int R>
+struct Operand {
+    // k depth of a transposed block: 4, or 2 for R = 64, where 4 x 2 blocks
+    // give exactly one block per thread
+    static constexpr int KD = R == 64 ? 2 : 4;
+    static constexpr int BLOCKS = (R / 4) * (BK / KD);  // blocks of a row-contiguous slice
+    static constexpr int ITEMS = KFAST ? R * BK / 4 / NT : (BLOCKS + NT - 1) / NT;
+    static constexpr int ITEM_F4 = KFAST ? 1 : KD;  // float4 per item
+    static constexpr int F4 = ITEMS * ITEM_F4;       // float4 registers per thread
+    static constexpr int FLOATS = R * KF;            // LDS floats of one stage
 };
 
 // A tile shape: WGM x (4 / WGM) waves, each TM x TN blocks of 32 x 32.
@@ -93,31 +106,25 @@ struct GemmParams {
 // aligned operands: a float4 is wholly inside or wholly outside), or per element.
 constexpr int kEdgeNone = 0, kEdgeVec = 1, kEdgeScalar = 2;
 
-// Element i (0 <= i < Slice<R>::V) of this thread's share of an R x 32 operand
-// slice.  KFAST: element (r,k) at base[r*ld + k]; otherwise at base[k*ld + r].
-// Edge modes zero-fill outside [Rlim) x [K).
-template <bool KFAST, int EDGE, int R>
-__device__ __forceinline__ f32x4 load_one(const float* __restrict__ base, int64_t ld, int64_t r0,
-                                          int64_t k0, int64_t Rlim, int64_t K, int i) {
-    const int idx = threadIdx.x + i * NT;
-    int rr, kk;
-    if(KFAST) {
-        rr = idx >> 3;
-        kk = (idx & 7) * 4;
-    } else {
-        kk = idx / Slice<R>::Q4;
-        rr = (idx % Slice<R>::Q4) * 4;
-    }
-    const int64_t r = r0 + rr, k = k0 + kk;
+// The float4 at logical (row r, k) of an operand: 4 consecutive k when
+// KFAST (element (r,k) at base[r*ld + k]), else 4 consecutive rows (element
+// (r,k) at base[k*ld + r]).  Edge modes zero-fill outside [Rlim) x [K).
+template <bool KFAST, int EDGE>
+__device__ __forceinline__ f32x4 load_f4(const float* __restrict__ base, int64_t ld, int64_t r,
+                                         int64_t k, int64_t Rlim, int64_t K) {
     if(EDGE == kEdgeNone) {
         const float* p = KFAST ? base + r * ld + k : base + k * ld + r;
         return *reinterpret_cast<const f32x4*>(p);
     }
     f32x4 x = {0.f, 0.f, 0.f, 0.f};
     if(EDGE == kEdgeVec) {
-        if(r < Rlim && k < K)
-            x = *reinterpret_cast<const f32x4*>(KFAST ? base + r * ld + k : base + k * ld + r);
-        return x;
+        // load from element (0, 0) when outside and select zero: no branch
+        // splits the main loop (the launcher guarantees M, N, K > 0 here)
+        const bool in = r < Rlim && k < K;
+        const int64_t rs = in ? r : 0, ks = in ? k : 0;
+        const f32x4 y =
+            *reinterpret_cast<const f32x4*>(KFAST ? base + rs * ld + ks : base + ks * ld + rs);
+        return in ? y : x;
     }
     if(KFAST) {
         if(r < Rlim) {
@@ -137,34 +144,79 @@ __device__ __forceinline__ f32x4 load_one(const float* __restrict__ base, int64_
     return x;
 }
 
+// staging item `item` of this thread: the (row, k) origin of its float4 or
+// block.  A row-contiguous slice has 2R blocks; when that is not a multiple
+// of the thread count (R = 96, 64) the remaining threads repeat blocks from
+// the start: they load the same data and store the same values to the same
+// LDS addresses, which keeps the loop free of branches.
 template <bool KFAST, int R>
-__device__ __forceinline__ void store_one(float* lds, int i, f32x4 v) {
-    const int idx = threadIdx.x + i * NT;
-    if(KFAST)
-        *reinterpret_cast<f32x4*>(lds + (idx >> 3) * KF + (idx & 7) * 4) = v;
-    else
-        *reinterpret_cast<f32x4*>(lds + (idx / Slice<R>::Q4) * Slice<R>::RF +
-                                  (idx % Slice<R>::Q4) * 4) = v;
+__device__ __forceinline__ void item_origin(int item, int& rr, int& kk) {
+    if(KFAST) {
+        const int u = threadIdx.x + item * NT;
+        rr = u >> 3;
+        kk = (u & 7) * 4;
+    } else {
+        // consecutive threads take consecutive k of one 4-row block: their
+        // LDS stores fill 128 contiguous bytes of a row, and each load row
+        // is read in 128-byte (KD = 4) or 64-byte (KD = 2) pieces
+        constexpr int KD = Operand<false, R>::KD, KQ = BK / KD;
+        const int u = (threadIdx.x + item * NT) % Operand<false, R>::BLOCKS;
+        rr = (u / KQ) * 4;
+        kk = (u % KQ) * KD;
+    }
+}
+
+template <bool KFAST, int EDGE, int R>
+__device__ __forceinline__ void load_item(const float* __restrict__ base, int64_t ld, int64_t r0,
+                                          int64_t k0, int64_t Rlim, int64_t K, int item,
+                                          f32x4* v) {
+    int rr, kk;
+    item_origin<KFAST, R>(item, rr, kk);
+    if(KFAST) {
+        v[0] = load_f4<true, EDGE>(base, ld, r0 + rr, k0 + kk, Rlim, K);
+    } else {
+#pragma unroll
+        for(int t = 0; t < Operand<false, R>::KD; ++t)
+            v[t] = load_f4<false, EDGE>(base, ld, r0 + rr, k0 + kk + t, Rlim, K);
+    }
+}
+
+template <bool KFAST, int R>
+__device__ __forceinline__ void store_item(float* lds, int item, const f32x4* v) {
+    int rr, kk;
+    item_origin<KFAST, R>(item, rr, kk);
+    if(KFAST) {
+        *reinterpret_cast<f32x4*>(lds + rr * KF + kk) = v[0];
+    } else if(Operand<false, R>::KD == 4) {
+        // v[t] holds rows rr..rr+3 at k = kk + t: row j of the block is {v[t][j]}
+#pragma unroll
+        for(int j = 0; j < 4; ++j) {
+            const f32x4 w = {v[0][j], v[1][j], v[2][j], v[3][j]};
+            *reinterpret_cast<f32x4*>(lds + (rr + j) * KF + kk) = w;
+        }
+    } else {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for(int j = 0; j < 4; ++j) {
+            const f32x2 w = {v[0][j], v[1][j]};
+            *reinterpret_cast<f32x2*>(lds + (rr + j) * KF + kk) = w;
+        }
+    }
 }
 
 // k-group q (k = 4q..4q+3 for lanes 0-31, 16+4q.. for lanes 32-63) of the
-// fragments of NB blocks starting at LDS row r0 (one row per lane).
-template <bool KFAST, int R, int NB>
+// fragments of NB blocks starting at LDS row r0 (one row per lane)
+template <int NB>
 __device__ __forceinline__ void read_group(const float* lds, int r0, int lr, int lh, int q,
                                            float (&f)[NB][4]) {
 #pragma unroll
     for(int b = 0; b < NB; ++b) {
-        const int r = r0 + b * 32 + lr;
-        if(KFAST) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(lds + r * KF + lh * 16 + 4 * q);
-            f[b][0] = x[0];
-            f[b][1] = x[1];
-            f[b][2] = x[2];
-            f[b][3] = x[3];
-        } else {
-#pragma unroll
-            for(int t = 0; t < 4; ++t) f[b][t] = lds[(lh * 16 + 4 * q + t) * Slice<R>::RF + r];
-        }
+        const f32x4 x =
+            *reinterpret_cast<const f32x4*>(lds + (r0 + b * 32 + lr) * KF + lh * 16 + 4 * q);
+        f[b][0] = x[0];
+        f[b][1] = x[1];
+        f[b][2] = x[2];
+        f[b][3] = x[3];
     }
 }
 
@@ -195,43 +247,66 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-// Staging of the next operand slice, spread over k-groups 0..2: group g moves
-// elements [lo(g), lo(g+1)) of the VA + VB float4 this thread holds (A's
-// first) from registers to LDS, then refetches them from k0.
-template <int TOT>
-constexpr int stage_lo(int g) {
-    return g >= 3 ? TOT : (g * TOT + 2) / 3;
-}
+// Staging of the next operand slice, spread over k-groups 0..2: the items
+// of A then B, split where the memory instructions (a store and a load per
+// float4) divide most evenly in three.  Each item is stored from registers to
+// LDS, then refetched from k slice kn.
+template <bool AK, bool BKF, class T>
+struct Staging {
+    using OA = Operand<AK, T::BM>;
+    using OB = Operand<BKF, T::BN>;
+    static constexpr int ITEMS = OA::ITEMS + OB::ITEMS;
+    static constexpr int ops(int item) { return 2 * (item < OA::ITEMS ? OA::ITEM_F4 : OB::ITEM_F4); }
+    static constexpr int ops_before(int item) {
+        int n = 0;
+        for(int i = 0; i < item; ++i) n += ops(i);
+        return n;
+    }
+    // first item of group g: the first whose preceding ops reach g/3 of the total
+    static constexpr int lo(int g) {
+        if(g >= 3) return ITEMS;
+        int i = 0;
+        while(i < ITEMS && 3 * ops_before(i) < g * ops_before(ITEMS)) ++i;
+        return i;
+    }
+    static constexpr int group_ops(int g) { return ops_before(lo(g + 1)) - ops_before(lo(g)); }
+};
 
-template <bool AK, bool BKF, int EDGE, class T, int G>
-__device__ __forceinline__ void stage(f32x4 (&ra)[Slice<T::BM>::V], f32x4 (&rb)[Slice<T::BN>::V],
-                                      float* sa, float* sb, const float* __restrict__ A,
-                                      const float* __restrict__ B, const GemmParams& p,
-                                      int64_t row0, int64_t col0, int64_t kn, int64_t kend) {
-    constexpr int VA = Slice<T::BM>::V, VB = Slice<T::BN>::V, TOT = VA + VB;
-    constexpr int lo = stage_lo<TOT>(G), hi = stage_lo<TOT>(G + 1);
+template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB>
+__device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], float* sa, float* sb,
+                                      const float* __restrict__ A, const float* __restrict__ B,
+                                      const GemmParams& p, int64_t row0, int64_t col0, int64_t kn,
+                                      int64_t kend) {
+    using S = Staging<AK, BKF, T>;
+    constexpr int IA = S::OA::ITEMS, FA = S::OA::ITEM_F4, FB = S::OB::ITEM_F4;
+    constexpr int lo = S::lo(G), hi = S::lo(G + 1);
 #pragma unroll
     for(int e = lo; e < hi; ++e) {
-        if(e < VA)
-            store_one<AK, T::BM>(sa, e, ra[e]);
+        if(e < IA)
+            store_item<AK, T::BM>(sa, e, &ra[e * FA]);
         else
-            store_one<BKF, T::BN>(sb, e - VA, rb[e - VA]);
+            store_item<BKF, T::BN>(sb, e - IA, &rb[(e - IA) * FB]);
     }
 #pragma unroll
     for(int e = lo; e < hi; ++e) {
-        if(e < VA)
-            ra[e] = load_one<AK, EDGE, T::BM>(A, p.lda, row0, kn, p.M, kend, e);
+        if(e < IA)
+            load_item<AK, EDGE, T::BM>(A, p.lda, row0, kn, p.M, kend, e, &ra[e * FA]);
         else
-            rb[e - VA] = load_one<BKF, EDGE, T::BN>(B, p.ldb, col0, kn, p.N, kend, e - VA);
+            load_item<BKF, EDGE, T::BN>(B, p.ldb, col0, kn, p.N, kend, e - IA, &rb[(e - IA) * FB]);
     }
 }
 
 template <bool TA, bool TB, int EDGE, class T>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
-    constexpr int VA = Slice<BM>::V, VB = Slice<BN>::V, TOT = VA + VB;
-    __shared__ __attribute__((aligned(16))) float ldsA[2][Slice<BM>::FLOATS];
-    __shared__ __attribute__((aligned(16))) float ldsB[2][Slice<BN>::FLOATS];
+    // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
+    // (indexed by n) are k-contiguous when B is transposed.
+    constexpr bool AK = !TA, BKF = TB;
+    using OA = Operand<AK, BM>;
+    using OB = Operand<BKF, BN>;
+    using S = Staging<AK, BKF, T>;
+    __shared__ __attribute__((aligned(16))) float ldsA[2][OA::FLOATS];
+    __shared__ __attribute__((aligned(16))) float ldsB[2][OB::FLOATS];
 
     // ---- tile selection: XCD-contiguous runs, grouped by GROUP_M tile-rows
     const int ntiles = p.tiles_m * p.tiles_n;
@@ -282,37 +357,36 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
 #pragma unroll
             for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
-    // (indexed by n) are k-contiguous when B is transposed.
-    constexpr bool AK = !TA, BKF = TB;
-    // LDS reads per k-group: one 128-bit load per k-contiguous block, two
-    // paired 32-bit loads per row-contiguous block
-    constexpr int RD = (AK ? TM : 2 * TM) + (BKF ? TN : 2 * TN);
+    constexpr int RD = TM + TN;  // 128-bit LDS reads per k-group
     constexpr int NMFMA = TM * TN * 4;
 
     if(nslices > 0) {
-        f32x4 ra[VA], rb[VB];
+        f32x4 ra[OA::F4], rb[OB::F4];
         // prologue: slice 0 into LDS buffer 0, slice 1 into registers
 #pragma unroll
-        for(int e = 0; e < VA; ++e) ra[e] = load_one<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, e);
+        for(int e = 0; e < OA::ITEMS; ++e)
+            load_item<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
-        for(int e = 0; e < VB; ++e) rb[e] = load_one<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, e);
+        for(int e = 0; e < OB::ITEMS; ++e)
+            load_item<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, e, &rb[e * OB::ITEM_F4]);
 #pragma unroll
-        for(int e = 0; e < VA; ++e) store_one<AK, BM>(ldsA[0], e, ra[e]);
+        for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, BM>(ldsA[0], e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
-        for(int e = 0; e < VB; ++e) store_one<BKF, BN>(ldsB[0], e, rb[e]);
+        for(int e = 0; e < OB::ITEMS; ++e) store_item<BKF, BN>(ldsB[0], e, &rb[e * OB::ITEM_F4]);
         {
             const int64_t k1 = kbeg + (nslices > 1 ? BK : 0);
 #pragma unroll
-            for(int e = 0; e < VA; ++e) ra[e] = load_one<AK, EDGE, BM>(A, p.lda, row0, k1, p.M, kend, e);
+            for(int e = 0; e < OA::ITEMS; ++e)
+                load_item<AK, EDGE, BM>(A, p.lda, row0, k1, p.M, kend, e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
-            for(int e = 0; e < VB; ++e) rb[e] = load_one<BKF, EDGE, BN>(B, p.ldb, col0, k1, p.N, kend, e);
+            for(int e = 0; e < OB::ITEMS; ++e)
+                load_item<BKF, EDGE, BN>(B, p.ldb, col0, k1, p.N, kend, e, &rb[e * OB::ITEM_F4]);
         }
         __syncthreads();
 
         float fa0[TM][4], fb0[TN][4], fa1[TM][4], fb1[TN][4];
-        read_group<AK, BM, TM>(ldsA[0], ar0, lr, lh, 0, fa0);
-        read_group<BKF, BN, TN>(ldsB[0], br0, lr, lh, 0, fb0);
+        read_group<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
+        read_group<TN>(ldsB[0], br0, lr, lh, 0, fb0);
         for(int s = 0; s < nslices; ++s) {
             const int cur = s & 1;
             const float* la = ldsA[cur];
@@ -324,32 +398,32 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
             const int64_t kn = kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
 
             // group 0: read group 1, stage part 0
-            read_group<AK, BM, TM>(la, ar0, lr, lh, 1, fa1);
-            read_group<BKF, BN, TN>(lb, br0, lr, lh, 1, fb1);
+            read_group<TM>(la, ar0, lr, lh, 1, fa1);
+            read_group<TN>(lb, br0, lr, lh, 1, fb1);
             stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
-            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(1) - stage_lo<TOT>(0))>();
+            interleave<NMFMA, RD + S::group_ops(0)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 1: read group 2, stage part 1
-            read_group<AK, BM, TM>(la, ar0, lr, lh, 2, fa0);
-            read_group<BKF, BN, TN>(lb, br0, lr, lh, 2, fb0);
+            read_group<TM>(la, ar0, lr, lh, 2, fa0);
+            read_group<TN>(lb, br0, lr, lh, 2, fb0);
             stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa1, fb1);
-            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(2) - stage_lo<TOT>(1))>();
+            interleave<NMFMA, RD + S::group_ops(1)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 2: read group 3, stage part 2
-            read_group<AK, BM, TM>(la, ar0, lr, lh, 3, fa1);
-            read_group<BKF, BN, TN>(lb, br0, lr, lh, 3, fb1);
+            read_group<TM>(la, ar0, lr, lh, 3, fa1);
+            read_group<TN>(lb, br0, lr, lh, 3, fb1);
             stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
-            interleave<NMFMA, RD + 2 * (stage_lo<TOT>(3) - stage_lo<TOT>(2))>();
+            interleave<NMFMA, RD + S::group_ops(2)>();
             __builtin_amdgcn_sched_barrier(0);
             // every wave has staged slice s+1 and finished reading slice s
             __syncthreads();
             // group 3, with group 0 of slice s+1 read underneath (on the last
             // slice this reads the re-staged data and is discarded)
-            read_group<AK, BM, TM>(sa, ar0, lr, lh, 0, fa0);
-            read_group<BKF, BN, TN>(sb, br0, lr, lh, 0, fb0);
+            read_group<TM>(sa, ar0, lr, lh, 0, fa0);
+            read_group<TN>(sb, br0, lr, lh, 0, fb0);
             mfma_group<TM, TN>(acc, fa1, fb1);
             interleave<NMFMA, RD>();
             __builtin_amdgcn_sched_barrier(0);
@@ -404,16 +478,24 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
 }
 
 // K split for a product whose output has too few tiles to fill the chip: 2
-// resident workgroups per CU x 256 CUs want >= 512 workgroups; each slice keeps
-// at least 256 of K (8 LDS stages) so the pipeline stays long.
-constexpr int64_t kSplitTarget = 512, kMinSliceK = 256;
+// resident workgroups per CU x 256 CUs want >= 512 workgroups.
+//  * K >= 1024 (weight gradients: M, N ~ d_model, K = tokens): slices of at
+//    least 256 (8 LDS stages), 5-16 of them at the training shapes.
+//  * 512 <= K < 1024: only when even 64x64 tiles would leave three quarters
+//    of the CUs idle (the MLP's [64, 784] . [784, 128]: 2 tiles); slices of
+//    at least 128, which turns one latency-bound workgroup chain into six.
+//    Wider outputs take the 64x64 tiles instead.
+//  * K < 512: never.
+constexpr int64_t kSplitTarget = 512, kMinSplitK = 512;
 
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
     *kchunk = K;
-    if(tiles <= 0 || tiles * 2 > kSplitTarget || K < 4 * kMinSliceK) return 1;
+    if(tiles <= 0 || tiles * 2 > kSplitTarget || K < kMinSplitK) return 1;
+    if(K < 1024 && ((M + 63) / 64) * ((N + 63) / 64) * 4 >= 256) return 1;
+    const int64_t min_slice = K >= 1024 ? 256 : 128;
     int64_t s = kSplitTarget / tiles;
-    if(s > K / kMinSliceK) s = K / kMinSliceK;
+    if(s > K / min_slice) s = K / min_slice;
     if(s < 2) return 1;
     const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
     *kchunk = chunk;

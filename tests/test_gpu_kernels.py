@@ -99,12 +99,15 @@ def test_gemm_large_sampled_rows(dev, ta, tb, n):
 
 
 @pytest.mark.parametrize("ta,tb", [("T", "N"), ("N", "T"), ("N", "N")])
-@pytest.mark.parametrize("M,N,Kd", [(768, 768, 8192), (768, 2048, 8192), (200, 136, 4000),
-                                    (64, 10, 784)])
-def test_gemm_splitk(dev, ta, tb, M, N, Kd):
-    # weight-gradient shapes: K split into slices summed in a fixed order
+@pytest.mark.parametrize("M,N,Kd,split", [(768, 768, 8192, True), (768, 2048, 8192, True),
+                                          (200, 136, 4000, True), (64, 128, 784, True),
+                                          (64, 10, 256, False), (1024, 512, 768, False)])
+def test_gemm_splitk(dev, ta, tb, M, N, Kd, split):
+    # weight-gradient shapes and a tiny output with a long K: K split into
+    # slices summed in a fixed order; short K, or an output the 64 x 64 tiles
+    # already spread over the chip, stays unsplit
     need = K.gemm_workspace(M, N, Kd)
-    assert (need > 0) == (Kd >= 1024)  # short K (the MLP's 784) stays unsplit
+    assert (need > 0) == split
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
     K.gemm_ex(ta, tb, cu(As), cu(Bs), C)
