@@ -30,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_FP32_PEAK = 157.3e12
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 matrix peak (no sparsity)
 HBM_PEAK = 8.0e12
 
 
@@ -104,7 +105,8 @@ def gemm_section(args, torch, K):
     }
 
 
-def sweep_section(torch, K, sizes):
+def sweep_section(torch, K, sizes, gemm=None):
+    gemm = gemm or K.gemm
     dev = torch.device("cuda:0")
     out = {}
     for n in sizes:
@@ -115,7 +117,7 @@ def sweep_section(torch, K, sizes):
         reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
         row = {}
         for ta, tb in (("N", "N"), ("N", "T"), ("T", "N")):
-            mean_ms, _ = _events_time(lambda: K.gemm(ta, tb, A, B, C), reps, 2)
+            mean_ms, _ = _events_time(lambda: gemm(ta, tb, A, B, C), reps, 2)
             row[ta + tb] = round(2.0 * n ** 3 / (mean_ms * 1e-3) / 1e12, 2)
         out[str(n)] = row
         del A, B, C
@@ -307,8 +309,9 @@ def mlp_section(steps, warmup):
             "config": {"model": "MLP 784-128-10 ReLU", "batch": 64, "optimizer": "SGD lr 0.01"}}
 
 
-def train_section(name, steps, warmup):
-    """one AdamW training step of the transformer per step, inputs resident"""
+def train_section(name, steps, warmup, precision=0):
+    """one AdamW training step of the transformer per step, inputs resident;
+    precision 1 runs pico_matmul's products in bf16 (pico_set_matmul_precision)"""
     import numpy as np
 
     from pico_amd.pico import Pico
@@ -316,6 +319,8 @@ def train_section(name, steps, warmup):
     cfg = TRAIN_CONFIGS[name]
     P = Pico()
     lib = P.lib
+    if lib.pico_set_matmul_precision(precision):
+        raise RuntimeError("pico_set_matmul_precision failed")
     model = P.gpt_init(cfg, 20261201)
     n = cfg["batch"] * cfg["seq_len"]
     # synthetic token stream: inputs and next-token targets, uniform ids
@@ -363,13 +368,15 @@ def train_section(name, steps, warmup):
     lib.arena_destroy(data)
     lib.pico_optim_adamw_free(opt)
     lib.pico_gpt_free(model)
+    lib.pico_set_matmul_precision(0)
     if err:
         raise RuntimeError(err)
     flop = train_flop_per_step(cfg)
     ms = wall * 1e3 / steps
     return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
             "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
-            "mfu": round(flop / (ms * 1e-3) / MFMA_FP32_PEAK, 4),
+            "mfu": round(flop / (ms * 1e-3) / (MFMA_BF16_PEAK if precision else MFMA_FP32_PEAK), 4),
+            "mfu_peak": "bf16 2.5 PFLOP/s" if precision else "fp32 157.3 TFLOP/s",
             "graph_ms_per_step": round(graph_ms, 3),
             "graph_tokens_per_s": round(n / (graph_ms * 1e-3), 1),
             "tokens_per_step": n, "steps": steps, "warmup": warmup,
@@ -422,7 +429,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4096)
-    ap.add_argument("--sections", default="train,sweep,rows,cpu")
+    ap.add_argument("--sections", default="train,sweep,bf16,rows,cpu")
     ap.add_argument("--train-steps", type=int, default=10)
     ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
     args = ap.parse_args()
@@ -482,6 +489,16 @@ def main():
                 line["train"][name] = train_section(name, args.train_steps, 3)
     if "sweep" in sections:
         line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
+    if "bf16" in sections:
+        # outside the fp32 parity contract: bf16 multiplies, fp32 accumulation,
+        # fp32 tensors (pk_gemm_bf16_f32 / pico_set_matmul_precision)
+        line["bf16"] = {
+            "sweep": sweep_section(torch, K, [1024, 2048, 4096, 8192], K.gemm_bf16),
+            "train": {name: train_section(name, args.train_steps, 3, precision=1)
+                      for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
+            "peak_tflops": MFMA_BF16_PEAK / 1e12,
+            "note": "bf16 products of fp32 operands (rounded to nearest even), fp32 "
+                    "accumulation; not the headline, which is fp32"}
     if "rows" in sections:
         line["row_kernels"] = rows_section(torch, K)
     if "cpu" in sections:

@@ -250,6 +250,19 @@ const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
 void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
 
+/* ---- matmul precision (no reference counterpart: pico is fp32 only) ----
+ * PICO_MATMUL_FP32 (the default): pico_matmul and its gradients multiply in
+ * fp32 on the fp32 matrix cores, within the fp32 parity contract.
+ * PICO_MATMUL_BF16: operands are rounded to bf16 (nearest even) and multiplied
+ * on the bf16 matrix cores, accumulating in fp32; tensors stay fp32.  Faster,
+ * and outside the fp32 parity contract (relative error of order 2^-8 per
+ * operand).  Attention and the other ops are unaffected.  Returns 0, or
+ * nonzero for an unknown value. */
+#define PICO_MATMUL_FP32 0
+#define PICO_MATMUL_BF16 1
+int pico_set_matmul_precision(int precision);
+int pico_get_matmul_precision(void);
+
 /* ---- checkpoints (no reference counterpart: the reference's params are plain
  * float arrays, src/tensor.h:14-15, and nothing is ever saved) ----
  * A safetensors file: 8-byte little-endian header length, a JSON header mapping

@@ -64,6 +64,20 @@ int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alph
                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                    void* workspace, size_t workspace_bytes, pk_stream_t stream);
 
+/* The same products with bf16 multiplies (no reference counterpart: pico is
+ * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
+ * multiplied on the bf16 matrix cores, accumulating in fp32; C and the
+ * workspace contract are as in pk_gemm_f32 / pk_gemm_ex_f32.  Each product
+ * of two bf16 values is exact in fp32, so the result equals the fp32 product
+ * of the rounded operands up to fp32 summation error. */
+int pk_gemm_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                     float* C, int64_t ldc, pk_stream_t stream);
+int pk_gemm_ex_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                        const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                        float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                        pk_stream_t stream);
+
 /* Batched form: batch index z = outer*inner_count + inner; operand X of batch z
  * starts at X + outer*sX_outer + inner*sX_inner.  'causal' restricts work for
  * attention-shaped products (no reference counterpart: pico's matmul is 2-D

@@ -181,25 +181,51 @@ __device__ __forceinline__ void load_item(const float* __restrict__ base, int64_
     }
 }
 
-template <bool KFAST, int R>
-__device__ __forceinline__ void store_item(float* lds, int item, const f32x4* v) {
+// Row stride (elements) of a k-contiguous LDS tile: fp32 [rows][36]; bf16
+// [rows][40] (80 bytes: the 16-lane passes of 128-bit reads down a column of
+// rows touch 16 distinct 4-bank groups).
+constexpr int KFB = BK + 8;
+template <class E>
+constexpr int lds_stride() {
+    return sizeof(E) == 4 ? KF : KFB;
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// store 4 consecutive k of one row; a bf16 tile gets them rounded to nearest even
+template <class E>
+__device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
+    if constexpr(sizeof(E) == 4) {
+        *reinterpret_cast<f32x4*>(lds + off) = w;
+    } else {
+        const bf16x4 b = {(__bf16)w[0], (__bf16)w[1], (__bf16)w[2], (__bf16)w[3]};
+        *reinterpret_cast<bf16x4*>(lds + off) = b;
+    }
+}
+
+template <bool KFAST, int R, class E>
+__device__ __forceinline__ void store_item(E* lds, int item, const f32x4* v) {
+    constexpr int LS = lds_stride<E>();
     int rr, kk;
     item_origin<KFAST, R>(item, rr, kk);
     if(KFAST) {
-        *reinterpret_cast<f32x4*>(lds + rr * KF + kk) = v[0];
+        put4(lds, rr * LS + kk, v[0]);
     } else if(Operand<false, R>::KD == 4) {
         // v[t] holds rows rr..rr+3 at k = kk + t: row j of the block is {v[t][j]}
 #pragma unroll
-        for(int j = 0; j < 4; ++j) {
-            const f32x4 w = {v[0][j], v[1][j], v[2][j], v[3][j]};
-            *reinterpret_cast<f32x4*>(lds + (rr + j) * KF + kk) = w;
-        }
+        for(int j = 0; j < 4; ++j) put4(lds, (rr + j) * LS + kk, f32x4{v[0][j], v[1][j], v[2][j], v[3][j]});
     } else {
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for(int j = 0; j < 4; ++j) {
-            const f32x2 w = {v[0][j], v[1][j]};
-            *reinterpret_cast<f32x2*>(lds + (rr + j) * KF + kk) = w;
+            if constexpr(sizeof(E) == 4) {
+                typedef float f32x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<f32x2*>(lds + (rr + j) * LS + kk) = f32x2{v[0][j], v[1][j]};
+            } else {
+                *reinterpret_cast<bf16x2*>(lds + (rr + j) * LS + kk) =
+                    bf16x2{(__bf16)v[0][j], (__bf16)v[1][j]};
+            }
         }
     }
 }
@@ -272,8 +298,8 @@ struct Staging {
     static constexpr int group_ops(int g) { return ops_before(lo(g + 1)) - ops_before(lo(g)); }
 };
 
-template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB>
-__device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], float* sa, float* sb,
+template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB, class E>
+__device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], E* sa, E* sb,
                                       const float* __restrict__ A, const float* __restrict__ B,
                                       const GemmParams& p, int64_t row0, int64_t col0, int64_t kn,
                                       int64_t kend) {
@@ -296,19 +322,21 @@ __device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], float* s
     }
 }
 
-template <bool TA, bool TB, int EDGE, class T>
-__global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
-    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
-    // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
-    // (indexed by n) are k-contiguous when B is transposed.
-    constexpr bool AK = !TA, BKF = TB;
-    using OA = Operand<AK, BM>;
-    using OB = Operand<BKF, BN>;
-    using S = Staging<AK, BKF, T>;
-    __shared__ __attribute__((aligned(16))) float ldsA[2][OA::FLOATS];
-    __shared__ __attribute__((aligned(16))) float ldsB[2][OB::FLOATS];
+// One workgroup's job: its tile, operand bases, output, K range.
+struct TileJob {
+    const float* A;
+    const float* B;
+    float* C;
+    int64_t ldc, row0, col0, kbeg, kend;
+    float alpha, beta;
+    int nslices;
+    bool skip;
+};
 
-    // ---- tile selection: XCD-contiguous runs, grouped by GROUP_M tile-rows
+template <class T>
+__device__ __forceinline__ TileJob tile_job(const GemmParams& p) {
+    TileJob j;
+    // tile selection: XCD-contiguous runs, grouped by GROUP_M tile-rows
     const int ntiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
     if((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
@@ -322,27 +350,100 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     // blockIdx.y is the batch index, or the K slice of a split product
     const int64_t z = p.splits > 1 ? 0 : blockIdx.y;
     const int64_t zo = z / p.inner, zi = z % p.inner;
-    const float* __restrict__ A = p.A + zo * p.sAo + zi * p.sAi;
-    const float* __restrict__ B = p.B + zo * p.sBo + zi * p.sBi;
-    float* __restrict__ C = p.C + zo * p.sCo + zi * p.sCi;
-    int64_t ldc = p.ldc;
-    float alpha = p.alpha, beta = p.beta;
+    j.A = p.A + zo * p.sAo + zi * p.sAi;
+    j.B = p.B + zo * p.sBo + zi * p.sBi;
+    j.C = p.C + zo * p.sCo + zi * p.sCi;
+    j.ldc = p.ldc;
+    j.alpha = p.alpha;
+    j.beta = p.beta;
 
-    const int64_t row0 = (int64_t)tm * BM, col0 = (int64_t)tn * BN;
-    int64_t kbeg = 0, kend = p.K;
-    if(p.causal == 1 && col0 > row0 + BM - 1) return;  // wholly above the diagonal
-    if(p.causal == 2) kend = min(p.K, row0 + BM);
-    if(p.causal == 3) kbeg = min(p.K, (row0 / BK) * BK);
+    j.row0 = (int64_t)tm * T::BM;
+    j.col0 = (int64_t)tn * T::BN;
+    j.kbeg = 0;
+    j.kend = p.K;
+    j.skip = p.causal == 1 && j.col0 > j.row0 + T::BM - 1;  // wholly above the diagonal
+    if(p.causal == 2) j.kend = min(p.K, j.row0 + T::BM);
+    if(p.causal == 3) j.kbeg = min(p.K, (j.row0 / BK) * BK);
     if(p.splits > 1) {
         // slice s of K; its partial product goes to workspace plane s
-        kbeg = (int64_t)blockIdx.y * p.kchunk;
-        kend = min(p.K, kbeg + p.kchunk);
-        C = p.ws + (int64_t)blockIdx.y * p.M * p.N;
-        ldc = p.N;
-        alpha = 1.0f;
-        beta = 0.0f;
+        j.kbeg = (int64_t)blockIdx.y * p.kchunk;
+        j.kend = min(p.K, j.kbeg + p.kchunk);
+        j.C = p.ws + (int64_t)blockIdx.y * p.M * p.N;
+        j.ldc = p.N;
+        j.alpha = 1.0f;
+        j.beta = 0.0f;
     }
-    const int nslices = (int)((kend - kbeg + BK - 1) / BK);
+    j.nslices = (int)((j.kend - j.kbeg + BK - 1) / BK);
+    return j;
+}
+
+// C tile = alpha * acc (+ beta * C).  32x32 block accumulator r of lane l is
+// row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+template <int EDGE, int TM, int TN>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j,
+                                           const f32x16 (&acc)[TM][TN], int ar0, int br0, int lr,
+                                           int lh) {
+#pragma unroll
+    for(int i = 0; i < TM; ++i)
+#pragma unroll
+        for(int jj = 0; jj < TN; ++jj) {
+            const int64_t col = j.col0 + br0 + jj * 32 + lr;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                const int64_t row = j.row0 + ar0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                if(EDGE != kEdgeNone && (row >= p.M || col >= p.N)) continue;
+                float v = j.alpha * acc[i][jj][r];
+                float* c = j.C + row * j.ldc + col;
+                if(j.beta != 0.0f) v += j.beta * *c;
+                *c = v;
+            }
+        }
+}
+
+// prologue shared by both kernels: slice 0 into LDS buffer 0, slice 1 into
+// the staging registers
+template <bool AK, bool BKF, int EDGE, class T, int NA, int NB, class E>
+__device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, f32x4 (&ra)[NA],
+                                         f32x4 (&rb)[NB], E* sa, E* sb) {
+    using OA = Operand<AK, T::BM>;
+    using OB = Operand<BKF, T::BN>;
+#pragma unroll
+    for(int e = 0; e < OA::ITEMS; ++e)
+        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, j.kbeg, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
+#pragma unroll
+    for(int e = 0; e < OB::ITEMS; ++e)
+        load_item<BKF, EDGE, T::BN>(j.B, p.ldb, j.col0, j.kbeg, p.N, j.kend, e, &rb[e * OB::ITEM_F4]);
+#pragma unroll
+    for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, T::BM>(sa, e, &ra[e * OA::ITEM_F4]);
+#pragma unroll
+    for(int e = 0; e < OB::ITEMS; ++e) store_item<BKF, T::BN>(sb, e, &rb[e * OB::ITEM_F4]);
+    const int64_t k1 = j.kbeg + (j.nslices > 1 ? BK : 0);
+#pragma unroll
+    for(int e = 0; e < OA::ITEMS; ++e)
+        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, k1, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
+#pragma unroll
+    for(int e = 0; e < OB::ITEMS; ++e)
+        load_item<BKF, EDGE, T::BN>(j.B, p.ldb, j.col0, k1, p.N, j.kend, e, &rb[e * OB::ITEM_F4]);
+}
+
+template <bool TA, bool TB, int EDGE, class T>
+__global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
+    // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
+    // (indexed by n) are k-contiguous when B is transposed.
+    constexpr bool AK = !TA, BKF = TB;
+    using OA = Operand<AK, BM>;
+    using OB = Operand<BKF, BN>;
+    using S = Staging<AK, BKF, T>;
+    __shared__ __attribute__((aligned(16))) float ldsA[2][OA::FLOATS];
+    __shared__ __attribute__((aligned(16))) float ldsB[2][OB::FLOATS];
+
+    const TileJob job = tile_job<T>(p);
+    if(job.skip) return;
+    const float* __restrict__ A = job.A;
+    const float* __restrict__ B = job.B;
+    const int64_t row0 = job.row0, col0 = job.col0, kbeg = job.kbeg, kend = job.kend;
+    const int nslices = job.nslices;
 
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
     const int wm = w / WGN, wn = w % WGN;
@@ -362,28 +463,8 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
 
     if(nslices > 0) {
         f32x4 ra[OA::F4], rb[OB::F4];
-        // prologue: slice 0 into LDS buffer 0, slice 1 into registers
-#pragma unroll
-        for(int e = 0; e < OA::ITEMS; ++e)
-            load_item<AK, EDGE, BM>(A, p.lda, row0, kbeg, p.M, kend, e, &ra[e * OA::ITEM_F4]);
-#pragma unroll
-        for(int e = 0; e < OB::ITEMS; ++e)
-            load_item<BKF, EDGE, BN>(B, p.ldb, col0, kbeg, p.N, kend, e, &rb[e * OB::ITEM_F4]);
-#pragma unroll
-        for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, BM>(ldsA[0], e, &ra[e * OA::ITEM_F4]);
-#pragma unroll
-        for(int e = 0; e < OB::ITEMS; ++e) store_item<BKF, BN>(ldsB[0], e, &rb[e * OB::ITEM_F4]);
-        {
-            const int64_t k1 = kbeg + (nslices > 1 ? BK : 0);
-#pragma unroll
-            for(int e = 0; e < OA::ITEMS; ++e)
-                load_item<AK, EDGE, BM>(A, p.lda, row0, k1, p.M, kend, e, &ra[e * OA::ITEM_F4]);
-#pragma unroll
-            for(int e = 0; e < OB::ITEMS; ++e)
-                load_item<BKF, EDGE, BN>(B, p.ldb, col0, k1, p.N, kend, e, &rb[e * OB::ITEM_F4]);
-        }
+        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, ldsA[0], ldsB[0]);
         __syncthreads();
-
         float fa0[TM][4], fb0[TN][4], fa1[TM][4], fb1[TN][4];
         read_group<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
         read_group<TN>(ldsB[0], br0, lr, lh, 0, fb0);
@@ -429,24 +510,99 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+}
 
-    // ---- epilogue: 32x32 block accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-    // column l%32
+// The same product with bf16 multiplies: op(A) and op(B) are rounded to bf16
+// (nearest even) on their way to LDS and multiplied by
+// v_mfma_f32_32x32x16_bf16 (32768 FLOP per instruction, eight times the fp32
+// rate), accumulating in fp32.  Global traffic, staging, tiles and split-K
+// are the fp32 kernel's; a 32-wide k slice is two MFMA steps of k 16, the
+// second step's fragments read under the first step's MFMAs and the next
+// slice's first fragments under the second.  A lane's 8 k of a step are k
+// 16t + 8*(lane/32) .. +7, the same for both operands.
+template <int NB>
+__device__ __forceinline__ void read_step(const __bf16* lds, int r0, int lr, int lh, int t,
+                                          bf16x8 (&f)[NB]) {
+#pragma unroll
+    for(int b = 0; b < NB; ++b)
+        f[b] = *reinterpret_cast<const bf16x8*>(lds + (r0 + b * 32 + lr) * KFB + 16 * t + 8 * lh);
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&fa)[TM],
+                                          const bf16x8 (&fb)[TN]) {
 #pragma unroll
     for(int i = 0; i < TM; ++i)
 #pragma unroll
-        for(int j = 0; j < TN; ++j) {
-            const int64_t col = col0 + br0 + j * 32 + lr;
+        for(int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+}
+
+template <bool TA, bool TB, int EDGE, class T>
+__global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
+    constexpr bool AK = !TA, BKF = TB;
+    using OA = Operand<AK, BM>;
+    using OB = Operand<BKF, BN>;
+    using S = Staging<AK, BKF, T>;
+    __shared__ __attribute__((aligned(16))) __bf16 ldsA[2][BM * KFB];
+    __shared__ __attribute__((aligned(16))) __bf16 ldsB[2][BN * KFB];
+
+    const TileJob job = tile_job<T>(p);
+    if(job.skip) return;
+    const int nslices = job.nslices;
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    const int wm = w / WGN, wn = w % WGN;
+    const int lr = l & 31, lh = l >> 5;
+    const int ar0 = wm * TM * 32, br0 = wn * TN * 32;
+
+    f32x16 acc[TM][TN];
 #pragma unroll
-            for(int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + ar0 + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                if(EDGE != kEdgeNone && (row >= p.M || col >= p.N)) continue;
-                float v = alpha * acc[i][j][r];
-                float* c = C + row * ldc + col;
-                if(beta != 0.0f) v += beta * *c;
-                *c = v;
-            }
+    for(int i = 0; i < TM; ++i)
+#pragma unroll
+        for(int j = 0; j < TN; ++j)
+#pragma unroll
+            for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    constexpr int RD = TM + TN;
+    constexpr int NMFMA = TM * TN;
+    constexpr int STAGE_OPS = S::group_ops(0) + S::group_ops(1) + S::group_ops(2);
+
+    if(nslices > 0) {
+        f32x4 ra[OA::F4], rb[OB::F4];
+        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, ldsA[0], ldsB[0]);
+        __syncthreads();
+        bf16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+        read_step<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
+        read_step<TN>(ldsB[0], br0, lr, lh, 0, fb0);
+        for(int s = 0; s < nslices; ++s) {
+            const int cur = s & 1;
+            __bf16* sa = ldsA[cur ^ 1];
+            __bf16* sb = ldsB[cur ^ 1];
+            const int64_t kn = job.kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
+            // step 0: read step 1, stage slice s+1 and fetch s+2
+            read_step<TM>(ldsA[cur], ar0, lr, lh, 1, fa1);
+            read_step<TN>(ldsB[cur], br0, lr, lh, 1, fb1);
+            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            mfma_step<TM, TN>(acc, fa0, fb0);
+            interleave<NMFMA, RD + STAGE_OPS>();
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            // step 1, with step 0 of slice s+1 read underneath
+            read_step<TM>(sa, ar0, lr, lh, 0, fa0);
+            read_step<TN>(sb, br0, lr, lh, 0, fb0);
+            mfma_step<TM, TN>(acc, fa1, fb1);
+            interleave<NMFMA, RD>();
+            __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
 }
 
 // C = alpha * sum_s ws[s] + beta * C, planes summed in order s = 0, 1, ...
@@ -541,25 +697,36 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
     return best;
 }
 
+enum Precision { kFp32 = 0, kBf16 = 1 };
+
+template <bool TA, bool TB, class T, int EDGE>
+void launch_kernel(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
+    if(prec == kBf16)
+        gemm_bf16_kernel<TA, TB, EDGE, T><<<grid, NT, 0, st>>>(gp);
+    else
+        gemm_f32_kernel<TA, TB, EDGE, T><<<grid, NT, 0, st>>>(gp);
+}
+
 template <bool TA, bool TB, class T>
-int launch_tile(const GemmParams& gp, int64_t batch, int edge, hipStream_t st) {
+int launch_tile(const GemmParams& gp, int64_t batch, int edge, int prec, hipStream_t st) {
     dim3 grid((unsigned)(gp.tiles_m * gp.tiles_n), (unsigned)(gp.splits > 1 ? gp.splits : batch));
     if(edge == kEdgeNone)
-        gemm_f32_kernel<TA, TB, kEdgeNone, T><<<grid, NT, 0, st>>>(gp);
+        launch_kernel<TA, TB, T, kEdgeNone>(gp, grid, prec, st);
     else if(edge == kEdgeVec)
-        gemm_f32_kernel<TA, TB, kEdgeVec, T><<<grid, NT, 0, st>>>(gp);
+        launch_kernel<TA, TB, T, kEdgeVec>(gp, grid, prec, st);
     else
-        gemm_f32_kernel<TA, TB, kEdgeScalar, T><<<grid, NT, 0, st>>>(gp);
-    return pk::launch_status("pk_gemm_f32");
+        launch_kernel<TA, TB, T, kEdgeScalar>(gp, grid, prec, st);
+    return pk::launch_status(prec == kBf16 ? "pk_gemm_bf16_f32" : "pk_gemm_f32");
 }
 
 template <bool TA, bool TB>
-int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, hipStream_t st) {
+int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, int prec,
+           hipStream_t st) {
     switch(kind) {
-    case kTile256: return launch_tile<TA, TB, Tile256>(gp, batch, edge, st);
-    case kTile96: return launch_tile<TA, TB, Tile96>(gp, batch, edge, st);
-    case kTile64: return launch_tile<TA, TB, Tile64>(gp, batch, edge, st);
-    default: return launch_tile<TA, TB, Tile128>(gp, batch, edge, st);
+    case kTile256: return launch_tile<TA, TB, Tile256>(gp, batch, edge, prec, st);
+    case kTile96: return launch_tile<TA, TB, Tile96>(gp, batch, edge, prec, st);
+    case kTile64: return launch_tile<TA, TB, Tile64>(gp, batch, edge, prec, st);
+    default: return launch_tile<TA, TB, Tile128>(gp, batch, edge, prec, st);
     }
 }
 
@@ -567,7 +734,7 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
               int64_t lda, int64_t sA_outer, int64_t sA_inner, const float* B, int64_t ldb,
               int64_t sB_outer, int64_t sB_inner, float beta, float* C, int64_t ldc,
               int64_t sC_outer, int64_t sC_inner, int64_t batch, int64_t inner_count, int causal,
-              float* ws, size_t ws_bytes, pk_stream_t stream) {
+              float* ws, size_t ws_bytes, int prec, pk_stream_t stream) {
     const bool TA = ta == 'T' || ta == 't', TB = tb == 'T' || tb == 't';
     if(!(TA || ta == 'N' || ta == 'n') || !(TB || tb == 'N' || tb == 'n'))
         return pk::fail("pk_gemm_f32: transpose flags must be 'N' or 'T' (got '%c','%c')", ta, tb);
@@ -643,13 +810,13 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     const TileKind kind = tc.kind;
     int rc;
     if(!TA && !TB)
-        rc = launch<false, false>(gp, batch, edge, kind, st);
+        rc = launch<false, false>(gp, batch, edge, kind, prec, st);
     else if(!TA && TB)
-        rc = launch<false, true>(gp, batch, edge, kind, st);
+        rc = launch<false, true>(gp, batch, edge, kind, prec, st);
     else if(TA && !TB)
-        rc = launch<true, false>(gp, batch, edge, kind, st);
+        rc = launch<true, false>(gp, batch, edge, kind, prec, st);
     else
-        rc = launch<true, true>(gp, batch, edge, kind, st);
+        rc = launch<true, true>(gp, batch, edge, kind, prec, st);
     if(rc || gp.splits == 1) return rc;
     splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(M, N, gp.splits, gp.ws, alpha,
                                                                   beta, C, ldc);
@@ -666,14 +833,14 @@ extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64
                                    int causal, pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, sA_outer, sA_inner, B, ldb, sB_outer,
                      sB_inner, beta, C, ldc, sC_outer, sC_inner, batch, inner_count, causal,
-                     nullptr, 0, stream);
+                     nullptr, 0, kFp32, stream);
 }
 
 extern "C" int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                            const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                            float* C, int64_t ldc, pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
-                     0, nullptr, 0, stream);
+                     0, nullptr, 0, kFp32, stream);
 }
 
 extern "C" size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K) {
@@ -688,5 +855,20 @@ extern "C" int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K,
                               float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
                               pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
-                     0, static_cast<float*>(workspace), workspace_bytes, stream);
+                     0, static_cast<float*>(workspace), workspace_bytes, kFp32, stream);
+}
+
+extern "C" int pk_gemm_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                const float* A, int64_t lda, const float* B, int64_t ldb,
+                                float beta, float* C, int64_t ldc, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, nullptr, 0, kBf16, stream);
+}
+
+extern "C" int pk_gemm_ex_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64_t K,
+                                   float alpha, const float* A, int64_t lda, const float* B,
+                                   int64_t ldb, float beta, float* C, int64_t ldc,
+                                   void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, static_cast<float*>(workspace), workspace_bytes, kBf16, stream);
 }

@@ -143,6 +143,20 @@ int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m)
 
 static inline char flip(char t) { return t == 'N' ? 'T' : 'N'; }
 
+/* precision of pico_matmul's products and of their gradients */
+static int g_matmul_precision = PICO_MATMUL_FP32;
+
+int pico_set_matmul_precision(int precision) {
+    if(precision != PICO_MATMUL_FP32 && precision != PICO_MATMUL_BF16) {
+        PKH_ERR("pico_set_matmul_precision: unknown precision %d!\n", precision);
+        return PK_EINVAL;
+    }
+    g_matmul_precision = precision;
+    return 0;
+}
+
+int pico_get_matmul_precision(void) { return g_matmul_precision; }
+
 /* products with too few output tiles (weight gradients) split K through the
  * library workspace; see pk_gemm_ex_f32 */
 int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
@@ -151,12 +165,15 @@ int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, fl
     size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
     void* ws = ws_bytes ? pkh_workspace(ws_bytes) : NULL;
     if(!ws) ws_bytes = 0;
+    int (*gemm)(char, char, int64_t, int64_t, int64_t, float, const float*, int64_t,
+                const float*, int64_t, float, float*, int64_t, void*, size_t, pk_stream_t) =
+        g_matmul_precision == PICO_MATMUL_BF16 ? pk_gemm_ex_bf16_f32 : pk_gemm_ex_f32;
     if(tc == 'N')
-        return pk_gemm_ex_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws,
-                              ws_bytes, pkh_stream());
+        return gemm(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws, ws_bytes,
+                    pkh_stream());
     /* C stored transposed: produce C^T [N, M] = B^T . A^T */
-    return pk_gemm_ex_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
-                          ws, ws_bytes, pkh_stream());
+    return gemm(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc, ws,
+                ws_bytes, pkh_stream());
 }
 
 static int matmul_views(struct PicoTensor* a, struct PicoTensor* b, struct PkMat* va,

@@ -58,6 +58,28 @@ def gemm(ta, tb, A, B, C, alpha=1.0, beta=0.0):
     return C
 
 
+def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
+    """gemm with bf16 multiplies and fp32 accumulation (fp32 tensors in and out);
+    ws: optional workspace for a K split (as gemm_ex)"""
+    _f32(A, B, C)
+    lda, ldb, ldc = _rowmajor(A, "A"), _rowmajor(B, "B"), _rowmajor(C, "C")
+    M = A.shape[1] if ta == "T" else A.shape[0]
+    K = A.shape[0] if ta == "T" else A.shape[1]
+    Kb = B.shape[1] if tb == "T" else B.shape[0]
+    N = B.shape[0] if tb == "T" else B.shape[1]
+    if K != Kb or tuple(C.shape) != (M, N):
+        raise ValueError(f"gemm shape mismatch: op(A) {M}x{K}, op(B) {Kb}x{N}, C {tuple(C.shape)}")
+    if ws is None:
+        check("pk_gemm_bf16_f32", hip_lib().pk_gemm_bf16_f32(
+            ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C),
+            ldc, _stream()))
+    else:
+        check("pk_gemm_ex_bf16_f32", hip_lib().pk_gemm_ex_bf16_f32(
+            ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C),
+            ldc, _ptr(ws), ws.numel() * ws.element_size(), _stream()))
+    return C
+
+
 def gemm_workspace(M, N, K):
     return int(hip_lib().pk_gemm_workspace_f32(M, N, K))
 

@@ -119,6 +119,8 @@ _GPU_SIGS = {
     "pico_gpt_param": (TP, [c_p, ctypes.c_int]),
     "pico_gpt_free": (None, [c_p]),
     "pico_gpt_param_name": (ctypes.c_char_p, [c_p, ctypes.c_int]),
+    "pico_set_matmul_precision": (ctypes.c_int, [ctypes.c_int]),
+    "pico_get_matmul_precision": (ctypes.c_int, []),
     "pico_checkpoint_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),
                                             ctypes.POINTER(ctypes.c_char_p), c_p]),
     "pico_checkpoint_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),
