@@ -79,6 +79,13 @@ def gemm_section(args, torch, K):
         K.gemm("N", "T", dC, B, dA)
         K.gemm("T", "N", A, dC, dB)
 
+    # untimed conditioning: ~0.3 s of the same products first, so the timed
+    # steps run at the loaded clock whatever W is (the first launches after an
+    # idle spell run slower while the clock ramps up)
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
+        step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

@@ -136,9 +136,68 @@ __device__ __forceinline__ void store_rowT(float* __restrict__ dst, const f32x16
         }
 }
 
+// ------------------------------------------------- direct-to-LDS block loads
+// buffer_load_dwordx4 ... lds writes lane l's 16 bytes to LDS at (wave-uniform
+// base) + 16*l, so one instruction fills 1 KB of a tile straight from global
+// memory, without passing through registers.  A padded 64-row tile (stride
+// LDT = 68 floats) is 17 KB: instruction n (0..16) covers floats 256n ..
+// 256n+255, and lane l lands at float f = 256n + 4l, i.e. row f / 68, column
+// f % 68.  Column 64 is the padding: that lane fetches the row's first chunk
+// again, which lands in the pad and is never read.  Wave w issues
+// instructions w, w+4, w+8, w+12, and wave 0 also instruction 16.
+//
+// The buffer resource spans exactly one head's rows (T rows of stride D from
+// the head's first column), so a load outside them returns zeros instead of
+// touching other memory.
+constexpr int LOADS = TILE * 4 / 1024;  // 17
+static_assert(TILE * 4 == LOADS * 1024, "a tile is a whole number of 1 KB loads");
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const float* head, int64_t T,
+                                                            int64_t D) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(head), (short)0,
+                                             (int)(((T - 1) * D + HD) * 4), 0x00020000);
+}
+
+// this lane's byte offsets (relative to the block's first row) for its wave's
+// instructions; slot 4 is used by wave 0 only
+struct BlockLoad {
+    unsigned off[5];
+    __device__ __forceinline__ BlockLoad(int64_t D, int w, int l) {
+#pragma unroll
+        for(int i = 0; i < 5; ++i) {
+            const int n = i < 4 ? w + 4 * i : LOADS - 1;
+            const int f = 256 * n + 4 * l, r = f / LDT, c = f % LDT;
+            off[i] = (unsigned)((r * D + (c < HD ? c : 0)) * 4);
+        }
+    }
+    // issue the loads of the head's rows row0..row0+63 into tile
+    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, int64_t D, int64_t row0,
+                                          float* tile, int w) const {
+        const unsigned so = (unsigned)(row0 * D * 4);
+#pragma unroll
+        for(int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(tile + 256 * (w + 4 * i)), 16,
+                                                     off[i], so, 0, 0);
+        if(w == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(tile + 256 * (LOADS - 1)), 16,
+                                                     off[4], so, 0, 0);
+    }
+};
+
+// wait for this wave's outstanding global loads (the direct-to-LDS ones
+// included); a barrier after it publishes every wave's loads
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // ======================================================================= forward
 // Workgroup: 128 queries of one (b, h), 4 waves of 32.  Heaviest query blocks
 // (the ones that see the most keys) are dispatched first.
+//
+// Pipeline: K runs one block ahead of V.  Iteration j computes the scores of
+// key block j+1 (MFMA) while it turns the scores of block j into
+// probabilities (VALU) and then adds P(j).V(j) to the output, so the softmax
+// of one block hides under the score products of the next.  In flight during
+// iteration j: K(j+2) and V(j+1).
 __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
     __shared__ __attribute__((aligned(16))) float sV[2][TILE];
@@ -147,77 +206,95 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.D + h * HD;
     const float *Q = p.q + base, *K = p.k + base, *V = p.v + base;
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l & 31, lh = l >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);  // blocks the workgroup streams
+    const int nw = (int)((q0 + 31) / BLK) + 1;          // blocks this wave sees
 
+    const BlockLoad ld(p.D, w, l);
+    const __amdgpu_buffer_rsrc_t rk = head_rsrc(K, p.T, p.D), rv = head_rsrc(V, p.T, p.D);
+    ld.issue(rk, p.D, 0, sK[0], w);
+    ld.issue(rv, p.D, 0, sV[0], w);
+    ld.issue(rk, p.D, BLK, sK[1], w);  // nkv >= 2 since T % 128 == 0
     float qf[32];
     load_frag32(Q + qi * p.D, lh, qf, p.scale * kLog2e);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
+    wait_loads();
+    __syncthreads();
+    f32x16 s[2] = {dot_rows(sK[0], 0, lq, lh, qf, zero16()),
+                   dot_rows(sK[0], 1, lq, lh, qf, zero16())};
 
-    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
-    f32x4 rk[4], rv[4];
-    fetch_block(K, p.D, 0, rk);
-    fetch_block(V, p.D, 0, rv);
-    store_block(sK[0], rk);
-    store_block(sV[0], rv);
-    for(int j = 0; j < nkv; ++j) {
-        const int st = j & 1;
+    // softmax of block j's scores s, then o += V(j)^T . P^T
+    auto soft_pv = [&](int j) {
+        // key kv0 + sub*32 + acc_row(r, lh) is hidden from query qi when it
+        // exceeds qi; lim folds the lane's offsets into one compare per element
+        const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;
+        float mx = -INFINITY;
+#pragma unroll
+        for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
+                mx = fmaxf(mx, s[sub][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        float ls = 0.0f;
+#pragma unroll
+        for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                s[sub][r] = __builtin_amdgcn_exp2f(s[sub][r] - mn);
+                ls += s[sub][r];
+            }
+        ls += __shfl_xor(ls, 32, 64);
+        lsum = lsum * alpha + ls;
+        m = mn;
+#pragma unroll
+        for(int r = 0; r < 16; ++r) {
+            o[0][r] *= alpha;
+            o[1][r] *= alpha;
+        }
+        const float* tv = sV[j & 1];
+#pragma unroll
+        for(int cb = 0; cb < 2; ++cb) {
+            o[cb] = dot_cols(tv, 0, cb, lq, lh, s[0], o[cb]);
+            o[cb] = dot_cols(tv, 1, cb, lq, lh, s[1], o[cb]);
+        }
+    };
+    // top of iteration j: K(j+1) and V(j) have landed, and sK[j&1] (K(j)) and
+    // sV[(j+1)&1] (V(j-1)) are free for K(j+2) and V(j+1)
+    auto next_loads = [&](int j) {
+        wait_loads();
         __syncthreads();
-        const bool more = j + 1 < nkv;
-        if(more) {
-            fetch_block(K, p.D, (int64_t)(j + 1) * BLK, rk);
-            fetch_block(V, p.D, (int64_t)(j + 1) * BLK, rv);
-        }
-        const int64_t kv0 = (int64_t)j * BLK;
-        if(kv0 <= q0 + 31) {  // some key of this block is visible to this wave
-            f32x16 s0 = dot_rows(sK[st], 0, lq, lh, qf, zero16());
-            f32x16 s1 = dot_rows(sK[st], 1, lq, lh, qf, zero16());
-            if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
-#pragma unroll
-                for(int r = 0; r < 16; ++r) {
-                    if(kv0 + acc_row(r, lh) > qi) s0[r] = -INFINITY;
-                    if(kv0 + 32 + acc_row(r, lh) > qi) s1[r] = -INFINITY;
-                }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for(int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m, mx);
-            const float alpha = exp2f(m - mn);  // m = -inf on the first block: 0
-            float ls = 0.0f;
-#pragma unroll
-            for(int r = 0; r < 16; ++r) {
-                s0[r] = exp2f(s0[r] - mn);
-                s1[r] = exp2f(s1[r] - mn);
-                ls += s0[r] + s1[r];
-            }
-            ls += __shfl_xor(ls, 32, 64);
-            lsum = lsum * alpha + ls;
-            m = mn;
-#pragma unroll
-            for(int r = 0; r < 16; ++r) {
-                o[0][r] *= alpha;
-                o[1][r] *= alpha;
-            }
-            // O^T[d][q] += sum_kv V[kv][d] P^T[kv][q]
-#pragma unroll
-            for(int cb = 0; cb < 2; ++cb) {
-                o[cb] = dot_cols(sV[st], 0, cb, lq, lh, s0, o[cb]);
-                o[cb] = dot_cols(sV[st], 1, cb, lq, lh, s1, o[cb]);
-            }
-        }
-        if(more) {
-            store_block(sK[st ^ 1], rk);
-            store_block(sV[st ^ 1], rv);
-        }
+        if(j + 2 < nkv) ld.issue(rk, p.D, (int64_t)(j + 2) * BLK, sK[j & 1], w);
+        if(j + 1 < nkv) ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
+    };
+
+    int j = 0;
+    for(; j + 1 < nw; ++j) {  // blocks with a successor this wave sees
+        next_loads(j);
+        const float* tk = sK[(j + 1) & 1];
+        const f32x16 n0 = dot_rows(tk, 0, lq, lh, qf, zero16());
+        const f32x16 n1 = dot_rows(tk, 1, lq, lh, qf, zero16());
+        soft_pv(j);
+        s[0] = n0;
+        s[1] = n1;
     }
+    next_loads(j);  // the wave's last block
+    soft_pv(j);
+    for(++j; j < nkv; ++j) next_loads(j);  // keep loading for the other waves
     store_rowT(p.out + base + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
 
-// ============================================================ backward: D = rowsum(dO*O)
+// ============================================== backward: per-query constants
+// For each 64-query block the workspace holds 64 values of L2 = lse*log2(e)
+// followed by 64 values of D = rowsum(dO*O): [B*H][T/64][2][64].  One 512-byte
+// load per block brings both into LDS.
 __global__ void flash_dsum(FlashParams p) {
     const int64_t BH = p.B * p.H, n = BH * p.T;
     for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -232,84 +309,92 @@ __global__ void flash_dsum(FlashParams p) {
             const f32x4 a = x[c], o = y[c];
             s += a[0] * o[0] + a[1] * o[1] + a[2] * o[2] + a[3] * o[3];
         }
-        p.dsum_out[i] = s;
+        float* blk = p.dsum_out + bh * 2 * p.T + (t / BLK) * 2 * BLK + t % BLK;
+        blk[0] = p.lse[i] * kLog2e;
+        blk[BLK] = s;
     }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t consts_rsrc(const float* ws, int64_t bh,
+                                                              int64_t T) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws + bh * 2 * T), (short)0,
+                                             (int)(2 * T * 4), 0x00020000);
 }
 
 // ================================================================ backward: dK, dV
 // Workgroup: 128 keys of one (b, h), one key per lane; query blocks of 64 with
-// q >= key are streamed through LDS (Q and dO rows, their lse and D).
-//   S = Q.K^T (per lane: its key's column)        P = exp2(S' - lse2)
+// q >= key stream through LDS (Q and dO rows, their L2 and D), loaded
+// straight into LDS one block ahead.
+//   S = Q.K^T (per lane: its key's column)        P = exp2(S' - L2)
 //   dV^T += dO^T.P         dP = dO.V^T           dS = P*(dP - D)
 //   dK^T += Q^T.dS  (x scale at the end)
+// Both 32-query halves of a block get their scores first, so the
+// exponentials of one half run while the other half's products are in flight.
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sQ[2][TILE];
-    __shared__ __attribute__((aligned(16))) float sO[2][TILE];  // dO rows
-    __shared__ float sL[2][BLK], sDs[2][BLK];
-    const int64_t BH = p.B * p.H, nkb = p.T / ROWS;
+    __shared__ __attribute__((aligned(16))) float sO[2][TILE];      // dO rows
+    __shared__ __attribute__((aligned(16))) float sLD[2][2 * BLK];  // L2, then D
+    const int64_t BH = p.B * p.H;
     const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.D + h * HD;
-    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
-    const float* lse = p.lse + bh * p.T;
-    const float* dsum = p.dsum + bh * p.T;
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l & 31, lh = l >> 5;
+    const float *K = p.k + base, *V = p.v + base;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
-    (void)nkb;
 
+    const BlockLoad ld(p.D, w, l);
+    const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.D);
+    const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + base, p.T, p.D);
+    const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.T);
+    auto issue = [&](int j, int st) {
+        ld.issue(rq, p.D, (int64_t)j * BLK, sQ[st], w);
+        ld.issue(ro, p.D, (int64_t)j * BLK, sO[st], w);
+        if(w == 1 && l < 32)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)sLD[st], 16, 16 * l,
+                                                     (unsigned)(j * 2 * BLK * 4), 0, 0);
+    };
+    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
+    issue(j0, 0);
     float kf[32], vf[32];
     load_frag32(K + ki * p.D, lh, kf, p.scale * kLog2e);
     load_frag32(V + ki * p.D, lh, vf, 1.0f);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
 
-    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
-    f32x4 rq[4], ro[4];
-    float rl = 0.0f, rd = 0.0f;
-    auto fetch = [&](int j) {
-        fetch_block(Q, p.D, (int64_t)j * BLK, rq);
-        fetch_block(dO, p.D, (int64_t)j * BLK, ro);
-        if(threadIdx.x < BLK) {
-            rl = lse[(int64_t)j * BLK + threadIdx.x] * kLog2e;
-            rd = dsum[(int64_t)j * BLK + threadIdx.x];
-        }
-    };
-    auto put = [&](int st) {
-        store_block(sQ[st], rq);
-        store_block(sO[st], ro);
-        if(threadIdx.x < BLK) {
-            sL[st][threadIdx.x] = rl;
-            sDs[st][threadIdx.x] = rd;
-        }
-    };
-    fetch(j0);
-    put(0);
     for(int j = j0; j < nq; ++j) {
         const int st = (j - j0) & 1;
-        __syncthreads();
-        const bool more = j + 1 < nq;
-        if(more) fetch(j + 1);
+        wait_loads();
+        __syncthreads();  // block j is in; buffer st^1 (block j-1) is free
+        if(j + 1 < nq) issue(j + 1, st ^ 1);
         const int64_t qs = (int64_t)j * BLK;
         if(qs + BLK - 1 >= k0) {  // some query of this block sees this wave's keys
+            const float *tq = sQ[st], *to = sO[st], *tl = sLD[st];
+            f32x16 s[2], dp[2];
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
-                f32x16 s = dot_rows(sQ[st], sub, lq, lh, kf, zero16());
-                f32x16 dp = dot_rows(sO[st], sub, lq, lh, vf, zero16());
+                s[sub] = dot_rows(tq, sub, lq, lh, kf, zero16());
+                dp[sub] = dot_rows(to, sub, lq, lh, vf, zero16());
+            }
+            // query qs + sub*32 + acc_row(r, lh) sees key ki when it is >= ki
+            const int lim = (int)(ki - qs) - 4 * lh;
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
                     const int qr = sub * 32 + acc_row(r, lh);
-                    const bool vis = qs + qr >= ki;
-                    const float pr = vis ? exp2f(s[r] - sL[st][qr]) : 0.0f;
-                    s[r] = pr;
-                    dp[r] = pr * (dp[r] - sDs[st][qr]);
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim
+                                         ? __builtin_amdgcn_exp2f(s[sub][r] - tl[qr])
+                                         : 0.0f;
+                    s[sub][r] = pr;
+                    dp[sub][r] = pr * (dp[sub][r] - tl[BLK + qr]);
                 }
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb) {
-                    dv[cb] = dot_cols(sO[st], sub, cb, lq, lh, s, dv[cb]);
-                    dk[cb] = dot_cols(sQ[st], sub, cb, lq, lh, dp, dk[cb]);
+                    dv[cb] = dot_cols(to, sub, cb, lq, lh, s[sub], dv[cb]);
+                    dk[cb] = dot_cols(tq, sub, cb, lq, lh, dp[sub], dk[cb]);
                 }
             }
         }
-        if(more) put(st ^ 1);
     }
     store_rowT(p.dv + base + ki * p.D, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
     store_rowT(p.dk + base + ki * p.D, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
@@ -317,8 +402,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
 
 // =================================================================== backward: dQ
 // Workgroup: 128 queries of one (b, h), one query per lane; key blocks of 64
-// with key <= query streamed through LDS (K and V rows).
-//   S^T = K.Q^T   P^T = exp2(S'^T - lse2)   dP^T = V.dO^T   dS^T = P^T*(dP^T - D)
+// with key <= query stream through LDS (K and V rows), loaded straight into
+// LDS one block ahead.
+//   S^T = K.Q^T   P^T = exp2(S'^T - L2)   dP^T = V.dO^T   dS^T = P^T*(dP^T - D)
 //   dQ^T += K^T.dS^T  (x scale at the end)
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
@@ -327,50 +413,55 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.D + h * HD;
-    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64, lq = l & 31, lh = l >> 5;
+    const float *Q = p.q + base, *dO = p.dout + base;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
+    const BlockLoad ld(p.D, w, l);
+    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.D);
+    const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v + base, p.T, p.D);
+    ld.issue(rk, p.D, 0, sK[0], w);
+    ld.issue(rv, p.D, 0, sV[0], w);
     float qf[32], of[32];
     load_frag32(Q + qi * p.D, lh, qf, p.scale * kLog2e);
     load_frag32(dO + qi * p.D, lh, of, 1.0f);
-    const float l2 = p.lse[bh * p.T + qi] * kLog2e;
-    const float dd = p.dsum[bh * p.T + qi];
+    const float* cst = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
+    const float l2 = cst[0], dd = cst[BLK];
     f32x16 dq[2] = {zero16(), zero16()};
 
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
-    f32x4 rk[4], rv[4];
-    fetch_block(K, p.D, 0, rk);
-    fetch_block(V, p.D, 0, rv);
-    store_block(sK[0], rk);
-    store_block(sV[0], rv);
     for(int j = 0; j < nkv; ++j) {
         const int st = j & 1;
+        wait_loads();
         __syncthreads();
-        const bool more = j + 1 < nkv;
-        if(more) {
-            fetch_block(K, p.D, (int64_t)(j + 1) * BLK, rk);
-            fetch_block(V, p.D, (int64_t)(j + 1) * BLK, rv);
+        if(j + 1 < nkv) {
+            ld.issue(rk, p.D, (int64_t)(j + 1) * BLK, sK[st ^ 1], w);
+            ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, sV[st ^ 1], w);
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
+            const float *tk = sK[st], *tv = sV[st];
+            f32x16 s[2], dp[2];
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
-                f32x16 s = dot_rows(sK[st], sub, lq, lh, qf, zero16());
-                f32x16 dp = dot_rows(sV[st], sub, lq, lh, of, zero16());
+                s[sub] = dot_rows(tk, sub, lq, lh, qf, zero16());
+                dp[sub] = dot_rows(tv, sub, lq, lh, of, zero16());
+            }
+            const int lim = (int)(qi - kv0) - 4 * lh;  // key kv0 + k visible when k <= lim
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
-                    const bool vis = kv0 + sub * 32 + acc_row(r, lh) <= qi;
-                    const float pr = vis ? exp2f(s[r] - l2) : 0.0f;
-                    dp[r] = pr * (dp[r] - dd);
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) <= lim
+                                         ? __builtin_amdgcn_exp2f(s[sub][r] - l2)
+                                         : 0.0f;
+                    dp[sub][r] = pr * (dp[sub][r] - dd);
                 }
 #pragma unroll
-                for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols(sK[st], sub, cb, lq, lh, dp, dq[cb]);
+                for(int cb = 0; cb < 2; ++cb)
+                    dq[cb] = dot_cols(tk, sub, cb, lq, lh, dp[sub], dq[cb]);
             }
-        }
-        if(more) {
-            store_block(sK[st ^ 1], rk);
-            store_block(sV[st ^ 1], rv);
         }
     }
     store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
@@ -383,7 +474,8 @@ int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, co
     if(T % ROWS) return pk::fail("%s: T=%lld must be a multiple of %d", who, (long long)T, ROWS);
     if(!pk::aligned16(a) || !pk::aligned16(b) || !pk::aligned16(c))
         return pk::fail("%s: q, k, v must be 16-byte aligned", who);
-    if(B * H * (T / ROWS) > 0x7fffffff) return pk::fail("%s: problem too large", who);
+    if(B * H * (T / ROWS) > 0x7fffffff || T * H * HD * 4 > 0x7fffffff)
+        return pk::fail("%s: problem too large", who);
     return PK_OK;
 }
 
@@ -417,7 +509,7 @@ extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd
 }
 
 extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
-    return B > 0 && H > 0 && T > 0 ? (size_t)(B * H * T) * sizeof(float) : 0;
+    return B > 0 && H > 0 && T > 0 ? (size_t)(2 * B * H * T) * sizeof(float) : 0;
 }
 
 extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
@@ -456,7 +548,7 @@ extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd
     p.flags = flags;
     hipStream_t st = pk::as_stream(stream);
     flash_dsum<<<pk::grid_for(B * H * T, 256), 256, 0, st>>>(p);
-    if((rc = pk::launch_status("pk_flash_attn_bwd_f32 (rowsum)"))) return rc;
+    if((rc = pk::launch_status("pk_flash_attn_bwd_f32 (row constants)"))) return rc;
     const unsigned grid = (unsigned)(B * H * (T / ROWS));
     flash_bwd_dkdv<<<grid, 256, 0, st>>>(p);
     if((rc = pk::launch_status("pk_flash_attn_bwd_f32 (dK, dV)"))) return rc;
