@@ -251,13 +251,15 @@ void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
 
 /* ---- matmul precision (no reference counterpart: pico is fp32 only) ----
- * PICO_MATMUL_FP32 (the default): pico_matmul and its gradients multiply in
- * fp32 on the fp32 matrix cores, within the fp32 parity contract.
- * PICO_MATMUL_BF16: operands are rounded to bf16 (nearest even) and multiplied
- * on the bf16 matrix cores, accumulating in fp32; tensors stay fp32.  Faster,
- * and outside the fp32 parity contract (relative error of order 2^-8 per
- * operand).  Attention and the other ops are unaffected.  Returns 0, or
- * nonzero for an unknown value. */
+ * PICO_MATMUL_FP32 (the default): pico_matmul, the fused attention's
+ * products and their gradients multiply in fp32 on the fp32 matrix cores,
+ * within the fp32 parity contract.
+ * PICO_MATMUL_BF16: their operands are rounded to bf16 (nearest even) and
+ * multiplied on the bf16 matrix cores, accumulating in fp32; tensors, the
+ * softmax statistics and every other op stay fp32.  Faster, and outside the
+ * fp32 parity contract (relative error of order 2^-8 per operand).  An
+ * attention node's backward uses the precision its forward ran in.  Returns
+ * 0, or nonzero for an unknown value. */
 #define PICO_MATMUL_FP32 0
 #define PICO_MATMUL_BF16 1
 int pico_set_matmul_precision(int precision);

@@ -222,9 +222,9 @@ int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float sc
  * are never written to memory.  Same layouts and lse as above; q, k, v, o,
  * dout, dq, dk, dv 16-byte aligned.  pk_flash_attn_supported(T, hd) says
  * whether these apply.  The backward needs pk_flash_attn_bwd_workspace(B, H,
- * T) bytes (the row sums of dO*O) and writes dv, then dk, then dq, each
- * accumulating when its flags bit is set (PK_ACCUM dq, PK_ACCUM2 dk,
- * PK_ACCUM3 dv). */
+ * T) bytes (per 64-query block: lse in base 2, then the row sums of dO*O)
+ * and writes dv, then dk, then dq, each accumulating when its flags bit is
+ * set (PK_ACCUM dq, PK_ACCUM2 dk, PK_ACCUM3 dv). */
 int pk_flash_attn_supported(int64_t T, int64_t hd);
 int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
                           const float* q, const float* k, const float* v, float* o, float* lse,
@@ -234,6 +234,19 @@ int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float sca
                           const float* q, const float* k, const float* v, const float* o,
                           const float* lse, const float* dout, float* dq, float* dk, float* dv,
                           void* workspace, size_t workspace_bytes, int flags, pk_stream_t stream);
+/* The same fused attention with bf16 multiplies (no reference counterpart:
+ * pico is fp32 only).  Q (pre-scaled), K, V, dO and the probabilities P and
+ * dS are rounded to bf16 (nearest even) where they enter a matrix product;
+ * the softmax statistics, exponentials and accumulators stay fp32, and every
+ * tensor, lse and the workspace are as in the fp32 entry points. */
+int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                               const float* q, const float* k, const float* v, float* o,
+                               float* lse, pk_stream_t stream);
+int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                               const float* q, const float* k, const float* v, const float* o,
+                               const float* lse, const float* dout, float* dq, float* dk,
+                               float* dv, void* workspace, size_t workspace_bytes, int flags,
+                               pk_stream_t stream);
 /* the two row kernels inside the chain, exposed for tests:
  * P = softmax(scale*S) over j <= i, zero for j > i, lse per row (P may alias S) */
 int pk_causal_softmax_fwd_f32(int64_t BH, int64_t T, float scale, const float* S, float* P,

@@ -467,6 +467,320 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
+// ================================================================ bf16 products
+// The same three kernels with bf16 multiplies (v_mfma_f32_32x32x16_bf16,
+// fp32 accumulation): Q (pre-scaled), K, V, dO and the probabilities P and
+// dS are rounded to bf16 (nearest even) where they enter a product; the
+// softmax statistics, exponentials and accumulators stay fp32.
+//
+// An MFMA contracts 16 values of k, lane l supplying slots 8*(l/32)..+7.  A
+// contraction over the head dims takes d = 16t + 8h + j (h = l/32).  A
+// contraction over the rows of an accumulator (keys in the forward, queries
+// in the backward) uses the rows the lane already holds: group g of a 32-row
+// sub-block pairs slot (h, j) with row 16g + 8(j/4) + 4h + j%4, which is
+// acc_row(8g + j, h) -- registers 8g..8g+7 of the accumulator.  The other
+// operand reads the same rows: two runs of 4 from a transposed tile.
+//
+// Blocks are staged from global memory through registers (rounded on the way
+// into LDS), as 4x4 sub-blocks per thread so that a tile can be written
+// row-major, transposed or both.  bf16 tiles have rows of LDB = 72 elements
+// (144 bytes): 16-byte aligned for the b128 reads and conflict-free for them.
+constexpr int LDB = HD + 8;
+constexpr int TILEB = BLK * LDB;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x16 mfma16(const bf16x8& a, const bf16x8& b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// thread t holds rows 4*(t/16)..+3, columns 4*(t%16)..+3 of a 64x64 block
+__device__ __forceinline__ void fetch_quad(const float* __restrict__ base, int64_t D, int64_t row0,
+                                           f32x4 (&x)[4]) {
+    const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+#pragma unroll
+    for(int i = 0; i < 4; ++i)
+        x[i] = *reinterpret_cast<const f32x4*>(base + (row0 + 4 * rq + i) * D + 4 * c4);
+}
+
+__device__ __forceinline__ void put_rows(__bf16* t, const f32x4 (&x)[4]) {
+    const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+#pragma unroll
+    for(int i = 0; i < 4; ++i)
+        *reinterpret_cast<bf16x4*>(t + (4 * rq + i) * LDB + 4 * c4) =
+            bf16x4{(__bf16)x[i][0], (__bf16)x[i][1], (__bf16)x[i][2], (__bf16)x[i][3]};
+}
+
+__device__ __forceinline__ void put_cols(__bf16* t, const f32x4 (&x)[4]) {
+    const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+#pragma unroll
+    for(int c = 0; c < 4; ++c)
+        *reinterpret_cast<bf16x4*>(t + (4 * c4 + c) * LDB + 4 * rq) =
+            bf16x4{(__bf16)x[0][c], (__bf16)x[1][c], (__bf16)x[2][c], (__bf16)x[3][c]};
+}
+
+// a lane's 32 head dims of one row, rounded, in the 4 MFMA steps' slots
+__device__ __forceinline__ void load_frag_bf16(const float* __restrict__ row, int h, bf16x8 (&f)[4],
+                                               float mul) {
+#pragma unroll
+    for(int t = 0; t < 4; ++t) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(row + 16 * t + 8 * h);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(row + 16 * t + 8 * h + 4);
+        f[t] = bf16x8{(__bf16)(a[0] * mul), (__bf16)(a[1] * mul), (__bf16)(a[2] * mul),
+                      (__bf16)(a[3] * mul), (__bf16)(b[0] * mul), (__bf16)(b[1] * mul),
+                      (__bf16)(b[2] * mul), (__bf16)(b[3] * mul)};
+    }
+}
+
+// acc (+)= A.B over the head dims: A = row (sub*32 + lane%32) of a row-major
+// tile, B = the lane's fragments
+__device__ __forceinline__ f32x16 dot_rows16(const __bf16* t, int sub, int lq, int lh,
+                                             const bf16x8 (&bf)[4], f32x16 acc) {
+    const __bf16* row = t + (sub * 32 + lq) * LDB + 8 * lh;
+#pragma unroll
+    for(int s = 0; s < 4; ++s) acc = mfma16(*reinterpret_cast<const bf16x8*>(row + 16 * s), bf[s], acc);
+    return acc;
+}
+
+// the accumulator rows of group g as a B operand (slot (h, j) <- register 8g + j)
+__device__ __forceinline__ bf16x8 pack_group(const f32x16& x, int g) {
+    return bf16x8{(__bf16)x[8 * g + 0], (__bf16)x[8 * g + 1], (__bf16)x[8 * g + 2],
+                  (__bf16)x[8 * g + 3], (__bf16)x[8 * g + 4], (__bf16)x[8 * g + 5],
+                  (__bf16)x[8 * g + 6], (__bf16)x[8 * g + 7]};
+}
+
+// acc (+)= X^T . W over the 32 accumulator rows of sub-block `sub`: A[i][row]
+// read from the transposed tile (row cb*32 + lane%32, the group's rows), B = w
+__device__ __forceinline__ f32x16 dot_cols16(const __bf16* t, int sub, int cb, int lq, int lh,
+                                             const f32x16& w, f32x16 acc) {
+    const __bf16* row = t + (cb * 32 + lq) * LDB + sub * 32 + 4 * lh;
+#pragma unroll
+    for(int g = 0; g < 2; ++g) {
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 16 * g);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 * g + 8);
+        const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc = mfma16(a, pack_group(w, g), acc);
+    }
+    return acc;
+}
+
+// ------------------------------------------------------------- bf16 forward
+__global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sVt[2][TILEB];  // [d][key]
+    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+
+    bf16x8 qf[4];
+    load_frag_bf16(Q + qi * p.D, lh, qf, p.scale * kLog2e);
+    f32x16 o[2] = {zero16(), zero16()};
+    float m = -INFINITY, lsum = 0.0f;
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
+    f32x4 rk[4], rv[4];
+    fetch_quad(K, p.D, 0, rk);
+    fetch_quad(V, p.D, 0, rv);
+    put_rows(sK[0], rk);
+    put_cols(sVt[0], rv);
+    for(int j = 0; j < nkv; ++j) {
+        const int st = j & 1;
+        __syncthreads();
+        const bool more = j + 1 < nkv;
+        if(more) {
+            fetch_quad(K, p.D, (int64_t)(j + 1) * BLK, rk);
+            fetch_quad(V, p.D, (int64_t)(j + 1) * BLK, rv);
+        }
+        const int64_t kv0 = (int64_t)j * BLK;
+        if(kv0 <= q0 + 31) {
+            f32x16 s[2] = {dot_rows16(sK[st], 0, lq, lh, qf, zero16()),
+                           dot_rows16(sK[st], 1, lq, lh, qf, zero16())};
+            if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
+                const int lim = (int)(qi - kv0) - 4 * lh;
+#pragma unroll
+                for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            float ls = 0.0f;
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    s[sub][r] = __builtin_amdgcn_exp2f(s[sub][r] - mn);
+                    ls += s[sub][r];
+                }
+            ls += __shfl_xor(ls, 32, 64);
+            lsum = lsum * alpha + ls;
+            m = mn;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                o[0][r] *= alpha;
+                o[1][r] *= alpha;
+            }
+#pragma unroll
+            for(int cb = 0; cb < 2; ++cb) {
+                o[cb] = dot_cols16(sVt[st], 0, cb, lq, lh, s[0], o[cb]);
+                o[cb] = dot_cols16(sVt[st], 1, cb, lq, lh, s[1], o[cb]);
+            }
+        }
+        if(more) {
+            put_rows(sK[st ^ 1], rk);
+            put_cols(sVt[st ^ 1], rv);
+        }
+    }
+    store_rowT(p.out + base + qi * p.D, o, lh, 1.0f / lsum, false);
+    if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
+}
+
+// ------------------------------------------------------- bf16 backward: dK, dV
+__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sQ[2][TILEB];   // [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sQt[2][TILEB];  // [d][q]
+    __shared__ __attribute__((aligned(16))) __bf16 sO[2][TILEB];   // dO [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sOt[2][TILEB];  // dO [d][q]
+    __shared__ float sLD[2][2 * BLK];                              // L2, then D
+    const int64_t BH = p.B * p.H;
+    const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
+    const float* cst = p.dsum + bh * 2 * p.T;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
+
+    bf16x8 kf[4], vf[4];
+    load_frag_bf16(K + ki * p.D, lh, kf, p.scale * kLog2e);
+    load_frag_bf16(V + ki * p.D, lh, vf, 1.0f);
+    f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
+
+    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
+    f32x4 rq[4], ro[4];
+    float rc = 0.0f;
+    auto fetch = [&](int j) {
+        fetch_quad(Q, p.D, (int64_t)j * BLK, rq);
+        fetch_quad(dO, p.D, (int64_t)j * BLK, ro);
+        if(threadIdx.x < 2 * BLK) rc = cst[(int64_t)j * 2 * BLK + threadIdx.x];
+    };
+    auto put = [&](int st) {
+        put_rows(sQ[st], rq);
+        put_cols(sQt[st], rq);
+        put_rows(sO[st], ro);
+        put_cols(sOt[st], ro);
+        if(threadIdx.x < 2 * BLK) sLD[st][threadIdx.x] = rc;
+    };
+    fetch(j0);
+    put(0);
+    for(int j = j0; j < nq; ++j) {
+        const int st = (j - j0) & 1;
+        __syncthreads();
+        const bool more = j + 1 < nq;
+        if(more) fetch(j + 1);
+        const int64_t qs = (int64_t)j * BLK;
+        if(qs + BLK - 1 >= k0) {
+            const float* tl = sLD[st];
+            const int lim = (int)(ki - qs) - 4 * lh;  // query row qr sees key ki when qr >= lim
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
+                f32x16 sc = dot_rows16(sQ[st], sub, lq, lh, kf, zero16());
+                f32x16 dp = dot_rows16(sO[st], sub, lq, lh, vf, zero16());
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const int qr = sub * 32 + acc_row(r, lh);
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim
+                                         ? __builtin_amdgcn_exp2f(sc[r] - tl[qr])
+                                         : 0.0f;
+                    sc[r] = pr;
+                    dp[r] = pr * (dp[r] - tl[BLK + qr]);
+                }
+#pragma unroll
+                for(int cb = 0; cb < 2; ++cb) {
+                    dv[cb] = dot_cols16(sOt[st], sub, cb, lq, lh, sc, dv[cb]);
+                    dk[cb] = dot_cols16(sQt[st], sub, cb, lq, lh, dp, dk[cb]);
+                }
+            }
+        }
+        if(more) put(st ^ 1);
+    }
+    store_rowT(p.dv + base + ki * p.D, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
+    store_rowT(p.dk + base + ki * p.D, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
+}
+
+// ----------------------------------------------------------- bf16 backward: dQ
+__global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sKt[2][TILEB];  // [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 sV[2][TILEB];   // [key][d]
+    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+
+    bf16x8 qf[4], of[4];
+    load_frag_bf16(Q + qi * p.D, lh, qf, p.scale * kLog2e);
+    load_frag_bf16(dO + qi * p.D, lh, of, 1.0f);
+    const float* cst = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
+    const float l2 = cst[0], dd = cst[BLK];
+    f32x16 dq[2] = {zero16(), zero16()};
+
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
+    f32x4 rk[4], rv[4];
+    fetch_quad(K, p.D, 0, rk);
+    fetch_quad(V, p.D, 0, rv);
+    put_rows(sK[0], rk);
+    put_cols(sKt[0], rk);
+    put_rows(sV[0], rv);
+    for(int j = 0; j < nkv; ++j) {
+        const int st = j & 1;
+        __syncthreads();
+        const bool more = j + 1 < nkv;
+        if(more) {
+            fetch_quad(K, p.D, (int64_t)(j + 1) * BLK, rk);
+            fetch_quad(V, p.D, (int64_t)(j + 1) * BLK, rv);
+        }
+        const int64_t kv0 = (int64_t)j * BLK;
+        if(kv0 <= q0 + 31) {
+            const int lim = (int)(qi - kv0) - 4 * lh;
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
+                const f32x16 sc = dot_rows16(sK[st], sub, lq, lh, qf, zero16());
+                f32x16 dp = dot_rows16(sV[st], sub, lq, lh, of, zero16());
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) <= lim
+                                         ? __builtin_amdgcn_exp2f(sc[r] - l2)
+                                         : 0.0f;
+                    dp[r] = pr * (dp[r] - dd);
+                }
+#pragma unroll
+                for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols16(sKt[st], sub, cb, lq, lh, dp, dq[cb]);
+            }
+        }
+        if(more) {
+            put_rows(sK[st ^ 1], rk);
+            put_cols(sKt[st ^ 1], rk);
+            put_rows(sV[st ^ 1], rv);
+        }
+    }
+    store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
+}
+
 int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, const void* a,
                 const void* b, const void* c) {
     if(B < 0 || H < 1 || T < 0) return pk::fail("%s: bad sizes", who);
@@ -485,13 +799,15 @@ extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) {
     return hd == HD && T > 0 && T % ROWS == 0;
 }
 
-extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                                     const float* q, const float* k, const float* v, float* o,
-                                     float* lse, pk_stream_t stream) {
-    int rc = flash_check("pk_flash_attn_fwd_f32", B, H, T, hd, q, k, v);
+namespace {
+
+int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
+                     float scale, const float* q, const float* k, const float* v, float* o,
+                     float* lse, pk_stream_t stream) {
+    int rc = flash_check(who, B, H, T, hd, q, k, v);
     if(rc) return rc;
     if(B == 0 || T == 0) return PK_OK;
-    if(!o || !pk::aligned16(o)) return pk::fail("pk_flash_attn_fwd_f32: o NULL or unaligned");
+    if(!o || !pk::aligned16(o)) return pk::fail("%s: o NULL or unaligned", who);
     FlashParams p = {};
     p.q = q;
     p.k = k;
@@ -504,30 +820,50 @@ extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd
     p.D = H * HD;
     p.scale = scale;
     const unsigned grid = (unsigned)(B * H * (T / ROWS));
-    flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
-    return pk::launch_status("pk_flash_attn_fwd_f32");
+    if(bf16)
+        flash_fwd_bf16<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
+    else
+        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
+    return pk::launch_status(who);
+}
+
+}  // namespace
+
+extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                                     const float* q, const float* k, const float* v, float* o,
+                                     float* lse, pk_stream_t stream) {
+    return flash_fwd_launch("pk_flash_attn_fwd_f32", false, B, H, T, hd, scale, q, k, v, o, lse,
+                            stream);
+}
+
+extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
+                                          float scale, const float* q, const float* k,
+                                          const float* v, float* o, float* lse,
+                                          pk_stream_t stream) {
+    return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", true, B, H, T, hd, scale, q, k, v, o,
+                            lse, stream);
 }
 
 extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
     return B > 0 && H > 0 && T > 0 ? (size_t)(2 * B * H * T) * sizeof(float) : 0;
 }
 
-extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                                     const float* q, const float* k, const float* v,
-                                     const float* o, const float* lse, const float* dout,
-                                     float* dq, float* dk, float* dv, void* workspace,
-                                     size_t workspace_bytes, int flags, pk_stream_t stream) {
-    int rc = flash_check("pk_flash_attn_bwd_f32", B, H, T, hd, q, k, v);
+namespace {
+
+int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
+                     float scale, const float* q, const float* k, const float* v, const float* o,
+                     const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                     void* workspace, size_t workspace_bytes, int flags, pk_stream_t stream) {
+    int rc = flash_check(who, B, H, T, hd, q, k, v);
     if(rc) return rc;
     if(B == 0 || T == 0) return PK_OK;
-    if(!o || !lse || !dout || !dq || !dk || !dv)
-        return pk::fail("pk_flash_attn_bwd_f32: NULL pointer");
+    if(!o || !lse || !dout || !dq || !dk || !dv) return pk::fail("%s: NULL pointer", who);
     if(!pk::aligned16(o) || !pk::aligned16(dout) || !pk::aligned16(dq) || !pk::aligned16(dk) ||
        !pk::aligned16(dv))
-        return pk::fail("pk_flash_attn_bwd_f32: o, dout, dq, dk, dv must be 16-byte aligned");
+        return pk::fail("%s: o, dout, dq, dk, dv must be 16-byte aligned", who);
     if(!workspace || workspace_bytes < pk_flash_attn_bwd_workspace(B, H, T))
-        return pk::fail("pk_flash_attn_bwd_f32: workspace needs %zu bytes",
-                        pk_flash_attn_bwd_workspace(B, H, T));
+        return pk::fail("%s: workspace needs %zu bytes", who, pk_flash_attn_bwd_workspace(B, H, T));
+    if(!pk::aligned16(workspace)) return pk::fail("%s: workspace must be 16-byte aligned", who);
     FlashParams p = {};
     p.q = q;
     p.k = k;
@@ -548,10 +884,37 @@ extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd
     p.flags = flags;
     hipStream_t st = pk::as_stream(stream);
     flash_dsum<<<pk::grid_for(B * H * T, 256), 256, 0, st>>>(p);
-    if((rc = pk::launch_status("pk_flash_attn_bwd_f32 (row constants)"))) return rc;
+    if((rc = pk::launch_status(who))) return rc;
     const unsigned grid = (unsigned)(B * H * (T / ROWS));
-    flash_bwd_dkdv<<<grid, 256, 0, st>>>(p);
-    if((rc = pk::launch_status("pk_flash_attn_bwd_f32 (dK, dV)"))) return rc;
-    flash_bwd_dq<<<grid, 256, 0, st>>>(p);
-    return pk::launch_status("pk_flash_attn_bwd_f32 (dQ)");
+    if(bf16)
+        flash_bwd_dkdv_bf16<<<grid, 256, 0, st>>>(p);
+    else
+        flash_bwd_dkdv<<<grid, 256, 0, st>>>(p);
+    if((rc = pk::launch_status(who))) return rc;
+    if(bf16)
+        flash_bwd_dq_bf16<<<grid, 256, 0, st>>>(p);
+    else
+        flash_bwd_dq<<<grid, 256, 0, st>>>(p);
+    return pk::launch_status(who);
+}
+
+}  // namespace
+
+extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
+                                     const float* q, const float* k, const float* v,
+                                     const float* o, const float* lse, const float* dout,
+                                     float* dq, float* dk, float* dv, void* workspace,
+                                     size_t workspace_bytes, int flags, pk_stream_t stream) {
+    return flash_bwd_launch("pk_flash_attn_bwd_f32", false, B, H, T, hd, scale, q, k, v, o, lse,
+                            dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
+}
+
+extern "C" int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
+                                          float scale, const float* q, const float* k,
+                                          const float* v, const float* o, const float* lse,
+                                          const float* dout, float* dq, float* dk, float* dv,
+                                          void* workspace, size_t workspace_bytes, int flags,
+                                          pk_stream_t stream) {
+    return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", true, B, H, T, hd, scale, q, k, v, o,
+                            lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
 }

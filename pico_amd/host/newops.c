@@ -185,7 +185,7 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
  * batched GEMMs and causal-softmax kernels runs and saves the probabilities
  * P [B*H, T, T] (arena device memory). */
 enum { AS_LSE = 0, AS_P = 1 };
-enum { AI_B = 0, AI_H = 1, AI_FLASH = 2 };
+enum { AI_B = 0, AI_H = 1, AI_FLASH = 2, AI_BF16 = 3 };
 
 static void attn_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
@@ -211,9 +211,10 @@ static void attn_backward(struct PicoTensor* self) {
     }
     int st;
     if(flash)
-        st = pk_flash_attn_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data, self->data,
-                                   (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad,
-                                   ws, ws_bytes, flags, pkh_stream());
+        st = (n->ival[AI_BF16] ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
+            B, H, T, hd, n->fval[0], q->data, k->data, v->data, self->data,
+            (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad, ws, ws_bytes, flags,
+            pkh_stream());
     else
         st = pk_attn_causal_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
                                     (const float*)n->saved[AS_P], dout, q->grad, k->grad, v->grad,
@@ -252,9 +253,13 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     n->ival[AI_B] = B;
     n->ival[AI_H] = H;
     n->ival[AI_FLASH] = flash;
+    /* the matmul precision switch covers attention's products too; the
+     * backward uses the precision the forward ran in */
+    n->ival[AI_BF16] = flash && pico_get_matmul_precision() == PICO_MATMUL_BF16;
     n->fval[0] = 1.0f / sqrtf((float)hd);
-    int st = flash ? pk_flash_attn_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
-                                           out->data, lse, pkh_stream())
+    int st = flash ? (n->ival[AI_BF16] ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
+                         B, H, T, hd, n->fval[0], q->data, k->data, v->data, out->data, lse,
+                         pkh_stream())
                    : pk_attn_causal_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
                                             out->data, lse, P, pkh_stream());
     if(pkh_status("pico_attention_causal", st)) return NULL;

@@ -327,23 +327,34 @@ def flash_supported(T, hd):
     return bool(hip_lib().pk_flash_attn_supported(T, hd))
 
 
-def flash_fwd(B, H, q, k, v, o, lse, scale=None):
-    BT, D = q.shape
+def _flash_shapes(B, H, *ts):
+    BT, D = ts[0].shape
     T, hd = BT // B, D // H
-    if B * T != BT or H * hd != D or lse.numel() < B * H * T or o.shape != q.shape:
+    _f32(*ts)
+    if B * T != BT or H * hd != D or any(t.shape != ts[0].shape for t in ts):
+        raise ValueError("attention shape mismatch")
+    return T, hd
+
+
+def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False):
+    """Fused causal attention; bf16=True rounds the matrix-product operands to
+    bf16 (pk_flash_attn_fwd_bf16_f32)."""
+    T, hd = _flash_shapes(B, H, q, k, v, o)
+    if lse.numel() < B * H * T:
         raise ValueError("attention shape mismatch")
     scale = hd ** -0.5 if scale is None else scale
-    check("pk_flash_attn_fwd_f32", hip_lib().pk_flash_attn_fwd_f32(
+    name = "pk_flash_attn_fwd_bf16_f32" if bf16 else "pk_flash_attn_fwd_f32"
+    check(name, getattr(hip_lib(), name)(
         B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
 
 
-def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None):
-    BT, D = q.shape
-    T, hd = BT // B, D // H
+def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False):
+    T, hd = _flash_shapes(B, H, q, k, v, o, dout, dq, dk, dv)
     scale = hd ** -0.5 if scale is None else scale
     need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
     ws = torch.empty(max(1, need // 4), device=q.device, dtype=torch.float32)
-    check("pk_flash_attn_bwd_f32", hip_lib().pk_flash_attn_bwd_f32(
+    name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
+    check(name, getattr(hip_lib(), name)(
         B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout), _ptr(dq),
         _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() * 4, flags, _stream()))
 
