@@ -37,6 +37,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 struct FlashParams {
     const float *q, *k, *v, *o, *dout, *lse, *dsum;
     float *out, *lse_out, *dq, *dk, *dv, *dsum_out;
+    float* ds;  // dS tiles: written by the dK/dV kernel, read by the dQ kernel
     int64_t B, H, T, D;  // D = H*64, the row stride
     float scale;         // softmax scale (normally 1/8)
     int flags;
@@ -189,6 +190,12 @@ struct BlockLoad {
 // included); a barrier after it publishes every wave's loads
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// The loop bodies take the block being read and the buffer being loaded as
+// __restrict__ pointers: that tells the compiler the two never overlap, so
+// the direct-to-LDS loads can run under the reads.  (Without it the compiler
+// has to assume they may overlap and waits for every direct-to-LDS load
+// before the next LDS read, which serialises the double buffering.)
+
 // ======================================================================= forward
 // Workgroup: 128 queries of one (b, h), 4 waves of 32.  Heaviest query blocks
 // (the ones that see the most keys) are dispatched first.
@@ -226,8 +233,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     f32x16 s[2] = {dot_rows(sK[0], 0, lq, lh, qf, zero16()),
                    dot_rows(sK[0], 1, lq, lh, qf, zero16())};
 
-    // softmax of block j's scores s, then o += V(j)^T . P^T
-    auto soft_pv = [&](int j) {
+    // softmax of block j's scores s (o rescaled to the new running max)
+    auto softmax = [&](int j) {
         // key kv0 + sub*32 + acc_row(r, lh) is hidden from query qi when it
         // exceeds qi; lim folds the lane's offsets into one compare per element
         const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;
@@ -258,7 +265,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
             o[0][r] *= alpha;
             o[1][r] *= alpha;
         }
-        const float* tv = sV[j & 1];
+    };
+    // o += V(j)^T . P^T
+    auto pv = [&](const float* tv) {
 #pragma unroll
         for(int cb = 0; cb < 2; ++cb) {
             o[cb] = dot_cols(tv, 0, cb, lq, lh, s[0], o[cb]);
@@ -267,26 +276,37 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     };
     // top of iteration j: K(j+1) and V(j) have landed, and sK[j&1] (K(j)) and
     // sV[(j+1)&1] (V(j-1)) are free for K(j+2) and V(j+1)
-    auto next_loads = [&](int j) {
+    auto next_loads = [&](int j, float* __restrict__ kd, float* __restrict__ vd) {
         wait_loads();
         __syncthreads();
-        if(j + 2 < nkv) ld.issue(rk, p.D, (int64_t)(j + 2) * BLK, sK[j & 1], w);
-        if(j + 1 < nkv) ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
+        if(j + 2 < nkv) ld.issue(rk, p.D, (int64_t)(j + 2) * BLK, kd, w);
+        if(j + 1 < nkv) ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, vd, w);
+    };
+    // a block with a successor this wave sees
+    auto steady = [&](int j, const float* __restrict__ tk, const float* __restrict__ tv,
+                      float* __restrict__ kd, float* __restrict__ vd) {
+        next_loads(j, kd, vd);
+        // the next block's scores (MFMA) under this block's softmax (VALU) ...
+        const f32x16 n0 = dot_rows(tk, 0, lq, lh, qf, zero16());
+        const f32x16 n1 = dot_rows(tk, 1, lq, lh, qf, zero16());
+        softmax(j);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(tv);  // ... then P.V: kept apart so the V reads are not hoisted above
+        __builtin_amdgcn_sched_barrier(0);
+        s[0] = n0;
+        s[1] = n1;
+    };
+    auto last = [&](int j, const float* __restrict__ tv, float* __restrict__ kd,
+                    float* __restrict__ vd) {
+        next_loads(j, kd, vd);
+        softmax(j);
+        pv(tv);
     };
 
     int j = 0;
-    for(; j + 1 < nw; ++j) {  // blocks with a successor this wave sees
-        next_loads(j);
-        const float* tk = sK[(j + 1) & 1];
-        const f32x16 n0 = dot_rows(tk, 0, lq, lh, qf, zero16());
-        const f32x16 n1 = dot_rows(tk, 1, lq, lh, qf, zero16());
-        soft_pv(j);
-        s[0] = n0;
-        s[1] = n1;
-    }
-    next_loads(j);  // the wave's last block
-    soft_pv(j);
-    for(++j; j < nkv; ++j) next_loads(j);  // keep loading for the other waves
+    for(; j + 1 < nw; ++j) steady(j, sK[(j + 1) & 1], sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);
+    last(j, sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);  // the wave's last block
+    for(++j; j < nkv; ++j) next_loads(j, sK[j & 1], sV[(j + 1) & 1]);  // loads for the others
     store_rowT(p.out + base + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
@@ -321,6 +341,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t consts_rsrc(const float* ws, i
                                              (int)(2 * T * 4), 0x00020000);
 }
 
+// dS of one (b, h) is kept as 32x32 tiles, one per (query group qg, key group
+// kg) with kg <= qg, packed by rows of that triangle: tile qg*(qg+1)/2 + kg.
+// Inside a tile the 16 values that the dQ kernel's lane (q, h) multiplies --
+// keys 8(s/4) + 4h + s%4 for s = 0..15, the accumulator-row order -- are the
+// consecutive floats (2q + h)*16 + s, so the dQ kernel reads a tile as one
+// contiguous 4 KB stream; the dK/dV kernel writes it 128 bytes per row.
+__host__ __device__ __forceinline__ int64_t ds_tiles(int64_t T) {
+    return (T / 32) * (T / 32 + 1) / 2;
+}
+__device__ __forceinline__ int64_t ds_tile(int64_t bh, int64_t T, int64_t qg, int64_t kg) {
+    return (bh * ds_tiles(T) + qg * (qg + 1) / 2 + kg) * 1024;
+}
+
 // ================================================================ backward: dK, dV
 // Workgroup: 128 keys of one (b, h), one key per lane; query blocks of 64 with
 // q >= key stream through LDS (Q and dO rows, their L2 and D), loaded
@@ -328,8 +361,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t consts_rsrc(const float* ws, i
 //   S = Q.K^T (per lane: its key's column)        P = exp2(S' - L2)
 //   dV^T += dO^T.P         dP = dO.V^T           dS = P*(dP - D)
 //   dK^T += Q^T.dS  (x scale at the end)
-// Both 32-query halves of a block get their scores first, so the
-// exponentials of one half run while the other half's products are in flight.
+// The two 32-query halves of a block run one after the other (two waves per
+// SIMD overlap one's exponentials with the other's products).  dS goes to the
+// tile store for the dQ kernel.
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sQ[2][TILE];
     __shared__ __attribute__((aligned(16))) float sO[2][TILE];      // dO rows
@@ -347,123 +381,149 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.D);
     const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + base, p.T, p.D);
     const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.T);
-    auto issue = [&](int j, int st) {
-        ld.issue(rq, p.D, (int64_t)j * BLK, sQ[st], w);
-        ld.issue(ro, p.D, (int64_t)j * BLK, sO[st], w);
+    auto issue = [&](int j, float* __restrict__ tq, float* __restrict__ to,
+                     float* __restrict__ tl) {
+        ld.issue(rq, p.D, (int64_t)j * BLK, tq, w);
+        ld.issue(ro, p.D, (int64_t)j * BLK, to, w);
         if(w == 1 && l < 32)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)sLD[st], 16, 16 * l,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)tl, 16, 16 * l,
                                                      (unsigned)(j * 2 * BLK * 4), 0, 0);
     };
     const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
-    issue(j0, 0);
+    issue(j0, sQ[0], sO[0], sLD[0]);
     float kf[32], vf[32];
     load_frag32(K + ki * p.D, lh, kf, p.scale * kLog2e);
     load_frag32(V + ki * p.D, lh, vf, 1.0f);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
+    // this lane's column of every dS tile of key group kg (rows 32 floats apart)
+    const int64_t kg = k0 / 32;
+    float* dsk = p.ds + ds_tile(bh, p.T, 0, 0) + ((lq >> 2) & 1) * 16 + 4 * (lq >> 3) + (lq & 3);
 
-    for(int j = j0; j < nq; ++j) {
-        const int st = (j - j0) & 1;
+    // iteration j reads buffer set st = (j - j0) & 1 and loads block j+1 into
+    // the other one
+    auto iter = [&](int j, const float* __restrict__ tq, const float* __restrict__ to,
+                    const float* __restrict__ tl, float* __restrict__ nq_, float* __restrict__ no_,
+                    float* __restrict__ nl_) {
         wait_loads();
-        __syncthreads();  // block j is in; buffer st^1 (block j-1) is free
-        if(j + 1 < nq) issue(j + 1, st ^ 1);
+        __syncthreads();  // block j is in; the other set (block j-1) is free
+        if(j + 1 < nq) issue(j + 1, nq_, no_, nl_);
         const int64_t qs = (int64_t)j * BLK;
         if(qs + BLK - 1 >= k0) {  // some query of this block sees this wave's keys
-            const float *tq = sQ[st], *to = sO[st], *tl = sLD[st];
-            f32x16 s[2], dp[2];
-#pragma unroll
-            for(int sub = 0; sub < 2; ++sub) {
-                s[sub] = dot_rows(tq, sub, lq, lh, kf, zero16());
-                dp[sub] = dot_rows(to, sub, lq, lh, vf, zero16());
-            }
             // query qs + sub*32 + acc_row(r, lh) sees key ki when it is >= ki
             const int lim = (int)(ki - qs) - 4 * lh;
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
+                f32x16 sc = dot_rows(tq, sub, lq, lh, kf, zero16());
+                f32x16 dp = dot_rows(to, sub, lq, lh, vf, zero16());
+                // one 128-bit operand read per 4 products, so the reads are
+                // not all hoisted into registers at once
+#pragma unroll
+                for(int i = 0; i < 16; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                }
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
                     const int qr = sub * 32 + acc_row(r, lh);
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim
-                                         ? __builtin_amdgcn_exp2f(s[sub][r] - tl[qr])
-                                         : 0.0f;
-                    s[sub][r] = pr;
-                    dp[sub][r] = pr * (dp[sub][r] - tl[BLK + qr]);
+                    // read and exponentiate unconditionally, then select: the
+                    // masked lanes' values are discarded
+                    const float e = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim ? e : 0.0f;
+                    sc[r] = pr;
+                    dp[r] = pr * (dp[r] - tl[BLK + qr]);
                 }
+                const int64_t qg = 2 * j + sub;
+                if(qg >= kg) {
+                    float* t = dsk + (qg * (qg + 1) / 2 + kg) * 1024;
+#pragma unroll
+                    for(int r = 0; r < 16; ++r) t[acc_row(r, lh) * 32] = dp[r];
+                }
+                // keep the dV/dK operand reads of this half below its softmax
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb) {
-                    dv[cb] = dot_cols(to, sub, cb, lq, lh, s[sub], dv[cb]);
-                    dk[cb] = dot_cols(tq, sub, cb, lq, lh, dp[sub], dk[cb]);
+                    dv[cb] = dot_cols(to, sub, cb, lq, lh, sc, dv[cb]);
+                    dk[cb] = dot_cols(tq, sub, cb, lq, lh, dp, dk[cb]);
                 }
+#pragma unroll
+                for(int i = 0; i < 32; ++i) {  // two 32-bit reads per 2 products
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+    };
+    for(int j = j0; j < nq; ++j) {
+        const int st = (j - j0) & 1;
+        iter(j, sQ[st], sO[st], sLD[st], sQ[st ^ 1], sO[st ^ 1], sLD[st ^ 1]);
     }
     store_rowT(p.dv + base + ki * p.D, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
     store_rowT(p.dk + base + ki * p.D, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
 }
 
 // =================================================================== backward: dQ
-// Workgroup: 128 queries of one (b, h), one query per lane; key blocks of 64
-// with key <= query stream through LDS (K and V rows), loaded straight into
-// LDS one block ahead.
-//   S^T = K.Q^T   P^T = exp2(S'^T - L2)   dP^T = V.dO^T   dS^T = P^T*(dP^T - D)
-//   dQ^T += K^T.dS^T  (x scale at the end)
+// Workgroup: 128 queries of one (b, h), one query per lane.  dQ^T += K^T.dS^T
+// (x scale at the end) over the key blocks of 64 with key <= query: K blocks
+// stream through LDS one block ahead, the dS tiles the dK/dV kernel stored
+// are read straight into registers one block ahead.
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
-    __shared__ __attribute__((aligned(16))) float sV[2][TILE];
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.D + h * HD;
-    const float *Q = p.q + base, *dO = p.dout + base;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
-    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq, qg = q0 / 32;
 
     const BlockLoad ld(p.D, w, l);
     const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.D);
-    const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v + base, p.T, p.D);
     ld.issue(rk, p.D, 0, sK[0], w);
-    ld.issue(rv, p.D, 0, sV[0], w);
-    float qf[32], of[32];
-    load_frag32(Q + qi * p.D, lh, qf, p.scale * kLog2e);
-    load_frag32(dO + qi * p.D, lh, of, 1.0f);
-    const float* cst = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
-    const float l2 = cst[0], dd = cst[BLK];
+    // tile (qg, kg) is at ds + kg*1024; this lane's 16 values at (2*lq + lh)*16
+    const float* ds = p.ds + ds_tile(bh, p.T, qg, 0) + (2 * lq + lh) * 16;
+    auto fetch = [&](int j, f32x16 (&x)[2]) {
+#pragma unroll
+        for(int sub = 0; sub < 2; ++sub) {
+            const int64_t kg = 2 * j + sub;
+            if(kg <= qg) {
+                const f32x4* src = reinterpret_cast<const f32x4*>(ds + kg * 1024);
+#pragma unroll
+                for(int i = 0; i < 4; ++i) {
+                    const f32x4 v = src[i];
+#pragma unroll
+                    for(int e = 0; e < 4; ++e) x[sub][4 * i + e] = v[e];
+                }
+            }
+        }
+    };
     f32x16 dq[2] = {zero16(), zero16()};
-
+    f32x16 cur[2] = {zero16(), zero16()}, nxt[2] = {zero16(), zero16()};
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
-    for(int j = 0; j < nkv; ++j) {
-        const int st = j & 1;
+    const int nw = (int)((q0 + 31) / BLK) + 1;  // key blocks this wave sees
+    fetch(0, cur);
+    auto iter = [&](int j, const float* __restrict__ tk, float* __restrict__ kd) {
         wait_loads();
         __syncthreads();
-        if(j + 1 < nkv) {
-            ld.issue(rk, p.D, (int64_t)(j + 1) * BLK, sK[st ^ 1], w);
-            ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, sV[st ^ 1], w);
-        }
-        const int64_t kv0 = (int64_t)j * BLK;
-        if(kv0 <= q0 + 31) {
-            const float *tk = sK[st], *tv = sV[st];
-            f32x16 s[2], dp[2];
+        if(j + 1 < nkv) ld.issue(rk, p.D, (int64_t)(j + 1) * BLK, kd, w);
+        if(j + 1 < nw) fetch(j + 1, nxt);
+        if(j < nw) {
+            const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;  // key offset <= lim visible
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
-                s[sub] = dot_rows(tk, sub, lq, lh, qf, zero16());
-                dp[sub] = dot_rows(tv, sub, lq, lh, of, zero16());
-            }
-            const int lim = (int)(qi - kv0) - 4 * lh;  // key kv0 + k visible when k <= lim
+                if(2 * j + sub > qg) continue;  // the whole key group is in this wave's future
 #pragma unroll
-            for(int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-                for(int r = 0; r < 16; ++r) {
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) <= lim
-                                         ? __builtin_amdgcn_exp2f(s[sub][r] - l2)
-                                         : 0.0f;
-                    dp[sub][r] = pr * (dp[sub][r] - dd);
-                }
+                for(int r = 0; r < 16; ++r)
+                    if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) cur[sub][r] = 0.0f;
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb)
-                    dq[cb] = dot_cols(tk, sub, cb, lq, lh, dp[sub], dq[cb]);
+                    dq[cb] = dot_cols(tk, sub, cb, lq, lh, cur[sub], dq[cb]);
             }
+            cur[0] = nxt[0];
+            cur[1] = nxt[1];
         }
-    }
+    };
+    for(int j = 0; j < nkv; ++j) iter(j, sK[j & 1], sK[(j + 1) & 1]);
     store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
@@ -699,9 +759,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
                     const int qr = sub * 32 + acc_row(r, lh);
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim
-                                         ? __builtin_amdgcn_exp2f(sc[r] - tl[qr])
-                                         : 0.0f;
+                    const float e = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
+                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim ? e : 0.0f;
                     sc[r] = pr;
                     dp[r] = pr * (dp[r] - tl[BLK + qr]);
                 }
@@ -844,8 +903,10 @@ extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64
                             lse, stream);
 }
 
+// row constants (2*B*H*T floats), then the dS tiles
 extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
-    return B > 0 && H > 0 && T > 0 ? (size_t)(2 * B * H * T) * sizeof(float) : 0;
+    if(B <= 0 || H <= 0 || T <= 0) return 0;
+    return (size_t)(2 * B * H * T + B * H * ds_tiles(T) * 1024) * sizeof(float);
 }
 
 namespace {
@@ -876,6 +937,7 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.dv = dv;
     p.dsum = static_cast<const float*>(workspace);
     p.dsum_out = static_cast<float*>(workspace);
+    p.ds = static_cast<float*>(workspace) + 2 * B * H * T;
     p.B = B;
     p.H = H;
     p.T = T;
