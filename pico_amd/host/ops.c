@@ -157,23 +157,29 @@ int pico_set_matmul_precision(int precision) {
 
 int pico_get_matmul_precision(void) { return g_matmul_precision; }
 
-/* products with too few output tiles (weight gradients) split K through the
- * library workspace; see pk_gemm_ex_f32 */
-int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
-             int64_t ldc, int flags) {
+/* products with too few output tiles (weight gradients) split K through a
+ * workspace; see pk_gemm_ex_f32.  On the side stream (side != 0) the product
+ * uses the side stream's own workspace. */
+static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
+                   char tc, int64_t ldc, int flags, pk_stream_t st, int side) {
     const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
     size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
-    void* ws = ws_bytes ? pkh_workspace(ws_bytes) : NULL;
+    void* ws = ws_bytes ? (side ? pkh_side_workspace(ws_bytes) : pkh_workspace(ws_bytes)) : NULL;
     if(!ws) ws_bytes = 0;
     int (*gemm)(char, char, int64_t, int64_t, int64_t, float, const float*, int64_t,
                 const float*, int64_t, float, float*, int64_t, void*, size_t, pk_stream_t) =
         g_matmul_precision == PICO_MATMUL_BF16 ? pk_gemm_ex_bf16_f32 : pk_gemm_ex_f32;
     if(tc == 'N')
         return gemm(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws, ws_bytes,
-                    pkh_stream());
+                    st);
     /* C stored transposed: produce C^T [N, M] = B^T . A^T */
     return gemm(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc, ws,
-                ws_bytes, pkh_stream());
+                ws_bytes, st);
+}
+
+int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
+             int64_t ldc, int flags) {
+    return gemm_on(A, B, M, N, K, C, tc, ldc, flags, pkh_stream(), 0);
 }
 
 static int matmul_views(struct PicoTensor* a, struct PicoTensor* b, struct PkMat* va,
@@ -198,7 +204,14 @@ int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTenso
 
 /* src/autograd.h:96-130: dA += dC . B^T, then dB += A^T . dC.  Each grad is
  * laid out with its tensor's strides, so a transposed view's grad is
- * produced transposed. */
+ * produced transposed.
+ *
+ * When b is a parameter (persistent) and a is not, dB -- a weight gradient,
+ * read only once the backward is over -- goes to the side stream and runs
+ * concurrently with the rest of the backward; the main stream waits for it
+ * before it next touches b's grad and at the end of pico_backward.  Writes to
+ * one grad keep their program order either way, so results are bit for bit
+ * those of a single stream. */
 void pico_matmul_backward_gpu(struct PicoTensor* self) {
     struct PicoTensor *a = self->parents[0], *b = self->parents[1];
     const float* g = pkh_upstream(self);
@@ -212,7 +225,17 @@ void pico_matmul_backward_gpu(struct PicoTensor* self) {
     int st = pkh_gemm(dC, BT, M, K, N, a->grad, va.t, va.ld, pkh_grad_flag(a));
     if(pkh_status("pico_matmul_backward", st)) return;
     pkh_grad_mark(a);
-    st = pkh_gemm(AT, dC, K, N, M, b->grad, vb.t, vb.ld, pkh_grad_flag(b));
+    struct PkNode* nb = pkh_node(b);
+    pk_stream_t side = (nb && b->is_persistent && !a->is_persistent && a != b) ? pkh_side_fork()
+                                                                                : NULL;
+    if(side) {
+        /* the side stream orders this write after every earlier write to b's
+         * grad: main-stream ones through the fork, side ones by issue order */
+        st = gemm_on(AT, dC, K, N, M, b->grad, vb.t, vb.ld, nb->grad_live ? PK_ACCUM : 0, side, 1);
+        nb->side_seq = pkh_side_seq();
+    } else {
+        st = pkh_gemm(AT, dC, K, N, M, b->grad, vb.t, vb.ld, pkh_grad_flag(b));
+    }
     if(pkh_status("pico_matmul_backward", st)) return;
     pkh_grad_mark(b);
 }

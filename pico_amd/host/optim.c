@@ -192,6 +192,7 @@ static int adamw_table(struct PicoOptimAdamW* o) {
 
 void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
     if(!o) return;
+    pkh_side_join(); /* the grads are read on the main stream */
     if(adamw_table(o)) return; /* the failing call recorded the error */
     o->t++;
     int32_t* step = (int32_t*)o->state;

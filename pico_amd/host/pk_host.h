@@ -28,6 +28,7 @@ struct PkNode {
     uint64_t visit;
     uint32_t seed_one; /* this node is the entry pico_backward seeded with 1 */
     uint32_t pad_;
+    uint64_t side_seq; /* the side-stream fork that last wrote this grad (0: none) */
     void* saved[PKH_MAX_SAVED];
     int64_t ival[PKH_MAX_SAVED];
     float fval[PKH_MAX_SAVED];
@@ -47,6 +48,23 @@ void pkh_set_error(const char* fmt, ...);
 int pkh_status(const char* op, int status);
 int pkh_sync(void);
 int pkh_capturing(void); /* a graph capture is in progress */
+
+/* The side stream: weight gradients (dW = X^T.dY of a parameter) run there,
+ * concurrently with the rest of the backward on the library's stream.
+ * pkh_side_fork() makes it wait for everything issued so far on the main
+ * stream and returns it (NULL if it cannot be created: run on the main
+ * stream then); each fork gets a sequence number (pkh_side_seq).
+ * pkh_side_join() makes the main stream wait for everything issued on the
+ * side stream; pkh_side_joined() is the last sequence number a join covers.
+ * Any main-stream access to a grad written on the side stream joins first
+ * (pkh_grad_flag / pkh_grad_is_live do it), pico_backward joins at its end,
+ * and so do synchronisation and copies. */
+pk_stream_t pkh_side_fork(void);
+uint64_t pkh_side_seq(void);
+uint64_t pkh_side_joined(void);
+void pkh_side_join(void);
+/* the side stream's own scratch buffer (pkh_workspace is the main stream's) */
+void* pkh_side_workspace(size_t bytes);
 
 /* AdamW state, for checkpoints (optim.c) */
 int pkh_adamw_moments(const struct PicoOptimAdamW* o, const struct PicoTensor* p, float** m,
@@ -73,8 +91,13 @@ struct Arena* pkh_need_arena(void);
 int pkh_is_gpu(const struct PicoTensor* t);
 /* flags for a write into t->grad: PK_ACCUM if it already holds values; the
  * caller marks it live after a successful launch */
+/* before the main stream touches t's grad: wait for side-stream writes to it */
+static inline void pkh_grad_on_main(const struct PkNode* n) {
+    if(n && n->side_seq > pkh_side_joined()) pkh_side_join();
+}
 static inline int pkh_grad_flag(const struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
+    pkh_grad_on_main(n);
     return (n && !n->grad_live) ? 0 : PK_ACCUM;
 }
 static inline void pkh_grad_mark(struct PicoTensor* t) {
@@ -83,6 +106,7 @@ static inline void pkh_grad_mark(struct PicoTensor* t) {
 }
 static inline int pkh_grad_is_live(const struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
+    pkh_grad_on_main(n);
     return n ? (int)n->grad_live : 1;
 }
 void pkh_set_parents(struct Arena* arena, struct PicoTensor* out, int n,

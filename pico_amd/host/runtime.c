@@ -32,6 +32,14 @@ static int g_capture_failed = 0;
 static void* g_ws = NULL;
 static size_t g_ws_bytes = 0;
 
+/* the side stream (weight gradients), its fork/join events and scratch */
+static hipStream_t g_side = NULL;
+static hipEvent_t g_fork_ev = NULL, g_join_ev = NULL;
+static uint64_t g_side_seq = 0, g_side_joined = 0;
+static int g_side_broken = 0;
+static void* g_side_ws = NULL;
+static size_t g_side_ws_bytes = 0;
+
 void pkh_set_error(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -71,10 +79,20 @@ void pico_init(void) { (void)pkh_init(); }
 
 void pico_shutdown(void) {
     if(!g_ready) return;
+    pkh_side_join();
     hipStreamSynchronize(g_own_stream);
     if(g_ws) pkh_device_free(g_ws);
     g_ws = NULL;
     g_ws_bytes = 0;
+    if(g_side) {
+        if(g_side_ws) pkh_device_free(g_side_ws);
+        g_side_ws = NULL;
+        g_side_ws_bytes = 0;
+        hipEventDestroy(g_fork_ev);
+        hipEventDestroy(g_join_ev);
+        hipStreamDestroy(g_side);
+        g_side = NULL;
+    }
     hipStreamDestroy(g_own_stream);
     g_own_stream = NULL;
     g_ready = 0;
@@ -104,9 +122,62 @@ int pkh_status(const char* op, int status) {
     return status;
 }
 
+pk_stream_t pkh_side_fork(void) {
+    if(pkh_init() || g_side_broken) return NULL;
+    if(!g_side) {
+        /* default priority, like the main stream */
+        hipError_t e = hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking);
+        if(e == hipSuccess) e = hipEventCreateWithFlags(&g_fork_ev, hipEventDisableTiming);
+        if(e == hipSuccess) e = hipEventCreateWithFlags(&g_join_ev, hipEventDisableTiming);
+        if(e != hipSuccess) {
+            (void)hipGetLastError();
+            g_side_broken = 1;
+            return NULL;
+        }
+    }
+    hipError_t e = hipEventRecord(g_fork_ev, (hipStream_t)pkh_stream());
+    if(e == hipSuccess) e = hipStreamWaitEvent(g_side, g_fork_ev, 0);
+    if(e != hipSuccess) {
+        pkh_status("side stream fork", (int)e);
+        return NULL;
+    }
+    ++g_side_seq;
+    return (pk_stream_t)g_side;
+}
+
+uint64_t pkh_side_seq(void) { return g_side_seq; }
+uint64_t pkh_side_joined(void) { return g_side_joined; }
+
+void pkh_side_join(void) {
+    if(g_side_joined == g_side_seq) return;
+    hipError_t e = hipEventRecord(g_join_ev, g_side);
+    if(e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)pkh_stream(), g_join_ev, 0);
+    if(e != hipSuccess) {
+        /* cannot order the streams: wait for the side stream from the host */
+        pkh_status("side stream join", (int)e);
+        hipStreamSynchronize(g_side);
+    }
+    g_side_joined = g_side_seq;
+}
+
+void* pkh_side_workspace(size_t bytes) {
+    if(bytes <= g_side_ws_bytes) return g_side_ws;
+    if(capture_refuses("growing the side-stream workspace")) return NULL;
+    if(g_side_ws) {
+        hipStreamSynchronize(g_side);
+        pkh_device_free(g_side_ws);
+        g_side_ws = NULL;
+        g_side_ws_bytes = 0;
+    }
+    g_side_ws = pkh_device_alloc(bytes);
+    if(g_side_ws) g_side_ws_bytes = bytes;
+    return g_side_ws;
+}
+
 int pkh_sync(void) {
     if(pkh_init()) return -1;
     if(capture_refuses("waiting on the device")) return -1;
+    pkh_side_join();
     hipError_t e = hipStreamSynchronize((hipStream_t)pkh_stream());
     if(e != hipSuccess) return pkh_status("pico_gpu_synchronize", (int)e);
     return 0;
@@ -178,6 +249,7 @@ int pkh_copy_h2d(void* dst, const void* src, size_t bytes) {
     if(pkh_init()) return -1;
     if(capture_refuses("a host-to-device copy")) return -1;
     if(bytes == 0) return 0;
+    pkh_side_join();
     hipStream_t st = (hipStream_t)pkh_stream();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
     if(e == hipSuccess) e = hipStreamSynchronize(st);
@@ -188,6 +260,7 @@ int pkh_copy_d2h(void* dst, const void* src, size_t bytes) {
     if(pkh_init()) return -1;
     if(capture_refuses("a device-to-host copy")) return -1;
     if(bytes == 0) return 0;
+    pkh_side_join();
     hipStream_t st = (hipStream_t)pkh_stream();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st);
     if(e == hipSuccess) e = hipStreamSynchronize(st);
@@ -222,6 +295,7 @@ struct PicoGraph* pico_graph_end(void) {
         PKH_ERR("%s\n", g_err);
         return NULL;
     }
+    pkh_side_join(); /* the side stream's work joins the captured graph */
     hipGraph_t graph = NULL;
     hipError_t e = hipStreamEndCapture((hipStream_t)pkh_stream(), &graph);
     g_capturing = 0;

@@ -456,6 +456,7 @@ void pico_backward(struct Arena* arena, struct PicoTensor* entry) {
         struct PicoTensor* t = order.v[i];
         if(t->_backward) t->_backward(t);
     }
+    pkh_side_join(); /* weight gradients computed on the side stream are in */
     pkh_node(entry)->seed_one = 0;
 done:
     free(order.v);

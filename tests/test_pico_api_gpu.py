@@ -86,6 +86,23 @@ def test_matmul_shared_parent_and_chain(P):
         assert P.grad(bias).tolist() == [2, 2]
 
 
+def test_weight_grad_side_stream_orders_with_main_stream_writes(P):
+    # x.W with x an activation puts dW on the side stream; W*W feeding a
+    # second product writes W's grad on the main stream.  Both contributions
+    # land, whichever runs first: dW[i][k] = s_i (1 + 2 W[i][k]) with
+    # s = column sums of x = (5, 7, 9).  A second graph over the same W then
+    # adds the same again (its intermediates are fresh).
+    w = [1, -2, 3, 0, 2, -1, 4, 1, -3]
+    W = P.param([3, 3], w)
+    want = [s * (1 + 2 * v) for s, v in zip([5] * 3 + [7] * 3 + [9] * 3, w)]
+    for rep in (1, 2):
+        with P.arena():
+            x = P.tensor([2, 3], [1, 2, 3, 4, 5, 6])
+            P.backward(P.add(P.matmul(x, W), P.matmul(x, P.mul(W, W))))
+            assert P.grad(W).tolist() == [rep * v for v in want]
+    P.free(W)
+
+
 def test_matmul_transposed_view_matches_oracle(P, C):
     # a pico_transpose_2d view (tensor.c:230-244) is read as 'T' and its grad
     # lands with the view's strides, as the reference's backward loops index it
