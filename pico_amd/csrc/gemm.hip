@@ -636,7 +636,16 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
 // K split for a product whose output has too few tiles to fill the chip: 2
 // resident workgroups per CU x 256 CUs want >= 512 workgroups.
 //  * K >= 1024 (weight gradients: M, N ~ d_model, K = tokens): slices of at
-//    least 256 (8 LDS stages), 5-16 of them at the training shapes.
+//    least 256 (8 LDS stages).  The split count minimises the estimated time
+//    in units of one 32-deep stage over a full round of 512 workgroups of
+//    128x128 tiles (~3.9 us):
+//        rounds x (stages per split + 2.5 for a workgroup's prologue and
+//        epilogue) + (s + 1) planes of M*N floats for the reduction (~19.5 MB
+//        of HBM traffic per unit).
+//    A second round of workgroups can beat one round that leaves slots idle:
+//    a [768, 4096] gradient with K = 8192 (192 tiles) takes 8 splits (three
+//    rounds of 32 stages) rather than 2 (one round of 128 stages, 384 of 512
+//    slots busy).  [768, 768] takes 14 and [768, 2048] 5.
 //  * 512 <= K < 1024: only when even 64x64 tiles would leave three quarters
 //    of the CUs idle (the MLP's [64, 784] . [784, 128]: 2 tiles); slices of
 //    at least 128, which turns one latency-bound workgroup chain into six.
@@ -650,10 +659,24 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     if(tiles <= 0 || tiles * 2 > kSplitTarget || K < kMinSplitK) return 1;
     if(K < 1024 && ((M + 63) / 64) * ((N + 63) / 64) * 4 >= 256) return 1;
     const int64_t min_slice = K >= 1024 ? 256 : 128;
-    int64_t s = kSplitTarget / tiles;
-    if(s > K / min_slice) s = K / min_slice;
-    if(s < 2) return 1;
-    const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
+    int64_t s_max = K / min_slice;
+    if(s_max > 64) s_max = 64;
+    int64_t best_s = 1;
+    double best = -1.0;
+    const double plane = (double)M * (double)N * 4.0 / 19.5e6;
+    for(int64_t s = 1; s <= s_max; ++s) {
+        const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
+        const int64_t splits = (K + chunk - 1) / chunk;
+        const int64_t rounds = (tiles * splits + kSplitTarget - 1) / kSplitTarget;
+        const double cost = (double)rounds * ((double)(chunk / BK) + 2.5) +
+                            (splits > 1 ? (double)(splits + 1) * plane : 0.0);
+        if(best < 0.0 || cost < best) {
+            best = cost;
+            best_s = s;
+        }
+    }
+    if(best_s < 2) return 1;
+    const int64_t chunk = ((K + best_s - 1) / best_s + BK - 1) / BK * BK;
     *kchunk = chunk;
     return (int)((K + chunk - 1) / chunk);
 }
