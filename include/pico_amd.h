@@ -103,6 +103,13 @@ struct PicoTensor* pico_tensor_from_scalar(float value);           /* tensor.c:1
 void pico_free(struct PicoTensor* tensor);                         /* tensor.c:136-168 */
 void pico_tensor_print(struct PicoTensor* t);                      /* tensor.c:210-228 */
 void pico_transpose_2d(struct PicoTensor* tensor);                 /* tensor.c:230-244 */
+/* n column-block views of t [M, n*C] (contiguous, in the current arena, not a
+ * param): outs[i] is [M, C] with row stride n*C and shares t's data and grad
+ * (no reference counterpart; the reference's only view is pico_transpose_2d).
+ * One product x.[W0|W1|..] split this way feeds several consumers.  Their
+ * gradients land in t's grad directly; the columns of a view that no consumer
+ * wrote read as zeros.  Returns 0, or nonzero for a tensor it cannot split. */
+int pico_split_cols(struct PicoTensor* t, int n, struct PicoTensor** outs);
 /* uniform [0,1) from pico's xorshift32 stream (tensor.c:249-273), drawn on the
  * host in the reference's order and copied to the device */
 struct PicoTensor* pico_rand(struct Arena* arena, int64_t* shape, uint8_t ndim);

@@ -124,6 +124,10 @@ int pk_relu_f32(int64_t n, const float* x, float* y, pk_stream_t stream);
 int pk_relu_bwd_f32(int64_t n, const float* y, const float* gy, float* gx, int flags,
                     pk_stream_t stream);
 int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream);
+/* x[r*ld + c] = value for r < rows, c < cols (no reference counterpart: the
+ * zeros of a column-block view's gradient that nothing wrote) */
+int pk_fill2d_f32(int64_t rows, int64_t cols, float value, float* x, int64_t ld,
+                  pk_stream_t stream);
 /* x[i] = mean + std * z_i, z_i ~ N(0,1) from a counter-based generator: element
  * i draws two uniforms from the 64-bit mix of (seed, i) and applies Box-Muller
  * (u1 in (0,1]), so the values do not depend on the launch shape.  Seeded
@@ -202,51 +206,56 @@ int pk_swiglu_bwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const f
 
 /* ---- causal attention ----------------------------------------------------
  * q, k, v, o are token-major [B*T, H*hd]; head h of batch b owns columns
- * h*hd..h*hd+hd-1 of rows b*T..b*T+T-1.  lse is [B*H, T] (log-sum-exp of each
+ * h*hd..h*hd+hd-1 of rows b*T..b*T+T-1.  q, k, v and their gradients dq, dk,
+ * dv have row stride ld >= H*hd (H*hd when contiguous; larger when they are
+ * column blocks of one fused projection); o and dout are contiguous.  lse is
+ * [B*H, T] (log-sum-exp of each
  * score row, kept for the backward).  P is a [B*H, T, T] buffer the forward
  * fills with the probabilities (zero above the diagonal) and the backward
  * reads; dP_ws is a [B*H, T, T] scratch buffer for the backward.
  * scale is normally 1/sqrt(hd). */
-int pk_attn_causal_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                           const float* q, const float* k, const float* v, float* o, float* lse,
-                           float* P, pk_stream_t stream);
+int pk_attn_causal_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                           float scale, const float* q, const float* k, const float* v, float* o,
+                           float* lse, float* P, pk_stream_t stream);
 /* dq, dk, dv (+)= gradients: flags bit 0 (PK_ACCUM) accumulates dq, bit 1
  * (PK_ACCUM2) dk, bit 2 (PK_ACCUM3) dv; a NULL gradient pointer is skipped.
  * The writes happen in the order dv, dq, dk, so aliased outputs accumulate
  * correctly when the later ones carry their accumulate bit. */
-int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                           const float* q, const float* k, const float* v, const float* P,
-                           const float* dout, float* dq, float* dk, float* dv, float* dP_ws,
-                           int flags, pk_stream_t stream);
+int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                           float scale, const float* q, const float* k, const float* v,
+                           const float* P, const float* dout, float* dq, float* dk, float* dv,
+                           float* dP_ws, int flags, pk_stream_t stream);
 /* Fused causal attention for head size 64 (T a multiple of 128): the scores
  * are never written to memory.  Same layouts and lse as above; q, k, v, o,
- * dout, dq, dk, dv 16-byte aligned.  pk_flash_attn_supported(T, hd) says
+ * dout, dq, dk, dv 16-byte aligned and ld a multiple of 4.
+ * pk_flash_attn_supported(T, hd) says
  * whether these apply.  The backward needs pk_flash_attn_bwd_workspace(B, H,
  * T) bytes (per 64-query block: lse in base 2, then the row sums of dO*O)
  * and writes dv, then dk, then dq, each accumulating when its flags bit is
  * set (PK_ACCUM dq, PK_ACCUM2 dk, PK_ACCUM3 dv). */
 int pk_flash_attn_supported(int64_t T, int64_t hd);
-int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                          const float* q, const float* k, const float* v, float* o, float* lse,
-                          pk_stream_t stream);
+int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                          float scale, const float* q, const float* k, const float* v, float* o,
+                          float* lse, pk_stream_t stream);
 size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T);
-int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                          const float* q, const float* k, const float* v, const float* o,
-                          const float* lse, const float* dout, float* dq, float* dk, float* dv,
-                          void* workspace, size_t workspace_bytes, int flags, pk_stream_t stream);
+int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                          float scale, const float* q, const float* k, const float* v,
+                          const float* o, const float* lse, const float* dout, float* dq,
+                          float* dk, float* dv, void* workspace, size_t workspace_bytes, int flags,
+                          pk_stream_t stream);
 /* The same fused attention with bf16 multiplies (no reference counterpart:
  * pico is fp32 only).  Q (pre-scaled), K, V, dO and the probabilities P and
  * dS are rounded to bf16 (nearest even) where they enter a matrix product;
  * the softmax statistics, exponentials and accumulators stay fp32, and every
  * tensor, lse and the workspace are as in the fp32 entry points. */
-int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                               const float* q, const float* k, const float* v, float* o,
-                               float* lse, pk_stream_t stream);
-int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                               const float* q, const float* k, const float* v, const float* o,
-                               const float* lse, const float* dout, float* dq, float* dk,
-                               float* dv, void* workspace, size_t workspace_bytes, int flags,
-                               pk_stream_t stream);
+int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                               float scale, const float* q, const float* k, const float* v,
+                               float* o, float* lse, pk_stream_t stream);
+int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                               float scale, const float* q, const float* k, const float* v,
+                               const float* o, const float* lse, const float* dout, float* dq,
+                               float* dk, float* dv, void* workspace, size_t workspace_bytes,
+                               int flags, pk_stream_t stream);
 /* the two row kernels inside the chain, exposed for tests:
  * P = softmax(scale*S) over j <= i, zero for j > i, lse per row (P may alias S) */
 int pk_causal_softmax_fwd_f32(int64_t BH, int64_t T, float scale, const float* S, float* P,

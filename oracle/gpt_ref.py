@@ -10,14 +10,45 @@ follow (pico has no sequence model); the hand-written backward is pinned
 against torch's float64 autograd in tests/test_gpt_ref.py ("parity pinned by
 an independent autodiff", not by the reference).
 
-Parameters are passed in gpt.c's order: E [V,d]; per layer g_attn [d], Wq,
-Wk, Wv, Wo [d,d], g_ffn [d], W1 [d,F], W3 [d,F], W2 [F,d]; g_final [d]; Wlm [d,V].
+Parameters are passed as separate weights: E [V,d]; per layer g_attn [d],
+Wq, Wk, Wv, Wo [d,d], g_ffn [d], W1 [d,F], W3 [d,F], W2 [F,d]; g_final [d];
+Wlm [d,V].  gpt.c stores the projections that read one input side by side --
+wqkv = [Wq | Wk | Wv] [d,3d] and w13 = [W1 | W3] [d,2F], six params per layer
+-- and split_fused / join_fused map between the two lists.
 """
 from __future__ import annotations
 
 import numpy as np
 
 PER_LAYER = 9
+FUSED_PER_LAYER = 6
+
+
+def split_fused(params, cfg):
+    """gpt.c's parameter list (per layer g_attn, wqkv, wo, g_ffn, w13, w2; flat
+    or shaped arrays) as this module's list of separate, shaped weights"""
+    d, F, V, L = cfg["d_model"], cfg["d_ff"], cfg["vocab"], cfg["n_layers"]
+    p = [np.asarray(x) for x in params]
+    assert len(p) == 3 + FUSED_PER_LAYER * L
+    out = [p[0].reshape(V, d)]
+    for l in range(L):
+        g1, wqkv, wo, g2, w13, w2 = p[1 + FUSED_PER_LAYER * l: 1 + FUSED_PER_LAYER * (l + 1)]
+        wqkv, w13 = wqkv.reshape(d, 3 * d), w13.reshape(d, 2 * F)
+        out += [g1.reshape(d), wqkv[:, :d], wqkv[:, d:2 * d], wqkv[:, 2 * d:], wo.reshape(d, d),
+                g2.reshape(d), w13[:, :F], w13[:, F:], w2.reshape(F, d)]
+    return out + [p[-2].reshape(d), p[-1].reshape(d, V)]
+
+
+def join_fused(params, cfg):
+    """the inverse of split_fused: separate weights into gpt.c's shaped list"""
+    d, F, L = cfg["d_model"], cfg["d_ff"], cfg["n_layers"]
+    p = [np.asarray(x) for x in params]
+    out = [p[0]]
+    for l in range(L):
+        g1, Wq, Wk, Wv, Wo, g2, W1, W3, W2 = p[1 + PER_LAYER * l: 1 + PER_LAYER * (l + 1)]
+        out += [g1, np.concatenate([Wq.reshape(d, d), Wk.reshape(d, d), Wv.reshape(d, d)], 1),
+                Wo, g2, np.concatenate([W1.reshape(d, F), W3.reshape(d, F)], 1), W2]
+    return out + p[-2:]
 
 
 def _rms_fwd(x, g, eps):

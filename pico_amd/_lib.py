@@ -51,6 +51,7 @@ PK_SIGNATURES = {
     "pk_relu_f32": [c_i64, c_p, c_p, c_p],
     "pk_relu_bwd_f32": [c_i64, c_p, c_p, c_p, c_int, c_p],
     "pk_fill_f32": [c_i64, c_f, c_p, c_p],
+    "pk_fill2d_f32": [c_i64, c_i64, c_f, c_p, c_i64, c_p],
     "pk_fill_normal_f32": [c_i64, ctypes.c_uint64, c_f, c_f, c_p, c_p],
     "pk_axpy_f32": [c_i64, c_f, c_p, c_p, c_p, c_int, c_p],
     "pk_reduce_sum_f32": [c_i64, c_p, c_f, c_p, c_int, c_p],
@@ -67,18 +68,20 @@ PK_SIGNATURES = {
     "pk_swiglu_fwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p],
     "pk_swiglu_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64,
                           c_int, c_p],
-    "pk_attn_causal_fwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p,
-                               c_p],
-    "pk_attn_causal_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p,
-                               c_p, c_p, c_p, c_int, c_p],
+    "pk_attn_causal_fwd_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
+                               c_p, c_p],
+    "pk_attn_causal_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
+                               c_p, c_p, c_p, c_p, c_int, c_p],
     "pk_flash_attn_supported": [c_i64, c_i64],
-    "pk_flash_attn_fwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p],
-    "pk_flash_attn_fwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p],
+    "pk_flash_attn_fwd_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
+                              c_p],
+    "pk_flash_attn_fwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
+                                   c_p, c_p],
     "pk_flash_attn_bwd_workspace": [c_i64, c_i64, c_i64],
-    "pk_flash_attn_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
-                              c_p, c_p, c_p, c_size, c_int, c_p],
-    "pk_flash_attn_bwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
-                                   c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
+    "pk_flash_attn_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
+                              c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
+    "pk_flash_attn_bwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
+                                   c_p, c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
     "pk_causal_softmax_fwd_f32": [c_i64, c_i64, c_f, c_p, c_p, c_p, c_p],
     "pk_causal_softmax_bwd_f32": [c_i64, c_i64, c_p, c_p, c_p, c_p],
     "pk_embed_fwd_f32": [c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p],

@@ -214,6 +214,15 @@ __global__ void fill_kernel(int64_t n, float v, float* __restrict__ x) {
         x[i] = v;
 }
 
+// a [rows, cols] block with row stride ld (grid-stride over rows x cols)
+__global__ void fill2d_kernel(int64_t rows, int64_t cols, float v, float* __restrict__ x,
+                              int64_t ld) {
+    const int64_t n = rows * cols;
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x)
+        x[(i / cols) * ld + i % cols] = v;
+}
+
 // splitmix64 finaliser: a bijective 64-bit mix (Steele, Lea & Flood 2014)
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
@@ -666,6 +675,16 @@ extern "C" int pk_fill_f32(int64_t n, float value, float* x, pk_stream_t stream)
     if(!x) return pk::fail("pk_fill_f32: NULL pointer");
     fill_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, value, x);
     return pk::launch_status("pk_fill_f32");
+}
+
+extern "C" int pk_fill2d_f32(int64_t rows, int64_t cols, float value, float* x, int64_t ld,
+                             pk_stream_t stream) {
+    if(rows < 0 || cols < 0 || (rows > 1 && ld < cols)) return pk::fail("pk_fill2d_f32: bad sizes");
+    if(rows == 0 || cols == 0) return PK_OK;
+    if(!x) return pk::fail("pk_fill2d_f32: NULL pointer");
+    fill2d_kernel<<<pk::grid_for(rows * cols, NT), NT, 0, pk::as_stream(stream)>>>(rows, cols,
+                                                                                 value, x, ld);
+    return pk::launch_status("pk_fill2d_f32");
 }
 
 extern "C" int pk_fill_normal_f32(int64_t n, uint64_t seed, float mean, float std, float* x,

@@ -3,7 +3,9 @@
 // the softmax Jacobian it would need is the comment at src/autograd.h:38-40).
 //
 // q, k, v, o are token-major [B*T, H*64]; head h of sequence b is the column
-// block h*64.. of rows b*T..; lse is [B*H, T] (natural log).  The score matrix
+// block h*64.. of rows b*T..; lse is [B*H, T] (natural log).  q, k, v (and
+// their gradients) may have a row stride ld > H*64 -- column blocks of one
+// fused [B*T, 3*H*64] projection; o and dout are contiguous.  The score matrix
 // is never written to memory: a workgroup keeps its 128 query (or key) rows in
 // registers and streams 64-row blocks of the other operand through LDS.
 //
@@ -38,7 +40,8 @@ struct FlashParams {
     const float *q, *k, *v, *o, *dout, *lse, *dsum;
     float *out, *lse_out, *dq, *dk, *dv, *dsum_out;
     float* ds;  // dS tiles: written by the dK/dV kernel, read by the dQ kernel
-    int64_t B, H, T, D;  // D = H*64, the row stride
+    int64_t B, H, T, D;  // D = H*64: row stride of o, dout (and the output)
+    int64_t ld;          // row stride of q, k, v and dq, dk, dv (>= D)
     float scale;         // softmax scale (normally 1/8)
     int flags;
 };
@@ -68,26 +71,6 @@ __device__ __forceinline__ void load_frag32(const float* __restrict__ row, int h
         f[4 * i + 1] = x[1] * mul;
         f[4 * i + 2] = x[2] * mul;
         f[4 * i + 3] = x[3] * mul;
-    }
-}
-
-// one 64x64 block (rows row0.. of a head) into registers: 4 float4 per thread
-__device__ __forceinline__ void fetch_block(const float* __restrict__ base, int64_t D, int64_t row0,
-                                            f32x4 (&v)[4]) {
-#pragma unroll
-    for(int i = 0; i < 4; ++i) {
-        const int idx = threadIdx.x + 256 * i;
-        const int r = idx >> 4, c4 = idx & 15;
-        v[i] = *reinterpret_cast<const f32x4*>(base + (row0 + r) * D + 4 * c4);
-    }
-}
-
-__device__ __forceinline__ void store_block(float* lds, const f32x4 (&v)[4]) {
-#pragma unroll
-    for(int i = 0; i < 4; ++i) {
-        const int idx = threadIdx.x + 256 * i;
-        const int r = idx >> 4, c4 = idx & 15;
-        *reinterpret_cast<f32x4*>(lds + r * LDT + 4 * c4) = v[i];
     }
 }
 
@@ -211,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
     const float *Q = p.q + base, *K = p.k + base, *V = p.v + base;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
@@ -219,13 +202,13 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);  // blocks the workgroup streams
     const int nw = (int)((q0 + 31) / BLK) + 1;          // blocks this wave sees
 
-    const BlockLoad ld(p.D, w, l);
-    const __amdgpu_buffer_rsrc_t rk = head_rsrc(K, p.T, p.D), rv = head_rsrc(V, p.T, p.D);
-    ld.issue(rk, p.D, 0, sK[0], w);
-    ld.issue(rv, p.D, 0, sV[0], w);
-    ld.issue(rk, p.D, BLK, sK[1], w);  // nkv >= 2 since T % 128 == 0
+    const BlockLoad blk(p.ld, w, l);
+    const __amdgpu_buffer_rsrc_t rk = head_rsrc(K, p.T, p.ld), rv = head_rsrc(V, p.T, p.ld);
+    blk.issue(rk, p.ld, 0, sK[0], w);
+    blk.issue(rv, p.ld, 0, sV[0], w);
+    blk.issue(rk, p.ld, BLK, sK[1], w);  // nkv >= 2 since T % 128 == 0
     float qf[32];
-    load_frag32(Q + qi * p.D, lh, qf, p.scale * kLog2e);
+    load_frag32(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
     wait_loads();
@@ -279,8 +262,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     auto next_loads = [&](int j, float* __restrict__ kd, float* __restrict__ vd) {
         wait_loads();
         __syncthreads();
-        if(j + 2 < nkv) ld.issue(rk, p.D, (int64_t)(j + 2) * BLK, kd, w);
-        if(j + 1 < nkv) ld.issue(rv, p.D, (int64_t)(j + 1) * BLK, vd, w);
+        if(j + 2 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 2) * BLK, kd, w);
+        if(j + 1 < nkv) blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, vd, w);
     };
     // a block with a successor this wave sees
     auto steady = [&](int j, const float* __restrict__ tk, const float* __restrict__ tv,
@@ -307,7 +290,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     for(; j + 1 < nw; ++j) steady(j, sK[(j + 1) & 1], sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);
     last(j, sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);  // the wave's last block
     for(++j; j < nkv; ++j) next_loads(j, sK[j & 1], sV[(j + 1) & 1]);  // loads for the others
-    store_rowT(p.out + base + qi * p.D, o, lh, 1.0f / lsum, false);
+    store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
 
@@ -371,20 +354,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     const int64_t BH = p.B * p.H;
     const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
     const float *K = p.k + base, *V = p.v + base;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
 
-    const BlockLoad ld(p.D, w, l);
-    const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.D);
-    const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + base, p.T, p.D);
+    const BlockLoad blq(p.ld, w, l), blo(p.D, w, l);
+    const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.ld);
+    const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + obase, p.T, p.D);
     const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.T);
     auto issue = [&](int j, float* __restrict__ tq, float* __restrict__ to,
                      float* __restrict__ tl) {
-        ld.issue(rq, p.D, (int64_t)j * BLK, tq, w);
-        ld.issue(ro, p.D, (int64_t)j * BLK, to, w);
+        blq.issue(rq, p.ld, (int64_t)j * BLK, tq, w);
+        blo.issue(ro, p.D, (int64_t)j * BLK, to, w);
         if(w == 1 && l < 32)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)tl, 16, 16 * l,
                                                      (unsigned)(j * 2 * BLK * 4), 0, 0);
@@ -392,8 +375,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
     issue(j0, sQ[0], sO[0], sLD[0]);
     float kf[32], vf[32];
-    load_frag32(K + ki * p.D, lh, kf, p.scale * kLog2e);
-    load_frag32(V + ki * p.D, lh, vf, 1.0f);
+    load_frag32(K + ki * p.ld, lh, kf, p.scale * kLog2e);
+    load_frag32(V + ki * p.ld, lh, vf, 1.0f);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
     // this lane's column of every dS tile of key group kg (rows 32 floats apart)
     const int64_t kg = k0 / 32;
@@ -458,8 +441,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
         const int st = (j - j0) & 1;
         iter(j, sQ[st], sO[st], sLD[st], sQ[st ^ 1], sO[st ^ 1], sLD[st ^ 1]);
     }
-    store_rowT(p.dv + base + ki * p.D, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
-    store_rowT(p.dk + base + ki * p.D, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
+    store_rowT(p.dv + base + ki * p.ld, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
+    store_rowT(p.dk + base + ki * p.ld, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
 }
 
 // =================================================================== backward: dQ
@@ -472,14 +455,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
+    const int64_t base = b * p.T * p.ld + h * HD;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq, qg = q0 / 32;
 
-    const BlockLoad ld(p.D, w, l);
-    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.D);
-    ld.issue(rk, p.D, 0, sK[0], w);
+    const BlockLoad blk(p.ld, w, l);
+    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.ld);
+    blk.issue(rk, p.ld, 0, sK[0], w);
     // tile (qg, kg) is at ds + kg*1024; this lane's 16 values at (2*lq + lh)*16
     const float* ds = p.ds + ds_tile(bh, p.T, qg, 0) + (2 * lq + lh) * 16;
     auto fetch = [&](int j, f32x16 (&x)[2]) {
@@ -505,7 +488,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     auto iter = [&](int j, const float* __restrict__ tk, float* __restrict__ kd) {
         wait_loads();
         __syncthreads();
-        if(j + 1 < nkv) ld.issue(rk, p.D, (int64_t)(j + 1) * BLK, kd, w);
+        if(j + 1 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, kd, w);
         if(j + 1 < nw) fetch(j + 1, nxt);
         if(j < nw) {
             const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;  // key offset <= lim visible
@@ -524,7 +507,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
         }
     };
     for(int j = 0; j < nkv; ++j) iter(j, sK[j & 1], sK[(j + 1) & 1]);
-    store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
+    store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
 // ================================================================ bf16 products
@@ -631,20 +614,20 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
     const float *Q = p.q + base, *K = p.k + base, *V = p.v + base;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
     bf16x8 qf[4];
-    load_frag_bf16(Q + qi * p.D, lh, qf, p.scale * kLog2e);
+    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
     f32x4 rk[4], rv[4];
-    fetch_quad(K, p.D, 0, rk);
-    fetch_quad(V, p.D, 0, rv);
+    fetch_quad(K, p.ld, 0, rk);
+    fetch_quad(V, p.ld, 0, rv);
     put_rows(sK[0], rk);
     put_cols(sVt[0], rv);
     for(int j = 0; j < nkv; ++j) {
@@ -652,8 +635,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
         __syncthreads();
         const bool more = j + 1 < nkv;
         if(more) {
-            fetch_quad(K, p.D, (int64_t)(j + 1) * BLK, rk);
-            fetch_quad(V, p.D, (int64_t)(j + 1) * BLK, rv);
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv);
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
@@ -700,7 +683,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
             put_cols(sVt[st ^ 1], rv);
         }
     }
-    store_rowT(p.out + base + qi * p.D, o, lh, 1.0f / lsum, false);
+    store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
 
@@ -714,23 +697,23 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
     const int64_t BH = p.B * p.H;
     const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
-    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + obase;
     const float* cst = p.dsum + bh * 2 * p.T;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
 
     bf16x8 kf[4], vf[4];
-    load_frag_bf16(K + ki * p.D, lh, kf, p.scale * kLog2e);
-    load_frag_bf16(V + ki * p.D, lh, vf, 1.0f);
+    load_frag_bf16(K + ki * p.ld, lh, kf, p.scale * kLog2e);
+    load_frag_bf16(V + ki * p.ld, lh, vf, 1.0f);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
 
     const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
     f32x4 rq[4], ro[4];
     float rc = 0.0f;
     auto fetch = [&](int j) {
-        fetch_quad(Q, p.D, (int64_t)j * BLK, rq);
+        fetch_quad(Q, p.ld, (int64_t)j * BLK, rq);
         fetch_quad(dO, p.D, (int64_t)j * BLK, ro);
         if(threadIdx.x < 2 * BLK) rc = cst[(int64_t)j * 2 * BLK + threadIdx.x];
     };
@@ -773,8 +756,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
         }
         if(more) put(st ^ 1);
     }
-    store_rowT(p.dv + base + ki * p.D, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
-    store_rowT(p.dk + base + ki * p.D, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
+    store_rowT(p.dv + base + ki * p.ld, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
+    store_rowT(p.dk + base + ki * p.ld, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
 }
 
 // ----------------------------------------------------------- bf16 backward: dQ
@@ -785,14 +768,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const int64_t base = b * p.T * p.D + h * HD;
-    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + base;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + obase;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
     bf16x8 qf[4], of[4];
-    load_frag_bf16(Q + qi * p.D, lh, qf, p.scale * kLog2e);
+    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
     load_frag_bf16(dO + qi * p.D, lh, of, 1.0f);
     const float* cst = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
     const float l2 = cst[0], dd = cst[BLK];
@@ -800,8 +783,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
 
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
     f32x4 rk[4], rv[4];
-    fetch_quad(K, p.D, 0, rk);
-    fetch_quad(V, p.D, 0, rv);
+    fetch_quad(K, p.ld, 0, rk);
+    fetch_quad(V, p.ld, 0, rv);
     put_rows(sK[0], rk);
     put_cols(sKt[0], rk);
     put_rows(sV[0], rv);
@@ -810,8 +793,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
         __syncthreads();
         const bool more = j + 1 < nkv;
         if(more) {
-            fetch_quad(K, p.D, (int64_t)(j + 1) * BLK, rk);
-            fetch_quad(V, p.D, (int64_t)(j + 1) * BLK, rv);
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv);
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
@@ -837,17 +820,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
             put_rows(sV[st ^ 1], rv);
         }
     }
-    store_rowT(p.dq + base + qi * p.D, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
+    store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
-int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, const void* a,
-                const void* b, const void* c) {
+int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                const void* a, const void* b, const void* c) {
     if(B < 0 || H < 1 || T < 0) return pk::fail("%s: bad sizes", who);
     if(hd != HD) return pk::fail("%s: head size %lld (this kernel handles 64)", who, (long long)hd);
     if(T % ROWS) return pk::fail("%s: T=%lld must be a multiple of %d", who, (long long)T, ROWS);
+    if(ld < H * HD || ld % 4)
+        return pk::fail("%s: row stride %lld of q, k, v must be >= %lld and a multiple of 4", who,
+                        (long long)ld, (long long)(H * HD));
     if(!pk::aligned16(a) || !pk::aligned16(b) || !pk::aligned16(c))
         return pk::fail("%s: q, k, v must be 16-byte aligned", who);
-    if(B * H * (T / ROWS) > 0x7fffffff || T * H * HD * 4 > 0x7fffffff)
+    if(B * H * (T / ROWS) > 0x7fffffff || T * ld * 4 > 0x7fffffff)
         return pk::fail("%s: problem too large", who);
     return PK_OK;
 }
@@ -861,9 +847,9 @@ extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) {
 namespace {
 
 int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
-                     float scale, const float* q, const float* k, const float* v, float* o,
-                     float* lse, pk_stream_t stream) {
-    int rc = flash_check(who, B, H, T, hd, q, k, v);
+                     int64_t ld, float scale, const float* q, const float* k, const float* v,
+                     float* o, float* lse, pk_stream_t stream) {
+    int rc = flash_check(who, B, H, T, hd, ld, q, k, v);
     if(rc) return rc;
     if(B == 0 || T == 0) return PK_OK;
     if(!o || !pk::aligned16(o)) return pk::fail("%s: o NULL or unaligned", who);
@@ -877,6 +863,7 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.H = H;
     p.T = T;
     p.D = H * HD;
+    p.ld = ld;
     p.scale = scale;
     const unsigned grid = (unsigned)(B * H * (T / ROWS));
     if(bf16)
@@ -888,19 +875,19 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
 
 }  // namespace
 
-extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                                     const float* q, const float* k, const float* v, float* o,
-                                     float* lse, pk_stream_t stream) {
-    return flash_fwd_launch("pk_flash_attn_fwd_f32", false, B, H, T, hd, scale, q, k, v, o, lse,
-                            stream);
+extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                     float scale, const float* q, const float* k, const float* v,
+                                     float* o, float* lse, pk_stream_t stream) {
+    return flash_fwd_launch("pk_flash_attn_fwd_f32", false, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, stream);
 }
 
 extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
-                                          float scale, const float* q, const float* k,
+                                          int64_t ld, float scale, const float* q, const float* k,
                                           const float* v, float* o, float* lse,
                                           pk_stream_t stream) {
-    return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", true, B, H, T, hd, scale, q, k, v, o,
-                            lse, stream);
+    return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", true, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, stream);
 }
 
 // row constants (2*B*H*T floats), then the dS tiles
@@ -912,10 +899,11 @@ extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
 namespace {
 
 int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
-                     float scale, const float* q, const float* k, const float* v, const float* o,
-                     const float* lse, const float* dout, float* dq, float* dk, float* dv,
-                     void* workspace, size_t workspace_bytes, int flags, pk_stream_t stream) {
-    int rc = flash_check(who, B, H, T, hd, q, k, v);
+                     int64_t ld, float scale, const float* q, const float* k, const float* v,
+                     const float* o, const float* lse, const float* dout, float* dq, float* dk,
+                     float* dv, void* workspace, size_t workspace_bytes, int flags,
+                     pk_stream_t stream) {
+    int rc = flash_check(who, B, H, T, hd, ld, q, k, v);
     if(rc) return rc;
     if(B == 0 || T == 0) return PK_OK;
     if(!o || !lse || !dout || !dq || !dk || !dv) return pk::fail("%s: NULL pointer", who);
@@ -942,6 +930,7 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.H = H;
     p.T = T;
     p.D = H * HD;
+    p.ld = ld;
     p.scale = scale;
     p.flags = flags;
     hipStream_t st = pk::as_stream(stream);
@@ -962,21 +951,21 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
 
 }  // namespace
 
-extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, float scale,
-                                     const float* q, const float* k, const float* v,
+extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                     float scale, const float* q, const float* k, const float* v,
                                      const float* o, const float* lse, const float* dout,
                                      float* dq, float* dk, float* dv, void* workspace,
                                      size_t workspace_bytes, int flags, pk_stream_t stream) {
-    return flash_bwd_launch("pk_flash_attn_bwd_f32", false, B, H, T, hd, scale, q, k, v, o, lse,
-                            dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
+    return flash_bwd_launch("pk_flash_attn_bwd_f32", false, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
 }
 
 extern "C" int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
-                                          float scale, const float* q, const float* k,
+                                          int64_t ld, float scale, const float* q, const float* k,
                                           const float* v, const float* o, const float* lse,
                                           const float* dout, float* dq, float* dk, float* dv,
                                           void* workspace, size_t workspace_bytes, int flags,
                                           pk_stream_t stream) {
-    return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", true, B, H, T, hd, scale, q, k, v, o,
-                            lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
+    return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", true, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
 }

@@ -579,6 +579,57 @@ __global__ void swiglu_bwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
     }
 }
 
+// Row-strided operands (the two halves of a fused [R, 2F] projection), F and
+// every row stride a multiple of 4 and every base 16-byte aligned: block
+// (x, y) covers float4 columns 256x.. of rows y, y + gridDim.y, ...
+__global__ void swiglu_fwd_rows4(int64_t R, int64_t F4, const float* __restrict__ a, int64_t lda,
+                                 const float* __restrict__ u, int64_t ldu, float* __restrict__ h,
+                                 int64_t ldh) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if(c >= F4) return;
+    for(int64_t r = blockIdx.y; r < R; r += gridDim.y) {
+        const f32x4 av = pk::ld_stream(reinterpret_cast<const f32x4*>(a + r * lda) + c);
+        const f32x4 uv = pk::ld_stream(reinterpret_cast<const f32x4*>(u + r * ldu) + c);
+        f32x4 o;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) o[e] = av[e] * sigmoidf_(av[e]) * uv[e];
+        pk::st_stream(reinterpret_cast<f32x4*>(h + r * ldh) + c, o);
+    }
+}
+
+__global__ void swiglu_bwd_rows4(int64_t R, int64_t F4, const float* __restrict__ a, int64_t lda,
+                                 const float* __restrict__ u, int64_t ldu,
+                                 const float* __restrict__ dh, int64_t ldh, float* __restrict__ da,
+                                 float* __restrict__ du, int64_t ldd, int flags) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if(c >= F4) return;
+    for(int64_t r = blockIdx.y; r < R; r += gridDim.y) {
+        const f32x4 av = pk::ld_stream(reinterpret_cast<const f32x4*>(a + r * lda) + c);
+        const f32x4 uv = pk::ld_stream(reinterpret_cast<const f32x4*>(u + r * ldu) + c);
+        const f32x4 g = pk::ld_stream(reinterpret_cast<const f32x4*>(dh + r * ldh) + c);
+        f32x4 ga, gu;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            const float s = sigmoidf_(av[e]);
+            ga[e] = g[e] * uv[e] * s * (1.0f + av[e] * (1.0f - s));
+            gu[e] = g[e] * av[e] * s;
+        }
+        if(flags & 4) {
+            f32x4* p = reinterpret_cast<f32x4*>(da + r * ldd) + c;
+            pk::st_stream(p, (flags & PK_ACCUM) ? *p + ga : ga);
+        }
+        if(flags & 8) {
+            f32x4* p = reinterpret_cast<f32x4*>(du + r * ldd) + c;
+            pk::st_stream(p, (flags & PK_ACCUM2) ? *p + gu : gu);
+        }
+    }
+}
+
+dim3 rows4_grid(int64_t R, int64_t F4) {
+    const int64_t gy = R < 8192 ? R : 8192;
+    return dim3((unsigned)((F4 + 255) / 256), (unsigned)gy);
+}
+
 __global__ void swiglu_bwd_any(int64_t R, int64_t F, const float* __restrict__ a, int64_t lda,
                                const float* __restrict__ u, int64_t ldu,
                                const float* __restrict__ dh, int64_t ldh, float* __restrict__ da,
@@ -889,10 +940,12 @@ extern "C" int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t l
     if(lda < F || ldu < F || ldh < F) return pk::fail("pk_swiglu_fwd_f32: row stride < F");
     hipStream_t st = pk::as_stream(stream);
     const int64_t n = R * F;
-    if(lda == F && ldu == F && ldh == F && n % 4 == 0 && pk::aligned16(a) && pk::aligned16(u) &&
-       pk::aligned16(h))
+    const bool al = pk::aligned16(a) && pk::aligned16(u) && pk::aligned16(h);
+    if(lda == F && ldu == F && ldh == F && n % 4 == 0 && al)
         swiglu_fwd4<<<pk::grid_stream(n / 4, 256), 256, 0, st>>>(n / 4, (const f32x4*)a,
                                                                        (const f32x4*)u, (f32x4*)h);
+    else if(F % 4 == 0 && lda % 4 == 0 && ldu % 4 == 0 && ldh % 4 == 0 && al)
+        swiglu_fwd_rows4<<<rows4_grid(R, F / 4), 256, 0, st>>>(R, F / 4, a, lda, u, ldu, h, ldh);
     else
         swiglu_fwd_any<<<pk::grid_for(n, 256, 256 * 8), 256, 0, st>>>(R, F, a, lda, u, ldu, h, ldh);
     return pk::launch_status("pk_swiglu_fwd_f32");
@@ -908,11 +961,14 @@ extern "C" int pk_swiglu_bwd_f32(int64_t R, int64_t F, const float* a, int64_t l
     hipStream_t st = pk::as_stream(stream);
     const int kf = (flags & (PK_ACCUM | PK_ACCUM2)) | (da ? 4 : 0) | (du ? 8 : 0);
     const int64_t n = R * F;
-    if(lda == F && ldu == F && ldh == F && ldd == F && n % 4 == 0 && pk::aligned16(a) &&
-       pk::aligned16(u) && pk::aligned16(dh) && (!da || pk::aligned16(da)) &&
-       (!du || pk::aligned16(du)))
+    const bool al = pk::aligned16(a) && pk::aligned16(u) && pk::aligned16(dh) &&
+                    (!da || pk::aligned16(da)) && (!du || pk::aligned16(du));
+    if(lda == F && ldu == F && ldh == F && ldd == F && n % 4 == 0 && al)
         swiglu_bwd4<<<pk::grid_stream(n / 4, 256), 256, 0, st>>>(
             n / 4, (const f32x4*)a, (const f32x4*)u, (const f32x4*)dh, (f32x4*)da, (f32x4*)du, kf);
+    else if(F % 4 == 0 && lda % 4 == 0 && ldu % 4 == 0 && ldh % 4 == 0 && ldd % 4 == 0 && al)
+        swiglu_bwd_rows4<<<rows4_grid(R, F / 4), 256, 0, st>>>(R, F / 4, a, lda, u, ldu, dh, ldh, da,
+                                                              du, ldd, kf);
     else
         swiglu_bwd_any<<<pk::grid_for(n, 256, 256 * 8), 256, 0, st>>>(R, F, a, lda, u, ldu, dh, ldh,
                                                                      da, du, ldd, kf);

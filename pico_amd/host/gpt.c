@@ -4,6 +4,14 @@
  * model (compare examples/02_relu_mlp/main.c:64-130 for the MLP).  It is the
  * training step of the benchmark configurations; the ops it calls are the
  * hot path.
+ *
+ * The projections that read the same input are one product each:
+ * wqkv = [Wq | Wk | Wv] (d x 3d) and w13 = [W1 | W3] (d x 2F), whose output
+ * pico_split_cols turns into the q, k, v (gate, up) column views that
+ * attention (SwiGLU) reads.  The math is that of separate Wq, Wk, Wv, W1, W3;
+ * one [8192, 2304] product replaces three [8192, 768] ones, and the
+ * backward's dX = dQKV . Wqkv^T is one K = 2304 product instead of three
+ * accumulating K = 768 ones.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -12,8 +20,10 @@
 #include "pk_host.h"
 
 struct PicoGPTLayer {
-    struct PicoTensor *g_attn, *wq, *wk, *wv, *wo, *g_ffn, *w1, *w3, *w2;
+    struct PicoTensor *g_attn, *wqkv, *wo, *g_ffn, *w13, *w2;
 };
+
+enum { PER_LAYER = 6 };
 
 struct PicoGPT {
     struct PicoGPTConfig cfg;
@@ -53,7 +63,7 @@ struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed) {
     struct PicoGPT* m = (struct PicoGPT*)calloc(1, sizeof(*m));
     if(!m) return NULL;
     m->cfg = *cfg;
-    int total = 3 + 9 * cfg->n_layers;
+    int total = 3 + PER_LAYER * cfg->n_layers;
     m->params = (struct PicoTensor**)calloc(total, sizeof(struct PicoTensor*));
     m->layers = (struct PicoGPTLayer*)calloc(cfg->n_layers ? cfg->n_layers : 1, sizeof(*m->layers));
     if(!m->params || !m->layers) {
@@ -65,10 +75,9 @@ struct PicoGPT* pico_gpt_init(const struct PicoGPTConfig* cfg, uint64_t seed) {
     int ok = (m->emb = new_param(m, V, d, 0, s++)) != NULL;
     for(int l = 0; ok && l < cfg->n_layers; l++) {
         struct PicoGPTLayer* L = &m->layers[l];
-        ok = (L->g_attn = new_param(m, 1, d, 1, 0)) && (L->wq = new_param(m, d, d, 0, s++)) &&
-             (L->wk = new_param(m, d, d, 0, s++)) && (L->wv = new_param(m, d, d, 0, s++)) &&
-             (L->wo = new_param(m, d, d, 0, s++)) && (L->g_ffn = new_param(m, 1, d, 1, 0)) &&
-             (L->w1 = new_param(m, d, F, 0, s++)) && (L->w3 = new_param(m, d, F, 0, s++)) &&
+        ok = (L->g_attn = new_param(m, 1, d, 1, 0)) &&
+             (L->wqkv = new_param(m, d, 3 * d, 0, s++)) && (L->wo = new_param(m, d, d, 0, s++)) &&
+             (L->g_ffn = new_param(m, 1, d, 1, 0)) && (L->w13 = new_param(m, d, 2 * F, 0, s++)) &&
              (L->w2 = new_param(m, F, d, 0, s++));
     }
     ok = ok && (m->g_final = new_param(m, 1, d, 1, 0)) && (m->wlm = new_param(m, d, V, 0, s++));
@@ -94,11 +103,11 @@ struct PicoTensor* pico_gpt_loss(struct PicoGPT* m, const int32_t* tokens,
         struct PicoGPTLayer* L = &m->layers[l];
         struct PicoTensor* h = pico_rmsnorm(x, L->g_attn, eps);
         if(!h) return NULL;
-        struct PicoTensor* q = pico_matmul(h, L->wq);
-        struct PicoTensor* k = pico_matmul(h, L->wk);
-        struct PicoTensor* v = pico_matmul(h, L->wv);
-        if(!q || !k || !v) return NULL;
-        struct PicoTensor* a = pico_attention_causal(q, k, v, c->batch, c->n_heads);
+        struct PicoTensor* qkv = pico_matmul(h, L->wqkv);
+        struct PicoTensor* qkv3[3];
+        if(!qkv || pico_split_cols(qkv, 3, qkv3)) return NULL;
+        struct PicoTensor* a =
+            pico_attention_causal(qkv3[0], qkv3[1], qkv3[2], c->batch, c->n_heads);
         if(!a) return NULL;
         struct PicoTensor* o = pico_matmul(a, L->wo);
         if(!o) return NULL;
@@ -106,10 +115,10 @@ struct PicoTensor* pico_gpt_loss(struct PicoGPT* m, const int32_t* tokens,
         if(!x) return NULL;
         h = pico_rmsnorm(x, L->g_ffn, eps);
         if(!h) return NULL;
-        struct PicoTensor* gate = pico_matmul(h, L->w1);
-        struct PicoTensor* up = pico_matmul(h, L->w3);
-        if(!gate || !up) return NULL;
-        struct PicoTensor* act = pico_swiglu(gate, up);
+        struct PicoTensor* gu = pico_matmul(h, L->w13);
+        struct PicoTensor* gu2[2];
+        if(!gu || pico_split_cols(gu, 2, gu2)) return NULL;
+        struct PicoTensor* act = pico_swiglu(gu2[0], gu2[1]);
         if(!act) return NULL;
         struct PicoTensor* down = pico_matmul(act, L->w2);
         if(!down) return NULL;
@@ -135,8 +144,8 @@ const char* pico_gpt_param_name(const struct PicoGPT* m, int i) {
 
 /* "emb", "layers.<l>.<part>", "final_norm", "lm_head", in param order */
 static int name_params(struct PicoGPT* m) {
-    static const char* const parts[9] = {"attn_norm", "wq", "wk", "wv", "wo",
-                                         "ffn_norm", "w1", "w3", "w2"};
+    static const char* const parts[PER_LAYER] = {"attn_norm", "wqkv", "wo",
+                                                 "ffn_norm", "w13", "w2"};
     m->names = (char**)calloc((size_t)m->n_params, sizeof(char*));
     if(!m->names) return -1;
     for(int i = 0; i < m->n_params; i++) {
@@ -148,7 +157,8 @@ static int name_params(struct PicoGPT* m) {
         else if(i == m->n_params - 1)
             snprintf(buf, sizeof(buf), "lm_head");
         else
-            snprintf(buf, sizeof(buf), "layers.%d.%s", (i - 1) / 9, parts[(i - 1) % 9]);
+            snprintf(buf, sizeof(buf), "layers.%d.%s", (i - 1) / PER_LAYER,
+                     parts[(i - 1) % PER_LAYER]);
         m->names[i] = (char*)malloc(strlen(buf) + 1);
         if(!m->names[i]) return -1;
         memcpy(m->names[i], buf, strlen(buf) + 1);

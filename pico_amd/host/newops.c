@@ -134,25 +134,39 @@ struct PicoTensor* pico_rmsnorm(struct PicoTensor* x, struct PicoTensor* gain, f
     return out;
 }
 
-/* ----------------------------------------------------------------- SwiGLU */
+/* ----------------------------------------------------------------- SwiGLU
+ * gate and up are contiguous, or 2-D with unit column stride and one shared
+ * row stride (the two halves of a fused [R, 2F] projection) */
+static int64_t swiglu_ld(const struct PicoTensor* t) {
+    const int64_t F = t->shape[t->ndim - 1];
+    if(t->ndim == 2 && t->strides[1] == 1 && t->strides[0] >= F) return t->strides[0];
+    int64_t s = 1;
+    for(int i = t->ndim - 1; i >= 0; i--) {
+        if(t->shape[i] > 1 && t->strides[i] != s) return -1;
+        s *= t->shape[i];
+    }
+    return F;
+}
+
 static void swiglu_backward(struct PicoTensor* self) {
     struct PicoTensor *a = self->parents[0], *u = self->parents[1];
     const float* dh = pkh_upstream(self);
     if(!dh) return;
     int64_t F = a->shape[a->ndim - 1], R = F ? a->numel / F : 0;
+    const int64_t ld = swiglu_ld(a);
     if(a == u) {
         /* h = silu(a)*a: two passes so the second accumulates onto the first */
-        int st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, a->grad, NULL, F,
+        int st = pk_swiglu_bwd_f32(R, F, a->data, ld, u->data, ld, dh, F, a->grad, NULL, ld,
                                    pkh_grad_flag(a), pkh_stream());
         if(pkh_status("pico_swiglu_backward", st)) return;
         pkh_grad_mark(a);
-        st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, NULL, u->grad, F, PK_ACCUM2,
-                               pkh_stream());
+        st = pk_swiglu_bwd_f32(R, F, a->data, ld, u->data, ld, dh, F, NULL, u->grad, ld,
+                               PK_ACCUM2, pkh_stream());
         pkh_status("pico_swiglu_backward", st);
         return;
     }
     int flags = (pkh_grad_flag(a) ? PK_ACCUM : 0) | (pkh_grad_flag(u) ? PK_ACCUM2 : 0);
-    int st = pk_swiglu_bwd_f32(R, F, a->data, F, u->data, F, dh, F, a->grad, u->grad, F, flags,
+    int st = pk_swiglu_bwd_f32(R, F, a->data, ld, u->data, ld, dh, F, a->grad, u->grad, ld, flags,
                                pkh_stream());
     if(pkh_status("pico_swiglu_backward", st)) return;
     pkh_grad_mark(a);
@@ -166,12 +180,17 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
         PKH_ERR("swiglu expects gate and up of the same shape!\n");
         return NULL;
     }
+    const int64_t ld = swiglu_ld(a);
+    if(ld < 0 || swiglu_ld(u) != ld) {
+        PKH_ERR("swiglu expects gate and up contiguous or with one row stride!\n");
+        return NULL;
+    }
     struct Arena* arena = pkh_need_arena();
     if(!arena) return NULL;
     int64_t F = a->shape[a->ndim - 1], R = F ? a->numel / F : 0;
     struct PicoTensor* out = pkh_new_tensor(arena, a->shape, a->ndim);
     if(!out) return NULL;
-    int st = pk_swiglu_fwd_f32(R, F, a->data, F, u->data, F, out->data, F, pkh_stream());
+    int st = pk_swiglu_fwd_f32(R, F, a->data, ld, u->data, ld, out->data, F, pkh_stream());
     if(pkh_status("pico_swiglu", st)) return NULL;
     struct PicoTensor* ps[2] = {a, u};
     pkh_set_parents(arena, out, 2, ps, swiglu_backward);
@@ -179,7 +198,9 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
 }
 
 /* -------------------------------------------------------- causal attention
- * q, k, v token-major [batch*T, heads*hd]; out the same.  For head size 64 and
+ * q, k, v token-major [batch*T, heads*hd] with unit column stride and one
+ * shared row stride (contiguous, or column blocks of one fused projection);
+ * out contiguous [batch*T, heads*hd].  For head size 64 and
  * T a multiple of 128 the fused kernels run (pk_flash_attn_*): only lse
  * [B*H*T] is saved and the scores never reach memory.  Otherwise the chain of
  * batched GEMMs and causal-softmax kernels runs and saves the probabilities
@@ -193,7 +214,7 @@ static void attn_backward(struct PicoTensor* self) {
     const float* dout = pkh_upstream(self);
     if(!dout) return;
     int64_t B = n->ival[AI_B], H = n->ival[AI_H];
-    int64_t T = q->shape[0] / B, hd = q->shape[1] / H;
+    int64_t T = q->shape[0] / B, hd = q->shape[1] / H, ld = q->strides[0];
     const int flash = (int)n->ival[AI_FLASH];
     size_t ws_bytes = flash ? pk_flash_attn_bwd_workspace(B, H, T)
                             : sizeof(float) * (size_t)(B * H * T * T);
@@ -212,11 +233,11 @@ static void attn_backward(struct PicoTensor* self) {
     int st;
     if(flash)
         st = (n->ival[AI_BF16] ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
-            B, H, T, hd, n->fval[0], q->data, k->data, v->data, self->data,
+            B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, self->data,
             (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad, ws, ws_bytes, flags,
             pkh_stream());
     else
-        st = pk_attn_causal_bwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+        st = pk_attn_causal_bwd_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
                                     (const float*)n->saved[AS_P], dout, q->grad, k->grad, v->grad,
                                     (float*)ws, flags, pkh_stream());
     pkh_status("pico_attention_causal_backward", st);
@@ -227,20 +248,23 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     if(need_gpu("pico_attention_causal", q) || need_gpu("pico_attention_causal", k) ||
        need_gpu("pico_attention_causal", v))
         return NULL;
-    int contiguous = 1;
+    int layout_ok = 1;
     struct PicoTensor* xs[3] = {q, k, v};
     for(int i = 0; i < 3; i++)
-        if(xs[i]->ndim != 2 || xs[i]->strides[1] != 1 || xs[i]->strides[0] != xs[i]->shape[1])
-            contiguous = 0;
-    if(!contiguous || q->shape[0] != k->shape[0] || q->shape[1] != k->shape[1] ||
+        if(xs[i]->ndim != 2 || xs[i]->strides[1] != 1 || xs[i]->strides[0] != q->strides[0] ||
+           xs[i]->strides[0] < xs[i]->shape[1] || xs[i]->strides[0] % 4)
+            layout_ok = 0;
+    if(!layout_ok || q->shape[0] != k->shape[0] || q->shape[1] != k->shape[1] ||
        q->shape[0] != v->shape[0] || q->shape[1] != v->shape[1] || batch <= 0 || n_heads <= 0 ||
        q->shape[0] % batch || q->shape[1] % n_heads) {
-        PKH_ERR("attention expects q, k, v [batch*T, heads*hd]!\n");
+        PKH_ERR("attention expects q, k, v [batch*T, heads*hd] with one row stride (a "
+                "multiple of 4) and unit columns!\n");
         return NULL;
     }
     struct Arena* arena = pkh_need_arena();
     if(!arena) return NULL;
     int64_t B = batch, H = n_heads, T = q->shape[0] / batch, hd = q->shape[1] / n_heads;
+    const int64_t ld = q->strides[0];
     struct PicoTensor* out = pkh_new_tensor(arena, q->shape, 2);
     if(!out) return NULL;
     struct PkNode* n = pkh_node(out);
@@ -258,9 +282,9 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     n->ival[AI_BF16] = flash && pico_get_matmul_precision() == PICO_MATMUL_BF16;
     n->fval[0] = 1.0f / sqrtf((float)hd);
     int st = flash ? (n->ival[AI_BF16] ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
-                         B, H, T, hd, n->fval[0], q->data, k->data, v->data, out->data, lse,
+                         B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, out->data, lse,
                          pkh_stream())
-                   : pk_attn_causal_fwd_f32(B, H, T, hd, n->fval[0], q->data, k->data, v->data,
+                   : pk_attn_causal_fwd_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
                                             out->data, lse, P, pkh_stream());
     if(pkh_status("pico_attention_causal", st)) return NULL;
     pkh_set_parents(arena, out, 3, xs, attn_backward);

@@ -27,8 +27,10 @@ struct PkNode {
     uint32_t grad_live;
     uint64_t visit;
     uint32_t seed_one; /* this node is the entry pico_backward seeded with 1 */
-    uint32_t pad_;
+    uint32_t n_views;  /* column-block views made of this tensor (pico_split_cols) */
     uint64_t side_seq; /* the side-stream fork that last wrote this grad (0: none) */
+    struct PicoTensor* base;    /* a view: the tensor whose data and grad it shares */
+    struct PicoTensor** views;  /* a split tensor: its views */
     void* saved[PKH_MAX_SAVED];
     int64_t ival[PKH_MAX_SAVED];
     float fval[PKH_MAX_SAVED];
@@ -95,10 +97,22 @@ int pkh_is_gpu(const struct PicoTensor* t);
 static inline void pkh_grad_on_main(const struct PkNode* n) {
     if(n && n->side_seq > pkh_side_joined()) pkh_side_join();
 }
+/* A split tensor's grad is the union of its views' grads.  Before it is used
+ * whole: if some views hold values, the columns of those that do not are
+ * zero-filled and the whole grad becomes live (tensor.c). */
+void pkh_grad_complete(struct PkNode* n);
+/* does t's grad hold values (for a view: its columns, written through it or
+ * through its base; for a split tensor: completed first) */
+static inline int pkh_node_live(struct PkNode* n) {
+    if(n->n_views && !n->grad_live) pkh_grad_complete(n);
+    if(n->grad_live) return 1;
+    struct PkNode* b = n->base ? pkh_node(n->base) : NULL;
+    return b ? (int)b->grad_live : 0;
+}
 static inline int pkh_grad_flag(const struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
     pkh_grad_on_main(n);
-    return (n && !n->grad_live) ? 0 : PK_ACCUM;
+    return (n && !pkh_node_live(n)) ? 0 : PK_ACCUM;
 }
 static inline void pkh_grad_mark(struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
@@ -107,7 +121,7 @@ static inline void pkh_grad_mark(struct PicoTensor* t) {
 static inline int pkh_grad_is_live(const struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
     pkh_grad_on_main(n);
-    return n ? (int)n->grad_live : 1;
+    return n ? pkh_node_live(n) : 1;
 }
 void pkh_set_parents(struct Arena* arena, struct PicoTensor* out, int n,
                      struct PicoTensor* const* ps, void (*bw)(struct PicoTensor*));

@@ -333,6 +333,71 @@ const float* pkh_upstream(struct PicoTensor* self) {
     return pkh_grad_is_live(self) ? self->grad : NULL;
 }
 
+/* ------------------------------------------------------ column-block views */
+void pkh_grad_complete(struct PkNode* n) {
+    int any = 0;
+    for(uint32_t i = 0; i < n->n_views; i++) any |= pkh_node(n->views[i])->grad_live != 0;
+    if(!any) return; /* nothing written: the grad stays empty */
+    for(uint32_t i = 0; i < n->n_views; i++) {
+        struct PicoTensor* v = n->views[i];
+        struct PkNode* vn = pkh_node(v);
+        if(vn->grad_live) continue;
+        if(pkh_status("pico_split_cols (zero grad)",
+                      pk_fill2d_f32(v->shape[0], v->shape[1], 0.0f, v->grad, v->strides[0],
+                                    pkh_stream())))
+            return;
+        vn->grad_live = 1;
+    }
+    n->grad_live = 1;
+}
+
+/* no reference counterpart (the reference's only view is pico_transpose_2d):
+ * views share t's data and grad, so nothing is copied either way */
+int pico_split_cols(struct PicoTensor* t, int n, struct PicoTensor** outs) {
+    struct PkNode* tn = pkh_node(t);
+    if(!t || !tn || !pkh_is_gpu(t) || !outs || n < 1) {
+        PKH_ERR("pico_split_cols: expects a GPU tensor of this library and n >= 1!\n");
+        return PK_EINVAL;
+    }
+    if(t->ndim != 2 || t->strides[1] != 1 || t->strides[0] != t->shape[1] ||
+       t->shape[1] % n || tn->base || tn->n_views || t->is_persistent) {
+        PKH_ERR("pico_split_cols: expects a contiguous, unsplit, non-parameter [M, n*C] tensor!\n");
+        return PK_EINVAL;
+    }
+    struct Arena* a = pkh_need_arena();
+    if(!a) return PK_EINVAL;
+    const int64_t M = t->shape[0], C = t->shape[1] / n;
+    struct PicoTensor** vs = (struct PicoTensor**)arena_alloc(a, sizeof(*vs) * (size_t)n);
+    if(!vs) return PK_EINVAL;
+    for(int i = 0; i < n; i++) {
+        struct PkNode* vn = (struct PkNode*)arena_alloc(a, sizeof(struct PkNode));
+        int64_t* shape = (int64_t*)arena_alloc(a, sizeof(int64_t) * 2);
+        int64_t* strides = (int64_t*)arena_alloc(a, sizeof(int64_t) * 2);
+        if(!vn || !shape || !strides) return PK_EINVAL;
+        memset(vn, 0, sizeof(*vn));
+        vn->magic = PKH_MAGIC;
+        vn->base = t;
+        struct PicoTensor* v = &vn->t;
+        shape[0] = M;
+        shape[1] = C;
+        strides[0] = t->shape[1];
+        strides[1] = 1;
+        v->shape = shape;
+        v->strides = strides;
+        v->ndim = 2;
+        v->numel = M * C;
+        v->backend = GPU;
+        v->data = t->data + i * C;
+        v->grad = t->grad + i * C;
+        pkh_set_parents(a, v, 1, &t, NULL);
+        vs[i] = v;
+    }
+    tn->views = vs;
+    tn->n_views = (uint32_t)n;
+    for(int i = 0; i < n; i++) outs[i] = vs[i];
+    return 0;
+}
+
 /* ------------------------------------------------------------ pico_rand/n */
 static inline uint32_t xorshift32(void) {
     uint32_t x = x_state;

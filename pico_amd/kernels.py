@@ -302,61 +302,71 @@ def swiglu_bwd(a, u, dh, da, du, accum_da=False, accum_du=False):
         _ptr(da), _ptr(du), ldd, flags, _stream()))
 
 
-def attn_fwd(B, H, q, k, v, o, lse, P, scale=None):
+def _attn_layout(B, H, q, k, v, o, *grads):
+    """(T, hd, ld): q, k, v and their grads [B*T, H*hd] with unit column stride
+    and one shared row stride ld >= H*hd (column blocks of a fused projection
+    allowed); o (and dout) contiguous."""
+    _f32(q, k, v, o, *grads)
     BT, D = q.shape
     T, hd = BT // B, D // H
-    if B * T != BT or H * hd != D or P.numel() < B * H * T * T or lse.numel() < B * H * T:
+    ld = q.stride(0) if BT > 1 else D
+    if B * T != BT or H * hd != D or o.shape != q.shape:
+        raise ValueError("attention shape mismatch")
+    for t in (q, k, v) + tuple(grads):
+        if t.shape != q.shape or (BT > 1 and t.stride(0) != ld) or (D > 1 and t.stride(1) != 1):
+            raise ValueError("q, k, v and their gradients need one row stride and unit columns")
+    if ld < D or not o.is_contiguous():
+        raise ValueError("attention: row stride below H*hd, or o not contiguous")
+    return T, hd, ld
+
+
+def attn_fwd(B, H, q, k, v, o, lse, P, scale=None):
+    T, hd, ld = _attn_layout(B, H, q, k, v, o)
+    if P.numel() < B * H * T * T or lse.numel() < B * H * T:
         raise ValueError("attention shape mismatch")
     scale = hd ** -0.5 if scale is None else scale
     check("pk_attn_causal_fwd_f32", hip_lib().pk_attn_causal_fwd_f32(
-        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(P), _stream()))
+        B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(P),
+        _stream()))
 
 
 def attn_bwd(B, H, q, k, v, P, dout, dq, dk, dv, dP_ws, accumulate=False, scale=None):
-    BT, D = q.shape
-    T, hd = BT // B, D // H
+    T, hd, ld = _attn_layout(B, H, q, k, v, dout, dq, dk, dv)
     if dP_ws.numel() < B * H * T * T:
         raise ValueError("attention backward workspace too small")
     scale = hd ** -0.5 if scale is None else scale
     check("pk_attn_causal_bwd_f32", hip_lib().pk_attn_causal_bwd_f32(
-        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(P), _ptr(dout), _ptr(dq), _ptr(dk),
-        _ptr(dv), _ptr(dP_ws), 7 if accumulate else 0, _stream()))
+        B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(P), _ptr(dout), _ptr(dq),
+        _ptr(dk), _ptr(dv), _ptr(dP_ws), 7 if accumulate else 0, _stream()))
 
 
 def flash_supported(T, hd):
     return bool(hip_lib().pk_flash_attn_supported(T, hd))
 
 
-def _flash_shapes(B, H, *ts):
-    BT, D = ts[0].shape
-    T, hd = BT // B, D // H
-    _f32(*ts)
-    if B * T != BT or H * hd != D or any(t.shape != ts[0].shape for t in ts):
-        raise ValueError("attention shape mismatch")
-    return T, hd
-
-
 def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False):
     """Fused causal attention; bf16=True rounds the matrix-product operands to
     bf16 (pk_flash_attn_fwd_bf16_f32)."""
-    T, hd = _flash_shapes(B, H, q, k, v, o)
+    T, hd, ld = _attn_layout(B, H, q, k, v, o)
     if lse.numel() < B * H * T:
         raise ValueError("attention shape mismatch")
     scale = hd ** -0.5 if scale is None else scale
     name = "pk_flash_attn_fwd_bf16_f32" if bf16 else "pk_flash_attn_fwd_f32"
     check(name, getattr(hip_lib(), name)(
-        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
+        B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
 
 
 def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False):
-    T, hd = _flash_shapes(B, H, q, k, v, o, dout, dq, dk, dv)
+    T, hd, ld = _attn_layout(B, H, q, k, v, o, dq, dk, dv)
+    if not dout.is_contiguous() or dout.shape != o.shape:
+        raise ValueError("attention: dout must be contiguous like o")
     scale = hd ** -0.5 if scale is None else scale
     need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
     ws = torch.empty(max(1, need // 4), device=q.device, dtype=torch.float32)
     name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
     check(name, getattr(hip_lib(), name)(
-        B, H, T, hd, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout), _ptr(dq),
-        _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() * 4, flags, _stream()))
+        B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout),
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() * 4, flags, _stream()))
 
 
 def causal_softmax_fwd(BH, T, S, P, lse, scale=1.0):

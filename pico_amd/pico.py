@@ -119,6 +119,7 @@ _GPU_SIGS = {
     "pico_gpt_param": (TP, [c_p, ctypes.c_int]),
     "pico_gpt_free": (None, [c_p]),
     "pico_gpt_param_name": (ctypes.c_char_p, [c_p, ctypes.c_int]),
+    "pico_split_cols": (ctypes.c_int, [TP, ctypes.c_int, ctypes.POINTER(TP)]),
     "pico_set_matmul_precision": (ctypes.c_int, [ctypes.c_int]),
     "pico_get_matmul_precision": (ctypes.c_int, []),
     "pico_checkpoint_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),
@@ -302,6 +303,13 @@ class Pico:
 
                 return call
         raise AttributeError(name)
+
+    def split_cols(self, t, n):
+        """pico_split_cols: n column-block views of t [M, n*C]"""
+        outs = (TP * n)()
+        if self.lib.pico_split_cols(t, n, outs):
+            raise PicoError("pico_split_cols failed")
+        return list(outs)
 
     def xent(self, logits, labels):
         return self._check(self.lib.pico_softmax_xent(logits, self.ids(labels)),

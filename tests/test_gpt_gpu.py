@@ -48,10 +48,10 @@ def _gpu_step(P, model, tokens, targets, arena_bytes=1 << 28):
 
 
 def _host_params(P, model, cfg):
-    out = []
-    for t in P.gpt_params(model):
-        out.append(P.value(t).astype(np.float64))
-    return out
+    """the GPU model's weights as the reference's separate float64 weights
+    (gpt.c keeps wqkv = [Wq|Wk|Wv] and w13 = [W1|W3] fused)"""
+    return [p.astype(np.float64) for p in
+            G.split_fused([P.value(t) for t in P.gpt_params(model)], cfg)]
 
 
 def _check_step(P, cfg, seed):
@@ -60,11 +60,12 @@ def _check_step(P, cfg, seed):
         tokens, targets, _ = _batch(cfg, seed + 1)
         params = _host_params(P, model, cfg)
         loss, grads = _gpu_step(P, model, tokens, targets)
+        grads = G.split_fused(grads, cfg)  # compared weight by weight
         ref_loss, ref_grads = G.loss_and_grads(params, cfg, tokens, targets)
         assert abs(loss - ref_loss) <= TOL * abs(ref_loss)
         assert len(grads) == len(ref_grads)
         for i, (g, r) in enumerate(zip(grads, ref_grads)):
-            assert max_rel(g, r.ravel()) <= TOL, (i, max_rel(g, r.ravel()))
+            assert max_rel(g.ravel(), r.ravel()) <= TOL, (i, max_rel(g.ravel(), r.ravel()))
     finally:
         P.gpt_free(model)
 
@@ -102,7 +103,7 @@ def test_config4_adamw_loss_curve(P):
                 P.optim_adamw_step(opt)
                 gpu.append(float(P.data(loss)[0]))
                 P.reset(ar)
-        final_gpu = [P.value(t) for t in tensors]
+        final_gpu = G.split_fused([P.value(t) for t in tensors], cfg)
         P.optim_adamw_free(opt)
         ref = []
         m = [np.zeros_like(p) for p in params]

@@ -73,3 +73,15 @@ def test_zero_weights_give_uniform_prediction():
     loss, grads = G.loss_and_grads(params, CFG, np.zeros(n, int), targets)
     assert loss == pytest.approx(np.log(CFG["vocab"]), rel=1e-15)
     assert all(not np.any(g) for g in grads[:-1])
+
+
+def test_fused_parameter_mapping_round_trips():
+    # gpt.c's fused wqkv = [Wq|Wk|Wv], w13 = [W1|W3] against separate weights
+    cfg = dict(vocab=7, d_model=4, n_layers=2, n_heads=2, d_ff=6)
+    sep = _params(cfg, 5)
+    fused = G.join_fused(sep, cfg)
+    assert len(fused) == 3 + G.FUSED_PER_LAYER * cfg["n_layers"]
+    assert fused[2].shape == (4, 12) and fused[5].shape == (4, 12)
+    assert np.array_equal(fused[2][:, 4:8], sep[3]) and np.array_equal(fused[5][:, 6:], sep[8])
+    back = G.split_fused([f.ravel() for f in fused], cfg)
+    assert all(np.array_equal(a.reshape(b.shape), b) for a, b in zip(back, sep))

@@ -456,6 +456,35 @@ def test_flash_attention_vs_oracle(dev, B, H, T):
         assert max_rel(host(got) - b0, ref) <= TOL
 
 
+@pytest.mark.parametrize("flash", [True, False])
+def test_attention_strided_qkv_views(dev, flash):
+    # q, k, v (and dq, dk, dv) as the column blocks of one [B*T, 3*H*hd]
+    # projection: row stride 3*H*hd; o and dout contiguous
+    B, H, T = 2, 2, 128
+    hd = 64 if flash else 32
+    D = H * hd
+    q, k, v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (81, 82, 83, 84))
+    qkv = cu(np.concatenate([q, k, v], 1))
+    qv, kv, vv = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    assert qv.stride(0) == 3 * D
+    o = torch.empty(B * T, D, device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    o_ref, lse_ref = O.attn_fwd(B, H, q, k, v)
+    g = torch.full((B * T, 3 * D), float("nan"), device=dev)
+    gq, gk, gv = g[:, :D], g[:, D:2 * D], g[:, 2 * D:]
+    if flash:
+        K.flash_fwd(B, H, qv, kv, vv, o, lse)
+        K.flash_bwd(B, H, qv, kv, vv, cu(o_ref), cu(lse_ref), cu(do), gq, gk, gv)
+    else:
+        P = torch.empty(B * H * T * T, device=dev)
+        K.attn_fwd(B, H, qv, kv, vv, o, lse, P)
+        K.attn_bwd(B, H, qv, kv, vv, P, cu(do), gq, gk, gv, torch.empty_like(P))
+    assert max_rel(host(o), o_ref) <= TOL and max_rel(host(lse), lse_ref) <= TOL
+    refs = O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)
+    for got, ref in zip((gq, gk, gv), refs):
+        assert max_rel(host(got), ref) <= TOL
+
+
 def test_flash_attention_causality(dev):
     # a change to the last key/value of each sequence leaves every earlier
     # query's output unchanged (bit for bit) and changes the last one

@@ -103,6 +103,40 @@ def test_weight_grad_side_stream_orders_with_main_stream_writes(P):
     P.free(W)
 
 
+def test_split_cols_views_share_data_and_grad(P):
+    # t = x.W [2, 6] split into three [2, 2] column views.  v0 feeds v0*v0, v2
+    # feeds the sum directly and v1 feeds nothing, so dt = [2*v0 | 0 | 1] and
+    # dW = x^T.dt; every value is a small integer, so the check is exact.
+    x_v = [1, 2, 3, 4]
+    w = [1, 0, 2, -1, 1, 3, 0, 1, -2, 1, 2, -1]
+    with P.arena():
+        x = P.tensor([2, 2], x_v)
+        W = P.param([2, 6], w)
+        t = P.matmul(x, W)
+        v0, v1, v2 = P.split_cols(t, 3)
+        tv = np.array(x_v, float).reshape(2, 2) @ np.array(w, float).reshape(2, 6)
+        assert np.array_equal(P.value(t), tv)
+        for i, v in enumerate((v0, v1, v2)):
+            # the views are windows into t's storage: same data and grad, 2*i floats in
+            assert P.shape(v) == (2, 2) and P.strides(v) == (6, 1)
+            assert (ctypes.cast(v.contents.data, ctypes.c_void_p).value ==
+                    ctypes.cast(t.contents.data, ctypes.c_void_p).value + 8 * i)
+            assert (ctypes.cast(v.contents.grad, ctypes.c_void_p).value ==
+                    ctypes.cast(t.contents.grad, ctypes.c_void_p).value + 8 * i)
+        P.backward(P.add(P.mul(v0, v0), v2))
+        dt = np.concatenate([2 * tv[:, 0:2], np.zeros((2, 2)), np.ones((2, 2))], 1)
+        want = np.array(x_v, float).reshape(2, 2).T @ dt
+        assert np.array_equal(P.grad_value(W), want)
+        # a view of a view, a param and a non-divisible width are refused
+        with pytest.raises(PicoError):
+            P.split_cols(v0, 2)
+        with pytest.raises(PicoError):
+            P.split_cols(W, 2)
+        with pytest.raises(PicoError):
+            P.split_cols(t, 4)
+    P.free(W)
+
+
 def test_matmul_transposed_view_matches_oracle(P, C):
     # a pico_transpose_2d view (tensor.c:230-244) is read as 'T' and its grad
     # lands with the view's strides, as the reference's backward loops index it
