@@ -6,14 +6,15 @@
 // restrictions attention uses.
 //
 // Design (one 256-thread workgroup = 4 waves per C tile):
-//  * Four tile shapes built from v_mfma_f32_32x32x2f32 blocks (4096 FLOP per
+//  * Five tile shapes built from v_mfma_f32_32x32x2f32 blocks (4096 FLOP per
 //    instruction, 16 fp32 accumulators per lane per block), chosen per call by
 //    how evenly they spread over the 256 CUs:
 //      256x256  2x2 waves of 128x128 (4x4 blocks, 256 accumulators held in
 //               AGPRs), one workgroup per CU -- large products;
+//      256x96   4x1 waves of 64x96, one per CU -- N a multiple of 96 (an
+//               [8192, 768] output, d_model 768, is 256 of them);
 //      128x128  2x2 waves of 64x64, two workgroups per CU;
-//      128x96   4x1 waves of 32x96, two per CU -- N a multiple of 96 (an
-//               [8192, 768] output, d_model 768, is 512 of them);
+//      128x96   4x1 waves of 32x96, two per CU -- N a multiple of 96;
 //      64x64    2x2 waves of 32x32, four per CU -- small products.
 //  * Tiles on the edge of C are handled in the same kernel: with M, N, K and
 //    the strides multiples of 4 each 128-bit load is predicated as a whole;
@@ -86,6 +87,7 @@ using Tile256 = Tile<256, 256, 2, 4, 4, 1>;
 using Tile128 = Tile<128, 128, 2, 2, 2, 2>;
 using Tile96 = Tile<128, 96, 4, 1, 3, 2>;
 using Tile64 = Tile<64, 64, 2, 1, 1, 4>;
+using Tile256x96 = Tile<256, 96, 4, 2, 3, 1>;
 
 struct GemmParams {
     const float* A;
@@ -683,15 +685,16 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
 
 // Tile shape: the estimated time of a shape is the work of the busiest CU --
 // its share of the tiles, ceil(tiles / 256 CUs), times the work of one tile in
-// units of a 128x128 tile (256x256: 4, 128x96: 0.75, 64x64: 0.25).
-// Workgroups resident on one CU share its matrix pipes, and a CU with no tile
-// adds nothing.  The 256x256 shape (one workgroup per CU) runs its MFMAs
-// about 5 % more efficiently; 64x64 tiles move twice the operand bytes per
-// FLOP of 128x128 ones and are charged 20 % for it.  Examples: 4096^2 -> 256
-// tiles of 256x256; an [8192, 768] output (every projection of a d_model-768
-// transformer) -> 512 of 128x96; 2048^2 -> 256 of 128x128; 1024^2 -> 256 of
-// 64x64 rather than 64 of 128x128.
-enum TileKind { kTile128, kTile96, kTile256, kTile64 };
+// units of a 128x128 tile (256x256: 4, 256x96: 1.5, 128x96: 0.75, 64x64:
+// 0.25).  Workgroups resident on one CU share its matrix pipes, and a CU with
+// no tile adds nothing.  The one-per-CU shapes (256x256, 256x96) run their
+// MFMAs about 5 % more efficiently (measured 1-5 % for 256x96 against 128x96
+// at [8192, 768] and [8192, 2304], K 768-4096); 64x64 tiles move twice the
+// operand bytes per FLOP of 128x128 ones and are charged 20 % for it.
+// Examples: 4096^2 -> 256 tiles of 256x256; an [8192, 768] output (every
+// projection of a d_model-768 transformer) -> 256 of 256x96; 2048^2 -> 256
+// of 128x128; 1024^2 -> 256 of 64x64 rather than 64 of 128x128.
+enum TileKind { kTile128, kTile96, kTile256, kTile64, kTile256x96 };
 constexpr int64_t kCUs = 256;
 
 struct TileChoice {
@@ -715,6 +718,10 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
     if(N % 96 == 0) consider(kTile96, 128, 96, cost(128, 96, 0.75));
     if(allow_all) {
         consider(kTile64, 64, 64, cost(64, 64, 0.25) * 1.2);
+        if(N % 96 == 0 && cost(256, 96, 1.5) / 1.05 <= c) {
+            c = cost(256, 96, 1.5) / 1.05;
+            best = {kTile256x96, 256, 96};
+        }
         if(cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
     }
     return best;
@@ -747,6 +754,7 @@ int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, int pre
            hipStream_t st) {
     switch(kind) {
     case kTile256: return launch_tile<TA, TB, Tile256>(gp, batch, edge, prec, st);
+    case kTile256x96: return launch_tile<TA, TB, Tile256x96>(gp, batch, edge, prec, st);
     case kTile96: return launch_tile<TA, TB, Tile96>(gp, batch, edge, prec, st);
     case kTile64: return launch_tile<TA, TB, Tile64>(gp, batch, edge, prec, st);
     default: return launch_tile<TA, TB, Tile128>(gp, batch, edge, prec, st);

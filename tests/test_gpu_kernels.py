@@ -504,10 +504,12 @@ def test_flash_attention_causality(dev):
 
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
 @pytest.mark.parametrize("M,N,Kd", [(8192, 768, 768), (1000, 768, 200), (4096, 2304, 256),
-                                    (8192, 768, 2048)])
+                                    (8192, 768, 2048), (8000, 768, 772), (8001, 768, 37)])
 def test_gemm_96_wide_tiles(dev, ta, tb, M, N, Kd):
-    # N a multiple of 96: these shapes take the 128 x 96 tiles that fill the
-    # 512 resident workgroup slots (a d_model-768 transformer's projections)
+    # N a multiple of 96: [8192, 768] (a d_model-768 transformer's
+    # projections) and 8000 / 8001 rows take the 256 x 96 tiles, one per CU --
+    # 8000 x 772 on the float4 edge path, 8001 x 37 on the scalar one; 1000 x
+    # 768 and 4096 x 2304 the 128 x 96 ones, two per CU
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 3 * N + Kd, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
     K.gemm(ta, tb, cu(As), cu(Bs), C)
@@ -543,7 +545,7 @@ def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
 def test_gemm_vector_edge_tiles(dev, ta, tb, M, N, Kd):
     # sizes that are multiples of 4 but not of the tile: partial tiles load
     # whole float4 under a predicate (d_ff = 1376 in the 1-layer config);
-    # 8192 x 768 takes 128 x 96 tiles, 1024^2 and 200 x 64 the 64 x 64 ones
+    # 8192 x 768 takes 256 x 96 tiles, 1024^2 and 200 x 64 the 64 x 64 ones
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 7 * N + Kd, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
     K.gemm(ta, tb, cu(As), cu(Bs), C)
