@@ -195,6 +195,15 @@ size_t pk_rmsnorm_bwd_workspace(int64_t R, int64_t C);
 int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const float* g, const float* rstd,
                        const float* dy, float* dx, float* dg, int flags, void* workspace,
                        size_t workspace_bytes, pk_stream_t stream);
+/* as pk_rmsnorm_bwd_f32, with the accumulated term of dx read from dx_in:
+ * dx = dx_in + rstd*(g*dy) - x*rstd^3*mean(g*dy*x), or without the dx_in term
+ * when dx_in is NULL (dx_in == dx is pk_rmsnorm_bwd_f32's accumulate); flags
+ * bit 1 accumulates dg, bit 0 is ignored.  pico's backward uses it to add the
+ * residual stream's gradient without first copying it into dx. */
+int pk_rmsnorm_bwd_into_f32(int64_t R, int64_t C, const float* x, const float* g,
+                            const float* rstd, const float* dy, const float* dx_in, float* dx,
+                            float* dg, int flags, void* workspace, size_t workspace_bytes,
+                            pk_stream_t stream);
 /* SwiGLU on [R,F] gate/up pairs (row strides lda, ldu, ldh): h = silu(a) * u */
 int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const float* u,
                       int64_t ldu, float* h, int64_t ldh, pk_stream_t stream);

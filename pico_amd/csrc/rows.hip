@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
                                                        const float* __restrict__ g,
                                                        const float* __restrict__ rstd,
                                                        const float* __restrict__ dy,
-                                                       float* __restrict__ dx,
+                                                       const float* dxin, float* dx,
                                                        float* __restrict__ ws, int flags) {
     extern __shared__ float part[];  // C floats
     const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -346,13 +346,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_reg(int64_t R, int64_t C,
         const float rs = rstd[row];
         const float k = rs * rs * rs * dot * invC;
         f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * C);
+        const f32x4* dxi = reinterpret_cast<const f32x4*>(dxin + row * C);
 #pragma unroll
         for(int v = 0; v < NV; ++v) {
             const int64_t c = lane + v * 64;
             if(c < C4) {
                 if(flags & 4) {
                     f32x4 o = rs * gv[v] * dv[v] - xv[v] * k;
-                    if(flags & PK_ACCUM) o = o + dxr[c];
+                    if(flags & PK_ACCUM) o = o + dxi[c];
                     pk::st_stream(dxr + c, o);
                 }
                 dg[v] = dg[v] + dv[v] * xv[v] * rs;
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_cols(int64_t R, int64_t C,
                                                         const float* __restrict__ g,
                                                         const float* __restrict__ rstd,
                                                         const float* __restrict__ dy,
-                                                        float* __restrict__ dx,
+                                                        const float* dxin, float* dx,
                                                         float* __restrict__ ws, int flags) {
     __shared__ float red[2][4];
     const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -442,13 +443,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_cols(int64_t R, int64_t C,
         const float rs = rstd[row];
         const float k = rs * rs * rs * dot * invC;
         f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * C) + c0;
+        const f32x4* dxi = reinterpret_cast<const f32x4*>(dxin + row * C) + c0;
 #pragma unroll
         for(int v = 0; v < NQ; ++v) {
             if(!on[v]) continue;
             const int64_t q = lane + v * 64;
             if(flags & 4) {
                 f32x4 o = rs * gv[v] * dv[v] - xv[v] * k;
-                if(flags & PK_ACCUM) o = o + dxr[q];
+                if(flags & PK_ACCUM) o = o + dxi[q];
                 pk::st_stream(dxr + q, o);
             }
             dg[v] = dg[v] + dv[v] * xv[v] * rs;
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_any(int64_t R, int64_t C,
                                                        const float* __restrict__ g,
                                                        const float* __restrict__ rstd,
                                                        const float* __restrict__ dy,
-                                                       float* __restrict__ dx,
+                                                       const float* dxin, float* dx,
                                                        float* __restrict__ ws, int flags) {
     // one wave per row for dx; dg partials accumulated per block column-wise
     const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -489,7 +491,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_any(int64_t R, int64_t C,
         if(flags & 4)
             for(int64_t c = lane; c < C; c += 64) {
                 float o = rs * g[c] * dyr[c] - xr[c] * k;
-                dx[row * C + c] = (flags & PK_ACCUM) ? dx[row * C + c] + o : o;
+                dx[row * C + c] = (flags & PK_ACCUM) ? dxin[row * C + c] + o : o;
             }
     }
     if(!(flags & 8)) return;
@@ -882,6 +884,14 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
                                   const float* rstd, const float* dy, float* dx, float* dg,
                                   int flags, void* workspace, size_t workspace_bytes,
                                   pk_stream_t stream) {
+    return pk_rmsnorm_bwd_into_f32(R, C, x, g, rstd, dy, (flags & PK_ACCUM) ? dx : nullptr, dx,
+                                   dg, flags & PK_ACCUM2, workspace, workspace_bytes, stream);
+}
+
+extern "C" int pk_rmsnorm_bwd_into_f32(int64_t R, int64_t C, const float* x, const float* g,
+                                       const float* rstd, const float* dy, const float* dx_in,
+                                       float* dx, float* dg, int flags, void* workspace,
+                                       size_t workspace_bytes, pk_stream_t stream) {
     if(R < 0 || C < 1) return pk::fail("pk_rmsnorm_bwd_f32: need R >= 0 and C >= 1");
     if(R == 0) return PK_OK;
     if(!x || !g || !rstd || !dy) return pk::fail("pk_rmsnorm_bwd_f32: NULL input pointer");
@@ -892,10 +902,12 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
                         pk_rmsnorm_bwd_workspace(R, C));
     hipStream_t st = pk::as_stream(stream);
     float* ws = (float*)workspace;
-    // internal flags: 4 = write dx, 8 = produce dg partials; bit 0 = accumulate dx
-    const int kf = (flags & PK_ACCUM) | (dx ? 4 : 0) | (dg ? 8 : 0);
+    // internal flags: 4 = write dx, 8 = produce dg partials; bit 0 = add dx_in
+    const float* dxin = dx ? dx_in : nullptr;
+    const int kf = (dxin ? PK_ACCUM : 0) | (dx ? 4 : 0) | (dg ? 8 : 0);
     const bool vec = C % 4 == 0 && pk::aligned16(x) && pk::aligned16(g) && pk::aligned16(dy) &&
-                     (!dx || pk::aligned16(dx)) && (!ws || pk::aligned16(ws));
+                     (!dx || pk::aligned16(dx)) && (!dxin || pk::aligned16(dxin)) &&
+                     (!ws || pk::aligned16(ws));
     const int nv = vec && C <= 8192 ? pick_nv(C) : 0;
     const size_t lds = (size_t)C * sizeof(float);
     if(vec && C / 4 >= 512 && C <= 16384) {
@@ -903,9 +915,9 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
         const unsigned grid = (unsigned)P;
 #define PK_RMSB(NQ_)                                                                           \
     if(C % 1024 == 0 && Q == NQ_ * 64)                                                          \
-        rmsnorm_bwd_cols<NQ_, true><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dx, ws, kf);   \
+        rmsnorm_bwd_cols<NQ_, true><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf);   \
     else                                                                                        \
-        rmsnorm_bwd_cols<NQ_, false><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dx, ws, kf)
+        rmsnorm_bwd_cols<NQ_, false><<<grid, 256, 0, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf)
         if(Q <= 128) {
             PK_RMSB(2);
         } else if(Q <= 256) {
@@ -917,13 +929,13 @@ extern "C" int pk_rmsnorm_bwd_f32(int64_t R, int64_t C, const float* x, const fl
         }
 #undef PK_RMSB
     } else switch(nv) {
-        case 1: rmsnorm_bwd_reg<1><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        case 2: rmsnorm_bwd_reg<2><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        case 4: rmsnorm_bwd_reg<4><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        case 8: rmsnorm_bwd_reg<8><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        case 16: rmsnorm_bwd_reg<16><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        case 32: rmsnorm_bwd_reg<32><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dx, ws, kf); break;
-        default: rmsnorm_bwd_any<<<(unsigned)P, 256, 0, st>>>(R, C, x, g, rstd, dy, dx, ws, kf);
+        case 1: rmsnorm_bwd_reg<1><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        case 2: rmsnorm_bwd_reg<2><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        case 4: rmsnorm_bwd_reg<4><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        case 8: rmsnorm_bwd_reg<8><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        case 16: rmsnorm_bwd_reg<16><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        case 32: rmsnorm_bwd_reg<32><<<(unsigned)P, 256, lds, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf); break;
+        default: rmsnorm_bwd_any<<<(unsigned)P, 256, 0, st>>>(R, C, x, g, rstd, dy, dxin, dx, ws, kf);
     }
     int rc = pk::launch_status("pk_rmsnorm_bwd_f32");
     if(rc || !dg) return rc;

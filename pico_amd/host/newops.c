@@ -103,9 +103,11 @@ static void rms_backward(struct PicoTensor* self) {
     size_t ws_bytes = pk_rmsnorm_bwd_workspace(R, C);
     void* ws = pkh_workspace(ws_bytes);
     if(!ws && ws_bytes) return;
-    int flags = (pkh_grad_flag(x) ? PK_ACCUM : 0) | (pkh_grad_flag(gain) ? PK_ACCUM2 : 0);
-    int st = pk_rmsnorm_bwd_f32(R, C, x->data, gain->data, (const float*)n->saved[RS_RSTD], dy,
-                                x->grad, gain->grad, flags, ws, ws_bytes, pkh_stream());
+    const float* dx_in = pkh_grad_base(x);
+    int flags = pkh_grad_flag(gain) ? PK_ACCUM2 : 0;
+    int st = pk_rmsnorm_bwd_into_f32(R, C, x->data, gain->data, (const float*)n->saved[RS_RSTD],
+                                     dy, dx_in, x->grad, gain->grad, flags, ws, ws_bytes,
+                                     pkh_stream());
     if(pkh_status("pico_rmsnorm_backward", st)) return;
     pkh_grad_mark(x);
     pkh_grad_mark(gain);
@@ -301,7 +303,7 @@ static void emb_backward(struct PicoTensor* self) {
     const float* g = pkh_upstream(self);
     if(!g) return;
     int64_t V = tab->shape[0], d = tab->shape[1];
-    if(!pkh_grad_is_live(tab)) {
+    if(!pkh_grad_flag(tab)) {
         /* rows no id touches must read as zero */
         if(pkh_status("pico_embedding_backward", pk_fill_f32(tab->numel, 0.0f, tab->grad,
                                                                pkh_stream())))

@@ -33,6 +33,19 @@ static void mapped_strides(const struct PicoTensor* t, int ndim, int64_t* out) {
     }
 }
 
+/* t has self's shape and is stored row-major, so its grad and self's index
+ * alike */
+static int same_layout(const struct PicoTensor* t, const struct PicoTensor* self) {
+    if(t->ndim != self->ndim) return 0;
+    int64_t stride = 1;
+    for(int d = t->ndim - 1; d >= 0; d--) {
+        if(t->shape[d] != self->shape[d]) return 0;
+        if(t->shape[d] > 1 && t->strides[d] != stride) return 0;
+        stride *= t->shape[d];
+    }
+    return 1;
+}
+
 /* ---------------------------------------------------- binary: seam twins */
 static int binary_gpu(int op, struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
     int64_t sa[256], sb[256];
@@ -63,14 +76,20 @@ static void binary_backward(int op, struct PicoTensor* self) {
     mapped_strides(a, nd, sa);
     mapped_strides(b, nd, sb);
     static const char* names[3] = {"pico_add_backward", "pico_sub_backward", "pico_mul_backward"};
-    int st = pk_binary_bwd_f32(op, 0, nd, self->shape, sa, sb, a->numel, g, b->data, a->grad,
-                               pkh_grad_flag(a), pkh_stream());
-    if(pkh_status(names[op], st)) return;
-    pkh_grad_mark(a);
-    st = pk_binary_bwd_f32(op, 1, nd, self->shape, sb, sa, b->numel, g, a->data, b->grad,
-                           pkh_grad_flag(b), pkh_stream());
-    if(pkh_status(names[op], st)) return;
-    pkh_grad_mark(b);
+    /* d(a+b)/da = d(a+b)/db = 1: an operand of self's shape whose grad is empty
+     * takes self's grad as it is (an alias) instead of a copy of it */
+    if(!(op == OP_ADD && same_layout(a, self) && pkh_grad_alias(a, self))) {
+        int st = pk_binary_bwd_f32(op, 0, nd, self->shape, sa, sb, a->numel, g, b->data, a->grad,
+                                   pkh_grad_flag(a), pkh_stream());
+        if(pkh_status(names[op], st)) return;
+        pkh_grad_mark(a);
+    }
+    if(!(op == OP_ADD && same_layout(b, self) && pkh_grad_alias(b, self))) {
+        int st = pk_binary_bwd_f32(op, 1, nd, self->shape, sb, sa, b->numel, g, a->data, b->grad,
+                                   pkh_grad_flag(b), pkh_stream());
+        if(pkh_status(names[op], st)) return;
+        pkh_grad_mark(b);
+    }
 }
 void pico_add_backward_gpu(struct PicoTensor* self) { binary_backward(OP_ADD, self); }
 void pico_sub_backward_gpu(struct PicoTensor* self) { binary_backward(OP_SUB, self); }

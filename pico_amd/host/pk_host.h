@@ -31,6 +31,8 @@ struct PkNode {
     uint64_t side_seq; /* the side-stream fork that last wrote this grad (0: none) */
     struct PicoTensor* base;    /* a view: the tensor whose data and grad it shares */
     struct PicoTensor** views;  /* a split tensor: its views */
+    float* own_grad; /* non-NULL: grad points at another tensor's final grad (an alias),
+                      * this is the tensor's own buffer */
     void* saved[PKH_MAX_SAVED];
     int64_t ival[PKH_MAX_SAVED];
     float fval[PKH_MAX_SAVED];
@@ -84,6 +86,8 @@ void* pkh_workspace(size_t bytes);
 int pkh_is_device_ptr(const void* p);
 int pkh_copy_h2d(void* dst, const void* src, size_t bytes);
 int pkh_copy_d2h(void* dst, const void* src, size_t bytes);
+/* device-to-device on the library's stream, not waited for */
+int pkh_copy_d2d_async(void* dst, const void* src, size_t bytes);
 
 /* tensors (tensor.c) */
 /* a GPU tensor node in `arena` with uninitialised device data and a
@@ -109,10 +113,34 @@ static inline int pkh_node_live(struct PkNode* n) {
     struct PkNode* b = n->base ? pkh_node(n->base) : NULL;
     return b ? (int)b->grad_live : 0;
 }
+/* Gradient aliases.  Where an op's backward would copy its upstream gradient
+ * unchanged into an operand's empty grad (the operands of c = a + b), the
+ * operand's grad pointer is set to c's grad instead (pkh_grad_alias): c's grad
+ * is final by then, and the operand reads the same values through it.  The
+ * first write into an aliased grad gives the tensor its own buffer back:
+ * pkh_grad_flag copies the aliased values into it and returns PK_ACCUM;
+ * pkh_grad_base returns the aliased buffer as the source of the accumulated
+ * term, for a kernel that writes own = source + contribution without the
+ * copy.  pico_backward restores the own buffers of the graph it is about to
+ * run, so a second backward over the same graph writes nothing shared. */
+int pkh_grad_alias(struct PicoTensor* t, const struct PicoTensor* src); /* 1: aliased */
+void pkh_grad_unalias(struct PkNode* n, int copy);
 static inline int pkh_grad_flag(const struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);
     pkh_grad_on_main(n);
+    if(n && n->own_grad) pkh_grad_unalias(n, 1);
     return (n && !pkh_node_live(n)) ? 0 : PK_ACCUM;
+}
+/* for a write t->grad = source + contribution: the source of the accumulated
+ * term (t's grad itself, an aliased grad, or NULL when t's grad is empty) */
+static inline const float* pkh_grad_base(struct PicoTensor* t) {
+    struct PkNode* n = pkh_node(t);
+    if(n && n->own_grad) {
+        const float* src = t->grad;
+        pkh_grad_unalias(n, 0);
+        return src;
+    }
+    return pkh_grad_flag(t) ? t->grad : NULL;
 }
 static inline void pkh_grad_mark(struct PicoTensor* t) {
     struct PkNode* n = pkh_node(t);

@@ -267,6 +267,13 @@ int pkh_copy_d2h(void* dst, const void* src, size_t bytes) {
     return e == hipSuccess ? 0 : pkh_status("device-to-host copy", (int)e);
 }
 
+int pkh_copy_d2d_async(void* dst, const void* src, size_t bytes) {
+    if(bytes == 0) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                  (hipStream_t)pkh_stream());
+    return e == hipSuccess ? 0 : pkh_status("device-to-device copy", (int)e);
+}
+
 /* ------------------------------------------------------------ device graphs */
 struct PicoGraph {
     hipGraph_t graph;

@@ -333,6 +333,28 @@ const float* pkh_upstream(struct PicoTensor* self) {
     return pkh_grad_is_live(self) ? self->grad : NULL;
 }
 
+/* ---------------------------------------------------------- grad aliases */
+int pkh_grad_alias(struct PicoTensor* t, const struct PicoTensor* src) {
+    struct PkNode* n = pkh_node(t);
+    struct PkNode* sn = pkh_node(src);
+    if(!n || !sn || t == src || t->is_persistent || n->base || n->n_views || n->own_grad ||
+       sn->base || t->numel != src->numel || !pkh_grad_is_live(src) || pkh_node_live(n))
+        return 0;
+    pkh_grad_on_main(n);
+    n->own_grad = t->grad;
+    t->grad = src->grad;
+    n->grad_live = 1;
+    return 1;
+}
+
+void pkh_grad_unalias(struct PkNode* n, int copy) {
+    if(!n->own_grad) return;
+    float* own = n->own_grad;
+    if(copy && pkh_copy_d2d_async(own, n->t.grad, sizeof(float) * (size_t)n->t.numel)) return;
+    n->t.grad = own;
+    n->own_grad = NULL;
+}
+
 /* ------------------------------------------------------ column-block views */
 void pkh_grad_complete(struct PkNode* n) {
     int any = 0;
@@ -512,6 +534,9 @@ void pico_backward(struct Arena* arena, struct PicoTensor* entry) {
             nv_push(&order, top);
         }
     }
+    /* a graph run a second time: its aliased grads get their own buffers
+     * back before anything accumulates into them */
+    for(int64_t i = 0; i < order.n; i++) pkh_grad_unalias(pkh_node(order.v[i]), 1);
     /* seed dL/dentry = 1 over every element (tensor.c:27-30) */
     if(pkh_status("pico_backward", pk_fill_f32(entry->numel, 1.0f, entry->grad, pkh_stream())))
         goto done;
@@ -551,6 +576,7 @@ int pico_tensor_grad_to_host(const struct PicoTensor* t, float* dst) {
 
 int pico_tensor_grad_from_host(struct PicoTensor* t, const float* src) {
     if(!t || !pkh_is_gpu(t)) return PK_EINVAL;
+    pkh_grad_unalias(pkh_node(t), 0);
     int rc = pkh_copy_h2d(t->grad, src, sizeof(float) * (size_t)t->numel);
     if(rc == 0) pkh_grad_mark(t);
     return rc;

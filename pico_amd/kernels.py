@@ -274,15 +274,23 @@ def rmsnorm_bwd_workspace(R, C):
     return int(hip_lib().pk_rmsnorm_bwd_workspace(R, C))
 
 
-def rmsnorm_bwd(x, g, rstd, dy, dx, dg, ws=None, accum_dx=False, accum_dg=False):
+def rmsnorm_bwd(x, g, rstd, dy, dx, dg, ws=None, accum_dx=False, accum_dg=False, dx_in=None):
+    """dx_in: the accumulated term of dx read from another buffer
+    (pk_rmsnorm_bwd_into_f32; accum_dx is then ignored)"""
     R, C = x.shape
     need = rmsnorm_bwd_workspace(R, C)
     if ws is None and dg is not None:
         ws = torch.empty(max(1, need // 4), device=x.device, dtype=torch.float32)
+    wsb = 0 if ws is None else ws.numel() * 4
+    if dx_in is not None:
+        check("pk_rmsnorm_bwd_into_f32", hip_lib().pk_rmsnorm_bwd_into_f32(
+            R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx_in), _ptr(dx), _ptr(dg),
+            ACCUM2 if accum_dg else 0, _ptr(ws), wsb, _stream()))
+        return
     flags = (ACCUM if accum_dx else 0) | (ACCUM2 if accum_dg else 0)
     check("pk_rmsnorm_bwd_f32", hip_lib().pk_rmsnorm_bwd_f32(
-        R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dg), flags, _ptr(ws),
-        0 if ws is None else ws.numel() * 4, _stream()))
+        R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dg), flags, _ptr(ws), wsb,
+        _stream()))
 
 
 def swiglu_fwd(a, u, h):

@@ -348,6 +348,12 @@ def test_rmsnorm_vs_oracle(dev, R, C):
     dx, dg = cu(dx0.copy()), cu(dg0.copy())
     K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx, dg, accum_dx=True, accum_dg=True)
     assert max_rel(host(dx), dx_ref) <= TOL and max_rel(host(dg), dg_ref) <= TOL
+    # the accumulated term read from another buffer: the same bits, the source untouched
+    src = cu(dx0.copy())
+    dx2, dg2 = torch.full((R, C), float("nan"), device=dev), cu(dg0.copy())
+    K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx2, dg2, accum_dg=True, dx_in=src)
+    assert np.array_equal(host(dx2), host(dx)) and np.array_equal(host(dg2), host(dg))
+    assert np.array_equal(host(src), dx0)
     dx, dg = torch.empty(R, C, device=dev), torch.empty(C, device=dev)  # overwrite mode
     K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx, dg)
     dx_ref, dg_ref = O.rmsnorm_bwd(x, g, rstd_ref, dy)
