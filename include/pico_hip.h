@@ -34,6 +34,9 @@ typedef void* pk_stream_t; /* a hipStream_t; NULL is the null stream */
 #define PK_ACCUM 1
 #define PK_ACCUM2 2
 #define PK_ACCUM3 4
+/* pk_rmsnorm_bwd_into_f32 with dg == NULL: leave dg's partial sums in the
+ * workspace for pk_rmsnorm_dg_reduce_f32 */
+#define PK_RMS_KEEP_PARTIALS 8
 
 /* ---- runtime ---------------------------------------------------------- */
 const char* pk_last_error(void);
@@ -204,6 +207,12 @@ int pk_rmsnorm_bwd_into_f32(int64_t R, int64_t C, const float* x, const float* g
                             const float* rstd, const float* dy, const float* dx_in, float* dx,
                             float* dg, int flags, void* workspace, size_t workspace_bytes,
                             pk_stream_t stream);
+/* dg (+)= the partial sums a pk_rmsnorm_bwd_into_f32 call with dg == NULL and
+ * PK_RMS_KEEP_PARTIALS left in `workspace` (same R, C); flags bit 0
+ * accumulates.  The two calls may run on different streams, ordered by the
+ * caller.  pico's backward runs this one on its weight-gradient stream. */
+int pk_rmsnorm_dg_reduce_f32(int64_t R, int64_t C, const void* workspace, size_t workspace_bytes,
+                             float* dg, int flags, pk_stream_t stream);
 /* SwiGLU on [R,F] gate/up pairs (row strides lda, ldu, ldh): h = silu(a) * u */
 int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const float* u,
                       int64_t ldu, float* h, int64_t ldh, pk_stream_t stream);

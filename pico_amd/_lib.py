@@ -67,6 +67,7 @@ PK_SIGNATURES = {
     "pk_rmsnorm_bwd_f32": [c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_size, c_p],
     "pk_rmsnorm_bwd_into_f32": [c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_p, c_size,
                                 c_p],
+    "pk_rmsnorm_dg_reduce_f32": [c_i64, c_i64, c_p, c_size, c_p, c_int, c_p],
     "pk_swiglu_fwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p],
     "pk_swiglu_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64,
                           c_int, c_p],

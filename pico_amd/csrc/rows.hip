@@ -895,16 +895,17 @@ extern "C" int pk_rmsnorm_bwd_into_f32(int64_t R, int64_t C, const float* x, con
     if(R < 0 || C < 1) return pk::fail("pk_rmsnorm_bwd_f32: need R >= 0 and C >= 1");
     if(R == 0) return PK_OK;
     if(!x || !g || !rstd || !dy) return pk::fail("pk_rmsnorm_bwd_f32: NULL input pointer");
-    if(!dx && !dg) return PK_OK;
+    const bool parts = dg || (flags & PK_RMS_KEEP_PARTIALS);
+    if(!dx && !parts) return PK_OK;
     const int64_t P = rms_parts(R);
-    if(dg && (!workspace || workspace_bytes < pk_rmsnorm_bwd_workspace(R, C)))
+    if(parts && (!workspace || workspace_bytes < pk_rmsnorm_bwd_workspace(R, C)))
         return pk::fail("pk_rmsnorm_bwd_f32: workspace needs %zu bytes",
                         pk_rmsnorm_bwd_workspace(R, C));
     hipStream_t st = pk::as_stream(stream);
     float* ws = (float*)workspace;
     // internal flags: 4 = write dx, 8 = produce dg partials; bit 0 = add dx_in
     const float* dxin = dx ? dx_in : nullptr;
-    const int kf = (dxin ? PK_ACCUM : 0) | (dx ? 4 : 0) | (dg ? 8 : 0);
+    const int kf = (dxin ? PK_ACCUM : 0) | (dx ? 4 : 0) | (parts ? 8 : 0);
     const bool vec = C % 4 == 0 && pk::aligned16(x) && pk::aligned16(g) && pk::aligned16(dy) &&
                      (!dx || pk::aligned16(dx)) && (!dxin || pk::aligned16(dxin)) &&
                      (!ws || pk::aligned16(ws));
@@ -942,6 +943,20 @@ extern "C" int pk_rmsnorm_bwd_into_f32(int64_t R, int64_t C, const float* x, con
     colsum_kernel<<<(unsigned)((C + 63) / 64), 64 * kColsumWaves, 0, st>>>(
         P, C, ws, dg, (flags & PK_ACCUM2) ? 1 : 0);
     return pk::launch_status("pk_rmsnorm_bwd_f32");
+}
+
+extern "C" int pk_rmsnorm_dg_reduce_f32(int64_t R, int64_t C, const void* workspace,
+                                        size_t workspace_bytes, float* dg, int flags,
+                                        pk_stream_t stream) {
+    if(R < 0 || C < 1) return pk::fail("pk_rmsnorm_dg_reduce_f32: need R >= 0 and C >= 1");
+    if(R == 0) return PK_OK;
+    if(!dg) return pk::fail("pk_rmsnorm_dg_reduce_f32: NULL dg");
+    if(!workspace || workspace_bytes < pk_rmsnorm_bwd_workspace(R, C))
+        return pk::fail("pk_rmsnorm_dg_reduce_f32: workspace needs %zu bytes",
+                        pk_rmsnorm_bwd_workspace(R, C));
+    colsum_kernel<<<(unsigned)((C + 63) / 64), 64 * kColsumWaves, 0, pk::as_stream(stream)>>>(
+        rms_parts(R), C, static_cast<const float*>(workspace), dg, (flags & PK_ACCUM) ? 1 : 0);
+    return pk::launch_status("pk_rmsnorm_dg_reduce_f32");
 }
 
 extern "C" int pk_swiglu_fwd_f32(int64_t R, int64_t F, const float* a, int64_t lda, const float* u,

@@ -92,7 +92,7 @@ struct PicoTensor* pico_softmax_xent(struct PicoTensor* logits, const int32_t* l
 
 /* ---------------------------------------------------------------- RMSNorm
  * y = x * rstd * gain over the last dim; the backward reads the saved rstd */
-enum { RS_RSTD = 0 };
+enum { RS_RSTD = 0, RS_PARTS = 1 };
 
 static void rms_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
@@ -101,13 +101,35 @@ static void rms_backward(struct PicoTensor* self) {
     if(!dy) return;
     int64_t C = x->shape[x->ndim - 1], R = C ? x->numel / C : 0;
     size_t ws_bytes = pk_rmsnorm_bwd_workspace(R, C);
-    void* ws = pkh_workspace(ws_bytes);
+    void* parts = n->saved[RS_PARTS];
+    void* ws = parts ? parts : pkh_workspace(ws_bytes);
     if(!ws && ws_bytes) return;
     const float* dx_in = pkh_grad_base(x);
+    const float* rstd = (const float*)n->saved[RS_RSTD];
+    if(parts) {
+        /* dgain like a weight gradient: the rows kernel leaves its partial
+         * sums in a buffer of this node, and the side stream reduces them */
+        int st = pk_rmsnorm_bwd_into_f32(R, C, x->data, gain->data, rstd, dy, dx_in, x->grad, NULL,
+                                         PK_RMS_KEEP_PARTIALS, parts, ws_bytes, pkh_stream());
+        if(pkh_status("pico_rmsnorm_backward", st)) return;
+        pkh_grad_mark(x);
+        struct PkNode* ng = pkh_node(gain);
+        pk_stream_t side = pkh_side_fork();
+        if(side) {
+            st = pk_rmsnorm_dg_reduce_f32(R, C, parts, ws_bytes, gain->grad,
+                                          ng->grad_live ? PK_ACCUM : 0, side);
+            ng->side_seq = pkh_side_seq();
+        } else {
+            st = pk_rmsnorm_dg_reduce_f32(R, C, parts, ws_bytes, gain->grad,
+                                          pkh_grad_flag(gain), pkh_stream());
+        }
+        if(pkh_status("pico_rmsnorm_backward", st)) return;
+        pkh_grad_mark(gain);
+        return;
+    }
     int flags = pkh_grad_flag(gain) ? PK_ACCUM2 : 0;
-    int st = pk_rmsnorm_bwd_into_f32(R, C, x->data, gain->data, (const float*)n->saved[RS_RSTD],
-                                     dy, dx_in, x->grad, gain->grad, flags, ws, ws_bytes,
-                                     pkh_stream());
+    int st = pk_rmsnorm_bwd_into_f32(R, C, x->data, gain->data, rstd, dy, dx_in, x->grad,
+                                     gain->grad, flags, ws, ws_bytes, pkh_stream());
     if(pkh_status("pico_rmsnorm_backward", st)) return;
     pkh_grad_mark(x);
     pkh_grad_mark(gain);
@@ -129,6 +151,12 @@ struct PicoTensor* pico_rmsnorm(struct PicoTensor* x, struct PicoTensor* gain, f
     if(!rstd) return NULL;
     n->saved[RS_RSTD] = rstd;
     n->fval[0] = eps;
+    /* a learned gain of an activation: its gradient's partial sums get a
+     * buffer of their own, so the reduction can run on the side stream */
+    if(gain->is_persistent && !x->is_persistent && R > 0) {
+        n->saved[RS_PARTS] = arena_alloc_device(arena, pk_rmsnorm_bwd_workspace(R, C));
+        if(!n->saved[RS_PARTS]) return NULL;
+    }
     int st = pk_rmsnorm_fwd_f32(R, C, eps, x->data, gain->data, out->data, rstd, pkh_stream());
     if(pkh_status("pico_rmsnorm", st)) return NULL;
     struct PicoTensor* ps[2] = {x, gain};

@@ -274,23 +274,35 @@ def rmsnorm_bwd_workspace(R, C):
     return int(hip_lib().pk_rmsnorm_bwd_workspace(R, C))
 
 
-def rmsnorm_bwd(x, g, rstd, dy, dx, dg, ws=None, accum_dx=False, accum_dg=False, dx_in=None):
+RMS_KEEP_PARTIALS = 8
+
+
+def rmsnorm_bwd(x, g, rstd, dy, dx, dg, ws=None, accum_dx=False, accum_dg=False, dx_in=None,
+                keep_partials=False):
     """dx_in: the accumulated term of dx read from another buffer
-    (pk_rmsnorm_bwd_into_f32; accum_dx is then ignored)"""
+    (pk_rmsnorm_bwd_into_f32; accum_dx is then ignored).  keep_partials (with
+    dg None): leave dg's partial sums in ws for rmsnorm_dg_reduce."""
     R, C = x.shape
     need = rmsnorm_bwd_workspace(R, C)
-    if ws is None and dg is not None:
+    if ws is None and (dg is not None or keep_partials):
         ws = torch.empty(max(1, need // 4), device=x.device, dtype=torch.float32)
     wsb = 0 if ws is None else ws.numel() * 4
-    if dx_in is not None:
+    if dx_in is not None or keep_partials:
+        flags = (ACCUM2 if accum_dg else 0) | (RMS_KEEP_PARTIALS if keep_partials else 0)
+        src = dx_in if dx_in is not None else (dx if accum_dx else None)
         check("pk_rmsnorm_bwd_into_f32", hip_lib().pk_rmsnorm_bwd_into_f32(
-            R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx_in), _ptr(dx), _ptr(dg),
-            ACCUM2 if accum_dg else 0, _ptr(ws), wsb, _stream()))
-        return
+            R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(src), _ptr(dx), _ptr(dg),
+            flags, _ptr(ws), wsb, _stream()))
+        return ws
     flags = (ACCUM if accum_dx else 0) | (ACCUM2 if accum_dg else 0)
     check("pk_rmsnorm_bwd_f32", hip_lib().pk_rmsnorm_bwd_f32(
         R, C, _ptr(x), _ptr(g), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dg), flags, _ptr(ws), wsb,
         _stream()))
+
+
+def rmsnorm_dg_reduce(R, C, ws, dg, accum=False):
+    check("pk_rmsnorm_dg_reduce_f32", hip_lib().pk_rmsnorm_dg_reduce_f32(
+        R, C, _ptr(ws), ws.numel() * 4, _ptr(dg), ACCUM if accum else 0, _stream()))
 
 
 def swiglu_fwd(a, u, h):

@@ -354,6 +354,13 @@ def test_rmsnorm_vs_oracle(dev, R, C):
     K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx2, dg2, accum_dg=True, dx_in=src)
     assert np.array_equal(host(dx2), host(dx)) and np.array_equal(host(dg2), host(dg))
     assert np.array_equal(host(src), dx0)
+    # dg's reduction as a second call (the partial sums kept in the workspace)
+    dx3, dg3 = torch.full((R, C), float("nan"), device=dev), cu(dg0.copy())
+    ws = K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx3, None, dx_in=src,
+                       keep_partials=True)
+    assert np.array_equal(host(dg3), dg0)  # not touched yet
+    K.rmsnorm_dg_reduce(R, C, ws, dg3, accum=True)
+    assert np.array_equal(host(dx3), host(dx)) and np.array_equal(host(dg3), host(dg))
     dx, dg = torch.empty(R, C, device=dev), torch.empty(C, device=dev)  # overwrite mode
     K.rmsnorm_bwd(cu(x), cu(g), cu(rstd_ref), cu(dy), dx, dg)
     dx_ref, dg_ref = O.rmsnorm_bwd(x, g, rstd_ref, dy)
