@@ -298,23 +298,27 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
 // For each 64-query block the workspace holds 64 values of L2 = lse*log2(e)
 // followed by 64 values of D = rowsum(dO*O): [B*H][T/64][2][64].  One 512-byte
 // load per block brings both into LDS.
+// Sixteen lanes per query row, one float4 of dO and O each, so a wave reads
+// four rows as four contiguous 256-byte runs.
 __global__ void flash_dsum(FlashParams p) {
     const int64_t BH = p.B * p.H, n = BH * p.T;
-    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-        i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = threadIdx.x & 15;
+    for(int64_t i = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 4; i < n;
+        i += ((int64_t)gridDim.x * blockDim.x) >> 4) {
         const int64_t bh = i / p.T, t = i % p.T, b = bh / p.H, h = bh % p.H;
         const int64_t off = (b * p.T + t) * p.D + h * HD;
-        const f32x4* x = reinterpret_cast<const f32x4*>(p.dout + off);
-        const f32x4* y = reinterpret_cast<const f32x4*>(p.o + off);
-        float s = 0.0f;
-#pragma unroll
-        for(int c = 0; c < HD / 4; ++c) {
-            const f32x4 a = x[c], o = y[c];
-            s += a[0] * o[0] + a[1] * o[1] + a[2] * o[2] + a[3] * o[3];
+        const f32x4 a = reinterpret_cast<const f32x4*>(p.dout + off)[c];
+        const f32x4 o = reinterpret_cast<const f32x4*>(p.o + off)[c];
+        float s = a[0] * o[0] + a[1] * o[1] + a[2] * o[2] + a[3] * o[3];
+        s += __shfl_xor(s, 8, 16);
+        s += __shfl_xor(s, 4, 16);
+        s += __shfl_xor(s, 2, 16);
+        s += __shfl_xor(s, 1, 16);
+        if(c == 0) {
+            float* blk = p.dsum_out + bh * 2 * p.T + (t / BLK) * 2 * BLK + t % BLK;
+            blk[0] = p.lse[i] * kLog2e;
+            blk[BLK] = s;
         }
-        float* blk = p.dsum_out + bh * 2 * p.T + (t / BLK) * 2 * BLK + t % BLK;
-        blk[0] = p.lse[i] * kLog2e;
-        blk[BLK] = s;
     }
 }
 
@@ -934,7 +938,7 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.scale = scale;
     p.flags = flags;
     hipStream_t st = pk::as_stream(stream);
-    flash_dsum<<<pk::grid_for(B * H * T, 256), 256, 0, st>>>(p);
+    flash_dsum<<<pk::grid_for(B * H * T * 16, 256), 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
     const unsigned grid = (unsigned)(B * H * (T / ROWS));
     if(bf16)
