@@ -35,6 +35,7 @@ constexpr int LDT = HD + 4;   // padded LDS row stride (floats)
 constexpr int TILE = BLK * LDT;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr int64_t kCUs = 256;  // MI355X
 
 struct FlashParams {
     const float *q, *k, *v, *o, *dout, *lse, *dsum;
@@ -457,7 +458,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
     const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
-    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    // heaviest query blocks first, in passes of one workgroup per CU: odd passes
+    // run in reverse, so a CU's resident workgroups mix heavy and light blocks
+    const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
+    const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
+    const int64_t rank = (pass & 1) ? lo + hi - 1 - blockIdx.x : blockIdx.x;
+    const int64_t qb = nqb - 1 - rank / BH, bh = rank % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
