@@ -350,7 +350,9 @@ int pkh_grad_alias(struct PicoTensor* t, const struct PicoTensor* src) {
 void pkh_grad_unalias(struct PkNode* n, int copy) {
     if(!n->own_grad) return;
     float* own = n->own_grad;
-    if(copy && pkh_copy_d2d_async(own, n->t.grad, sizeof(float) * (size_t)n->t.numel)) return;
+    /* a failed copy is reported (the error is recorded); the tensor gets its
+     * own buffer back either way, so no later write reaches the shared grad */
+    if(copy) pkh_copy_d2d_async(own, n->t.grad, sizeof(float) * (size_t)n->t.numel);
     n->t.grad = own;
     n->own_grad = NULL;
 }
