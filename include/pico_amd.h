@@ -150,8 +150,8 @@ void pico_mul_backward_gpu(struct PicoTensor* self);
 void pico_matmul_backward_gpu(struct PicoTensor* self);
 void pico_relu_backward_gpu(struct PicoTensor* self);
 
-/* ---- hot-path ops the reference lacks (no reference
- * code: the softmax Jacobian comment at src/autograd.h:38-40 and the plan at
+/* ---- hot-path ops the reference lacks (softmax-CE, RMSNorm, SwiGLU, causal
+ * attention, embedding, AdamW, argmax; no reference code: the softmax Jacobian comment at src/autograd.h:38-40 and the plan at
  * todo.md:95 are the only traces).  Same op template as src/ops.c:12-54.
  * `labels` / `ids` are int32 arrays in host or device memory; host arrays are
  * staged into the current arena's device memory. ---- */
