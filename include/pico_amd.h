@@ -151,8 +151,9 @@ void pico_matmul_backward_gpu(struct PicoTensor* self);
 void pico_relu_backward_gpu(struct PicoTensor* self);
 
 /* ---- hot-path ops the reference lacks (softmax-CE, RMSNorm, SwiGLU, causal
- * attention, embedding, AdamW, argmax; no reference code: the softmax Jacobian comment at src/autograd.h:38-40 and the plan at
- * todo.md:95 are the only traces).  Same op template as src/ops.c:12-54.
+ * attention, embedding, AdamW, argmax).  No reference code: the softmax
+ * Jacobian comment at src/autograd.h:38-40 and the plan at todo.md:95 are the
+ * only traces.  Same op template as src/ops.c:12-54.
  * `labels` / `ids` are int32 arrays in host or device memory; host arrays are
  * staged into the current arena's device memory. ---- */
 /* loss [1] = mean_r (logsumexp(z_r) - z_r[labels[r]]) over logits [R, V] */
