@@ -313,23 +313,26 @@ __global__ void adamw_prep_kernel(int32_t* step, float lr, float b1, float b2, f
     coef[1] = (float)sqrt(bc2);
 }
 
-// one workgroup per chunk (<= PK_ADAMW_CHUNK elements of one tensor)
+// kAdamwSplit workgroups per chunk (<= PK_ADAMW_CHUNK elements of one tensor),
+// interleaved by float4: four times the workgroups of one per chunk, so more
+// loads are in flight and the last round is short
+constexpr int kAdamwSplit = 4;
 __global__ __launch_bounds__(256) void adamw_multi_kernel(const PkAdamwChunk* __restrict__ chunks,
                                                           float b1, float b2, float eps,
                                                           float decay,
                                                           const float* __restrict__ coef) {
-    const PkAdamwChunk c = chunks[blockIdx.x];
+    const PkAdamwChunk c = chunks[blockIdx.x / kAdamwSplit];
     const float step_size = coef[0], bc2_sqrt = coef[1];
     const uintptr_t align = reinterpret_cast<uintptr_t>(c.p) | reinterpret_cast<uintptr_t>(c.g) |
                             reinterpret_cast<uintptr_t>(c.m) | reinterpret_cast<uintptr_t>(c.v);
     const int64_t n4 = (align & 15) ? 0 : c.n / 4;
-    f32x4* p4 = reinterpret_cast<f32x4*>(c.p);
-    f32x4* m4 = reinterpret_cast<f32x4*>(c.m);
-    f32x4* v4 = reinterpret_cast<f32x4*>(c.v);
-    const f32x4* g4 = reinterpret_cast<const f32x4*>(c.g);
-    for(int64_t i = threadIdx.x; i < n4; i += blockDim.x) {
-        f32x4 p = p4[i], m = m4[i], v = v4[i];
-        const f32x4 g = c.g ? g4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    // four distinct tensors, each element read and written once: streaming
+    // (nontemporal) accesses, two float4 of each per lane in flight
+    f32x4* __restrict__ p4 = reinterpret_cast<f32x4*>(c.p);
+    f32x4* __restrict__ m4 = reinterpret_cast<f32x4*>(c.m);
+    f32x4* __restrict__ v4 = reinterpret_cast<f32x4*>(c.v);
+    const f32x4* __restrict__ g4 = reinterpret_cast<const f32x4*>(c.g);
+    auto update = [&](f32x4& p, const f32x4& g, f32x4& m, f32x4& v) {
 #pragma unroll
         for(int e = 0; e < 4; ++e) {
             float pe = p[e], me = m[e], ve = v[e];
@@ -338,10 +341,34 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(const PkAdamwChunk* __
             m[e] = me;
             v[e] = ve;
         }
-        p4[i] = p;
-        m4[i] = m;
-        v4[i] = v;
+    };
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const int64_t stride = (int64_t)blockDim.x * kAdamwSplit;
+    int64_t i = threadIdx.x + (int64_t)(blockIdx.x % kAdamwSplit) * blockDim.x;
+    for(; i + stride < n4; i += 2 * stride) {
+        const int64_t j = i + stride;
+        f32x4 pa = pk::ld_stream(p4 + i), ma = pk::ld_stream(m4 + i), va = pk::ld_stream(v4 + i);
+        f32x4 pb = pk::ld_stream(p4 + j), mb = pk::ld_stream(m4 + j), vb = pk::ld_stream(v4 + j);
+        const f32x4 ga = c.g ? pk::ld_stream(g4 + i) : zero;
+        const f32x4 gb = c.g ? pk::ld_stream(g4 + j) : zero;
+        update(pa, ga, ma, va);
+        update(pb, gb, mb, vb);
+        pk::st_stream(p4 + i, pa);
+        pk::st_stream(m4 + i, ma);
+        pk::st_stream(v4 + i, va);
+        pk::st_stream(p4 + j, pb);
+        pk::st_stream(m4 + j, mb);
+        pk::st_stream(v4 + j, vb);
     }
+    for(; i < n4; i += stride) {
+        f32x4 p = pk::ld_stream(p4 + i), m = pk::ld_stream(m4 + i), v = pk::ld_stream(v4 + i);
+        const f32x4 g = c.g ? pk::ld_stream(g4 + i) : zero;
+        update(p, g, m, v);
+        pk::st_stream(p4 + i, p);
+        pk::st_stream(m4 + i, m);
+        pk::st_stream(v4 + i, v);
+    }
+    if(blockIdx.x % kAdamwSplit) return;  // the scalar tail: the chunk's first workgroup
     for(int64_t i = n4 * 4 + threadIdx.x; i < c.n; i += blockDim.x) {
         const float gi = c.g ? c.g[i] : 0.0f;
         adamw_elem(c.p[i], gi, c.m[i], c.v[i], b1, b2, eps, decay, step_size, bc2_sqrt);
@@ -751,8 +778,9 @@ extern "C" int pk_adamw_multi_f32(int64_t nchunks, const PkAdamwChunk* chunks, f
     if(!chunks || !coef) return pk::fail("pk_adamw_multi_f32: NULL pointer");
     if(nchunks > 0x7fffffff) return pk::fail("pk_adamw_multi_f32: too many chunks");
     const float decay = 1.0f - lr * weight_decay;
-    adamw_multi_kernel<<<(unsigned)nchunks, 256, 0, pk::as_stream(stream)>>>(chunks, beta1, beta2,
-                                                                           eps, decay, coef);
+    if(nchunks > 0x7fffffff / kAdamwSplit) return pk::fail("pk_adamw_multi_f32: too many chunks");
+    adamw_multi_kernel<<<(unsigned)(nchunks * kAdamwSplit), 256, 0, pk::as_stream(stream)>>>(
+        chunks, beta1, beta2, eps, decay, coef);
     return pk::launch_status("pk_adamw_multi_f32");
 }
 
