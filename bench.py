@@ -318,7 +318,8 @@ def mlp_section(steps, warmup):
 
 def train_section(name, steps, warmup, precision=0):
     """one AdamW training step of the transformer per step, inputs resident;
-    precision 1 runs pico_matmul's products in bf16 (pico_set_matmul_precision)"""
+    precision 1 runs pico_matmul's products in bf16, 2 as three bf16 products per fp32
+    one (pico_set_matmul_precision)"""
     import numpy as np
 
     from pico_amd.pico import Pico
@@ -380,10 +381,14 @@ def train_section(name, steps, warmup, precision=0):
         raise RuntimeError(err)
     flop = train_flop_per_step(cfg)
     ms = wall * 1e3 / steps
+    # bf16x3: three bf16 matrix instructions per fp32 product
+    peak, peak_name = {1: (MFMA_BF16_PEAK, "bf16 2.5 PFLOP/s"),
+                       2: (MFMA_BF16_PEAK / 3, "bf16x3: 2.5 PFLOP/s / 3")}.get(
+        precision, (MFMA_FP32_PEAK, "fp32 157.3 TFLOP/s"))
     return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
             "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
-            "mfu": round(flop / (ms * 1e-3) / (MFMA_BF16_PEAK if precision else MFMA_FP32_PEAK), 4),
-            "mfu_peak": "bf16 2.5 PFLOP/s" if precision else "fp32 157.3 TFLOP/s",
+            "mfu": round(flop / (ms * 1e-3) / peak, 4),
+            "mfu_peak": peak_name,
             "graph_ms_per_step": round(graph_ms, 3),
             "graph_tokens_per_s": round(n / (graph_ms * 1e-3), 1),
             "tokens_per_step": n, "steps": steps, "warmup": warmup,
@@ -506,6 +511,15 @@ def main():
             "peak_tflops": MFMA_BF16_PEAK / 1e12,
             "note": "bf16 products of fp32 operands (rounded to nearest even), fp32 "
                     "accumulation; not the headline, which is fp32"}
+        # three bf16 products per fp32 one (hi/lo operand split): within ~1e-5 of
+        # fp32; TFLOP/s counted as fp32 products (2n^3), not bf16 instructions
+        line["bf16x3"] = {
+            "sweep": sweep_section(torch, K, [2048, 4096, 8192], K.gemm_bf16x3),
+            "train": {name: train_section(name, args.train_steps, 3, precision=2)
+                      for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
+            "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
+                    "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "
+                    "fp32; not the headline, which is fp32"}
     if "rows" in sections:
         line["row_kernels"] = rows_section(torch, K)
     if "cpu" in sections:

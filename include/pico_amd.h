@@ -266,10 +266,14 @@ void pico_gpu_clear_error(void);
  * multiplied on the bf16 matrix cores, accumulating in fp32; tensors, the
  * softmax statistics and every other op stay fp32.  Faster, and outside the
  * fp32 parity contract (relative error of order 2^-8 per operand).  An
- * attention node's backward uses the precision its forward ran in.  Returns
- * 0, or nonzero for an unknown value. */
+ * attention node's backward uses the precision its forward ran in.
+ * PICO_MATMUL_BF16X3: pico_matmul's products and their gradients take three
+ * bf16 products per fp32 one (pk_gemm_bf16x3_f32): within about 1e-5 of
+ * fp32, inside the 1e-4 parity bound; attention stays fp32.  Returns 0, or
+ * nonzero for an unknown value. */
 #define PICO_MATMUL_FP32 0
 #define PICO_MATMUL_BF16 1
+#define PICO_MATMUL_BF16X3 2
 int pico_set_matmul_precision(int precision);
 int pico_get_matmul_precision(void);
 

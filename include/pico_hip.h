@@ -80,6 +80,20 @@ int pk_gemm_ex_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float
                         const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                         float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
                         pk_stream_t stream);
+/* fp32 products from three bf16 ones (no reference counterpart): each operand
+ * x is split as hi = bf16(x), lo = bf16(x - hi) on its way to LDS, and
+ * a.b is taken as ahi.bhi + ahi.blo + alo.bhi on the bf16 matrix cores,
+ * accumulating in fp32.  hi + lo is x to 2^-17, and the dropped alo.blo is
+ * below 2^-16 of a.b, so the result is within about 1e-5 (norm-wise) of the
+ * fp32 product, against 2^-8 for pk_gemm_bf16_f32.  C and the workspace
+ * contract are as in pk_gemm_f32 / pk_gemm_ex_f32. */
+int pk_gemm_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                       const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                       float* C, int64_t ldc, pk_stream_t stream);
+int pk_gemm_ex_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                          const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                          float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                          pk_stream_t stream);
 
 /* Batched form: batch index z = outer*inner_count + inner; operand X of batch z
  * starts at X + outer*sX_outer + inner*sX_inner.  'causal' restricts work for

@@ -41,6 +41,10 @@ PK_SIGNATURES = {
                          c_p, c_i64, c_p],
     "pk_gemm_ex_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
                             c_f, c_p, c_i64, c_p, c_size, c_p],
+    "pk_gemm_bf16x3_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
+                         c_p, c_i64, c_p],
+    "pk_gemm_ex_bf16x3_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
+                            c_f, c_p, c_i64, c_p, c_size, c_p],
     "pk_gemm_batched_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_i64, c_i64,
                             c_p, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_i64, c_i64, c_i64,
                             c_i64, c_int, c_p],

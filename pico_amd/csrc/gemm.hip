@@ -46,6 +46,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "pk_common.h"
 
 namespace {
@@ -196,7 +198,40 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// store 4 consecutive k of one row; a bf16 tile gets them rounded to nearest even
+// An element of a split-bf16 tile: x is stored as hi = bf16(x) and
+// lo = bf16(x - hi), in two tiles LO elements apart (x - hi is exact in fp32,
+// so hi + lo is x to 2^-17 relative).
+template <int LO>
+struct SplitBf16 {
+    __bf16 hi;
+};
+
+template <int LO>
+__device__ __forceinline__ void put_split(__bf16* t, int off, const float* w, int n) {
+#pragma unroll
+    for(int e = 0; e < 4; ++e) {
+        if(e >= n) break;
+        const __bf16 h = (__bf16)w[e];
+        t[off + e] = h;
+        t[off + LO + e] = (__bf16)(w[e] - (float)h);
+    }
+}
+
+// store 4 consecutive k of one row; a bf16 tile gets them rounded to nearest
+// even, a split tile their hi and lo parts
+template <int LO>
+__device__ __forceinline__ void put4(SplitBf16<LO>* lds, int off, f32x4 w) {
+    __bf16* t = reinterpret_cast<__bf16*>(lds);
+    bf16x4 h, l;
+#pragma unroll
+    for(int e = 0; e < 4; ++e) {
+        h[e] = (__bf16)w[e];
+        l[e] = (__bf16)(w[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x4*>(t + off) = h;
+    *reinterpret_cast<bf16x4*>(t + off + LO) = l;
+}
+
 template <class E>
 __device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
     if constexpr(sizeof(E) == 4) {
@@ -206,6 +241,17 @@ __device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
         *reinterpret_cast<bf16x4*>(lds + off) = b;
     }
 }
+
+template <class E>
+struct is_split {
+    static constexpr bool value = false;
+    static constexpr int LO = 0;
+};
+template <int L>
+struct is_split<SplitBf16<L>> {
+    static constexpr bool value = true;
+    static constexpr int LO = L;
+};
 
 template <bool KFAST, int R, class E>
 __device__ __forceinline__ void store_item(E* lds, int item, const f32x4* v) {
@@ -224,6 +270,9 @@ __device__ __forceinline__ void store_item(E* lds, int item, const f32x4* v) {
             if constexpr(sizeof(E) == 4) {
                 typedef float f32x2 __attribute__((ext_vector_type(2)));
                 *reinterpret_cast<f32x2*>(lds + (rr + j) * LS + kk) = f32x2{v[0][j], v[1][j]};
+            } else if constexpr(is_split<E>::value) {
+                const float w2[2] = {v[0][j], v[1][j]};
+                put_split<is_split<E>::LO>(reinterpret_cast<__bf16*>(lds), (rr + j) * LS + kk, w2, 2);
             } else {
                 *reinterpret_cast<bf16x2*>(lds + (rr + j) * LS + kk) =
                     bf16x2{(__bf16)v[0][j], (__bf16)v[1][j]};
@@ -300,8 +349,8 @@ struct Staging {
     static constexpr int group_ops(int g) { return ops_before(lo(g + 1)) - ops_before(lo(g)); }
 };
 
-template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB, class E>
-__device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], E* sa, E* sb,
+template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB, class EA, class EB>
+__device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], EA* sa, EB* sb,
                                       const float* __restrict__ A, const float* __restrict__ B,
                                       const GemmParams& p, int64_t row0, int64_t col0, int64_t kn,
                                       int64_t kend) {
@@ -404,9 +453,9 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j
 
 // prologue shared by both kernels: slice 0 into LDS buffer 0, slice 1 into
 // the staging registers
-template <bool AK, bool BKF, int EDGE, class T, int NA, int NB, class E>
+template <bool AK, bool BKF, int EDGE, class T, int NA, int NB, class EA, class EB>
 __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, f32x4 (&ra)[NA],
-                                         f32x4 (&rb)[NB], E* sa, E* sb) {
+                                         f32x4 (&rb)[NB], EA* sa, EB* sb) {
     using OA = Operand<AK, T::BM>;
     using OB = Operand<BKF, T::BN>;
 #pragma unroll
@@ -541,15 +590,19 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 }
 
-template <bool TA, bool TB, int EDGE, class T>
+template <bool TA, bool TB, int EDGE, class T, bool SPLIT>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
     constexpr bool AK = !TA, BKF = TB;
     using OA = Operand<AK, BM>;
     using OB = Operand<BKF, BN>;
     using S = Staging<AK, BKF, T>;
-    __shared__ __attribute__((aligned(16))) __bf16 ldsA[2][BM * KFB];
-    __shared__ __attribute__((aligned(16))) __bf16 ldsB[2][BN * KFB];
+    // SPLIT: each operand tile is followed by its lo tile (split-bf16)
+    constexpr int LA = BM * KFB, LB = BN * KFB, NS = SPLIT ? 2 : 1;
+    using EA = typename std::conditional<SPLIT, SplitBf16<LA>, __bf16>::type;
+    using EB = typename std::conditional<SPLIT, SplitBf16<LB>, __bf16>::type;
+    __shared__ __attribute__((aligned(16))) __bf16 ldsA[2][NS * LA];
+    __shared__ __attribute__((aligned(16))) __bf16 ldsB[2][NS * LB];
 
     const TileJob job = tile_job<T>(p);
     if(job.skip) return;
@@ -567,39 +620,58 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
             for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    constexpr int RD = TM + TN;
-    constexpr int NMFMA = TM * TN;
+    constexpr int RD = NS * (TM + TN);
+    constexpr int NMFMA = (SPLIT ? 3 : 1) * TM * TN;
     constexpr int STAGE_OPS = S::group_ops(0) + S::group_ops(1) + S::group_ops(2);
 
     if(nslices > 0) {
         f32x4 ra[OA::F4], rb[OB::F4];
-        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, ldsA[0], ldsB[0]);
+        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, reinterpret_cast<EA*>(ldsA[0]),
+                                   reinterpret_cast<EB*>(ldsB[0]));
         __syncthreads();
+        // fragments of step 0 / step 1 (and their lo parts when SPLIT)
         bf16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-        read_step<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
-        read_step<TN>(ldsB[0], br0, lr, lh, 0, fb0);
+        bf16x8 la0[SPLIT ? TM : 1], lb0[SPLIT ? TN : 1], la1[SPLIT ? TM : 1], lb1[SPLIT ? TN : 1];
+        auto read = [&](const __bf16* ta, const __bf16* tb, int t, bf16x8 (&fa)[TM],
+                        bf16x8 (&fb)[TN], bf16x8 (&la)[SPLIT ? TM : 1],
+                        bf16x8 (&lb)[SPLIT ? TN : 1]) {
+            read_step<TM>(ta, ar0, lr, lh, t, fa);
+            read_step<TN>(tb, br0, lr, lh, t, fb);
+            if constexpr(SPLIT) {
+                read_step<TM>(ta + LA, ar0, lr, lh, t, la);
+                read_step<TN>(tb + LB, br0, lr, lh, t, lb);
+            }
+        };
+        // a.b ~ ahi.bhi + ahi.blo + alo.bhi (alo.blo is below 2^-16 of a.b)
+        auto mma = [&](const bf16x8 (&fa)[TM], const bf16x8 (&fb)[TN],
+                       const bf16x8 (&la)[SPLIT ? TM : 1], const bf16x8 (&lb)[SPLIT ? TN : 1]) {
+            mfma_step<TM, TN>(acc, fa, fb);
+            if constexpr(SPLIT) {
+                mfma_step<TM, TN>(acc, fa, lb);
+                mfma_step<TM, TN>(acc, la, fb);
+            }
+        };
+        read(ldsA[0], ldsB[0], 0, fa0, fb0, la0, lb0);
         for(int s = 0; s < nslices; ++s) {
             const int cur = s & 1;
             __bf16* sa = ldsA[cur ^ 1];
             __bf16* sb = ldsB[cur ^ 1];
             const int64_t kn = job.kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
             // step 0: read step 1, stage slice s+1 and fetch s+2
-            read_step<TM>(ldsA[cur], ar0, lr, lh, 1, fa1);
-            read_step<TN>(ldsB[cur], br0, lr, lh, 1, fb1);
-            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
-                                       job.kend);
-            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
-                                       job.kend);
-            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
-                                       job.kend);
-            mfma_step<TM, TN>(acc, fa0, fb0);
+            read(ldsA[cur], ldsB[cur], 1, fa1, fb1, la1, lb1);
+            stage<AK, BKF, EDGE, T, 0>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+                                       job.A, job.B, p, job.row0, job.col0, kn, job.kend);
+            stage<AK, BKF, EDGE, T, 1>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+                                       job.A, job.B, p, job.row0, job.col0, kn, job.kend);
+            stage<AK, BKF, EDGE, T, 2>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+                                       job.A, job.B, p, job.row0, job.col0, kn, job.kend);
+            mma(fa0, fb0, la0, lb0);
             interleave<NMFMA, RD + STAGE_OPS>();
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
             // step 1, with step 0 of slice s+1 read underneath
-            read_step<TM>(sa, ar0, lr, lh, 0, fa0);
-            read_step<TN>(sb, br0, lr, lh, 0, fb0);
-            mfma_step<TM, TN>(acc, fa1, fb1);
+            read(sa, sb, 0, fa0, fb0, la0, lb0);
+            mma(fa1, fb1, la1, lb1);
             interleave<NMFMA, RD>();
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -727,12 +799,14 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
     return best;
 }
 
-enum Precision { kFp32 = 0, kBf16 = 1 };
+enum Precision { kFp32 = 0, kBf16 = 1, kBf16x3 = 2 };
 
 template <bool TA, bool TB, class T, int EDGE>
 void launch_kernel(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
     if(prec == kBf16)
-        gemm_bf16_kernel<TA, TB, EDGE, T><<<grid, NT, 0, st>>>(gp);
+        gemm_bf16_kernel<TA, TB, EDGE, T, false><<<grid, NT, 0, st>>>(gp);
+    else if(prec == kBf16x3)
+        gemm_bf16_kernel<TA, TB, EDGE, T, true><<<grid, NT, 0, st>>>(gp);
     else
         gemm_f32_kernel<TA, TB, EDGE, T><<<grid, NT, 0, st>>>(gp);
 }
@@ -746,7 +820,9 @@ int launch_tile(const GemmParams& gp, int64_t batch, int edge, int prec, hipStre
         launch_kernel<TA, TB, T, kEdgeVec>(gp, grid, prec, st);
     else
         launch_kernel<TA, TB, T, kEdgeScalar>(gp, grid, prec, st);
-    return pk::launch_status(prec == kBf16 ? "pk_gemm_bf16_f32" : "pk_gemm_f32");
+    return pk::launch_status(prec == kBf16     ? "pk_gemm_bf16_f32"
+                             : prec == kBf16x3 ? "pk_gemm_bf16x3_f32"
+                                               : "pk_gemm_f32");
 }
 
 template <bool TA, bool TB>
@@ -902,4 +978,19 @@ extern "C" int pk_gemm_ex_bf16_f32(char ta, char tb, int64_t M, int64_t N, int64
                                    void* workspace, size_t workspace_bytes, pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
                      0, static_cast<float*>(workspace), workspace_bytes, kBf16, stream);
+}
+
+extern "C" int pk_gemm_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                  const float* A, int64_t lda, const float* B, int64_t ldb,
+                                  float beta, float* C, int64_t ldc, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, nullptr, 0, kBf16x3, stream);
+}
+
+extern "C" int pk_gemm_ex_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int64_t K,
+                                     float alpha, const float* A, int64_t lda, const float* B,
+                                     int64_t ldb, float beta, float* C, int64_t ldc,
+                                     void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, static_cast<float*>(workspace), workspace_bytes, kBf16x3, stream);
 }

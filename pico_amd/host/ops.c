@@ -166,7 +166,8 @@ static inline char flip(char t) { return t == 'N' ? 'T' : 'N'; }
 static int g_matmul_precision = PICO_MATMUL_FP32;
 
 int pico_set_matmul_precision(int precision) {
-    if(precision != PICO_MATMUL_FP32 && precision != PICO_MATMUL_BF16) {
+    if(precision != PICO_MATMUL_FP32 && precision != PICO_MATMUL_BF16 &&
+       precision != PICO_MATMUL_BF16X3) {
         PKH_ERR("pico_set_matmul_precision: unknown precision %d!\n", precision);
         return PK_EINVAL;
     }
@@ -187,7 +188,9 @@ static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t
     if(!ws) ws_bytes = 0;
     int (*gemm)(char, char, int64_t, int64_t, int64_t, float, const float*, int64_t,
                 const float*, int64_t, float, float*, int64_t, void*, size_t, pk_stream_t) =
-        g_matmul_precision == PICO_MATMUL_BF16 ? pk_gemm_ex_bf16_f32 : pk_gemm_ex_f32;
+        g_matmul_precision == PICO_MATMUL_BF16     ? pk_gemm_ex_bf16_f32
+        : g_matmul_precision == PICO_MATMUL_BF16X3 ? pk_gemm_ex_bf16x3_f32
+                                                   : pk_gemm_ex_f32;
     if(tc == 'N')
         return gemm(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws, ws_bytes,
                     st);

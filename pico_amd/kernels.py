@@ -58,9 +58,15 @@ def gemm(ta, tb, A, B, C, alpha=1.0, beta=0.0):
     return C
 
 
-def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
+def gemm_bf16x3(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
+    """gemm as three bf16 products per fp32 one (pk_gemm_bf16x3_f32)"""
+    return gemm_bf16(ta, tb, A, B, C, alpha, beta, ws, split=True)
+
+
+def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False):
     """gemm with bf16 multiplies and fp32 accumulation (fp32 tensors in and out);
-    ws: optional workspace for a K split (as gemm_ex)"""
+    ws: optional workspace for a K split (as gemm_ex); split: hi/lo operands,
+    three products (pk_gemm_bf16x3_f32)"""
     _f32(A, B, C)
     lda, ldb, ldc = _rowmajor(A, "A"), _rowmajor(B, "B"), _rowmajor(C, "C")
     M = A.shape[1] if ta == "T" else A.shape[0]
@@ -69,12 +75,14 @@ def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
     N = B.shape[0] if tb == "T" else B.shape[1]
     if K != Kb or tuple(C.shape) != (M, N):
         raise ValueError(f"gemm shape mismatch: op(A) {M}x{K}, op(B) {Kb}x{N}, C {tuple(C.shape)}")
+    name = "pk_gemm_bf16x3_f32" if split else "pk_gemm_bf16_f32"
     if ws is None:
-        check("pk_gemm_bf16_f32", hip_lib().pk_gemm_bf16_f32(
+        check(name, getattr(hip_lib(), name)(
             ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C),
             ldc, _stream()))
     else:
-        check("pk_gemm_ex_bf16_f32", hip_lib().pk_gemm_ex_bf16_f32(
+        name = name.replace("pk_gemm_", "pk_gemm_ex_")
+        check(name, getattr(hip_lib(), name)(
             ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C),
             ldc, _ptr(ws), ws.numel() * ws.element_size(), _stream()))
     return C
