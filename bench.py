@@ -131,6 +131,29 @@ def sweep_section(torch, K, sizes, gemm=None):
     return out
 
 
+def attn_section(torch, K):
+    """the fused causal attention at config 5's shapes (B 8, H 12, T 1024, hd 64),
+    fp32 and bf16 products, randn inputs; TFLOP/s by the causal count (4*hd FLOP
+    per visible (query, key) pair forward, 10*hd backward)"""
+    dev = torch.device("cuda:0")
+    B, H, T, hd = 8, 12, 1024, 64
+    D = H * hd
+    gen = torch.Generator(device=dev).manual_seed(1)
+    q, k, v, do = (torch.randn(B * T, D, device=dev, generator=gen) for _ in range(4))
+    o, lse = torch.empty_like(q), torch.empty(B * H * T, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    pairs = B * H * T * (T + 1) / 2
+    out = {"config": {"batch": B, "heads": H, "seq_len": T, "head_dim": hd}}
+    for name, bf in (("fp32", False), ("bf16", True)):
+        fwd, _ = _events_time(lambda: K.flash_fwd(B, H, q, k, v, o, lse, bf16=bf), 20, 3)
+        bwd, _ = _events_time(lambda: K.flash_bwd(B, H, q, k, v, o, lse, do, dq, dk, dv, bf16=bf),
+                              20, 3)
+        out[name] = {"fwd_us": round(fwd * 1e3, 1), "bwd_us": round(bwd * 1e3, 1),
+                     "fwd_tflops": round(4 * hd * pairs / (fwd * 1e-3) / 1e12, 1),
+                     "bwd_tflops": round(10 * hd * pairs / (bwd * 1e-3) / 1e12, 1)}
+    return out
+
+
 def rows_section(torch, K):
     """config-3 row kernels; 4 rotating buffer sets (> 256 MB MALL)"""
     dev = torch.device("cuda:0")
@@ -441,7 +464,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4096)
-    ap.add_argument("--sections", default="train,sweep,bf16,rows,cpu")
+    ap.add_argument("--sections", default="train,sweep,bf16,attn,rows,cpu")
     ap.add_argument("--train-steps", type=int, default=10)
     ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
     args = ap.parse_args()
@@ -520,6 +543,8 @@ def main():
             "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
                     "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "
                     "fp32; not the headline, which is fp32"}
+    if "attn" in sections:
+        line["attention"] = attn_section(torch, K)
     if "rows" in sections:
         line["row_kernels"] = rows_section(torch, K)
     if "cpu" in sections:
