@@ -222,14 +222,18 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
         // key kv0 + sub*32 + acc_row(r, lh) is hidden from query qi when it
         // exceeds qi; lim folds the lane's offsets into one compare per element
         const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;
+        if((int64_t)j * BLK + BLK - 1 > q0) {  // the block crosses this wave's diagonal
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for(int r = 0; r < 16; ++r)
+                    if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
         for(int sub = 0; sub < 2; ++sub)
 #pragma unroll
-            for(int r = 0; r < 16; ++r) {
-                if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
-                mx = fmaxf(mx, s[sub][r]);
-            }
+            for(int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sub][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query
         const float alpha = __builtin_amdgcn_exp2f(m - mn);
@@ -399,6 +403,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
         if(qs + BLK - 1 >= k0) {  // some query of this block sees this wave's keys
             // query qs + sub*32 + acc_row(r, lh) sees key ki when it is >= ki
             const int lim = (int)(ki - qs) - 4 * lh;
+            const bool diag = qs < k0 + 32;  // some query of the block precedes a key
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
                 f32x16 sc = dot_rows(tq, sub, lq, lh, kf, zero16());
@@ -410,15 +415,26 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 }
+                // read and exponentiate unconditionally, then select: the
+                // masked lanes' values are discarded.  Only a block that
+                // crosses this wave's diagonal has masked lanes.
+                if(diag) {
 #pragma unroll
-                for(int r = 0; r < 16; ++r) {
-                    const int qr = sub * 32 + acc_row(r, lh);
-                    // read and exponentiate unconditionally, then select: the
-                    // masked lanes' values are discarded
-                    const float e = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim ? e : 0.0f;
-                    sc[r] = pr;
-                    dp[r] = pr * (dp[r] - tl[BLK + qr]);
+                    for(int r = 0; r < 16; ++r) {
+                        const int qr = sub * 32 + acc_row(r, lh);
+                        const float e = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
+                        const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim ? e : 0.0f;
+                        sc[r] = pr;
+                        dp[r] = pr * (dp[r] - tl[BLK + qr]);
+                    }
+                } else {
+#pragma unroll
+                    for(int r = 0; r < 16; ++r) {
+                        const int qr = sub * 32 + acc_row(r, lh);
+                        const float pr = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
+                        sc[r] = pr;
+                        dp[r] = pr * (dp[r] - tl[BLK + qr]);
+                    }
                 }
                 const int64_t qg = 2 * j + sub;
                 if(qg >= kg) {
@@ -505,9 +521,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
                 if(2 * j + sub > qg) continue;  // the whole key group is in this wave's future
+                if((int64_t)j * BLK + BLK - 1 > q0) {  // the block crosses the diagonal
 #pragma unroll
-                for(int r = 0; r < 16; ++r)
-                    if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) cur[sub][r] = 0.0f;
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) cur[sub][r] = 0.0f;
+                }
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb)
                     dq[cb] = dot_cols(tk, sub, cb, lq, lh, cur[sub], dq[cb]);
