@@ -763,6 +763,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
         if(qs + BLK - 1 >= k0) {
             const float* tl = sLD[st];
             const int lim = (int)(ki - qs) - 4 * lh;  // query row qr sees key ki when qr >= lim
+            const bool diag = qs < k0 + 32;           // some query of the block precedes a key
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
                 f32x16 sc = dot_rows16(sQ[st], sub, lq, lh, kf, zero16());
@@ -770,10 +771,17 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
                     const int qr = sub * 32 + acc_row(r, lh);
-                    const float e = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) >= lim ? e : 0.0f;
-                    sc[r] = pr;
-                    dp[r] = pr * (dp[r] - tl[BLK + qr]);
+                    sc[r] = __builtin_amdgcn_exp2f(sc[r] - tl[qr]);
+                }
+                if(diag) {
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) < lim) sc[r] = 0.0f;
+                }
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const int qr = sub * 32 + acc_row(r, lh);
+                    dp[r] = sc[r] * (dp[r] - tl[BLK + qr]);
                 }
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb) {
@@ -829,15 +837,17 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
             const int lim = (int)(qi - kv0) - 4 * lh;
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
-                const f32x16 sc = dot_rows16(sK[st], sub, lq, lh, qf, zero16());
+                f32x16 sc = dot_rows16(sK[st], sub, lq, lh, qf, zero16());
                 f32x16 dp = dot_rows16(sV[st], sub, lq, lh, of, zero16());
 #pragma unroll
-                for(int r = 0; r < 16; ++r) {
-                    const float pr = sub * 32 + 8 * (r >> 2) + (r & 3) <= lim
-                                         ? __builtin_amdgcn_exp2f(sc[r] - l2)
-                                         : 0.0f;
-                    dp[r] = pr * (dp[r] - dd);
+                for(int r = 0; r < 16; ++r) sc[r] = __builtin_amdgcn_exp2f(sc[r] - l2);
+                if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) sc[r] = 0.0f;
                 }
+#pragma unroll
+                for(int r = 0; r < 16; ++r) dp[r] = sc[r] * (dp[r] - dd);
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols16(sKt[st], sub, cb, lq, lh, dp, dq[cb]);
             }
