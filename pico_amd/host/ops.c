@@ -245,15 +245,17 @@ void pico_matmul_backward_gpu(struct PicoTensor* self) {
     struct PkMat BT = {b->data, flip(vb.t), vb.ld};
     struct PkMat AT = {a->data, flip(va.t), va.ld};
     struct PkNode* nb = pkh_node(b);
-    pk_stream_t side = (nb && b->is_persistent && !a->is_persistent && a != b) ? pkh_side_fork()
-                                                                                : NULL;
+    const int to_side = nb && b->is_persistent && !a->is_persistent && a != b;
+    /* Eagerly, dB is forked before dA is issued, so that it runs beside dA
+     * rather than beside the memory-bound kernels that follow dA (config 5:
+     * about 1.3 ms less per step).  A captured graph keeps dA first: replays
+     * of the dB-first order measured slower.  Either way the side stream
+     * orders dB's write after every earlier write to b's grad: main-stream
+     * ones through the fork, side ones by issue order. */
+    const int db_first = to_side && !pkh_capturing();
+    pk_stream_t side = db_first ? pkh_side_fork() : NULL;
     int st;
     if(side) {
-        /* forked before dA is issued, so dB runs beside dA rather than beside
-         * the memory-bound kernels that follow it (config 5: 1.4 ms less per
-         * step on one box).  The side stream orders this write after every
-         * earlier write to b's grad: main-stream ones through the fork, side
-         * ones by issue order. */
         st = gemm_on(AT, dC, K, N, M, b->grad, vb.t, vb.ld, nb->grad_live ? PK_ACCUM : 0, side, 1);
         nb->side_seq = pkh_side_seq();
         if(pkh_status("pico_matmul_backward", st)) return;
@@ -262,11 +264,16 @@ void pico_matmul_backward_gpu(struct PicoTensor* self) {
     st = pkh_gemm(dC, BT, M, K, N, a->grad, va.t, va.ld, pkh_grad_flag(a));
     if(pkh_status("pico_matmul_backward", st)) return;
     pkh_grad_mark(a);
-    if(!side) {
+    if(side) return;
+    side = to_side ? pkh_side_fork() : NULL;
+    if(side) {
+        st = gemm_on(AT, dC, K, N, M, b->grad, vb.t, vb.ld, nb->grad_live ? PK_ACCUM : 0, side, 1);
+        nb->side_seq = pkh_side_seq();
+    } else {
         st = pkh_gemm(AT, dC, K, N, M, b->grad, vb.t, vb.ld, pkh_grad_flag(b));
-        if(pkh_status("pico_matmul_backward", st)) return;
-        pkh_grad_mark(b);
     }
+    if(pkh_status("pico_matmul_backward", st)) return;
+    pkh_grad_mark(b);
 }
 
 /* src/ops.c:144-190 (checks in the reference's order) */
