@@ -406,6 +406,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
             const bool diag = qs < k0 + 32;  // some query of the block precedes a key
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
+                // every query of this half precedes the wave's first key: its
+                // P and dS would be all zeros (and no dS tile holds them)
+                if(qs + sub * 32 + 31 < k0) continue;
                 f32x16 sc = dot_rows(tq, sub, lq, lh, kf, zero16());
                 f32x16 dp = dot_rows(to, sub, lq, lh, vf, zero16());
                 // one 128-bit operand read per 4 products, so the reads are
@@ -766,6 +769,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
             const bool diag = qs < k0 + 32;           // some query of the block precedes a key
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
+                if(qs + sub * 32 + 31 < k0) continue;  // all of P would be zeros
                 f32x16 sc = dot_rows16(sQ[st], sub, lq, lh, kf, zero16());
                 f32x16 dp = dot_rows16(sO[st], sub, lq, lh, vf, zero16());
 #pragma unroll
