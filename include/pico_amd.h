@@ -21,12 +21,18 @@
  *    contribution reads as zeros (pico_tensor_grad_to_host) and the first
  *    contribution overwrites instead of adding, which is bit-identical to
  *    adding into zeros and saves one full write of every grad.
- *  - An arena owns a device arena beside its host blocks: tensor structs,
- *    shapes and parent lists live in host memory, tensor data in one device
- *    block per arena block.  arena_reset rewinds both in O(#blocks) and keeps
- *    the device blocks for the next step; an allocation larger than a block
- *    gets a block of its own size (the reference's growth cannot serve it,
- *    src/arena.h:78-116).
+ *  - An arena has device blocks beside its host blocks: tensor structs,
+ *    shapes and parent lists live in host memory, tensor data in device
+ *    blocks.  struct Arena keeps pico's two-pointer layout; the device blocks
+ *    are held in a side table keyed by the arena's address, so an arena pico
+ *    allocated itself can be passed to arena_alloc_device.  arena_reset
+ *    rewinds both and keeps the device blocks for the next step; an
+ *    allocation larger than a block gets a block of its own size (the
+ *    reference's growth cannot serve it, src/arena.h:78-116).
+ *  - This library recognises its own tensors by address (a registry), never
+ *    by reading past sizeof(struct PicoTensor): tensors pico made itself, with
+ *    device data and grad, are accepted by the *_gpu twins below and treated
+ *    as plain pico tensors (grads always live, every contribution += ).
  *  - Kernels run asynchronously on one HIP stream (pico_gpu_stream).  The
  *    copy helpers synchronise it.  A failed launch inside a backward hook
  *    prints "[Pico] Error: ..." and is kept for pico_gpu_last_error().
@@ -43,7 +49,7 @@
 extern "C" {
 #endif
 
-/* ---- core types: identical layout to src/tensor.h:9-23 and src/arena.h:20-29 ---- */
+/* ---- core types: the layout of src/tensor.h:9-23 and src/arena.h:20-29 ---- */
 typedef enum { CPU, GPU } PicoBackend;
 
 struct PicoTensor {
@@ -67,13 +73,10 @@ struct ArenaBlock {
     unsigned char* curr;
 };
 
-struct PicoDeviceBlock;
-
-/* pico's two-pointer arena (src/arena.h:27-29) plus its device twin */
+/* pico's two-pointer arena (src/arena.h:27-29); its device blocks live in a
+ * side table of this library, keyed by the arena's address */
 struct Arena {
     struct ArenaBlock *begin, *end;
-    struct PicoDeviceBlock *dev_begin, *dev_end;
-    size_t dev_block_bytes;
 };
 
 /* ---- init (src/global.c:29-75) ----
@@ -91,8 +94,17 @@ void arena_destroy(struct Arena* arena);
 void arena_ctx_push(struct Arena* arena);
 void arena_ctx_pop(void);
 struct Arena* arena_ctx_current(void);
-/* device memory from the arena's device twin, 256-byte aligned */
+/* device memory from the arena's device blocks, 256-byte aligned (no
+ * reference counterpart: the device twin of arena_alloc, src/arena.h:105-116).
+ * `arena` may be one this library made or one pico made itself (its device
+ * blocks are then sized like its first host block, at least 1 MiB). */
 void* arena_alloc_device(struct Arena* arena, size_t size);
+/* For an arena pico made itself, the two calls its arena_reset and
+ * arena_destroy (src/arena.h:123-153) add: rewind the device blocks (kept for
+ * the next step), and free them with the side-table entry.  This library's
+ * own arena_reset / arena_destroy call them. */
+void arena_device_reset(struct Arena* arena);
+void arena_device_release(struct Arena* arena);
 
 /* ---- tensors (src/tensor.h:25-57, src/tensor.c) ---- */
 void pico_backward(struct Arena* arena, struct PicoTensor* entry); /* tensor.c:15-42 */

@@ -47,6 +47,22 @@ static int same_layout(const struct PicoTensor* t, const struct PicoTensor* self
 }
 
 /* ---------------------------------------------------- binary: seam twins */
+/* The seam twins may be called by pico itself (its ops.c with the GPU stubs
+ * filled in) on tensors it allocated: nothing here assumes they are this
+ * library's nodes, only that data and grad are device memory. */
+static int twin_refuses(const char* op, const struct PicoTensor* a, const struct PicoTensor* b,
+                        const struct PicoTensor* out) {
+    if(pkh_init()) return PK_EINVAL;
+    const char* why = (!a || !b || !out) ? "NULL tensor"
+                      : (!pkh_is_gpu(a) || !pkh_is_gpu(b) || !pkh_is_gpu(out))
+                          ? "expects tensors whose backend is GPU (device data and grad)"
+                          : NULL;
+    if(!why) return 0;
+    pkh_set_error("%s: %s", op, why);
+    PKH_ERR("%s: %s!\n", op, why);
+    return PK_EINVAL;
+}
+
 static int binary_gpu(int op, struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
     int64_t sa[256], sb[256];
     int nd = out->ndim;
@@ -56,18 +72,22 @@ static int binary_gpu(int op, struct PicoTensor* a, struct PicoTensor* b, struct
 }
 
 int pico_add_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    if(twin_refuses("pico_add_gpu", a, b, out)) return PK_EINVAL;
     return pkh_status("pico_add", binary_gpu(OP_ADD, a, b, out));
 }
 int pico_sub_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    if(twin_refuses("pico_sub_gpu", a, b, out)) return PK_EINVAL;
     return pkh_status("pico_sub", binary_gpu(OP_SUB, a, b, out));
 }
 int pico_mul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    if(twin_refuses("pico_mul_gpu", a, b, out)) return PK_EINVAL;
     return pkh_status("pico_mul", binary_gpu(OP_MUL, a, b, out));
 }
 
 /* src/autograd.h:53-94: a.grad += g (or g*b), b.grad += g (-g, g*a), summed
  * over each operand's broadcast dims */
 static void binary_backward(int op, struct PicoTensor* self) {
+    if(pkh_init()) return;
     struct PicoTensor *a = self->parents[0], *b = self->parents[1];
     const float* g = pkh_upstream(self);
     if(!g) return;
@@ -217,6 +237,7 @@ static int matmul_views(struct PicoTensor* a, struct PicoTensor* b, struct PkMat
 /* out = a . b, out contiguous [rows(a), cols(b)] (pico's kernels += into a
  * zeroed out, src/kernels/cpu/cpu_scalar.h:39-54; here it is overwritten) */
 int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* out) {
+    if(twin_refuses("pico_matmul_gpu", a, b, out)) return PK_EINVAL;
     struct PkMat va, vb;
     if(matmul_views(a, b, &va, &vb)) return PK_EINVAL;
     int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
@@ -235,6 +256,7 @@ int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTenso
  * one grad keep their program order either way, so results are bit for bit
  * those of a single stream. */
 void pico_matmul_backward_gpu(struct PicoTensor* self) {
+    if(pkh_init()) return;
     struct PicoTensor *a = self->parents[0], *b = self->parents[1];
     const float* g = pkh_upstream(self);
     if(!g) return;
@@ -364,6 +386,7 @@ struct PicoTensor* pico_tensor_log(struct PicoTensor* a) {
 /* ------------------------------------------------------------------ relu */
 /* src/act/autograd.h:9-17: parent.grad += g * (y > 0) */
 void pico_relu_backward_gpu(struct PicoTensor* self) {
+    if(pkh_init()) return;
     struct PicoTensor* x = self->parents[0];
     const float* g = pkh_upstream(self);
     if(!g) return;

@@ -14,7 +14,6 @@
 /* everything declared below is internal to libpico_amd.so */
 #pragma GCC visibility push(hidden)
 
-#define PKH_MAGIC 0x4E4B5050u /* "PPKN" */
 #define PKH_MAX_SAVED 4
 
 /* Every tensor made by this library is the first member of a node.  The node
@@ -23,7 +22,6 @@
  * state an op's backward needs (saved device buffers and sizes). */
 struct PkNode {
     struct PicoTensor t;
-    uint32_t magic;
     uint32_t grad_live;
     uint64_t visit;
     uint32_t seed_one; /* this node is the entry pico_backward seeded with 1 */
@@ -38,10 +36,15 @@ struct PkNode {
     float fval[PKH_MAX_SAVED];
 };
 
-static inline struct PkNode* pkh_node(const struct PicoTensor* t) {
-    struct PkNode* n = (struct PkNode*)t;
-    return (n && n->magic == PKH_MAGIC) ? n : NULL;
-}
+/* Node registry (arena.c).  pkh_node(t) is t's node when this library made t,
+ * else NULL; it looks t's address up in a hash set and reads nothing of *t,
+ * so a tensor pico allocated itself (exactly sizeof(struct PicoTensor) bytes)
+ * is safe to pass.  Nodes made in an arena are registered with it and
+ * forgotten at arena_reset / arena_destroy; params (arena NULL) at pico_free. */
+struct PkNode* pkh_node(const struct PicoTensor* t);
+int pkh_node_register(struct PkNode* n, struct Arena* arena);
+void pkh_node_unregister(const struct PkNode* n);
+void pkh_registry_clear(void);
 
 /* runtime (runtime.c) */
 int pkh_init(void);              /* 0 once the device and stream are up */

@@ -4,9 +4,10 @@
  *
  * Follows the reference's contracts (docs/contracts/01-allocation-and-
  * ownership.md): params are persistent and freed by pico_free; everything
- * else lives in the current arena until arena_reset / arena_destroy.  Here an
- * arena has a device twin: struct metadata stays in host blocks (pico's
- * layout, src/arena.h:20-29), tensor data goes to device blocks.
+ * else lives in the current arena until arena_reset / arena_destroy.  Struct
+ * metadata stays in the arena's host blocks, tensor data goes to its device
+ * twin (arena.c).  Every node made here is registered (pkh_node_register),
+ * which is how pkh_node tells this library's tensors from pico's own.
  */
 #include <math.h>
 #include <stdlib.h>
@@ -15,163 +16,6 @@
 #include "pk_host.h"
 
 #define DEV_ALIGN 256
-#define HOST_ALIGN 16
-#define MAX_ARENA_STACK 16
-
-/* ------------------------------------------------------------------ arena */
-struct PicoDeviceBlock {
-    struct PicoDeviceBlock* next;
-    size_t capacity;
-    size_t used;
-    unsigned char* bottom; /* device memory */
-};
-
-static _Thread_local struct Arena* g_arena_stack[MAX_ARENA_STACK];
-static _Thread_local int g_arena_top = -1;
-
-static struct ArenaBlock* host_block_new(size_t bytes) {
-    struct ArenaBlock* b = (struct ArenaBlock*)malloc(sizeof(*b));
-    if(!b) return NULL;
-    b->bottom = (unsigned char*)malloc(bytes);
-    if(!b->bottom) {
-        free(b);
-        return NULL;
-    }
-    b->curr = b->bottom;
-    b->capacity = bytes;
-    b->next = NULL;
-    return b;
-}
-
-/* src/arena.h:38-64.  `bytes` sizes both the first host block and each device
- * block; host blocks hold only structs, shapes and parent lists, so they are
- * capped at 4 MiB and grow on demand. */
-struct Arena* arena_init(size_t bytes) {
-    struct Arena* a = (struct Arena*)calloc(1, sizeof(*a));
-    if(!a) return NULL;
-    size_t hb = bytes < ((size_t)4 << 20) ? bytes : ((size_t)4 << 20);
-    if(hb < 4096) hb = 4096;
-    a->begin = host_block_new(hb);
-    if(!a->begin) {
-        free(a);
-        return NULL;
-    }
-    a->end = a->begin;
-    a->dev_block_bytes = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-    return a;
-}
-
-/* src/arena.h:105-116; a request larger than the block size gets a block of
- * its own size instead of failing */
-void* arena_alloc(struct Arena* a, size_t size) {
-    size = (size + HOST_ALIGN - 1) & ~(size_t)(HOST_ALIGN - 1);
-    struct ArenaBlock* b = a->end;
-    if((size_t)(b->curr - b->bottom) + size > b->capacity) {
-        size_t cap = a->begin->capacity > size ? a->begin->capacity : size;
-        struct ArenaBlock* nb = host_block_new(cap);
-        if(!nb) {
-            printf("Memory allocation failed!\n");
-            exit(1);
-        }
-        b->next = nb;
-        a->end = nb;
-        b = nb;
-    }
-    void* p = b->curr;
-    b->curr += size;
-    return p;
-}
-
-void* arena_alloc_device(struct Arena* a, size_t size) {
-    size = (size + DEV_ALIGN - 1) & ~(size_t)(DEV_ALIGN - 1);
-    if(size == 0) size = DEV_ALIGN;
-    struct PicoDeviceBlock* b = a->dev_end;
-    while(b && b->used + size > b->capacity) b = b->next;
-    if(!b) {
-        size_t cap = a->dev_block_bytes > size ? a->dev_block_bytes : size;
-        struct PicoDeviceBlock* nb = (struct PicoDeviceBlock*)calloc(1, sizeof(*nb));
-        if(!nb) return NULL;
-        nb->bottom = (unsigned char*)pkh_device_alloc(cap);
-        if(!nb->bottom) {
-            free(nb);
-            PKH_ERR("arena: device memory exhausted (%zu bytes requested)\n", size);
-            return NULL;
-        }
-        nb->capacity = cap;
-        if(!a->dev_begin) {
-            a->dev_begin = nb;
-        } else {
-            struct PicoDeviceBlock* last = a->dev_begin;
-            while(last->next) last = last->next;
-            last->next = nb;
-        }
-        b = nb;
-    }
-    a->dev_end = b;
-    void* p = b->bottom + b->used;
-    b->used += size;
-    return p;
-}
-
-/* src/arena.h:123-136: the host side frees its extra blocks as pico does; the
- * device blocks are rewound and kept, so a training loop allocates device
- * memory only in its first step */
-void arena_reset(struct Arena* a) {
-    struct ArenaBlock* c = a->begin->next;
-    while(c) {
-        struct ArenaBlock* n = c->next;
-        free(c->bottom);
-        free(c);
-        c = n;
-    }
-    a->begin->curr = a->begin->bottom;
-    a->begin->next = NULL;
-    a->end = a->begin;
-    for(struct PicoDeviceBlock* d = a->dev_begin; d; d = d->next) d->used = 0;
-    a->dev_end = a->dev_begin;
-}
-
-void arena_destroy(struct Arena* a) {
-    if(!a) return;
-    if(a->dev_begin) pkh_sync();
-    struct ArenaBlock* c = a->begin;
-    while(c) {
-        struct ArenaBlock* n = c->next;
-        free(c->bottom);
-        free(c);
-        c = n;
-    }
-    struct PicoDeviceBlock* d = a->dev_begin;
-    while(d) {
-        struct PicoDeviceBlock* n = d->next;
-        pkh_device_free(d->bottom);
-        free(d);
-        d = n;
-    }
-    free(a);
-}
-
-/* src/arena.h:155-169 */
-void arena_ctx_push(struct Arena* a) {
-    if(g_arena_top + 1 >= MAX_ARENA_STACK) {
-        PKH_ERR("arena context stack overflow (max %d)\n", MAX_ARENA_STACK);
-        return;
-    }
-    g_arena_stack[++g_arena_top] = a;
-}
-void arena_ctx_pop(void) {
-    if(g_arena_top >= 0) g_arena_top--;
-}
-struct Arena* arena_ctx_current(void) {
-    if(g_arena_top < 0 || g_arena_top >= MAX_ARENA_STACK) return NULL;
-    return g_arena_stack[g_arena_top];
-}
-
-struct Arena* pkh_need_arena(void) {
-    struct Arena* a = arena_ctx_current();
-    if(!a) PKH_ERR("No current arena in context!\n");
-    return a;
-}
 
 /* ---------------------------------------------------------------- tensors */
 static int64_t numel_of(const int64_t* shape, int ndim) {
@@ -198,7 +42,7 @@ struct PicoTensor* pkh_new_tensor(struct Arena* a, const int64_t* shape, int ndi
     }
     struct PkNode* n = (struct PkNode*)arena_alloc(a, sizeof(struct PkNode));
     memset(n, 0, sizeof(*n));
-    n->magic = PKH_MAGIC;
+    if(pkh_node_register(n, a)) return NULL;
     struct PicoTensor* t = &n->t;
     t->ndim = (uint8_t)ndim;
     t->shape = (int64_t*)arena_alloc(a, sizeof(int64_t) * ndim);
@@ -238,7 +82,6 @@ struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
         printf("Memory allocation failed!\n");
         return NULL;
     }
-    n->magic = PKH_MAGIC;
     struct PicoTensor* t = &n->t;
     t->ndim = ndim;
     t->is_persistent = 1;
@@ -265,7 +108,8 @@ struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
     }
     t->data = (float*)base;
     t->grad = (float*)(base + half);
-    if(pkh_status("pico_param", pk_fill_f32(t->numel, 0.0f, t->data, pkh_stream()))) {
+    if(pkh_status("pico_param", pk_fill_f32(t->numel, 0.0f, t->data, pkh_stream())) ||
+       pkh_node_register(n, NULL)) {
         pkh_device_free(base);
         free(t->shape);
         free(t->strides);
@@ -278,6 +122,12 @@ struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
 /* src/tensor.c:136-168 */
 void pico_free(struct PicoTensor* t) {
     if(!t || t->is_persistent == 0) return;
+    struct PkNode* n = pkh_node(t);
+    if(!n) {
+        PKH_ERR("pico_free: not a tensor of this library!\n");
+        return;
+    }
+    pkh_node_unregister(n);
     pkh_sync();
     free(t->shape);
     free(t->strides);
@@ -399,7 +249,7 @@ int pico_split_cols(struct PicoTensor* t, int n, struct PicoTensor** outs) {
         int64_t* strides = (int64_t*)arena_alloc(a, sizeof(int64_t) * 2);
         if(!vn || !shape || !strides) return PK_EINVAL;
         memset(vn, 0, sizeof(*vn));
-        vn->magic = PKH_MAGIC;
+        if(pkh_node_register(vn, a)) return PK_EINVAL;
         vn->base = t;
         struct PicoTensor* v = &vn->t;
         shape[0] = M;
