@@ -226,14 +226,55 @@ TRAIN_CONFIGS = {
 ADAMW = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
 
 
-def train_flop_per_step(cfg):
-    """6 x GEMM params x tokens, plus dense causal-attention products
-    (QK^T and PV forward, 2x that backward) counted over the full T x T"""
+def train_flop_per_step(cfg, causal=True):
+    """6 x GEMM params x tokens, plus the attention products (QK^T and PV
+    forward, 2x that backward).  causal=True counts the (query, key) pairs the
+    kernels compute, T(T+1)/2 per head; causal=False the full T x T that dense
+    attention would"""
     d, F, V, L = cfg["d_model"], cfg["d_ff"], cfg["vocab"], cfg["n_layers"]
-    tok = cfg["batch"] * cfg["seq_len"]
+    T = cfg["seq_len"]
+    tok = cfg["batch"] * T
     gemm_params = L * (4 * d * d + 3 * d * F) + d * V
-    attn = L * 3 * 2 * 2 * cfg["batch"] * cfg["seq_len"] ** 2 * d
+    pairs = T * (T + 1) / 2 if causal else T * T
+    attn = L * 3 * 2 * 2 * cfg["batch"] * pairs * d
     return 6.0 * gemm_params * tok + attn
+
+
+def xorshift_ids(seed, n, vocab):
+    """n int32 ids xorshift32() % vocab from `seed`: pico's generator
+    (src/tensor.c:249-266, shifts 13/17/5), the synthetic-input recipe for
+    labels and token ids"""
+    import numpy as np
+
+    s = seed & 0xFFFFFFFF
+    out = np.empty(n, np.int32)
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = s % vocab
+    return out
+
+
+def _loss_recorder(P, n):
+    """a device buffer of n floats and a function that copies a loss tensor's
+    value into slot i on the library's stream (no host synchronisation)"""
+    import ctypes
+
+    import torch
+
+    from pico_amd import _lib
+
+    buf = torch.zeros(n, device="cuda:0")
+    hip = _lib.hip_lib()
+    P.lib.pico_gpu_stream.restype = ctypes.c_void_p
+
+    def record(loss, i):
+        st = P.lib.pico_gpu_stream()
+        _lib.check("pk_axpy_f32", hip.pk_axpy_f32(1, 1.0, None, loss.contents.data,
+                                                   buf.data_ptr() + 4 * i, 0, st))
+
+    return buf, record
 
 
 def _gpt_step_launches(lib, model, opt, tok, tgt, work):
@@ -270,35 +311,46 @@ def _graph_replay_ms(P, launch_step, steps):
     return wall * 1e3 / steps
 
 
+SEEDS = {"mlp_x": 20261201, "mlp_labels": 20261202, "mlp_w1": 20261203, "mlp_w2": 20261204,
+         "tokens": 20261205, "model_init": 20261201}
+
+
 def mlp_section(steps, warmup):
     """config 1: pico's 784 -> 128 -> 10 ReLU MLP (examples/02_relu_mlp shapes),
     softmax cross-entropy, SGD lr 0.01, batch 64, inputs resident; eager steps
-    and a captured step replayed"""
+    and a captured step replayed.  Inputs come from the library's own seeded
+    generators: x = pico_randn, W = U(-1/sqrt(fan_in), 1/sqrt(fan_in)) from
+    pico_rand, labels xorshift32 % 10, each from a recorded seed."""
     import ctypes
 
     import numpy as np
 
-    from oracle import oracle as O
     from pico_amd.pico import TP, Pico
 
     P = Pico()
     lib = P.lib
+    x_state = ctypes.c_uint32.in_dll(lib, "x_state")
     data = lib.arena_init(1 << 20)
     lib.arena_ctx_push(data)
-    labels = lib.pico_ids_to_device(P.ids(O.labels(64, 20261202, 10)), 64)
+    labels = lib.pico_ids_to_device(P.ids(xorshift_ids(SEEDS["mlp_labels"], 64, 10)), 64)
     lib.arena_ctx_pop()
     work = lib.arena_init(1 << 24)
     lib.arena_ctx_push(work)
     fc1 = lib.pico_nn_linear_init(784, 128, True)
     fc2 = lib.pico_nn_linear_init(128, 10, True)
     opt = lib.pico_optim_sgd_init(0.01)
-    for fc, (fan, seed) in ((fc1, (784, 3)), (fc2, (128, 4))):
+    for fc, (fan, key) in ((fc1, (784, "mlp_w1")), (fc2, (128, "mlp_w2"))):
         w = ctypes.cast(fc + 8, ctypes.POINTER(TP)).contents
         b = ctypes.cast(fc + 16, ctypes.POINTER(TP)).contents
-        P.set(w, O.uniform(w.contents.numel, 20261200 + seed, -fan ** -0.5, fan ** -0.5))
+        x_state.value = SEEDS[key]
+        u = P.data(P.rand(work, w.contents.shape, w.contents.ndim))
+        P.set(w, (2.0 * u.astype(np.float64) - 1.0) * fan ** -0.5)
         lib.pico_optim_sgd_add(opt, w)
         lib.pico_optim_sgd_add(opt, b)
-    x = P.param([64, 784], O.normal(64 * 784, 20261201))
+    x_state.value = SEEDS["mlp_x"]
+    xs = (ctypes.c_int64 * 2)(64, 784)
+    x = P.param([64, 784], P.data(P.randn(work, xs, 2)))
+    lib.arena_reset(work)
 
     def launch_step():
         lib.pico_optim_sgd_zero_grad(opt)
@@ -336,6 +388,10 @@ def mlp_section(steps, warmup):
             "graph_samples_per_s": round(64 / (graph_ms * 1e-3), 1),
             "flop_per_step": flop, "steps": steps, "warmup": warmup,
             "loss_first": round(losses[0], 5), "loss_after_warmup": round(losses[-1], 5),
+            "inputs": {"x": f"pico_randn, x_state {SEEDS['mlp_x']}",
+                       "w1": f"pico_rand -> U(+-1/sqrt(784)), x_state {SEEDS['mlp_w1']}",
+                       "w2": f"pico_rand -> U(+-1/sqrt(128)), x_state {SEEDS['mlp_w2']}",
+                       "labels": f"xorshift32 % 10, seed {SEEDS['mlp_labels']}", "biases": 0},
             "config": {"model": "MLP 784-128-10 ReLU", "batch": 64, "optimizer": "SGD lr 0.01"}}
 
 
@@ -352,11 +408,11 @@ def train_section(name, steps, warmup, precision=0):
     lib = P.lib
     if lib.pico_set_matmul_precision(precision):
         raise RuntimeError("pico_set_matmul_precision failed")
-    model = P.gpt_init(cfg, 20261201)
+    model = P.gpt_init(cfg, SEEDS["model_init"])
     n = cfg["batch"] * cfg["seq_len"]
-    # synthetic token stream: inputs and next-token targets, uniform ids
-    rng = np.random.default_rng(20261201)
-    seq = rng.integers(0, cfg["vocab"], (cfg["batch"], cfg["seq_len"] + 1), dtype=np.int32)
+    # synthetic token stream: inputs and next-token targets, xorshift32 % vocab
+    seq = xorshift_ids(SEEDS["tokens"], cfg["batch"] * (cfg["seq_len"] + 1), cfg["vocab"])
+    seq = seq.reshape(cfg["batch"], cfg["seq_len"] + 1)
     data = lib.arena_init(1 << 20)
     lib.arena_ctx_push(data)
     tok = lib.pico_ids_to_device(P.ids(np.ascontiguousarray(seq[:, :-1])), n)
@@ -368,28 +424,33 @@ def train_section(name, steps, warmup, precision=0):
         lib.pico_optim_adamw_add(opt, t)
     work = lib.arena_init(1 << 30)
     lib.arena_ctx_push(work)
-    losses = []
+    # the loss of every step, copied on the device into a buffer read once
+    # at the end, so recording the curve adds no host synchronisation
+    curve, record = _loss_recorder(P, warmup + steps + 1)
+    done = [0]
 
-    def step(keep_loss):
+    def step():
         loss = lib.pico_gpt_loss(model, tok, tgt)
         if not loss:
             raise RuntimeError("pico_gpt_loss failed")
         lib.pico_optim_adamw_zero_grad(opt)
         lib.pico_backward(work, loss)
         lib.pico_optim_adamw_step(opt)
-        if keep_loss:
-            losses.append(float(P.data(loss)[0]))
+        record(loss, done[0])
+        done[0] += 1
         lib.arena_reset(work)
 
     for i in range(warmup):
-        step(keep_loss=(i == 0))
+        step()
     P.sync()
     t0 = time.perf_counter()
     for i in range(steps):
-        step(keep_loss=False)
+        step()
     P.sync()
     wall = time.perf_counter() - t0
-    step(keep_loss=True)
+    step()
+    P.sync()
+    losses = [float(v) for v in curve.cpu().numpy()]
     graph_ms = _graph_replay_ms(P, lambda: _gpt_step_launches(lib, model, opt, tok, tgt, work),
                                 steps)
     _, peak_bytes = P.memory()
@@ -402,7 +463,8 @@ def train_section(name, steps, warmup, precision=0):
     lib.pico_set_matmul_precision(0)
     if err:
         raise RuntimeError(err)
-    flop = train_flop_per_step(cfg)
+    flop = train_flop_per_step(cfg, causal=True)
+    flop_dense = train_flop_per_step(cfg, causal=False)
     ms = wall * 1e3 / steps
     # bf16x3: three bf16 matrix instructions per fp32 product
     peak, peak_name = {1: (MFMA_BF16_PEAK, "bf16 2.5 PFLOP/s"),
@@ -411,11 +473,19 @@ def train_section(name, steps, warmup, precision=0):
     return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
             "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
             "mfu": round(flop / (ms * 1e-3) / peak, 4),
+            "mfu_count": "causal: attention over the T(T+1)/2 pairs the kernels compute",
+            "mfu_dense_count": round(flop_dense / (ms * 1e-3) / peak, 4),
+            "flop_per_step": flop, "flop_per_step_dense_attention": flop_dense,
             "mfu_peak": peak_name,
             "graph_ms_per_step": round(graph_ms, 3),
             "graph_tokens_per_s": round(n / (graph_ms * 1e-3), 1),
             "tokens_per_step": n, "steps": steps, "warmup": warmup,
             "loss_first": round(losses[0], 5), "loss_after": round(losses[-1], 5),
+            "loss_curve": [round(v, 5) for v in losses],
+            "loss_curve_note": f"one batch repeated: {warmup} warmup steps, {steps} timed "
+                               "steps, 1 more; each step's loss copied on the device",
+            "inputs": {"tokens": f"xorshift32 % vocab, seed {SEEDS['tokens']}",
+                       "weights": f"N(0, 0.02) from pico_gpt_init seed {SEEDS['model_init']}"},
             "device_gib_peak": round(peak_bytes / 2 ** 30, 2),
             "optimizer": dict(ADAMW, name="AdamW"), "config": cfg}
 
@@ -452,8 +522,17 @@ def cpu_baseline(n):
         run()
         ts.append(time.perf_counter() - t0)
     t = sorted(ts)[1]
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {"value": round(2.0 * n ** 3 / t / 1e12, 4), "unit": "TFLOP/s", "cores": 8,
-            "kind": kind, "host_cpus": os.cpu_count(),
+            "kind": kind, "host_cpus": os.cpu_count(), "cpu_model": model,
             "sample": f"one fp32 matmul {n}^3 (forward A.B), pico's AVX+FMA kernel on its 8-worker "
                       f"pool, median of 3 after 1 warmup, {t:.2f} s each"}
 
@@ -465,7 +544,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--sections", default="train,sweep,bf16,attn,rows,cpu")
-    ap.add_argument("--train-steps", type=int, default=10)
+    ap.add_argument("--train-steps", type=int, default=50)
+    ap.add_argument("--variant-steps", type=int, default=10)
     ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -524,12 +604,17 @@ def main():
                 line["train"][name] = train_section(name, args.train_steps, 3)
     if "sweep" in sections:
         line["sweep"] = sweep_section(torch, K, [512, 1024, 2048, 4096, 8192])
+        # the headline kernel again, timed where the sweep times it (after the
+        # training sections, on a warm chip) rather than first in the run
+        line["roofline"]["achieved_in_sweep_position"] = line["sweep"]["4096"]["NN"]
+        line["roofline"]["frac_in_sweep_position"] = round(
+            line["sweep"]["4096"]["NN"] * 1e12 / MFMA_FP32_PEAK, 4)
     if "bf16" in sections:
         # outside the fp32 parity contract: bf16 multiplies, fp32 accumulation,
         # fp32 tensors (pk_gemm_bf16_f32 / pico_set_matmul_precision)
         line["bf16"] = {
             "sweep": sweep_section(torch, K, [1024, 2048, 4096, 8192], K.gemm_bf16),
-            "train": {name: train_section(name, args.train_steps, 3, precision=1)
+            "train": {name: train_section(name, args.variant_steps, 3, precision=1)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
             "peak_tflops": MFMA_BF16_PEAK / 1e12,
             "note": "bf16 products of fp32 operands (rounded to nearest even), fp32 "
@@ -538,7 +623,7 @@ def main():
         # fp32; TFLOP/s counted as fp32 products (2n^3), not bf16 instructions
         line["bf16x3"] = {
             "sweep": sweep_section(torch, K, [2048, 4096, 8192], K.gemm_bf16x3),
-            "train": {name: train_section(name, args.train_steps, 3, precision=2)
+            "train": {name: train_section(name, args.variant_steps, 3, precision=2)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
             "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
                     "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "

@@ -18,6 +18,8 @@ wqkv = [Wq | Wk | Wv] [d,3d] and w13 = [W1 | W3] [d,2F], six params per layer
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 PER_LAYER = 9
@@ -96,13 +98,16 @@ def _attn_bwd(cache, dout, B, T, H):
     return _merge(dQ), _merge(dK), _merge(dV)
 
 
-def loss_and_grads(params, cfg, tokens, targets, eps=1e-6, need_grads=True):
-    """mean cross-entropy (float) and, if asked, one float64 gradient per param"""
+def loss_and_grads(params, cfg, tokens, targets, eps=1e-6, need_grads=True, n_norm=None):
+    """mean cross-entropy (float) and, if asked, one float64 gradient per param.
+    n_norm (default: the number of positions) is the denominator of the mean,
+    so a share of a batch can be run alone and the shares summed."""
     P = [np.asarray(p, np.float64) for p in params]
     B, T, H, L = cfg["batch"], cfg["seq_len"], cfg["n_heads"], cfg["n_layers"]
     tokens = np.asarray(tokens, np.int64).ravel()
     targets = np.asarray(targets, np.int64).ravel()
     n = tokens.size
+    n_norm = n if n_norm is None else n_norm
     E = P[0]
     x = E[tokens]
     caches = []
@@ -123,13 +128,13 @@ def loss_and_grads(params, cfg, tokens, targets, eps=1e-6, need_grads=True):
     logits = hf @ Wlm
     m = logits.max(-1, keepdims=True)
     lse = m[:, 0] + np.log(np.exp(logits - m).sum(-1))
-    loss = float(np.mean(lse - logits[np.arange(n), targets]))
+    loss = float(np.sum(lse - logits[np.arange(n), targets]) / n_norm)
     if not need_grads:
         return loss, None
     grads = [None] * len(P)
     dlogits = np.exp(logits - lse[:, None])
     dlogits[np.arange(n), targets] -= 1.0
-    dlogits /= n
+    dlogits /= n_norm
     grads[-1] = hf.T @ dlogits
     dx, grads[-2] = _rms_bwd(x, gf, rf, dlogits @ Wlm.T)
     for l in reversed(range(L)):
@@ -157,6 +162,48 @@ def loss_and_grads(params, cfg, tokens, targets, eps=1e-6, need_grads=True):
     np.add.at(dE, tokens, dx)
     grads[0] = dE
     return loss, grads
+
+
+def loss_and_grads_by_sequence(params, cfg, tokens, targets, eps=1e-6, workers=8):
+    """loss_and_grads over the batch, one sequence at a time in a thread pool.
+
+    Sequences are independent up to the mean over positions and the sums that
+    form the parameter gradients, so each sequence runs alone with the whole
+    batch's denominator and the results are added (float64: the changed
+    summation order is far below the tests' tolerance).  numpy's BLAS calls
+    and large ufuncs release the GIL, so the threads run in parallel; this is
+    what makes the 12-layer, 8 x 1024-token configuration's reference
+    affordable."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    B, T = cfg["batch"], cfg["seq_len"]
+    tokens = np.asarray(tokens, np.int64).reshape(B, T)
+    targets = np.asarray(targets, np.int64).reshape(B, T)
+    one = dict(cfg, batch=1)
+    P = [np.asarray(p, np.float64) for p in params]
+
+    def run(b):
+        return loss_and_grads(P, one, tokens[b], targets[b], eps=eps, n_norm=B * T)
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    inner = max(1, (os.cpu_count() or 8) // max(1, min(workers, B)))
+    ctx = threadpool_limits(limits=inner) if threadpool_limits else _nullctx()
+    with ctx, ThreadPoolExecutor(max_workers=min(workers, B)) as ex:
+        parts = list(ex.map(run, range(B)))
+    loss = float(sum(p[0] for p in parts))
+    grads = [sum(p[1][i] for p in parts) for i in range(len(P))]
+    return loss, grads
+
+
+class _nullctx:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
 
 
 def adamw(p, g, m, v, step, lr, b1, b2, eps, wd):

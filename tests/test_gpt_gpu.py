@@ -5,9 +5,10 @@ seeded weights (read back to the host).
 Bar (the north star's floating-point tolerance): max relative error <= 1e-4
 on the loss and on every parameter gradient (max|gpu - ref| / max|ref| per
 tensor), and the loss curve of AdamW steps within 1e-4.  Config 5's full
-12-layer step is checked at full size through properties (initial loss of a
-near-uniform model, loss falls when one batch is repeated, finite grads) and
-at its full widths and sequence length with two layers against the reference.
+12-layer step (batch 8, T 1024) is compared with the reference in full, loss
+and every gradient (the reference runs one sequence per thread); it is also
+checked through properties over three AdamW steps, and at its full widths with
+two layers.
 """
 import math
 
@@ -54,14 +55,15 @@ def _host_params(P, model, cfg):
             G.split_fused([P.value(t) for t in P.gpt_params(model)], cfg)]
 
 
-def _check_step(P, cfg, seed):
+def _check_step(P, cfg, seed, arena_bytes=1 << 28, by_sequence=False):
     model = P.gpt_init(cfg, seed)
     try:
         tokens, targets, _ = _batch(cfg, seed + 1)
         params = _host_params(P, model, cfg)
-        loss, grads = _gpu_step(P, model, tokens, targets)
+        loss, grads = _gpu_step(P, model, tokens, targets, arena_bytes)
         grads = G.split_fused(grads, cfg)  # compared weight by weight
-        ref_loss, ref_grads = G.loss_and_grads(params, cfg, tokens, targets)
+        ref = G.loss_and_grads_by_sequence if by_sequence else G.loss_and_grads
+        ref_loss, ref_grads = ref(params, cfg, tokens, targets)
         assert abs(loss - ref_loss) <= TOL * abs(ref_loss)
         assert len(grads) == len(ref_grads)
         for i, (g, r) in enumerate(zip(grads, ref_grads)):
@@ -84,8 +86,16 @@ def test_config5_widths_two_layers_loss_and_grads(P):
     _check_step(P, dict(CONFIG5, n_layers=2, batch=2), 31)
 
 
+@pytest.mark.slow
+@pytest.mark.timeout(600)
+def test_config5_full_step_loss_and_grads(P):
+    # the benchmark configuration itself: 12 layers, batch 8, T 1024, d 768,
+    # vocab 32000; the float64 reference takes about a minute on 16 cores
+    _check_step(P, CONFIG5, 61, arena_bytes=1 << 30, by_sequence=True)
+
+
 def test_config4_adamw_loss_curve(P):
-    cfg, steps = CONFIG4, 8
+    cfg, steps = CONFIG4, 12
     model = P.gpt_init(cfg, 41)
     try:
         tokens, targets, _ = _batch(cfg, 42)
@@ -117,7 +127,7 @@ def test_config4_adamw_loss_curve(P):
                                                ADAMW["eps"], ADAMW["wd"])
         assert gpu[-1] < gpu[0]
         assert max_rel(np.array(gpu), np.array(ref)) <= TOL
-        # weights after 8 updates: AdamW's normalised step turns fp32-vs-fp64
+        # weights after 12 updates: AdamW's normalised step turns fp32-vs-fp64
         # rounding in the sign of a near-zero gradient into a full +-lr move of that
         # one element, so the weights are compared by their Frobenius-relative error
         for i, (fg, fr) in enumerate(zip(final_gpu, params)):

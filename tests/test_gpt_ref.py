@@ -85,3 +85,18 @@ def test_fused_parameter_mapping_round_trips():
     assert np.array_equal(fused[2][:, 4:8], sep[3]) and np.array_equal(fused[5][:, 6:], sep[8])
     back = G.split_fused([f.ravel() for f in fused], cfg)
     assert all(np.array_equal(a.reshape(b.shape), b) for a, b in zip(back, sep))
+
+
+def test_by_sequence_split_equals_the_whole_batch():
+    """loss_and_grads_by_sequence (one sequence per thread, shares summed) is
+    the same function as loss_and_grads over the whole batch"""
+    cfg = dict(CFG, batch=3, seq_len=6)
+    params = _params(cfg, 5)
+    rng = np.random.default_rng(6)
+    tokens = rng.integers(0, cfg["vocab"], cfg["batch"] * cfg["seq_len"])
+    targets = rng.integers(0, cfg["vocab"], cfg["batch"] * cfg["seq_len"])
+    l0, g0 = G.loss_and_grads(params, cfg, tokens, targets)
+    l1, g1 = G.loss_and_grads_by_sequence(params, cfg, tokens, targets, workers=3)
+    assert abs(l0 - l1) <= 1e-12 * abs(l0)
+    for a, b in zip(g0, g1):
+        assert np.max(np.abs(a - b)) <= 1e-12 * max(1.0, float(np.max(np.abs(a))))

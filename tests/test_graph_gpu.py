@@ -1,7 +1,8 @@
 """Device graphs (pico_graph_begin / end / launch): one training step recorded
 once and replayed must give bit-for-bit the results of running the same steps
 eagerly -- the replay launches the same kernels with the same arguments on the
-same addresses.  Each replay is read back and compared, with eager work and
+same addresses -- and replayed curves must match the CPU oracle (config 1's 100
+SGD steps) and the float64 transformer reference (AdamW steps) within 1e-4.  Each replay is read back and compared, with eager work and
 synchronisations between replays.  Also: the multi-tensor AdamW that makes an
 optimizer step replayable matches the per-tensor kernel bit for bit, and a
 capture that would allocate or copy is refused with a clear error while the
@@ -145,6 +146,124 @@ def test_mlp_sgd_graph_replay_matches_eager(P):
     assert np.array_equal(l0, l1)
     for a, b in zip(p0, p1):
         assert np.array_equal(a, b)
+
+
+def test_mlp_graph_replay_loss_curve_matches_cpu_oracle(P):
+    """Config 1's 100 SGD steps with the step captured once and replayed 99
+    times, against the CPU oracle's pico API (pico's own loops restated) running
+    the same 100 steps eagerly: every loss and the final weights within 1e-4.
+    The replay is compared with the CPU here, not only with eager GPU steps,
+    so an error shared by both GPU paths would show."""
+    from tests._util import max_rel
+
+    C = Pico(O.lib(), device=False)
+    x = O.normal(64 * 784, 20261201).reshape(64, 784)
+    labels = O.labels(64, 20261202, 10)
+    w1 = O.uniform(784 * 128, 20261203, -784 ** -0.5, 784 ** -0.5).reshape(784, 128)
+    w2 = O.uniform(128 * 10, 20261204, -128 ** -0.5, 128 ** -0.5).reshape(128, 10)
+    steps = 100
+    # CPU oracle, eager
+    cpu = []
+    with C.arena(1 << 24) as ar:
+        fc1, fc2, params, opt, xt = _mlp(C, x, w1, w2)
+        for _ in range(steps):
+            loss = _mlp_step(C, fc1, fc2, opt, xt, C.ids(labels))
+            cpu.append(float(C.data(loss)[0]))
+            C.reset(ar)
+        cpu_final = [C.data(p) for p in params]
+        C.optim_sgd_free(opt)
+        C.free(xt)
+        C.nn_linear_free(fc1)
+        C.nn_linear_free(fc2)
+    # GPU: one eager step, then the captured step replayed
+    ids_arena = P.lib.arena_init(1 << 16)
+    gpu = []
+    with P.arena(1 << 24) as ar:
+        fc1, fc2, params, opt, xt = _mlp(P, x, w1, w2)
+        dlab = _device_ids(P, ids_arena, labels)
+        gpu.append(float(P.data(_mlp_step(P, fc1, fc2, opt, xt, dlab))[0]))
+        P.reset(ar)
+        assert P.lib.pico_graph_begin() == 0
+        loss = _mlp_step(P, fc1, fc2, opt, xt, dlab)
+        graph = P.lib.pico_graph_end()
+        assert graph, P.lib.pico_gpu_last_error()
+        for s in range(1, steps):
+            assert P.lib.pico_graph_launch(graph) == 0
+            gpu.append(float(P.data(loss)[0]))
+            if s % 25 == 0:
+                _eager_noise(P)
+        gpu_final = [P.data(p) for p in params]
+        P.lib.pico_graph_free(graph)
+        P.optim_sgd_free(opt)
+        P.free(xt)
+        P.nn_linear_free(fc1)
+        P.nn_linear_free(fc2)
+    P.lib.arena_destroy(ids_arena)
+    gpu, cpu = np.array(gpu), np.array(cpu)
+    assert np.all(np.diff(gpu) < 0) and gpu[-1] < 0.5 * gpu[0]
+    assert max_rel(gpu, cpu) <= 1e-4
+    for g, c in zip(gpu_final, cpu_final):
+        assert max_rel(g, c) <= 1e-4
+
+
+def test_gpt_graph_replay_loss_curve_matches_float64_reference(P):
+    """A small transformer's AdamW steps (one eager, then the captured step
+    replayed 9 times on one batch) against the float64 reference's 10 steps
+    (oracle/gpt_ref.py with its own AdamW): losses within 1e-4."""
+    from oracle import gpt_ref as G
+    from tests._util import max_rel
+
+    cfg = dict(vocab=96, d_model=64, n_layers=2, n_heads=2, d_ff=160, batch=2, seq_len=64)
+    hp = dict(lr=1e-3, b1=0.9, b2=0.95, eps=1e-8, wd=0.1)
+    seq = O.labels(cfg["batch"] * (cfg["seq_len"] + 1), 91, cfg["vocab"])
+    seq = seq.reshape(cfg["batch"], cfg["seq_len"] + 1)
+    tokens, targets = seq[:, :-1].ravel().copy(), seq[:, 1:].ravel().copy()
+    steps = 10
+    model = P.gpt_init(cfg, 92)
+    tensors = P.gpt_params(model)
+    ref_params = [p.astype(np.float64) for p in
+                  G.split_fused([P.value(t) for t in tensors], cfg)]
+    opt = P.optim_adamw_init(hp["lr"], hp["b1"], hp["b2"], hp["eps"], hp["wd"])
+    for t in tensors:
+        P.optim_adamw_add(opt, t)
+    ids_arena = P.lib.arena_init(1 << 20)
+    tok = _device_ids(P, ids_arena, tokens)
+    tgt = _device_ids(P, ids_arena, targets)
+
+    def step():
+        P.optim_adamw_zero_grad(opt)
+        loss = P.gpt_loss(model, tok, tgt)
+        P.backward(loss)
+        P.optim_adamw_step(opt)
+        return loss
+
+    gpu = []
+    with P.arena(1 << 26) as ar:
+        gpu.append(float(P.data(step())[0]))
+        P.reset(ar)
+        assert P.lib.pico_graph_begin() == 0
+        loss = step()
+        graph = P.lib.pico_graph_end()
+        assert graph, P.lib.pico_gpu_last_error()
+        for _ in range(1, steps):
+            assert P.lib.pico_graph_launch(graph) == 0
+            gpu.append(float(P.data(loss)[0]))
+        P.lib.pico_graph_free(graph)
+    P.optim_adamw_free(opt)
+    P.gpt_free(model)
+    P.lib.arena_destroy(ids_arena)
+    ref = []
+    m = [np.zeros_like(p) for p in ref_params]
+    v = [np.zeros_like(p) for p in ref_params]
+    for s in range(1, steps + 1):
+        loss, grads = G.loss_and_grads(ref_params, cfg, tokens, targets)
+        ref.append(loss)
+        for i, g in enumerate(grads):
+            ref_params[i], m[i], v[i] = G.adamw(ref_params[i], g.reshape(ref_params[i].shape),
+                                               m[i], v[i], s, hp["lr"], hp["b1"], hp["b2"],
+                                               hp["eps"], hp["wd"])
+    assert gpu[-1] < gpu[0]
+    assert max_rel(np.array(gpu), np.array(ref)) <= 1e-4
 
 
 # ---------------------------------------------------- transformer (AdamW)
