@@ -344,9 +344,10 @@ def test_pico_arena_device_blocks_and_a_small_graph(lib):
     finally:
         lib.arena_device_release(arena)
         F.close()
+        untouched = ar[0] == block and ar[1] == block  # pico's own fields
         for p in (bottom, block, arena):
             libc.free(p)
-    assert ar[0] == block and ar[1] == block  # pico's own fields untouched
+    assert untouched
 
 
 def test_twins_refuse_cpu_tensors(lib):
