@@ -67,6 +67,21 @@ int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alph
                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                    void* workspace, size_t workspace_bytes, pk_stream_t stream);
 
+/* pk_gemm_ex_f32 that allocates nothing and takes no workspace.  No
+ * counterpart in the reference (pico allocates freely); it is for callers that
+ * cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  A product that splits K puts its
+ * partial planes in a static device array of pk_gemm_noalloc_scratch_bytes()
+ * (128 MiB) that each GPU holds until the process ends; a product whose
+ * partials need more (pk_gemm_workspace_f32 above that size) is refused with
+ * PK_EINVAL and a message.  Results equal pk_gemm_ex_f32's bit for bit.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads) race, so serialise them. */
+size_t pk_gemm_noalloc_scratch_bytes(void);
+int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                        const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                        float* C, int64_t ldc, pk_stream_t stream);
+
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
  * multiplied on the bf16 matrix cores, accumulating in fp32; C and the

@@ -37,6 +37,9 @@ PK_SIGNATURES = {
     "pk_gemm_workspace_f32": [c_i64, c_i64, c_i64],
     "pk_gemm_ex_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f, c_p,
                        c_i64, c_p, c_size, c_p],
+    "pk_gemm_noalloc_scratch_bytes": [],
+    "pk_gemm_noalloc_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
+                            c_f, c_p, c_i64, c_p],
     "pk_gemm_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
                          c_p, c_i64, c_p],
     "pk_gemm_ex_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
@@ -98,7 +101,7 @@ PK_SIGNATURES = {
 }
 _RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size,
              "pk_gemm_workspace_f32": c_size, "pk_flash_attn_bwd_workspace": c_size,
-             "pk_embed_bwd_workspace": c_size}
+             "pk_embed_bwd_workspace": c_size, "pk_gemm_noalloc_scratch_bytes": c_size}
 
 _hip = None
 

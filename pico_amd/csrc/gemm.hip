@@ -46,6 +46,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "pk_common.h"
@@ -993,4 +994,65 @@ extern "C" int pk_gemm_ex_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int
                                      void* workspace, size_t workspace_bytes, pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
                      0, static_cast<float*>(workspace), workspace_bytes, kBf16x3, stream);
+}
+
+// ---- pk_gemm_noalloc_f32: the split-K GEMM without a caller workspace ------
+// For callers that cannot allocate (code under graph capture, tight serving
+// loops): the split-K partial planes go to `scratch`, a file-scope device
+// array of kNoAllocScratchBytes that every GPU holds from the code object's
+// load until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory, so the kernels get the array's device address,
+// looked up once per device with hipGetSymbolAddress (each GPU holds its own
+// copy at its own address).  Calls that overlap on one GPU (two streams, two
+// threads) share that GPU's array and race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+float* g_scratch_dev[kMaxDevices];  // the array's device address, per device
+std::mutex g_scratch_lock;
+
+// the current device's address of `scratch` (nullptr + message on failure)
+float* scratch_on_current_device() {
+    int dev = -1;
+    if(hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        pk::fail("pk_gemm_noalloc_f32: no current HIP device (or device id above %d)",
+                 kMaxDevices - 1);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if(!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if(e != hipSuccess || !p) {
+            pk::fail("pk_gemm_noalloc_f32: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                     dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_dev[dev] = static_cast<float*>(p);
+    }
+    return g_scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" size_t pk_gemm_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                   const float* A, int64_t lda, const float* B, int64_t ldb,
+                                   float beta, float* C, int64_t ldc, pk_stream_t stream) {
+    const size_t need = pk_gemm_workspace_f32(M, N, K);
+    if(need > kNoAllocScratchBytes)
+        return pk::fail("pk_gemm_noalloc_f32: this product's split-K partials need %zu bytes, "
+                        "above the %zu-byte static scratch (use pk_gemm_ex_f32 with a workspace)",
+                        need, kNoAllocScratchBytes);
+    float* ws = nullptr;
+    if(need > 0 && !(ws = scratch_on_current_device())) return PK_EINVAL;
+    // every partial-plane element the reduction reads is written by its split
+    // in the same call, so nothing in the scratch has to start at zero
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, ws, ws ? kNoAllocScratchBytes : 0, kFp32, stream);
 }
