@@ -183,6 +183,22 @@ struct PicoTensor* pico_embedding(struct PicoTensor* table, const int32_t* ids, 
 /* idx[r] = first argmax of row r of x [R, V]; idx is host memory (R int32) */
 int pico_argmax(struct PicoTensor* x, int32_t* idx);
 
+/* ---- fused ops (no reference counterpart: pico runs a matmul and the op
+ * that consumes it as two passes over memory).  Same template as src/ops.c
+ * :144-190; each equals the composition of the ops it fuses, bit for bit.
+ * pico_matmul_add(a, b, c) = c + a.b, c a contiguous [rows(a), cols(b)]
+ *   (a residual connection added in the product's epilogue).
+ * pico_swiglu_matmul_add(gate, up, w, c) = c + swiglu(gate, up).w, c (a
+ *   contiguous [M, N]) may be NULL; gate and up distinct [M, F] with one row
+ *   stride (column views of
+ *   one [M, 2F] product are fine), w row-contiguous [F, N].  The backward
+ *   never stores dh: the product dY.w^T writes the gate and up gradients
+ *   from its tiles. ---- */
+struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
+                                   struct PicoTensor* c);
+struct PicoTensor* pico_swiglu_matmul_add(struct PicoTensor* gate, struct PicoTensor* up,
+                                          struct PicoTensor* w, struct PicoTensor* c);
+
 /* ---- nn (src/nn/linear.h:6-15) ---- */
 struct PicoLinear {
     int in_features;

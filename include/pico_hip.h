@@ -82,6 +82,31 @@ int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float
                         const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                         float* C, int64_t ldc, pk_stream_t stream);
 
+/* Products with a fused epilogue (no reference counterpart: pico runs a matmul
+ * and the op that consumes it as two passes over memory).  precision selects
+ * the multiplies: 0 fp32 (as pk_gemm_ex_f32), 1 bf16 (pk_gemm_ex_bf16_f32),
+ * 2 three bf16 products (pk_gemm_ex_bf16x3_f32).
+ * pk_gemm_add_f32: C = alpha * op(A).op(B) + beta * X, X [M,N] with row stride
+ *   ldx (X == C with ldx == ldc is pk_gemm_ex_f32's accumulate); a residual
+ *   connection x + a.W in one pass.  Same workspace contract as pk_gemm_ex_f32.
+ * pk_gemm_swiglu_bwd_f32: dh = alpha * op(A).op(B) [M,N] is the upstream
+ *   gradient of h = silu(gate) * up and is never stored; each tile writes
+ *   dgate (+)= dh*up*s*(1 + gate*(1-s)) (flags bit 0 accumulates) and
+ *   dup (+)= dh*gate*s (bit 1), s = sigmoid(gate), with pk_swiglu_bwd_f32's
+ *   arithmetic; gate, up [M,N] (row strides ldg, ldu) are read in the tile's
+ *   epilogue, dgate and dup (distinct) share the row stride ldd.  In a
+ *   transformer block it is the down projection's input gradient dY.W2^T
+ *   turned straight into the gate/up gradients. */
+int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                    const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                    const float* X, int64_t ldx, float* C, int64_t ldc, int precision,
+                    void* workspace, size_t workspace_bytes, pk_stream_t stream);
+int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                           const float* A, int64_t lda, const float* B, int64_t ldb,
+                           const float* gate, int64_t ldg, const float* up, int64_t ldu,
+                           float* dgate, float* dup, int64_t ldd, int flags, int precision,
+                           pk_stream_t stream);
+
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
  * multiplied on the bf16 matrix cores, accumulating in fp32; C and the

@@ -104,6 +104,20 @@ struct GemmParams {
     int splits;      // > 1: blockIdx.y is a K slice of kchunk, partials go to ws
     int64_t kchunk;
     float* ws;
+    // the beta term's source: C itself, or another matrix (batch 1 only)
+    const float* Cin;
+    int64_t ldcin;
+    // SwiGLU-backward epilogue (sg_a non-null, batch 1, no K split): the
+    // product is the upstream gradient dh of h = silu(a) * u and is not
+    // stored; the tile writes da (+)= dh*u*s*(1 + a*(1-s)) and du (+)= dh*a*s
+    // (s = sigmoid(a)), accumulating per sg_flags bit 0 (da) and bit 1 (du)
+    const float *sg_a, *sg_u;
+    float *sg_da, *sg_du;
+    int64_t sg_lda, sg_ldu, sg_ldd;
+    int sg_flags;
+    // the staged epilogue may use float4 accesses: every matrix it touches is
+    // 16-byte aligned with a row stride that is a multiple of 4
+    int epi_vec;
 };
 
 // Bounds handling of a tile's loads and stores: none (whole tiles), per float4
@@ -379,7 +393,8 @@ struct TileJob {
     const float* A;
     const float* B;
     float* C;
-    int64_t ldc, row0, col0, kbeg, kend;
+    const float* Cin;
+    int64_t ldc, ldcin, row0, col0, kbeg, kend;
     float alpha, beta;
     int nslices;
     bool skip;
@@ -406,6 +421,8 @@ __device__ __forceinline__ TileJob tile_job(const GemmParams& p) {
     j.B = p.B + zo * p.sBo + zi * p.sBi;
     j.C = p.C + zo * p.sCo + zi * p.sCi;
     j.ldc = p.ldc;
+    j.Cin = p.Cin ? p.Cin : j.C;
+    j.ldcin = p.Cin ? p.ldcin : p.ldc;
     j.alpha = p.alpha;
     j.beta = p.beta;
 
@@ -422,6 +439,8 @@ __device__ __forceinline__ TileJob tile_job(const GemmParams& p) {
         j.kend = min(p.K, j.kbeg + p.kchunk);
         j.C = p.ws + (int64_t)blockIdx.y * p.M * p.N;
         j.ldc = p.N;
+        j.Cin = j.C;
+        j.ldcin = p.N;
         j.alpha = 1.0f;
         j.beta = 0.0f;
     }
@@ -430,7 +449,8 @@ __device__ __forceinline__ TileJob tile_job(const GemmParams& p) {
 }
 
 // C tile = alpha * acc (+ beta * C).  32x32 block accumulator r of lane l is
-// row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// row 8*(r/4) + 4*(l/32) + r%4, column l%32: each half-wave writes 128
+// contiguous bytes per register.
 template <int EDGE, int TM, int TN>
 __device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j,
                                            const f32x16 (&acc)[TM][TN], int ar0, int br0, int lr,
@@ -450,6 +470,109 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j
                 *c = v;
             }
         }
+}
+
+// Epilogues that read other matrices: the tile goes through LDS (free once
+// the main loop is done) in passes of RP rows, and all 256 threads then walk
+// the staged rows in float4 runs, so every global access is a coalesced
+// 128-bit one and no per-element loads wait inside the accumulator loops
+// (which, in the 256x256 tile, also pushed the accumulators out of
+// registers).
+//   kEpiAdd:    C = alpha * acc + beta * Cin
+//   kEpiSwiglu: dh = alpha * acc; da (+)= dh*u*s*(1 + a*(1-s)), du (+)= dh*a*s
+constexpr int kEpiPlain = 0, kEpiAdd = 1, kEpiSwiglu = 2;
+
+template <int EPI>
+__device__ __forceinline__ void epi_one(const GemmParams& p, const TileJob& j, int64_t row,
+                                        int64_t col, float x) {
+    if constexpr(EPI == kEpiAdd) {
+        float v = j.alpha * x;
+        if(j.beta != 0.0f) v += j.beta * j.Cin[row * j.ldcin + col];
+        j.C[row * j.ldc + col] = v;
+    } else {
+        float ga, gu;
+        pk::swiglu_bwd1(p.sg_a[row * p.sg_lda + col], p.sg_u[row * p.sg_ldu + col], j.alpha * x,
+                        ga, gu);
+        float* da = p.sg_da + row * p.sg_ldd + col;
+        float* du = p.sg_du + row * p.sg_ldd + col;
+        if(p.sg_flags & PK_ACCUM) ga = pk::add_nc(*da, ga);
+        if(p.sg_flags & PK_ACCUM2) gu = pk::add_nc(*du, gu);
+        *da = ga;
+        *du = gu;
+    }
+}
+
+template <int EPI>
+__device__ __forceinline__ void epi_four(const GemmParams& p, const TileJob& j, int64_t row,
+                                         int64_t col, f32x4 x) {
+    if constexpr(EPI == kEpiAdd) {
+        f32x4 v;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) v[e] = j.alpha * x[e];
+        if(j.beta != 0.0f) {
+            const f32x4 c = *reinterpret_cast<const f32x4*>(j.Cin + row * j.ldcin + col);
+#pragma unroll
+            for(int e = 0; e < 4; ++e) v[e] += j.beta * c[e];
+        }
+        *reinterpret_cast<f32x4*>(j.C + row * j.ldc + col) = v;
+    } else {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(p.sg_a + row * p.sg_lda + col);
+        const f32x4 u = *reinterpret_cast<const f32x4*>(p.sg_u + row * p.sg_ldu + col);
+        f32x4* dap = reinterpret_cast<f32x4*>(p.sg_da + row * p.sg_ldd + col);
+        f32x4* dup = reinterpret_cast<f32x4*>(p.sg_du + row * p.sg_ldd + col);
+        f32x4 pa = {0.f, 0.f, 0.f, 0.f}, pu = {0.f, 0.f, 0.f, 0.f};
+        if(p.sg_flags & PK_ACCUM) pa = *dap;
+        if(p.sg_flags & PK_ACCUM2) pu = *dup;
+        f32x4 ga, gu;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            float y, z;
+            pk::swiglu_bwd1(a[e], u[e], j.alpha * x[e], y, z);
+            ga[e] = (p.sg_flags & PK_ACCUM) ? pk::add_nc(pa[e], y) : y;
+            gu[e] = (p.sg_flags & PK_ACCUM2) ? pk::add_nc(pu[e], z) : z;
+        }
+        *dap = ga;
+        *dup = gu;
+    }
+}
+
+template <int EPI, class T>
+__device__ __forceinline__ void staged_epilogue(const GemmParams& p, const TileJob& j,
+                                                const f32x16 (&acc)[T::TM][T::TN], float* lds,
+                                                int lds_floats, int ar0, int br0, int lr, int lh) {
+    constexpr int BN = T::BN, LDE = BN + 4, TM = T::TM, TN = T::TN;
+    // rows per pass: whole 32-row blocks that fit in the operand buffers
+    const int rp = min(T::BM, (lds_floats / LDE) / 32 * 32);
+    __syncthreads();  // every wave is done reading the operand tiles
+    for(int lo = 0; lo < T::BM; lo += rp) {
+#pragma unroll
+        for(int i = 0; i < TM; ++i) {
+            const int rb = ar0 + i * 32;
+            if(rb < lo || rb >= lo + rp) continue;
+#pragma unroll
+            for(int jj = 0; jj < TN; ++jj)
+#pragma unroll
+                for(int r = 0; r < 16; ++r)
+                    lds[(rb - lo + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDE + br0 + jj * 32 + lr] =
+                        acc[i][jj][r];
+        }
+        __syncthreads();
+        const int rows = min(rp, T::BM - lo);
+        for(int idx = threadIdx.x; idx < rows * (BN / 4); idx += NT) {
+            const int rr = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+            const int64_t row = j.row0 + lo + rr, col = j.col0 + c;
+            const f32x4 x = *reinterpret_cast<const f32x4*>(lds + rr * LDE + c);
+            if(row >= p.M) continue;
+            if(p.epi_vec && col + 3 < p.N) {
+                epi_four<EPI>(p, j, row, col, x);
+            } else {
+#pragma unroll
+                for(int e = 0; e < 4; ++e)
+                    if(col + e < p.N) epi_one<EPI>(p, j, row, col + e, x[e]);
+            }
+        }
+        __syncthreads();
+    }
 }
 
 // prologue shared by both kernels: slice 0 into LDS buffer 0, slice 1 into
@@ -478,7 +601,7 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
         load_item<BKF, EDGE, T::BN>(j.B, p.ldb, j.col0, k1, p.N, j.kend, e, &rb[e * OB::ITEM_F4]);
 }
 
-template <bool TA, bool TB, int EDGE, class T>
+template <bool TA, bool TB, int EDGE, class T, int EPI>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
     // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
@@ -562,7 +685,14 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+    if constexpr(EPI == kEpiPlain)
+        store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+    else if constexpr(sizeof(ldsA) >= sizeof(ldsB))
+        staged_epilogue<EPI, T>(p, job, acc, &ldsA[0][0], (int)(sizeof(ldsA) / sizeof(float)), ar0,
+                                br0, lr, lh);
+    else
+        staged_epilogue<EPI, T>(p, job, acc, &ldsB[0][0], (int)(sizeof(ldsB) / sizeof(float)), ar0,
+                                br0, lr, lh);
 }
 
 // The same product with bf16 multiplies: op(A) and op(B) are rounded to bf16
@@ -591,7 +721,7 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 }
 
-template <bool TA, bool TB, int EDGE, class T, bool SPLIT>
+template <bool TA, bool TB, int EDGE, class T, bool SPLIT, int EPI>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
     constexpr bool AK = !TA, BKF = TB;
@@ -677,23 +807,31 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+    if constexpr(EPI == kEpiPlain)
+        store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+    else if constexpr(sizeof(ldsA) >= sizeof(ldsB))
+        staged_epilogue<EPI, T>(p, job, acc, reinterpret_cast<float*>(&ldsA[0][0]),
+                                (int)(sizeof(ldsA) / sizeof(float)), ar0, br0, lr, lh);
+    else
+        staged_epilogue<EPI, T>(p, job, acc, reinterpret_cast<float*>(&ldsB[0][0]),
+                                (int)(sizeof(ldsB) / sizeof(float)), ar0, br0, lr, lh);
 }
 
-// C = alpha * sum_s ws[s] + beta * C, planes summed in order s = 0, 1, ...
+// C = alpha * sum_s ws[s] + beta * Cin, planes summed in order s = 0, 1, ...
 __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restrict__ ws,
-                              float alpha, float beta, float* __restrict__ C, int64_t ldc) {
+                              float alpha, float beta, const float* Cin, int64_t ldcin, float* C,
+                              int64_t ldc) {
     const int64_t plane = M * N;
-    if((N & 3) == 0 && (ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+    if((N & 3) == 0 && (ldc & 3) == 0 && (ldcin & 3) == 0 &&
+       (reinterpret_cast<uintptr_t>(C) & 15) == 0 && (reinterpret_cast<uintptr_t>(Cin) & 15) == 0) {
         const int64_t n4 = plane / 4, N4 = N / 4;
         for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
             i += (int64_t)gridDim.x * blockDim.x) {
             f32x4 acc = reinterpret_cast<const f32x4*>(ws)[i];
             for(int s = 1; s < S; ++s) acc += reinterpret_cast<const f32x4*>(ws + s * plane)[i];
-            f32x4* c = reinterpret_cast<f32x4*>(C + (i / N4) * ldc) + (i % N4);
             f32x4 v = alpha * acc;
-            if(beta != 0.0f) v += beta * *c;
-            *c = v;
+            if(beta != 0.0f) v += beta * reinterpret_cast<const f32x4*>(Cin + (i / N4) * ldcin)[i % N4];
+            reinterpret_cast<f32x4*>(C + (i / N4) * ldc)[i % N4] = v;
         }
         return;
     }
@@ -701,10 +839,9 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
         i += (int64_t)gridDim.x * blockDim.x) {
         float acc = ws[i];
         for(int s = 1; s < S; ++s) acc += ws[s * plane + i];
-        float* c = C + (i / N) * ldc + (i % N);
         float v = alpha * acc;
-        if(beta != 0.0f) v += beta * *c;
-        *c = v;
+        if(beta != 0.0f) v += beta * Cin[(i / N) * ldcin + (i % N)];
+        C[(i / N) * ldc + (i % N)] = v;
     }
 }
 
@@ -802,14 +939,28 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
 
 enum Precision { kFp32 = 0, kBf16 = 1, kBf16x3 = 2 };
 
+template <bool TA, bool TB, class T, int EDGE, int EPI>
+void launch_epi(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
+    if(prec == kBf16)
+        gemm_bf16_kernel<TA, TB, EDGE, T, false, EPI><<<grid, NT, 0, st>>>(gp);
+    else if(prec == kBf16x3)
+        gemm_bf16_kernel<TA, TB, EDGE, T, true, EPI><<<grid, NT, 0, st>>>(gp);
+    else
+        gemm_f32_kernel<TA, TB, EDGE, T, EPI><<<grid, NT, 0, st>>>(gp);
+}
+
+// The staged epilogues are instantiated only where they are used: the
+// residual add for 'N','N' (x + a.W), the SwiGLU backward for 'N','T'
+// (dY . W2^T); gemm_impl refuses other combinations.
 template <bool TA, bool TB, class T, int EDGE>
 void launch_kernel(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
-    if(prec == kBf16)
-        gemm_bf16_kernel<TA, TB, EDGE, T, false><<<grid, NT, 0, st>>>(gp);
-    else if(prec == kBf16x3)
-        gemm_bf16_kernel<TA, TB, EDGE, T, true><<<grid, NT, 0, st>>>(gp);
-    else
-        gemm_f32_kernel<TA, TB, EDGE, T><<<grid, NT, 0, st>>>(gp);
+    if constexpr(!TA && TB) {
+        if(gp.sg_a) return launch_epi<TA, TB, T, EDGE, kEpiSwiglu>(gp, grid, prec, st);
+    }
+    if constexpr(!TA && !TB) {
+        if(gp.Cin) return launch_epi<TA, TB, T, EDGE, kEpiAdd>(gp, grid, prec, st);
+    }
+    launch_epi<TA, TB, T, EDGE, kEpiPlain>(gp, grid, prec, st);
 }
 
 template <bool TA, bool TB, class T>
@@ -838,11 +989,23 @@ int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, int pre
     }
 }
 
+// what a product's tiles write besides alpha * op(A) . op(B): the beta term's
+// source when it is not C, or the SwiGLU-backward epilogue
+struct Epilogue {
+    const float* Cin = nullptr;
+    int64_t ldcin = 0;
+    const float *sg_a = nullptr, *sg_u = nullptr;
+    float *sg_da = nullptr, *sg_du = nullptr;
+    int64_t sg_lda = 0, sg_ldu = 0, sg_ldd = 0;
+    int sg_flags = 0;
+};
+
 int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
               int64_t lda, int64_t sA_outer, int64_t sA_inner, const float* B, int64_t ldb,
               int64_t sB_outer, int64_t sB_inner, float beta, float* C, int64_t ldc,
               int64_t sC_outer, int64_t sC_inner, int64_t batch, int64_t inner_count, int causal,
-              float* ws, size_t ws_bytes, int prec, pk_stream_t stream) {
+              float* ws, size_t ws_bytes, int prec, pk_stream_t stream,
+              const Epilogue& epi = Epilogue()) {
     const bool TA = ta == 'T' || ta == 't', TB = tb == 'T' || tb == 't';
     if(!(TA || ta == 'N' || ta == 'n') || !(TB || tb == 'N' || tb == 'n'))
         return pk::fail("pk_gemm_f32: transpose flags must be 'N' or 'T' (got '%c','%c')", ta, tb);
@@ -852,14 +1015,16 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     if(causal < 0 || causal > 3) return pk::fail("pk_gemm_f32: causal mode %d not in 0..3", causal);
     if(inner_count < 1) return pk::fail("pk_gemm_f32: inner_count must be >= 1");
     if(M == 0 || N == 0 || batch == 0) return PK_OK;
-    if(!C) return pk::fail("pk_gemm_f32: C is NULL");
+    const bool swiglu = epi.sg_a != nullptr;
+    if(!C && !swiglu) return pk::fail("pk_gemm_f32: C is NULL");
     if(K > 0 && (!A || !B)) return pk::fail("pk_gemm_f32: A or B is NULL");
     const int64_t a_cols = TA ? M : K, b_cols = TB ? K : N;
     if(K > 0 && (lda < a_cols || ldb < b_cols))
         return pk::fail("pk_gemm_f32: leading dimension too small (lda=%lld needs >= %lld, "
                         "ldb=%lld needs >= %lld)",
                         (long long)lda, (long long)a_cols, (long long)ldb, (long long)b_cols);
-    if(ldc < N) return pk::fail("pk_gemm_f32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
+    if(!swiglu && ldc < N)
+        return pk::fail("pk_gemm_f32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
     if(batch > 65535) return pk::fail("pk_gemm_f32: problem too large for one launch");
 
     GemmParams gp;
@@ -882,11 +1047,27 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     gp.alpha = alpha;
     gp.beta = beta;
     gp.causal = causal;
+    // a beta source that is C itself is the plain accumulate
+    const bool own_c = epi.Cin == nullptr || (epi.Cin == C && epi.ldcin == ldc) || beta == 0.0f;
+    if(!own_c && (TA || TB))
+        return pk::fail("pk_gemm_add_f32: a separate X is built for the ('N','N') layout only");
+    if(swiglu && (TA || !TB))
+        return pk::fail("pk_gemm_swiglu_bwd_f32: only the ('N','T') layout (dY . W^T) is built");
+    gp.Cin = own_c ? nullptr : epi.Cin;
+    gp.ldcin = own_c ? 0 : epi.ldcin;
+    gp.sg_a = epi.sg_a;
+    gp.sg_u = epi.sg_u;
+    gp.sg_da = epi.sg_da;
+    gp.sg_du = epi.sg_du;
+    gp.sg_lda = epi.sg_lda;
+    gp.sg_ldu = epi.sg_ldu;
+    gp.sg_ldd = epi.sg_ldd;
+    gp.sg_flags = epi.sg_flags;
     hipStream_t st = pk::as_stream(stream);
     gp.splits = 1;
     gp.kchunk = K;
     gp.ws = nullptr;
-    if(batch == 1 && causal == 0 && ws && K > 0) {
+    if(batch == 1 && causal == 0 && ws && K > 0 && !swiglu) {
         int64_t kchunk;
         const int S = choose_splits(M, N, K, &kchunk);
         if(S > 1 && ws_bytes >= (size_t)S * (size_t)M * (size_t)N * sizeof(float)) {
@@ -895,6 +1076,12 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
             gp.ws = ws;
         }
     }
+    auto v4 = [](const void* q, int64_t ld) {
+        return q == nullptr || (pk::aligned16(q) && ld % 4 == 0);
+    };
+    gp.epi_vec = v4(C, ldc) && v4(gp.Cin, gp.ldcin) && v4(gp.sg_a, gp.sg_lda) &&
+                 v4(gp.sg_u, gp.sg_ldu) && v4(gp.sg_da, gp.sg_ldd) && v4(gp.sg_du, gp.sg_ldd) &&
+                 (gp.splits == 1 || v4(gp.ws, N));
     // split products keep 128x128 tiles (the split count is sized for them);
     // causal products keep 128-row tiles (the attention chain's diagonal logic
     // is exercised at that size)
@@ -926,8 +1113,8 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     else
         rc = launch<true, true>(gp, batch, edge, kind, prec, st);
     if(rc || gp.splits == 1) return rc;
-    splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(M, N, gp.splits, gp.ws, alpha,
-                                                                  beta, C, ldc);
+    splitk_reduce<<<pk::grid_for(M * N / 4 + 1, NT), NT, 0, st>>>(
+        M, N, gp.splits, gp.ws, alpha, beta, gp.Cin ? gp.Cin : C, gp.Cin ? gp.ldcin : ldc, C, ldc);
     return pk::launch_status("pk_gemm_ex_f32 (split-K reduction)");
 }
 
@@ -994,6 +1181,63 @@ extern "C" int pk_gemm_ex_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int
                                      void* workspace, size_t workspace_bytes, pk_stream_t stream) {
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
                      0, static_cast<float*>(workspace), workspace_bytes, kBf16x3, stream);
+}
+
+// ---- fused epilogues -------------------------------------------------------
+namespace {
+int prec_of(int precision, const char* who) {
+    if(precision < kFp32 || precision > kBf16x3)
+        return pk::fail("%s: precision %d is not 0 (fp32), 1 (bf16) or 2 (bf16x3)", who, precision);
+    return precision;
+}
+}  // namespace
+
+extern "C" int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                               const float* A, int64_t lda, const float* B, int64_t ldb,
+                               float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                               int precision, void* workspace, size_t workspace_bytes,
+                               pk_stream_t stream) {
+    const int prec = prec_of(precision, "pk_gemm_add_f32");
+    if(prec < 0) return PK_EINVAL;
+    Epilogue e;
+    if(beta != 0.0f && M > 0 && N > 0) {
+        if(!X) return pk::fail("pk_gemm_add_f32: X is NULL");
+        if(ldx < N) return pk::fail("pk_gemm_add_f32: ldx=%lld < N=%lld", (long long)ldx,
+                                    (long long)N);
+        e.Cin = X;
+        e.ldcin = ldx;
+    }
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, static_cast<float*>(workspace), workspace_bytes, prec, stream, e);
+}
+
+extern "C" int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K,
+                                      float alpha, const float* A, int64_t lda, const float* B,
+                                      int64_t ldb, const float* gate, int64_t ldg, const float* up,
+                                      int64_t ldu, float* dgate, float* dup, int64_t ldd, int flags,
+                                      int precision, pk_stream_t stream) {
+    const int prec = prec_of(precision, "pk_gemm_swiglu_bwd_f32");
+    if(prec < 0) return PK_EINVAL;
+    if(M > 0 && N > 0) {
+        if(!gate || !up || !dgate || !dup)
+            return pk::fail("pk_gemm_swiglu_bwd_f32: NULL gate, up or gradient pointer");
+        if(ldg < N || ldu < N || ldd < N)
+            return pk::fail("pk_gemm_swiglu_bwd_f32: a row stride is below N=%lld", (long long)N);
+        if(dgate == dup) return pk::fail("pk_gemm_swiglu_bwd_f32: dgate and dup must differ");
+    }
+    const bool nt = (ta == 'N' || ta == 'n') && (tb == 'T' || tb == 't');
+    if(!nt) return pk::fail("pk_gemm_swiglu_bwd_f32: only the ('N','T') layout (dY . W^T) is built");
+    Epilogue e;
+    e.sg_a = gate;
+    e.sg_u = up;
+    e.sg_da = dgate;
+    e.sg_du = dup;
+    e.sg_lda = ldg;
+    e.sg_ldu = ldu;
+    e.sg_ldd = ldd;
+    e.sg_flags = flags & (PK_ACCUM | PK_ACCUM2);
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, 0.0f, nullptr, N, 0, 0, 1,
+                     1, 0, nullptr, 0, prec, stream, e);
 }
 
 // ---- pk_gemm_noalloc_f32: the split-K GEMM without a caller workspace ------

@@ -81,6 +81,31 @@ __device__ __forceinline__ void st_stream(T* p, T v) {
     __builtin_nontemporal_store(v, p);
 }
 
+// SwiGLU h = silu(a) * u = a * s * u with s = sigmoid(a), and its gradients
+// for an upstream g: dh/da = u * s * (1 + a * (1 - s)), dh/du = a * s.  One
+// definition for the row kernels and the GEMM epilogue that fuses the
+// backward, so both round alike: contraction is off here (and in add_nc, the
+// accumulation of a gradient), so no multiply is fused with an add of the
+// surrounding code, whose shape differs between the two callers.
+__device__ __forceinline__ float swiglu_sigmoid(float a) {
+#pragma clang fp contract(off)
+    return 1.0f / (1.0f + expf(-a));
+}
+__device__ __forceinline__ float swiglu_fwd1(float a, float u) {
+#pragma clang fp contract(off)
+    return a * swiglu_sigmoid(a) * u;
+}
+__device__ __forceinline__ void swiglu_bwd1(float a, float u, float g, float& ga, float& gu) {
+#pragma clang fp contract(off)
+    const float s = swiglu_sigmoid(a);
+    ga = g * u * s * (1.0f + a * (1.0f - s));
+    gu = g * a * s;
+}
+__device__ __forceinline__ float add_nc(float x, float y) {
+#pragma clang fp contract(off)
+    return x + y;
+}
+
 // grid for a streaming kernel that gives each thread one element per pass
 inline unsigned grid_stream(int64_t work_items, int threads) {
     int64_t g = (work_items + threads - 1) / threads;

@@ -539,7 +539,6 @@ int64_t rms_parts(int64_t R) {
 }
 
 // ================================================================== SwiGLU
-__device__ __forceinline__ float sigmoidf_(float a) { return 1.0f / (1.0f + expf(-a)); }
 
 __global__ void swiglu_fwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4* __restrict__ u,
                             f32x4* __restrict__ h) {
@@ -548,7 +547,7 @@ __global__ void swiglu_fwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
         const f32x4 av = pk::ld_stream(a + i), uv = pk::ld_stream(u + i);
         f32x4 o;
 #pragma unroll
-        for(int e = 0; e < 4; ++e) o[e] = av[e] * sigmoidf_(av[e]) * uv[e];
+        for(int e = 0; e < 4; ++e) o[e] = pk::swiglu_fwd1(av[e], uv[e]);
         pk::st_stream(h + i, o);
     }
 }
@@ -561,7 +560,7 @@ __global__ void swiglu_fwd_any(int64_t R, int64_t F, const float* __restrict__ a
         i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / F, c = i % F;
         const float av = a[r * lda + c];
-        h[r * ldh + c] = av * sigmoidf_(av) * u[r * ldu + c];
+        h[r * ldh + c] = pk::swiglu_fwd1(av, u[r * ldu + c]);
     }
 }
 
@@ -574,12 +573,22 @@ __global__ void swiglu_bwd4(int64_t n4, const f32x4* __restrict__ a, const f32x4
         f32x4 ga, gu;
 #pragma unroll
         for(int e = 0; e < 4; ++e) {
-            const float s = sigmoidf_(av[e]);
-            ga[e] = g[e] * uv[e] * s * (1.0f + av[e] * (1.0f - s));
-            gu[e] = g[e] * av[e] * s;
+            float x, y;
+            pk::swiglu_bwd1(av[e], uv[e], g[e], x, y);
+            ga[e] = x;
+            gu[e] = y;
         }
-        if(flags & 4) pk::st_stream(da + i, (flags & PK_ACCUM) ? da[i] + ga : ga);
-        if(flags & 8) pk::st_stream(du + i, (flags & PK_ACCUM2) ? du[i] + gu : gu);
+        if(flags & (PK_ACCUM | PK_ACCUM2)) {
+            const f32x4 pa = (flags & PK_ACCUM) ? da[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 pu = (flags & PK_ACCUM2) ? du[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for(int e = 0; e < 4; ++e) {
+                if(flags & PK_ACCUM) ga[e] = pk::add_nc(pa[e], ga[e]);
+                if(flags & PK_ACCUM2) gu[e] = pk::add_nc(pu[e], gu[e]);
+            }
+        }
+        if(flags & 4) pk::st_stream(da + i, ga);
+        if(flags & 8) pk::st_stream(du + i, gu);
     }
 }
 
@@ -596,7 +605,7 @@ __global__ void swiglu_fwd_rows4(int64_t R, int64_t F4, const float* __restrict_
         const f32x4 uv = pk::ld_stream(reinterpret_cast<const f32x4*>(u + r * ldu) + c);
         f32x4 o;
 #pragma unroll
-        for(int e = 0; e < 4; ++e) o[e] = av[e] * sigmoidf_(av[e]) * uv[e];
+        for(int e = 0; e < 4; ++e) o[e] = pk::swiglu_fwd1(av[e], uv[e]);
         pk::st_stream(reinterpret_cast<f32x4*>(h + r * ldh) + c, o);
     }
 }
@@ -614,17 +623,28 @@ __global__ void swiglu_bwd_rows4(int64_t R, int64_t F4, const float* __restrict_
         f32x4 ga, gu;
 #pragma unroll
         for(int e = 0; e < 4; ++e) {
-            const float s = sigmoidf_(av[e]);
-            ga[e] = g[e] * uv[e] * s * (1.0f + av[e] * (1.0f - s));
-            gu[e] = g[e] * av[e] * s;
+            float x, y;
+            pk::swiglu_bwd1(av[e], uv[e], g[e], x, y);
+            ga[e] = x;
+            gu[e] = y;
         }
         if(flags & 4) {
             f32x4* p = reinterpret_cast<f32x4*>(da + r * ldd) + c;
-            pk::st_stream(p, (flags & PK_ACCUM) ? *p + ga : ga);
+            if(flags & PK_ACCUM) {
+                const f32x4 old = *p;
+#pragma unroll
+                for(int e = 0; e < 4; ++e) ga[e] = pk::add_nc(old[e], ga[e]);
+            }
+            pk::st_stream(p, ga);
         }
         if(flags & 8) {
             f32x4* p = reinterpret_cast<f32x4*>(du + r * ldd) + c;
-            pk::st_stream(p, (flags & PK_ACCUM2) ? *p + gu : gu);
+            if(flags & PK_ACCUM2) {
+                const f32x4 old = *p;
+#pragma unroll
+                for(int e = 0; e < 4; ++e) gu[e] = pk::add_nc(old[e], gu[e]);
+            }
+            pk::st_stream(p, gu);
         }
     }
 }
@@ -643,12 +663,11 @@ __global__ void swiglu_bwd_any(int64_t R, int64_t F, const float* __restrict__ a
         i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / F, c = i % F;
         const float av = a[r * lda + c], uv = u[r * ldu + c], g = dh[r * ldh + c];
-        const float s = sigmoidf_(av);
-        const float ga = g * uv * s * (1.0f + av * (1.0f - s));
-        const float gu = g * av * s;
+        float ga, gu;
+        pk::swiglu_bwd1(av, uv, g, ga, gu);
         const int64_t o = r * ldd + c;
-        if(flags & 4) da[o] = (flags & PK_ACCUM) ? da[o] + ga : ga;
-        if(flags & 8) du[o] = (flags & PK_ACCUM2) ? du[o] + gu : gu;
+        if(flags & 4) da[o] = (flags & PK_ACCUM) ? pk::add_nc(da[o], ga) : ga;
+        if(flags & 8) du[o] = (flags & PK_ACCUM2) ? pk::add_nc(du[o], gu) : gu;
     }
 }
 

@@ -109,20 +109,15 @@ struct PicoTensor* pico_gpt_loss(struct PicoGPT* m, const int32_t* tokens,
         struct PicoTensor* a =
             pico_attention_causal(qkv3[0], qkv3[1], qkv3[2], c->batch, c->n_heads);
         if(!a) return NULL;
-        struct PicoTensor* o = pico_matmul(a, L->wo);
-        if(!o) return NULL;
-        x = pico_add(x, o);
+        x = pico_matmul_add(a, L->wo, x); /* x + a.Wo in the product's epilogue */
         if(!x) return NULL;
         h = pico_rmsnorm(x, L->g_ffn, eps);
         if(!h) return NULL;
         struct PicoTensor* gu = pico_matmul(h, L->w13);
         struct PicoTensor* gu2[2];
         if(!gu || pico_split_cols(gu, 2, gu2)) return NULL;
-        struct PicoTensor* act = pico_swiglu(gu2[0], gu2[1]);
-        if(!act) return NULL;
-        struct PicoTensor* down = pico_matmul(act, L->w2);
-        if(!down) return NULL;
-        x = pico_add(x, down);
+        /* x + swiglu(gate, up).W2; the backward's dY.W2^T writes d(gate), d(up) */
+        x = pico_swiglu_matmul_add(gu2[0], gu2[1], L->w2, x);
     }
     if(!x) return NULL;
     struct PicoTensor* hf = pico_rmsnorm(x, m->g_final, eps);

@@ -200,23 +200,24 @@ int pico_get_matmul_precision(void) { return g_matmul_precision; }
 /* products with too few output tiles (weight gradients) split K through a
  * workspace; see pk_gemm_ex_f32.  On the side stream (side != 0) the product
  * uses the side stream's own workspace. */
-static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
-                   char tc, int64_t ldc, int flags, pk_stream_t st, int side) {
-    const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+static int gemm_add_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
+                       char tc, int64_t ldc, float beta, const float* X, int64_t ldx,
+                       pk_stream_t st, int side) {
     size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
     void* ws = ws_bytes ? (side ? pkh_side_workspace(ws_bytes) : pkh_workspace(ws_bytes)) : NULL;
     if(!ws) ws_bytes = 0;
-    int (*gemm)(char, char, int64_t, int64_t, int64_t, float, const float*, int64_t,
-                const float*, int64_t, float, float*, int64_t, void*, size_t, pk_stream_t) =
-        g_matmul_precision == PICO_MATMUL_BF16     ? pk_gemm_ex_bf16_f32
-        : g_matmul_precision == PICO_MATMUL_BF16X3 ? pk_gemm_ex_bf16x3_f32
-                                                   : pk_gemm_ex_f32;
     if(tc == 'N')
-        return gemm(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, C, ldc, ws, ws_bytes,
-                    st);
-    /* C stored transposed: produce C^T [N, M] = B^T . A^T */
-    return gemm(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc, ws,
-                ws_bytes, st);
+        return pk_gemm_add_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, X, ldx, C, ldc,
+                               g_matmul_precision, ws, ws_bytes, st);
+    /* C stored transposed: produce C^T [N, M] = B^T . A^T (X is C itself here) */
+    return pk_gemm_add_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
+                           C, ldc, g_matmul_precision, ws, ws_bytes, st);
+}
+
+static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
+                   char tc, int64_t ldc, int flags, pk_stream_t st, int side) {
+    const float beta = (flags & PK_ACCUM) ? 1.0f : 0.0f;
+    return gemm_add_on(A, B, M, N, K, C, tc, ldc, beta, C, ldc, st, side);
 }
 
 int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
@@ -245,35 +246,38 @@ int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTenso
                       pkh_gemm(va, vb, M, N, K, out->data, 'N', N > 0 ? N : 1, 0));
 }
 
-/* src/autograd.h:96-130: dA += dC . B^T, then dB += A^T . dC.  Each grad is
- * laid out with its tensor's strides, so a transposed view's grad is
- * produced transposed.
+/* The two products of a matmul's backward (src/autograd.h:96-130) for
+ * self = A.B (+ ...) with upstream gradient g [M, N]: the input gradient
+ * (dA (+)= g.B^T, issued by dA_fn) and the weight gradient dB (+)= A^T.g,
+ * each laid out with its tensor's strides, so a transposed view's grad is
+ * produced transposed.  A is given as a matrix view of its data, since a
+ * fused op's A may be a buffer the op saved rather than a graph tensor.
  *
- * When b is a parameter (persistent) and a is not, dB -- a weight gradient,
+ * When B is a parameter (persistent) and A is not, dB -- a weight gradient,
  * read only once the backward is over -- goes to the side stream and runs
  * concurrently with the rest of the backward; the main stream waits for it
- * before it next touches b's grad and at the end of pico_backward.  Writes to
+ * before it next touches B's grad and at the end of pico_backward.  Writes to
  * one grad keep their program order either way, so results are bit for bit
- * those of a single stream. */
-void pico_matmul_backward_gpu(struct PicoTensor* self) {
-    if(pkh_init()) return;
-    struct PicoTensor *a = self->parents[0], *b = self->parents[1];
-    const float* g = pkh_upstream(self);
-    if(!g) return;
-    struct PkMat va, vb;
-    if(matmul_views(a, b, &va, &vb)) return;
-    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+ * those of a single stream.
+ *
+ * Eagerly, dB is forked before dA is issued, so that it runs beside dA
+ * rather than beside the memory-bound kernels that follow dA (config 5: about
+ * 1.3 ms less per step).  A captured graph keeps dA first: replays of the
+ * dB-first order measured slower.  Either way the side stream orders dB's
+ * write after every earlier write to B's grad: main-stream ones through the
+ * fork, side ones by issue order. */
+static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor* b,
+                                 const float* g, int64_t M, int64_t K, int64_t N,
+                                 int (*dA_fn)(void*), void* ctx) {
+    struct PkMat vb;
+    if(pkh_mat_view(b, b->data, &vb)) {
+        pkh_status("pico_matmul_backward", PK_EINVAL);
+        return;
+    }
     struct PkMat dC = {g, 'N', N > 0 ? N : 1};
-    struct PkMat BT = {b->data, flip(vb.t), vb.ld};
-    struct PkMat AT = {a->data, flip(va.t), va.ld};
+    struct PkMat AT = {va.p, flip(va.t), va.ld};
     struct PkNode* nb = pkh_node(b);
-    const int to_side = nb && b->is_persistent && !a->is_persistent && a != b;
-    /* Eagerly, dB is forked before dA is issued, so that it runs beside dA
-     * rather than beside the memory-bound kernels that follow dA (config 5:
-     * about 1.3 ms less per step).  A captured graph keeps dA first: replays
-     * of the dB-first order measured slower.  Either way the side stream
-     * orders dB's write after every earlier write to b's grad: main-stream
-     * ones through the fork, side ones by issue order. */
+    const int to_side = nb && b->is_persistent && !a_param && va.p != b->data;
     const int db_first = to_side && !pkh_capturing();
     pk_stream_t side = db_first ? pkh_side_fork() : NULL;
     int st;
@@ -283,9 +287,7 @@ void pico_matmul_backward_gpu(struct PicoTensor* self) {
         if(pkh_status("pico_matmul_backward", st)) return;
         pkh_grad_mark(b);
     }
-    st = pkh_gemm(dC, BT, M, K, N, a->grad, va.t, va.ld, pkh_grad_flag(a));
-    if(pkh_status("pico_matmul_backward", st)) return;
-    pkh_grad_mark(a);
+    if(dA_fn(ctx)) return;
     if(side) return;
     side = to_side ? pkh_side_fork() : NULL;
     if(side) {
@@ -296,6 +298,36 @@ void pico_matmul_backward_gpu(struct PicoTensor* self) {
     }
     if(pkh_status("pico_matmul_backward", st)) return;
     pkh_grad_mark(b);
+}
+
+/* dA (+)= g . B^T into a tensor's grad (the plain matmul's input gradient) */
+struct DaPlain {
+    struct PicoTensor *a, *b;
+    const float* g;
+    int64_t M, K, N;
+};
+static int da_plain(void* ctx) {
+    struct DaPlain* c = (struct DaPlain*)ctx;
+    struct PkMat va, vb;
+    if(matmul_views(c->a, c->b, &va, &vb)) return PK_EINVAL;
+    struct PkMat dC = {c->g, 'N', c->N > 0 ? c->N : 1};
+    struct PkMat BT = {c->b->data, flip(vb.t), vb.ld};
+    int st = pkh_gemm(dC, BT, c->M, c->K, c->N, c->a->grad, va.t, va.ld, pkh_grad_flag(c->a));
+    if(pkh_status("pico_matmul_backward", st)) return st;
+    pkh_grad_mark(c->a);
+    return 0;
+}
+
+void pico_matmul_backward_gpu(struct PicoTensor* self) {
+    if(pkh_init()) return;
+    struct PicoTensor *a = self->parents[0], *b = self->parents[1];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    struct DaPlain ctx = {a, b, g, M, K, N};
+    matmul_backward_with(va, a->is_persistent || a == b, b, g, M, K, N, da_plain, &ctx);
 }
 
 /* src/ops.c:144-190 (checks in the reference's order) */
@@ -325,6 +357,169 @@ struct PicoTensor* pico_matmul(struct PicoTensor* a, struct PicoTensor* b) {
     if(pico_matmul_gpu(a, b, out)) return NULL;
     struct PicoTensor* ps[2] = {a, b};
     pkh_set_parents(arena, out, 2, ps, pico_matmul_backward_gpu);
+    return out;
+}
+
+/* ----------------------------------------------------------- fused ops
+ * No reference counterpart: pico runs a matmul and the op that consumes it as
+ * two passes over memory.  These produce the same values as the composed ops
+ * (the fused epilogue rounds exactly as the separate kernels do), with one
+ * pass fewer and no intermediate tensor in the graph. */
+
+/* a residual matrix added in the product's epilogue: the output's shape,
+ * contiguous */
+static int residual_ok(const struct PicoTensor* c, int64_t M, int64_t N) {
+    return c->ndim == 2 && c->shape[0] == M && c->shape[1] == N && c->strides[1] == 1 &&
+           (c->strides[0] == N || M <= 1);
+}
+
+/* d(out)/dc = 1: an empty grad takes out's grad by pointer (an alias),
+ * otherwise out's grad is added to it */
+static int residual_backward(struct PicoTensor* self, struct PicoTensor* c, const float* g) {
+    if(same_layout(c, self) && pkh_grad_alias(c, self)) return 0;
+    int st = pk_axpy_f32(c->numel, 1.0f, NULL, g, c->grad, pkh_grad_flag(c), pkh_stream());
+    if(pkh_status("pico_matmul_add_backward", st)) return st;
+    pkh_grad_mark(c);
+    return 0;
+}
+
+static void matmul_add_backward(struct PicoTensor* self) {
+    if(pkh_init()) return;
+    struct PicoTensor *a = self->parents[0], *b = self->parents[1], *c = self->parents[2];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    if(residual_backward(self, c, g)) return;
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    struct DaPlain ctx = {a, b, g, M, K, N};
+    matmul_backward_with(va, a->is_persistent || a == b, b, g, M, K, N, da_plain, &ctx);
+}
+
+/* out = c + a . b in one pass: the product's epilogue adds c (a residual
+ * connection, x + attn.Wo) */
+struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
+                                   struct PicoTensor* c) {
+    if(!a || !b || !c) {
+        PKH_ERR("pico_matmul_add: NULL tensor!\n");
+        return NULL;
+    }
+    if(a->ndim != 2 || b->ndim != 2 || a->shape[1] != b->shape[0]) {
+        PKH_ERR("2d matmul matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->backend != b->backend || a->backend != c->backend) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu("pico_matmul_add", a)) return NULL;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    if(!residual_ok(c, M, N)) {
+        PKH_ERR("pico_matmul_add: the added tensor must be a contiguous [rows(a), cols(b)]!\n");
+        return NULL;
+    }
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return NULL;
+    int64_t shape[2] = {M, N};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    int st = gemm_add_on(va, vb, M, N, K, out->data, 'N', N > 0 ? N : 1, 1.0f, c->data,
+                         c->strides[0], pkh_stream(), 0);
+    if(pkh_status("pico_matmul_add", st)) return NULL;
+    struct PicoTensor* ps[3] = {a, b, c};
+    pkh_set_parents(arena, out, 3, ps, matmul_add_backward);
+    return out;
+}
+
+/* SwiGLU then a product: out = (c +) swiglu(gate, up) . w.  h = silu(gate) *
+ * up is kept in the arena for the weight gradient; the backward never stores
+ * dh: the input-gradient product dY . w^T writes the gate and up gradients
+ * straight from its tiles (pk_gemm_swiglu_bwd_f32). */
+enum { SM_H = 0 };
+enum { SM_LD = 0, SM_RESID = 1 };
+
+struct DaSwiglu {
+    struct PicoTensor *gate, *up, *w;
+    const float* g;
+    int64_t M, F, N, ld;
+};
+static int da_swiglu(void* ctx) {
+    struct DaSwiglu* c = (struct DaSwiglu*)ctx;
+    const int flags = (pkh_grad_flag(c->gate) ? PK_ACCUM : 0) | (pkh_grad_flag(c->up) ? PK_ACCUM2 : 0);
+    /* dh = g [M, N] . w^T, w [F, N] row-major */
+    int st = pk_gemm_swiglu_bwd_f32('N', 'T', c->M, c->F, c->N, 1.0f, c->g, c->N > 0 ? c->N : 1,
+                                    c->w->data, c->w->strides[0], c->gate->data, c->ld,
+                                    c->up->data, c->ld, c->gate->grad, c->up->grad, c->ld, flags,
+                                    g_matmul_precision, pkh_stream());
+    if(pkh_status("pico_swiglu_matmul_add_backward", st)) return st;
+    pkh_grad_mark(c->gate);
+    pkh_grad_mark(c->up);
+    return 0;
+}
+
+static void swiglu_matmul_backward(struct PicoTensor* self) {
+    if(pkh_init()) return;
+    struct PkNode* n = pkh_node(self);
+    struct PicoTensor *gate = self->parents[0], *up = self->parents[1], *w = self->parents[2];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    if(n->ival[SM_RESID] && residual_backward(self, self->parents[3], g)) return;
+    const int64_t M = gate->shape[0], F = gate->shape[1], N = w->shape[1];
+    struct PkMat vh = {(const float*)n->saved[SM_H], 'N', F > 0 ? F : 1};
+    struct DaSwiglu ctx = {gate, up, w, g, M, F, N, n->ival[SM_LD]};
+    matmul_backward_with(vh, 0, w, g, M, F, N, da_swiglu, &ctx);
+}
+
+struct PicoTensor* pico_swiglu_matmul_add(struct PicoTensor* gate, struct PicoTensor* up,
+                                          struct PicoTensor* w, struct PicoTensor* c) {
+    if(!gate || !up || !w) {
+        PKH_ERR("pico_swiglu_matmul_add: NULL tensor!\n");
+        return NULL;
+    }
+    if(gate->backend != up->backend || gate->backend != w->backend ||
+       (c && c->backend != gate->backend)) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu("pico_swiglu_matmul_add", gate)) return NULL;
+    if(gate->ndim != 2 || up->ndim != 2 || gate->shape[0] != up->shape[0] ||
+       gate->shape[1] != up->shape[1] || gate->strides[1] != 1 || up->strides[1] != 1 ||
+       gate->strides[0] != up->strides[0] || gate->strides[0] < gate->shape[1] || gate == up) {
+        PKH_ERR("pico_swiglu_matmul_add: gate and up must be distinct [M, F] tensors with unit "
+                "columns and one row stride!\n");
+        return NULL;
+    }
+    const int64_t M = gate->shape[0], F = gate->shape[1];
+    if(w->ndim != 2 || w->shape[0] != F || w->strides[1] != 1 || w->strides[0] < w->shape[1]) {
+        PKH_ERR("pico_swiglu_matmul_add: w must be a row-contiguous [F, N] tensor!\n");
+        return NULL;
+    }
+    const int64_t N = w->shape[1], ld = gate->strides[0];
+    if(c && !residual_ok(c, M, N)) {
+        PKH_ERR("pico_swiglu_matmul_add: the added tensor must be a contiguous [M, N]!\n");
+        return NULL;
+    }
+    float* h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F > 0 ? M * F : 1));
+    if(!h) return NULL;
+    int64_t shape[2] = {M, N};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    int st = pk_swiglu_fwd_f32(M, F, gate->data, ld, up->data, ld, h, F, pkh_stream());
+    if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;
+    struct PkMat vh = {h, 'N', F > 0 ? F : 1}, vw = {w->data, 'N', w->strides[0]};
+    st = gemm_add_on(vh, vw, M, N, F, out->data, 'N', N > 0 ? N : 1, c ? 1.0f : 0.0f,
+                     c ? c->data : NULL, c ? c->strides[0] : 0, pkh_stream(), 0);
+    if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;
+    struct PkNode* n = pkh_node(out);
+    n->saved[SM_H] = h;
+    n->ival[SM_LD] = ld;
+    n->ival[SM_RESID] = c != NULL;
+    struct PicoTensor* ps[4] = {gate, up, w, c};
+    pkh_set_parents(arena, out, c ? 4 : 3, ps, swiglu_matmul_backward);
     return out;
 }
 

@@ -1,0 +1,220 @@
+"""Fused epilogues: pk_gemm_add_f32 / pk_gemm_swiglu_bwd_f32 (launcher layer)
+and the ops built on them, pico_matmul_add and pico_swiglu_matmul_add.
+
+Each fused path must equal the composition of the kernels it replaces bit for
+bit: the product is accumulated identically, and the epilogue applies the same
+single rounding (c + a.b) or the same SwiGLU-gradient expression the row
+kernels use.  The compositions themselves are pinned against the CPU oracle
+elsewhere; here the composed ops' results are also compared with the oracle
+within 1e-4, so an error shared by both GPU paths would show.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from pico_amd import _lib
+from pico_amd import kernels as kern
+from pico_amd.pico import Pico
+from tests._util import max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def P():
+    return Pico()
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+
+
+# ---------------------------------------------------------------- launchers
+@pytest.mark.parametrize("M,N,K", [(512, 768, 768), (200, 136, 96), (768, 768, 8192),
+                                   (97, 33, 1030)])
+@pytest.mark.parametrize("prec", [0, 1, 2])
+def test_gemm_add_equals_product_then_add(dev, M, N, K, prec):
+    """C = A.B + X with X != C against the product written to C and X added
+    by the elementwise kernel (the split-K reduction carries X when K splits)"""
+    L = _lib.hip_lib()
+    A = _t(O.uniform(M * K, 1).reshape(M, K), dev)
+    B = _t(O.uniform(K * N, 2).reshape(K, N), dev)
+    X = _t(O.uniform(M * N, 3).reshape(M, N), dev)
+    need = L.pk_gemm_workspace_f32(M, N, K)
+    ws = torch.empty(max(need, 4) // 4, device=dev)
+    got = torch.full((M, N), 7.0, device=dev)
+    _lib.check("pk_gemm_add_f32", L.pk_gemm_add_f32(
+        b"N", b"N", M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(), N, 1.0, X.data_ptr(), N,
+        got.data_ptr(), N, prec, ws.data_ptr(), need, None))
+    prod = torch.empty(M, N, device=dev)
+    fn = {0: L.pk_gemm_ex_f32, 1: L.pk_gemm_ex_bf16_f32, 2: L.pk_gemm_ex_bf16x3_f32}[prec]
+    _lib.check("pk_gemm_ex", fn(b"N", b"N", M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(), N, 0.0,
+                                prod.data_ptr(), N, ws.data_ptr(), need, None))
+    ref = torch.empty(M, N, device=dev)
+    kern.binary("add", prod, X, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    if prec == 0:
+        want = O.gemm_ref_f64("N", "N", A.cpu().numpy(), B.cpu().numpy()) + X.cpu().numpy()
+        assert max_rel(got.cpu().numpy(), want) <= 1e-5
+
+
+@pytest.mark.parametrize("M,F,N", [(256, 512, 128), (300, 200, 136), (8192, 2048, 768)])
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
+    L = _lib.hip_lib()
+    ld = 2 * F  # gate and up as the two halves of one [M, 2F] projection
+    gu = _t(O.normal(M * ld, 11).reshape(M, ld), dev)
+    dY = _t(O.normal(M * N, 12).reshape(M, N), dev)
+    W = _t(O.normal(F * N, 13, 0.0, 0.05).reshape(F, N), dev)
+    g0 = _t(O.normal(M * ld, 14).reshape(M, ld), dev)
+    gate, up = gu[:, :F], gu[:, F:]
+    got = g0.clone()
+    _lib.check("pk_gemm_swiglu_bwd_f32", L.pk_gemm_swiglu_bwd_f32(
+        b"N", b"T", M, F, N, 1.0, dY.data_ptr(), N, W.data_ptr(), N, gate.data_ptr(), ld,
+        up.data_ptr(), ld, got.data_ptr(), got.data_ptr() + 4 * F, ld, flags, 0, None))
+    dh = torch.empty(M, F, device=dev)
+    _lib.check("pk_gemm_f32", L.pk_gemm_f32(b"N", b"T", M, F, N, 1.0, dY.data_ptr(), N,
+                                            W.data_ptr(), N, 0.0, dh.data_ptr(), F, None))
+    ref = g0.clone()
+    _lib.check("pk_swiglu_bwd_f32", L.pk_swiglu_bwd_f32(
+        M, F, gate.data_ptr(), ld, up.data_ptr(), ld, dh.data_ptr(), F, ref.data_ptr(),
+        ref.data_ptr() + 4 * F, ld, flags, None))
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    if M <= 300:
+        a, u = gate.cpu().numpy(), up.cpu().numpy()
+        dh_ref = dY.cpu().numpy().astype(np.float64) @ W.cpu().numpy().astype(np.float64).T
+        da, du = O.swiglu_bwd(a, u, dh_ref.astype(np.float32))
+        base = g0.cpu().numpy()
+        want_a = da + (base[:, :F] if flags & 1 else 0)
+        want_u = du + (base[:, F:] if flags & 2 else 0)
+        out = got.cpu().numpy()
+        assert max_rel(out[:, :F], want_a) <= 1e-4
+        assert max_rel(out[:, F:], want_u) <= 1e-4
+
+
+def test_gemm_swiglu_bwd_refuses_other_layouts(dev):
+    L = _lib.hip_lib()
+    x = torch.zeros(64, 64, device=dev)
+    st = L.pk_gemm_swiglu_bwd_f32(b"N", b"N", 64, 64, 64, 1.0, x.data_ptr(), 64, x.data_ptr(), 64,
+                                  x.data_ptr(), 64, x.data_ptr(), 64, x.data_ptr(),
+                                  x.data_ptr() + 4, 64, 0, 0, None)
+    assert st == -1 and b"layout" in L.pk_last_error()
+
+
+# ------------------------------------------------------------------- ops
+def _grads(P, ts):
+    return [P.grad(t).copy() for t in ts]
+
+
+def _run_matmul_add(P, fused, av, bv, cv, seed_grad, b_param):
+    with P.arena(1 << 26):
+        a = P.tensor(list(av.shape), av)
+        b = (P.param if b_param else P.tensor)(list(bv.shape), bv)
+        c = P.tensor(list(cv.shape), cv)
+        out = P.matmul_add(a, b, c) if fused else P.add(c, P.matmul(a, b))
+        loss = P.mul(out, P.tensor(list(seed_grad.shape), seed_grad))
+        P.backward(loss)
+        res = (P.data(out), *_grads(P, [a, b, c]))
+        if b_param:
+            P.free(b)
+        return res
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 48, 40), (512, 768, 768), (37, 100, 65)])
+@pytest.mark.parametrize("b_param", [False, True])
+def test_matmul_add_equals_composition(P, M, K, N, b_param):
+    av = O.uniform(M * K, 21).reshape(M, K)
+    bv = O.uniform(K * N, 22).reshape(K, N)
+    cv = O.uniform(M * N, 23).reshape(M, N)
+    sg = O.uniform(M * N, 24).reshape(M, N)
+    fused = _run_matmul_add(P, True, av, bv, cv, sg, b_param)
+    plain = _run_matmul_add(P, False, av, bv, cv, sg, b_param)
+    for x, y in zip(fused, plain):
+        assert np.array_equal(x, y)
+    # and the values, against the oracle's loops
+    out_ref = O.binary(0, cv, O.matmul_scalar(av, bv))
+    assert max_rel(fused[0], out_ref.ravel()) <= 1e-5
+    dA, dB = O.matmul_backward(av, bv, sg)
+    assert max_rel(fused[1], dA.ravel()) <= 1e-4 and max_rel(fused[2], dB.ravel()) <= 1e-4
+    assert np.array_equal(fused[3], sg.ravel())
+
+
+def _run_swiglu_mm(P, fused, xv, w13v, w2v, cv, seed_grad, split):
+    M, d = xv.shape
+    F = w2v.shape[0]
+    with P.arena(1 << 27):
+        x = P.tensor([M, d], xv)
+        w13 = P.param([d, 2 * F], w13v)
+        w2 = P.param([F, w2v.shape[1]], w2v)
+        c = P.tensor(list(cv.shape), cv) if cv is not None else None
+        if split:
+            gate, up = P.split_cols(P.matmul(x, w13), 2)
+        else:
+            g_ = P.tensor([M, F], (xv @ w13v)[:, :F])
+            u_ = P.tensor([M, F], (xv @ w13v)[:, F:])
+            gate, up = g_, u_
+        if fused:
+            out = P.swiglu_matmul_add(gate, up, w2, c)
+        else:
+            out = P.matmul(P.swiglu(gate, up), w2)
+            if c is not None:
+                out = P.add(c, out)
+        P.backward(P.mul(out, P.tensor(list(seed_grad.shape), seed_grad)))
+        ts = [x, w13, w2] + ([c] if c is not None else []) + ([] if split else [gate, up])
+        res = (P.data(out), *_grads(P, ts))
+        P.free(w13)
+        P.free(w2)
+        return res
+
+
+@pytest.mark.parametrize("M,d,F,N", [(128, 64, 160, 64), (300, 96, 200, 72), (1024, 768, 2048, 768)])
+@pytest.mark.parametrize("resid", [False, True])
+@pytest.mark.parametrize("split", [True, False])
+def test_swiglu_matmul_add_equals_composition(P, M, d, F, N, resid, split):
+    xv = O.normal(M * d, 31).reshape(M, d)
+    w13v = O.normal(d * 2 * F, 32, 0.0, 0.05).reshape(d, 2 * F)
+    w2v = O.normal(F * N, 33, 0.0, 0.05).reshape(F, N)
+    cv = O.normal(M * N, 34).reshape(M, N) if resid else None
+    sg = O.normal(M * N, 35).reshape(M, N)
+    fused = _run_swiglu_mm(P, True, xv, w13v, w2v, cv, sg, split)
+    plain = _run_swiglu_mm(P, False, xv, w13v, w2v, cv, sg, split)
+    assert len(fused) == len(plain)
+    for i, (x, y) in enumerate(zip(fused, plain)):
+        assert np.array_equal(x, y), i
+
+
+def test_swiglu_matmul_add_values_against_oracle(P):
+    M, F, N = 96, 160, 80
+    gv = O.normal(M * F, 41).reshape(M, F)
+    uv = O.normal(M * F, 42).reshape(M, F)
+    wv = O.normal(F * N, 43, 0.0, 0.1).reshape(F, N)
+    cv = O.normal(M * N, 44).reshape(M, N)
+    sg = O.normal(M * N, 45).reshape(M, N)
+    with P.arena(1 << 24):
+        gate, up = P.tensor([M, F], gv), P.tensor([M, F], uv)
+        w, c = P.tensor([F, N], wv), P.tensor([M, N], cv)
+        out = P.swiglu_matmul_add(gate, up, w, c)
+        P.backward(P.mul(out, P.tensor([M, N], sg)))
+        got = [P.data(out), P.grad(gate), P.grad(up), P.grad(w), P.grad(c)]
+    h = O.swiglu_fwd(gv, uv)
+    want_out = O.binary(0, cv, O.matmul_scalar(h, wv))
+    dh, dw = O.matmul_backward(h, wv, sg)
+    da, du = O.swiglu_bwd(gv, uv, dh)
+    for g, w_ in zip(got, [want_out, da, du, dw, sg]):
+        assert max_rel(g, w_.ravel()) <= 1e-4
+
+
+def test_fused_ops_refuse_bad_shapes(P):
+    with P.arena(1 << 20):
+        a = P.tensor([4, 3], np.ones(12))
+        b = P.tensor([3, 5], np.ones(15))
+        bad = P.tensor([4, 6], np.ones(24))
+        assert not P.lib.pico_matmul_add(a, b, bad)
+        g = P.tensor([4, 3], np.ones(12))
+        assert not P.lib.pico_swiglu_matmul_add(g, g, b, None)  # gate == up
+        assert not P.lib.pico_swiglu_matmul_add(g, a, P.tensor([4, 5], np.ones(20)), None)
