@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 MFMA_FP32_PEAK = 157.3e12
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 matrix peak (no sparsity)
+MFMA_FP8_PEAK = 5.0e15  # dense fp8 matrix peak (no sparsity)
 HBM_PEAK = 8.0e12
 
 
@@ -468,7 +469,8 @@ def train_section(name, steps, warmup, precision=0):
     ms = wall * 1e3 / steps
     # bf16x3: three bf16 matrix instructions per fp32 product
     peak, peak_name = {1: (MFMA_BF16_PEAK, "bf16 2.5 PFLOP/s"),
-                       2: (MFMA_BF16_PEAK / 3, "bf16x3: 2.5 PFLOP/s / 3")}.get(
+                       2: (MFMA_BF16_PEAK / 3, "bf16x3: 2.5 PFLOP/s / 3"),
+                       3: (MFMA_FP8_PEAK, "fp8 5.0 PFLOP/s")}.get(
         precision, (MFMA_FP32_PEAK, "fp32 157.3 TFLOP/s"))
     return {"tokens_per_s": round(n * steps / wall, 1), "ms_per_step": round(ms, 3),
             "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
@@ -543,7 +545,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=4096)
-    ap.add_argument("--sections", default="train,sweep,bf16,attn,rows,cpu")
+    ap.add_argument("--sections", default="train,sweep,bf16,fp8,attn,rows,cpu")
     ap.add_argument("--train-steps", type=int, default=50)
     ap.add_argument("--variant-steps", type=int, default=10)
     ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
@@ -628,6 +630,16 @@ def main():
             "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
                     "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "
                     "fp32; not the headline, which is fp32"}
+    if "fp8" in sections:
+        # e4m3 operands (clamped to +-448, nearest even), fp32 accumulation and
+        # tensors: far outside the fp32 parity contract, for experiments
+        line["fp8"] = {
+            "sweep": sweep_section(torch, K, [2048, 4096, 8192], K.gemm_fp8),
+            "train": {name: train_section(name, args.variant_steps, 3, precision=3)
+                      for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
+            "note": "pico_set_matmul_precision(PICO_MATMUL_FP8): matmul products on the fp8 "
+                    "matrix cores from fp32 tensors rounded on the way to LDS, attention fp32; "
+                    "not the headline, which is fp32"}
     if "attn" in sections:
         line["attention"] = attn_section(torch, K)
     if "rows" in sections:

@@ -297,11 +297,17 @@ void pico_gpu_clear_error(void);
  * attention node's backward uses the precision its forward ran in.
  * PICO_MATMUL_BF16X3: pico_matmul's products and their gradients take three
  * bf16 products per fp32 one (pk_gemm_bf16x3_f32): within about 1e-5 of
- * fp32, inside the 1e-4 parity bound; attention stays fp32.  Returns 0, or
- * nonzero for an unknown value. */
+ * fp32, inside the 1e-4 parity bound; attention stays fp32.
+ * PICO_MATMUL_FP8: pico_matmul's products and their gradients round both
+ * operands to e4m3 (OCP FP8 E4M3, clamped to +-448, nearest even) and multiply
+ * on the fp8 matrix cores, accumulating in fp32 (pk_gemm_ex_fp8_f32);
+ * attention stays fp32.  Relative error of order 2^-4 per operand: far
+ * outside the fp32 parity contract, for experiments.  Returns 0, or nonzero
+ * for an unknown value. */
 #define PICO_MATMUL_FP32 0
 #define PICO_MATMUL_BF16 1
 #define PICO_MATMUL_BF16X3 2
+#define PICO_MATMUL_FP8 3
 int pico_set_matmul_precision(int precision);
 int pico_get_matmul_precision(void);
 

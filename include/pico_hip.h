@@ -82,10 +82,26 @@ int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float
                         const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                         float* C, int64_t ldc, pk_stream_t stream);
 
+/* The same products with fp8 multiplies (no reference counterpart): op(A)
+ * and op(B) are clamped to +-448 and rounded to e4m3 (OCP FP8 E4M3: bias 7, 3
+ * mantissa bits, nearest even; NaN stays NaN) on their way to LDS and
+ * multiplied on the fp8 matrix cores (v_mfma_f32_32x32x16_fp8_fp8),
+ * accumulating in fp32.  A product of two e4m3 values is exact in fp32, so
+ * the result equals the fp32 product of the rounded operands up to fp32
+ * summation error.  C and the workspace contract are as in pk_gemm_f32 /
+ * pk_gemm_ex_f32. */
+int pk_gemm_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                    const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                    float* C, int64_t ldc, pk_stream_t stream);
+int pk_gemm_ex_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                       const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                       float* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                       pk_stream_t stream);
+
 /* Products with a fused epilogue (no reference counterpart: pico runs a matmul
  * and the op that consumes it as two passes over memory).  precision selects
  * the multiplies: 0 fp32 (as pk_gemm_ex_f32), 1 bf16 (pk_gemm_ex_bf16_f32),
- * 2 three bf16 products (pk_gemm_ex_bf16x3_f32).
+ * 2 three bf16 products (pk_gemm_ex_bf16x3_f32), 3 fp8 (pk_gemm_ex_fp8_f32).
  * pk_gemm_add_f32: C = alpha * op(A).op(B) + beta * X, X [M,N] with row stride
  *   ldx (X == C with ldx == ldc is pk_gemm_ex_f32's accumulate); a residual
  *   connection x + a.W in one pass.  Same workspace contract as pk_gemm_ex_f32.
@@ -100,12 +116,25 @@ int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float
 int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                     const float* X, int64_t ldx, float* C, int64_t ldc, int precision,
-                    void* workspace, size_t workspace_bytes, pk_stream_t stream);
+                    const float* fp8_scales, void* workspace, size_t workspace_bytes,
+                    pk_stream_t stream);
 int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                            const float* A, int64_t lda, const float* B, int64_t ldb,
                            const float* gate, int64_t ldg, const float* up, int64_t ldu,
                            float* dgate, float* dup, int64_t ldd, int flags, int precision,
-                           pk_stream_t stream);
+                           const float* fp8_scales, pk_stream_t stream);
+
+/* fp8 operand scaling (no reference counterpart).  scales[0] and scales[1]
+ * (device memory) receive 2^floor(log2(448 / max|A|)) and the same for B (1 for
+ * an all-zero matrix): the largest powers of two that keep each operand
+ * within e4m3's finite range, so small values (gradients of order 1e-5, far
+ * below e4m3's smallest subnormal 2^-9) are not flushed to zero.  A [ra, ca]
+ * and B [rb, cb] are given as stored, with row strides lda, ldb.  Passed as
+ * fp8_scales to the fused launchers with precision 3, the operands are
+ * multiplied by them before rounding and the product divided by both
+ * (powers of two: exact).  NULL scales mean 1 and 1, as in pk_gemm_fp8_f32. */
+int pk_fp8_scales_f32(int64_t ra, int64_t ca, const float* A, int64_t lda, int64_t rb, int64_t cb,
+                      const float* B, int64_t ldb, float* scales, pk_stream_t stream);
 
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and

@@ -40,10 +40,15 @@ PK_SIGNATURES = {
     "pk_gemm_noalloc_scratch_bytes": [],
     "pk_gemm_noalloc_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
                             c_f, c_p, c_i64, c_p],
+    "pk_gemm_fp8_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
+                        c_p, c_i64, c_p],
+    "pk_gemm_ex_fp8_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
+                           c_f, c_p, c_i64, c_p, c_size, c_p],
     "pk_gemm_add_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
-                        c_p, c_i64, c_p, c_i64, c_int, c_p, c_size, c_p],
+                        c_p, c_i64, c_p, c_i64, c_int, c_p, c_p, c_size, c_p],
     "pk_gemm_swiglu_bwd_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
-                               c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_int, c_int, c_p],
+                               c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_int, c_int, c_p, c_p],
+    "pk_fp8_scales_f32": [c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "pk_gemm_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
                          c_p, c_i64, c_p],
     "pk_gemm_ex_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,

@@ -118,6 +118,8 @@ struct GemmParams {
     // the staged epilogue may use float4 accesses: every matrix it touches is
     // 16-byte aligned with a row stride that is a multiple of 4
     int epi_vec;
+    // fp8 products: the device address of the two operand scales (NULL: 1, 1)
+    const float* fp8_scale;
 };
 
 // Bounds handling of a tile's loads and stores: none (whole tiles), per float4
@@ -204,9 +206,37 @@ __device__ __forceinline__ void load_item(const float* __restrict__ base, int64_
 // [rows][40] (80 bytes: the 16-lane passes of 128-bit reads down a column of
 // rows touch 16 distinct 4-bank groups).
 constexpr int KFB = BK + 8;
+// An e4m3 element of an fp8 tile (OCP FP8 E4M3: bias 7, 3 mantissa bits,
+// largest finite 448), one byte.  fp8 tiles have rows of KF8 = 48 bytes:
+// the 64-bit fragment reads of 16 consecutive rows then start 12 banks apart
+// and never share a bank.
+template <int OP>  // OP 0: an element of op(A)'s tile, 1: of op(B)'s
+struct Fp8T {
+    unsigned char v;
+};
+using Fp8A = Fp8T<0>;
+using Fp8B = Fp8T<1>;
+constexpr int KF8 = BK + 16;
+
+// The fp8 kernel's operand scales (powers of two, so scaling is exact): op(A)
+// and op(B) are multiplied by them before rounding, and the accumulated
+// product is divided by both.  Set by each workgroup at its start.
+__shared__ float g_fp8_scale[2];
+
 template <class E>
 constexpr int lds_stride() {
-    return sizeof(E) == 4 ? KF : KFB;
+    return sizeof(E) == 4 ? KF : sizeof(E) == 1 ? KF8 : KFB;
+}
+
+// x rounded to e4m3 (nearest even) after clamping to the finite range, so
+// the conversion's overflow handling never matters; NaN stays NaN
+__device__ __forceinline__ float fp8_clamp(float x) {
+    return x != x ? x : fminf(fmaxf(x, -448.0f), 448.0f);
+}
+// two e4m3 values into bytes 0-1 (HI false) or 2-3 (HI true) of old
+template <bool HI>
+__device__ __forceinline__ int fp8_pack2(float a, float b, int old) {
+    return __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), old, HI);
 }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -247,6 +277,19 @@ __device__ __forceinline__ void put4(SplitBf16<LO>* lds, int off, f32x4 w) {
     *reinterpret_cast<bf16x4*>(t + off + LO) = l;
 }
 
+template <int OP>
+__device__ __forceinline__ void put4(Fp8T<OP>* lds, int off, f32x4 w) {
+    const float sc = g_fp8_scale[OP];
+    const int v = fp8_pack2<true>(w[2] * sc, w[3] * sc, fp8_pack2<false>(w[0] * sc, w[1] * sc, 0));
+    *reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(lds) + off) = v;
+}
+template <int OP>
+__device__ __forceinline__ void put2(Fp8T<OP>* lds, int off, float a, float b) {
+    const float sc = g_fp8_scale[OP];
+    *reinterpret_cast<short*>(reinterpret_cast<unsigned char*>(lds) + off) =
+        (short)fp8_pack2<false>(a * sc, b * sc, 0);
+}
+
 template <class E>
 __device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
     if constexpr(sizeof(E) == 4) {
@@ -285,6 +328,8 @@ __device__ __forceinline__ void store_item(E* lds, int item, const f32x4* v) {
             if constexpr(sizeof(E) == 4) {
                 typedef float f32x2 __attribute__((ext_vector_type(2)));
                 *reinterpret_cast<f32x2*>(lds + (rr + j) * LS + kk) = f32x2{v[0][j], v[1][j]};
+            } else if constexpr(sizeof(E) == 1) {
+                put2(lds, (rr + j) * LS + kk, v[0][j], v[1][j]);
             } else if constexpr(is_split<E>::value) {
                 const float w2[2] = {v[0][j], v[1][j]};
                 put_split<is_split<E>::LO>(reinterpret_cast<__bf16*>(lds), (rr + j) * LS + kk, w2, 2);
@@ -536,13 +581,14 @@ __device__ __forceinline__ void epi_four(const GemmParams& p, const TileJob& j, 
     }
 }
 
-template <int EPI, class T>
+template <int EPI, class T, int LDS_FLOATS>
 __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const TileJob& j,
                                                 const f32x16 (&acc)[T::TM][T::TN], float* lds,
-                                                int lds_floats, int ar0, int br0, int lr, int lh) {
+                                                int ar0, int br0, int lr, int lh) {
     constexpr int BN = T::BN, LDE = BN + 4, TM = T::TM, TN = T::TN;
     // rows per pass: whole 32-row blocks that fit in the operand buffers
-    const int rp = min(T::BM, (lds_floats / LDE) / 32 * 32);
+    constexpr int rp = (LDS_FLOATS / LDE) / 32 * 32 < T::BM ? (LDS_FLOATS / LDE) / 32 * 32 : T::BM;
+    static_assert(rp >= 32, "the staging buffer must hold at least one 32-row block");
     __syncthreads();  // every wave is done reading the operand tiles
     for(int lo = 0; lo < T::BM; lo += rp) {
 #pragma unroll
@@ -557,7 +603,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const TileJ
                         acc[i][jj][r];
         }
         __syncthreads();
-        const int rows = min(rp, T::BM - lo);
+        const int rows = rp < T::BM - lo ? rp : T::BM - lo;
         for(int idx = threadIdx.x; idx < rows * (BN / 4); idx += NT) {
             const int rr = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
             const int64_t row = j.row0 + lo + rr, col = j.col0 + c;
@@ -688,11 +734,11 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     if constexpr(EPI == kEpiPlain)
         store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
     else if constexpr(sizeof(ldsA) >= sizeof(ldsB))
-        staged_epilogue<EPI, T>(p, job, acc, &ldsA[0][0], (int)(sizeof(ldsA) / sizeof(float)), ar0,
-                                br0, lr, lh);
+        staged_epilogue<EPI, T, sizeof(ldsA) / sizeof(float)>(p, job, acc, &ldsA[0][0], ar0, br0,
+                                                             lr, lh);
     else
-        staged_epilogue<EPI, T>(p, job, acc, &ldsB[0][0], (int)(sizeof(ldsB) / sizeof(float)), ar0,
-                                br0, lr, lh);
+        staged_epilogue<EPI, T, sizeof(ldsB) / sizeof(float)>(p, job, acc, &ldsB[0][0], ar0, br0,
+                                                             lr, lh);
 }
 
 // The same product with bf16 multiplies: op(A) and op(B) are rounded to bf16
@@ -810,11 +856,114 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
     if constexpr(EPI == kEpiPlain)
         store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
     else if constexpr(sizeof(ldsA) >= sizeof(ldsB))
-        staged_epilogue<EPI, T>(p, job, acc, reinterpret_cast<float*>(&ldsA[0][0]),
-                                (int)(sizeof(ldsA) / sizeof(float)), ar0, br0, lr, lh);
+        staged_epilogue<EPI, T, sizeof(ldsA) / sizeof(float)>(
+            p, job, acc, reinterpret_cast<float*>(&ldsA[0][0]), ar0, br0, lr, lh);
     else
-        staged_epilogue<EPI, T>(p, job, acc, reinterpret_cast<float*>(&ldsB[0][0]),
-                                (int)(sizeof(ldsB) / sizeof(float)), ar0, br0, lr, lh);
+        staged_epilogue<EPI, T, sizeof(ldsB) / sizeof(float)>(
+            p, job, acc, reinterpret_cast<float*>(&ldsB[0][0]), ar0, br0, lr, lh);
+}
+
+// The same product with fp8 multiplies: op(A) and op(B) are rounded to e4m3
+// (after clamping to +-448) on their way to LDS and multiplied by
+// v_mfma_f32_32x32x16_fp8_fp8, accumulating in fp32.  Staging, tiles,
+// split-K and epilogues are the bf16 kernel's; a lane's 8 k of an MFMA step
+// are k 16t + 8*(lane/32) .. +7, read as one 64-bit LDS load.
+template <int NB>
+__device__ __forceinline__ void read_step8(const unsigned char* lds, int r0, int lr, int lh, int t,
+                                           long (&f)[NB]) {
+#pragma unroll
+    for(int b = 0; b < NB; ++b)
+        f[b] = *reinterpret_cast<const long*>(lds + (r0 + b * 32 + lr) * KF8 + 16 * t + 8 * lh);
+}
+
+template <bool TA, bool TB, int EDGE, class T, int EPI>
+__global__ __launch_bounds__(NT, T::OCC) void gemm_fp8_kernel(GemmParams p) {
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
+    constexpr bool AK = !TA, BKF = TB;
+    using OA = Operand<AK, BM>;
+    using OB = Operand<BKF, BN>;
+    using S = Staging<AK, BKF, T>;
+    constexpr int LA = BM * KF8, LB = BN * KF8;
+    // ldsA also stages the epilogue: at least one 32-row block of floats
+    constexpr int EPI_BYTES = EPI == kEpiPlain ? 0 : 32 * (BN + 4) * 4;
+    constexpr int A_BYTES = 2 * LA > EPI_BYTES ? 2 * LA : EPI_BYTES;
+    __shared__ __attribute__((aligned(16))) unsigned char ldsA_buf[A_BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char ldsB[2][LB];
+    unsigned char* const ldsA0 = ldsA_buf;
+    unsigned char* const ldsA1 = ldsA_buf + LA;
+
+    TileJob job = tile_job<T>(p);
+    if(job.skip) return;
+    if(threadIdx.x < 2) g_fp8_scale[threadIdx.x] = p.fp8_scale ? p.fp8_scale[threadIdx.x] : 1.0f;
+    __syncthreads();
+    job.alpha *= 1.0f / (g_fp8_scale[0] * g_fp8_scale[1]);  // powers of two: exact
+    const int nslices = job.nslices;
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    const int wm = w / WGN, wn = w % WGN;
+    const int lr = l & 31, lh = l >> 5;
+    const int ar0 = wm * TM * 32, br0 = wn * TN * 32;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for(int i = 0; i < TM; ++i)
+#pragma unroll
+        for(int j = 0; j < TN; ++j)
+#pragma unroll
+            for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    constexpr int RD = TM + TN;
+    constexpr int NMFMA = TM * TN;
+    constexpr int STAGE_OPS = S::group_ops(0) + S::group_ops(1) + S::group_ops(2);
+
+    if(nslices > 0) {
+        f32x4 ra[OA::F4], rb[OB::F4];
+        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, reinterpret_cast<Fp8A*>(ldsA0),
+                                   reinterpret_cast<Fp8B*>(ldsB[0]));
+        __syncthreads();
+        long fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+        auto mma = [&](const long (&fa)[TM], const long (&fb)[TN]) {
+#pragma unroll
+            for(int i = 0; i < TM; ++i)
+#pragma unroll
+                for(int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(fa[i], fb[j], acc[i][j],
+                                                                          0, 0, 0);
+        };
+        read_step8<TM>(ldsA0, ar0, lr, lh, 0, fa0);
+        read_step8<TN>(ldsB[0], br0, lr, lh, 0, fb0);
+        for(int s = 0; s < nslices; ++s) {
+            const int cur = s & 1;
+            unsigned char* const la = cur ? ldsA1 : ldsA0;
+            unsigned char* const na = cur ? ldsA0 : ldsA1;
+            Fp8A* sa = reinterpret_cast<Fp8A*>(na);
+            Fp8B* sb = reinterpret_cast<Fp8B*>(ldsB[cur ^ 1]);
+            const int64_t kn = job.kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
+            // step 0: read step 1, stage slice s+1 and fetch s+2
+            read_step8<TM>(la, ar0, lr, lh, 1, fa1);
+            read_step8<TN>(ldsB[cur], br0, lr, lh, 1, fb1);
+            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+                                       job.kend);
+            mma(fa0, fb0);
+            interleave<NMFMA, RD + STAGE_OPS>();
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            // step 1, with step 0 of slice s+1 read underneath
+            read_step8<TM>(na, ar0, lr, lh, 0, fa0);
+            read_step8<TN>(ldsB[cur ^ 1], br0, lr, lh, 0, fb0);
+            mma(fa1, fb1);
+            interleave<NMFMA, RD>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if constexpr(EPI == kEpiPlain)
+        store_tile<EDGE, TM, TN>(p, job, acc, ar0, br0, lr, lh);
+    else
+        staged_epilogue<EPI, T, A_BYTES / sizeof(float)>(
+            p, job, acc, reinterpret_cast<float*>(ldsA_buf), ar0, br0, lr, lh);
 }
 
 // C = alpha * sum_s ws[s] + beta * Cin, planes summed in order s = 0, 1, ...
@@ -937,11 +1086,13 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
     return best;
 }
 
-enum Precision { kFp32 = 0, kBf16 = 1, kBf16x3 = 2 };
+enum Precision { kFp32 = 0, kBf16 = 1, kBf16x3 = 2, kFp8 = 3 };
 
 template <bool TA, bool TB, class T, int EDGE, int EPI>
 void launch_epi(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
-    if(prec == kBf16)
+    if(prec == kFp8)
+        gemm_fp8_kernel<TA, TB, EDGE, T, EPI><<<grid, NT, 0, st>>>(gp);
+    else if(prec == kBf16)
         gemm_bf16_kernel<TA, TB, EDGE, T, false, EPI><<<grid, NT, 0, st>>>(gp);
     else if(prec == kBf16x3)
         gemm_bf16_kernel<TA, TB, EDGE, T, true, EPI><<<grid, NT, 0, st>>>(gp);
@@ -974,6 +1125,7 @@ int launch_tile(const GemmParams& gp, int64_t batch, int edge, int prec, hipStre
         launch_kernel<TA, TB, T, kEdgeScalar>(gp, grid, prec, st);
     return pk::launch_status(prec == kBf16     ? "pk_gemm_bf16_f32"
                              : prec == kBf16x3 ? "pk_gemm_bf16x3_f32"
+                             : prec == kFp8    ? "pk_gemm_fp8_f32"
                                                : "pk_gemm_f32");
 }
 
@@ -992,6 +1144,7 @@ int launch(const GemmParams& gp, int64_t batch, int edge, TileKind kind, int pre
 // what a product's tiles write besides alpha * op(A) . op(B): the beta term's
 // source when it is not C, or the SwiGLU-backward epilogue
 struct Epilogue {
+    const float* fp8_scale = nullptr;
     const float* Cin = nullptr;
     int64_t ldcin = 0;
     const float *sg_a = nullptr, *sg_u = nullptr;
@@ -1063,6 +1216,7 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     gp.sg_ldu = epi.sg_ldu;
     gp.sg_ldd = epi.sg_ldd;
     gp.sg_flags = epi.sg_flags;
+    gp.fp8_scale = prec == kFp8 ? epi.fp8_scale : nullptr;
     hipStream_t st = pk::as_stream(stream);
     gp.splits = 1;
     gp.kchunk = K;
@@ -1183,11 +1337,80 @@ extern "C" int pk_gemm_ex_bf16x3_f32(char ta, char tb, int64_t M, int64_t N, int
                      0, static_cast<float*>(workspace), workspace_bytes, kBf16x3, stream);
 }
 
+extern "C" int pk_gemm_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                               const float* A, int64_t lda, const float* B, int64_t ldb,
+                               float beta, float* C, int64_t ldc, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, nullptr, 0, kFp8, stream);
+}
+
+extern "C" int pk_gemm_ex_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                  const float* A, int64_t lda, const float* B, int64_t ldb,
+                                  float beta, float* C, int64_t ldc, void* workspace,
+                                  size_t workspace_bytes, pk_stream_t stream) {
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, beta, C, ldc, 0, 0, 1, 1,
+                     0, static_cast<float*>(workspace), workspace_bytes, kFp8, stream);
+}
+
+// ---- fp8 operand scales -------------------------------------------------------
+namespace {
+__global__ void fp8_scale_zero(unsigned* bits) {
+    if(threadIdx.x < 2) bits[threadIdx.x] = 0u;
+}
+
+// max |x| over matrix blockIdx.y (0: A, 1: B), as the bits of a non-negative
+// float (their unsigned order is the float order); NaNs are ignored
+__global__ void fp8_scale_amax(int64_t ra, int64_t ca, const float* __restrict__ A, int64_t lda,
+                               int64_t rb, int64_t cb, const float* __restrict__ B, int64_t ldb,
+                               unsigned* bits) {
+    __shared__ float red[NT / 64];
+    const bool isb = blockIdx.y == 1;
+    const int64_t rows = isb ? rb : ra, cols = isb ? cb : ca, ld = isb ? ldb : lda;
+    const float* x = isb ? B : A;
+    float m = 0.0f;
+    for(int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < rows * cols;
+        i += (int64_t)gridDim.x * NT)
+        m = fmaxf(m, fabsf(x[(i / cols) * ld + i % cols]));
+    m = pk::block_max<NT / 64>(m, red);
+    if(threadIdx.x == 0 && m > 0.0f) atomicMax(bits + blockIdx.y, __float_as_uint(m));
+}
+
+// scale = 2^floor(log2(448 / amax)): the largest power of two that keeps
+// amax * scale within e4m3's finite range; 1 for an all-zero or non-finite amax
+__global__ void fp8_scale_finish(unsigned* bits) {
+    if(threadIdx.x >= 2) return;
+    const float a = __uint_as_float(bits[threadIdx.x]);
+    float sc = 1.0f;
+    if(a > 0.0f && a <= 3.0e38f) sc = exp2f(floorf(log2f(448.0f / a)));
+    reinterpret_cast<float*>(bits)[threadIdx.x] = sc;
+}
+}  // namespace
+
+extern "C" int pk_fp8_scales_f32(int64_t ra, int64_t ca, const float* A, int64_t lda, int64_t rb,
+                                 int64_t cb, const float* B, int64_t ldb, float* scales,
+                                 pk_stream_t stream) {
+    if(ra < 0 || ca < 0 || rb < 0 || cb < 0)
+        return pk::fail("pk_fp8_scales_f32: negative size");
+    if(!scales) return pk::fail("pk_fp8_scales_f32: scales is NULL");
+    if((ra * ca > 0 && (!A || lda < ca)) || (rb * cb > 0 && (!B || ldb < cb)))
+        return pk::fail("pk_fp8_scales_f32: NULL matrix or row stride below its columns");
+    hipStream_t st = pk::as_stream(stream);
+    unsigned* bits = reinterpret_cast<unsigned*>(scales);
+    fp8_scale_zero<<<1, 64, 0, st>>>(bits);
+    const int64_t most = ra * ca > rb * cb ? ra * ca : rb * cb;
+    if(most > 0)
+        fp8_scale_amax<<<dim3(pk::grid_for(most, NT, 1024), 2), NT, 0, st>>>(ra, ca, A, lda, rb, cb,
+                                                                           B, ldb, bits);
+    fp8_scale_finish<<<1, 64, 0, st>>>(bits);
+    return pk::launch_status("pk_fp8_scales_f32");
+}
+
 // ---- fused epilogues -------------------------------------------------------
 namespace {
 int prec_of(int precision, const char* who) {
-    if(precision < kFp32 || precision > kBf16x3)
-        return pk::fail("%s: precision %d is not 0 (fp32), 1 (bf16) or 2 (bf16x3)", who, precision);
+    if(precision < kFp32 || precision > kFp8)
+        return pk::fail("%s: precision %d is not 0 (fp32), 1 (bf16), 2 (bf16x3) or 3 (fp8)", who,
+                        precision);
     return precision;
 }
 }  // namespace
@@ -1195,11 +1418,12 @@ int prec_of(int precision, const char* who) {
 extern "C" int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                                const float* A, int64_t lda, const float* B, int64_t ldb,
                                float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
-                               int precision, void* workspace, size_t workspace_bytes,
-                               pk_stream_t stream) {
+                               int precision, const float* fp8_scales, void* workspace,
+                               size_t workspace_bytes, pk_stream_t stream) {
     const int prec = prec_of(precision, "pk_gemm_add_f32");
     if(prec < 0) return PK_EINVAL;
     Epilogue e;
+    e.fp8_scale = fp8_scales;
     if(beta != 0.0f && M > 0 && N > 0) {
         if(!X) return pk::fail("pk_gemm_add_f32: X is NULL");
         if(ldx < N) return pk::fail("pk_gemm_add_f32: ldx=%lld < N=%lld", (long long)ldx,
@@ -1215,7 +1439,7 @@ extern "C" int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, in
                                       float alpha, const float* A, int64_t lda, const float* B,
                                       int64_t ldb, const float* gate, int64_t ldg, const float* up,
                                       int64_t ldu, float* dgate, float* dup, int64_t ldd, int flags,
-                                      int precision, pk_stream_t stream) {
+                                      int precision, const float* fp8_scales, pk_stream_t stream) {
     const int prec = prec_of(precision, "pk_gemm_swiglu_bwd_f32");
     if(prec < 0) return PK_EINVAL;
     if(M > 0 && N > 0) {
@@ -1228,6 +1452,7 @@ extern "C" int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, in
     const bool nt = (ta == 'N' || ta == 'n') && (tb == 'T' || tb == 't');
     if(!nt) return pk::fail("pk_gemm_swiglu_bwd_f32: only the ('N','T') layout (dY . W^T) is built");
     Epilogue e;
+    e.fp8_scale = fp8_scales;
     e.sg_a = gate;
     e.sg_u = up;
     e.sg_da = dgate;

@@ -187,7 +187,7 @@ static int g_matmul_precision = PICO_MATMUL_FP32;
 
 int pico_set_matmul_precision(int precision) {
     if(precision != PICO_MATMUL_FP32 && precision != PICO_MATMUL_BF16 &&
-       precision != PICO_MATMUL_BF16X3) {
+       precision != PICO_MATMUL_BF16X3 && precision != PICO_MATMUL_FP8) {
         PKH_ERR("pico_set_matmul_precision: unknown precision %d!\n", precision);
         return PK_EINVAL;
     }
@@ -200,18 +200,58 @@ int pico_get_matmul_precision(void) { return g_matmul_precision; }
 /* products with too few output tiles (weight gradients) split K through a
  * workspace; see pk_gemm_ex_f32.  On the side stream (side != 0) the product
  * uses the side stream's own workspace. */
+/* fp8 products scale each operand by a power of two computed from its
+ * largest magnitude (pk_fp8_scales_f32), into the first FP8_SCALE_BYTES of
+ * the workspace, so small values (gradients) are not flushed to zero */
+#define FP8_SCALE_BYTES 256
+
+/* the stored shape of a matrix view of logical shape [rows, cols] */
+static void stored_dims(struct PkMat m, int64_t rows, int64_t cols, int64_t* r, int64_t* c) {
+    *r = m.t == 'N' ? rows : cols;
+    *c = m.t == 'N' ? cols : rows;
+}
+
+/* scales of the kernel's operands A [M, K] and B [K, N] (logical) */
+static int fp8_scales_for(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K,
+                          float* scales, pk_stream_t st) {
+    int64_t ra, ca, rb, cb;
+    stored_dims(A, M, K, &ra, &ca);
+    stored_dims(B, K, N, &rb, &cb);
+    return pk_fp8_scales_f32(ra, ca, A.p, A.ld, rb, cb, B.p, B.ld, scales, st);
+}
+
 static int gemm_add_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
                        char tc, int64_t ldc, float beta, const float* X, int64_t ldx,
                        pk_stream_t st, int side) {
+    const int fp8 = g_matmul_precision == PICO_MATMUL_FP8;
     size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
-    void* ws = ws_bytes ? (side ? pkh_side_workspace(ws_bytes) : pkh_workspace(ws_bytes)) : NULL;
+    const size_t lead = fp8 ? FP8_SCALE_BYTES : 0;
+    void* ws = ws_bytes + lead ? (side ? pkh_side_workspace(ws_bytes + lead)
+                                       : pkh_workspace(ws_bytes + lead))
+                               : NULL;
+    float* scales = NULL;
+    if(fp8) {
+        if(!ws) return PK_EINVAL;
+        scales = (float*)ws;
+        ws = (unsigned char*)ws + lead;
+    }
     if(!ws) ws_bytes = 0;
-    if(tc == 'N')
+    if(tc == 'N') {
+        if(fp8) {
+            int st8 = fp8_scales_for(A, B, M, N, K, scales, st);
+            if(st8) return st8;
+        }
         return pk_gemm_add_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, X, ldx, C, ldc,
-                               g_matmul_precision, ws, ws_bytes, st);
+                               g_matmul_precision, scales, ws, ws_bytes, st);
+    }
     /* C stored transposed: produce C^T [N, M] = B^T . A^T (X is C itself here) */
-    return pk_gemm_add_f32(flip(B.t), flip(A.t), N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc,
-                           C, ldc, g_matmul_precision, ws, ws_bytes, st);
+    struct PkMat BT = {B.p, flip(B.t), B.ld}, AT = {A.p, flip(A.t), A.ld};
+    if(fp8) {
+        int st8 = fp8_scales_for(BT, AT, N, M, K, scales, st);
+        if(st8) return st8;
+    }
+    return pk_gemm_add_f32(BT.t, AT.t, N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc, C, ldc,
+                           g_matmul_precision, scales, ws, ws_bytes, st);
 }
 
 static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
@@ -448,11 +488,18 @@ struct DaSwiglu {
 static int da_swiglu(void* ctx) {
     struct DaSwiglu* c = (struct DaSwiglu*)ctx;
     const int flags = (pkh_grad_flag(c->gate) ? PK_ACCUM : 0) | (pkh_grad_flag(c->up) ? PK_ACCUM2 : 0);
+    float* scales = NULL;
+    struct PkMat g = {c->g, 'N', c->N > 0 ? c->N : 1}, wt = {c->w->data, 'T', c->w->strides[0]};
+    if(g_matmul_precision == PICO_MATMUL_FP8) {
+        scales = (float*)pkh_workspace(FP8_SCALE_BYTES);
+        int st8 = scales ? fp8_scales_for(g, wt, c->M, c->F, c->N, scales, pkh_stream()) : PK_EINVAL;
+        if(pkh_status("pico_swiglu_matmul_add_backward", st8)) return st8;
+    }
     /* dh = g [M, N] . w^T, w [F, N] row-major */
-    int st = pk_gemm_swiglu_bwd_f32('N', 'T', c->M, c->F, c->N, 1.0f, c->g, c->N > 0 ? c->N : 1,
-                                    c->w->data, c->w->strides[0], c->gate->data, c->ld,
-                                    c->up->data, c->ld, c->gate->grad, c->up->grad, c->ld, flags,
-                                    g_matmul_precision, pkh_stream());
+    int st = pk_gemm_swiglu_bwd_f32('N', 'T', c->M, c->F, c->N, 1.0f, g.p, g.ld, wt.p, wt.ld,
+                                    c->gate->data, c->ld, c->up->data, c->ld, c->gate->grad,
+                                    c->up->grad, c->ld, flags, g_matmul_precision, scales,
+                                    pkh_stream());
     if(pkh_status("pico_swiglu_matmul_add_backward", st)) return st;
     pkh_grad_mark(c->gate);
     pkh_grad_mark(c->up);

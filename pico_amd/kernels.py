@@ -63,7 +63,12 @@ def gemm_bf16x3(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
     return gemm_bf16(ta, tb, A, B, C, alpha, beta, ws, split=True)
 
 
-def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False):
+def gemm_fp8(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
+    """gemm with e4m3 multiplies and fp32 accumulation (pk_gemm_fp8_f32)"""
+    return gemm_bf16(ta, tb, A, B, C, alpha, beta, ws, _name="pk_gemm_fp8_f32")
+
+
+def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False, _name=None):
     """gemm with bf16 multiplies and fp32 accumulation (fp32 tensors in and out);
     ws: optional workspace for a K split (as gemm_ex); split: hi/lo operands,
     three products (pk_gemm_bf16x3_f32)"""
@@ -75,7 +80,7 @@ def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False):
     N = B.shape[0] if tb == "T" else B.shape[1]
     if K != Kb or tuple(C.shape) != (M, N):
         raise ValueError(f"gemm shape mismatch: op(A) {M}x{K}, op(B) {Kb}x{N}, C {tuple(C.shape)}")
-    name = "pk_gemm_bf16x3_f32" if split else "pk_gemm_bf16_f32"
+    name = _name or ("pk_gemm_bf16x3_f32" if split else "pk_gemm_bf16_f32")
     if ws is None:
         check(name, getattr(hip_lib(), name)(
             ta.encode(), tb.encode(), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C),

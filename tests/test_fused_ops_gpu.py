@@ -48,7 +48,7 @@ def test_gemm_add_equals_product_then_add(dev, M, N, K, prec):
     got = torch.full((M, N), 7.0, device=dev)
     _lib.check("pk_gemm_add_f32", L.pk_gemm_add_f32(
         b"N", b"N", M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(), N, 1.0, X.data_ptr(), N,
-        got.data_ptr(), N, prec, ws.data_ptr(), need, None))
+        got.data_ptr(), N, prec, None, ws.data_ptr(), need, None))
     prod = torch.empty(M, N, device=dev)
     fn = {0: L.pk_gemm_ex_f32, 1: L.pk_gemm_ex_bf16_f32, 2: L.pk_gemm_ex_bf16x3_f32}[prec]
     _lib.check("pk_gemm_ex", fn(b"N", b"N", M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(), N, 0.0,
@@ -75,7 +75,7 @@ def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
     got = g0.clone()
     _lib.check("pk_gemm_swiglu_bwd_f32", L.pk_gemm_swiglu_bwd_f32(
         b"N", b"T", M, F, N, 1.0, dY.data_ptr(), N, W.data_ptr(), N, gate.data_ptr(), ld,
-        up.data_ptr(), ld, got.data_ptr(), got.data_ptr() + 4 * F, ld, flags, 0, None))
+        up.data_ptr(), ld, got.data_ptr(), got.data_ptr() + 4 * F, ld, flags, 0, None, None))
     dh = torch.empty(M, F, device=dev)
     _lib.check("pk_gemm_f32", L.pk_gemm_f32(b"N", b"T", M, F, N, 1.0, dY.data_ptr(), N,
                                             W.data_ptr(), N, 0.0, dh.data_ptr(), F, None))
@@ -102,7 +102,7 @@ def test_gemm_swiglu_bwd_refuses_other_layouts(dev):
     x = torch.zeros(64, 64, device=dev)
     st = L.pk_gemm_swiglu_bwd_f32(b"N", b"N", 64, 64, 64, 1.0, x.data_ptr(), 64, x.data_ptr(), 64,
                                   x.data_ptr(), 64, x.data_ptr(), 64, x.data_ptr(),
-                                  x.data_ptr() + 4, 64, 0, 0, None)
+                                  x.data_ptr() + 4, 64, 0, 0, None, None)
     assert st == -1 and b"layout" in L.pk_last_error()
 
 
