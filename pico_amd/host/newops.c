@@ -232,7 +232,9 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
  * shared row stride (contiguous, or column blocks of one fused projection);
  * out contiguous [batch*T, heads*hd].  For head size 64 and
  * T a multiple of 128 the fused kernels run (pk_flash_attn_*): only lse
- * [B*H*T] is saved and the scores never reach memory.  Otherwise the chain of
+ * [B*H*T] is saved, and the forward never writes scores or probabilities;
+ * the backward passes dS from its dK/dV kernel to its dQ kernel as 32x32 tiles
+ * of each head's causal triangle in a workspace of about 2*B*H*T^2 bytes.  Otherwise the chain of
  * batched GEMMs and causal-softmax kernels runs and saves the probabilities
  * P [B*H, T, T] (arena device memory). */
 enum { AS_LSE = 0, AS_P = 1 };
@@ -249,7 +251,13 @@ static void attn_backward(struct PicoTensor* self) {
     size_t ws_bytes = flash ? pk_flash_attn_bwd_workspace(B, H, T)
                             : sizeof(float) * (size_t)(B * H * T * T);
     void* ws = pkh_workspace(ws_bytes);
-    if(!ws) return;
+    if(!ws) {
+        pkh_set_error("pico_attention_causal_backward: no device workspace of %zu bytes; the q, "
+                      "k and v grads are not written",
+                      ws_bytes);
+        PKH_ERR("%s\n", pico_gpu_last_error());
+        return;
+    }
     /* aliased grads (q, k or v the same tensor) accumulate when each write
      * after the first carries its accumulate bit; the write order is dv, dk,
      * dq (fused) or dv, dq, dk (chain) */

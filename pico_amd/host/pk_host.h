@@ -50,6 +50,7 @@ void pkh_registry_clear(void);
 int pkh_init(void);              /* 0 once the device and stream are up */
 pk_stream_t pkh_stream(void);
 void pkh_set_error(const char* fmt, ...);
+uint64_t pkh_error_count(void); /* errors recorded so far (pico_backward stops on a new one) */
 /* maps a launcher status to the pico convention: prints "[Pico] Error: op: msg"
  * and records it; returns status */
 int pkh_status(const char* op, int status);

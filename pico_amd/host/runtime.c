@@ -40,12 +40,17 @@ static int g_side_broken = 0;
 static void* g_side_ws = NULL;
 static size_t g_side_ws_bytes = 0;
 
+static uint64_t g_err_count = 0;
+
 void pkh_set_error(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_err, sizeof(g_err), fmt, ap);
     va_end(ap);
+    g_err_count++;
 }
+
+uint64_t pkh_error_count(void) { return g_err_count; }
 
 /* refuses a call that cannot be recorded in a graph; returns nonzero then */
 static int capture_refuses(const char* what) {

@@ -394,9 +394,16 @@ void pico_backward(struct Arena* arena, struct PicoTensor* entry) {
         goto done;
     pkh_grad_mark(entry);
     pkh_node(entry)->seed_one = 1;
+    /* a hook that fails records an error and leaves its parents' grads
+     * unwritten: stop there rather than propagate from partial grads */
+    const uint64_t errors = pkh_error_count();
     for(int64_t i = order.n - 1; i >= 0; i--) {
         struct PicoTensor* t = order.v[i];
         if(t->_backward) t->_backward(t);
+        if(pkh_error_count() != errors) {
+            PKH_ERR("pico_backward: stopped at a failed backward hook (%s)\n", pico_gpu_last_error());
+            break;
+        }
     }
     pkh_side_join(); /* weight gradients computed on the side stream are in */
     pkh_node(entry)->seed_one = 0;
