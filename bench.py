@@ -193,6 +193,12 @@ def rows_section(torch, K):
     bw("rmsnorm_bwd", 3 * R * Cc * 4,
        [lambda j=j: K.rmsnorm_bwd(xs[j], g, rs[j], ys[(j + 1) % sets], ys[(j + 2) % sets], dgs, ws)
         for j in range(sets)], f"{R}x{Cc}")
+    # the part a training step runs on its critical path: dx plus dg's partial
+    # sums left in the workspace (their column sum runs on the side stream)
+    bw("rmsnorm_bwd_dx_and_partials", 3 * R * Cc * 4,
+       [lambda j=j: K.rmsnorm_bwd(xs[j], g, rs[j], ys[(j + 1) % sets], ys[(j + 2) % sets], None,
+                                  ws, keep_partials=True)
+        for j in range(sets)], f"{R}x{Cc}")
     del xs, ys, rs
     # SwiGLU 8192 x 11008
     R, F = 8192, 11008

@@ -994,54 +994,6 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
     }
 }
 
-// K split for a product whose output has too few tiles to fill the chip: 2
-// resident workgroups per CU x 256 CUs want >= 512 workgroups.
-//  * K >= 1024 (weight gradients: M, N ~ d_model, K = tokens): slices of at
-//    least 256 (8 LDS stages).  The split count minimises the estimated time
-//    in units of one 32-deep stage over a full round of 512 workgroups of
-//    128x128 tiles (~3.9 us):
-//        rounds x (stages per split + 2.5 for a workgroup's prologue and
-//        epilogue) + (s + 1) planes of M*N floats for the reduction (~19.5 MB
-//        of HBM traffic per unit).
-//    A second round of workgroups can beat one round that leaves slots idle:
-//    a [768, 4096] gradient with K = 8192 (192 tiles) takes 8 splits (three
-//    rounds of 32 stages) rather than 2 (one round of 128 stages, 384 of 512
-//    slots busy).  [768, 768] takes 14 and [768, 2048] 5.
-//  * 512 <= K < 1024: only when even 64x64 tiles would leave three quarters
-//    of the CUs idle (the MLP's [64, 784] . [784, 128]: 2 tiles); slices of
-//    at least 128, which turns one latency-bound workgroup chain into six.
-//    Wider outputs take the 64x64 tiles instead.
-//  * K < 512: never.
-constexpr int64_t kSplitTarget = 512, kMinSplitK = 512;
-
-int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
-    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
-    *kchunk = K;
-    if(tiles <= 0 || tiles * 2 > kSplitTarget || K < kMinSplitK) return 1;
-    if(K < 1024 && ((M + 63) / 64) * ((N + 63) / 64) * 4 >= 256) return 1;
-    const int64_t min_slice = K >= 1024 ? 256 : 128;
-    int64_t s_max = K / min_slice;
-    if(s_max > 64) s_max = 64;
-    int64_t best_s = 1;
-    double best = -1.0;
-    const double plane = (double)M * (double)N * 4.0 / 19.5e6;
-    for(int64_t s = 1; s <= s_max; ++s) {
-        const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
-        const int64_t splits = (K + chunk - 1) / chunk;
-        const int64_t rounds = (tiles * splits + kSplitTarget - 1) / kSplitTarget;
-        const double cost = (double)rounds * ((double)(chunk / BK) + 2.5) +
-                            (splits > 1 ? (double)(splits + 1) * plane : 0.0);
-        if(best < 0.0 || cost < best) {
-            best = cost;
-            best_s = s;
-        }
-    }
-    if(best_s < 2) return 1;
-    const int64_t chunk = ((K + best_s - 1) / best_s + BK - 1) / BK * BK;
-    *kchunk = chunk;
-    return (int)((K + chunk - 1) / chunk);
-}
-
 // Tile shape: the estimated time of a shape is the work of the busiest CU --
 // its share of the tiles, ceil(tiles / 256 CUs), times the work of one tile in
 // units of a 128x128 tile (256x256: 4, 256x96: 1.5, 128x96: 0.75, 64x64:
@@ -1084,6 +1036,65 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
         if(cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
     }
     return best;
+}
+
+// K split for a product whose output has too few tiles to fill the chip: 2
+// resident workgroups per CU x 256 CUs want >= 512 workgroups.
+//  * K >= 1024 (weight gradients: M, N ~ d_model, K = tokens): slices of at
+//    least 256 (8 LDS stages).  The split count minimises the estimated time
+//    in units of one 32-deep stage over a full round of 512 workgroups of
+//    128x128 tiles (~3.9 us):
+//        rounds x (stages per split + 2.5 for a workgroup's prologue and
+//        epilogue) + (s + 1) planes of M*N floats for the reduction (~19.5 MB
+//        of HBM traffic per unit).
+//    A second round of workgroups can beat one round that leaves slots idle:
+//    a [768, 4096] gradient with K = 8192 (192 tiles) takes 8 splits (three
+//    rounds of 32 stages) rather than 2 (one round of 128 stages, 384 of 512
+//    slots busy).  [768, 768] takes 14 and [768, 2048] 5.
+//  * 512 <= K < 1024: only when even 64x64 tiles would leave three quarters
+//    of the CUs idle (the MLP's [64, 784] . [784, 128]: 2 tiles); slices of
+//    at least 128, which turns one latency-bound workgroup chain into six.
+//    Wider outputs take the 64x64 tiles instead.
+//  * K < 512: never.
+//  * K < 4096 and the unsplit tile choice already gives every CU a tile
+//    (2048^2: 256 tiles of 128x128; 1024^2: 256 of 64x64): never.  The split
+//    adds a second workgroup per CU but not its throughput, and pays for the
+//    reduction (measured best of three: 2048^3 130 TF/s unsplit against 122
+//    with 2 splits; 1024^3 82 against 72 with 4).  Longer K keeps splitting:
+//    [768, 2304] with K = 8192 (432 tiles of 64x64) runs at 97 TF/s unsplit
+//    and 109-115 split.
+constexpr int64_t kSplitTarget = 512, kMinSplitK = 512;
+
+int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
+    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    *kchunk = K;
+    if(tiles <= 0 || tiles * 2 > kSplitTarget || K < kMinSplitK) return 1;
+    if(K < 1024 && ((M + 63) / 64) * ((N + 63) / 64) * 4 >= 256) return 1;
+    if(K < 4096) {
+        const TileChoice t = pick_tile(M, N, 1, true);
+        if(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) >= kCUs) return 1;
+    }
+    const int64_t min_slice = K >= 1024 ? 256 : 128;
+    int64_t s_max = K / min_slice;
+    if(s_max > 64) s_max = 64;
+    int64_t best_s = 1;
+    double best = -1.0;
+    const double plane = (double)M * (double)N * 4.0 / 19.5e6;
+    for(int64_t s = 1; s <= s_max; ++s) {
+        const int64_t chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
+        const int64_t splits = (K + chunk - 1) / chunk;
+        const int64_t rounds = (tiles * splits + kSplitTarget - 1) / kSplitTarget;
+        const double cost = (double)rounds * ((double)(chunk / BK) + 2.5) +
+                            (splits > 1 ? (double)(splits + 1) * plane : 0.0);
+        if(best < 0.0 || cost < best) {
+            best = cost;
+            best_s = s;
+        }
+    }
+    if(best_s < 2) return 1;
+    const int64_t chunk = ((K + best_s - 1) / best_s + BK - 1) / BK * BK;
+    *kchunk = chunk;
+    return (int)((K + chunk - 1) / chunk);
 }
 
 enum Precision { kFp32 = 0, kBf16 = 1, kBf16x3 = 2, kFp8 = 3 };
