@@ -193,9 +193,15 @@ int pico_argmax(struct PicoTensor* x, int32_t* idx);
  *   stride (column views of
  *   one [M, 2F] product are fine), w row-contiguous [F, N].  The backward
  *   never stores dh: the product dY.w^T writes the gate and up gradients
- *   from its tiles. ---- */
+ *   from its tiles.
+ * pico_matmul_gate_up(a, w) = a.w for w = [W1 | W3] [K, 2F]: a matmul, whose
+ *   product also writes h = silu(gate) * up (gate, up the two column halves
+ *   of the result) and keeps it; pico_swiglu_matmul_add over the two views
+ *   pico_split_cols(result, 2) makes uses that h instead of computing it.
+ *   (F not a multiple of 32 or a transposed a: a plain matmul.) ---- */
 struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
                                    struct PicoTensor* c);
+struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* w);
 struct PicoTensor* pico_swiglu_matmul_add(struct PicoTensor* gate, struct PicoTensor* up,
                                           struct PicoTensor* w, struct PicoTensor* c);
 

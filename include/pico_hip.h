@@ -112,7 +112,14 @@ int pk_gemm_ex_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float 
  *   arithmetic; gate, up [M,N] (row strides ldg, ldu) are read in the tile's
  *   epilogue, dgate and dup (distinct) share the row stride ldd.  In a
  *   transformer block it is the down projection's input gradient dY.W2^T
- *   turned straight into the gate/up gradients. */
+ *   turned straight into the gate/up gradients.
+ * pk_gemm_swiglu_fwd_f32: ('N','N' only, batch 1) C = alpha * A.B [M, N]
+ *   with N = 2F (C = [gate | up], B = [W1 | W3]) and h [M, F] (row stride
+ *   ldh) = silu(gate) * up with pk_swiglu_fwd_f32's arithmetic; C holds the
+ *   values pk_gemm_ex_f32 writes.  A tile takes F-aligned pairs of gate and
+ *   up columns, so F must be a multiple of 32 (4 for whole-column tiles of
+ *   64); refused otherwise.  The gate/up projection of a SwiGLU block and
+ *   its activation in one pass. */
 int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                     const float* X, int64_t ldx, float* C, int64_t ldc, int precision,
@@ -122,6 +129,10 @@ int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, fl
                            const float* A, int64_t lda, const float* B, int64_t ldb,
                            const float* gate, int64_t ldg, const float* up, int64_t ldu,
                            float* dgate, float* dup, int64_t ldd, int flags, int precision,
+                           const float* fp8_scales, pk_stream_t stream);
+int pk_gemm_swiglu_fwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
+                           const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                           int64_t ldc, float* h, int64_t ldh, int precision,
                            const float* fp8_scales, pk_stream_t stream);
 
 /* fp8 operand scaling (no reference counterpart).  scales[0] and scales[1]

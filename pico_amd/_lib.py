@@ -48,6 +48,8 @@ PK_SIGNATURES = {
                         c_p, c_i64, c_p, c_i64, c_int, c_p, c_p, c_size, c_p],
     "pk_gemm_swiglu_bwd_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
                                c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_int, c_int, c_p, c_p],
+    "pk_gemm_swiglu_fwd_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
+                               c_p, c_i64, c_p, c_i64, c_int, c_p, c_p],
     "pk_fp8_scales_f32": [c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "pk_gemm_bf16_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
                          c_p, c_i64, c_p],

@@ -120,6 +120,13 @@ struct GemmParams {
     int epi_vec;
     // fp8 products: the device address of the two operand scales (NULL: 1, 1)
     const float* fp8_scale;
+    // SwiGLU-forward epilogue (pair_F > 0, 'N','N', batch 1, no K split): C is
+    // [gate | up], N = 2 pair_F columns.  A tile takes BN/2 gate columns and
+    // the BN/2 up columns pair_F to their right, so it holds matching pairs;
+    // it writes both to C and h = silu(gate) * up to sf_h
+    int64_t pair_F;
+    float* sf_h;
+    int64_t sf_ldh;
 };
 
 // Bounds handling of a tile's loads and stores: none (whole tiles), per float4
@@ -187,18 +194,21 @@ __device__ __forceinline__ void item_origin(int item, int& rr, int& kk) {
     }
 }
 
-template <bool KFAST, int EDGE, int R>
+// PAIR: rows R/2.. of the slice come from `shift` rows further on (the up
+// columns of a paired SwiGLU product; an item's 4 rows never straddle R/2)
+template <bool KFAST, int EDGE, int R, bool PAIR = false>
 __device__ __forceinline__ void load_item(const float* __restrict__ base, int64_t ld, int64_t r0,
                                           int64_t k0, int64_t Rlim, int64_t K, int item,
-                                          f32x4* v) {
+                                          f32x4* v, int64_t shift = 0) {
     int rr, kk;
     item_origin<KFAST, R>(item, rr, kk);
+    const int64_t r = r0 + rr + (PAIR && rr >= R / 2 ? shift : 0);
     if(KFAST) {
-        v[0] = load_f4<true, EDGE>(base, ld, r0 + rr, k0 + kk, Rlim, K);
+        v[0] = load_f4<true, EDGE>(base, ld, r, k0 + kk, Rlim, K);
     } else {
 #pragma unroll
         for(int t = 0; t < Operand<false, R>::KD; ++t)
-            v[t] = load_f4<false, EDGE>(base, ld, r0 + rr, k0 + kk + t, Rlim, K);
+            v[t] = load_f4<false, EDGE>(base, ld, r, k0 + kk + t, Rlim, K);
     }
 }
 
@@ -409,7 +419,8 @@ struct Staging {
     static constexpr int group_ops(int g) { return ops_before(lo(g + 1)) - ops_before(lo(g)); }
 };
 
-template <bool AK, bool BKF, int EDGE, class T, int G, int NA, int NB, class EA, class EB>
+template <bool AK, bool BKF, int EDGE, class T, int G, bool PAIR = false, int NA, int NB, class EA,
+          class EB>
 __device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], EA* sa, EB* sb,
                                       const float* __restrict__ A, const float* __restrict__ B,
                                       const GemmParams& p, int64_t row0, int64_t col0, int64_t kn,
@@ -429,7 +440,8 @@ __device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], EA* sa, 
         if(e < IA)
             load_item<AK, EDGE, T::BM>(A, p.lda, row0, kn, p.M, kend, e, &ra[e * FA]);
         else
-            load_item<BKF, EDGE, T::BN>(B, p.ldb, col0, kn, p.N, kend, e - IA, &rb[(e - IA) * FB]);
+            load_item<BKF, EDGE, T::BN, PAIR>(B, p.ldb, col0, kn, p.N, kend, e - IA,
+                                              &rb[(e - IA) * FB], p.pair_F - T::BN / 2);
     }
 }
 
@@ -472,7 +484,7 @@ __device__ __forceinline__ TileJob tile_job(const GemmParams& p) {
     j.beta = p.beta;
 
     j.row0 = (int64_t)tm * T::BM;
-    j.col0 = (int64_t)tn * T::BN;
+    j.col0 = (int64_t)tn * (p.pair_F ? T::BN / 2 : T::BN);
     j.kbeg = 0;
     j.kend = p.K;
     j.skip = p.causal == 1 && j.col0 > j.row0 + T::BM - 1;  // wholly above the diagonal
@@ -525,7 +537,10 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j
 // registers).
 //   kEpiAdd:    C = alpha * acc + beta * Cin
 //   kEpiSwiglu: dh = alpha * acc; da (+)= dh*u*s*(1 + a*(1-s)), du (+)= dh*a*s
-constexpr int kEpiPlain = 0, kEpiAdd = 1, kEpiSwiglu = 2;
+//   kEpiSwigluFwd: the tile's two column halves are matching gate and up
+//               columns: C gets g = alpha * acc and u alike (as the plain
+//               store writes them), sf_h gets silu(g) * u
+constexpr int kEpiPlain = 0, kEpiAdd = 1, kEpiSwiglu = 2, kEpiSwigluFwd = 3;
 
 template <int EPI>
 __device__ __forceinline__ void epi_one(const GemmParams& p, const TileJob& j, int64_t row,
@@ -604,17 +619,51 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const TileJ
         }
         __syncthreads();
         const int rows = rp < T::BM - lo ? rp : T::BM - lo;
-        for(int idx = threadIdx.x; idx < rows * (BN / 4); idx += NT) {
-            const int rr = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
-            const int64_t row = j.row0 + lo + rr, col = j.col0 + c;
-            const f32x4 x = *reinterpret_cast<const f32x4*>(lds + rr * LDE + c);
-            if(row >= p.M) continue;
-            if(p.epi_vec && col + 3 < p.N) {
-                epi_four<EPI>(p, j, row, col, x);
-            } else {
+        if constexpr(EPI == kEpiSwigluFwd) {
+            // column c of the gate half pairs with column BN/2 + c; the host
+            // guarantees whole column halves (pair_F a multiple of BN/2)
+            constexpr int HB = BN / 2;
+            for(int idx = threadIdx.x; idx < rows * (HB / 4); idx += NT) {
+                const int rr = idx / (HB / 4), c = (idx % (HB / 4)) * 4;
+                const int64_t row = j.row0 + lo + rr, col = j.col0 + c;
+                if(row >= p.M) continue;
+                const f32x4 g = *reinterpret_cast<const f32x4*>(lds + rr * LDE + c);
+                const f32x4 u = *reinterpret_cast<const f32x4*>(lds + rr * LDE + HB + c);
+                f32x4 gv, uv, hv;
 #pragma unroll
-                for(int e = 0; e < 4; ++e)
-                    if(col + e < p.N) epi_one<EPI>(p, j, row, col + e, x[e]);
+                for(int e = 0; e < 4; ++e) {
+                    gv[e] = j.alpha * g[e];
+                    uv[e] = j.alpha * u[e];
+                    hv[e] = pk::swiglu_fwd1(gv[e], uv[e]);
+                }
+                float* cg = j.C + row * j.ldc + col;
+                float* hp = p.sf_h + row * p.sf_ldh + col;
+                if(p.epi_vec) {
+                    *reinterpret_cast<f32x4*>(cg) = gv;
+                    *reinterpret_cast<f32x4*>(cg + p.pair_F) = uv;
+                    *reinterpret_cast<f32x4*>(hp) = hv;
+                } else {
+#pragma unroll
+                    for(int e = 0; e < 4; ++e) {
+                        cg[e] = gv[e];
+                        cg[p.pair_F + e] = uv[e];
+                        hp[e] = hv[e];
+                    }
+                }
+            }
+        } else {
+            for(int idx = threadIdx.x; idx < rows * (BN / 4); idx += NT) {
+                const int rr = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+                const int64_t row = j.row0 + lo + rr, col = j.col0 + c;
+                const f32x4 x = *reinterpret_cast<const f32x4*>(lds + rr * LDE + c);
+                if(row >= p.M) continue;
+                if(p.epi_vec && col + 3 < p.N) {
+                    epi_four<EPI>(p, j, row, col, x);
+                } else {
+#pragma unroll
+                    for(int e = 0; e < 4; ++e)
+                        if(col + e < p.N) epi_one<EPI>(p, j, row, col + e, x[e]);
+                }
             }
         }
         __syncthreads();
@@ -623,7 +672,8 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& p, const TileJ
 
 // prologue shared by both kernels: slice 0 into LDS buffer 0, slice 1 into
 // the staging registers
-template <bool AK, bool BKF, int EDGE, class T, int NA, int NB, class EA, class EB>
+template <bool AK, bool BKF, int EDGE, class T, bool PAIR = false, int NA, int NB, class EA,
+          class EB>
 __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, f32x4 (&ra)[NA],
                                          f32x4 (&rb)[NB], EA* sa, EB* sb) {
     using OA = Operand<AK, T::BM>;
@@ -633,7 +683,8 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
         load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, j.kbeg, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
     for(int e = 0; e < OB::ITEMS; ++e)
-        load_item<BKF, EDGE, T::BN>(j.B, p.ldb, j.col0, j.kbeg, p.N, j.kend, e, &rb[e * OB::ITEM_F4]);
+        load_item<BKF, EDGE, T::BN, PAIR>(j.B, p.ldb, j.col0, j.kbeg, p.N, j.kend, e,
+                                          &rb[e * OB::ITEM_F4], p.pair_F - T::BN / 2);
 #pragma unroll
     for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, T::BM>(sa, e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
@@ -644,7 +695,8 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
         load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, k1, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
 #pragma unroll
     for(int e = 0; e < OB::ITEMS; ++e)
-        load_item<BKF, EDGE, T::BN>(j.B, p.ldb, j.col0, k1, p.N, j.kend, e, &rb[e * OB::ITEM_F4]);
+        load_item<BKF, EDGE, T::BN, PAIR>(j.B, p.ldb, j.col0, k1, p.N, j.kend, e,
+                                          &rb[e * OB::ITEM_F4], p.pair_F - T::BN / 2);
 }
 
 template <bool TA, bool TB, int EDGE, class T, int EPI>
@@ -684,7 +736,7 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
 
     if(nslices > 0) {
         f32x4 ra[OA::F4], rb[OB::F4];
-        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, ldsA[0], ldsB[0]);
+        prologue<AK, BKF, EDGE, T, EPI == kEpiSwigluFwd>(p, job, ra, rb, ldsA[0], ldsB[0]);
         __syncthreads();
         float fa0[TM][4], fb0[TN][4], fa1[TM][4], fb1[TN][4];
         read_group<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
@@ -702,21 +754,24 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
             // group 0: read group 1, stage part 0
             read_group<TM>(la, ar0, lr, lh, 1, fa1);
             read_group<TN>(lb, br0, lr, lh, 1, fb1);
-            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            stage<AK, BKF, EDGE, T, 0, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
+                                                             kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
             interleave<NMFMA, RD + S::group_ops(0)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 1: read group 2, stage part 1
             read_group<TM>(la, ar0, lr, lh, 2, fa0);
             read_group<TN>(lb, br0, lr, lh, 2, fb0);
-            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            stage<AK, BKF, EDGE, T, 1, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
+                                                             kend);
             mfma_group<TM, TN>(acc, fa1, fb1);
             interleave<NMFMA, RD + S::group_ops(1)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 2: read group 3, stage part 2
             read_group<TM>(la, ar0, lr, lh, 3, fa1);
             read_group<TN>(lb, br0, lr, lh, 3, fb1);
-            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, A, B, p, row0, col0, kn, kend);
+            stage<AK, BKF, EDGE, T, 2, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
+                                                             kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
             interleave<NMFMA, RD + S::group_ops(2)>();
             __builtin_amdgcn_sched_barrier(0);
@@ -803,7 +858,7 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
 
     if(nslices > 0) {
         f32x4 ra[OA::F4], rb[OB::F4];
-        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, reinterpret_cast<EA*>(ldsA[0]),
+        prologue<AK, BKF, EDGE, T, EPI == kEpiSwigluFwd>(p, job, ra, rb, reinterpret_cast<EA*>(ldsA[0]),
                                    reinterpret_cast<EB*>(ldsB[0]));
         __syncthreads();
         // fragments of step 0 / step 1 (and their lo parts when SPLIT)
@@ -836,11 +891,11 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_bf16_kernel(GemmParams p) {
             const int64_t kn = job.kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
             // step 0: read step 1, stage slice s+1 and fetch s+2
             read(ldsA[cur], ldsB[cur], 1, fa1, fb1, la1, lb1);
-            stage<AK, BKF, EDGE, T, 0>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+            stage<AK, BKF, EDGE, T, 0, EPI == kEpiSwigluFwd>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
                                        job.A, job.B, p, job.row0, job.col0, kn, job.kend);
-            stage<AK, BKF, EDGE, T, 1>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+            stage<AK, BKF, EDGE, T, 1, EPI == kEpiSwigluFwd>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
                                        job.A, job.B, p, job.row0, job.col0, kn, job.kend);
-            stage<AK, BKF, EDGE, T, 2>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
+            stage<AK, BKF, EDGE, T, 2, EPI == kEpiSwigluFwd>(ra, rb, reinterpret_cast<EA*>(sa), reinterpret_cast<EB*>(sb),
                                        job.A, job.B, p, job.row0, job.col0, kn, job.kend);
             mma(fa0, fb0, la0, lb0);
             interleave<NMFMA, RD + STAGE_OPS>();
@@ -917,7 +972,7 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_fp8_kernel(GemmParams p) {
 
     if(nslices > 0) {
         f32x4 ra[OA::F4], rb[OB::F4];
-        prologue<AK, BKF, EDGE, T>(p, job, ra, rb, reinterpret_cast<Fp8A*>(ldsA0),
+        prologue<AK, BKF, EDGE, T, EPI == kEpiSwigluFwd>(p, job, ra, rb, reinterpret_cast<Fp8A*>(ldsA0),
                                    reinterpret_cast<Fp8B*>(ldsB[0]));
         __syncthreads();
         long fa0[TM], fb0[TN], fa1[TM], fb1[TN];
@@ -941,11 +996,11 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_fp8_kernel(GemmParams p) {
             // step 0: read step 1, stage slice s+1 and fetch s+2
             read_step8<TM>(la, ar0, lr, lh, 1, fa1);
             read_step8<TN>(ldsB[cur], br0, lr, lh, 1, fb1);
-            stage<AK, BKF, EDGE, T, 0>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+            stage<AK, BKF, EDGE, T, 0, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
                                        job.kend);
-            stage<AK, BKF, EDGE, T, 1>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+            stage<AK, BKF, EDGE, T, 1, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
                                        job.kend);
-            stage<AK, BKF, EDGE, T, 2>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
+            stage<AK, BKF, EDGE, T, 2, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, job.A, job.B, p, job.row0, job.col0, kn,
                                        job.kend);
             mma(fa0, fb0);
             interleave<NMFMA, RD + STAGE_OPS>();
@@ -1013,27 +1068,32 @@ struct TileChoice {
     int bm, bn;
 };
 
-TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all) {
+// pair_F > 0 (the SwiGLU-forward product): only shapes whose half width
+// divides pair_F, so every tile holds whole gate/up column pairs; bm = 0 when
+// none does.
+TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all, int64_t pair_F = 0) {
     auto cost = [&](int bm, int bn, double units) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
         return units * (double)((tiles + kCUs - 1) / kCUs);
     };
+    auto fits = [&](int bn) { return pair_F == 0 || pair_F % (bn / 2) == 0; };
     TileChoice best = {kTile128, 128, 128};
-    double c = cost(128, 128, 1.0);
+    double c = fits(128) ? cost(128, 128, 1.0) : 1e300;
+    if(!fits(128)) best.bm = 0;
     auto consider = [&](TileKind k, int bm, int bn, double ck) {
         if(ck < c) {
             c = ck;
             best = {k, bm, bn};
         }
     };
-    if(N % 96 == 0) consider(kTile96, 128, 96, cost(128, 96, 0.75));
+    if(N % 96 == 0 && fits(96)) consider(kTile96, 128, 96, cost(128, 96, 0.75));
     if(allow_all) {
-        consider(kTile64, 64, 64, cost(64, 64, 0.25) * 1.2);
-        if(N % 96 == 0 && cost(256, 96, 1.5) / 1.05 <= c) {
+        if(fits(64)) consider(kTile64, 64, 64, cost(64, 64, 0.25) * 1.2);
+        if(N % 96 == 0 && fits(96) && cost(256, 96, 1.5) / 1.05 <= c) {
             c = cost(256, 96, 1.5) / 1.05;
             best = {kTile256x96, 256, 96};
         }
-        if(cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
+        if(fits(256) && cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
     }
     return best;
 }
@@ -1112,14 +1172,16 @@ void launch_epi(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
 }
 
 // The staged epilogues are instantiated only where they are used: the
-// residual add for 'N','N' (x + a.W), the SwiGLU backward for 'N','T'
-// (dY . W2^T); gemm_impl refuses other combinations.
+// residual add and the SwiGLU forward for 'N','N' (x + a.W, x.[W1 | W3]), the
+// SwiGLU backward for 'N','T' (dY . W2^T); gemm_impl refuses other
+// combinations.
 template <bool TA, bool TB, class T, int EDGE>
 void launch_kernel(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
     if constexpr(!TA && TB) {
         if(gp.sg_a) return launch_epi<TA, TB, T, EDGE, kEpiSwiglu>(gp, grid, prec, st);
     }
     if constexpr(!TA && !TB) {
+        if(gp.sf_h) return launch_epi<TA, TB, T, EDGE, kEpiSwigluFwd>(gp, grid, prec, st);
         if(gp.Cin) return launch_epi<TA, TB, T, EDGE, kEpiAdd>(gp, grid, prec, st);
     }
     launch_epi<TA, TB, T, EDGE, kEpiPlain>(gp, grid, prec, st);
@@ -1162,6 +1224,8 @@ struct Epilogue {
     float *sg_da = nullptr, *sg_du = nullptr;
     int64_t sg_lda = 0, sg_ldu = 0, sg_ldd = 0;
     int sg_flags = 0;
+    float* sf_h = nullptr;  // SwiGLU forward: h [M, N/2]
+    int64_t sf_ldh = 0;
 };
 
 int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
@@ -1179,7 +1243,7 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     if(causal < 0 || causal > 3) return pk::fail("pk_gemm_f32: causal mode %d not in 0..3", causal);
     if(inner_count < 1) return pk::fail("pk_gemm_f32: inner_count must be >= 1");
     if(M == 0 || N == 0 || batch == 0) return PK_OK;
-    const bool swiglu = epi.sg_a != nullptr;
+    const bool swiglu = epi.sg_a != nullptr, sfwd = epi.sf_h != nullptr;
     if(!C && !swiglu) return pk::fail("pk_gemm_f32: C is NULL");
     if(K > 0 && (!A || !B)) return pk::fail("pk_gemm_f32: A or B is NULL");
     const int64_t a_cols = TA ? M : K, b_cols = TB ? K : N;
@@ -1228,11 +1292,27 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     gp.sg_ldd = epi.sg_ldd;
     gp.sg_flags = epi.sg_flags;
     gp.fp8_scale = prec == kFp8 ? epi.fp8_scale : nullptr;
+    gp.pair_F = 0;
+    gp.sf_h = nullptr;
+    gp.sf_ldh = 0;
+    if(sfwd) {
+        if(TA || TB || batch != 1 || causal != 0 || beta != 0.0f || !own_c)
+            return pk::fail("pk_gemm_swiglu_fwd_f32: only the plain ('N','N') product is built");
+        if(N % 8 != 0)
+            return pk::fail("pk_gemm_swiglu_fwd_f32: N=%lld must be 2F with F a multiple of 4",
+                            (long long)N);
+        if(epi.sf_ldh < N / 2)
+            return pk::fail("pk_gemm_swiglu_fwd_f32: ldh=%lld < F=%lld", (long long)epi.sf_ldh,
+                            (long long)(N / 2));
+        gp.pair_F = N / 2;
+        gp.sf_h = epi.sf_h;
+        gp.sf_ldh = epi.sf_ldh;
+    }
     hipStream_t st = pk::as_stream(stream);
     gp.splits = 1;
     gp.kchunk = K;
     gp.ws = nullptr;
-    if(batch == 1 && causal == 0 && ws && K > 0 && !swiglu) {
+    if(batch == 1 && causal == 0 && ws && K > 0 && !swiglu && !sfwd) {
         int64_t kchunk;
         const int S = choose_splits(M, N, K, &kchunk);
         if(S > 1 && ws_bytes >= (size_t)S * (size_t)M * (size_t)N * sizeof(float)) {
@@ -1246,12 +1326,15 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     };
     gp.epi_vec = v4(C, ldc) && v4(gp.Cin, gp.ldcin) && v4(gp.sg_a, gp.sg_lda) &&
                  v4(gp.sg_u, gp.sg_ldu) && v4(gp.sg_da, gp.sg_ldd) && v4(gp.sg_du, gp.sg_ldd) &&
-                 (gp.splits == 1 || v4(gp.ws, N));
+                 v4(gp.sf_h, gp.sf_ldh) && (gp.splits == 1 || v4(gp.ws, N));
     // split products keep 128x128 tiles (the split count is sized for them);
     // causal products keep 128-row tiles (the attention chain's diagonal logic
     // is exercised at that size)
     const TileChoice tc = gp.splits > 1 ? TileChoice{kTile128, 128, 128}
-                                        : pick_tile(M, N, batch, causal == 0);
+                                        : pick_tile(M, N, batch, causal == 0, gp.pair_F);
+    if(tc.bm == 0)
+        return pk::fail("pk_gemm_swiglu_fwd_f32: F=%lld is not a multiple of 32 (no tile holds "
+                        "whole gate/up column pairs)", (long long)gp.pair_F);
     const int64_t tiles_m = (M + tc.bm - 1) / tc.bm, tiles_n = (N + tc.bn - 1) / tc.bn;
     if(tiles_m * tiles_n > (int64_t)1 << 30)
         return pk::fail("pk_gemm_f32: problem too large for one launch");
@@ -1474,6 +1557,21 @@ extern "C" int pk_gemm_swiglu_bwd_f32(char ta, char tb, int64_t M, int64_t N, in
     e.sg_flags = flags & (PK_ACCUM | PK_ACCUM2);
     return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, 0.0f, nullptr, N, 0, 0, 1,
                      1, 0, nullptr, 0, prec, stream, e);
+}
+
+extern "C" int pk_gemm_swiglu_fwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K,
+                                      float alpha, const float* A, int64_t lda, const float* B,
+                                      int64_t ldb, float* C, int64_t ldc, float* h, int64_t ldh,
+                                      int precision, const float* fp8_scales, pk_stream_t stream) {
+    const int prec = prec_of(precision, "pk_gemm_swiglu_fwd_f32");
+    if(prec < 0) return PK_EINVAL;
+    if(M > 0 && N > 0 && (!C || !h)) return pk::fail("pk_gemm_swiglu_fwd_f32: NULL C or h");
+    Epilogue e;
+    e.fp8_scale = fp8_scales;
+    e.sf_h = h;
+    e.sf_ldh = ldh;
+    return gemm_impl(ta, tb, M, N, K, alpha, A, lda, 0, 0, B, ldb, 0, 0, 0.0f, C, ldc, 0, 0, 1, 1,
+                     0, nullptr, 0, prec, stream, e);
 }
 
 // ---- pk_gemm_noalloc_f32: the split-K GEMM without a caller workspace ------

@@ -113,7 +113,8 @@ struct PicoTensor* pico_gpt_loss(struct PicoGPT* m, const int32_t* tokens,
         if(!x) return NULL;
         h = pico_rmsnorm(x, L->g_ffn, eps);
         if(!h) return NULL;
-        struct PicoTensor* gu = pico_matmul(h, L->w13);
+        /* [gate | up] = h.W13; the product also writes silu(gate) * up */
+        struct PicoTensor* gu = pico_matmul_gate_up(h, L->w13);
         struct PicoTensor* gu2[2];
         if(!gu || pico_split_cols(gu, 2, gu2)) return NULL;
         /* x + swiglu(gate, up).W2; the backward's dY.W2^T writes d(gate), d(up) */

@@ -473,10 +473,88 @@ struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
     return out;
 }
 
+/* The gate/up projection of a SwiGLU block (no reference counterpart): out =
+ * a . w for w = [W1 | W3] (two column halves), a matmul to autograd.  Its
+ * product also writes h = silu(out[:, :F]) * out[:, F:] from the tiles
+ * (pk_gemm_swiglu_fwd_f32: each tile holds matching gate and up columns), and
+ * the node keeps h: pico_swiglu_matmul_add over the two column views of out
+ * (pico_split_cols(out, 2)) takes it instead of running the SwiGLU kernel.
+ * Shapes the paired product does not take (a transposed view, F not a
+ * multiple of 32) run the plain product and keep nothing. */
+enum { GU_H = 0 };
+enum { GU_MARK = 0 };
+#define PKH_GU_MARK 0x53574947 /* "GIWS": this node holds h */
+
+struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* w) {
+    if(!a || !w) {
+        PKH_ERR("pico_matmul_gate_up: NULL tensor!\n");
+        return NULL;
+    }
+    if(a->ndim != 2 || w->ndim != 2 || a->shape[1] != w->shape[0]) {
+        PKH_ERR("2d matmul matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->backend != w->backend) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu("pico_matmul_gate_up", a)) return NULL;
+    const int64_t M = a->shape[0], K = a->shape[1], N = w->shape[1], F = N / 2;
+    if(N % 2) {
+        PKH_ERR("pico_matmul_gate_up: w must have an even number of columns [W1 | W3]!\n");
+        return NULL;
+    }
+    struct PkMat va, vw;
+    if(matmul_views(a, w, &va, &vw)) return NULL;
+    int64_t shape[2] = {M, N};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    float* h = NULL;
+    if(va.t == 'N' && vw.t == 'N' && F % 32 == 0 && M > 0 && K > 0 && F > 0) {
+        h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F));
+        if(!h) return NULL;
+        float* scales = NULL;
+        if(g_matmul_precision == PICO_MATMUL_FP8) {
+            scales = (float*)pkh_workspace(FP8_SCALE_BYTES);
+            int st8 = scales ? fp8_scales_for(va, vw, M, N, K, scales, pkh_stream()) : PK_EINVAL;
+            if(pkh_status("pico_matmul_gate_up", st8)) return NULL;
+        }
+        int st = pk_gemm_swiglu_fwd_f32('N', 'N', M, N, K, 1.0f, va.p, va.ld, vw.p, vw.ld,
+                                        out->data, N, h, F, g_matmul_precision, scales,
+                                        pkh_stream());
+        if(pkh_status("pico_matmul_gate_up", st)) return NULL;
+    } else if(pico_matmul_gpu(a, w, out)) {
+        return NULL;
+    }
+    struct PkNode* n = pkh_node(out);
+    n->saved[GU_H] = h;
+    n->ival[GU_MARK] = h ? PKH_GU_MARK : 0;
+    struct PicoTensor* ps[2] = {a, w};
+    pkh_set_parents(arena, out, 2, ps, pico_matmul_backward_gpu);
+    return out;
+}
+
+/* h that pico_matmul_gate_up kept for exactly these two column views, else NULL */
+static const float* gate_up_h(struct PicoTensor* gate, struct PicoTensor* up) {
+    struct PkNode *gn = pkh_node(gate), *un = pkh_node(up);
+    if(!gn || !un || !gn->base || gn->base != un->base) return NULL;
+    struct PicoTensor* src = gn->base;
+    struct PkNode* sn = pkh_node(src);
+    const int64_t F = gate->shape[1];
+    if(!sn || sn->ival[GU_MARK] != PKH_GU_MARK || !sn->saved[GU_H] || src->ndim != 2 ||
+       src->shape[1] != 2 * F || src->shape[0] != gate->shape[0] || gate->data != src->data ||
+       up->data != src->data + F)
+        return NULL;
+    return (const float*)sn->saved[GU_H];
+}
+
 /* SwiGLU then a product: out = (c +) swiglu(gate, up) . w.  h = silu(gate) *
- * up is kept in the arena for the weight gradient; the backward never stores
- * dh: the input-gradient product dY . w^T writes the gate and up gradients
- * straight from its tiles (pk_gemm_swiglu_bwd_f32). */
+ * up is kept in the arena for the weight gradient (or taken from
+ * pico_matmul_gate_up, which made it); the backward never stores dh: the
+ * input-gradient product dY . w^T writes the gate and up gradients straight
+ * from its tiles (pk_gemm_swiglu_bwd_f32). */
 enum { SM_H = 0 };
 enum { SM_LD = 0, SM_RESID = 1 };
 
@@ -550,13 +628,17 @@ struct PicoTensor* pico_swiglu_matmul_add(struct PicoTensor* gate, struct PicoTe
         PKH_ERR("pico_swiglu_matmul_add: the added tensor must be a contiguous [M, N]!\n");
         return NULL;
     }
-    float* h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F > 0 ? M * F : 1));
-    if(!h) return NULL;
+    float* h = (float*)gate_up_h(gate, up);
     int64_t shape[2] = {M, N};
     struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
     if(!out) return NULL;
-    int st = pk_swiglu_fwd_f32(M, F, gate->data, ld, up->data, ld, h, F, pkh_stream());
-    if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;
+    int st;
+    if(!h) {
+        h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F > 0 ? M * F : 1));
+        if(!h) return NULL;
+        st = pk_swiglu_fwd_f32(M, F, gate->data, ld, up->data, ld, h, F, pkh_stream());
+        if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;
+    }
     struct PkMat vh = {h, 'N', F > 0 ? F : 1}, vw = {w->data, 'N', w->strides[0]};
     st = gemm_add_on(vh, vw, M, N, F, out->data, 'N', N > 0 ? N : 1, c ? 1.0f : 0.0f,
                      c ? c->data : NULL, c ? c->strides[0] : 0, pkh_stream(), 0);

@@ -122,6 +122,7 @@ _GPU_SIGS = {
     "pico_split_cols": (ctypes.c_int, [TP, ctypes.c_int, ctypes.POINTER(TP)]),
     "pico_matmul_add": (TP, [TP, TP, TP]),
     "pico_swiglu_matmul_add": (TP, [TP, TP, TP, TP]),
+    "pico_matmul_gate_up": (TP, [TP, TP]),
     "pico_set_matmul_precision": (ctypes.c_int, [ctypes.c_int]),
     "pico_get_matmul_precision": (ctypes.c_int, []),
     "pico_checkpoint_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(TP),

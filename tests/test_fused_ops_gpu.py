@@ -1,5 +1,6 @@
-"""Fused epilogues: pk_gemm_add_f32 / pk_gemm_swiglu_bwd_f32 (launcher layer)
-and the ops built on them, pico_matmul_add and pico_swiglu_matmul_add.
+"""Fused epilogues: pk_gemm_add_f32 / pk_gemm_swiglu_bwd_f32 /
+pk_gemm_swiglu_fwd_f32 (launcher layer) and the ops built on them,
+pico_matmul_add, pico_swiglu_matmul_add and pico_matmul_gate_up.
 
 Each fused path must equal the composition of the kernels it replaces bit for
 bit: the product is accumulated identically, and the epilogue applies the same
@@ -97,6 +98,68 @@ def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
         assert max_rel(out[:, F:], want_u) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,F", [(512, 768, 2048), (300, 96, 160), (200, 64, 96), (64, 40, 32),
+                                   (1000, 256, 384)])
+@pytest.mark.parametrize("prec", [0, 1, 2, 3])
+def test_gemm_swiglu_fwd_equals_product_then_swiglu(dev, M, K, F, prec):
+    """C = A.[W1 | W3] and h = silu(C[:, :F]) * C[:, F:] from one product,
+    against the plain product (pk_gemm_ex_*, the same multiplies) and the
+    SwiGLU row kernel on its two column views: C and h bit for bit (the
+    paired tiles -- 256x256, 128x96, 64x64 ... by F -- accumulate k in the
+    same order as every other tile)"""
+    L = _lib.hip_lib()
+    A = _t(O.uniform(M * K, 51).reshape(M, K), dev)
+    W = _t(O.uniform(K * 2 * F, 52).reshape(K, 2 * F) * 0.2, dev)
+    C = torch.full((M, 2 * F), float("nan"), device=dev)
+    h = torch.full((M, F), float("nan"), device=dev)
+    _lib.check("pk_gemm_swiglu_fwd_f32", L.pk_gemm_swiglu_fwd_f32(
+        b"N", b"N", M, 2 * F, K, 1.0, A.data_ptr(), K, W.data_ptr(), 2 * F, C.data_ptr(), 2 * F,
+        h.data_ptr(), F, prec, None, None))
+    ref = torch.empty(M, 2 * F, device=dev)
+    fn = {0: L.pk_gemm_ex_f32, 1: L.pk_gemm_ex_bf16_f32, 2: L.pk_gemm_ex_bf16x3_f32,
+          3: L.pk_gemm_ex_fp8_f32}[prec]
+    _lib.check("pk_gemm_ex", fn(b"N", b"N", M, 2 * F, K, 1.0, A.data_ptr(), K, W.data_ptr(),
+                                2 * F, 0.0, ref.data_ptr(), 2 * F, None, 0, None))
+    href = torch.empty(M, F, device=dev)
+    _lib.check("pk_swiglu_fwd_f32", L.pk_swiglu_fwd_f32(
+        M, F, ref.data_ptr(), 2 * F, ref.data_ptr() + 4 * F, 2 * F, href.data_ptr(), F, None))
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref)
+    assert torch.equal(h, href)
+    if prec == 0 and M <= 512:
+        c64 = O.gemm_ref_f64("N", "N", A.cpu().numpy(), W.cpu().numpy())
+        assert max_rel(C.cpu().numpy(), c64) <= 1e-5
+        want = O.swiglu_fwd(c64[:, :F].astype(np.float32), c64[:, F:].astype(np.float32))
+        assert max_rel(h.cpu().numpy(), want) <= 1e-4
+
+
+def test_gemm_swiglu_fwd_strided_h_and_refusals(dev):
+    L = _lib.hip_lib()
+    M, K, F = 96, 64, 128
+    A = _t(O.uniform(M * K, 61).reshape(M, K), dev)
+    W = _t(O.uniform(K * 2 * F, 62).reshape(K, 2 * F), dev)
+    C = torch.empty(M, 2 * F, device=dev)
+    hbuf = torch.full((M, F + 36), -7.0, device=dev)  # h with row stride F + 36
+    _lib.check("pk_gemm_swiglu_fwd_f32", L.pk_gemm_swiglu_fwd_f32(
+        b"N", b"N", M, 2 * F, K, 1.0, A.data_ptr(), K, W.data_ptr(), 2 * F, C.data_ptr(), 2 * F,
+        hbuf.data_ptr(), F + 36, 0, None, None))
+    href = torch.empty(M, F, device=dev)
+    _lib.check("pk_swiglu_fwd_f32", L.pk_swiglu_fwd_f32(
+        M, F, C.data_ptr(), 2 * F, C.data_ptr() + 4 * F, 2 * F, href.data_ptr(), F, None))
+    torch.cuda.synchronize()
+    assert torch.equal(hbuf[:, :F], href)
+    assert bool((hbuf[:, F:] == -7.0).all())  # the padding is untouched
+
+    def call(ta, tb, N, ldh):
+        return L.pk_gemm_swiglu_fwd_f32(ta, tb, M, N, K, 1.0, A.data_ptr(), K, W.data_ptr(),
+                                        2 * F, C.data_ptr(), 2 * F, hbuf.data_ptr(), ldh, 0, None,
+                                        None)
+    assert call(b"N", b"T", 2 * F, F) == -1 and b"N','N'" in L.pk_last_error()
+    assert call(b"N", b"N", 2 * F - 4, F) == -1  # N not 2F with F a multiple of 4
+    assert call(b"N", b"N", 200, 100) == -1 and b"multiple of 32" in L.pk_last_error()
+    assert call(b"N", b"N", 2 * F, F - 1) == -1 and b"ldh" in L.pk_last_error()
+
+
 def test_gemm_swiglu_bwd_refuses_other_layouts(dev):
     L = _lib.hip_lib()
     x = torch.zeros(64, 64, device=dev)
@@ -144,7 +207,7 @@ def test_matmul_add_equals_composition(P, M, K, N, b_param):
     assert np.array_equal(fused[3], sg.ravel())
 
 
-def _run_swiglu_mm(P, fused, xv, w13v, w2v, cv, seed_grad, split):
+def _run_swiglu_mm(P, fused, xv, w13v, w2v, cv, seed_grad, split, gate_up=False):
     M, d = xv.shape
     F = w2v.shape[0]
     with P.arena(1 << 27):
@@ -153,7 +216,8 @@ def _run_swiglu_mm(P, fused, xv, w13v, w2v, cv, seed_grad, split):
         w2 = P.param([F, w2v.shape[1]], w2v)
         c = P.tensor(list(cv.shape), cv) if cv is not None else None
         if split:
-            gate, up = P.split_cols(P.matmul(x, w13), 2)
+            gu = P.matmul_gate_up(x, w13) if gate_up else P.matmul(x, w13)
+            gate, up = P.split_cols(gu, 2)
         else:
             g_ = P.tensor([M, F], (xv @ w13v)[:, :F])
             u_ = P.tensor([M, F], (xv @ w13v)[:, F:])
@@ -174,14 +238,18 @@ def _run_swiglu_mm(P, fused, xv, w13v, w2v, cv, seed_grad, split):
 
 @pytest.mark.parametrize("M,d,F,N", [(128, 64, 160, 64), (300, 96, 200, 72), (1024, 768, 2048, 768)])
 @pytest.mark.parametrize("resid", [False, True])
-@pytest.mark.parametrize("split", [True, False])
-def test_swiglu_matmul_add_equals_composition(P, M, d, F, N, resid, split):
+@pytest.mark.parametrize("split,gate_up", [(True, False), (True, True), (False, False)])
+def test_swiglu_matmul_add_equals_composition(P, M, d, F, N, resid, split, gate_up):
+    """the fused path (gate_up: the projection by pico_matmul_gate_up, whose h
+    pico_swiglu_matmul_add then takes -- F = 200 is not a multiple of 32, so
+    there it is a plain product) against matmul, swiglu, matmul, add: outputs
+    and every gradient bit for bit"""
     xv = O.normal(M * d, 31).reshape(M, d)
     w13v = O.normal(d * 2 * F, 32, 0.0, 0.05).reshape(d, 2 * F)
     w2v = O.normal(F * N, 33, 0.0, 0.05).reshape(F, N)
     cv = O.normal(M * N, 34).reshape(M, N) if resid else None
     sg = O.normal(M * N, 35).reshape(M, N)
-    fused = _run_swiglu_mm(P, True, xv, w13v, w2v, cv, sg, split)
+    fused = _run_swiglu_mm(P, True, xv, w13v, w2v, cv, sg, split, gate_up)
     plain = _run_swiglu_mm(P, False, xv, w13v, w2v, cv, sg, split)
     assert len(fused) == len(plain)
     for i, (x, y) in enumerate(zip(fused, plain)):
