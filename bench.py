@@ -152,6 +152,19 @@ def attn_section(torch, K):
         out[name] = {"fwd_us": round(fwd * 1e3, 1), "bwd_us": round(bwd * 1e3, 1),
                      "fwd_tflops": round(4 * hd * pairs / (fwd * 1e-3) / 1e12, 1),
                      "bwd_tflops": round(10 * hd * pairs / (bwd * 1e-3) / 1e12, 1)}
+    # the same kernels on sequences 4x longer: 32 query blocks per head instead
+    # of 8, so the causal tail (the last, longest blocks) is a small part of
+    # the launch and the rate is the kernels' steady state
+    T4 = 4 * T
+    q, k, v, do = (torch.randn(B * T4, D, device=dev, generator=gen) for _ in range(4))
+    o, lse = torch.empty_like(q), torch.empty(B * H * T4, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    pairs4 = B * H * T4 * (T4 + 1) / 2
+    fwd, _ = _events_time(lambda: K.flash_fwd(B, H, q, k, v, o, lse), 5, 2)
+    bwd, _ = _events_time(lambda: K.flash_bwd(B, H, q, k, v, o, lse, do, dq, dk, dv), 5, 2)
+    out["fp32_T4096"] = {"seq_len": T4, "fwd_us": round(fwd * 1e3, 1), "bwd_us": round(bwd * 1e3, 1),
+                         "fwd_tflops": round(4 * hd * pairs4 / (fwd * 1e-3) / 1e12, 1),
+                         "bwd_tflops": round(10 * hd * pairs4 / (bwd * 1e-3) / 1e12, 1)}
     return out
 
 
