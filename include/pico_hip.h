@@ -37,6 +37,9 @@ typedef void* pk_stream_t; /* a hipStream_t; NULL is the null stream */
 /* pk_rmsnorm_bwd_into_f32 with dg == NULL: leave dg's partial sums in the
  * workspace for pk_rmsnorm_dg_reduce_f32 */
 #define PK_RMS_KEEP_PARTIALS 8
+/* pk_flash_attn_bwd_f32: recompute dQ's scores instead of passing dS through
+ * the workspace (which then holds only the row constants) */
+#define PK_FLASH_RECOMPUTE 16
 
 /* ---- runtime ---------------------------------------------------------- */
 const char* pk_last_error(void);
@@ -344,12 +347,18 @@ int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t 
  * whether these apply.  The backward needs pk_flash_attn_bwd_workspace(B, H,
  * T) bytes (per 64-query block: lse in base 2, then the row sums of dO*O)
  * and writes dv, then dk, then dq, each accumulating when its flags bit is
- * set (PK_ACCUM dq, PK_ACCUM2 dk, PK_ACCUM3 dv). */
+ * set (PK_ACCUM dq, PK_ACCUM2 dk, PK_ACCUM3 dv).  The dS tiles take about
+ * 2*B*H*T^2 bytes of that workspace; with PK_FLASH_RECOMPUTE in flags (fp32
+ * only) the dQ kernel recomputes the scores and dP block by block instead --
+ * three products per block rather than one, the same results bit for bit --
+ * and the workspace needs only pk_flash_attn_bwd_workspace_recompute(B, H, T)
+ * = 8*B*H*T bytes. */
 int pk_flash_attn_supported(int64_t T, int64_t hd);
 int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
                           float scale, const float* q, const float* k, const float* v, float* o,
                           float* lse, pk_stream_t stream);
 size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T);
+size_t pk_flash_attn_bwd_workspace_recompute(int64_t B, int64_t H, int64_t T);
 int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
                           float scale, const float* q, const float* k, const float* v,
                           const float* o, const float* lse, const float* dout, float* dq,

@@ -99,6 +99,7 @@ PK_SIGNATURES = {
     "pk_flash_attn_fwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
                                    c_p, c_p],
     "pk_flash_attn_bwd_workspace": [c_i64, c_i64, c_i64],
+    "pk_flash_attn_bwd_workspace_recompute": [c_i64, c_i64, c_i64],
     "pk_flash_attn_bwd_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p,
                               c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
     "pk_flash_attn_bwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
@@ -112,6 +113,7 @@ PK_SIGNATURES = {
 }
 _RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_size,
              "pk_gemm_workspace_f32": c_size, "pk_flash_attn_bwd_workspace": c_size,
+             "pk_flash_attn_bwd_workspace_recompute": c_size,
              "pk_embed_bwd_workspace": c_size, "pk_gemm_noalloc_scratch_bytes": c_size}
 
 _hip = None

@@ -395,7 +395,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
     // this lane's column of every dS tile of key group kg (rows 32 floats apart)
     const int64_t kg = k0 / 32;
-    float* dsk = p.ds + ds_tile(bh, p.T, 0, 0) + ((lq >> 2) & 1) * 16 + 4 * (lq >> 3) + (lq & 3);
+    float* dsk = p.ds ? p.ds + ds_tile(bh, p.T, 0, 0) + ((lq >> 2) & 1) * 16 + 4 * (lq >> 3) + (lq & 3)
+                      : nullptr;
 
     // iteration j reads buffer set st = (j - j0) & 1 and loads block j+1 into
     // the other one
@@ -446,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
                     }
                 }
                 const int64_t qg = 2 * j + sub;
-                if(qg >= kg) {
+                if(qg >= kg && dsk) {  // no tile store: the dQ kernel recomputes dS
                     float* t = dsk + (qg * (qg + 1) / 2 + kg) * 1024;
 #pragma unroll
                     for(int r = 0; r < 16; ++r) t[acc_row(r, lh) * 32] = dp[r];
@@ -544,6 +545,94 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
         }
     };
     for(int j = 0; j < nkv; ++j) iter(j, sK[j & 1], sK[(j + 1) & 1]);
+    store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
+}
+
+// ====================================================== backward: dQ, recomputed
+// The dQ kernel for callers whose workspace cannot hold the dS tiles (they take
+// about 2*B*H*T^2 bytes): each workgroup recomputes its queries' scores and
+// dP block by block instead of reading dS.  Workgroup: 128 queries of one
+// (b, h), one query per lane; K and V blocks of 64 stream through LDS one
+// block ahead.  Per block: S^T = K'.Q^T (K' = K * scale*log2(e), rounded as
+// the dK/dV kernel rounds its K fragment), dP^T = V.dO^T, dS = P*(dP - D),
+// dQ^T += K^T.dS^T.  Every product multiplies the same fp32 values in the same
+// order as the dK/dV kernel (whose lanes hold keys) and the stored-dS dQ
+// kernel, so dS and dQ come out bit for bit the same; it costs three products
+// per block where the stored path costs one.
+__device__ __forceinline__ f32x16 dot_rows_scaled(const float* lds, int sub, int lq, int lh,
+                                                  const float (&bf)[32], float mul) {
+    const f32x4* a4 = reinterpret_cast<const f32x4*>(lds + (sub * 32 + lq) * LDT + 32 * lh);
+    f32x16 acc = zero16();
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        const f32x4 a = a4[i];
+        acc = mfma(a[0] * mul, bf[4 * i + 0], acc);
+        acc = mfma(a[1] * mul, bf[4 * i + 1], acc);
+        acc = mfma(a[2] * mul, bf[4 * i + 2], acc);
+        acc = mfma(a[3] * mul, bf[4 * i + 3], acc);
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) float sK[2][TILE];
+    __shared__ __attribute__((aligned(16))) float sV[2][TILE];
+    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    // heaviest query blocks first, alternate passes of one workgroup per CU reversed
+    const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
+    const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
+    const int64_t rank = (pass & 1) ? lo + hi - 1 - blockIdx.x : blockIdx.x;
+    const int64_t qb = nqb - 1 - rank / BH, bh = rank % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq, qg = q0 / 32;
+
+    const BlockLoad blk(p.ld, w, l);
+    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.ld);
+    const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v + base, p.T, p.ld);
+    blk.issue(rk, p.ld, 0, sK[0], w);
+    blk.issue(rv, p.ld, 0, sV[0], w);
+    float qf[32], of[32];
+    load_frag32(p.q + base + qi * p.ld, lh, qf, 1.0f);
+    load_frag32(p.dout + obase + qi * p.D, lh, of, 1.0f);
+    // this query's L2 = lse*log2(e) and D = rowsum(dO*O) ([B*H][T/64][2][64])
+    const float* rc = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
+    const float L2 = rc[0], Dq = rc[BLK];
+    const float mul = p.scale * kLog2e;
+    f32x16 dq[2] = {zero16(), zero16()};
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
+    const int nw = (int)((q0 + 31) / BLK) + 1;  // key blocks this wave sees
+    for(int j = 0; j < nkv; ++j) {
+        const float* __restrict__ tk = sK[j & 1];
+        const float* __restrict__ tv = sV[j & 1];
+        wait_loads();
+        __syncthreads();  // block j is in; the other buffers (block j-1) are free
+        if(j + 1 < nkv) {
+            blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, sK[(j + 1) & 1], w);
+            blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
+        }
+        if(j >= nw) continue;
+        const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;  // key offset <= lim visible
+        const bool diag = (int64_t)j * BLK + BLK - 1 > q0;       // the block crosses the diagonal
+#pragma unroll
+        for(int sub = 0; sub < 2; ++sub) {
+            if(2 * j + sub > qg) continue;  // the whole key group is in this wave's future
+            const f32x16 sc = dot_rows_scaled(tk, sub, lq, lh, qf, mul);
+            const f32x16 dp = dot_rows(tv, sub, lq, lh, of, zero16());
+            f32x16 ds;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                const float pr = __builtin_amdgcn_exp2f(sc[r] - L2);
+                ds[r] = pr * (dp[r] - Dq);
+                if(diag && sub * 32 + 8 * (r >> 2) + (r & 3) > lim) ds[r] = 0.0f;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols(tk, sub, cb, lq, lh, ds, dq[cb]);
+        }
+    }
     store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
@@ -944,6 +1033,12 @@ extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
     return (size_t)(2 * B * H * T + B * H * ds_tiles(T) * 1024) * sizeof(float);
 }
 
+// the row constants only (PK_FLASH_RECOMPUTE)
+extern "C" size_t pk_flash_attn_bwd_workspace_recompute(int64_t B, int64_t H, int64_t T) {
+    if(B <= 0 || H <= 0 || T <= 0) return 0;
+    return (size_t)(2 * B * H * T) * sizeof(float);
+}
+
 namespace {
 
 int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
@@ -958,8 +1053,13 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     if(!pk::aligned16(o) || !pk::aligned16(dout) || !pk::aligned16(dq) || !pk::aligned16(dk) ||
        !pk::aligned16(dv))
         return pk::fail("%s: o, dout, dq, dk, dv must be 16-byte aligned", who);
-    if(!workspace || workspace_bytes < pk_flash_attn_bwd_workspace(B, H, T))
-        return pk::fail("%s: workspace needs %zu bytes", who, pk_flash_attn_bwd_workspace(B, H, T));
+    const bool recompute = (flags & PK_FLASH_RECOMPUTE) != 0;
+    if(recompute && bf16)
+        return pk::fail("%s: PK_FLASH_RECOMPUTE is built for the fp32 products only", who);
+    const size_t need = recompute ? pk_flash_attn_bwd_workspace_recompute(B, H, T)
+                                  : pk_flash_attn_bwd_workspace(B, H, T);
+    if(!workspace || workspace_bytes < need)
+        return pk::fail("%s: workspace needs %zu bytes", who, need);
     if(!pk::aligned16(workspace)) return pk::fail("%s: workspace must be 16-byte aligned", who);
     FlashParams p = {};
     p.q = q;
@@ -973,14 +1073,14 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.dv = dv;
     p.dsum = static_cast<const float*>(workspace);
     p.dsum_out = static_cast<float*>(workspace);
-    p.ds = static_cast<float*>(workspace) + 2 * B * H * T;
+    p.ds = recompute ? nullptr : static_cast<float*>(workspace) + 2 * B * H * T;
     p.B = B;
     p.H = H;
     p.T = T;
     p.D = H * HD;
     p.ld = ld;
     p.scale = scale;
-    p.flags = flags;
+    p.flags = flags & (PK_ACCUM | PK_ACCUM2 | PK_ACCUM3);
     hipStream_t st = pk::as_stream(stream);
     flash_dsum<<<pk::grid_for(B * H * T * 16, 256), 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
@@ -992,6 +1092,8 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     if((rc = pk::launch_status(who))) return rc;
     if(bf16)
         flash_bwd_dq_bf16<<<grid, 256, 0, st>>>(p);
+    else if(recompute)
+        flash_bwd_dq_recompute<<<grid, 256, 0, st>>>(p);
     else
         flash_bwd_dq<<<grid, 256, 0, st>>>(p);
     return pk::launch_status(who);

@@ -9,6 +9,7 @@
  * state (rstd, lse, probabilities, staged labels) lives in the node and in
  * the arena's device memory, so it is released by arena_reset.
  */
+#include <stdlib.h>
 #include <math.h>
 #include <string.h>
 
@@ -234,10 +235,25 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
  * T a multiple of 128 the fused kernels run (pk_flash_attn_*): only lse
  * [B*H*T] is saved, and the forward never writes scores or probabilities;
  * the backward passes dS from its dK/dV kernel to its dQ kernel as 32x32 tiles
- * of each head's causal triangle in a workspace of about 2*B*H*T^2 bytes.  Otherwise the chain of
+ * of each head's causal triangle in a workspace of about 2*B*H*T^2 bytes.  Above
+ * attn_ds_cap() bytes of tiles the fp32 backward recomputes dQ's scores
+ * instead (PK_FLASH_RECOMPUTE: a workspace of 8*B*H*T bytes, the same
+ * results).  Otherwise the chain of
  * batched GEMMs and causal-softmax kernels runs and saves the probabilities
  * P [B*H, T, T] (arena device memory). */
 enum { AS_LSE = 0, AS_P = 1 };
+/* largest dS-tile workspace the fused backward takes: 4 GiB (B*H*T^2 up to
+ * about 2^31; 8 x 12 heads at T 8192 recompute), or PICO_ATTN_DS_CAP bytes
+ * from the environment */
+static size_t attn_ds_cap(void) {
+    const char* e = getenv("PICO_ATTN_DS_CAP");
+    if(e && *e) {
+        char* end = NULL;
+        unsigned long long v = strtoull(e, &end, 10);
+        if(end && *end == '\0') return (size_t)v;
+    }
+    return (size_t)4 << 30;
+}
 enum { AI_B = 0, AI_H = 1, AI_FLASH = 2, AI_BF16 = 3 };
 
 static void attn_backward(struct PicoTensor* self) {
@@ -247,9 +263,11 @@ static void attn_backward(struct PicoTensor* self) {
     if(!dout) return;
     int64_t B = n->ival[AI_B], H = n->ival[AI_H];
     int64_t T = q->shape[0] / B, hd = q->shape[1] / H, ld = q->strides[0];
-    const int flash = (int)n->ival[AI_FLASH];
+    const int flash = (int)n->ival[AI_FLASH], bf16 = flash && n->ival[AI_BF16];
     size_t ws_bytes = flash ? pk_flash_attn_bwd_workspace(B, H, T)
                             : sizeof(float) * (size_t)(B * H * T * T);
+    const int recompute = flash && !bf16 && ws_bytes > attn_ds_cap();
+    if(recompute) ws_bytes = pk_flash_attn_bwd_workspace_recompute(B, H, T);
     void* ws = pkh_workspace(ws_bytes);
     if(!ws) {
         pkh_set_error("pico_attention_causal_backward: no device workspace of %zu bytes; the q, "
@@ -263,14 +281,14 @@ static void attn_backward(struct PicoTensor* self) {
      * dq (fused) or dv, dq, dk (chain) */
     struct PicoTensor* order[3] = {v, flash ? k : q, flash ? q : k};
     const int bit[3] = {PK_ACCUM3, flash ? PK_ACCUM2 : PK_ACCUM, flash ? PK_ACCUM : PK_ACCUM2};
-    int flags = 0;
+    int flags = recompute ? PK_FLASH_RECOMPUTE : 0;
     for(int i = 0; i < 3; i++) {
         if(pkh_grad_flag(order[i])) flags |= bit[i];
         pkh_grad_mark(order[i]);
     }
     int st;
     if(flash)
-        st = (n->ival[AI_BF16] ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
+        st = (bf16 ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
             B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, self->data,
             (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad, ws, ws_bytes, flags,
             pkh_stream());

@@ -389,12 +389,22 @@ def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False):
         B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
 
 
-def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False):
+FLASH_RECOMPUTE = 16
+
+
+def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False,
+              recompute=False):
+    """recompute: PK_FLASH_RECOMPUTE, dQ from recomputed scores (a workspace of
+    the row constants only)"""
     T, hd, ld = _attn_layout(B, H, q, k, v, o, dq, dk, dv)
     if not dout.is_contiguous() or dout.shape != o.shape:
         raise ValueError("attention: dout must be contiguous like o")
     scale = hd ** -0.5 if scale is None else scale
-    need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
+    if recompute:
+        flags |= FLASH_RECOMPUTE
+        need = int(hip_lib().pk_flash_attn_bwd_workspace_recompute(B, H, T))
+    else:
+        need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
     ws = torch.empty(max(1, need // 4), device=q.device, dtype=torch.float32)
     name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
     check(name, getattr(hip_lib(), name)(

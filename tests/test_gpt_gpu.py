@@ -77,6 +77,37 @@ def test_small_model_loss_and_grads(P):
                         seq_len=64), 11)
 
 
+def test_attention_recompute_path_in_a_step(P, monkeypatch):
+    """PICO_ATTN_DS_CAP=0 sends every fused attention backward down the
+    recompute path (no dS tiles): loss and every gradient equal the default
+    step's bit for bit, and the oracle's within the tolerance"""
+    cfg = dict(vocab=96, d_model=128, n_layers=2, n_heads=2, d_ff=160, batch=2, seq_len=128)
+    model = P.gpt_init(cfg, 71)
+    # an optimizer only to zero the parameters' grads between the two steps
+    opt = P.optim_adamw_init(ADAMW["lr"], ADAMW["b1"], ADAMW["b2"], ADAMW["eps"], ADAMW["wd"])
+    try:
+        for t in P.gpt_params(model):
+            P.optim_adamw_add(opt, t)
+        tokens, targets, _ = _batch(cfg, 72)
+        monkeypatch.delenv("PICO_ATTN_DS_CAP", raising=False)
+        P.optim_adamw_zero_grad(opt)
+        loss0, g0 = _gpu_step(P, model, tokens, targets)
+        monkeypatch.setenv("PICO_ATTN_DS_CAP", "0")
+        P.optim_adamw_zero_grad(opt)
+        loss1, g1 = _gpu_step(P, model, tokens, targets)
+        monkeypatch.delenv("PICO_ATTN_DS_CAP")
+        assert loss0 == loss1
+        for a, b in zip(g0, g1):
+            assert np.array_equal(a, b)
+        ref_loss, ref_grads = G.loss_and_grads(_host_params(P, model, cfg), cfg, tokens, targets)
+        assert abs(loss1 - ref_loss) <= TOL * abs(ref_loss)
+        for g, r in zip(G.split_fused(g1, cfg), ref_grads):
+            assert max_rel(g.ravel(), r.ravel()) <= TOL
+    finally:
+        P.optim_adamw_free(opt)
+        P.gpt_free(model)
+
+
 def test_config4_one_step_loss_and_grads(P):
     _check_step(P, CONFIG4, 21)
 

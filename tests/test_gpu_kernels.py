@@ -469,6 +469,60 @@ def test_flash_attention_vs_oracle(dev, B, H, T):
         assert max_rel(host(got) - b0, ref) <= TOL
 
 
+@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (8, 12, 1024)])
+def test_flash_attention_recompute_dq_equals_stored_ds(dev, B, H, T):
+    """PK_FLASH_RECOMPUTE (dQ from recomputed scores, no dS tiles) against the
+    stored-dS backward: dq, dk and dv bit for bit, plain and accumulating, and
+    within the tolerance of the oracle; q, k, v as column views of one fused
+    projection"""
+    hd, D = 64, H * 64
+    q, k, v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (31, 32, 33, 34))
+    qkv = cu(np.concatenate([q, k, v], 1))
+    qv, kv, vv = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    o = torch.empty(B * T, D, device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    K.flash_fwd(B, H, qv, kv, vv, o, lse)
+    outs = []
+    for rc in (False, True):
+        g = torch.full((B * T, 3 * D), float("nan"), device=dev)
+        K.flash_bwd(B, H, qv, kv, vv, o, lse, cu(do), g[:, :D], g[:, D:2 * D], g[:, 2 * D:],
+                    recompute=rc)
+        base = O.normal(B * T * 3 * D, 40).reshape(B * T, 3 * D)
+        a = cu(base.copy())
+        K.flash_bwd(B, H, qv, kv, vv, o, lse, cu(do), a[:, :D], a[:, D:2 * D], a[:, 2 * D:],
+                    flags=7, recompute=rc)
+        outs.append((host(g), host(a)))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+    if T <= 384:
+        refs = O.attn_bwd(B, H, q, k, v, host(o), host(lse), do)
+        for i, ref in enumerate(refs):
+            assert max_rel(outs[1][0][:, i * D:(i + 1) * D], ref) <= TOL
+
+
+def test_flash_attention_recompute_workspace_and_refusal(dev):
+    from pico_amd import _lib
+    L = _lib.hip_lib()
+    B, H, T = 2, 3, 256
+    assert L.pk_flash_attn_bwd_workspace_recompute(B, H, T) == 8 * B * H * T
+    assert L.pk_flash_attn_bwd_workspace(B, H, T) > 8 * B * H * T
+    D = H * 64
+    x = torch.zeros(B * T, D, device=dev)
+    lse = torch.zeros(B * H * T, device=dev)
+    ws = torch.empty(2 * B * H * T, device=dev)
+    for bf16 in (False, True):
+        name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
+        # the row-constant workspace is enough for the recompute path only
+        st = getattr(L, name)(B, H, T, 64, D, 0.125, *([x.data_ptr()] * 3), x.data_ptr(),
+                              lse.data_ptr(), x.data_ptr(), *([x.data_ptr()] * 3),
+                              ws.data_ptr(), ws.numel() * 4, 0, None)
+        assert st == -1 and b"workspace" in L.pk_last_error()
+    st = L.pk_flash_attn_bwd_bf16_f32(B, H, T, 64, D, 0.125, *([x.data_ptr()] * 3), x.data_ptr(),
+                                      lse.data_ptr(), x.data_ptr(), *([x.data_ptr()] * 3),
+                                      ws.data_ptr(), ws.numel() * 4, 16, None)
+    assert st == -1 and b"fp32" in L.pk_last_error()
+
+
 @pytest.mark.parametrize("flash", [True, False])
 def test_attention_strided_qkv_views(dev, flash):
     # q, k, v (and dq, dk, dv) as the column blocks of one [B*T, 3*H*hd]
