@@ -42,6 +42,7 @@ struct FlashParams {
     float *out, *lse_out, *dq, *dk, *dv, *dsum_out;
     float* ds;  // dS tiles: written by the dK/dV kernel, read by the dQ kernel
     int64_t B, H, T, D;  // D = H*64: row stride of o, dout (and the output)
+    int64_t Tp;          // T rounded up to 128: the grid and workspace layout
     int64_t ld;          // row stride of q, k, v and dq, dk, dv (>= D)
     float scale;         // softmax scale (normally 1/8)
     int flags;
@@ -63,7 +64,12 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 
 // 32 consecutive floats of one row: the lane's k-slots 32*h .. 32*h+31
 __device__ __forceinline__ void load_frag32(const float* __restrict__ row, int h, float (&f)[32],
-                                            float mul) {
+                                            float mul, bool ok = true) {
+    if(!ok) {  // a row past the sequence's end (T not a multiple of 128): zeros
+#pragma unroll
+        for(int i = 0; i < 32; ++i) f[i] = 0.0f;
+        return;
+    }
     const f32x4* p = reinterpret_cast<const f32x4*>(row + 32 * h);
 #pragma unroll
     for(int i = 0; i < 8; ++i) {
@@ -195,7 +201,7 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70
 __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
     __shared__ __attribute__((aligned(16))) float sV[2][TILE];
-    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
     const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
     const int64_t rank = (pass & 1) ? lo + hi - 1 - blockIdx.x : blockIdx.x;
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     blk.issue(rv, p.ld, 0, sV[0], w);
     blk.issue(rk, p.ld, BLK, sK[1], w);  // nkv >= 2 since T % 128 == 0
     float qf[32];
-    load_frag32(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
+    load_frag32(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
     wait_loads();
@@ -301,6 +307,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
     for(; j + 1 < nw; ++j) steady(j, sK[(j + 1) & 1], sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);
     last(j, sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);  // the wave's last block
     for(++j; j < nkv; ++j) next_loads(j, sK[j & 1], sV[(j + 1) & 1]);  // loads for the others
+    if(qi >= p.T) return;  // a padding row of the last block
     store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
@@ -311,12 +318,22 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
 // load per block brings both into LDS.
 // Sixteen lanes per query row, one float4 of dO and O each, so a wave reads
 // four rows as four contiguous 256-byte runs.
+// Rows T..Tp-1 (T not a multiple of 128) get L2 = +inf and D = 0, so their
+// probabilities, and with them their share of dS, dK and dV, are exactly 0.
 __global__ void flash_dsum(FlashParams p) {
-    const int64_t BH = p.B * p.H, n = BH * p.T;
+    const int64_t BH = p.B * p.H, n = BH * p.Tp;
     const int c = threadIdx.x & 15;
     for(int64_t i = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 4; i < n;
         i += ((int64_t)gridDim.x * blockDim.x) >> 4) {
-        const int64_t bh = i / p.T, t = i % p.T, b = bh / p.H, h = bh % p.H;
+        const int64_t bh = i / p.Tp, t = i % p.Tp, b = bh / p.H, h = bh % p.H;
+        float* blk = p.dsum_out + bh * 2 * p.Tp + (t / BLK) * 2 * BLK + t % BLK;
+        if(t >= p.T) {  // the whole 16-lane group: one row
+            if(c == 0) {
+                blk[0] = INFINITY;
+                blk[BLK] = 0.0f;
+            }
+            continue;
+        }
         const int64_t off = (b * p.T + t) * p.D + h * HD;
         const f32x4 a = reinterpret_cast<const f32x4*>(p.dout + off)[c];
         const f32x4 o = reinterpret_cast<const f32x4*>(p.o + off)[c];
@@ -326,8 +343,7 @@ __global__ void flash_dsum(FlashParams p) {
         s += __shfl_xor(s, 2, 16);
         s += __shfl_xor(s, 1, 16);
         if(c == 0) {
-            float* blk = p.dsum_out + bh * 2 * p.T + (t / BLK) * 2 * BLK + t % BLK;
-            blk[0] = p.lse[i] * kLog2e;
+            blk[0] = p.lse[bh * p.T + t] * kLog2e;
             blk[BLK] = s;
         }
     }
@@ -378,7 +394,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     const BlockLoad blq(p.ld, w, l), blo(p.D, w, l);
     const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.ld);
     const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + obase, p.T, p.D);
-    const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.T);
+    const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.Tp);
     auto issue = [&](int j, float* __restrict__ tq, float* __restrict__ to,
                      float* __restrict__ tl) {
         blq.issue(rq, p.ld, (int64_t)j * BLK, tq, w);
@@ -387,15 +403,15 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)tl, 16, 16 * l,
                                                      (unsigned)(j * 2 * BLK * 4), 0, 0);
     };
-    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
+    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.Tp / BLK);
     issue(j0, sQ[0], sO[0], sLD[0]);
     float kf[32], vf[32];
-    load_frag32(K + ki * p.ld, lh, kf, p.scale * kLog2e);
-    load_frag32(V + ki * p.ld, lh, vf, 1.0f);
+    load_frag32(K + ki * p.ld, lh, kf, p.scale * kLog2e, ki < p.T);
+    load_frag32(V + ki * p.ld, lh, vf, 1.0f, ki < p.T);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
     // this lane's column of every dS tile of key group kg (rows 32 floats apart)
     const int64_t kg = k0 / 32;
-    float* dsk = p.ds ? p.ds + ds_tile(bh, p.T, 0, 0) + ((lq >> 2) & 1) * 16 + 4 * (lq >> 3) + (lq & 3)
+    float* dsk = p.ds ? p.ds + ds_tile(bh, p.Tp, 0, 0) + ((lq >> 2) & 1) * 16 + 4 * (lq >> 3) + (lq & 3)
                       : nullptr;
 
     // iteration j reads buffer set st = (j - j0) & 1 and loads block j+1 into
@@ -472,6 +488,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
         const int st = (j - j0) & 1;
         iter(j, sQ[st], sO[st], sLD[st], sQ[st ^ 1], sO[st ^ 1], sLD[st ^ 1]);
     }
+    if(ki >= p.T) return;  // a padding row of the last block
     store_rowT(p.dv + base + ki * p.ld, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
     store_rowT(p.dk + base + ki * p.ld, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
 }
@@ -483,7 +500,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
 // are read straight into registers one block ahead.
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
-    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     // heaviest query blocks first, in passes of one workgroup per CU: odd passes
     // run in reverse, so a CU's resident workgroups mix heavy and light blocks
     const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
@@ -500,7 +517,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
     const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.ld);
     blk.issue(rk, p.ld, 0, sK[0], w);
     // tile (qg, kg) is at ds + kg*1024; this lane's 16 values at (2*lq + lh)*16
-    const float* ds = p.ds + ds_tile(bh, p.T, qg, 0) + (2 * lq + lh) * 16;
+    const float* ds = p.ds + ds_tile(bh, p.Tp, qg, 0) + (2 * lq + lh) * 16;
     auto fetch = [&](int j, f32x16 (&x)[2]) {
 #pragma unroll
         for(int sub = 0; sub < 2; ++sub) {
@@ -545,6 +562,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
         }
     };
     for(int j = 0; j < nkv; ++j) iter(j, sK[j & 1], sK[(j + 1) & 1]);
+    if(qi >= p.T) return;  // a padding row of the last block
     store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
@@ -577,7 +595,7 @@ __device__ __forceinline__ f32x16 dot_rows_scaled(const float* lds, int sub, int
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
     __shared__ __attribute__((aligned(16))) float sV[2][TILE];
-    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     // heaviest query blocks first, alternate passes of one workgroup per CU reversed
     const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
     const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
@@ -595,10 +613,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) 
     blk.issue(rk, p.ld, 0, sK[0], w);
     blk.issue(rv, p.ld, 0, sV[0], w);
     float qf[32], of[32];
-    load_frag32(p.q + base + qi * p.ld, lh, qf, 1.0f);
-    load_frag32(p.dout + obase + qi * p.D, lh, of, 1.0f);
-    // this query's L2 = lse*log2(e) and D = rowsum(dO*O) ([B*H][T/64][2][64])
-    const float* rc = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
+    load_frag32(p.q + base + qi * p.ld, lh, qf, 1.0f, qi < p.T);
+    load_frag32(p.dout + obase + qi * p.D, lh, of, 1.0f, qi < p.T);
+    // this query's L2 = lse*log2(e) and D = rowsum(dO*O) ([B*H][Tp/64][2][64])
+    const float* rc = p.dsum + bh * 2 * p.Tp + (qi / BLK) * 2 * BLK + qi % BLK;
     const float L2 = rc[0], Dq = rc[BLK];
     const float mul = p.scale * kLog2e;
     f32x16 dq[2] = {zero16(), zero16()};
@@ -633,6 +651,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) 
             for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols(tk, sub, cb, lq, lh, ds, dq[cb]);
         }
     }
+    if(qi >= p.T) return;  // a padding row of the last block
     store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
@@ -663,13 +682,17 @@ __device__ __forceinline__ f32x16 mfma16(const bf16x8& a, const bf16x8& b, f32x1
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// thread t holds rows 4*(t/16)..+3, columns 4*(t%16)..+3 of a 64x64 block
+// thread t holds rows 4*(t/16)..+3, columns 4*(t%16)..+3 of a 64x64 block;
+// rows at or past T read as zeros
 __device__ __forceinline__ void fetch_quad(const float* __restrict__ base, int64_t D, int64_t row0,
-                                           f32x4 (&x)[4]) {
+                                           f32x4 (&x)[4], int64_t T) {
     const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
 #pragma unroll
-    for(int i = 0; i < 4; ++i)
-        x[i] = *reinterpret_cast<const f32x4*>(base + (row0 + 4 * rq + i) * D + 4 * c4);
+    for(int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 4 * rq + i;
+        x[i] = r < T ? *reinterpret_cast<const f32x4*>(base + r * D + 4 * c4)
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 }
 
 __device__ __forceinline__ void put_rows(__bf16* t, const f32x4 (&x)[4]) {
@@ -690,7 +713,13 @@ __device__ __forceinline__ void put_cols(__bf16* t, const f32x4 (&x)[4]) {
 
 // a lane's 32 head dims of one row, rounded, in the 4 MFMA steps' slots
 __device__ __forceinline__ void load_frag_bf16(const float* __restrict__ row, int h, bf16x8 (&f)[4],
-                                               float mul) {
+                                               float mul, bool ok = true) {
+    if(!ok) {
+        const __bf16 z = (__bf16)0.0f;
+#pragma unroll
+        for(int t = 0; t < 4; ++t) f[t] = bf16x8{z, z, z, z, z, z, z, z};
+        return;
+    }
 #pragma unroll
     for(int t = 0; t < 4; ++t) {
         const f32x4 a = *reinterpret_cast<const f32x4*>(row + 16 * t + 8 * h);
@@ -737,7 +766,7 @@ __device__ __forceinline__ f32x16 dot_cols16(const __bf16* t, int sub, int cb, i
 __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
     __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 sVt[2][TILEB];  // [d][key]
-    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
@@ -747,13 +776,13 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
     bf16x8 qf[4];
-    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
+    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
     f32x4 rk[4], rv[4];
-    fetch_quad(K, p.ld, 0, rk);
-    fetch_quad(V, p.ld, 0, rv);
+    fetch_quad(K, p.ld, 0, rk, p.T);
+    fetch_quad(V, p.ld, 0, rv, p.T);
     put_rows(sK[0], rk);
     put_cols(sVt[0], rv);
     for(int j = 0; j < nkv; ++j) {
@@ -761,8 +790,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
         __syncthreads();
         const bool more = j + 1 < nkv;
         if(more) {
-            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk);
-            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv);
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk, p.T);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv, p.T);
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
@@ -809,6 +838,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
             put_cols(sVt[st ^ 1], rv);
         }
     }
+    if(qi >= p.T) return;  // a padding row of the last block
     store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
@@ -825,22 +855,22 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
     const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + obase;
-    const float* cst = p.dsum + bh * 2 * p.T;
+    const float* cst = p.dsum + bh * 2 * p.Tp;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
 
     bf16x8 kf[4], vf[4];
-    load_frag_bf16(K + ki * p.ld, lh, kf, p.scale * kLog2e);
-    load_frag_bf16(V + ki * p.ld, lh, vf, 1.0f);
+    load_frag_bf16(K + ki * p.ld, lh, kf, p.scale * kLog2e, ki < p.T);
+    load_frag_bf16(V + ki * p.ld, lh, vf, 1.0f, ki < p.T);
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
 
-    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.T / BLK);
+    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.Tp / BLK);
     f32x4 rq[4], ro[4];
     float rc = 0.0f;
     auto fetch = [&](int j) {
-        fetch_quad(Q, p.ld, (int64_t)j * BLK, rq);
-        fetch_quad(dO, p.D, (int64_t)j * BLK, ro);
+        fetch_quad(Q, p.ld, (int64_t)j * BLK, rq, p.T);
+        fetch_quad(dO, p.D, (int64_t)j * BLK, ro, p.T);
         if(threadIdx.x < 2 * BLK) rc = cst[(int64_t)j * 2 * BLK + threadIdx.x];
     };
     auto put = [&](int st) {
@@ -891,6 +921,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
         }
         if(more) put(st ^ 1);
     }
+    if(ki >= p.T) return;  // a padding row of the last block
     store_rowT(p.dv + base + ki * p.ld, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
     store_rowT(p.dk + base + ki * p.ld, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
 }
@@ -900,7 +931,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 sKt[2][TILEB];  // [d][key]
     __shared__ __attribute__((aligned(16))) __bf16 sV[2][TILEB];   // [key][d]
-    const int64_t BH = p.B * p.H, nqb = p.T / ROWS;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
@@ -910,16 +941,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
     bf16x8 qf[4], of[4];
-    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e);
-    load_frag_bf16(dO + qi * p.D, lh, of, 1.0f);
-    const float* cst = p.dsum + bh * 2 * p.T + (qi / BLK) * 2 * BLK + qi % BLK;
+    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
+    load_frag_bf16(dO + qi * p.D, lh, of, 1.0f, qi < p.T);
+    const float* cst = p.dsum + bh * 2 * p.Tp + (qi / BLK) * 2 * BLK + qi % BLK;
     const float l2 = cst[0], dd = cst[BLK];
     f32x16 dq[2] = {zero16(), zero16()};
 
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
     f32x4 rk[4], rv[4];
-    fetch_quad(K, p.ld, 0, rk);
-    fetch_quad(V, p.ld, 0, rv);
+    fetch_quad(K, p.ld, 0, rk, p.T);
+    fetch_quad(V, p.ld, 0, rv, p.T);
     put_rows(sK[0], rk);
     put_cols(sKt[0], rk);
     put_rows(sV[0], rv);
@@ -928,8 +959,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
         __syncthreads();
         const bool more = j + 1 < nkv;
         if(more) {
-            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk);
-            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv);
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk, p.T);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv, p.T);
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
@@ -957,6 +988,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
             put_rows(sV[st ^ 1], rv);
         }
     }
+    if(qi >= p.T) return;  // a padding row of the last block
     store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
@@ -964,22 +996,20 @@ int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, in
                 const void* a, const void* b, const void* c) {
     if(B < 0 || H < 1 || T < 0) return pk::fail("%s: bad sizes", who);
     if(hd != HD) return pk::fail("%s: head size %lld (this kernel handles 64)", who, (long long)hd);
-    if(T % ROWS) return pk::fail("%s: T=%lld must be a multiple of %d", who, (long long)T, ROWS);
     if(ld < H * HD || ld % 4)
         return pk::fail("%s: row stride %lld of q, k, v must be >= %lld and a multiple of 4", who,
                         (long long)ld, (long long)(H * HD));
     if(!pk::aligned16(a) || !pk::aligned16(b) || !pk::aligned16(c))
         return pk::fail("%s: q, k, v must be 16-byte aligned", who);
-    if(B * H * (T / ROWS) > 0x7fffffff || T * ld * 4 > 0x7fffffff)
+    const int64_t Tp = (T + ROWS - 1) / ROWS * ROWS;
+    if(B * H * (Tp / ROWS) > 0x7fffffff || Tp * ld * 4 > 0x7fffffff)
         return pk::fail("%s: problem too large", who);
     return PK_OK;
 }
 
 }  // namespace
 
-extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) {
-    return hd == HD && T > 0 && T % ROWS == 0;
-}
+extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) { return hd == HD && T > 0; }
 
 namespace {
 
@@ -999,10 +1029,11 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.B = B;
     p.H = H;
     p.T = T;
+    p.Tp = (T + ROWS - 1) / ROWS * ROWS;
     p.D = H * HD;
     p.ld = ld;
     p.scale = scale;
-    const unsigned grid = (unsigned)(B * H * (T / ROWS));
+    const unsigned grid = (unsigned)(B * H * (p.Tp / ROWS));
     if(bf16)
         flash_fwd_bf16<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
     else
@@ -1027,16 +1058,18 @@ extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64
                             o, lse, stream);
 }
 
-// row constants (2*B*H*T floats), then the dS tiles
+// row constants (2*B*H*Tp floats, Tp = T rounded up to 128), then the dS tiles
 extern "C" size_t pk_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t T) {
     if(B <= 0 || H <= 0 || T <= 0) return 0;
-    return (size_t)(2 * B * H * T + B * H * ds_tiles(T) * 1024) * sizeof(float);
+    const int64_t Tp = (T + ROWS - 1) / ROWS * ROWS;
+    return (size_t)(2 * B * H * Tp + B * H * ds_tiles(Tp) * 1024) * sizeof(float);
 }
 
 // the row constants only (PK_FLASH_RECOMPUTE)
 extern "C" size_t pk_flash_attn_bwd_workspace_recompute(int64_t B, int64_t H, int64_t T) {
     if(B <= 0 || H <= 0 || T <= 0) return 0;
-    return (size_t)(2 * B * H * T) * sizeof(float);
+    const int64_t Tp = (T + ROWS - 1) / ROWS * ROWS;
+    return (size_t)(2 * B * H * Tp) * sizeof(float);
 }
 
 namespace {
@@ -1073,18 +1106,20 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.dv = dv;
     p.dsum = static_cast<const float*>(workspace);
     p.dsum_out = static_cast<float*>(workspace);
-    p.ds = recompute ? nullptr : static_cast<float*>(workspace) + 2 * B * H * T;
+    const int64_t Tp = (T + ROWS - 1) / ROWS * ROWS;
+    p.ds = recompute ? nullptr : static_cast<float*>(workspace) + 2 * B * H * Tp;
     p.B = B;
     p.H = H;
     p.T = T;
+    p.Tp = (T + ROWS - 1) / ROWS * ROWS;
     p.D = H * HD;
     p.ld = ld;
     p.scale = scale;
     p.flags = flags & (PK_ACCUM | PK_ACCUM2 | PK_ACCUM3);
     hipStream_t st = pk::as_stream(stream);
-    flash_dsum<<<pk::grid_for(B * H * T * 16, 256), 256, 0, st>>>(p);
+    flash_dsum<<<pk::grid_for(B * H * p.Tp * 16, 256), 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
-    const unsigned grid = (unsigned)(B * H * (T / ROWS));
+    const unsigned grid = (unsigned)(B * H * (p.Tp / ROWS));
     if(bf16)
         flash_bwd_dkdv_bf16<<<grid, 256, 0, st>>>(p);
     else

@@ -231,8 +231,8 @@ struct PicoTensor* pico_swiglu(struct PicoTensor* a, struct PicoTensor* u) {
 /* -------------------------------------------------------- causal attention
  * q, k, v token-major [batch*T, heads*hd] with unit column stride and one
  * shared row stride (contiguous, or column blocks of one fused projection);
- * out contiguous [batch*T, heads*hd].  For head size 64 and
- * T a multiple of 128 the fused kernels run (pk_flash_attn_*): only lse
+ * out contiguous [batch*T, heads*hd].  For head size 64 (any T) the fused
+ * kernels run (pk_flash_attn_*): only lse
  * [B*H*T] is saved, and the forward never writes scores or probabilities;
  * the backward passes dS from its dK/dV kernel to its dQ kernel as 32x32 tiles
  * of each head's causal triangle in a workspace of about 2*B*H*T^2 bytes.  Above

@@ -92,7 +92,8 @@ def test_bf16_attention_forward_matches_restatement(dev, B, H, T):
     assert np.max(np.abs(host(lse) - lse_ref)) <= 1e-4 * np.max(np.abs(lse_ref))
 
 
-@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (1, 2, 1024)])
+@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (1, 2, 1024), (2, 2, 100),
+                                   (1, 2, 999)])
 def test_bf16_attention_vs_fp32_oracle(dev, B, H, T):
     D = H * 64
     q, k, v, do = _inputs(B, H, T, 50)

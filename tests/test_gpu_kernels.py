@@ -446,10 +446,13 @@ def test_embedding(dev):
 
 
 # ------------------------------------------------------- fused attention (hd 64)
-@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (1, 2, 1024)])
+@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (1, 2, 1024),
+                                   (2, 2, 1), (2, 2, 50), (1, 3, 200), (2, 1, 1000)])
 def test_flash_attention_vs_oracle(dev, B, H, T):
+    """any T (the last 128-row block padded: rows past T read as zeros, get no
+    probability and are never stored), against the oracle"""
     hd, D = 64, H * 64
-    assert K.flash_supported(T, hd) and not K.flash_supported(T + 64, hd)
+    assert K.flash_supported(T, hd) and not K.flash_supported(T, 32)
     q, k, v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (11, 12, 13, 14))
     o = torch.empty(B * T, D, device=dev)
     lse = torch.empty(B * H * T, device=dev)
@@ -459,17 +462,25 @@ def test_flash_attention_vs_oracle(dev, B, H, T):
     dq, dk, dv = (torch.full((B * T, D), float("nan"), device=dev) for _ in range(3))
     K.flash_bwd(B, H, cu(q), cu(k), cu(v), cu(o_ref), cu(lse_ref), cu(do), dq, dk, dv)
     refs = O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)
+
+    def close(got, ref):
+        # at T = 1 dq and dk are exactly 0 (one key: dS = P*(dP - D) = 0), and
+        # the kernels return rounding residue of dO's scale
+        if not np.any(ref):
+            return np.max(np.abs(got)) <= TOL * np.max(np.abs(do))
+        return max_rel(got, ref) <= TOL
     for got, ref in zip((dq, dk, dv), refs):
-        assert max_rel(host(got), ref) <= TOL
+        assert close(host(got), ref)
     # accumulate bits: each output adds onto what it holds
     base = [O.normal(B * T * D, 20 + i).reshape(B * T, D) for i in range(3)]
     acc = [cu(b.copy()) for b in base]
     K.flash_bwd(B, H, cu(q), cu(k), cu(v), cu(o_ref), cu(lse_ref), cu(do), *acc, flags=7)
     for got, ref, b0 in zip(acc, refs, base):
-        assert max_rel(host(got) - b0, ref) <= TOL
+        assert close(host(got) - b0, ref)
 
 
-@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (8, 12, 1024)])
+@pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (8, 12, 1024),
+                                   (2, 2, 200)])
 def test_flash_attention_recompute_dq_equals_stored_ds(dev, B, H, T):
     """PK_FLASH_RECOMPUTE (dQ from recomputed scores, no dS tiles) against the
     stored-dS backward: dq, dk and dv bit for bit, plain and accumulating, and
@@ -505,6 +516,7 @@ def test_flash_attention_recompute_workspace_and_refusal(dev):
     L = _lib.hip_lib()
     B, H, T = 2, 3, 256
     assert L.pk_flash_attn_bwd_workspace_recompute(B, H, T) == 8 * B * H * T
+    assert L.pk_flash_attn_bwd_workspace_recompute(B, H, 200) == 8 * B * H * 256
     assert L.pk_flash_attn_bwd_workspace(B, H, T) > 8 * B * H * T
     D = H * 64
     x = torch.zeros(B * T, D, device=dev)
