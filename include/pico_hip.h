@@ -340,7 +340,7 @@ int pk_attn_causal_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t 
                            float scale, const float* q, const float* k, const float* v,
                            const float* P, const float* dout, float* dq, float* dk, float* dv,
                            float* dP_ws, int flags, pk_stream_t stream);
-/* Fused causal attention for head size 64 (T a multiple of 128): the scores
+/* Fused causal attention for head size 64 (any T): the scores
  * are never written to memory.  Same layouts and lse as above; q, k, v, o,
  * dout, dq, dk, dv 16-byte aligned and ld a multiple of 4.
  * pk_flash_attn_supported(T, hd) says
