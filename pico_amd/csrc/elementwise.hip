@@ -405,106 +405,61 @@ __global__ void embed_fwd4_kernel(int64_t n, int64_t d4, int64_t vocab,
 // ---- deterministic embedding backward -------------------------------------
 // dtable[r,:] += dout[i,:] for every i with ids[i] == r, the adds of one row
 // made in increasing i -- the order of the sequential loop, so the result is
-// the same bits on every run and replay.  Four launches:
-//   group:  for each position i, rank_i = #{j < i : ids[j] == ids[i]},
-//           first_i = the smallest such j (i itself when rank_i == 0) and
-//           cnt_i = #{j : ids[j] == ids[i]}.  Each workgroup owns 64
-//           positions (one per lane) and its 8 waves split the j range, with
-//           the ids staged through LDS in tiles of 4096: O(n^2) compares, a
-//           few microseconds at the n = B*T of a training step.
-//   scan:   start_i = sum over j < i of (first occurrence of a valid id ?
-//           cnt_j : 0), one workgroup.
-//   place:  perm[start_{first_i} + rank_i] = i, so each id's positions are
-//           contiguous and in increasing order.
-//   sum:    one workgroup per first occurrence adds its rows in that order.
-constexpr int kGroupWaves = 8, kGroupTile = 4096, kScanThreads = 1024;
+// the same bits on every run and replay.
+//   sort:  the positions are sorted by id with a stable LSD radix sort of 8-bit
+//          digits (an id outside [0, vocab) takes the key vocab and sorts
+//          last), ceil(bits(vocab)/8) passes of O(n) work.  A pass is a
+//          histogram of each 2048-key block, one exclusive scan over (digit,
+//          block), and a scatter that keeps a block's keys of one digit in
+//          position order (ranks within a wave from ballots, across waves and
+//          chunks from counts in LDS), so equal ids stay in increasing i.
+//   sum:   one workgroup per run of equal ids adds its rows in that order.
+constexpr int kSortThreads = 256, kSortItems = 8, kSortTile = kSortThreads * kSortItems;
+constexpr int kDigits = 256, kScanThreads = 1024, kScanPer = 8;
 
-struct EmbedWs {
-    int32_t *rank, *first, *cnt, *start, *perm;
-};
-
-__global__ __launch_bounds__(64 * kGroupWaves) void embed_group_kernel(
-    int64_t n64, const int32_t* __restrict__ ids, EmbedWs ws) {
-    __shared__ __attribute__((aligned(16))) int32_t tile[kGroupTile];
-    __shared__ int32_t part[3][kGroupWaves][64];
-    const int n = (int)n64;  // the launcher refuses n >= 2^31
-    const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
-    const int i = blockIdx.x * 64 + lane;
-    const int32_t my = i < n ? ids[i] : 0;
-    // r counts matches before i; the first occurrence is the smallest match
-    // over all j (i itself when nothing earlier matches)
-    int32_t r = 0, c = 0, f = 0x7fffffff;
-    constexpr int per_wave = kGroupTile / kGroupWaves;
-    for(int j0 = 0; j0 < n; j0 += kGroupTile) {
-        __syncthreads();
-        for(int t = threadIdx.x; t < kGroupTile; t += blockDim.x)
-            tile[t] = j0 + t < n ? ids[j0 + t] : 0;
-        __syncthreads();
-        const int lim = min(kGroupTile, n - j0);
-        const int tb = w * per_wave, te = min(lim, tb + per_wave);
-        const int4* t4 = reinterpret_cast<const int4*>(tile);
-        int t = tb;
-        for(; t + 4 <= te; t += 4) {
-            const int4 x = t4[t >> 2];
-            const int32_t xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-            for(int e = 0; e < 4; ++e) {
-                const int j = j0 + t + e;
-                const bool eq = xs[e] == my;
-                c += eq;
-                r += eq && j < i;
-                f = eq ? min(f, j) : f;
-            }
-        }
-        for(; t < te; ++t) {
-            const int j = j0 + t;
-            const bool eq = tile[t] == my;
-            c += eq;
-            r += eq && j < i;
-            f = eq ? min(f, j) : f;
-        }
-    }
-    part[0][w][lane] = r;
-    part[1][w][lane] = c;
-    part[2][w][lane] = f;
-    __syncthreads();
-    if(w == 0 && i < n) {
-        for(int k = 1; k < kGroupWaves; ++k) {
-            r += part[0][k][lane];
-            c += part[1][k][lane];
-            f = min(f, part[2][k][lane]);
-        }
-        ws.rank[i] = r;
-        ws.cnt[i] = c;
-        ws.first[i] = f;  // i matches itself, so f <= i
-    }
+__device__ __forceinline__ int32_t embed_key(const int32_t* __restrict__ ids, int64_t i,
+                                             int64_t vocab) {
+    const int32_t id = ids[i];
+    return (id >= 0 && id < vocab) ? id : (int32_t)vocab;
 }
 
-// start_i = sum over j < i of the group sizes of first occurrences of valid
-// ids: each thread owns kScanPer consecutive positions, loaded up front
-constexpr int kScanPer = 8;
+// hist[digit * blocks + block]: the block's keys with that digit (keys NULL:
+// the first pass, keys made from ids)
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(
+    int64_t n, int64_t vocab, const int32_t* __restrict__ ids, const int32_t* __restrict__ keys,
+    int shift, int32_t* __restrict__ hist) {
+    __shared__ int32_t h[kDigits];
+    for(int t = threadIdx.x; t < kDigits; t += kSortThreads) h[t] = 0;
+    __syncthreads();
+    const int64_t b0 = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll
+    for(int e = 0; e < kSortItems; ++e) {
+        const int64_t i = b0 + e * kSortThreads + threadIdx.x;
+        if(i < n) {
+            const int32_t k = keys ? keys[i] : embed_key(ids, i, vocab);
+            atomicAdd(&h[(k >> shift) & (kDigits - 1)], 1);  // integer counts: any order
+        }
+    }
+    __syncthreads();
+    for(int t = threadIdx.x; t < kDigits; t += kSortThreads)
+        hist[(int64_t)t * gridDim.x + blockIdx.x] = h[t];
+}
 
-__global__ __launch_bounds__(kScanThreads) void embed_scan_kernel(int64_t n, int64_t vocab,
-                                                                  const int32_t* __restrict__ ids,
-                                                                  EmbedWs ws) {
+// exclusive prefix sums of a[0..m), in place, one workgroup
+__global__ __launch_bounds__(kScanThreads) void radix_scan_kernel(int64_t m,
+                                                                  int32_t* __restrict__ a) {
     __shared__ int32_t sums[kScanThreads];
     __shared__ int32_t carry;
     if(threadIdx.x == 0) carry = 0;
-    for(int64_t base = 0; base < n; base += (int64_t)kScanThreads * kScanPer) {
+    for(int64_t base = 0; base < m; base += (int64_t)kScanThreads * kScanPer) {
         const int64_t b = base + (int64_t)threadIdx.x * kScanPer;
-        int32_t wgt[kScanPer];
-#pragma unroll
-        for(int e = 0; e < kScanPer; ++e) {
-            const int64_t i = b + e;
-            const bool in = i < n;
-            const int32_t id = in ? ids[i] : -1;
-            const int32_t rk = in ? ws.rank[i] : 1;
-            const int32_t ct = in ? ws.cnt[i] : 0;
-            wgt[e] = (rk == 0 && id >= 0 && id < vocab) ? ct : 0;
-        }
+        int32_t v[kScanPer];
         int32_t local = 0;
 #pragma unroll
-        for(int e = 0; e < kScanPer; ++e) local += wgt[e];
+        for(int e = 0; e < kScanPer; ++e) {
+            v[e] = b + e < m ? a[b + e] : 0;
+            local += v[e];
+        }
         __syncthreads();
         sums[threadIdx.x] = local;
         __syncthreads();
@@ -517,46 +472,99 @@ __global__ __launch_bounds__(kScanThreads) void embed_scan_kernel(int64_t n, int
         int32_t run = carry + (threadIdx.x ? sums[threadIdx.x - 1] : 0);
 #pragma unroll
         for(int e = 0; e < kScanPer; ++e) {
-            if(b + e < n) ws.start[b + e] = run;
-            run += wgt[e];
+            if(b + e < m) a[b + e] = run;
+            run += v[e];
         }
         __syncthreads();
         if(threadIdx.x == kScanThreads - 1) carry = run;
     }
 }
 
-__global__ void embed_place_kernel(int64_t n, int64_t vocab, const int32_t* __restrict__ ids,
-                                   EmbedWs ws) {
-    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-        i += (int64_t)gridDim.x * blockDim.x) {
-        const int32_t id = ids[i];
-        if(id < 0 || id >= vocab) continue;
-        ws.perm[ws.start[ws.first[i]] + ws.rank[i]] = (int32_t)i;
+// stable scatter of one pass: key i of the block goes to offs[digit, block] +
+// (keys of that digit earlier in the block).  keys_in NULL: the first pass
+// (keys from ids, values the positions).
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    int64_t n, int64_t vocab, const int32_t* __restrict__ ids, const int32_t* __restrict__ keys_in,
+    const int32_t* __restrict__ vals_in, int shift, const int32_t* __restrict__ offs,
+    int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out) {
+    constexpr int W = kSortThreads / 64;
+    __shared__ int32_t run[kDigits];     // where this block's next key of each digit goes
+    __shared__ int32_t wcnt[W][kDigits];  // keys of each digit per wave, this chunk
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for(int t = threadIdx.x; t < kDigits; t += kSortThreads) {
+        run[t] = offs[(int64_t)t * gridDim.x + blockIdx.x];
+#pragma unroll
+        for(int ww = 0; ww < W; ++ww) wcnt[ww][t] = 0;
+    }
+    __syncthreads();
+    const uint64_t below_mask = (1ull << lane) - 1;
+    const int64_t b0 = (int64_t)blockIdx.x * kSortTile;
+    for(int e = 0; e < kSortItems; ++e) {
+        const int64_t i = b0 + e * kSortThreads + threadIdx.x;
+        const bool ok = i < n;
+        int32_t k = 0, v = 0, dg = 0;
+        if(ok) {
+            k = keys_in ? keys_in[i] : embed_key(ids, i, vocab);
+            v = vals_in ? vals_in[i] : (int32_t)i;
+            dg = (k >> shift) & (kDigits - 1);
+        }
+        // the lanes of this wave holding the same digit
+        uint64_t same = __ballot(ok);
+#pragma unroll
+        for(int bit = 0; bit < 8; ++bit) {
+            const bool set = (dg >> bit) & 1;
+            const uint64_t bb = __ballot(set);
+            same &= set ? bb : ~bb;
+        }
+        const int below = __popcll(same & below_mask);
+        if(ok && below == 0) wcnt[w][dg] = __popcll(same);  // the digit's lowest lane
+        __syncthreads();
+        if(ok) {
+            int32_t pos = run[dg] + below;
+            for(int ww = 0; ww < w; ++ww) pos += wcnt[ww][dg];
+            keys_out[pos] = k;
+            vals_out[pos] = v;
+        }
+        __syncthreads();
+        for(int t = threadIdx.x; t < kDigits; t += kSortThreads) {
+            int32_t c = 0;
+#pragma unroll
+            for(int ww = 0; ww < W; ++ww) {
+                c += wcnt[ww][t];
+                wcnt[ww][t] = 0;
+            }
+            run[t] += c;
+        }
+        __syncthreads();
     }
 }
 
-__global__ __launch_bounds__(256) void embed_sum_kernel(int64_t d, int64_t vocab,
-                                                        const int32_t* __restrict__ ids,
+// one workgroup per sorted position; the first of each run of equal valid
+// keys adds the run's rows, in order, into its table row
+__global__ __launch_bounds__(256) void embed_sum_kernel(int64_t n, int64_t d, int64_t vocab,
+                                                        const int32_t* __restrict__ keys,
+                                                        const int32_t* __restrict__ pos,
                                                         const float* __restrict__ dout,
-                                                        float* __restrict__ dtable, EmbedWs ws) {
-    const int64_t i = blockIdx.x;
-    const int32_t id = ids[i];
-    if(ws.rank[i] != 0 || id < 0 || id >= vocab) return;
-    const int32_t s = ws.start[i], c = ws.cnt[i];
+                                                        float* __restrict__ dtable) {
+    const int64_t s = blockIdx.x;
+    const int32_t id = keys[s];
+    if(id >= vocab || (s > 0 && keys[s - 1] == id)) return;
+    int64_t c = 1;
+    while(s + c < n && keys[s + c] == id) ++c;
     float* row = dtable + (int64_t)id * d;
     if((d & 3) == 0 && pk::aligned16(dout) && pk::aligned16(dtable)) {
         const int64_t d4 = d / 4;
         for(int64_t col = threadIdx.x; col < d4; col += blockDim.x) {
             f32x4 acc = reinterpret_cast<f32x4*>(row)[col];
-            for(int32_t k = 0; k < c; ++k)
-                acc += reinterpret_cast<const f32x4*>(dout + (int64_t)ws.perm[s + k] * d)[col];
+            for(int64_t k = 0; k < c; ++k)
+                acc += reinterpret_cast<const f32x4*>(dout + (int64_t)pos[s + k] * d)[col];
             reinterpret_cast<f32x4*>(row)[col] = acc;
         }
         return;
     }
     for(int64_t col = threadIdx.x; col < d; col += blockDim.x) {
         float acc = row[col];
-        for(int32_t k = 0; k < c; ++k) acc += dout[(int64_t)ws.perm[s + k] * d + col];
+        for(int64_t k = 0; k < c; ++k) acc += dout[(int64_t)pos[s + k] * d + col];
         row[col] = acc;
     }
 }
@@ -800,10 +808,12 @@ extern "C" int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32
     return pk::launch_status("pk_embed_fwd_f32");
 }
 
+// keys and positions, twice (the passes ping-pong), then the histogram
 extern "C" size_t pk_embed_bwd_workspace(int64_t n) {
-    return n > 0 ? (size_t)5 * (size_t)n * sizeof(int32_t) + 256 : 0;
+    if(n <= 0) return 0;
+    const int64_t blocks = (n + kSortTile - 1) / kSortTile;
+    return (size_t)(4 * n + kDigits * blocks) * sizeof(int32_t) + 256;
 }
-
 extern "C" int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids,
                                 const float* dout, float* dtable, void* workspace,
                                 size_t workspace_bytes, pk_stream_t stream) {
@@ -811,15 +821,30 @@ extern "C" int pk_embed_bwd_f32(int64_t n, int64_t d, int64_t vocab, const int32
     if(n == 0 || d == 0) return PK_OK;
     if(!ids || !dout || !dtable) return pk::fail("pk_embed_bwd_f32: NULL pointer");
     if(n > 0x7fffffff) return pk::fail("pk_embed_bwd_f32: more than 2^31 - 1 ids");
+    if(vocab > 0x7fffffff) return pk::fail("pk_embed_bwd_f32: vocab above 2^31 - 1");
     if(!workspace || workspace_bytes < pk_embed_bwd_workspace(n))
         return pk::fail("pk_embed_bwd_f32: workspace of %zu bytes, %zu needed", workspace_bytes,
                         pk_embed_bwd_workspace(n));
+    const int64_t blocks = (n + kSortTile - 1) / kSortTile;
     int32_t* base = static_cast<int32_t*>(workspace);
-    EmbedWs ws = {base, base + n, base + 2 * n, base + 3 * n, base + 4 * n};
+    int32_t *ka = base, *va = base + n, *kb = base + 2 * n, *vb = base + 3 * n;
+    int32_t* hist = base + 4 * n;
+    int bits = 1;  // keys run 0..vocab
+    while(bits < 31 && ((int64_t)1 << bits) <= vocab) ++bits;
     hipStream_t st = pk::as_stream(stream);
-    embed_group_kernel<<<(unsigned)((n + 63) / 64), 64 * kGroupWaves, 0, st>>>(n, ids, ws);
-    embed_scan_kernel<<<1, kScanThreads, 0, st>>>(n, vocab, ids, ws);
-    embed_place_kernel<<<pk::grid_for(n, NT), NT, 0, st>>>(n, vocab, ids, ws);
-    embed_sum_kernel<<<(unsigned)n, 256, 0, st>>>(d, vocab, ids, dout, dtable, ws);
+    const int32_t *kin = nullptr, *vin = nullptr;  // the first pass reads ids
+    int32_t *kout = ka, *vout = va;
+    for(int shift = 0; shift < bits; shift += 8) {
+        radix_hist_kernel<<<(unsigned)blocks, kSortThreads, 0, st>>>(n, vocab, ids, kin, shift,
+                                                                    hist);
+        radix_scan_kernel<<<1, kScanThreads, 0, st>>>(kDigits * blocks, hist);
+        radix_scatter_kernel<<<(unsigned)blocks, kSortThreads, 0, st>>>(
+            n, vocab, ids, kin, vin, shift, hist, kout, vout);
+        kin = kout;
+        vin = vout;
+        kout = kout == ka ? kb : ka;
+        vout = vout == va ? vb : va;
+    }
+    embed_sum_kernel<<<(unsigned)n, 256, 0, st>>>(n, d, vocab, kin, vin, dout, dtable);
     return pk::launch_status("pk_embed_bwd_f32");
 }

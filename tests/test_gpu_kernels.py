@@ -409,11 +409,14 @@ def test_attention_vs_oracle(dev, B, H, T, hd):
     _attn_case(dev, B, H, T, hd, q, k, v, do)
 
 
-@pytest.mark.parametrize("V,d,n", [(50, 6, 5000), (32000, 768, 8192), (7, 3, 1), (3, 64, 4097)])
+@pytest.mark.parametrize("V,d,n", [(50, 6, 5000), (32000, 768, 8192), (7, 3, 1), (3, 64, 4097),
+                                   (32000, 64, 100000), (1000, 16, 200000), (1 << 20, 8, 5000),
+                                   (1, 4, 3000)])
 def test_embedding_backward_deterministic_order(dev, V, d, n):
-    # many repeats per id (n >> V) and sizes crossing the 64-position groups and
-    # 4096-id tiles: the same bits as the position-ordered loop, every time;
-    # an accumulating call adds onto the existing rows; out-of-range ids add nothing
+    # many repeats per id (n >> V), one id only (V = 1), keys of 1 to 3 radix
+    # digits and sizes crossing the sort's 2048-key blocks: the same bits as the
+    # position-ordered loop, every time; an accumulating call adds onto the
+    # existing rows; out-of-range ids add nothing
     ids = O.labels(n, V + n, V)
     if n > 4:
         ids[::97] = -1
