@@ -198,7 +198,8 @@ int pico_argmax(struct PicoTensor* x, int32_t* idx);
  *   product also writes h = silu(gate) * up (gate, up the two column halves
  *   of the result) and keeps it; pico_swiglu_matmul_add over the two views
  *   pico_split_cols(result, 2) makes uses that h instead of computing it.
- *   (F not a multiple of 32 or a transposed a: a plain matmul.) ---- */
+ *   (F not a multiple of 32, a transposed a, or a product that pico_matmul
+ *   would split along K: a plain matmul.) ---- */
 struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
                                    struct PicoTensor* c);
 struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* w);

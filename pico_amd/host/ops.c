@@ -512,7 +512,10 @@ struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* 
     struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
     if(!out) return NULL;
     float* h = NULL;
-    if(va.t == 'N' && vw.t == 'N' && F % 32 == 0 && M > 0 && K > 0 && F > 0) {
+    /* the paired product never splits K; where the plain product would, the
+     * plain product runs, so both ways sum k in the same order */
+    if(va.t == 'N' && vw.t == 'N' && F % 32 == 0 && M > 0 && K > 0 && F > 0 &&
+       pk_gemm_workspace_f32(M, N, K) == 0) {
         h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F));
         if(!h) return NULL;
         float* scales = NULL;
