@@ -409,8 +409,11 @@ def _new_ops_graph(L, gv, wv, ids, labels, table, B, H):
     return loss, [x, n, q, k, v, att, h, logits]
 
 
-def test_new_ops_graph_vs_oracle(P, C):
-    B, T, H, hd, V = 2, 64, 2, 32, 50
+@pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 32), (2, 100, 2, 64), (1, 200, 1, 64)])
+def test_new_ops_graph_vs_oracle(P, C, B, T, H, hd):
+    # head size 32: the chain of GEMMs and softmax kernels; 64 at T 100 and 200:
+    # the fused kernels with a padded last query block
+    V = 50
     D = H * hd
     table = O.normal(V * D, 1).reshape(V, D)
     gv = O.normal(D, 2, 1.0, 0.02)
