@@ -6,8 +6,14 @@
  * (a calloc'd 64-byte PicoTensor, tensors packed back to back in one block, a
  * malloc'd 16-byte two-pointer Arena) go through the node lookup and the
  * device-arena calls without a byte read or written outside them, and that
- * the registry finds exactly the nodes this library registered.
+ * the registry finds exactly the nodes this library registered.  Eight
+ * threads then check what pico's tests/test_arena.c:160-247 checks of the
+ * arena context stack (each thread has its own, the main thread's survives
+ * the workers' pushes) while they register, look up and drop nodes in the
+ * shared registry at the same time.
  */
+#include <pthread.h>
+#include <sched.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -49,6 +55,55 @@ static void pico_style_arena_free(struct Arena* a) {
     free(a->begin->bottom);
     free(a->begin);
     free(a);
+}
+
+/* one worker: its own arena on its own context stack, which must stay the
+ * current one whatever the other threads do; meanwhile it churns the shared
+ * node registry (src/arena.h:155-169 for the stack) */
+enum { CTX_THREADS = 8, CTX_SPINS = 2000, CTX_NODES = 256 };
+static void* ctx_worker(void* arg) {
+    int* ok = (int*)arg;
+    *ok = 0;
+    if(arena_ctx_current() != NULL) return NULL;  /* a fresh thread's stack is empty */
+    struct Arena* mine = arena_init(1 << 12);
+    if(!mine) return NULL;
+    arena_ctx_push(mine);
+    struct PkNode* nodes[CTX_NODES];
+    int good = 1;
+    for(int i = 0; i < CTX_NODES; i++) {
+        nodes[i] = (struct PkNode*)calloc(1, sizeof(struct PkNode));
+        good &= pkh_node_register(nodes[i], NULL) == 0;
+    }
+    for(int i = 0; i < CTX_SPINS; i++) {
+        if(arena_ctx_current() != mine) good = 0;
+        if(pkh_node(&nodes[i % CTX_NODES]->t) == NULL) good = 0;
+        sched_yield();
+    }
+    for(int i = 0; i < CTX_NODES; i++) {
+        pkh_node_unregister(nodes[i]);
+        if(pkh_node(&nodes[i]->t) != NULL) good = 0;
+        free(nodes[i]);
+    }
+    arena_ctx_pop();
+    if(arena_ctx_current() != NULL) good = 0;
+    arena_destroy(mine);
+    *ok = good;
+    return NULL;
+}
+
+static void ctx_threads_test(void) {
+    struct Arena* main_arena = arena_init(1 << 12);
+    CHECK(main_arena != NULL);
+    arena_ctx_push(main_arena);
+    pthread_t th[CTX_THREADS];
+    int ok[CTX_THREADS];
+    for(int i = 0; i < CTX_THREADS; i++) CHECK(pthread_create(&th[i], NULL, ctx_worker, &ok[i]) == 0);
+    for(int i = 0; i < CTX_THREADS; i++) CHECK(pthread_join(th[i], NULL) == 0);
+    for(int i = 0; i < CTX_THREADS; i++) CHECK(ok[i] == 1);
+    CHECK(arena_ctx_current() == main_arena);  /* the workers never touched this stack */
+    arena_ctx_pop();
+    CHECK(arena_ctx_current() == NULL);
+    arena_destroy(main_arena);
 }
 
 int main(void) {
@@ -130,6 +185,7 @@ int main(void) {
         free(many[i]);
     }
     free(many);
+    ctx_threads_test();
     pkh_registry_clear();
 
     free(ft);

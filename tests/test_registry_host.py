@@ -40,6 +40,18 @@ def test_registry_and_foreign_arena_under_asan(tmp_path):
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_arena_context_and_registry_threads_under_tsan(tmp_path):
+    """Eight threads with their own arena context stacks (pico's
+    tests/test_arena.c:160-247) registering and dropping nodes in the shared
+    registry at once: ThreadSanitizer reports no race."""
+    exe = _build(tmp_path, ["-fsanitize=thread"])
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "registry host test ok" in r.stdout
+    assert "ThreadSanitizer" not in r.stderr
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
 def test_sanitizer_catches_a_read_past_a_pico_tensor(tmp_path):
     """The check above is only as good as the sanitizer: reading the byte after
     a calloc'd 64-byte tensor, as a magic-number test at offset 64 would, is
