@@ -24,6 +24,10 @@
 // exponentials are exp2.
 #include <math.h>
 
+#include <queue>
+#include <utility>
+#include <vector>
+
 #include "pk_common.h"
 
 namespace {
@@ -46,6 +50,22 @@ struct FlashParams {
     int64_t ld;          // row stride of q, k, v and dq, dk, dv (>= D)
     float scale;         // softmax scale (normally 1/8)
     int flags;
+};
+
+// Which query block each of the forward's first kFwdSlots*kCUs workgroups
+// takes.  Three forward workgroups share a CU, and the dispatcher places
+// workgroup b on CU b % 256 as slot b / 256 (measured: b, b+256 and b+512
+// run on one CU, all from the start), so this table decides each CU's work.
+// The host fills it longest-first, each block to the CU with the least work
+// so far; config 5's CUs then hold 26-28 key blocks each (the plain
+// heaviest-first order left 24-30, and the launch waited on the 30s).  Later
+// workgroups (more than 768) take the remaining query blocks heaviest first
+// as slots free.  The table only moves work between CUs: every block is
+// computed the same way wherever it runs.
+constexpr int kFwdSlots = 3;
+struct FlashFwdPlan {
+    uint16_t rank[kFwdSlots * kCUs];  // workgroup b < n takes rank[b]; others rank b
+    int n;
 };
 
 __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
@@ -97,6 +117,37 @@ __device__ __forceinline__ f32x16 dot_rows(const float* lds, int sub, int lq, in
     return acc;
 }
 
+// The same product for both 32-row sub-blocks of the tile at once, the two
+// accumulator chains alternating: consecutive MFMAs are then independent, so
+// neither waits for the previous one's result.  The 128-bit operand reads run
+// two k-groups (16 products) ahead of their use; scheduling barriers keep
+// that order.  Every chain still accumulates k in increasing order, as
+// dot_rows does.
+__device__ __forceinline__ void dot_rows2(const float* lds, int lq, int lh, const float (&bf)[32],
+                                          f32x16& acc0, f32x16& acc1) {
+    const f32x4* a0 = reinterpret_cast<const f32x4*>(lds + lq * LDT + 32 * lh);
+    const f32x4* a1 = reinterpret_cast<const f32x4*>(lds + (32 + lq) * LDT + 32 * lh);
+    f32x4 x[8], y[8];
+    x[0] = a0[0];
+    y[0] = a1[0];
+    x[1] = a0[1];
+    y[1] = a1[1];
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        if(i + 2 < 8) {
+            x[i + 2] = a0[i + 2];
+            y[i + 2] = a1[i + 2];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            acc0 = mfma(x[i][e], bf[4 * i + e], acc0);
+            acc1 = mfma(y[i][e], bf[4 * i + e], acc1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // acc (+)= X^T . W over the 32 rows of sub-block `sub`: A[d][row] read from the
 // row-major lds tile (column cb*32 + lane%32), B = the lane's 16 registers w,
 // rows taken in acc_row order
@@ -108,6 +159,40 @@ __device__ __forceinline__ f32x16 dot_cols(const float* lds, int sub, int cb, in
         acc = mfma(a, w[s], acc);
     }
     return acc;
+}
+
+// acc0 (+)= X^T.W over columns lq and acc1 over columns 32 + lq of the tile's
+// 64 rows, the rows taken as dot_cols takes them (sub-block 0, then 1, each in
+// acc_row order), so each chain accumulates in dot_cols's order.  The two
+// chains alternate, and the operand reads (one 2-float read per pair of
+// products) run two groups of 8 products ahead, fenced by scheduling barriers
+// so that only three groups' operands are live.
+__device__ __forceinline__ void dot_cols2(const float* lds, int lq, int lh, const f32x16 (&w)[2],
+                                          f32x16& acc0, f32x16& acc1) {
+    const float* base = lds + 4 * lh * LDT + lq;
+    float a0[32], a1[32];
+    auto rd = [&](int t) {
+        const int sub = t >> 4, s = t & 15;
+        const float* q = base + (sub * 32 + 8 * (s >> 2) + (s & 3)) * LDT;
+        a0[t] = q[0];
+        a1[t] = q[32];
+    };
+#pragma unroll
+    for(int t = 0; t < 8; ++t) rd(t);
+#pragma unroll
+    for(int g = 0; g < 8; ++g) {
+        if(g + 2 < 8) {
+#pragma unroll
+            for(int t = 4 * (g + 2); t < 4 * (g + 3); ++t) rd(t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for(int t = 4 * g; t < 4 * g + 4; ++t) {
+            acc0 = mfma(a0[t], w[t >> 4][t & 15], acc0);
+            acc1 = mfma(a1[t], w[t >> 4][t & 15], acc1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 // store a transposed accumulator pair (d rows, one row of the output per lane)
@@ -187,24 +272,37 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70
 // before the next LDS read, which serialises the double buffering.)
 
 // ======================================================================= forward
-// Workgroup: 128 queries of one (b, h), 4 waves of 32.  Heaviest query blocks
-// (the ones that see the most keys) are dispatched first, in passes of one
-// workgroup per CU whose odd passes run in reverse, so a CU's resident
-// workgroups mix heavy and light blocks (config 5: 138 -> 132-134 us, results
-// bit for bit the same).
+// Workgroup: 128 queries of one (b, h), 4 waves of 32; which query block a
+// workgroup takes comes from the dispatch plan (FlashFwdPlan).
 //
-// Pipeline: K runs one block ahead of V.  Iteration j computes the scores of
-// key block j+1 (MFMA) while it turns the scores of block j into
-// probabilities (VALU) and then adds P(j).V(j) to the output, so the softmax
-// of one block hides under the score products of the next.  In flight during
-// iteration j: K(j+2) and V(j+1).
-__global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
-    __shared__ __attribute__((aligned(16))) float sK[2][TILE];
+// Three workgroups share a CU (at most 168 VGPRs and 51 KB of LDS each), so
+// config 5's 768 workgroups (B 8, H 12, T 1024) are all resident from the
+// start: no second dispatch round, whose light query blocks would otherwise
+// start late on CUs still busy with heavy ones.  Per key block j:
+//   wait for K(j), V(j); barrier; load V(j+1) into the other V buffer;
+//   S = Q.K(j)^T; barrier; load K(j+1) into the one K buffer;
+//   softmax; O += P.V(j)
+// so K(j+1) lands under the softmax and P.V, V(j+1) under a whole block.
+//
+// VALU and MFMA work of the waves sharing a SIMD do not run concurrently on
+// gfx950, so every VALU instruction of the softmax adds to the kernel's time.
+// The softmax therefore keeps a stale running max m: m is exact after the
+// first key block and is raised only when a block's scores exceed it by more
+// than kTau (a wave-wide decision, rare after the first blocks), so the output
+// and the row sum are rescaled only then.  The score products start from -m
+// instead of 0, so the scores come out already relative to m and exp2 needs no
+// subtraction.  A block's scores are exponentiated against an m at most kTau
+// below the true running max (values <= 2^kTau) and never against one above
+// it, so nothing underflows that the exact online softmax would keep, and O
+// and l (the row sum) are the same sums in exact arithmetic.
+constexpr float kTau = 8.0f;
+
+__global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, FlashFwdPlan plan) {
+    __shared__ __attribute__((aligned(16))) float sK[TILE];
     __shared__ __attribute__((aligned(16))) float sV[2][TILE];
     const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
-    const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
-    const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
-    const int64_t rank = (pass & 1) ? lo + hi - 1 - blockIdx.x : blockIdx.x;
+    // ranks run heaviest first: rank r is query block nqb-1-r/BH of head r%BH
+    const int64_t rank = (int)blockIdx.x < plan.n ? (int64_t)plan.rank[blockIdx.x] : (int64_t)blockIdx.x;
     const int64_t qb = nqb - 1 - rank / BH, bh = rank % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
@@ -217,97 +315,134 @@ __global__ __launch_bounds__(256, 2) void flash_fwd(FlashParams p) {
 
     const BlockLoad blk(p.ld, w, l);
     const __amdgpu_buffer_rsrc_t rk = head_rsrc(K, p.T, p.ld), rv = head_rsrc(V, p.T, p.ld);
-    blk.issue(rk, p.ld, 0, sK[0], w);
+    blk.issue(rk, p.ld, 0, sK, w);
     blk.issue(rv, p.ld, 0, sV[0], w);
-    blk.issue(rk, p.ld, BLK, sK[1], w);  // nkv >= 2 since T % 128 == 0
     float qf[32];
     load_frag32(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
     f32x16 o[2] = {zero16(), zero16()};
-    float m = -INFINITY, lsum = 0.0f;
-    wait_loads();
-    __syncthreads();
-    f32x16 s[2] = {dot_rows(sK[0], 0, lq, lh, qf, zero16()),
-                   dot_rows(sK[0], 1, lq, lh, qf, zero16())};
+    // m: the offset the scores are taken against (log2 units); ls: this lane's
+    // share of the row sum (its 32 keys of each block; the two halves of the
+    // wave hold the other keys of the same queries and are added at the end)
+    float m = 0.0f, ls = 0.0f;
 
-    // softmax of block j's scores s (o rescaled to the new running max)
-    auto softmax = [&](int j) {
-        // key kv0 + sub*32 + acc_row(r, lh) is hidden from query qi when it
-        // exceeds qi; lim folds the lane's offsets into one compare per element
+    // A wave's last block j = nw-1 is the one that crosses its diagonal: key
+    // kv0 + sub*32 + acc_row(r, lh) is hidden from query qi when it exceeds
+    // qi; lim folds the lane's offsets into one compare per element
+    auto mask = [&](int j, f32x16 (&s)[2]) {
         const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;
-        if((int64_t)j * BLK + BLK - 1 > q0) {  // the block crosses this wave's diagonal
 #pragma unroll
-            for(int sub = 0; sub < 2; ++sub)
+        for(int sub = 0; sub < 2; ++sub)
 #pragma unroll
-                for(int r = 0; r < 16; ++r)
-                    if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
-        }
+            for(int r = 0; r < 16; ++r)
+                if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
+    };
+    auto lane_max = [&](const f32x16 (&s)[2]) {
         float mx = -INFINITY;
 #pragma unroll
         for(int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for(int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sub][r]);
+        return mx;
+    };
+    auto exp_sum = [&](f32x16 (&s)[2]) {
+        float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+        for(int r = 0; r < 16; ++r) {
+            s[0][r] = __builtin_amdgcn_exp2f(s[0][r]);
+            l0 += s[0][r];
+            s[1][r] = __builtin_amdgcn_exp2f(s[1][r]);
+            l1 += s[1][r];
+        }
+        ls += l0 + l1;
+    };
+    // -m in all 16 registers: the start of the next block's score products
+    auto start_scores = [&]() {
+        f32x16 z;
+#pragma unroll
+        for(int r = 0; r < 16; ++r) z[r] = -m;
+        return z;
+    };
+    // block 0: m is its exact row max (finite: key 0 is visible to every query)
+    auto softmax_first = [&](f32x16 (&s)[2]) {
+        float mx = lane_max(s);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        float ls = 0.0f;
 #pragma unroll
         for(int sub = 0; sub < 2; ++sub)
 #pragma unroll
-            for(int r = 0; r < 16; ++r) {
-                s[sub][r] = __builtin_amdgcn_exp2f(s[sub][r] - mn);
-                ls += s[sub][r];
-            }
-        ls += __shfl_xor(ls, 32, 64);
-        lsum = lsum * alpha + ls;
-        m = mn;
+            for(int r = 0; r < 16; ++r) s[sub][r] -= mx;
+        m = mx;
+        exp_sum(s);
+    };
+    auto softmax = [&](f32x16 (&s)[2]) {
+        float mx = lane_max(s);
+        if(__builtin_amdgcn_ballot_w64(mx > kTau)) {  // raise m to the block's row max
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float d = fmaxf(mx, 0.0f);
+            const float alpha = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-        for(int r = 0; r < 16; ++r) {
-            o[0][r] *= alpha;
-            o[1][r] *= alpha;
+            for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for(int r = 0; r < 16; ++r) s[sub][r] -= d;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                o[0][r] *= alpha;
+                o[1][r] *= alpha;
+            }
+            ls *= alpha;
+            m += d;
         }
+        exp_sum(s);
     };
     // o += V(j)^T . P^T
-    auto pv = [&](const float* tv) {
-#pragma unroll
-        for(int cb = 0; cb < 2; ++cb) {
-            o[cb] = dot_cols(tv, 0, cb, lq, lh, s[0], o[cb]);
-            o[cb] = dot_cols(tv, 1, cb, lq, lh, s[1], o[cb]);
-        }
-    };
-    // top of iteration j: K(j+1) and V(j) have landed, and sK[j&1] (K(j)) and
-    // sV[(j+1)&1] (V(j-1)) are free for K(j+2) and V(j+1)
-    auto next_loads = [&](int j, float* __restrict__ kd, float* __restrict__ vd) {
+    auto pv = [&](const float* tv, const f32x16 (&s)[2]) { dot_cols2(tv, lq, lh, s, o[0], o[1]); };
+    // every block j of the workgroup: wait for K(j), V(j); barrier; load
+    // V(j+1); S; barrier; load K(j+1); softmax and P.V.  The waves whose last
+    // query precedes the workgroup's last key block skip the products there.
+    auto begin_block = [&](int j) {
         wait_loads();
-        __syncthreads();
-        if(j + 2 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 2) * BLK, kd, w);
-        if(j + 1 < nkv) blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, vd, w);
+        __syncthreads();  // K(j), V(j) are in; V(j-1)'s buffer is free
+        if(j + 1 < nkv) blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
     };
-    // a block with a successor this wave sees
-    auto steady = [&](int j, const float* __restrict__ tk, const float* __restrict__ tv,
-                      float* __restrict__ kd, float* __restrict__ vd) {
-        next_loads(j, kd, vd);
-        // the next block's scores (MFMA) under this block's softmax (VALU) ...
-        const f32x16 n0 = dot_rows(tk, 0, lq, lh, qf, zero16());
-        const f32x16 n1 = dot_rows(tk, 1, lq, lh, qf, zero16());
-        softmax(j);
-        __builtin_amdgcn_sched_barrier(0);
-        pv(tv);  // ... then P.V: kept apart so the V reads are not hoisted above
-        __builtin_amdgcn_sched_barrier(0);
-        s[0] = n0;
-        s[1] = n1;
+    auto mid_block = [&](int j) {
+        __syncthreads();  // every wave has read K(j)
+        if(j + 1 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, sK, w);
     };
-    auto last = [&](int j, const float* __restrict__ tv, float* __restrict__ kd,
-                    float* __restrict__ vd) {
-        next_loads(j, kd, vd);
-        softmax(j);
-        pv(tv);
-    };
-
-    int j = 0;
-    for(; j + 1 < nw; ++j) steady(j, sK[(j + 1) & 1], sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);
-    last(j, sV[j & 1], sK[j & 1], sV[(j + 1) & 1]);  // the wave's last block
-    for(++j; j < nkv; ++j) next_loads(j, sK[j & 1], sV[(j + 1) & 1]);  // loads for the others
+    {  // block 0: the exact max; masked when it is also the wave's last
+        begin_block(0);
+        f32x16 s[2] = {zero16(), zero16()};
+        dot_rows2(sK, lq, lh, qf, s[0], s[1]);
+        mid_block(0);
+        if(nw == 1) mask(0, s);
+        softmax_first(s);
+        pv(sV[0], s);
+    }
+    int j = 1;
+    for(; j < nw - 1; ++j) {  // blocks wholly below the diagonal
+        begin_block(j);
+        f32x16 s[2];
+        s[0] = s[1] = start_scores();
+        dot_rows2(sK, lq, lh, qf, s[0], s[1]);
+        mid_block(j);
+        softmax(s);
+        pv(sV[j & 1], s);
+    }
+    if(j == nw - 1) {  // the wave's last block (when it is not block 0)
+        begin_block(j);
+        f32x16 s[2];
+        s[0] = s[1] = start_scores();
+        dot_rows2(sK, lq, lh, qf, s[0], s[1]);
+        mid_block(j);
+        mask(j, s);
+        softmax(s);
+        pv(sV[j & 1], s);
+        ++j;
+    }
+    for(; j < nkv; ++j) {  // the workgroup's blocks past this wave's last
+        begin_block(j);
+        mid_block(j);
+    }
     if(qi >= p.T) return;  // a padding row of the last block
+    const float lsum = ls + __shfl_xor(ls, 32, 64);
     store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
     if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
 }
@@ -1013,6 +1148,34 @@ extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) { return hd == HD 
 
 namespace {
 
+// The forward's dispatch table for BH heads of nqb query blocks (cached per
+// shape, per host thread).  Rank r (heaviest first) streams 2*(nqb - r/BH)
+// key blocks.  Slot k of CU c is workgroup c + kCUs*k and exists when that is
+// below the table's length.
+const FlashFwdPlan& fwd_plan(int64_t BH, int64_t nqb) {
+    thread_local int64_t cached_bh = -1, cached_nqb = -1;
+    thread_local FlashFwdPlan plan;
+    if(cached_bh == BH && cached_nqb == nqb) return plan;
+    const int n = (int)std::min<int64_t>(BH * nqb, kFwdSlots * kCUs);
+    std::vector<int> used(kCUs, 0);
+    // (work so far, cu) of the CUs with a free slot, least work first
+    std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
+                        std::greater<std::pair<int64_t, int>>>
+        free_cus;
+    for(int c = 0; c < kCUs && c < n; ++c) free_cus.push({0, c});
+    for(int r = 0; r < n; ++r) {
+        const std::pair<int64_t, int> top = free_cus.top();
+        free_cus.pop();
+        const int c = top.second, b = c + kCUs * used[c]++;
+        plan.rank[b] = (uint16_t)r;
+        if(c + kCUs * used[c] < n) free_cus.push({top.first + 2 * (nqb - r / BH), c});
+    }
+    plan.n = n;
+    cached_bh = BH;
+    cached_nqb = nqb;
+    return plan;
+}
+
 int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
                      int64_t ld, float scale, const float* q, const float* k, const float* v,
                      float* o, float* lse, pk_stream_t stream) {
@@ -1037,7 +1200,7 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     if(bf16)
         flash_fwd_bf16<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
     else
-        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
+        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p, fwd_plan(B * H, p.Tp / ROWS));
     return pk::launch_status(who);
 }
 
