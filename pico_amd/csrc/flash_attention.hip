@@ -52,21 +52,27 @@ struct FlashParams {
     int flags;
 };
 
-// Which query block each of the forward's first kFwdSlots*kCUs workgroups
-// takes.  Three forward workgroups share a CU, and the dispatcher places
-// workgroup b on CU b % 256 as slot b / 256 (measured: b, b+256 and b+512
-// run on one CU, all from the start), so this table decides each CU's work.
-// The host fills it longest-first, each block to the CU with the least work
-// so far; config 5's CUs then hold 26-28 key blocks each (the plain
-// heaviest-first order left 24-30, and the launch waited on the 30s).  Later
-// workgroups (more than 768) take the remaining query blocks heaviest first
-// as slots free.  The table only moves work between CUs: every block is
-// computed the same way wherever it runs.
-constexpr int kFwdSlots = 3;
-struct FlashFwdPlan {
-    uint16_t rank[kFwdSlots * kCUs];  // workgroup b < n takes rank[b]; others rank b
+// Which block (a forward or dQ query block, a dK/dV key block) each of a
+// launch's first slots*kCUs workgroups takes.  `slots` workgroups of a kernel
+// share a CU, and the dispatcher places workgroup b on CU b % 256 as slot
+// b / 256 (measured: b, b+256, b+512 run on one CU, all from the start), so
+// this table decides each CU's work.  The host fills it longest-first, each
+// block to the CU with the least work so far; config 5's forward CUs then hold
+// 26-28 key blocks each (the plain heaviest-first order left 24-30, and the
+// launch waited on the 30s).  Later workgroups take the remaining blocks
+// heaviest first as slots free.  The table only moves work between CUs:
+// every block is computed the same way wherever it runs.
+constexpr int kMaxSlots = 4;
+struct FlashPlan {
+    uint16_t rank[kMaxSlots * kCUs];  // workgroup b < n takes rank[b]; others rank b
     int n;
 };
+// ranks run heaviest first: rank r is block (nblk-1-r/BH) of the forward and
+// dQ (a query block seeing the most keys first), block r/BH of dK/dV (a key
+// block seen by the most queries first), of head r%BH
+__device__ __forceinline__ int64_t plan_rank(const FlashPlan& plan) {
+    return (int)blockIdx.x < plan.n ? (int64_t)plan.rank[blockIdx.x] : (int64_t)blockIdx.x;
+}
 
 __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -273,7 +279,7 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70
 
 // ======================================================================= forward
 // Workgroup: 128 queries of one (b, h), 4 waves of 32; which query block a
-// workgroup takes comes from the dispatch plan (FlashFwdPlan).
+// workgroup takes comes from the dispatch plan (FlashPlan).
 //
 // Three workgroups share a CU (at most 168 VGPRs and 51 KB of LDS each), so
 // config 5's 768 workgroups (B 8, H 12, T 1024) are all resident from the
@@ -297,12 +303,12 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70
 // and l (the row sum) are the same sums in exact arithmetic.
 constexpr float kTau = 8.0f;
 
-__global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, FlashFwdPlan plan) {
+constexpr int kFwdSlots = 3;
+__global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, FlashPlan plan) {
     __shared__ __attribute__((aligned(16))) float sK[TILE];
     __shared__ __attribute__((aligned(16))) float sV[2][TILE];
     const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
-    // ranks run heaviest first: rank r is query block nqb-1-r/BH of head r%BH
-    const int64_t rank = (int)blockIdx.x < plan.n ? (int64_t)plan.rank[blockIdx.x] : (int64_t)blockIdx.x;
+    const int64_t rank = plan_rank(plan);
     const int64_t qb = nqb - 1 - rank / BH, bh = rank % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
@@ -633,14 +639,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
 // (x scale at the end) over the key blocks of 64 with key <= query: K blocks
 // stream through LDS one block ahead, the dS tiles the dK/dV kernel stored
 // are read straight into registers one block ahead.
-__global__ __launch_bounds__(256, 2) void flash_bwd_dq(FlashParams p) {
+// Four workgroups share a CU (124 VGPRs, 34 KB of LDS), so config 5's 768
+// are resident at once, placed by the dispatch plan.
+constexpr int kDqSlots = 4;
+__global__ __launch_bounds__(256, kDqSlots) void flash_bwd_dq(FlashParams p, FlashPlan plan) {
     __shared__ __attribute__((aligned(16))) float sK[2][TILE];
-    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
-    // heaviest query blocks first, in passes of one workgroup per CU: odd passes
-    // run in reverse, so a CU's resident workgroups mix heavy and light blocks
-    const int64_t nwg = BH * nqb, pass = blockIdx.x / kCUs;
-    const int64_t lo = pass * kCUs, hi = min(lo + kCUs, nwg);
-    const int64_t rank = (pass & 1) ? lo + hi - 1 - blockIdx.x : blockIdx.x;
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS, rank = plan_rank(plan);
     const int64_t qb = nqb - 1 - rank / BH, bh = rank % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t base = b * p.T * p.ld + h * HD;
@@ -1148,15 +1152,17 @@ extern "C" int pk_flash_attn_supported(int64_t T, int64_t hd) { return hd == HD 
 
 namespace {
 
-// The forward's dispatch table for BH heads of nqb query blocks (cached per
-// shape, per host thread).  Rank r (heaviest first) streams 2*(nqb - r/BH)
-// key blocks.  Slot k of CU c is workgroup c + kCUs*k and exists when that is
-// below the table's length.
-const FlashFwdPlan& fwd_plan(int64_t BH, int64_t nqb) {
+// The dispatch table of a launch over BH heads of nqb 128-row blocks with
+// `slots` workgroups per CU (cached per shape, per host thread).  Rank r
+// (heaviest first) streams 2*(nqb - r/BH) 64-row blocks of the other operand
+// in each of the three kernels.  Slot k of CU c is workgroup c + kCUs*k and
+// exists when that is below the table's length.
+const FlashPlan& flash_plan(int64_t BH, int64_t nqb, int slots) {
     thread_local int64_t cached_bh = -1, cached_nqb = -1;
-    thread_local FlashFwdPlan plan;
-    if(cached_bh == BH && cached_nqb == nqb) return plan;
-    const int n = (int)std::min<int64_t>(BH * nqb, kFwdSlots * kCUs);
+    thread_local int cached_slots = -1;
+    thread_local FlashPlan plan;
+    if(cached_bh == BH && cached_nqb == nqb && cached_slots == slots) return plan;
+    const int n = (int)std::min<int64_t>(BH * nqb, slots * kCUs);
     std::vector<int> used(kCUs, 0);
     // (work so far, cu) of the CUs with a free slot, least work first
     std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
@@ -1173,6 +1179,7 @@ const FlashFwdPlan& fwd_plan(int64_t BH, int64_t nqb) {
     plan.n = n;
     cached_bh = BH;
     cached_nqb = nqb;
+    cached_slots = slots;
     return plan;
 }
 
@@ -1200,7 +1207,7 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     if(bf16)
         flash_fwd_bf16<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
     else
-        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p, fwd_plan(B * H, p.Tp / ROWS));
+        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p, flash_plan(B * H, p.Tp / ROWS, kFwdSlots));
     return pk::launch_status(who);
 }
 
@@ -1293,7 +1300,7 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     else if(recompute)
         flash_bwd_dq_recompute<<<grid, 256, 0, st>>>(p);
     else
-        flash_bwd_dq<<<grid, 256, 0, st>>>(p);
+        flash_bwd_dq<<<grid, 256, 0, st>>>(p, flash_plan(B * H, p.Tp / ROWS, kDqSlots));
     return pk::launch_status(who);
 }
 
