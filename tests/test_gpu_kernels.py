@@ -482,6 +482,59 @@ def test_flash_attention_vs_oracle(dev, B, H, T):
         assert close(host(got) - b0, ref)
 
 
+@pytest.mark.parametrize("trend", ["rising", "falling"])
+def test_flash_attention_running_max_raises_and_underflow(dev, trend):
+    """The forward keeps a stale running max, raised only when a key block's
+    scores exceed it by 2^8 (in log2 units).  Keys whose scale grows along the
+    sequence (scores up to ~100 log2 units) take that raise on most blocks;
+    keys whose scale shrinks leave the first block dominant, so later blocks'
+    exponentials underflow as in the exact online softmax.  Both against the
+    float64 oracle, forward and backward."""
+    B, H, T, hd = 1, 2, 1024, 64
+    D = H * hd
+    t = np.arange(B * T, dtype=np.float64).reshape(-1, 1)
+    ramp = 1 + 16 * t / T if trend == "rising" else 17 - 16 * t / T
+    q = O.normal(B * T * D, 61).reshape(B * T, D)
+    k = (O.normal(B * T * D, 62).reshape(B * T, D) * ramp).astype(np.float32)
+    v, do = (O.normal(B * T * D, s).reshape(B * T, D) for s in (63, 64))
+    o, lse = torch.empty(B * T, D, device=dev), torch.empty(B * H * T, device=dev)
+    K.flash_fwd(B, H, cu(q), cu(k), cu(v), o, lse)
+    o_ref, lse_ref = O.attn_fwd(B, H, q, k, v)
+    assert max_rel(host(o), o_ref) <= TOL and max_rel(host(lse), lse_ref) <= TOL
+    dq, dk, dv = (torch.empty(B * T, D, device=dev) for _ in range(3))
+    K.flash_bwd(B, H, cu(q), cu(k), cu(v), o, lse, cu(do), dq, dk, dv)
+    for got, ref in zip((dq, dk, dv), O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)):
+        assert max_rel(host(got), ref) <= TOL
+
+
+@pytest.mark.parametrize("B,T", [(5, 1664), (10, 1152)])
+def test_flash_attention_beyond_dispatch_plan(dev, B, T):
+    """Launches with more workgroups than the dispatch plans place (the
+    forward plans 768 = 3 per CU, the dQ kernel 1024 = 4 per CU): 780 and 1080
+    query blocks of 12 heads; the later workgroups take the remaining blocks
+    in order.  Every head's output is written (NaN-filled before), and
+    sampled heads match the oracle."""
+    H, hd = 12, 64
+    D = H * hd
+    q, k, v, do = (O.normal(B * T * D, 151 + i).reshape(B * T, D) for i in range(4))
+    o = torch.full((B * T, D), float("nan"), device=dev)
+    lse = torch.empty(B * H * T, device=dev)
+    K.flash_fwd(B, H, cu(q), cu(k), cu(v), o, lse)
+    dq, dk, dv = (torch.full((B * T, D), float("nan"), device=dev) for _ in range(3))
+    K.flash_bwd(B, H, cu(q), cu(k), cu(v), o, lse, cu(do), dq, dk, dv)
+    o, lse, dq, dk, dv = (host(x) for x in (o, lse, dq, dk, dv))
+    for x in (o, lse, dq, dk, dv):
+        assert np.isfinite(x).all()
+    for b, h in ((0, 0), (B - 1, H - 1), (B // 2, 5)):
+        rows, cols = slice(b * T, (b + 1) * T), slice(h * hd, (h + 1) * hd)
+        qh, kh, vh, doh = (np.ascontiguousarray(x[rows, cols]) for x in (q, k, v, do))
+        o_ref, lse_ref = O.attn_fwd(1, 1, qh, kh, vh)
+        assert max_rel(o[rows, cols], o_ref) <= TOL, (b, h)
+        assert max_rel(lse[(b * H + h) * T:(b * H + h + 1) * T], lse_ref) <= TOL, (b, h)
+        for got, ref in zip((dq, dk, dv), O.attn_bwd(1, 1, qh, kh, vh, o_ref, lse_ref, doh)):
+            assert max_rel(got[rows, cols], ref) <= TOL, (b, h)
+
+
 @pytest.mark.parametrize("B,H,T", [(2, 2, 128), (1, 3, 256), (2, 2, 384), (8, 12, 1024),
                                    (2, 2, 200)])
 def test_flash_attention_recompute_dq_equals_stored_ds(dev, B, H, T):
