@@ -31,8 +31,11 @@
 //    slice sits before group 3, so group 0 of the next slice is read under
 //    group 3's MFMAs.
 //  * LDS holds every operand k-contiguous, [rows][32 + 4 pad]: an operand that
-//    is row-contiguous in memory is fetched as 4 x 4 blocks and transposed in
-//    registers on its way to LDS.  Within a 32-wide k slice, lanes 0-31 take
+//    is row-contiguous in memory is fetched one row and four consecutive k per
+//    thread (four 32-bit loads, each a contiguous run of 64 rows per wave), so
+//    its values arrive k-contiguous in registers and go to LDS as one 128-bit
+//    store, with no transposing moves (VALU work, which on gfx950 does not
+//    overlap the matrix products).  Within a 32-wide k slice, lanes 0-31 take
 //    k 0..15 and lanes 32-63 take k 16..31, so every fragment read is a 128-bit
 //    LDS load, for all four layouts (measured: paired 32-bit reads of a
 //    row-contiguous tile held NN and TN 5 % below NT).
@@ -58,25 +61,22 @@ constexpr int KF = BK + 4;  // row stride of a k-contiguous LDS tile [rows][36]
 constexpr int GROUP_M = 8;
 
 // One operand's R x BK slice, staged into a k-contiguous LDS tile [R][KF].
+// Each staging item is 4 consecutive k of one row, held as one float4 and
+// stored to LDS as one 128-bit write; R/32 items per thread.
 //  * k-contiguous in memory (KFAST: op(A) when A is not transposed, op(B)^T
-//    when B is): each staging item is one float4 of 4 consecutive k in a row;
-//    R/32 items per thread.
-//  * row-contiguous in memory: each item is a 4 x 4 block -- 4 consecutive
-//    rows at 4 consecutive k, fetched as 4 float4 along the rows and
-//    transposed in registers -- so LDS holds the same k-contiguous form and
-//    every fragment read is a 128-bit load.  The slice has 2R such blocks:
-//    one per thread (two at R = 256; at R = 96 some threads repeat one; at
-//    R = 64 the blocks are 4 rows x 2 k, one per thread).
+//    when B is): the item is one 128-bit load.
+//  * row-contiguous in memory: the item is four 32-bit loads, one per k, and
+//    consecutive threads take consecutive rows, so each load instruction of a
+//    wave reads one k-row's 64 consecutive floats.  (An earlier staging of
+//    4 x 4 blocks -- 128-bit loads along the rows, transposed in registers --
+//    spent 15-30 VALU moves per slice, and its loads touched 8 k-rows 64 KB
+//    apart per instruction, which shared vector-L1 sets.)
 template <bool KFAST, int R>
 struct Operand {
-    // k depth of a transposed block: 4, or 2 for R = 64, where 4 x 2 blocks
-    // give exactly one block per thread
-    static constexpr int KD = R == 64 ? 2 : 4;
-    static constexpr int BLOCKS = (R / 4) * (BK / KD);  // blocks of a row-contiguous slice
-    static constexpr int ITEMS = KFAST ? R * BK / 4 / NT : (BLOCKS + NT - 1) / NT;
-    static constexpr int ITEM_F4 = KFAST ? 1 : KD;  // float4 per item
-    static constexpr int F4 = ITEMS * ITEM_F4;       // float4 registers per thread
-    static constexpr int FLOATS = R * KF;            // LDS floats of one stage
+    static constexpr int ITEMS = R * BK / 4 / NT;
+    static constexpr int F4 = ITEMS;            // float4 registers per thread
+    static constexpr int OPS = KFAST ? 2 : 5;   // memory instructions per item (loads + store)
+    static constexpr int FLOATS = R * KF;       // LDS floats of one stage
 };
 
 // A tile shape: WGM x (4 / WGM) waves, each TM x TN blocks of 32 x 32.
@@ -172,43 +172,91 @@ __device__ __forceinline__ f32x4 load_f4(const float* __restrict__ base, int64_t
     return x;
 }
 
-// staging item `item` of this thread: the (row, k) origin of its float4 or
-// block.  A row-contiguous slice has 2R blocks; when that is not a multiple
-// of the thread count (R = 96, 64) the remaining threads repeat blocks from
-// the start: they load the same data and store the same values to the same
-// LDS addresses, which keeps the loop free of branches.
+// The 4 consecutive k (k..k+3) of row r of a row-contiguous operand
+// (element (r, k) at base[k*ld + r]): four 32-bit loads.  Edge modes
+// zero-fill outside [Rlim) x [K); with kEdgeVec K is a multiple of 4, so the
+// four are in or out together.
+template <int EDGE>
+__device__ __forceinline__ f32x4 load_k4(const float* __restrict__ base, int64_t ld, int64_t r,
+                                         int64_t k, int64_t Rlim, int64_t K) {
+    f32x4 x;
+    if(EDGE == kEdgeNone) {
+        const float* p = base + k * ld + r;
+#pragma unroll
+        for(int t = 0; t < 4; ++t) x[t] = p[t * ld];
+        return x;
+    }
+    if(EDGE == kEdgeVec) {
+        // load from element (0, 0) when outside and select zero: no branch
+        // splits the main loop (the launcher guarantees M, N, K > 0 here)
+        const bool in = r < Rlim && k < K;
+        const int64_t off = in ? k * ld + r : 0, step = in ? ld : 0;
+#pragma unroll
+        for(int t = 0; t < 4; ++t) {
+            const float y = base[off + t * step];
+            x[t] = in ? y : 0.0f;
+        }
+        return x;
+    }
+#pragma unroll
+    for(int t = 0; t < 4; ++t) x[t] = r < Rlim && k + t < K ? base[(k + t) * ld + r] : 0.0f;
+    return x;
+}
+
+// staging item `item` of this thread: the (row, k) origin of its 4 k
 template <bool KFAST, int R>
 __device__ __forceinline__ void item_origin(int item, int& rr, int& kk) {
+    const int u = threadIdx.x + item * NT;
     if(KFAST) {
-        const int u = threadIdx.x + item * NT;
+        // 8 consecutive threads read one row's 32 k (128 contiguous bytes)
         rr = u >> 3;
         kk = (u & 7) * 4;
     } else {
-        // consecutive threads take consecutive k of one 4-row block: their
-        // LDS stores fill 128 contiguous bytes of a row, and each load row
-        // is read in 128-byte (KD = 4) or 64-byte (KD = 2) pieces
-        constexpr int KD = Operand<false, R>::KD, KQ = BK / KD;
-        const int u = (threadIdx.x + item * NT) % Operand<false, R>::BLOCKS;
-        rr = (u / KQ) * 4;
-        kk = (u % KQ) * KD;
+        // consecutive threads take consecutive rows at the same 4 k; their
+        // 128-bit LDS stores (rows 36 floats apart) fall in distinct banks
+        rr = u % R;
+        kk = (u / R) * 4;
     }
 }
 
 // PAIR: rows R/2.. of the slice come from `shift` rows further on (the up
-// columns of a paired SwiGLU product; an item's 4 rows never straddle R/2)
+// columns of a paired SwiGLU product).
+// Whole tiles (kEdgeNone) load through a buffer resource over the operand:
+// the byte offset splits into a per-lane part (the item's place in the
+// slice), which stays the same from slice to slice, and a uniform part (the
+// tile's first row, the slice's first k, the k row of each of a row-contiguous
+// item's four loads) that goes to the instruction's scalar offset, so no
+// per-lane address arithmetic is repeated per slice.  The launcher takes this
+// path only when every operand's extent is below 2^31 bytes.
 template <bool KFAST, int EDGE, int R, bool PAIR = false>
 __device__ __forceinline__ void load_item(const float* __restrict__ base, int64_t ld, int64_t r0,
                                           int64_t k0, int64_t Rlim, int64_t K, int item,
                                           f32x4* v, int64_t shift = 0) {
     int rr, kk;
     item_origin<KFAST, R>(item, rr, kk);
+    if constexpr(EDGE == kEdgeNone) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(base), (short)0, 0x7fffffff, 0x00020000);
+        const int lshift = PAIR && rr >= R / 2 ? (int)shift : 0;
+        if(KFAST) {
+            const int voff = ((rr + lshift) * (int)ld + kk) * 4;
+            const int soff = (int)((r0 * ld + k0) * 4);
+            v[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+        } else {
+            const int voff = (kk * (int)ld + rr + lshift) * 4;
+            const int soff = (int)((k0 * ld + r0) * 4), step = (int)(ld * 4);
+#pragma unroll
+            for(int t = 0; t < 4; ++t)
+                v[0][t] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + t * step, 0));
+        }
+        return;
+    }
     const int64_t r = r0 + rr + (PAIR && rr >= R / 2 ? shift : 0);
     if(KFAST) {
         v[0] = load_f4<true, EDGE>(base, ld, r, k0 + kk, Rlim, K);
     } else {
-#pragma unroll
-        for(int t = 0; t < Operand<false, R>::KD; ++t)
-            v[t] = load_f4<false, EDGE>(base, ld, r, k0 + kk + t, Rlim, K);
+        v[0] = load_k4<EDGE>(base, ld, r, k0 + kk, Rlim, K);
     }
 }
 
@@ -293,12 +341,6 @@ __device__ __forceinline__ void put4(Fp8T<OP>* lds, int off, f32x4 w) {
     const int v = fp8_pack2<true>(w[2] * sc, w[3] * sc, fp8_pack2<false>(w[0] * sc, w[1] * sc, 0));
     *reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(lds) + off) = v;
 }
-template <int OP>
-__device__ __forceinline__ void put2(Fp8T<OP>* lds, int off, float a, float b) {
-    const float sc = g_fp8_scale[OP];
-    *reinterpret_cast<short*>(reinterpret_cast<unsigned char*>(lds) + off) =
-        (short)fp8_pack2<false>(a * sc, b * sc, 0);
-}
 
 template <class E>
 __device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
@@ -310,45 +352,12 @@ __device__ __forceinline__ void put4(E* lds, int off, f32x4 w) {
     }
 }
 
-template <class E>
-struct is_split {
-    static constexpr bool value = false;
-    static constexpr int LO = 0;
-};
-template <int L>
-struct is_split<SplitBf16<L>> {
-    static constexpr bool value = true;
-    static constexpr int LO = L;
-};
-
 template <bool KFAST, int R, class E>
 __device__ __forceinline__ void store_item(E* lds, int item, const f32x4* v) {
     constexpr int LS = lds_stride<E>();
     int rr, kk;
     item_origin<KFAST, R>(item, rr, kk);
-    if(KFAST) {
-        put4(lds, rr * LS + kk, v[0]);
-    } else if(Operand<false, R>::KD == 4) {
-        // v[t] holds rows rr..rr+3 at k = kk + t: row j of the block is {v[t][j]}
-#pragma unroll
-        for(int j = 0; j < 4; ++j) put4(lds, (rr + j) * LS + kk, f32x4{v[0][j], v[1][j], v[2][j], v[3][j]});
-    } else {
-#pragma unroll
-        for(int j = 0; j < 4; ++j) {
-            if constexpr(sizeof(E) == 4) {
-                typedef float f32x2 __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<f32x2*>(lds + (rr + j) * LS + kk) = f32x2{v[0][j], v[1][j]};
-            } else if constexpr(sizeof(E) == 1) {
-                put2(lds, (rr + j) * LS + kk, v[0][j], v[1][j]);
-            } else if constexpr(is_split<E>::value) {
-                const float w2[2] = {v[0][j], v[1][j]};
-                put_split<is_split<E>::LO>(reinterpret_cast<__bf16*>(lds), (rr + j) * LS + kk, w2, 2);
-            } else {
-                *reinterpret_cast<bf16x2*>(lds + (rr + j) * LS + kk) =
-                    bf16x2{(__bf16)v[0][j], (__bf16)v[1][j]};
-            }
-        }
-    }
+    put4(lds, rr * LS + kk, v[0]);
 }
 
 // k-group q (k = 4q..4q+3 for lanes 0-31, 16+4q.. for lanes 32-63) of the
@@ -403,7 +412,7 @@ struct Staging {
     using OA = Operand<AK, T::BM>;
     using OB = Operand<BKF, T::BN>;
     static constexpr int ITEMS = OA::ITEMS + OB::ITEMS;
-    static constexpr int ops(int item) { return 2 * (item < OA::ITEMS ? OA::ITEM_F4 : OB::ITEM_F4); }
+    static constexpr int ops(int item) { return item < OA::ITEMS ? OA::OPS : OB::OPS; }
     static constexpr int ops_before(int item) {
         int n = 0;
         for(int i = 0; i < item; ++i) n += ops(i);
@@ -426,7 +435,7 @@ __device__ __forceinline__ void stage(f32x4 (&ra)[NA], f32x4 (&rb)[NB], EA* sa, 
                                       const GemmParams& p, int64_t row0, int64_t col0, int64_t kn,
                                       int64_t kend) {
     using S = Staging<AK, BKF, T>;
-    constexpr int IA = S::OA::ITEMS, FA = S::OA::ITEM_F4, FB = S::OB::ITEM_F4;
+    constexpr int IA = S::OA::ITEMS, FA = 1, FB = 1;
     constexpr int lo = S::lo(G), hi = S::lo(G + 1);
 #pragma unroll
     for(int e = lo; e < hi; ++e) {
@@ -680,23 +689,23 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
     using OB = Operand<BKF, T::BN>;
 #pragma unroll
     for(int e = 0; e < OA::ITEMS; ++e)
-        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, j.kbeg, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
+        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, j.kbeg, p.M, j.kend, e, &ra[e]);
 #pragma unroll
     for(int e = 0; e < OB::ITEMS; ++e)
         load_item<BKF, EDGE, T::BN, PAIR>(j.B, p.ldb, j.col0, j.kbeg, p.N, j.kend, e,
-                                          &rb[e * OB::ITEM_F4], p.pair_F - T::BN / 2);
+                                          &rb[e], p.pair_F - T::BN / 2);
 #pragma unroll
-    for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, T::BM>(sa, e, &ra[e * OA::ITEM_F4]);
+    for(int e = 0; e < OA::ITEMS; ++e) store_item<AK, T::BM>(sa, e, &ra[e]);
 #pragma unroll
-    for(int e = 0; e < OB::ITEMS; ++e) store_item<BKF, T::BN>(sb, e, &rb[e * OB::ITEM_F4]);
+    for(int e = 0; e < OB::ITEMS; ++e) store_item<BKF, T::BN>(sb, e, &rb[e]);
     const int64_t k1 = j.kbeg + (j.nslices > 1 ? BK : 0);
 #pragma unroll
     for(int e = 0; e < OA::ITEMS; ++e)
-        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, k1, p.M, j.kend, e, &ra[e * OA::ITEM_F4]);
+        load_item<AK, EDGE, T::BM>(j.A, p.lda, j.row0, k1, p.M, j.kend, e, &ra[e]);
 #pragma unroll
     for(int e = 0; e < OB::ITEMS; ++e)
         load_item<BKF, EDGE, T::BN, PAIR>(j.B, p.ldb, j.col0, k1, p.N, j.kend, e,
-                                          &rb[e * OB::ITEM_F4], p.pair_F - T::BN / 2);
+                                          &rb[e], p.pair_F - T::BN / 2);
 }
 
 template <bool TA, bool TB, int EDGE, class T, int EPI>
@@ -1347,7 +1356,13 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
                      (sA_inner % 4) == 0 && (sB_outer % 4) == 0 && (sB_inner % 4) == 0 &&
                      pk::aligned16(A) && pk::aligned16(B);
     const bool whole = (M % tc.bm) == 0 && (N % tc.bn) == 0 && (K % BK) == 0;
-    const int edge = vec && whole ? kEdgeNone
+    // whole tiles load through buffer resources with 32-bit offsets from each
+    // operand's start: op(A) and op(B) must each span less than 2^31 bytes
+    auto extent = [K](bool kfast, int64_t rows, int64_t ld) {
+        return 4 * (kfast ? (rows - 1) * ld + K : (K - 1) * ld + rows);
+    };
+    const bool small = extent(!TA, M, lda) < INT32_MAX && extent(TB, N, ldb) < INT32_MAX;
+    const int edge = vec && whole && small ? kEdgeNone
                      : vec && (M % 4) == 0 && (N % 4) == 0 && (K % 4) == 0 ? kEdgeVec
                                                                            : kEdgeScalar;
     const TileKind kind = tc.kind;
