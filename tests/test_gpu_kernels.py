@@ -675,6 +675,30 @@ def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
 
 
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(4352, 4096, 96), (3072, 3072, 64), (768, 32000, 64),
+                                    (8192, 2304, 128), (4096, 2304, 64), (6144, 4096, 160)])
+def test_gemm_tile_rounds(dev, ta, tb, M, N, Kd):
+    # whole tiles, more of them than resident workgroups, so later tiles run
+    # on workgroups dispatched as earlier ones finish: 4352 x 4096 is 272
+    # tiles of 256 x 256 for 256 slots (16 in a second round); 3072^2 and the
+    # LM head's weight gradient [768, 32000] 576 and 1500 tiles of 128 x 128
+    # for 512; 8192 x 2304 768 of 256 x 96 for 256; 4096 x 2304 768 of
+    # 128 x 96 for 512; 6144 x 4096 384 of 256 x 256
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 11 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    C = cu(ref.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)  # C - A.B = 0 exactly
+    assert not np.any(host(C))
+    C0 = O.uniform(M * N, 13).reshape(M, N)
+    C = cu(C0.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=0.5, beta=2.0)
+    assert np.array_equal(host(C), (0.5 * ref).astype(np.float32) + 2.0 * C0)
+
+
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
 @pytest.mark.parametrize("M,N,Kd", [(4096, 1376, 512), (1000, 1376, 516), (516, 960, 100),
                                     (8192, 768, 772), (1024, 1024, 1024), (200, 64, 36)])
 def test_gemm_vector_edge_tiles(dev, ta, tb, M, N, Kd):
