@@ -123,6 +123,14 @@ def sweep_section(torch, K, sizes, gemm=None):
         B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
         C = torch.empty(n, n, device=dev)
         reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
+        # untimed conditioning at each size, as for the headline: the clock
+        # settles to the load of the new size before its first timed layout
+        # (without it the first layout after a smaller size measured 5-6 %
+        # slow at 4096^3)
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            gemm("N", "N", A, B, C)
+            torch.cuda.synchronize()
         row = {}
         for ta, tb in (("N", "N"), ("N", "T"), ("T", "N")):
             mean_ms, _ = _events_time(lambda: gemm(ta, tb, A, B, C), reps, 2)
