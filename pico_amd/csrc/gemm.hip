@@ -708,7 +708,7 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
                                           &rb[e], p.pair_F - T::BN / 2);
 }
 
-template <bool TA, bool TB, int EDGE, class T, int EPI>
+template <bool TA, bool TB, int EDGE, class T, int EPI, bool DEEP = false>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
     // op(A) rows are k-contiguous when A is not transposed; op(B)^T rows
@@ -744,43 +744,59 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int NMFMA = TM * TN * 4;
 
     if(nslices > 0) {
+        constexpr bool PAIR = EPI == kEpiSwigluFwd;
+        // DEEP (tiles of at most 128x128, whose slices are short: 0.4-1.7 us):
+        // two slices in the staging registers, fetched three slices ahead, so
+        // a load has two slices' time to arrive rather than one.  It costs
+        // 15-30 VGPRs, which the launcher spends only on unsplit products
+        constexpr bool PF2 = DEEP && BM * BN <= 128 * 128;
+        constexpr int AHEAD = PF2 ? 3 : 2;
         f32x4 ra[OA::F4], rb[OB::F4];
-        prologue<AK, BKF, EDGE, T, EPI == kEpiSwigluFwd>(p, job, ra, rb, ldsA[0], ldsB[0]);
+        prologue<AK, BKF, EDGE, T, PAIR>(p, job, ra, rb, ldsA[0], ldsB[0]);
+        f32x4 ra2[PF2 ? OA::F4 : 1], rb2[PF2 ? OB::F4 : 1];
+        if constexpr(PF2) {
+            const int64_t k2 = kbeg + (int64_t)min(2, nslices - 1) * BK;
+#pragma unroll
+            for(int e = 0; e < OA::ITEMS; ++e)
+                load_item<AK, EDGE, BM>(A, p.lda, row0, k2, p.M, kend, e, &ra2[e]);
+#pragma unroll
+            for(int e = 0; e < OB::ITEMS; ++e)
+                load_item<BKF, EDGE, BN, PAIR>(B, p.ldb, col0, k2, p.N, kend, e, &rb2[e],
+                                               p.pair_F - BN / 2);
+        }
         __syncthreads();
         float fa0[TM][4], fb0[TN][4], fa1[TM][4], fb1[TN][4];
         read_group<TM>(ldsA[0], ar0, lr, lh, 0, fa0);
         read_group<TN>(ldsB[0], br0, lr, lh, 0, fb0);
-        for(int s = 0; s < nslices; ++s) {
+        // slice s: stage (xa, xb) -- slice s+1 -- into the other LDS buffer and
+        // refill them with slice s+AHEAD; past the end the refill re-fetches the
+        // last slice, which keeps the loop free of branches
+        auto slice = [&](int s, f32x4 (&xa)[OA::F4], f32x4 (&xb)[OB::F4]) {
             const int cur = s & 1;
             const float* la = ldsA[cur];
             const float* lb = ldsB[cur];
             float* sa = ldsA[cur ^ 1];
             float* sb = ldsB[cur ^ 1];
-            // the slice the staging registers fetch next; past the end it
-            // re-fetches the last slice, which keeps the loop free of branches
-            const int64_t kn = kbeg + (int64_t)min(s + 2, nslices - 1) * BK;
+            const int64_t kn = kbeg + (int64_t)min(s + AHEAD, nslices - 1) * BK;
 
             // group 0: read group 1, stage part 0
             read_group<TM>(la, ar0, lr, lh, 1, fa1);
             read_group<TN>(lb, br0, lr, lh, 1, fb1);
-            stage<AK, BKF, EDGE, T, 0, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
-                                                             kend);
+            stage<AK, BKF, EDGE, T, 0, PAIR>(xa, xb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
             interleave<NMFMA, RD + S::group_ops(0)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 1: read group 2, stage part 1
             read_group<TM>(la, ar0, lr, lh, 2, fa0);
             read_group<TN>(lb, br0, lr, lh, 2, fb0);
-            stage<AK, BKF, EDGE, T, 1, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
-                                                             kend);
+            stage<AK, BKF, EDGE, T, 1, PAIR>(xa, xb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa1, fb1);
             interleave<NMFMA, RD + S::group_ops(1)>();
             __builtin_amdgcn_sched_barrier(0);
             // group 2: read group 3, stage part 2
             read_group<TM>(la, ar0, lr, lh, 3, fa1);
             read_group<TN>(lb, br0, lr, lh, 3, fb1);
-            stage<AK, BKF, EDGE, T, 2, EPI == kEpiSwigluFwd>(ra, rb, sa, sb, A, B, p, row0, col0, kn,
-                                                             kend);
+            stage<AK, BKF, EDGE, T, 2, PAIR>(xa, xb, sa, sb, A, B, p, row0, col0, kn, kend);
             mfma_group<TM, TN>(acc, fa0, fb0);
             interleave<NMFMA, RD + S::group_ops(2)>();
             __builtin_amdgcn_sched_barrier(0);
@@ -793,6 +809,17 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
             mfma_group<TM, TN>(acc, fa1, fb1);
             interleave<NMFMA, RD>();
             __builtin_amdgcn_sched_barrier(0);
+        };
+        if constexpr(PF2) {
+            // even slices stage ra/rb, odd ones ra2/rb2
+            int s = 0;
+            for(; s + 1 < nslices; s += 2) {
+                slice(s, ra, rb);
+                slice(s + 1, ra2, rb2);
+            }
+            if(s < nslices) slice(s, ra, rb);
+        } else {
+            for(int s = 0; s < nslices; ++s) slice(s, ra, rb);
         }
     }
     if constexpr(EPI == kEpiPlain)
@@ -1176,8 +1203,18 @@ void launch_epi(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
         gemm_bf16_kernel<TA, TB, EDGE, T, false, EPI><<<grid, NT, 0, st>>>(gp);
     else if(prec == kBf16x3)
         gemm_bf16_kernel<TA, TB, EDGE, T, true, EPI><<<grid, NT, 0, st>>>(gp);
-    else
+    else if constexpr(T::BM * T::BN <= 128 * 128) {
+        // unsplit products of the small tiles stage two slices ahead; a split
+        // product (weight gradients, concurrent with other work) keeps the
+        // smaller register footprint, which lets more of that work share its
+        // CUs (a config-5 step measured 0.5 ms slower with both deep)
+        if(gp.splits == 1)
+            gemm_f32_kernel<TA, TB, EDGE, T, EPI, true><<<grid, NT, 0, st>>>(gp);
+        else
+            gemm_f32_kernel<TA, TB, EDGE, T, EPI><<<grid, NT, 0, st>>>(gp);
+    } else {
         gemm_f32_kernel<TA, TB, EDGE, T, EPI><<<grid, NT, 0, st>>>(gp);
+    }
 }
 
 // The staged epilogues are instantiated only where they are used: the
