@@ -24,7 +24,9 @@
 //    read from LDS while the MFMAs of group q run (two register sets).  The
 //    next slice is staged into the other LDS buffer, and the slice after it
 //    fetched into registers with 128-bit global loads, spread over groups 0-2.
-//    Every memory instruction is interleaved with the MFMAs through
+//    Unsplit products of the tiles up to 128x128, whose slices are short and
+//    which have at most two workgroups per CU to hide a load, hold two slices
+//    in registers and fetch three ahead.  Every memory instruction is interleaved with the MFMAs through
 //    sched_group_barrier, so the wave never issues a long run of loads or
 //    stores while the matrix pipe drains (measured: a block of 16 back-to-back
 //    stores + 16 loads per slice cost 13 % of the MFMA rate).  One barrier per
