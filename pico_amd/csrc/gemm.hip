@@ -24,9 +24,9 @@
 //    read from LDS while the MFMAs of group q run (two register sets).  The
 //    next slice is staged into the other LDS buffer, and the slice after it
 //    fetched into registers with 128-bit global loads, spread over groups 0-2.
-//    Unsplit products of the tiles up to 128x128, whose slices are short and
-//    which have at most two workgroups per CU to hide a load, hold two slices
-//    in registers and fetch three ahead.  Every memory instruction is interleaved with the MFMAs through
+//    Unsplit products of the tiles up to 128x128 and of 256x96, which have at
+//    most two workgroups per CU to hide a load, hold two slices in registers
+//    and fetch three ahead.  Every memory instruction is interleaved with the MFMAs through
 //    sched_group_barrier, so the wave never issues a long run of loads or
 //    stores while the matrix pipe drains (measured: a block of 16 back-to-back
 //    stores + 16 loads per slice cost 13 % of the MFMA rate).  One barrier per
@@ -710,6 +710,12 @@ __device__ __forceinline__ void prologue(const GemmParams& p, const TileJob& j, 
                                           &rb[e], p.pair_F - T::BN / 2);
 }
 
+// the tiles that can hold a second slice in their staging registers
+template <class T>
+constexpr bool deep_staging() {
+    return T::BM * T::BN <= 128 * 128 || (T::BM == 256 && T::BN == 96);
+}
+
 template <bool TA, bool TB, int EDGE, class T, int EPI, bool DEEP = false>
 __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, WGN = T::WGN;
@@ -747,11 +753,12 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_f32_kernel(GemmParams p) {
 
     if(nslices > 0) {
         constexpr bool PAIR = EPI == kEpiSwigluFwd;
-        // DEEP (tiles of at most 128x128, whose slices are short: 0.4-1.7 us):
-        // two slices in the staging registers, fetched three slices ahead, so
-        // a load has two slices' time to arrive rather than one.  It costs
-        // 15-30 VGPRs, which the launcher spends only on unsplit products
-        constexpr bool PF2 = DEEP && BM * BN <= 128 * 128;
+        // DEEP (tiles of at most 128x128, whose slices are short: 0.4-1.7 us,
+        // and 256x96, one workgroup per CU): two slices in the staging
+        // registers, fetched three slices ahead, so a load has two slices'
+        // time to arrive rather than one.  It costs 15-60 VGPRs, which the
+        // launcher spends only on unsplit products; 256x256 has none to spare
+        constexpr bool PF2 = DEEP && deep_staging<T>();
         constexpr int AHEAD = PF2 ? 3 : 2;
         f32x4 ra[OA::F4], rb[OB::F4];
         prologue<AK, BKF, EDGE, T, PAIR>(p, job, ra, rb, ldsA[0], ldsB[0]);
@@ -1205,7 +1212,7 @@ void launch_epi(const GemmParams& gp, dim3 grid, int prec, hipStream_t st) {
         gemm_bf16_kernel<TA, TB, EDGE, T, false, EPI><<<grid, NT, 0, st>>>(gp);
     else if(prec == kBf16x3)
         gemm_bf16_kernel<TA, TB, EDGE, T, true, EPI><<<grid, NT, 0, st>>>(gp);
-    else if constexpr(T::BM * T::BN <= 128 * 128) {
+    else if constexpr(deep_staging<T>()) {
         // unsplit products of the small tiles stage two slices ahead; a split
         // product (weight gradients, concurrent with other work) keeps the
         // smaller register footprint, which lets more of that work share its
