@@ -63,8 +63,10 @@ int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, 
  * order of d_model, K = tokens), K is split into slices whose partial products
  * go to the workspace and are summed by a second kernel in slice order, so the
  * result is deterministic.  pk_gemm_workspace_f32 returns the bytes a split
- * needs (0 when the product runs unsplit); a NULL or smaller workspace runs it
- * unsplit.  Same backward roles as pk_gemm_f32 (src/autograd.h:96-130). */
+ * of this shape needs in any layout (0 when no layout splits it: A^T.B splits
+ * wherever another layout does, while A.B and A.B^T with a long K run unsplit
+ * once 64x64 tiles give every CU two); a NULL or smaller workspace runs the
+ * product unsplit.  Same backward roles as pk_gemm_f32 (src/autograd.h:96-130). */
 size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K);
 int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
@@ -76,8 +78,8 @@ int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alph
  * loops, harnesses that forbid hipMalloc.  A product that splits K puts its
  * partial planes in a static device array of pk_gemm_noalloc_scratch_bytes()
  * (128 MiB) that each GPU holds until the process ends; a product whose
- * partials need more (pk_gemm_workspace_f32 above that size) is refused with
- * PK_EINVAL and a message.  Results equal pk_gemm_ex_f32's bit for bit.
+ * partials need more (in its own layout; pk_gemm_workspace_f32 is the largest
+ * over layouts) is refused with PK_EINVAL and a message.  Results equal pk_gemm_ex_f32's bit for bit.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (two streams, two threads) race, so serialise them. */
 size_t pk_gemm_noalloc_scratch_bytes(void);

@@ -1168,9 +1168,17 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all, int64_
 //    with 2 splits; 1024^3 82 against 72 with 4).  Longer K keeps splitting:
 //    [768, 2304] with K = 8192 (432 tiles of 64x64) runs at 97 TF/s unsplit
 //    and 109-115 split.
+//  * K >= 4096, op(A) not transposed (NN, NT: a training step's forward and
+//    input-gradient products, on its critical stream), fp32 and at least two
+//    64x64 tiles per CU: never.  Those run unsplit with the two-slice staging and
+//    no reduction pass (config 4's LM-head input gradient [4096, 512] with
+//    K 8192: step 1.79-1.81 against 1.81-1.82 ms).  A^T.B products (weight
+//    gradients, which a training step runs beside other work) keep splitting:
+//    their shorter split workgroups share the CUs better ([768, 4096] unsplit
+//    cost a config-5 step 1 ms).
 constexpr int64_t kSplitTarget = 512, kMinSplitK = 512;
 
-int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
+int choose_splits(int64_t M, int64_t N, int64_t K, bool ta, bool fp32, int64_t* kchunk) {
     const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
     *kchunk = K;
     if(tiles <= 0 || tiles * 2 > kSplitTarget || K < kMinSplitK) return 1;
@@ -1178,6 +1186,8 @@ int choose_splits(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
     if(K < 4096) {
         const TileChoice t = pick_tile(M, N, 1, true);
         if(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) >= kCUs) return 1;
+    } else if(!ta && fp32 && ((M + 63) / 64) * ((N + 63) / 64) >= 2 * kCUs) {
+        return 1;
     }
     const int64_t min_slice = K >= 1024 ? 256 : 128;
     int64_t s_max = K / min_slice;
@@ -1369,7 +1379,7 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     gp.ws = nullptr;
     if(batch == 1 && causal == 0 && ws && K > 0 && !swiglu && !sfwd) {
         int64_t kchunk;
-        const int S = choose_splits(M, N, K, &kchunk);
+        const int S = choose_splits(M, N, K, TA, prec == kFp32, &kchunk);
         if(S > 1 && ws_bytes >= (size_t)S * (size_t)M * (size_t)N * sizeof(float)) {
             gp.splits = S;
             gp.kchunk = kchunk;
@@ -1447,11 +1457,17 @@ extern "C" int pk_gemm_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, fl
                      0, nullptr, 0, kFp32, stream);
 }
 
-extern "C" size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K) {
+// the split-K partials of op(A) . op(B) for one layout of A
+static size_t gemm_workspace(int64_t M, int64_t N, int64_t K, bool ta) {
     if(M <= 0 || N <= 0 || K <= 0) return 0;
     int64_t kchunk;
-    const int S = choose_splits(M, N, K, &kchunk);
+    const int S = choose_splits(M, N, K, ta, true, &kchunk);
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+// any layout: A^T.B splits whenever another layout of the shape does
+extern "C" size_t pk_gemm_workspace_f32(int64_t M, int64_t N, int64_t K) {
+    return gemm_workspace(M, N, K, true);
 }
 
 extern "C" int pk_gemm_ex_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
@@ -1683,7 +1699,7 @@ extern "C" size_t pk_gemm_noalloc_scratch_bytes(void) { return kNoAllocScratchBy
 extern "C" int pk_gemm_noalloc_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                                    const float* A, int64_t lda, const float* B, int64_t ldb,
                                    float beta, float* C, int64_t ldc, pk_stream_t stream) {
-    const size_t need = pk_gemm_workspace_f32(M, N, K);
+    const size_t need = gemm_workspace(M, N, K, ta == 'T' || ta == 't');
     if(need > kNoAllocScratchBytes)
         return pk::fail("pk_gemm_noalloc_f32: this product's split-K partials need %zu bytes, "
                         "above the %zu-byte static scratch (use pk_gemm_ex_f32 with a workspace)",

@@ -101,11 +101,14 @@ def test_gemm_large_sampled_rows(dev, ta, tb, n):
 @pytest.mark.parametrize("ta,tb", [("T", "N"), ("N", "T"), ("N", "N")])
 @pytest.mark.parametrize("M,N,Kd,split", [(768, 768, 8192, True), (768, 2048, 8192, True),
                                           (200, 136, 4000, True), (64, 128, 784, True),
-                                          (64, 10, 256, False), (1024, 512, 768, False)])
+                                          (64, 10, 256, False), (1024, 512, 768, False),
+                                          (2048, 1024, 4096, True)])
 def test_gemm_splitk(dev, ta, tb, M, N, Kd, split):
     # weight-gradient shapes and a tiny output with a long K: K split into
     # slices summed in a fixed order; short K, or an output the 64 x 64 tiles
-    # already spread over the chip, stays unsplit
+    # already spread over the chip, stays unsplit.  2048 x 1024 with K 4096
+    # splits as A^T.B only: A.B and A.B^T have two 64 x 64 tiles per CU and run
+    # unsplit (the workspace size is the largest over layouts)
     need = K.gemm_workspace(M, N, Kd)
     assert (need > 0) == split
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N, integer=True)

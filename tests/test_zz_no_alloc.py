@@ -70,18 +70,32 @@ def test_noalloc_matches_workspace_entry_point_twice(dev):
 
 def test_noalloc_refuses_partials_above_its_scratch(dev):
     L = _lib.hip_lib()
-    M, N, K = 1408, 2048, 65536  # 286 MiB of partial planes
+    # A^T.B (a weight gradient's layout) splits K: 286 MiB of partial planes
+    M, N, K = 1408, 2048, 65536
     need = L.pk_gemm_workspace_f32(M, N, K)
     assert need > L.pk_gemm_noalloc_scratch_bytes()
     # valid buffers of the right sizes, although a refused call touches none
-    A = torch.zeros(M, K, device=dev)
+    A = torch.zeros(K, M, device=dev)
     B = torch.zeros(K, N, device=dev)
     C = torch.full((M, N), 7.0, device=dev)
-    st = _noalloc("N", "N", M, N, K, A, K, B, N, 0.0, C, N)
+    st = _noalloc("T", "N", M, N, K, A, M, B, N, 0.0, C, N)
     assert st == -1
     assert b"static scratch" in L.pk_last_error()
     torch.cuda.synchronize()
     assert bool((C == 7.0).all())
+
+
+def test_noalloc_long_k_forward_layout_runs_unsplit(dev):
+    """The same shape as A.B: two 64x64 tiles per CU, so it runs unsplit and
+    needs no scratch, whatever the A^T.B layout would."""
+    L = _lib.hip_lib()
+    M, N, K = 1408, 2048, 65536
+    A = torch.ones(M, K, device=dev)
+    B = torch.full((K, N), 0.5, device=dev)
+    C = torch.full((M, N), 7.0, device=dev)
+    assert _noalloc("N", "N", M, N, K, A, K, B, N, 0.0, C, N) == 0
+    torch.cuda.synchronize()
+    assert bool((C == 0.5 * K).all())
 
 
 def test_noalloc_unsplit_product_needs_no_scratch(dev):
