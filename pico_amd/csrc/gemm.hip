@@ -1172,7 +1172,7 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all, int64_
 //    input-gradient products, on its critical stream), fp32 and at least two
 //    64x64 tiles per CU: never.  Those run unsplit with the two-slice staging and
 //    no reduction pass (config 4's LM-head input gradient [4096, 512] with
-//    K 8192: step 1.79-1.81 against 1.81-1.82 ms).  A^T.B products (weight
+//    K 8192: step 1.78-1.80 against 1.82-1.84 ms).  A^T.B products (weight
 //    gradients, which a training step runs beside other work) keep splitting:
 //    their shorter split workgroups share the CUs better ([768, 4096] unsplit
 //    cost a config-5 step 1 ms).
