@@ -1395,8 +1395,20 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     // split products keep 128x128 tiles (the split count is sized for them);
     // causal products keep 128-row tiles (the attention chain's diagonal logic
     // is exercised at that size)
-    const TileChoice tc = gp.splits > 1 ? TileChoice{kTile128, 128, 128}
-                                        : pick_tile(M, N, batch, causal == 0, gp.pair_F);
+    TileChoice tc = gp.splits > 1 ? TileChoice{kTile128, 128, 128}
+                                  : pick_tile(M, N, batch, causal == 0, gp.pair_F);
+    // a short K over two or more rounds of 256x256 tiles (fp32, unsplit):
+    // 128x128 tiles with the two-slice staging, two per CU, where one tile's
+    // C stores and first loads overlap the other's products.  Measured in the
+    // config-5 forward (the SwiGLU-forward [8192, 4096] and LM-head [8192,
+    // 32000] products, K 768) and config 4's LM head ([4096, 8192], K 512):
+    // config-5 step 46.36-46.44 -> 46.16-46.23 ms on one box, 47.48-47.56 ->
+    // 47.40-47.46 on another.  One round (4096^2) and long K (8192^3) keep
+    // 256x256.
+    if(prec == kFp32 && gp.splits == 1 && tc.kind == kTile256 && K <= 1024 &&
+       ((M + 255) / 256) * ((N + 255) / 256) * batch > kCUs &&
+       (gp.pair_F == 0 || gp.pair_F % 64 == 0))
+        tc = TileChoice{kTile128, 128, 128};
     if(tc.bm == 0)
         return pk::fail("pk_gemm_swiglu_fwd_f32: F=%lld is not a multiple of 32 (no tile holds "
                         "whole gate/up column pairs)", (long long)gp.pair_F);

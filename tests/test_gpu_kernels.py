@@ -661,10 +661,11 @@ def test_gemm_96_wide_tiles(dev, ta, tb, M, N, Kd):
 
 
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
-@pytest.mark.parametrize("M,N,Kd", [(4096, 4096, 256), (4000, 4000, 200), (4096, 8192, 96),
+@pytest.mark.parametrize("M,N,Kd", [(4096, 4096, 256), (4000, 4000, 200), (4096, 8192, 1088),
                                     (4352, 3840, 1)])
 def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
-    # outputs of >= 256 tiles of 256 x 256 take the one-workgroup-per-CU shape;
+    # outputs of >= 256 tiles of 256 x 256 take the one-workgroup-per-CU shape
+    # (two rounds of them only with K > 1024: a shorter K takes 128 x 128);
     # 4000 and Kd = 200 / 1 exercise its edge path
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 5 * N + Kd, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
@@ -678,15 +679,16 @@ def test_gemm_256_tiles(dev, ta, tb, M, N, Kd):
 
 
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
-@pytest.mark.parametrize("M,N,Kd", [(4352, 4096, 96), (3072, 3072, 64), (768, 32000, 64),
+@pytest.mark.parametrize("M,N,Kd", [(4352, 4096, 1056), (3072, 3072, 64), (768, 32000, 64),
                                     (8192, 2304, 128), (4096, 2304, 64), (6144, 4096, 160)])
 def test_gemm_tile_rounds(dev, ta, tb, M, N, Kd):
     # whole tiles, more of them than resident workgroups, so later tiles run
-    # on workgroups dispatched as earlier ones finish: 4352 x 4096 is 272
-    # tiles of 256 x 256 for 256 slots (16 in a second round); 3072^2 and the
-    # LM head's weight gradient [768, 32000] 576 and 1500 tiles of 128 x 128
-    # for 512; 8192 x 2304 768 of 256 x 96 for 256; 4096 x 2304 768 of
-    # 128 x 96 for 512; 6144 x 4096 384 of 256 x 256
+    # on workgroups dispatched as earlier ones finish: 4352 x 4096 (K 1056) is
+    # 272 tiles of 256 x 256 for 256 slots (16 in a second round); 3072^2 and
+    # the LM head's weight gradient [768, 32000] 576 and 1500 tiles of
+    # 128 x 128 for 512; 8192 x 2304 768 of 256 x 96 for 256; 4096 x 2304 768
+    # of 128 x 96 for 512; 6144 x 4096 with K 160, two rounds of 256 x 256 with
+    # a short K, 1536 of 128 x 128
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 11 * N + Kd, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
     K.gemm(ta, tb, cu(As), cu(Bs), C)
