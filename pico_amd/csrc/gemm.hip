@@ -1409,6 +1409,15 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
        ((M + 255) / 256) * ((N + 255) / 256) * batch > kCUs &&
        (gp.pair_F == 0 || gp.pair_F % 64 == 0))
         tc = TileChoice{kTile128, 128, 128};
+    // A.B products on 256x96 tiles (one per CU) take 128x96 (two per CU,
+    // two-slice staging), so one tile's start and C writes overlap the other's
+    // products.  In a training step the A.B products are the forward's, which
+    // run alone: config 5's Q/K/V projection 213 -> 207 us, the residual-add
+    // products 81 -> 76 us (K 768) and 184 -> 180 us (K 2048), step 46.63-46.67
+    // -> 46.36-46.39 ms.  A.B^T and A^T.B keep 256x96: the backward runs them
+    // beside the weight-gradient stream, where 128x96 cost the step 0.75 ms.
+    if(prec == kFp32 && gp.splits == 1 && tc.kind == kTile256x96 && !TA && !TB)
+        tc = TileChoice{kTile96, 128, 96};
     if(tc.bm == 0)
         return pk::fail("pk_gemm_swiglu_fwd_f32: F=%lld is not a multiple of 32 (no tile holds "
                         "whole gate/up column pairs)", (long long)gp.pair_F);

@@ -645,9 +645,10 @@ def test_flash_attention_causality(dev):
                                     (8192, 768, 2048), (8000, 768, 772), (8001, 768, 37)])
 def test_gemm_96_wide_tiles(dev, ta, tb, M, N, Kd):
     # N a multiple of 96: [8192, 768] (a d_model-768 transformer's
-    # projections) and 8000 / 8001 rows take the 256 x 96 tiles, one per CU --
-    # 8000 x 772 on the float4 edge path, 8001 x 37 on the scalar one; 1000 x
-    # 768 and 4096 x 2304 the 128 x 96 ones, two per CU
+    # projections) and 8000 / 8001 rows take the 256 x 96 tiles, one per CU,
+    # except as A.B, which takes 128 x 96 -- 8000 x 772 on the float4 edge
+    # path, 8001 x 37 on the scalar one; 1000 x 768 and 4096 x 2304 the 128 x 96
+    # ones, two per CU
     A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 3 * N + Kd, integer=True)
     C = torch.full((M, N), float("nan"), device=dev)
     K.gemm(ta, tb, cu(As), cu(Bs), C)
