@@ -292,6 +292,11 @@ const char* pico_gpu_last_error(void);  /* "" when no error has occurred */
  * arena blocks, optimizer moments, scratch) */
 void pico_gpu_memory(size_t* in_use, size_t* peak);
 void pico_gpu_clear_error(void);
+/* testing aid (no reference counterpart): the next n requests for the
+ * optional split-K scratch of a matmul product are refused as if the device
+ * were out of memory, so the product runs unsplit; no error is recorded for
+ * them and pico_backward carries on */
+void pico_gpu_fail_next_workspaces(int n);
 
 /* ---- matmul precision (no reference counterpart: pico is fp32 only) ----
  * PICO_MATMUL_FP32 (the default): pico_matmul, the fused attention's

@@ -322,11 +322,7 @@ def api():
                  "pico_tensor_tanh", "pico_tensor_log", "pico_relu"):
         getattr(L, name).argtypes = [PT]
         getattr(L, name).restype = PT
-    L.pico_param.argtypes = [ctypes.POINTER(c_i64), ctypes.c_uint8]
-    L.pico_param.restype = PT
-    L.pico_free.argtypes = [PT]
-    L.pico_backward.argtypes = [c_p, PT]
-    L.pico_transpose_2d.argtypes = [PT]
+    _declare_api(L)
     L.arena_init.argtypes = [ctypes.c_size_t]
     L.arena_init.restype = c_p
     L.arena_ctx_push.argtypes = [c_p]
@@ -342,12 +338,6 @@ def api():
     L.pico_attention_causal.restype = PT
     L.pico_embedding.argtypes = [PT, c_p, c_i64]
     L.pico_embedding.restype = PT
-    L.pico_optim_sgd_init.argtypes = [c_f]
-    L.pico_optim_sgd_init.restype = c_p
-    L.pico_optim_sgd_add.argtypes = [c_p, PT]
-    L.pico_optim_sgd_step.argtypes = [c_p]
-    L.pico_optim_sgd_zero_grad.argtypes = [c_p]
-    L.pico_optim_sgd_free.argtypes = [c_p]
     L.pico_optim_adamw_init.argtypes = [c_f, c_f, c_f, c_f, c_f]
     L.pico_optim_adamw_init.restype = c_p
     L.pico_optim_adamw_add.argtypes = [c_p, PT]
@@ -356,6 +346,61 @@ def api():
     L.pico_optim_adamw_free.argtypes = [c_p]
     L._api_ready = True
     return L
+
+
+class PicoLinear(ctypes.Structure):
+    """struct PicoLinear (src/nn/linear.h:6-11)."""
+    _fields_ = [("in_features", c_int), ("out_features", c_int), ("weights", PT), ("bias", PT)]
+
+
+def _declare_api(L):
+    for name in ("pico_add", "pico_sub", "pico_mul", "pico_matmul"):
+        getattr(L, name).argtypes = [PT, PT]
+        getattr(L, name).restype = PT
+    L.pico_relu.argtypes = [PT]
+    L.pico_relu.restype = PT
+    L.pico_param.argtypes = [ctypes.POINTER(c_i64), ctypes.c_uint8]
+    L.pico_param.restype = PT
+    L.pico_create_tensor.argtypes = [c_p, ctypes.POINTER(c_i64), ctypes.c_uint8]
+    L.pico_create_tensor.restype = PT
+    L.pico_free.argtypes = [PT]
+    L.pico_backward.argtypes = [c_p, PT]
+    L.pico_transpose_2d.argtypes = [PT]
+    L.pico_optim_sgd_init.argtypes = [c_f]
+    L.pico_optim_sgd_init.restype = c_p
+    for name in ("pico_optim_sgd_step", "pico_optim_sgd_zero_grad", "pico_optim_sgd_free"):
+        getattr(L, name).argtypes = [c_p]
+    L.pico_optim_sgd_add.argtypes = [c_p, PT]
+    L.pico_nn_linear_init.argtypes = [c_int, c_int, ctypes.c_bool]
+    L.pico_nn_linear_init.restype = ctypes.POINTER(PicoLinear)
+    L.pico_nn_linear_forward.argtypes = [ctypes.POINTER(PicoLinear), PT]
+    L.pico_nn_linear_forward.restype = PT
+    L.pico_nn_linear_free.argtypes = [ctypes.POINTER(PicoLinear)]
+
+
+def ref_api():
+    """The compiled reference's own pico API (src/ops.h, tensor.h, act/,
+    optim/, nn/) with its C types declared, plus its static-inline arena
+    helpers under their pico names (ref_shim.c's wrappers), so one call
+    sequence runs on both ``api()`` and ``ref_api()``.  ``simd`` picks the
+    reference's kernel level (pico_init's AVX2 by default, as the oracle's
+    pico_init does)."""
+    R = ref()
+    if not getattr(R, "_api_ready", False):
+        _declare_api(R)
+        for name in ("arena_init", "arena_destroy", "arena_ctx_push", "arena_ctx_pop"):
+            setattr(R, name, getattr(R, "picoref_" + name))
+        R.arena_init.argtypes = [ctypes.c_size_t]
+        R.arena_init.restype = c_p
+        R.arena_destroy.argtypes = [c_p]
+        R.arena_ctx_push.argtypes = [c_p]
+        R._api_ready = True
+    return R
+
+
+def set_simd(L, level):
+    """g_simd_level of a library that exports it (src/global.h:7: 0 none .. 3 AVX2)"""
+    c_int.in_dll(L, "g_simd_level").value = level
 
 
 def param(shape, values=None):

@@ -119,3 +119,11 @@ void picoref_unary_bwd(int op, int64_t n, float* x, float* y, float* gy, float* 
         default: pico_tensor_log_backward(&self); break;
     }
 }
+
+/* pico's arena helpers are static inline in src/arena.h: entry points for the
+ * ones a caller of its op API needs (the ops themselves allocate from
+ * arena_ctx_current()) */
+struct Arena* picoref_arena_init(size_t bytes) { return arena_init(bytes); }
+void picoref_arena_destroy(struct Arena* arena) { arena_destroy(arena); }
+void picoref_arena_ctx_push(struct Arena* arena) { arena_ctx_push(arena); }
+void picoref_arena_ctx_pop(void) { arena_ctx_pop(); }

@@ -228,17 +228,23 @@ __device__ __forceinline__ void store_rowT(float* __restrict__ dst, const f32x16
 // again, which lands in the pad and is never read.  Wave w issues
 // instructions w, w+4, w+8, w+12, and wave 0 also instruction 16.
 //
-// The buffer resource spans exactly one head's rows (T rows of stride D from
-// the head's first column), so a load outside them returns zeros instead of
-// touching other memory.
+// Each block load builds a buffer resource that starts at the block's first
+// row and ends at the head's last element (row T-1, column 63), and puts the
+// whole per-lane offset in the bounds-checked vector offset (the scalar offset
+// of a buffer access is not bounds checked).  Rows at or past T -- the padding
+// rows of a last block when T is not a multiple of 128 -- therefore load as
+// zeros without reading memory: not the next sequence's rows, and nothing past
+// the end of the tensor.
 constexpr int LOADS = TILE * 4 / 1024;  // 17
 static_assert(TILE * 4 == LOADS * 1024, "a tile is a whole number of 1 KB loads");
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const float* head, int64_t T,
-                                                            int64_t D) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(head), (short)0,
-                                             (int)(((T - 1) * D + HD) * 4), 0x00020000);
+// rows row0.. of a head (row stride D) that holds T rows; empty when row0 >= T
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const float* head, int64_t T,
+                                                             int64_t D, int64_t row0) {
+    const int64_t bytes = T > row0 ? ((T - 1 - row0) * D + HD) * 4 : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(head + row0 * D), (short)0,
+                                             (int)bytes, 0x00020000);
 }
 
 // this lane's byte offsets (relative to the block's first row) for its wave's
@@ -253,17 +259,17 @@ struct BlockLoad {
             off[i] = (unsigned)((r * D + (c < HD ? c : 0)) * 4);
         }
     }
-    // issue the loads of the head's rows row0..row0+63 into tile
-    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, int64_t D, int64_t row0,
+    // issue the loads of rows row0..row0+63 of a head of T rows into tile
+    __device__ __forceinline__ void issue(const float* head, int64_t T, int64_t D, int64_t row0,
                                           float* tile, int w) const {
-        const unsigned so = (unsigned)(row0 * D * 4);
+        const __amdgpu_buffer_rsrc_t rs = block_rsrc(head, T, D, row0);
 #pragma unroll
         for(int i = 0; i < 4; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(tile + 256 * (w + 4 * i)), 16,
-                                                     off[i], so, 0, 0);
+                                                     off[i], 0, 0, 0);
         if(w == 0)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(tile + 256 * (LOADS - 1)), 16,
-                                                     off[4], so, 0, 0);
+                                                     off[4], 0, 0, 0);
     }
 };
 
@@ -320,9 +326,8 @@ __global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, Flash
     const int nw = (int)((q0 + 31) / BLK) + 1;          // blocks this wave sees
 
     const BlockLoad blk(p.ld, w, l);
-    const __amdgpu_buffer_rsrc_t rk = head_rsrc(K, p.T, p.ld), rv = head_rsrc(V, p.T, p.ld);
-    blk.issue(rk, p.ld, 0, sK, w);
-    blk.issue(rv, p.ld, 0, sV[0], w);
+    blk.issue(K, p.T, p.ld, 0, sK, w);
+    blk.issue(V, p.T, p.ld, 0, sV[0], w);
     float qf[32];
     load_frag32(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
     f32x16 o[2] = {zero16(), zero16()};
@@ -407,11 +412,11 @@ __global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, Flash
     auto begin_block = [&](int j) {
         wait_loads();
         __syncthreads();  // K(j), V(j) are in; V(j-1)'s buffer is free
-        if(j + 1 < nkv) blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
+        if(j + 1 < nkv) blk.issue(V, p.T, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
     };
     auto mid_block = [&](int j) {
         __syncthreads();  // every wave has read K(j)
-        if(j + 1 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, sK, w);
+        if(j + 1 < nkv) blk.issue(K, p.T, p.ld, (int64_t)(j + 1) * BLK, sK, w);
     };
     {  // block 0: the exact max; masked when it is also the wave's last
         begin_block(0);
@@ -533,13 +538,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
 
     const BlockLoad blq(p.ld, w, l), blo(p.D, w, l);
-    const __amdgpu_buffer_rsrc_t rq = head_rsrc(p.q + base, p.T, p.ld);
-    const __amdgpu_buffer_rsrc_t ro = head_rsrc(p.dout + obase, p.T, p.D);
+    const float *Qh = p.q + base, *Oh = p.dout + obase;
     const __amdgpu_buffer_rsrc_t rc = consts_rsrc(p.dsum, bh, p.Tp);
     auto issue = [&](int j, float* __restrict__ tq, float* __restrict__ to,
                      float* __restrict__ tl) {
-        blq.issue(rq, p.ld, (int64_t)j * BLK, tq, w);
-        blo.issue(ro, p.D, (int64_t)j * BLK, to, w);
+        blq.issue(Qh, p.T, p.ld, (int64_t)j * BLK, tq, w);
+        blo.issue(Oh, p.T, p.D, (int64_t)j * BLK, to, w);
         if(w == 1 && l < 32)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr_t*)tl, 16, 16 * l,
                                                      (unsigned)(j * 2 * BLK * 4), 0, 0);
@@ -653,8 +657,8 @@ __global__ __launch_bounds__(256, kDqSlots) void flash_bwd_dq(FlashParams p, Fla
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq, qg = q0 / 32;
 
     const BlockLoad blk(p.ld, w, l);
-    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.ld);
-    blk.issue(rk, p.ld, 0, sK[0], w);
+    const float* Kh = p.k + base;
+    blk.issue(Kh, p.T, p.ld, 0, sK[0], w);
     // tile (qg, kg) is at ds + kg*1024; this lane's 16 values at (2*lq + lh)*16
     const float* ds = p.ds + ds_tile(bh, p.Tp, qg, 0) + (2 * lq + lh) * 16;
     auto fetch = [&](int j, f32x16 (&x)[2]) {
@@ -680,7 +684,7 @@ __global__ __launch_bounds__(256, kDqSlots) void flash_bwd_dq(FlashParams p, Fla
     auto iter = [&](int j, const float* __restrict__ tk, float* __restrict__ kd) {
         wait_loads();
         __syncthreads();
-        if(j + 1 < nkv) blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, kd, w);
+        if(j + 1 < nkv) blk.issue(Kh, p.T, p.ld, (int64_t)(j + 1) * BLK, kd, w);
         if(j + 1 < nw) fetch(j + 1, nxt);
         if(j < nw) {
             const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;  // key offset <= lim visible
@@ -747,10 +751,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) 
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq, qg = q0 / 32;
 
     const BlockLoad blk(p.ld, w, l);
-    const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k + base, p.T, p.ld);
-    const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v + base, p.T, p.ld);
-    blk.issue(rk, p.ld, 0, sK[0], w);
-    blk.issue(rv, p.ld, 0, sV[0], w);
+    const float *Kh = p.k + base, *Vh = p.v + base;
+    blk.issue(Kh, p.T, p.ld, 0, sK[0], w);
+    blk.issue(Vh, p.T, p.ld, 0, sV[0], w);
     float qf[32], of[32];
     load_frag32(p.q + base + qi * p.ld, lh, qf, 1.0f, qi < p.T);
     load_frag32(p.dout + obase + qi * p.D, lh, of, 1.0f, qi < p.T);
@@ -767,8 +770,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_recompute(FlashParams p) 
         wait_loads();
         __syncthreads();  // block j is in; the other buffers (block j-1) are free
         if(j + 1 < nkv) {
-            blk.issue(rk, p.ld, (int64_t)(j + 1) * BLK, sK[(j + 1) & 1], w);
-            blk.issue(rv, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
+            blk.issue(Kh, p.T, p.ld, (int64_t)(j + 1) * BLK, sK[(j + 1) & 1], w);
+            blk.issue(Vh, p.T, p.ld, (int64_t)(j + 1) * BLK, sV[(j + 1) & 1], w);
         }
         if(j >= nw) continue;
         const int lim = (int)(qi - (int64_t)j * BLK) - 4 * lh;  // key offset <= lim visible

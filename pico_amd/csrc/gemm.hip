@@ -1568,12 +1568,25 @@ __global__ void fp8_scale_amax(int64_t ra, int64_t ca, const float* __restrict__
 }
 
 // scale = 2^floor(log2(448 / amax)): the largest power of two that keeps
-// amax * scale within e4m3's finite range; 1 for an all-zero or non-finite amax
+// amax * scale within e4m3's finite range; 1 for an all-zero or non-finite
+// amax.  The exponent is held to [-kFp8ScaleExp, kFp8ScaleExp], so each scale,
+// the product of two and its reciprocal (the kernel's alpha / (sA * sB)) stay
+// finite normals: below amax ~ 5e-17 (448 * 2^-63) the operand is scaled by
+// 2^63 only, above ~ 4e21 by 2^-63 only (and saturates at +-448).
+constexpr float kFp8ScaleExp = 63.0f;
 __global__ void fp8_scale_finish(unsigned* bits) {
     if(threadIdx.x >= 2) return;
     const float a = __uint_as_float(bits[threadIdx.x]);
     float sc = 1.0f;
-    if(a > 0.0f && a <= 3.0e38f) sc = exp2f(floorf(log2f(448.0f / a)));
+    if(a > 0.0f && a <= 3.0e38f) {
+        // a = m * 2^E with m in [0.5, 1) (subnormal a included) and 448 =
+        // 0.875 * 2^9, so a * 2^s <= 448 for s = 9 - E when m <= 0.875 and
+        // 8 - E otherwise, and not for s + 1: exact, no logarithm or 448 / a
+        int E;
+        const float m = frexpf(a, &E);
+        const float s = (float)((m <= 0.875f ? 9 : 8) - E);
+        sc = ldexpf(1.0f, (int)fminf(fmaxf(s, -kFp8ScaleExp), kFp8ScaleExp));
+    }
     reinterpret_cast<float*>(bits)[threadIdx.x] = sc;
 }
 }  // namespace

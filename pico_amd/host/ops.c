@@ -226,9 +226,13 @@ static int gemm_add_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int
     const int fp8 = g_matmul_precision == PICO_MATMUL_FP8;
     size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
     const size_t lead = fp8 ? FP8_SCALE_BYTES : 0;
-    void* ws = ws_bytes + lead ? (side ? pkh_side_workspace(ws_bytes + lead)
-                                       : pkh_workspace(ws_bytes + lead))
-                               : NULL;
+    /* split-K scratch is optional (the product runs unsplit without it); fp8's
+     * scales are not */
+    void* ws = NULL;
+    if(fp8)
+        ws = side ? pkh_side_workspace(ws_bytes + lead) : pkh_workspace(ws_bytes + lead);
+    else if(ws_bytes)
+        ws = side ? pkh_side_workspace_opt(ws_bytes) : pkh_workspace_opt(ws_bytes);
     float* scales = NULL;
     if(fp8) {
         if(!ws) return PK_EINVAL;

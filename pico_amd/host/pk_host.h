@@ -73,6 +73,9 @@ uint64_t pkh_side_joined(void);
 void pkh_side_join(void);
 /* the side stream's own scratch buffer (pkh_workspace is the main stream's) */
 void* pkh_side_workspace(size_t bytes);
+/* the same for a caller with a fallback (an unsplit product): NULL without a
+ * recorded error when the buffer cannot be had */
+void* pkh_side_workspace_opt(size_t bytes);
 
 /* AdamW state, for checkpoints (optim.c) */
 int pkh_adamw_moments(const struct PicoOptimAdamW* o, const struct PicoTensor* p, float** m,
@@ -87,6 +90,7 @@ void pkh_device_free(void* p);
 /* a device scratch buffer of at least `bytes`, reused across calls (the
  * previous contents are not preserved); valid until the next call */
 void* pkh_workspace(size_t bytes);
+void* pkh_workspace_opt(size_t bytes); /* optional: NULL without a recorded error */
 int pkh_is_device_ptr(const void* p);
 int pkh_copy_h2d(void* dst, const void* src, size_t bytes);
 int pkh_copy_d2h(void* dst, const void* src, size_t bytes);

@@ -165,19 +165,43 @@ void pkh_side_join(void) {
     g_side_joined = g_side_seq;
 }
 
-void* pkh_side_workspace(size_t bytes) {
-    if(bytes <= g_side_ws_bytes) return g_side_ws;
-    if(capture_refuses("growing the side-stream workspace")) return NULL;
-    if(g_side_ws) {
-        hipStreamSynchronize(g_side);
-        pkh_device_free(g_side_ws);
-        g_side_ws = NULL;
-        g_side_ws_bytes = 0;
+static void* device_alloc(size_t bytes, int quiet);
+static int g_fail_opt_ws = 0; /* pico_gpu_fail_next_workspaces */
+
+/* a scratch buffer of at least `bytes` in *buf, grown (after the stream that
+ * may still read the old one is done) when smaller.  `optional`: the caller
+ * has a fallback without it, so a failed allocation records no error (it
+ * would otherwise stop pico_backward) and returns NULL. */
+static void* grow_workspace(void** buf, size_t* have, hipStream_t st, size_t bytes, int optional,
+                            const char* what) {
+    if(optional && g_fail_opt_ws > 0) {
+        g_fail_opt_ws--;
+        return NULL;
     }
-    g_side_ws = pkh_device_alloc(bytes);
-    if(g_side_ws) g_side_ws_bytes = bytes;
-    return g_side_ws;
+    if(bytes <= *have) return *buf;
+    if(capture_refuses(what)) return NULL;
+    if(*buf) {
+        hipStreamSynchronize(st);
+        pkh_device_free(*buf);
+        *buf = NULL;
+        *have = 0;
+    }
+    *buf = device_alloc(bytes, optional);
+    if(*buf) *have = bytes;
+    return *buf;
 }
+
+void* pkh_side_workspace(size_t bytes) {
+    return grow_workspace(&g_side_ws, &g_side_ws_bytes, g_side, bytes, 0,
+                          "growing the side-stream workspace");
+}
+
+void* pkh_side_workspace_opt(size_t bytes) {
+    return grow_workspace(&g_side_ws, &g_side_ws_bytes, g_side, bytes, 1,
+                          "growing the side-stream workspace");
+}
+
+void pico_gpu_fail_next_workspaces(int n) { g_fail_opt_ws = n > 0 ? n : 0; }
 
 int pkh_sync(void) {
     if(pkh_init()) return -1;
@@ -194,13 +218,17 @@ void pico_gpu_clear_error(void) { g_err[0] = 0; }
 
 static size_t g_dev_bytes = 0, g_dev_peak = 0;
 
-void* pkh_device_alloc(size_t bytes) {
+/* quiet: a failure is the caller's to handle; it records no error and
+ * clears HIP's sticky status, so the next launch check does not see it */
+static void* device_alloc(size_t bytes, int quiet) {
     if(pkh_init()) return NULL;
     if(capture_refuses("device allocation")) return NULL;
     void* p = NULL;
     if(!bytes) bytes = 256;
     hipError_t e = hipMalloc(&p, bytes);
     if(e != hipSuccess) {
+        (void)hipGetLastError();
+        if(quiet) return NULL;
         pkh_set_error("device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
         PKH_ERR("%s\n", g_err);
         return NULL;
@@ -209,6 +237,8 @@ void* pkh_device_alloc(size_t bytes) {
     if(g_dev_bytes > g_dev_peak) g_dev_peak = g_dev_bytes;
     return p;
 }
+
+void* pkh_device_alloc(size_t bytes) { return device_alloc(bytes, 0); }
 
 void pkh_device_free(void* p) {
     if(!p) return;
@@ -224,18 +254,13 @@ void pico_gpu_memory(size_t* in_use, size_t* peak) {
 }
 
 void* pkh_workspace(size_t bytes) {
-    if(bytes <= g_ws_bytes) return g_ws;
-    if(capture_refuses("growing the GEMM workspace")) return NULL;
-    /* grow: wait for work that may still read the old buffer */
-    if(g_ws) {
-        hipStreamSynchronize((hipStream_t)pkh_stream());
-        pkh_device_free(g_ws);
-        g_ws = NULL;
-        g_ws_bytes = 0;
-    }
-    g_ws = pkh_device_alloc(bytes);
-    if(g_ws) g_ws_bytes = bytes;
-    return g_ws;
+    return grow_workspace(&g_ws, &g_ws_bytes, (hipStream_t)pkh_stream(), bytes, 0,
+                          "growing the GEMM workspace");
+}
+
+void* pkh_workspace_opt(size_t bytes) {
+    return grow_workspace(&g_ws, &g_ws_bytes, (hipStream_t)pkh_stream(), bytes, 1,
+                          "growing the GEMM workspace");
 }
 
 int pkh_is_device_ptr(const void* p) {

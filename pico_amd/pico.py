@@ -111,6 +111,7 @@ _GPU_SIGS = {
     "pico_gpu_synchronize": (ctypes.c_int, []),
     "pico_gpu_last_error": (ctypes.c_char_p, []),
     "pico_gpu_clear_error": (None, []),
+    "pico_gpu_fail_next_workspaces": (None, [ctypes.c_int]),
     "pico_gpu_memory": (None, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "pico_randn": (TP, [c_p, ctypes.POINTER(c_i64), ctypes.c_uint8]),
     "pico_gpt_init": (c_p, [ctypes.POINTER(PicoGPTConfig), ctypes.c_uint64]),

@@ -143,6 +143,51 @@ def test_fp8_scales_are_the_largest_safe_powers_of_two(dev):
                 assert 224.0 < amax * s_ <= 448.0
 
 
+def test_fp8_scales_of_extreme_magnitudes_stay_finite(dev):
+    """The scale's exponent is held to [-63, 63]: operands of magnitude 1e-37
+    (448 / amax overflows float), 1e-20 and near float's largest (1e38) all get
+    finite power-of-two scales whose product and its reciprocal are finite
+    normals, and a scaled product of two tiny operands is neither NaN nor
+    flushed to zero by the descale."""
+    from pico_amd import _lib
+
+    L = _lib.hip_lib()
+    sc = torch.full((2,), float("nan"), device=dev)
+    cases = [(1e-37, 1e-37), (1e-20, 3e-21), (2.0, 5e-38), (1e38, 1e38), (3e21, 1e-30)]
+    for amax_a, amax_b in cases:
+        A = cu(np.full((4, 8), amax_a, np.float32))
+        B = cu(np.full((8, 4), amax_b, np.float32))
+        _lib.check("pk_fp8_scales_f32", L.pk_fp8_scales_f32(
+            4, 8, A.data_ptr(), 8, 8, 4, B.data_ptr(), 4, sc.data_ptr(), None))
+        got = host(sc).astype(np.float64)
+        amax = (float(np.float32(amax_a)), float(np.float32(amax_b)))
+        for s_, m_ in zip(got, amax):
+            e = np.log2(s_)
+            assert np.isfinite(s_) and e == np.floor(e) and -63 <= e <= 63, (amax_a, amax_b)
+            # the largest power of two keeping amax within e4m3, unless clamped
+            want = min(max(np.floor(np.log2(448.0 / m_)), -63), 63)
+            assert e == want, (m_, e, want)
+        prod = np.float32(got[0]) * np.float32(got[1])
+        assert np.isfinite(prod) and prod > 0 and np.isfinite(np.float32(1.0) / prod)
+    # two operands of 1e-17: scaled by 2^63 each (448 / 1e-17 would want 2^65),
+    # their product, 32 * 1e-34 (a normal float), comes back through the
+    # descale 2^-126 exactly, not as 0 or NaN
+    A = cu(np.full((32, 32), 1e-17, np.float32))
+    _lib.check("pk_fp8_scales_f32", L.pk_fp8_scales_f32(
+        32, 32, A.data_ptr(), 32, 32, 32, A.data_ptr(), 32, sc.data_ptr(), None))
+    C = torch.full((32, 32), float("nan"), device=dev)
+    _lib.check("pk_gemm_add_f32", L.pk_gemm_add_f32(
+        b"N", b"N", 32, 32, 32, 1.0, A.data_ptr(), 32, A.data_ptr(), 32, 0.0, None, 32,
+        C.data_ptr(), 32, 3, sc.data_ptr(), None, 0, None))
+    s0 = float(host(sc)[0])
+    assert s0 == 2.0 ** 63
+    a8 = float(e4m3_round(np.array([np.float32(1e-17) * s0], np.float32))[0]) / s0
+    want = np.float32(32 * a8 * a8)
+    got = host(C)
+    assert np.isfinite(got).all() and np.all(got > 0)
+    assert np.max(np.abs(got - want)) <= 1e-4 * want
+
+
 def test_fp8_scaled_product_keeps_small_operands(dev):
     """gradient-sized operands (|x| ~ 1e-5, below e4m3's smallest subnormal)
     through the scaled fp8 product: the result equals the product of the

@@ -485,6 +485,47 @@ def test_flash_attention_vs_oracle(dev, B, H, T):
         assert close(host(got) - b0, ref)
 
 
+@pytest.mark.parametrize("B,T", [(2, 200), (1, 999)])
+def test_flash_attention_padding_rows_are_not_read(dev, B, T):
+    """A T that is not a multiple of 128 pads the last 128-row block; its rows
+    past T must load as zeros without reading memory.  Here q, k, v, dout and o
+    are the first B*T rows of larger buffers whose further rows are NaN
+    (inside the allocation, past the last sequence).  Every output must be
+    finite and equal bit for bit to the same call on zero-padded buffers, for
+    the fp32 kernels (stored and recomputed dQ) and the bf16 ones; the fp32
+    outputs also match the oracle."""
+    H, hd = 2, 64
+    D = H * hd
+    q, k, v, do = (O.normal(B * T * D, 171 + i).reshape(B * T, D) for i in range(4))
+
+    def padded(x, fill):
+        buf = torch.full((B * T + 128, D), fill, device=dev)
+        buf[:B * T] = cu(x)
+        return buf[:B * T]
+
+    runs = {}
+    for fill in ("zero", "nan"):
+        val = 0.0 if fill == "zero" else float("nan")
+        qv, kv, vv, dov = (padded(x, val) for x in (q, k, v, do))
+        for mode in ("fp32", "recompute", "bf16"):
+            o = padded(np.zeros_like(q), val)
+            lse = torch.empty(B * H * T, device=dev)
+            K.flash_fwd(B, H, qv, kv, vv, o, lse, bf16=mode == "bf16")
+            dq, dk, dv = (torch.full((B * T, D), float("nan"), device=dev) for _ in range(3))
+            K.flash_bwd(B, H, qv, kv, vv, o, lse, dov, dq, dk, dv, bf16=mode == "bf16",
+                        recompute=mode == "recompute")
+            runs[(fill, mode)] = [host(x) for x in (o, lse, dq, dk, dv)]
+    for mode in ("fp32", "recompute", "bf16"):
+        for got, want in zip(runs[("nan", mode)], runs[("zero", mode)]):
+            assert np.isfinite(got).all(), mode
+            assert np.array_equal(got, want), mode
+    o, lse, dq, dk, dv = runs[("nan", "fp32")]
+    o_ref, lse_ref = O.attn_fwd(B, H, q, k, v)
+    assert max_rel(o, o_ref) <= TOL and max_rel(lse, lse_ref) <= TOL
+    for got, ref in zip((dq, dk, dv), O.attn_bwd(B, H, q, k, v, o_ref, lse_ref, do)):
+        assert max_rel(got, ref) <= TOL
+
+
 @pytest.mark.parametrize("trend", ["rising", "falling"])
 def test_flash_attention_running_max_raises_and_underflow(dev, trend):
     """The forward keeps a stale running max, raised only when a key block's

@@ -6,6 +6,7 @@ where it was built), (3) torch-CPU float64 golden vectors for the ops the
 reference lacks, and (4) closed forms and invariants chosen so a dropped term,
 wrong sign or transposed operand fails.
 """
+import ctypes
 import os
 
 import numpy as np
@@ -221,6 +222,193 @@ def test_pico_rand_stream_matches_reference():
     theirs = np.empty(50, np.float32)
     O.ref().picoref_rand(ctypes.c_uint32(12345), ctypes.c_int64(50), O.p(theirs))
     assert np.array_equal(O.pico_rand(50, 12345), theirs)
+
+
+# ---------------- the op API, graph walk and optimizer vs the reference's own
+# The same call sequence runs on the oracle (O.api()) and on the compiled
+# reference's exported pico API (O.ref_api(): src/ops.c, act/activations.c,
+# autograd.h through pico_backward, optim/SGD.c, nn/linear.c), on seeded random
+# values with random upstream gradients, so the order of every sum over
+# stretched dims and every accumulation into a shared parent's grad shows.
+def _pv(L, shape, values):
+    arr = (ctypes.c_int64 * len(shape))(*shape)
+    t = L.pico_param(arr, len(shape))
+    O.set_data(t, values)
+    return t
+
+
+def _on_both(build, simd=3):
+    """build(L, arena) -> list of tensors; their data and grads, oracle then
+    reference, as uint32 bit patterns"""
+    outs = []
+    for L in (O.api(), O.ref_api()):
+        O.set_simd(L, simd)
+        ar = L.arena_init(1 << 24)
+        L.arena_ctx_push(ar)
+        try:
+            ts, owned = build(L, ar)
+            outs.append([np.concatenate([O.data(t), O.grad(t)]).view(np.uint32) for t in ts])
+            for t in owned:
+                L.pico_free(t)
+        finally:
+            L.arena_ctx_pop()
+            L.arena_destroy(ar)
+    O.set_simd(O.api(), 3)  # pico_init's level
+    return outs
+
+
+BCAST = [((5, 1, 3), (1, 4, 1)), ((2, 3, 4), (3, 1)), ((3, 64, 10), (1, 10)), ((4, 5), (5,)),
+         ((7, 1), (1, 6)), ((16, 19), (16, 19)), ((2, 1, 3, 1), (5, 1, 4)), ((6,), (1,)),
+         ((1,), (3, 2))]
+
+
+@needs_ref
+@pytest.mark.parametrize("simd", [0, 3])
+@pytest.mark.parametrize("sa,sb", BCAST)
+def test_broadcast_graph_bitexact_vs_reference(sa, sb, simd):
+    """add, sub and mul with numpy-style broadcasting, forward and backward
+    through pico_backward: s = a + b, d = s - b, m = d * b, y = m * w (b feeds
+    three ops, w random so every upstream gradient is random)"""
+    so = np.broadcast_shapes(sa, sb)
+    a0, b0 = O.normal(int(np.prod(sa)), 1), O.normal(int(np.prod(sb)), 2)
+    w0 = O.normal(int(np.prod(so)), 3)
+
+    def build(L, ar):
+        a, b, w = _pv(L, sa, a0), _pv(L, sb, b0), _pv(L, so, w0)
+        s = L.pico_add(a, b)
+        d = L.pico_sub(s, b)
+        m = L.pico_mul(d, b)
+        y = L.pico_mul(m, w)
+        L.pico_backward(ar, y)
+        return [a, b, w, s, d, m, y], [a, b, w]
+
+    ours, theirs = _on_both(build, simd)
+    for i, (x, r) in enumerate(zip(ours, theirs)):
+        assert np.array_equal(x, r), i
+
+
+@needs_ref
+def test_transposed_view_graph_bitexact_vs_reference():
+    """a pico_transpose_2d view (swapped shape and strides) as an operand of a
+    broadcast add and a same-shape mul, and its grad written at the view's
+    strides, against the reference's scalar kernels (cpu_scalar.h:12-30, which
+    index both operands through map_index).
+
+    The reference's AVX2 level differs here: its same-shape fast path
+    (cpu_avx_2.h:15-33) reads both operands in storage order and ignores a
+    view's strides, so w * a^T comes out as w * a elementwise in memory order.
+    The oracle (and the GPU library) keep the strided semantics of the scalar
+    path and of every backward hook; the second half pins that the AVX2
+    difference is exactly that flat read."""
+    a0, b0, w0 = O.normal(15, 4), O.normal(3, 5), O.normal(15, 6)
+
+    def build(L, ar):
+        a, b, w = _pv(L, [3, 5], a0), _pv(L, [3], b0), _pv(L, [5, 3], w0)
+        L.pico_transpose_2d(a)
+        wa = L.pico_mul(w, a)
+        y = L.pico_mul(L.pico_add(a, b), wa)
+        L.pico_backward(ar, y)
+        return [a, b, w, wa, y], [a, b, w]
+
+    ours, theirs = _on_both(build, simd=0)
+    for i, (x, r) in enumerate(zip(ours, theirs)):
+        assert np.array_equal(x, r), i
+    # the strided product, as the oracle computes it at any level
+    wa_ours = ours[3][:15].view(np.float32)
+    assert np.array_equal(wa_ours, (w0.reshape(5, 3) * a0.reshape(3, 5).T).ravel())
+    # the reference's AVX2 same-shape path: the flat storage-order product
+    _, avx2 = _on_both(build, simd=3)
+    assert np.array_equal(avx2[3][:15].view(np.float32), w0 * a0)
+
+
+@needs_ref
+def test_relu_graph_bitexact_vs_reference():
+    """relu forward (NaN -> 0, -0.0, exact zeros) and its gate y > 0"""
+    x0 = O.normal(64 * 33, 7)
+    x0[::17] = 0.0
+    x0[5::23] = -0.0
+    x0[3::31] = np.nan
+    w0 = O.normal(64 * 33, 8)
+
+    def build(L, ar):
+        x, w = _pv(L, [64, 33], x0), _pv(L, [64, 33], w0)
+        r = L.pico_relu(x)
+        y = L.pico_mul(r, w)
+        L.pico_backward(ar, y)
+        return [r, y, w], [x, w]
+
+    ours, theirs = _on_both(build)
+    for i, (x, r) in enumerate(zip(ours, theirs)):
+        assert np.array_equal(x, r), i
+
+
+@needs_ref
+def test_graph_walk_shared_parents_bitexact_vs_reference():
+    """a diamond-rich graph (a and b feed several ops, c feeds two): the
+    post-order walk fixes the order of the += into each shared grad, hence its
+    rounding; a second pico_backward over the same graph accumulates again"""
+    a0, b0, w0 = O.normal(6 * 5, 9), O.normal(6 * 5, 10), O.normal(6 * 5, 11)
+    bias0 = O.normal(5, 12)
+
+    def build(L, ar):
+        a, b, w, bias = (_pv(L, [6, 5], a0), _pv(L, [6, 5], b0), _pv(L, [6, 5], w0),
+                         _pv(L, [5], bias0))
+        c = L.pico_mul(a, b)
+        d = L.pico_add(c, a)
+        e = L.pico_mul(d, c)
+        f = L.pico_sub(e, L.pico_add(b, bias))
+        g = L.pico_mul(L.pico_add(f, a), w)
+        L.pico_backward(ar, g)
+        L.pico_backward(ar, g)
+        return [a, b, w, bias, c, d, e, f, g], [a, b, w, bias]
+
+    ours, theirs = _on_both(build)
+    for i, (x, r) in enumerate(zip(ours, theirs)):
+        assert np.array_equal(x, r), i
+
+
+@needs_ref
+def test_linear_and_sgd_steps_bitexact_vs_reference():
+    """PicoLinear (x.W + b, bias broadcast over the batch) through a two-layer
+    graph with relu, backward, then SGD steps (p -= lr*g, two roundings) and
+    zero_grad, three times: every weight, bias and activation bit for bit"""
+    x0 = O.normal(8 * 7, 13)
+    w10, b10 = O.normal(7 * 5, 14, 0.0, 0.5), O.normal(5, 15)
+    w20, b20 = O.normal(5 * 3, 16, 0.0, 0.5), O.normal(3, 17)
+    gy0 = O.normal(8 * 3, 18)
+
+    def build(L, ar):
+        l1 = L.pico_nn_linear_init(7, 5, True)
+        l2 = L.pico_nn_linear_init(5, 3, True)
+        for lin, wv, bv in ((l1, w10, b10), (l2, w20, b20)):
+            O.set_data(lin.contents.weights, wv)
+            O.set_data(lin.contents.bias, bv)
+        opt = L.pico_optim_sgd_init(ctypes.c_float(0.05))
+        params = [l1.contents.weights, l1.contents.bias, l2.contents.weights, l2.contents.bias]
+        for t in params:
+            L.pico_optim_sgd_add(opt, t)
+        x, gy = _pv(L, [8, 7], x0), _pv(L, [8, 3], gy0)
+        acts = []
+        for _ in range(3):
+            h = L.pico_relu(L.pico_nn_linear_forward(l1, x))
+            out = L.pico_nn_linear_forward(l2, h)
+            y = L.pico_mul(out, gy)
+            L.pico_backward(ar, y)
+            acts += [h, out]
+            L.pico_optim_sgd_step(opt)
+            grads = [O.grad(t).copy() for t in params]
+            L.pico_optim_sgd_zero_grad(opt)
+            assert not any(np.any(O.grad(t)) for t in params)
+            acts.append(_pv(L, [sum(g.size for g in grads)], np.concatenate(grads)))
+        L.pico_optim_sgd_free(opt)
+        snap = [_pv(L, [t.contents.numel], O.data(t)) for t in params]
+        L.pico_nn_linear_free(l1)
+        L.pico_nn_linear_free(l2)
+        return snap + acts, [x, gy] + snap + acts[2::3]
+
+    ours, theirs = _on_both(build)
+    for i, (x, r) in enumerate(zip(ours, theirs)):
+        assert np.array_equal(x, r), i
 
 
 # ------------------------------------------------------- math pins (GEMM)

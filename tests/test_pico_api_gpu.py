@@ -394,6 +394,37 @@ def test_residual_add_grads_vs_oracle(P, C):
         assert max_rel(g, c) <= TOL, i
 
 
+def test_backward_completes_without_split_k_scratch(P, C):
+    """A matmul product runs unsplit when its optional split-K scratch cannot be
+    had (pico_gpu_fail_next_workspaces refuses it as an out-of-memory would).
+    That is no error: pico_backward carries on to the hooks after it, and every
+    grad matches the oracle.  Weight gradients with K = 4096 rows and under 256
+    output tiles take split-K scratch, on the side stream (W2, W1) and on the
+    main stream (x . W1 with x a parameter too)."""
+    R, D, F = 4096, 128, 96
+    xv = O.normal(R * D, 1).reshape(R, D)
+    w1 = O.normal(D * F, 2, 0.0, 0.1).reshape(D, F)
+    w2 = O.normal(F * 64, 3, 0.0, 0.1).reshape(F, 64)
+    out = []
+    for L, fail in ((P, 0), (P, 8), (C, 0)):
+        with L.arena(1 << 24):
+            x = L.tensor([R, D], xv)
+            W1, W2, X2 = L.param([D, F], w1), L.param([F, 64], w2), L.param([R, D], xv)
+            y = L.add(L.matmul(L.matmul(x, W1), W2), L.matmul(L.matmul(X2, W1), W2))
+            if fail:
+                L.lib.pico_gpu_fail_next_workspaces(fail)
+            L.backward(y)  # raises on a recorded error
+            if fail:
+                L.lib.pico_gpu_fail_next_workspaces(0)
+                assert L.lib.pico_gpu_last_error() == b""
+            out.append([L.grad(t) for t in (W1, W2, X2)])
+            for t in (W1, W2, X2):
+                L.free(t)
+    for i in range(3):
+        assert max_rel(out[0][i], out[2][i]) <= TOL, i
+        assert max_rel(out[1][i], out[2][i]) <= TOL, i
+
+
 # ------------------------------------------------------ new hot-path ops
 def _new_ops_graph(L, gv, wv, ids, labels, table, B, H):
     x = L.embedding(L.param(list(table.shape), table), ids)
