@@ -187,6 +187,7 @@ def attn_section(torch, K):
 def rows_section(torch, K):
     """config-3 row kernels; 4 rotating buffer sets (> 256 MB MALL)"""
     dev = torch.device("cuda:0")
+    torch.manual_seed(3)  # the row kernels' inputs: torch's seeded device generator
     res = {}
     sets = 4
 
@@ -527,8 +528,105 @@ def train_section(name, steps, warmup, precision=0):
             "optimizer": dict(ADAMW, name="AdamW"), "config": cfg}
 
 
-def cpu_baseline(n):
-    """pico's AVX matmul on the host: warmup 1, median of 3 (bench_matmul_large.c:16-18)"""
+def _median_of_3(run):
+    """the reference benches' method (bench/bench_matmul_large.c:16-18,42-61):
+    one warmup call, then the median of three timed calls, in seconds"""
+    run()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[1]
+
+
+def cpu_matmul_backward(n):
+    """pico's pico_matmul_backward (src/autograd.h:96-130: dA += dC.B^T then
+    dB += A^T.dC, scalar, one thread) on n x n operands; 4n^3 FLOP a call"""
+    import ctypes
+
+    import numpy as np
+
+    from oracle import oracle as O
+
+    A, B, dC = (O.uniform(n * n, s).reshape(n, n) for s in (1, 2, 3))
+    dA, dB = np.zeros((n, n), np.float32), np.zeros((n, n), np.float32)
+    if O.ref_available():
+        kind, R = "reference", O.ref()
+
+        def run():
+            R.picoref_matmul_backward(ctypes.c_int(n), ctypes.c_int(n), ctypes.c_int(n), O.p(A),
+                                      O.p(B), O.p(dC), O.p(dA), O.p(dB))
+    else:
+        kind = "port"
+
+        def run():
+            O.matmul_backward(A, B, dC, dA, dB)
+
+    t = _median_of_3(run)
+    return {"n": n, "value": round(4.0 * n ** 3 / t / 1e9, 3), "unit": "GFLOP/s", "cores": 1,
+            "kind": kind, "s_per_call": round(t, 3),
+            "sample": f"pico_matmul_backward at {n}^3 (dA and dB, scalar loops), median of 3 after "
+                      "1 warmup"}
+
+
+def cpu_mlp_steps(steps=100):
+    """config 1 on the host: the same 784-128-10 ReLU MLP, softmax-CE and SGD
+    lr 0.01 step through the oracle's pico API (pico's CPU path as pico_init
+    configures it: the scalar matmul and backward loops, one thread), in the
+    pattern of examples/02_relu_mlp/main.c:96-110; the softmax-CE node is the
+    oracle's (pico has none).  Median of 3 runs of `steps` steps after 1."""
+    import ctypes
+
+    from oracle import oracle as O
+
+    L = O.api()
+    keep = L.arena_init(1 << 20)
+    L.arena_ctx_push(keep)
+    fc1, fc2 = L.pico_nn_linear_init(784, 128, True), L.pico_nn_linear_init(128, 10, True)
+    O.set_data(fc1.contents.weights, O.uniform(784 * 128, SEEDS["mlp_w1"], -784 ** -0.5,
+                                               784 ** -0.5))
+    O.set_data(fc2.contents.weights, O.uniform(128 * 10, SEEDS["mlp_w2"], -128 ** -0.5,
+                                               128 ** -0.5))
+    opt = L.pico_optim_sgd_init(ctypes.c_float(0.01))
+    for fc in (fc1, fc2):
+        L.pico_optim_sgd_add(opt, fc.contents.weights)
+        L.pico_optim_sgd_add(opt, fc.contents.bias)
+    x = O.param([64, 784], O.normal(64 * 784, SEEDS["mlp_x"]))
+    labels = O.labels(64, SEEDS["mlp_labels"], 10)
+    work = L.arena_init(1 << 24)
+    L.arena_ctx_push(work)
+    last = [0.0]
+
+    def run():
+        for _ in range(steps):
+            L.pico_optim_sgd_zero_grad(opt)
+            h = L.pico_relu(L.pico_nn_linear_forward(fc1, x))
+            loss = L.pico_softmax_xent(L.pico_nn_linear_forward(fc2, h), O.p(labels))
+            L.pico_backward(work, loss)
+            L.pico_optim_sgd_step(opt)
+            last[0] = float(O.data(loss)[0])
+            L.arena_reset(work)
+
+    t = _median_of_3(run)
+    L.arena_ctx_pop()
+    L.arena_destroy(work)
+    L.pico_optim_sgd_free(opt)
+    L.pico_free(x)
+    L.pico_nn_linear_free(fc1)
+    L.pico_nn_linear_free(fc2)
+    L.arena_ctx_pop()
+    L.arena_destroy(keep)
+    ms = t * 1e3 / steps
+    return {"value": round(64 / (ms * 1e-3), 1), "unit": "samples/s", "ms_per_step": round(ms, 4),
+            "cores": 1, "kind": "port", "loss_last": round(last[0], 5),
+            "sample": f"{steps} SGD steps of config 1 (batch 64), the oracle's restatement of "
+                      "pico's CPU path, median of 3 runs after 1"}
+
+
+def cpu_baseline(n, bwd_sizes=(1024,)):
+    """pico's AVX matmul on the host: warmup 1, median of 3 (bench_matmul_large.c:16-18);
+    then pico's scalar matmul backward and a config-1 training step"""
     import ctypes
 
     import numpy as np
@@ -552,13 +650,7 @@ def cpu_baseline(n):
         def run():
             O.matmul_avx(A, B)
 
-    run()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        ts.append(time.perf_counter() - t0)
-    t = sorted(ts)[1]
+    t = _median_of_3(run)
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -571,7 +663,9 @@ def cpu_baseline(n):
     return {"value": round(2.0 * n ** 3 / t / 1e12, 4), "unit": "TFLOP/s", "cores": 8,
             "kind": kind, "host_cpus": os.cpu_count(), "cpu_model": model,
             "sample": f"one fp32 matmul {n}^3 (forward A.B), pico's AVX+FMA kernel on its 8-worker "
-                      f"pool, median of 3 after 1 warmup, {t:.2f} s each"}
+                      f"pool, median of 3 after 1 warmup, {t:.2f} s each",
+            "matmul_backward": [cpu_matmul_backward(m) for m in bwd_sizes],
+            "config1_mlp_step": cpu_mlp_steps()}
 
 
 def main():
@@ -584,6 +678,9 @@ def main():
     ap.add_argument("--train-steps", type=int, default=50)
     ap.add_argument("--variant-steps", type=int, default=10)
     ap.add_argument("--train-configs", default=",".join(["config1"] + list(TRAIN_CONFIGS)))
+    # pico's scalar matmul backward on the host: 1024 takes ~10 s a call, 2048
+    # over a minute, so the default run times 1024 only
+    ap.add_argument("--cpu-bwd-sizes", default="1024")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -680,7 +777,31 @@ def main():
     if "rows" in sections:
         line["row_kernels"] = rows_section(torch, K)
     if "cpu" in sections:
-        line["cpu_baseline"] = cpu_baseline(args.n)
+        line["cpu_baseline"] = cpu_baseline(
+            args.n, [int(v) for v in args.cpu_bwd_sizes.split(",") if v])
+    # the training half of the metric at the top level, and a compact summary
+    # as the line's last key (a record that keeps only the end of the line
+    # still carries it)
+    c5 = line.get("train", {}).get("config5")
+    if c5:
+        line["train_config"] = "config5 fp32: 12 layers, d 768, batch 8 x seq 1024, AdamW"
+        line["train_tokens_per_s"] = c5["tokens_per_s"]
+        line["train_ms_per_step"] = c5["ms_per_step"]
+        line["train_mfu"] = c5["mfu"]
+    summary = {"gemm_4096_tflops": line["value"], "gemm_frac": line["roofline"]["frac"]}
+    for name in ("config1", "config4", "config5"):
+        t = line.get("train", {}).get(name)
+        if t:
+            summary[name] = {k: t[k] for k in ("tokens_per_s", "samples_per_s", "ms_per_step",
+                                               "graph_ms_per_step", "mfu") if k in t}
+    if "sweep" in line:
+        summary["sweep_tflops"] = {n: line["sweep"][n]["NN"] for n in line["sweep"]}
+    if "attention" in line:
+        summary["attention_fp32_us"] = {k: line["attention"]["fp32"][k]
+                                        for k in ("fwd_us", "bwd_us")}
+    if "row_kernels" in line:
+        summary["row_kernels_frac"] = {k: v["frac"] for k, v in line["row_kernels"].items()}
+    line["summary"] = summary
     print(json.dumps(line), flush=True)
 
 
