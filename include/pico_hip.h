@@ -109,7 +109,9 @@ int pk_gemm_ex_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float 
  * 2 three bf16 products (pk_gemm_ex_bf16x3_f32), 3 fp8 (pk_gemm_ex_fp8_f32).
  * pk_gemm_add_f32: C = alpha * op(A).op(B) + beta * X, X [M,N] with row stride
  *   ldx (X == C with ldx == ldc is pk_gemm_ex_f32's accumulate); a residual
- *   connection x + a.W in one pass.  Same workspace contract as pk_gemm_ex_f32.
+ *   connection x + a.W in one pass.  ldx == 0 adds the one row X [N] to every
+ *   row: a Linear layer's x.W + b (src/nn/linear.c:57-64) in one pass.  Same
+ *   workspace contract as pk_gemm_ex_f32.
  * pk_gemm_swiglu_bwd_f32: dh = alpha * op(A).op(B) [M,N] is the upstream
  *   gradient of h = silu(gate) * up and is never stored; each tile writes
  *   dgate (+)= dh*up*s*(1 + gate*(1-s)) (flags bit 0 accumulates) and
@@ -249,6 +251,11 @@ int pk_reduce_sum_f32(int64_t n, const float* x, float scale, float* out, int fl
  * AdamW: decoupled decay then bias-corrected Adam (no reference code; the
  * reference's optim.h:19-23 only names Adam).  g == NULL means a zero gradient. */
 int pk_sgd_f32(int64_t n, float lr, float* p, const float* g, pk_stream_t stream);
+/* pk_sgd_f32 over `count` tensors (p[i], g[i], n[i] elements) in as few
+ * launches as possible (32 tensors each): the loop over an optimizer's params
+ * of src/optim/SGD.c:29-37 as one launch, same arithmetic per element. */
+int pk_sgd_multi_f32(int count, float* const* p, const float* const* g, const int64_t* n,
+                     float lr, pk_stream_t stream);
 int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps, float weight_decay,
                  int step, float* p, const float* g, float* m, float* v, pk_stream_t stream);
 

@@ -74,6 +74,7 @@ PK_SIGNATURES = {
     "pk_axpy_f32": [c_i64, c_f, c_p, c_p, c_p, c_int, c_p],
     "pk_reduce_sum_f32": [c_i64, c_p, c_f, c_p, c_int, c_p],
     "pk_sgd_f32": [c_i64, c_f, c_p, c_p, c_p],
+    "pk_sgd_multi_f32": [c_int, c_p, c_p, c_p, c_f, c_p],
     "pk_adamw_f32": [c_i64, c_f, c_f, c_f, c_f, c_f, c_int, c_p, c_p, c_p, c_p, c_p],
     "pk_adamw_prep_f32": [c_p, c_f, c_f, c_f, c_p, c_p],
     "pk_adamw_multi_f32": [c_i64, c_p, c_f, c_f, c_f, c_f, c_f, c_p, c_p],

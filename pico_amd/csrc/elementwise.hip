@@ -276,6 +276,27 @@ __global__ void sgd_kernel(int64_t n, float lr, float* __restrict__ p, const flo
     }
 }
 
+// SGD over up to kSgdMax tensors in one launch: blockIdx.y picks the tensor,
+// each element updated as sgd_kernel updates it
+constexpr int kSgdMax = 32;
+struct SgdBatch {
+    float* p[kSgdMax];
+    const float* g[kSgdMax];
+    int64_t n[kSgdMax];
+};
+
+__global__ void sgd_multi_kernel(SgdBatch b, float lr) {
+    const int t = blockIdx.y;
+    float* __restrict__ p = b.p[t];
+    const float* __restrict__ g = b.g[t];
+    const int64_t n = b.n[t];
+    for(int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+        i += (int64_t)gridDim.x * blockDim.x) {
+        const float step = lr * g[i];
+        p[i] = p[i] - step;
+    }
+}
+
 // decoupled decay, then the bias-corrected Adam update of one element
 __device__ __forceinline__ float adamw_elem(float& p, float gi, float& m, float& v, float b1,
                                             float b2, float eps, float decay, float step_size,
@@ -755,6 +776,32 @@ extern "C" int pk_sgd_f32(int64_t n, float lr, float* p, const float* g, pk_stre
     if(!p || !g) return pk::fail("pk_sgd_f32: NULL pointer");
     sgd_kernel<<<pk::grid_for(n, NT), NT, 0, pk::as_stream(stream)>>>(n, lr, p, g);
     return pk::launch_status("pk_sgd_f32");
+}
+
+extern "C" int pk_sgd_multi_f32(int count, float* const* p, const float* const* g,
+                                const int64_t* n, float lr, pk_stream_t stream) {
+    if(count < 0) return pk::fail("pk_sgd_multi_f32: negative count");
+    if(count > 0 && (!p || !g || !n)) return pk::fail("pk_sgd_multi_f32: NULL array");
+    for(int base = 0; base < count; base += kSgdMax) {
+        SgdBatch b = {};
+        int k = 0;
+        int64_t most = 0;
+        for(int i = base; i < count && i < base + kSgdMax; ++i) {
+            if(n[i] < 0) return pk::fail("pk_sgd_multi_f32: tensor %d has a negative size", i);
+            if(n[i] == 0) continue;
+            if(!p[i] || !g[i]) return pk::fail("pk_sgd_multi_f32: tensor %d has a NULL pointer", i);
+            b.p[k] = p[i];
+            b.g[k] = g[i];
+            b.n[k] = n[i];
+            most = n[i] > most ? n[i] : most;
+            ++k;
+        }
+        if(k == 0) continue;
+        sgd_multi_kernel<<<dim3(pk::grid_for(most, NT), k), NT, 0, pk::as_stream(stream)>>>(b, lr);
+        const int rc = pk::launch_status("pk_sgd_multi_f32");
+        if(rc) return rc;
+    }
+    return PK_OK;
 }
 
 extern "C" int pk_adamw_f32(int64_t n, float lr, float beta1, float beta2, float eps,

@@ -61,6 +61,7 @@ namespace {
 constexpr int BK = 32, NT = 256;
 constexpr int KF = BK + 4;  // row stride of a k-contiguous LDS tile [rows][36]
 constexpr int GROUP_M = 8;
+constexpr int64_t kCUs = 256;  // MI355X
 
 // One operand's R x BK slice, staged into a k-contiguous LDS tile [R][KF].
 // Each staging item is 4 consecutive k of one row, held as one float4 and
@@ -1066,6 +1067,177 @@ __global__ __launch_bounds__(NT, T::OCC) void gemm_fp8_kernel(GemmParams p) {
             p, job, acc, reinterpret_cast<float*>(ldsA_buf), ar0, br0, lr, lh);
 }
 
+// ---- small products ---------------------------------------------------------
+// A product whose output is too small to give every CU a tile of the shapes
+// above (512^3: 64 tiles of 64x64 for 256 CUs) runs on 32x32 tiles, one per
+// workgroup of W waves, with K split between the waves: wave w multiplies the
+// tile's 32 rows and 32 columns over its own K range of `kq` (k slices of 32),
+// taking its MFMA operands straight from global memory into registers (no LDS
+// staging, no barrier in the main loop), D slices in flight.  A lane holds 16
+// consecutive k of one row of op(A) and of one column of op(B) per slice --
+// the same fragment assignment as the tiled kernel: lanes 0-31 take k 0..15 of
+// the slice, lanes 32-63 k 16..31 -- loaded as four 128-bit loads when the
+// operand is k-contiguous in memory, else as 16 32-bit loads, each a
+// contiguous 128-byte row run across the lanes.  The W partial tiles then meet
+// in LDS and are added in wave order (ascending K), so the result is
+// deterministic.  Whole tiles only: M, N multiples of 32, K a multiple of
+// 32*W*D, operands 16-byte aligned with leading dimensions multiples of 4.
+struct SmallParams {
+    const float *A, *B, *Cin;
+    float* C;
+    int64_t lda, ldb, ldc, ldcin;
+    int64_t kq;  // K per wave
+    float alpha, beta;
+    int tiles_m, tiles_n;
+};
+
+// One operand's fragment of a slice through a buffer resource over the
+// operand: the per-lane byte offset `voff` stays fixed, the slice moves the
+// uniform `soff`.  k-contiguous (element (r, k) at base[r*ld + k]): 16
+// consecutive floats, four 128-bit loads; row-contiguous (element (r, k) at
+// base[k*ld + r]): one float per k row, `step` = ld*4 bytes apart.
+template <bool KFAST>
+__device__ __forceinline__ void small_frag(__amdgpu_buffer_rsrc_t rs, int voff, int soff, int step,
+                                           float (&f)[16]) {
+    if(KFAST) {
+#pragma unroll
+        for(int i = 0; i < 4; ++i) {
+            const f32x4 x =
+                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0));
+            f[4 * i + 0] = x[0];
+            f[4 * i + 1] = x[1];
+            f[4 * i + 2] = x[2];
+            f[4 * i + 3] = x[3];
+        }
+    } else {
+#pragma unroll
+        for(int i = 0; i < 16; ++i)
+            f[i] = __builtin_bit_cast(float,
+                                      __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + i * step, 0));
+    }
+}
+
+template <bool TA, bool TB, int W, int D>
+__global__ __launch_bounds__(64 * W) void gemm_small_kernel(SmallParams p) {
+    __shared__ __attribute__((aligned(16))) float part[W][32 * 32];
+    // XCD-contiguous runs of tiles (the dispatcher deals workgroups to the 8
+    // XCDs in turn), walked down GROUP_M tile-rows at a time
+    const int ntiles = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+    const int group_span = GROUP_M * p.tiles_n;
+    const int first_m = (bid / group_span) * GROUP_M;
+    const int gm = min(p.tiles_m - first_m, GROUP_M);
+    const int local = bid % group_span;
+    const int row0 = (first_m + local % gm) * 32, col0 = (local / gm) * 32;
+
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lr = l & 31, lh = l >> 5;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    const int kw = w * (int)p.kq;   // this wave's first k
+    const int ns = (int)(p.kq / BK);  // a multiple of D
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.A), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.B), (short)0, 0x7fffffff, 0x00020000);
+    // op(A) is k-contiguous unless TA, op(B) unless !TB
+    const int va = !TA ? (lr * lda + 16 * lh) * 4 : (16 * lh * lda + lr) * 4;
+    const int vb = TB ? (lr * ldb + 16 * lh) * 4 : (16 * lh * ldb + lr) * 4;
+    auto fetch = [&](int s, float (&fa)[16], float (&fb)[16]) {
+        const int k = kw + s * BK;
+        small_frag<!TA>(ra, va, !TA ? (row0 * lda + k) * 4 : (k * lda + row0) * 4, lda * 4, fa);
+        small_frag<TB>(rb, vb, TB ? (col0 * ldb + k) * 4 : (k * ldb + col0) * 4, ldb * 4, fb);
+    };
+    float a[D][16], b[D][16];
+#pragma unroll
+    for(int d = 0; d < D; ++d) {
+        fetch(d, a[d], b[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    f32x16 acc;
+#pragma unroll
+    for(int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    auto mul = [&](const float (&fa)[16], const float (&fb)[16]) {
+#pragma unroll
+        for(int i = 0; i < 16; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[i], acc, 0, 0, 0);
+    };
+    // every slice's buffer is refilled right after its products, D slices
+    // ahead, with no condition inside the loop, and the scheduling barriers
+    // keep the slices' loads in slice order: the wait-count analysis then
+    // knows at the loop head and after it which loads a slice's products
+    // wait for (with a conditional refill, or loads of different slices
+    // interleaved, it lost that, and every slice waited for all loads in
+    // flight); the last D slices refill nothing
+    __builtin_amdgcn_sched_barrier(0);
+    int s0 = 0;
+    for(; s0 + D < ns; s0 += D) {
+#pragma unroll
+        for(int d = 0; d < D; ++d) {
+            mul(a[d], b[d]);
+            fetch(s0 + d + D, a[d], b[d]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for(int d = 0; d < D; ++d) mul(a[d], b[d]);
+    // partial tile of wave w: C[row][col] with col = lane%32 and row =
+    // 8(r/4) + 4(lane/32) + r%4 for accumulator register r
+#pragma unroll
+    for(int r = 0; r < 16; ++r) part[w][(8 * (r >> 2) + 4 * lh + (r & 3)) * 32 + lr] = acc[r];
+    __syncthreads();
+    constexpr int PER = 32 * 32 / (64 * W);  // outputs per thread: 4 (W 4) or 2 (W 8)
+    const int e0 = threadIdx.x * PER, row = e0 / 32, col = e0 % 32;
+    float v[PER];
+#pragma unroll
+    for(int e = 0; e < PER; ++e) v[e] = part[0][e0 + e];
+#pragma unroll
+    for(int q = 1; q < W; ++q)
+#pragma unroll
+        for(int e = 0; e < PER; ++e) v[e] += part[q][e0 + e];
+    typedef float vec_t __attribute__((ext_vector_type(PER)));
+    vec_t* c = reinterpret_cast<vec_t*>(p.C + (row0 + row) * p.ldc + col0 + col);
+    vec_t x;
+#pragma unroll
+    for(int e = 0; e < PER; ++e) x[e] = p.alpha * v[e];
+    if(p.beta != 0.0f) {
+        const vec_t y = *reinterpret_cast<const vec_t*>(p.Cin + (row0 + row) * p.ldcin + col0 + col);
+#pragma unroll
+        for(int e = 0; e < PER; ++e) x[e] += p.beta * y[e];
+    }
+    *c = x;
+}
+
+// W = 0 when the small-product kernel does not apply
+struct SmallChoice {
+    int W, D;
+};
+
+// Only for one round of tiles (at most one per CU): with more, the 64x64
+// tiles' LDS staging, which reads each operand once per 64 rows instead of
+// once per 32, wins (measured 768^3: 576 small tiles 48-62 TFLOP/s against
+// 59-64 tiled; 1024^3: 69-82 against 107-117).  Eight waves split K when it
+// divides (512^3: 51-53 TFLOP/s against 40-47 with four, 24-25 tiled); D =
+// the most slices in flight (4, 2 or 1) that divides a wave's slice count.
+SmallChoice small_choice(int64_t M, int64_t N, int64_t K) {
+    if(M % 32 || N % 32 || K <= 0 || (M / 32) * (N / 32) > kCUs) return {0, 0};
+    const int W = K % (BK * 8) == 0 ? 8 : K % (BK * 4) == 0 ? 4 : 0;
+    if(!W) return {0, 0};
+    const int64_t ns = K / (BK * W);  // odd when W is 4
+    return {W, ns % 4 == 0 ? 4 : ns % 2 == 0 ? 2 : 1};
+}
+
+template <bool TA, bool TB>
+void launch_small(const SmallParams& sp, SmallChoice sc, hipStream_t st) {
+    const unsigned grid = (unsigned)(sp.tiles_m * sp.tiles_n);
+    if(sc.W == 8) {
+        if(sc.D == 4) gemm_small_kernel<TA, TB, 8, 4><<<grid, 512, 0, st>>>(sp);
+        else if(sc.D == 2) gemm_small_kernel<TA, TB, 8, 2><<<grid, 512, 0, st>>>(sp);
+        else gemm_small_kernel<TA, TB, 8, 1><<<grid, 512, 0, st>>>(sp);
+    } else {  // four waves: K/128 is odd, one slice in flight
+        gemm_small_kernel<TA, TB, 4, 1><<<grid, 256, 0, st>>>(sp);
+    }
+}
+
 // C = alpha * sum_s ws[s] + beta * Cin, planes summed in order s = 0, 1, ...
 __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restrict__ ws,
                               float alpha, float beta, const float* Cin, int64_t ldcin, float* C,
@@ -1106,7 +1278,6 @@ __global__ void splitk_reduce(int64_t M, int64_t N, int S, const float* __restri
 // projection of a d_model-768 transformer) -> 256 of 256x96; 2048^2 -> 256
 // of 128x128; 1024^2 -> 256 of 64x64 rather than 64 of 128x128.
 enum TileKind { kTile128, kTile96, kTile256, kTile64, kTile256x96 };
-constexpr int64_t kCUs = 256;
 
 struct TileChoice {
     TileKind kind;
@@ -1442,6 +1613,35 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     const int edge = vec && whole && small ? kEdgeNone
                      : vec && (M % 4) == 0 && (N % 4) == 0 && (K % 4) == 0 ? kEdgeVec
                                                                            : kEdgeScalar;
+    // an output of fewer tiles than CUs, unsplit: the small-product kernel
+    // when its whole-tile conditions hold
+    if(prec == kFp32 && batch == 1 && causal == 0 && !swiglu && !sfwd && gp.splits == 1 && vec &&
+       small && tiles_m * tiles_n < kCUs) {
+        const SmallChoice sc = small_choice(M, N, K);
+        const bool cvec = pk::aligned16(C) && ldc % 4 == 0 &&
+                          (gp.Cin == nullptr || (pk::aligned16(gp.Cin) && gp.ldcin % 4 == 0));
+        if(sc.W && cvec) {
+            SmallParams sp;
+            sp.A = A;
+            sp.B = B;
+            sp.C = C;
+            sp.Cin = gp.Cin ? gp.Cin : C;
+            sp.lda = lda;
+            sp.ldb = ldb;
+            sp.ldc = ldc;
+            sp.ldcin = gp.Cin ? gp.ldcin : ldc;
+            sp.kq = K / sc.W;
+            sp.alpha = alpha;
+            sp.beta = beta;
+            sp.tiles_m = (int)(M / 32);
+            sp.tiles_n = (int)(N / 32);
+            if(!TA && !TB) launch_small<false, false>(sp, sc, st);
+            else if(!TA && TB) launch_small<false, true>(sp, sc, st);
+            else if(TA && !TB) launch_small<true, false>(sp, sc, st);
+            else launch_small<true, true>(sp, sc, st);
+            return pk::launch_status("pk_gemm_f32 (small product)");
+        }
+    }
     const TileKind kind = tc.kind;
     int rc;
     if(!TA && !TB)
@@ -1631,8 +1831,10 @@ extern "C" int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K
     e.fp8_scale = fp8_scales;
     if(beta != 0.0f && M > 0 && N > 0) {
         if(!X) return pk::fail("pk_gemm_add_f32: X is NULL");
-        if(ldx < N) return pk::fail("pk_gemm_add_f32: ldx=%lld < N=%lld", (long long)ldx,
-                                    (long long)N);
+        // ldx 0: one row of X for every row of C (a bias)
+        if(ldx != 0 && ldx < N)
+            return pk::fail("pk_gemm_add_f32: ldx=%lld < N=%lld (and not 0)", (long long)ldx,
+                            (long long)N);
         e.Cin = X;
         e.ldcin = ldx;
     }

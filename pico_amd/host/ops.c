@@ -477,6 +477,90 @@ struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
     return out;
 }
 
+/* ------------------------------------------------- Linear in one product
+ * pico's Linear forward is pico_matmul then pico_add of the bias row
+ * (src/nn/linear.c:57-64): two nodes, two passes.  Here one node x.W + b: the
+ * product's epilogue adds the bias row (pk_gemm_add_f32 with ldx = 0), which
+ * rounds exactly as the separate add does (the product is the same fp32
+ * accumulator, then one rounding of its sum with b).  Its backward gives the
+ * same gradients as the two nodes': db is the broadcast add's column sums in
+ * pico's order (src/autograd.h:53-65), dx and dW the matmul's products. */
+
+/* db (+)= the column sums of g [M, N]; on the side stream with the weight
+ * gradient when the layer's input is not a parameter (a bias is read only
+ * once the backward is over) */
+static int bias_backward(struct PicoTensor* self, struct PicoTensor* bias, const float* g,
+                         int input_param) {
+    int64_t sb[2], sg[2] = {self->strides[0], self->strides[1]};
+    mapped_strides(bias, 2, sb);
+    struct PkNode* nb = pkh_node(bias);
+    pk_stream_t side = nb && bias->is_persistent && !input_param ? pkh_side_fork() : NULL;
+    const int flag = side ? (nb->grad_live ? PK_ACCUM : 0) : pkh_grad_flag(bias);
+    int st = pk_binary_bwd_f32(OP_ADD, 1, 2, self->shape, sb, sg, bias->numel, g, g, bias->grad,
+                               flag, side ? side : pkh_stream());
+    if(side) nb->side_seq = pkh_side_seq();
+    if(pkh_status("pico_add_backward", st)) return st;
+    pkh_grad_mark(bias);
+    return 0;
+}
+
+static void linear_backward(struct PicoTensor* self) {
+    if(pkh_init()) return;
+    struct PicoTensor *a = self->parents[0], *b = self->parents[1], *bias = self->parents[2];
+    const float* g = pkh_upstream(self);
+    if(!g) return;
+    const int a_param = a->is_persistent || a == b;
+    if(bias_backward(self, bias, g, a_param)) return;
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return;
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    struct DaPlain ctx = {a, b, g, M, K, N};
+    matmul_backward_with(va, a_param, b, g, M, K, N, da_plain, &ctx);
+}
+
+/* x . W + bias with the checks of pico_matmul then pico_add (bias [N] or
+ * [1, N]); NULL (with the reference's message) where either would refuse */
+struct PicoTensor* pkh_linear(struct PicoTensor* a, struct PicoTensor* b, struct PicoTensor* bias) {
+    if(!a || !b || !bias) {
+        PKH_ERR("pico_matmul: NULL tensor!\n");
+        return NULL;
+    }
+    if(a->shape[a->ndim - 1] != b->shape[0]) {
+        PKH_ERR("2 matmuls matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->ndim != 2 || b->ndim != 2) {
+        PKH_ERR("2d matmul matrices must be compatible\n");
+        return NULL;
+    }
+    if(a->backend != b->backend || a->backend != bias->backend) {
+        PKH_ERR("PicoTensor backends are not compatible!\n");
+        return NULL;
+    }
+    int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    const int row = (bias->ndim == 1 && bias->shape[0] == N) ||
+                    (bias->ndim == 2 && bias->shape[0] == 1 && bias->shape[1] == N);
+    if(!row || bias->strides[bias->ndim - 1] != 1) {
+        /* another broadcast: the two ops */
+        struct PicoTensor* prod = pico_matmul(a, b);
+        return prod ? pico_add(prod, bias) : NULL;
+    }
+    struct Arena* arena = pkh_need_arena();
+    if(!arena) return NULL;
+    if(refuse_cpu("pico_matmul", a)) return NULL;
+    struct PkMat va, vb;
+    if(matmul_views(a, b, &va, &vb)) return NULL;
+    int64_t shape[2] = {M, N};
+    struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
+    if(!out) return NULL;
+    int st = gemm_add_on(va, vb, M, N, K, out->data, 'N', N > 0 ? N : 1, 1.0f, bias->data, 0,
+                         pkh_stream(), 0);
+    if(pkh_status("pico_matmul", st)) return NULL;
+    struct PicoTensor* ps[3] = {a, b, bias};
+    pkh_set_parents(arena, out, 3, ps, linear_backward);
+    return out;
+}
+
 /* The gate/up projection of a SwiGLU block (no reference counterpart): out =
  * a . w for w = [W1 | W3] (two column halves), a matmul to autograd.  Its
  * product also writes h = silu(out[:, :F]) * out[:, F:] from the tiles

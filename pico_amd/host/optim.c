@@ -58,14 +58,27 @@ void pico_optim_sgd_add(struct PicoOptimSGD* o, struct PicoTensor* p) {
     pl_push(&o->params, p);
 }
 
-/* p -= lr * g (src/optim/SGD.c:29-37); a grad holding nothing is zero, and
- * p - lr*0 == p, so such params are skipped */
+/* p -= lr * g (src/optim/SGD.c:29-37) for every param in one launch; a grad
+ * holding nothing is zero, and p - lr*0 == p, so such params are skipped */
 void pico_optim_sgd_step(struct PicoOptimSGD* o) {
-    for(int i = 0; i < o->params.n; i++) {
-        struct PicoTensor* p = o->params.v[i];
-        if(!pkh_grad_is_live(p)) continue;
-        pkh_status("pico_optim_sgd_step", pk_sgd_f32(p->numel, o->lr, p->data, p->grad,
-                                                     pkh_stream()));
+    enum { BATCH = 32 };
+    float* ps[BATCH];
+    const float* gs[BATCH];
+    int64_t ns[BATCH];
+    int k = 0;
+    for(int i = 0; i <= o->params.n; i++) {
+        if(i < o->params.n) {
+            struct PicoTensor* p = o->params.v[i];
+            if(!pkh_grad_is_live(p)) continue;
+            ps[k] = p->data;
+            gs[k] = p->grad;
+            ns[k] = p->numel;
+            k++;
+        }
+        if(k == BATCH || (i == o->params.n && k > 0)) {
+            pkh_status("pico_optim_sgd_step", pk_sgd_multi_f32(k, ps, gs, ns, o->lr, pkh_stream()));
+            k = 0;
+        }
     }
 }
 
@@ -285,7 +298,8 @@ struct PicoLinear* pico_nn_linear_init(int in_features, int out_features, bool b
     return l;
 }
 
-/* src/nn/linear.c:40-67: x . W, then + b broadcast over rows */
+/* src/nn/linear.c:40-67: x . W, then + b broadcast over rows, as one node
+ * whose product adds the bias in its epilogue (pkh_linear) */
 struct PicoTensor* pico_nn_linear_forward(struct PicoLinear* layer, struct PicoTensor* input) {
     if(!layer || !input) {
         PKH_ERR("In Linear - NULL layer or input!\n");
@@ -303,9 +317,8 @@ struct PicoTensor* pico_nn_linear_forward(struct PicoLinear* layer, struct PicoT
         PKH_ERR("In Linear - No current arena in context!\n");
         return NULL;
     }
-    struct PicoTensor* out = pico_matmul(input, layer->weights);
-    if(out && layer->bias) out = pico_add(out, layer->bias);
-    return out;
+    if(layer->bias) return pkh_linear(input, layer->weights, layer->bias);
+    return pico_matmul(input, layer->weights);
 }
 
 void pico_nn_linear_free(struct PicoLinear* l) {

@@ -97,6 +97,9 @@ int pkh_copy_d2h(void* dst, const void* src, size_t bytes);
 /* device-to-device on the library's stream, not waited for */
 int pkh_copy_d2d_async(void* dst, const void* src, size_t bytes);
 
+/* x . W + bias as one node (ops.c): pico's Linear forward in one product */
+struct PicoTensor* pkh_linear(struct PicoTensor* x, struct PicoTensor* w, struct PicoTensor* bias);
+
 /* tensors (tensor.c) */
 /* a GPU tensor node in `arena` with uninitialised device data and a
  * not-yet-live grad; `node_bytes` >= sizeof(struct PkNode) */

@@ -18,7 +18,7 @@ import torch
 from oracle import oracle as O
 from pico_amd import _lib
 from pico_amd import kernels as kern
-from pico_amd.pico import Pico
+from pico_amd.pico import TP, Pico
 from tests._util import max_rel
 
 pytestmark = pytest.mark.gpu
@@ -63,7 +63,10 @@ def test_gemm_add_equals_product_then_add(dev, M, N, K, prec):
         assert max_rel(got.cpu().numpy(), want) <= 1e-5
 
 
-@pytest.mark.parametrize("M,F,N", [(256, 512, 128), (300, 200, 136), (8192, 2048, 768)])
+# (an output of at most 256 tiles of 32 x 32, e.g. 256 x 512 with K 128, takes
+# the small-product kernel as a plain product, whose K split rounds differently
+# from the tiled kernels the fused epilogues run on: 264 rows keep it tiled)
+@pytest.mark.parametrize("M,F,N", [(264, 512, 128), (300, 200, 136), (8192, 2048, 768)])
 @pytest.mark.parametrize("flags", [0, 1, 2, 3])
 def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
     L = _lib.hip_lib()
@@ -286,3 +289,69 @@ def test_fused_ops_refuse_bad_shapes(P):
         g = P.tensor([4, 3], np.ones(12))
         assert not P.lib.pico_swiglu_matmul_add(g, g, b, None)  # gate == up
         assert not P.lib.pico_swiglu_matmul_add(g, a, P.tensor([4, 5], np.ones(20)), None)
+
+
+# ------------------------------------------------------------------ Linear
+def _linear_layer(P, K, N, wv, bv):
+    layer = P.lib.pico_nn_linear_init(K, N, True)
+    w = ctypes.cast(layer + 8, ctypes.POINTER(TP)).contents
+    b = ctypes.cast(layer + 16, ctypes.POINTER(TP)).contents
+    P.set(w, wv)
+    P.set(b, bv)
+    return layer, w, b
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 784, 128), (64, 128, 10), (512, 512, 512), (300, 96, 200),
+                                   (4096, 512, 1376)])
+@pytest.mark.parametrize("x_param", [False, True])
+def test_linear_equals_matmul_then_add(P, M, K, N, x_param):
+    """pico_nn_linear_forward is one node, x.W + b with the bias row added in
+    the product's epilogue (pk_gemm_add_f32, ldx 0).  It equals pico_matmul
+    then pico_add (src/nn/linear.c:57-64) bit for bit: the output and the
+    gradients of x, W and b, with x an activation (the weight and bias
+    gradients then run on the side stream) or a parameter.  The shapes take the
+    split-K product (64 x 784 . 784 x 128), the scalar edge path (N 10), the
+    small-product kernel (512^3) and the tiled kernel."""
+    xv = O.normal(M * K, 51).reshape(M, K)
+    wv = O.normal(K * N, 52, 0.0, 0.1).reshape(K, N)
+    bv = O.normal(N, 53)
+    sg = O.normal(M * N, 54).reshape(M, N)
+    runs = []
+    for fused in (True, False):
+        with P.arena(1 << 26):
+            layer, w, b = _linear_layer(P, K, N, wv, bv)
+            x = P.param([M, K], xv) if x_param else P.tensor([M, K], xv)
+            out = (P.lib.pico_nn_linear_forward(layer, x) if fused
+                   else P.add(P.matmul(x, w), b))
+            assert out
+            P.backward(P.mul(out, P.tensor([M, N], sg)))
+            runs.append([P.data(out), P.grad(x), P.grad(w), P.grad(b)])
+            if x_param:
+                P.free(x)
+            P.lib.pico_nn_linear_free(layer)
+    for i, (f, c) in enumerate(zip(*runs)):
+        assert np.array_equal(f, c), i
+    want = O.gemm_ref_f64("N", "N", xv, wv) + bv
+    assert max_rel(runs[0][0], want.ravel()) <= 1e-5
+    assert max_rel(runs[0][3], sg.astype(np.float64).sum(0)) <= 1e-5
+
+
+def test_linear_bias_row_epilogue_launcher(dev):
+    """pk_gemm_add_f32 with ldx 0 adds one row to every row of C, for the
+    tiled, small-product and split-K paths: integer operands, bit for bit"""
+    L = _lib.hip_lib()
+    rng = np.random.default_rng(7)
+    for M, N, K in ((256, 256, 256), (1024, 768, 256), (64, 128, 4096), (100, 36, 20)):
+        A = rng.integers(-8, 9, (M, K)).astype(np.float32)
+        B = rng.integers(-8, 9, (K, N)).astype(np.float32)
+        x = rng.integers(-100, 100, N).astype(np.float32)
+        need = L.pk_gemm_workspace_f32(M, N, K)
+        ws = torch.empty(max(need, 4) // 4, device=dev)
+        C = torch.full((M, N), float("nan"), device=dev)
+        dA, dB, dx = _t(A, dev), _t(B, dev), _t(x, dev)
+        _lib.check("pk_gemm_add_f32", L.pk_gemm_add_f32(
+            b"N", b"N", M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(), N, 1.0, dx.data_ptr(), 0,
+            C.data_ptr(), N, 0, None, ws.data_ptr(), need, None))
+        ref = (A.astype(np.float64) @ B.astype(np.float64) + x).astype(np.float32)
+        torch.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy(), ref), (M, N, K)

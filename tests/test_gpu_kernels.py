@@ -73,6 +73,39 @@ def test_gemm_integer_bitexact(dev, ta, tb, M, N, Kd):
     assert np.array_equal(host(C), ref)
 
 
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(512, 512, 512), (256, 256, 256), (512, 256, 1536),
+                                    (256, 512, 384), (96, 64, 128), (32, 480, 2048)])
+def test_gemm_small_products(dev, ta, tb, M, N, Kd):
+    """Outputs of at most 256 tiles of 32 x 32 (and fewer 64 x 64 tiles than
+    CUs) run one tile per workgroup with K split over its waves: eight when
+    K/256 is whole (2, 1, 6 and 8 slices of 32 per wave here, 2, 1, 2 and 4 in
+    flight), else four (3 and 1 slices, 1 in flight).  Integer operands bit for
+    bit, the beta accumulate exact, a separate X (pk_gemm_add_f32), and uniform
+    operands within the fp64 bound"""
+    from pico_amd import _lib
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 13 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    C = cu(ref.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)  # C - A.B = 0 exactly
+    assert not np.any(host(C))
+    if (ta, tb) == ("N", "N"):  # a separate X is built for A.B only
+        X = O.uniform(M * N, 17).reshape(M, N)
+        C = torch.full((M, N), float("nan"), device=dev)
+        dA, dB, dX = cu(As), cu(Bs), cu(X)
+        _lib.check("pk_gemm_add_f32", _lib.hip_lib().pk_gemm_add_f32(
+            b"N", b"N", M, N, Kd, 0.5, dA.data_ptr(), Kd, dB.data_ptr(), N, 2.0, dX.data_ptr(), N,
+            C.data_ptr(), N, 0, None, None, 0, None))
+        assert np.array_equal(host(C), (0.5 * ref).astype(np.float32) + 2.0 * X)
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N + 3 * Kd)
+    C = torch.empty(M, N, device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    assert gemm_err(host(C), A, B) <= TOL
+
+
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N")])
 @pytest.mark.parametrize("n", [512, 1024, 2048])
 def test_gemm_uniform_vs_fp64(dev, ta, tb, n):
@@ -760,3 +793,26 @@ def test_gemm_vector_edge_tiles(dev, ta, tb, M, N, Kd):
     C = cu(ref.copy())
     K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)
     assert not np.any(host(C))
+
+
+def test_sgd_multi_equals_per_tensor(dev):
+    """pk_sgd_multi_f32 over 40 tensors (two launches of up to 32; sizes 0 to
+    100000, odd ones included) equals pk_sgd_f32 on each, bit for bit"""
+    from pico_amd import _lib
+    import ctypes
+    L = _lib.hip_lib()
+    sizes = [0, 1, 3, 10, 128, 1000, 100352, 4097] * 5
+    ps = [cu(O.normal(n, 60 + i)) if n else torch.empty(1, device=dev) for i, n in enumerate(sizes)]
+    gs = [cu(O.normal(n, 160 + i)) if n else torch.empty(1, device=dev) for i, n in enumerate(sizes)]
+    ref = [p.clone() for p in ps]
+    st = torch.cuda.current_stream().cuda_stream
+    for p, g, n in zip(ref, gs, sizes):
+        _lib.check("pk_sgd_f32", L.pk_sgd_f32(n, 0.01, p.data_ptr(), g.data_ptr(), st))
+    k = len(sizes)
+    parr = (ctypes.c_void_p * k)(*[p.data_ptr() for p in ps])
+    garr = (ctypes.c_void_p * k)(*[g.data_ptr() for g in gs])
+    narr = (ctypes.c_int64 * k)(*sizes)
+    _lib.check("pk_sgd_multi_f32", L.pk_sgd_multi_f32(k, parr, garr, narr, 0.01, st))
+    torch.cuda.synchronize()
+    for p, r in zip(ps, ref):
+        assert torch.equal(p, r)
