@@ -127,6 +127,14 @@ int pk_gemm_ex_fp8_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float 
  *   up columns, so F must be a multiple of 32 (4 for whole-column tiles of
  *   64); refused otherwise.  The gate/up projection of a SwiGLU block and
  *   its activation in one pass. */
+/* 1 when the fp32 products above (pk_gemm_f32, pk_gemm_ex_f32, pk_gemm_add_f32)
+ * run an [M, N] output with inner size K (contiguous operands) on the
+ * small-product kernels: an output that the tiled kernels leave short of one
+ * tile per CU and one round of 32x32 tiles covers, K <= 1024.  Those split K
+ * over a workgroup's waves, so their sums round differently from the tiled
+ * kernels that the SwiGLU epilogues below run on; pico's fused SwiGLU ops use
+ * their composition for such shapes, so fused and composed stay bit-equal. */
+int pk_gemm_small_product_f32(int64_t M, int64_t N, int64_t K);
 int pk_gemm_add_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                     const float* X, int64_t ldx, float* C, int64_t ldc, int precision,

@@ -44,6 +44,7 @@ PK_SIGNATURES = {
                         c_p, c_i64, c_p],
     "pk_gemm_ex_fp8_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,
                            c_f, c_p, c_i64, c_p, c_size, c_p],
+    "pk_gemm_small_product_f32": [c_i64, c_i64, c_i64],
     "pk_gemm_add_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64, c_f,
                         c_p, c_i64, c_p, c_i64, c_int, c_p, c_p, c_size, c_p],
     "pk_gemm_swiglu_bwd_f32": [c_char, c_char, c_i64, c_i64, c_i64, c_f, c_p, c_i64, c_p, c_i64,

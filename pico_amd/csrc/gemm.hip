@@ -1207,19 +1207,127 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(SmallParams p) {
     *c = x;
 }
 
+// The same product for any M, N, K (partial tiles, K not a multiple of the
+// slice, unaligned operands): every operand element is one 32-bit load of an
+// in-range address, selected to zero outside [0, rows) x [0, K), and wave w
+// takes slices w, w + W, w + 2W, ... (one in flight), so every wave has
+// ceil or floor of ns/W slices; stores are predicated.  For tiny products (a
+// training step of a small MLP: [64, 784] . [784, 128] and smaller), where a
+// launch is a few workgroups' latency chain.
+template <bool KFAST, bool VEC>
+__device__ __forceinline__ void small_frag_edge(__amdgpu_buffer_rsrc_t rs, int ld, int r, int rlim,
+                                                int k, int K, float (&f)[16]) {
+    const int rr = r < rlim ? r : rlim - 1;  // a valid row; its products are never stored
+    if constexpr(KFAST && VEC) {
+        // 16-byte aligned rows and K a multiple of 4: four 128-bit loads, each
+        // float4 wholly inside or outside [0, K)
+#pragma unroll
+        for(int i = 0; i < 4; ++i) {
+            const bool in = k + 4 * i < K;
+            const int off = (rr * ld + (in ? k + 4 * i : 0)) * 4;
+            const f32x4 x =
+                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+#pragma unroll
+            for(int e = 0; e < 4; ++e) f[4 * i + e] = in ? x[e] : 0.0f;
+        }
+        return;
+    }
+#pragma unroll
+    for(int i = 0; i < 16; ++i) {
+        const bool in = k + i < K;
+        const int kk = in ? k + i : 0;
+        const int off = KFAST ? (rr * ld + kk) * 4 : (kk * ld + rr) * 4;
+        const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+        f[i] = in ? x : 0.0f;
+    }
+}
+
+struct SmallEdgeParams {
+    const float *A, *B, *Cin;
+    float* C;
+    int M, N, K, lda, ldb;
+    int64_t ldc, ldcin;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+};
+
+template <bool TA, bool TB, int W, bool VEC>
+__global__ __launch_bounds__(64 * W) void gemm_small_edge_kernel(SmallEdgeParams p) {
+    __shared__ __attribute__((aligned(16))) float part[W][32 * 32];
+    const int tm = blockIdx.x % p.tiles_m, tn = blockIdx.x / p.tiles_m;
+    const int row0 = tm * 32, col0 = tn * 32;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lr = l & 31, lh = l >> 5;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.A), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.B), (short)0, 0x7fffffff, 0x00020000);
+    const int ns = (p.K + BK - 1) / BK;
+    f32x16 acc;
+#pragma unroll
+    for(int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for(int s = w; s < ns; s += W) {
+        float a[16], b[16];
+        const int k = s * BK + 16 * lh;
+        small_frag_edge<!TA, VEC>(ra, p.lda, row0 + lr, p.M, k, p.K, a);
+        small_frag_edge<TB, VEC>(rb, p.ldb, col0 + lr, p.N, k, p.K, b);
+#pragma unroll
+        for(int i = 0; i < 16; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for(int r = 0; r < 16; ++r) part[w][(8 * (r >> 2) + 4 * lh + (r & 3)) * 32 + lr] = acc[r];
+    __syncthreads();
+    for(int e = threadIdx.x; e < 32 * 32; e += 64 * W) {
+        const int row = row0 + e / 32, col = col0 + e % 32;
+        if(row >= p.M || col >= p.N) continue;
+        float v = part[0][e];
+#pragma unroll
+        for(int q = 1; q < W; ++q) v += part[q][e];
+        float x = p.alpha * v;
+        if(p.beta != 0.0f) x += p.beta * p.Cin[row * p.ldcin + col];
+        p.C[row * p.ldc + col] = x;
+    }
+}
+
 // W = 0 when the small-product kernel does not apply
 struct SmallChoice {
     int W, D;
 };
 
-// Only for one round of tiles (at most one per CU): with more, the 64x64
-// tiles' LDS staging, which reads each operand once per 64 rows instead of
-// once per 32, wins (measured 768^3: 576 small tiles 48-62 TFLOP/s against
-// 59-64 tiled; 1024^3: 69-82 against 107-117).  Eight waves split K when it
-// divides (512^3: 51-53 TFLOP/s against 40-47 with four, 24-25 tiled); D =
-// the most slices in flight (4, 2 or 1) that divides a wave's slice count.
+// Whether a product goes to the small-product kernels: the tiled kernels'
+// choice leaves CUs without a tile, at most one round of 32x32 tiles covers
+// the output, and each operand spans under 2^31 bytes (32-bit offsets).
+bool small_product(int64_t M, int64_t N, int64_t K, bool TA, bool TB, int64_t lda, int64_t ldb);
+
+template <bool TA, bool TB, bool VEC>
+void launch_small_edge_v(const SmallEdgeParams& ep, hipStream_t st) {
+    const unsigned grid = (unsigned)(ep.tiles_m * ep.tiles_n);
+    // sixteen waves when there are twelve or more slices of 32 k (one or two
+    // slices each), else four
+    if((ep.K + BK - 1) / BK >= 12)
+        gemm_small_edge_kernel<TA, TB, 16, VEC><<<grid, 1024, 0, st>>>(ep);
+    else
+        gemm_small_edge_kernel<TA, TB, 4, VEC><<<grid, 256, 0, st>>>(ep);
+}
+
+// vec: a k-contiguous operand is 16-byte aligned with a row stride and K that
+// are multiples of 4, so it loads 128 bits at a time
+template <bool TA, bool TB>
+void launch_small_edge(const SmallEdgeParams& ep, bool vec, hipStream_t st) {
+    if(vec) launch_small_edge_v<TA, TB, true>(ep, st);
+    else launch_small_edge_v<TA, TB, false>(ep, st);
+}
+
+// The whole-tile kernel's shape (W = 0: the edge kernel instead).  Small
+// products are limited to one round of tiles (at most one per CU): with more,
+// the 64x64 tiles' LDS staging, which reads each operand once per 64 rows
+// instead of once per 32, wins (measured 768^3: 576 small tiles 48-62 TFLOP/s
+// against 59-64 tiled; 1024^3: 69-82 against 107-117).  Eight waves split K
+// when it divides (512^3: 51-53 TFLOP/s against 40-47 with four, 24-25
+// tiled); D = the most slices in flight (4, 2 or 1) that divides a wave's
+// slice count.
 SmallChoice small_choice(int64_t M, int64_t N, int64_t K) {
-    if(M % 32 || N % 32 || K <= 0 || (M / 32) * (N / 32) > kCUs) return {0, 0};
+    if(M % 32 || N % 32 || K <= 0) return {0, 0};
     const int W = K % (BK * 8) == 0 ? 8 : K % (BK * 4) == 0 ? 4 : 0;
     if(!W) return {0, 0};
     const int64_t ns = K / (BK * W);  // odd when W is 4
@@ -1312,6 +1420,17 @@ TileChoice pick_tile(int64_t M, int64_t N, int64_t batch, bool allow_all, int64_
         if(fits(256) && cost(256, 256, 4.0) / 1.05 <= c) best = {kTile256, 256, 256};
     }
     return best;
+}
+
+bool small_product(int64_t M, int64_t N, int64_t K, bool TA, bool TB, int64_t lda, int64_t ldb) {
+    if(((M + 31) / 32) * ((N + 31) / 32) > kCUs) return false;
+    const TileChoice t = pick_tile(M, N, 1, true);
+    if(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) >= kCUs) return false;
+    auto extent = [K](bool kfast, int64_t rows, int64_t ld) {
+        return 4 * (kfast ? (rows - 1) * ld + K : (K - 1) * ld + rows);
+    };
+    return lda < INT32_MAX && ldb < INT32_MAX && extent(!TA, M, lda) < INT32_MAX &&
+           extent(TB, N, ldb) < INT32_MAX;
 }
 
 // K split for a product whose output has too few tiles to fill the chip: 2
@@ -1545,6 +1664,64 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
         gp.sf_ldh = epi.sf_ldh;
     }
     hipStream_t st = pk::as_stream(stream);
+    // an output that the tiled kernels leave short of one tile per CU, with
+    // K <= 1024: the small-product kernels, before any K split is considered
+    // (a split of such a product is a few workgroups' latency chain plus a
+    // reduction pass; longer K, such as a weight gradient over a batch of
+    // tokens, keeps the tiled kernels and their split)
+    if(prec == kFp32 && batch == 1 && causal == 0 && !swiglu && !sfwd && K > 0 && K <= 1024 &&
+       small_product(M, N, K, TA, TB, lda, ldb)) {
+        const bool vec = pk::aligned16(A) && pk::aligned16(B) && lda % 4 == 0 && ldb % 4 == 0 &&
+                         pk::aligned16(C) && ldc % 4 == 0 &&
+                         (gp.Cin == nullptr || (pk::aligned16(gp.Cin) && gp.ldcin % 4 == 0));
+        const SmallChoice sc = vec ? small_choice(M, N, K) : SmallChoice{0, 0};
+        if(sc.W) {
+            SmallParams sp;
+            sp.A = A;
+            sp.B = B;
+            sp.C = C;
+            sp.Cin = gp.Cin ? gp.Cin : C;
+            sp.lda = lda;
+            sp.ldb = ldb;
+            sp.ldc = ldc;
+            sp.ldcin = gp.Cin ? gp.ldcin : ldc;
+            sp.kq = K / sc.W;
+            sp.alpha = alpha;
+            sp.beta = beta;
+            sp.tiles_m = (int)(M / 32);
+            sp.tiles_n = (int)(N / 32);
+            if(!TA && !TB) launch_small<false, false>(sp, sc, st);
+            else if(!TA && TB) launch_small<false, true>(sp, sc, st);
+            else if(TA && !TB) launch_small<true, false>(sp, sc, st);
+            else launch_small<true, true>(sp, sc, st);
+        } else {
+            SmallEdgeParams ep;
+            ep.A = A;
+            ep.B = B;
+            ep.C = C;
+            ep.Cin = gp.Cin ? gp.Cin : C;
+            ep.M = (int)M;
+            ep.N = (int)N;
+            ep.K = (int)K;
+            ep.lda = (int)lda;
+            ep.ldb = (int)ldb;
+            ep.ldc = ldc;
+            ep.ldcin = gp.Cin ? gp.ldcin : ldc;
+            ep.alpha = alpha;
+            ep.beta = beta;
+            ep.tiles_m = (int)((M + 31) / 32);
+            ep.tiles_n = (int)((N + 31) / 32);
+            // the k-contiguous operands (op(A) unless TA, op(B) if TB) may load
+            // 128 bits at a time
+            const bool kvec = K % 4 == 0 && (TA || (pk::aligned16(A) && lda % 4 == 0)) &&
+                              (!TB || (pk::aligned16(B) && ldb % 4 == 0));
+            if(!TA && !TB) launch_small_edge<false, false>(ep, kvec, st);
+            else if(!TA && TB) launch_small_edge<false, true>(ep, kvec, st);
+            else if(TA && !TB) launch_small_edge<true, false>(ep, kvec, st);
+            else launch_small_edge<true, true>(ep, kvec, st);
+        }
+        return pk::launch_status("pk_gemm_f32 (small product)");
+    }
     gp.splits = 1;
     gp.kchunk = K;
     gp.ws = nullptr;
@@ -1613,35 +1790,6 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
     const int edge = vec && whole && small ? kEdgeNone
                      : vec && (M % 4) == 0 && (N % 4) == 0 && (K % 4) == 0 ? kEdgeVec
                                                                            : kEdgeScalar;
-    // an output of fewer tiles than CUs, unsplit: the small-product kernel
-    // when its whole-tile conditions hold
-    if(prec == kFp32 && batch == 1 && causal == 0 && !swiglu && !sfwd && gp.splits == 1 && vec &&
-       small && tiles_m * tiles_n < kCUs) {
-        const SmallChoice sc = small_choice(M, N, K);
-        const bool cvec = pk::aligned16(C) && ldc % 4 == 0 &&
-                          (gp.Cin == nullptr || (pk::aligned16(gp.Cin) && gp.ldcin % 4 == 0));
-        if(sc.W && cvec) {
-            SmallParams sp;
-            sp.A = A;
-            sp.B = B;
-            sp.C = C;
-            sp.Cin = gp.Cin ? gp.Cin : C;
-            sp.lda = lda;
-            sp.ldb = ldb;
-            sp.ldc = ldc;
-            sp.ldcin = gp.Cin ? gp.ldcin : ldc;
-            sp.kq = K / sc.W;
-            sp.alpha = alpha;
-            sp.beta = beta;
-            sp.tiles_m = (int)(M / 32);
-            sp.tiles_n = (int)(N / 32);
-            if(!TA && !TB) launch_small<false, false>(sp, sc, st);
-            else if(!TA && TB) launch_small<false, true>(sp, sc, st);
-            else if(TA && !TB) launch_small<true, false>(sp, sc, st);
-            else launch_small<true, true>(sp, sc, st);
-            return pk::launch_status("pk_gemm_f32 (small product)");
-        }
-    }
     const TileKind kind = tc.kind;
     int rc;
     if(!TA && !TB)
@@ -1659,6 +1807,10 @@ int gemm_impl(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha, co
 }
 
 }  // namespace
+
+extern "C" int pk_gemm_small_product_f32(int64_t M, int64_t N, int64_t K) {
+    return M > 0 && N > 0 && K > 0 && K <= 1024 && small_product(M, N, K, false, false, K, N);
+}
 
 extern "C" int pk_gemm_batched_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, float alpha,
                                    const float* A, int64_t lda, int64_t sA_outer, int64_t sA_inner,

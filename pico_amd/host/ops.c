@@ -600,10 +600,11 @@ struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* 
     struct PicoTensor* out = pkh_new_tensor(arena, shape, 2);
     if(!out) return NULL;
     float* h = NULL;
-    /* the paired product never splits K; where the plain product would, the
+    /* the paired product never splits K and runs on the tiled kernels; where
+     * the plain product would split K or run on the small-product kernels, the
      * plain product runs, so both ways sum k in the same order */
     if(va.t == 'N' && vw.t == 'N' && F % 32 == 0 && M > 0 && K > 0 && F > 0 &&
-       pk_gemm_workspace_f32(M, N, K) == 0) {
+       pk_gemm_workspace_f32(M, N, K) == 0 && !pk_gemm_small_product_f32(M, N, K)) {
         h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F));
         if(!h) return NULL;
         float* scales = NULL;
@@ -659,6 +660,22 @@ static int da_swiglu(void* ctx) {
     const int flags = (pkh_grad_flag(c->gate) ? PK_ACCUM : 0) | (pkh_grad_flag(c->up) ? PK_ACCUM2 : 0);
     float* scales = NULL;
     struct PkMat g = {c->g, 'N', c->N > 0 ? c->N : 1}, wt = {c->w->data, 'T', c->w->strides[0]};
+    if(g_matmul_precision == PICO_MATMUL_FP32 && pk_gemm_small_product_f32(c->M, c->F, c->N)) {
+        /* a small product: dh into the arena, then SwiGLU's backward row
+         * kernel, as the composed ops compute it */
+        struct Arena* arena = pkh_need_arena();
+        float* dh = arena ? (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(c->M * c->F))
+                          : NULL;
+        if(!dh) return pkh_status("pico_swiglu_matmul_add_backward", PK_EINVAL);
+        int st = pkh_gemm(g, wt, c->M, c->F, c->N, dh, 'N', c->F, 0);
+        if(!st)
+            st = pk_swiglu_bwd_f32(c->M, c->F, c->gate->data, c->ld, c->up->data, c->ld, dh, c->F,
+                                   c->gate->grad, c->up->grad, c->ld, flags, pkh_stream());
+        if(pkh_status("pico_swiglu_matmul_add_backward", st)) return st;
+        pkh_grad_mark(c->gate);
+        pkh_grad_mark(c->up);
+        return 0;
+    }
     if(g_matmul_precision == PICO_MATMUL_FP8) {
         scales = (float*)pkh_workspace(FP8_SCALE_BYTES);
         int st8 = scales ? fp8_scales_for(g, wt, c->M, c->F, c->N, scales, pkh_stream()) : PK_EINVAL;

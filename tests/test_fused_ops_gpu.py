@@ -33,6 +33,17 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
 
 
+def _same_or_small(got, ref, small):
+    """bit for bit, unless the plain fp32 product of the shape runs on the
+    small-product kernels (pk_gemm_small_product_f32), whose K split rounds
+    differently from the tiled kernels the fused epilogues use: then within
+    fp32 rounding of the sum (pico's fused ops use the composition there)"""
+    if not small:
+        assert torch.equal(got, ref)
+    else:
+        assert max_rel(got.cpu().numpy(), ref.cpu().numpy()) <= 2e-6
+
+
 # ---------------------------------------------------------------- launchers
 @pytest.mark.parametrize("M,N,K", [(512, 768, 768), (200, 136, 96), (768, 768, 8192),
                                    (97, 33, 1030)])
@@ -63,10 +74,8 @@ def test_gemm_add_equals_product_then_add(dev, M, N, K, prec):
         assert max_rel(got.cpu().numpy(), want) <= 1e-5
 
 
-# (an output of at most 256 tiles of 32 x 32, e.g. 256 x 512 with K 128, takes
-# the small-product kernel as a plain product, whose K split rounds differently
-# from the tiled kernels the fused epilogues run on: 264 rows keep it tiled)
-@pytest.mark.parametrize("M,F,N", [(264, 512, 128), (300, 200, 136), (8192, 2048, 768)])
+@pytest.mark.parametrize("M,F,N", [(256, 512, 128), (300, 200, 136), (1024, 512, 128),
+                                   (8192, 2048, 768)])
 @pytest.mark.parametrize("flags", [0, 1, 2, 3])
 def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
     L = _lib.hip_lib()
@@ -88,7 +97,7 @@ def test_gemm_swiglu_bwd_equals_product_then_swiglu_bwd(dev, M, F, N, flags):
         M, F, gate.data_ptr(), ld, up.data_ptr(), ld, dh.data_ptr(), F, ref.data_ptr(),
         ref.data_ptr() + 4 * F, ld, flags, None))
     torch.cuda.synchronize()
-    assert torch.equal(got, ref)
+    _same_or_small(got, ref, L.pk_gemm_small_product_f32(M, F, N))
     if M <= 300:
         a, u = gate.cpu().numpy(), up.cpu().numpy()
         dh_ref = dY.cpu().numpy().astype(np.float64) @ W.cpu().numpy().astype(np.float64).T
@@ -127,8 +136,9 @@ def test_gemm_swiglu_fwd_equals_product_then_swiglu(dev, M, K, F, prec):
     _lib.check("pk_swiglu_fwd_f32", L.pk_swiglu_fwd_f32(
         M, F, ref.data_ptr(), 2 * F, ref.data_ptr() + 4 * F, 2 * F, href.data_ptr(), F, None))
     torch.cuda.synchronize()
-    assert torch.equal(C, ref)
-    assert torch.equal(h, href)
+    small = prec == 0 and L.pk_gemm_small_product_f32(M, 2 * F, K)
+    _same_or_small(C, ref, small)
+    _same_or_small(h, href, small)
     if prec == 0 and M <= 512:
         c64 = O.gemm_ref_f64("N", "N", A.cpu().numpy(), W.cpu().numpy())
         assert max_rel(C.cpu().numpy(), c64) <= 1e-5

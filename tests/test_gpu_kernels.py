@@ -106,6 +106,40 @@ def test_gemm_small_products(dev, ta, tb, M, N, Kd):
     assert gemm_err(host(C), A, B) <= TOL
 
 
+@pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,Kd", [(64, 128, 784), (64, 10, 128), (784, 128, 64), (64, 784, 128),
+                                    (37, 45, 1001), (1, 1, 1), (130, 257, 70), (500, 33, 3)])
+def test_gemm_small_edge_products(dev, ta, tb, M, N, Kd):
+    """Small products whose sizes or strides are not whole tiles (the MLP's
+    784 / 10 widths, K 784 = 24.5 slices, K 1 and 3) run on the edge kernel:
+    masked 32-bit loads, waves taking slices w, w + W, ... (sixteen waves from
+    12 slices up, else four), predicated stores.  Integer operands bit for bit
+    with beta 0 (C starts NaN), the beta accumulate exact, a bias row added by
+    pk_gemm_add_f32 with ldx 0, and uniform operands within the fp64 bound"""
+    from pico_amd import _lib
+    L = _lib.hip_lib()
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + 19 * N + Kd, integer=True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    C = cu(ref.copy())
+    K.gemm(ta, tb, cu(As), cu(Bs), C, alpha=-1.0, beta=1.0)
+    assert not np.any(host(C))
+    if (ta, tb) == ("N", "N"):
+        x = np.random.default_rng(M + N).integers(-50, 50, N).astype(np.float32)
+        C = torch.full((M, N), float("nan"), device=dev)
+        dA, dB, dx = cu(As), cu(Bs), cu(x)
+        _lib.check("pk_gemm_add_f32", L.pk_gemm_add_f32(
+            b"N", b"N", M, N, Kd, 1.0, dA.data_ptr(), Kd, dB.data_ptr(), N, 1.0, dx.data_ptr(), 0,
+            C.data_ptr(), N, 0, None, None, 0, None))
+        assert np.array_equal(host(C), ref + x)
+    A, B, As, Bs = _operands(ta, tb, M, N, Kd, seed=M + N + 5 * Kd)
+    C = torch.empty(M, N, device=dev)
+    K.gemm(ta, tb, cu(As), cu(Bs), C)
+    assert gemm_err(host(C), A, B) <= TOL
+
+
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N")])
 @pytest.mark.parametrize("n", [512, 1024, 2048])
 def test_gemm_uniform_vs_fp64(dev, ta, tb, n):
