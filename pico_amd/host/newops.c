@@ -95,6 +95,19 @@ struct PicoTensor* pico_softmax_xent(struct PicoTensor* logits, const int32_t* l
  * y = x * rstd * gain over the last dim; the backward reads the saved rstd */
 enum { RS_RSTD = 0, RS_PARTS = 1 };
 
+struct RmsDgJob {
+    int64_t R, C;
+    const void* parts;
+    size_t bytes;
+    float* grad;
+    int flag;
+};
+static void rms_dg_job(const void* args, pk_stream_t side) {
+    const struct RmsDgJob* j = (const struct RmsDgJob*)args;
+    pkh_status("pico_rmsnorm_backward",
+               pk_rmsnorm_dg_reduce_f32(j->R, j->C, j->parts, j->bytes, j->grad, j->flag, side));
+}
+
 static void rms_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
     struct PicoTensor *x = self->parents[0], *gain = self->parents[1];
@@ -115,6 +128,17 @@ static void rms_backward(struct PicoTensor* self) {
         if(pkh_status("pico_rmsnorm_backward", st)) return;
         pkh_grad_mark(x);
         struct PkNode* ng = pkh_node(gain);
+        if(pkh_capturing()) {
+            /* captured, the reduction waits for the next fork (after the main
+             * stream's next kernel), so a replay keeps the main chain on its
+             * stream */
+            struct RmsDgJob j = {R, C, parts, ws_bytes, gain->grad, ng->grad_live ? PK_ACCUM : 0};
+            if(pkh_side_defer(rms_dg_job, &j, sizeof(j))) {
+                ng->side_seq = pkh_side_seq() + 1;
+                pkh_grad_mark(gain);
+                return;
+            }
+        }
         pk_stream_t side = pkh_side_fork();
         if(side) {
             st = pk_rmsnorm_dg_reduce_f32(R, C, parts, ws_bytes, gain->grad,

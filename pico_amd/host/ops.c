@@ -306,8 +306,10 @@ int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTenso
  *
  * Eagerly, dB is forked before dA is issued, so that it runs beside dA
  * rather than beside the memory-bound kernels that follow dA (config 5: about
- * 1.3 ms less per step).  A captured graph keeps dA first: replays of the
- * dB-first order measured slower.  Either way the side stream orders dB's
+ * 1.3 ms less per step).  Under graph capture dA is captured first and dB
+ * after it, waiting for the same point before dA (pkh_side_prepare): a
+ * replay continues each stream with a node's first captured child, so dA's
+ * chain stays on the main stream.  Either way the side stream orders dB's
  * write after every earlier write to B's grad: main-stream ones through the
  * fork, side ones by issue order. */
 static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor* b,
@@ -331,6 +333,9 @@ static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor
         if(pkh_status("pico_matmul_backward", st)) return;
         pkh_grad_mark(b);
     }
+    /* under capture: dA is captured before dB, and dB waits for the point
+     * before dA (as eagerly), so a replay keeps dA's chain on the main stream */
+    if(to_side && !side) pkh_side_prepare();
     if(dA_fn(ctx)) return;
     if(side) return;
     side = to_side ? pkh_side_fork() : NULL;
@@ -489,12 +494,36 @@ struct PicoTensor* pico_matmul_add(struct PicoTensor* a, struct PicoTensor* b,
 /* db (+)= the column sums of g [M, N]; on the side stream with the weight
  * gradient when the layer's input is not a parameter (a bias is read only
  * once the backward is over) */
+struct BiasJob {
+    int64_t shape[2], sb[2], sg[2], numel;
+    const float* g;
+    float* grad;
+    int flag;
+};
+static void bias_job(const void* args, pk_stream_t side) {
+    const struct BiasJob* j = (const struct BiasJob*)args;
+    pkh_status("pico_add_backward", pk_binary_bwd_f32(OP_ADD, 1, 2, j->shape, j->sb, j->sg,
+                                                      j->numel, j->g, j->g, j->grad, j->flag, side));
+}
+
 static int bias_backward(struct PicoTensor* self, struct PicoTensor* bias, const float* g,
                          int input_param) {
     int64_t sb[2], sg[2] = {self->strides[0], self->strides[1]};
     mapped_strides(bias, 2, sb);
     struct PkNode* nb = pkh_node(bias);
-    pk_stream_t side = nb && bias->is_persistent && !input_param ? pkh_side_fork() : NULL;
+    const int to_side = nb && bias->is_persistent && !input_param;
+    if(to_side && pkh_capturing()) {
+        /* captured, the side work waits for the next fork (after the main
+         * stream's next kernel), so a replay keeps the main chain on its stream */
+        struct BiasJob j = {{self->shape[0], self->shape[1]}, {sb[0], sb[1]}, {sg[0], sg[1]},
+                            bias->numel, g, bias->grad, nb->grad_live ? PK_ACCUM : 0};
+        if(pkh_side_defer(bias_job, &j, sizeof(j))) {
+            nb->side_seq = pkh_side_seq() + 1;
+            pkh_grad_mark(bias);
+            return 0;
+        }
+    }
+    pk_stream_t side = to_side ? pkh_side_fork() : NULL;
     const int flag = side ? (nb->grad_live ? PK_ACCUM : 0) : pkh_grad_flag(bias);
     int st = pk_binary_bwd_f32(OP_ADD, 1, 2, self->shape, sb, sg, bias->numel, g, g, bias->grad,
                                flag, side ? side : pkh_stream());

@@ -68,6 +68,18 @@ int pkh_capturing(void); /* a graph capture is in progress */
  * (pkh_grad_flag / pkh_grad_is_live do it), pico_backward joins at its end,
  * and so do synchronisation and copies. */
 pk_stream_t pkh_side_fork(void);
+/* Under graph capture only (else they do nothing and return 0):
+ * pkh_side_prepare() records the next fork's point on the main stream now, so
+ * that the caller can issue a main-stream kernel before the pkh_side_fork()
+ * whose side work must not wait for it; pkh_side_defer() queues side work
+ * (fn(args, side) with a copy of n <= PKH_SIDE_JOB_ARGS bytes of args) to be
+ * issued at the next fork or join, and returns 1 when it did.  A deferred job
+ * must leave its tensor's side_seq at pkh_side_seq() + 1 (the fork that
+ * issues it), so a main-stream access joins, and so issues it, first. */
+int pkh_side_prepare(void);
+#define PKH_SIDE_JOB_ARGS 96
+typedef void (*pkh_side_job_fn)(const void* args, pk_stream_t side);
+int pkh_side_defer(pkh_side_job_fn fn, const void* args, size_t n);
 uint64_t pkh_side_seq(void);
 uint64_t pkh_side_joined(void);
 void pkh_side_join(void);

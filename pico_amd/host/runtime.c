@@ -127,33 +127,87 @@ int pkh_status(const char* op, int status) {
     return status;
 }
 
-pk_stream_t pkh_side_fork(void) {
-    if(pkh_init() || g_side_broken) return NULL;
-    if(!g_side) {
-        /* default priority, like the main stream */
-        hipError_t e = hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking);
-        if(e == hipSuccess) e = hipEventCreateWithFlags(&g_fork_ev, hipEventDisableTiming);
-        if(e == hipSuccess) e = hipEventCreateWithFlags(&g_join_ev, hipEventDisableTiming);
-        if(e != hipSuccess) {
-            (void)hipGetLastError();
-            g_side_broken = 1;
-            return NULL;
-        }
+/* Graph capture and the side stream.  A replay runs the captured graph's
+ * branches on several streams, and a node's stream continues with its first
+ * captured child (ROCm's executor walks the graph depth first along first
+ * children).  At an eager fork the side-stream work is issued first, so
+ * captured the same way the weight-gradient chain would take the launch
+ * stream and the critical path's kernels would queue behind it (measured:
+ * RMSNorm's backward waiting for weight-gradient products, config 4's replay
+ * 8 % slower than its eager step).  So under capture a fork is taken in two
+ * steps, with the main stream's next kernel captured in between:
+ * pkh_side_prepare() records the fork point on the main stream, the caller
+ * issues its main-stream kernel, then pkh_side_fork() makes the side stream
+ * wait for the prepared point (not for that kernel).  Side work that has no
+ * main-stream kernel of its own to follow (RMSNorm's gain reduction, a
+ * bias gradient) is deferred under capture (pkh_side_defer) and issued at the
+ * next fork or join. */
+static int g_prepared = 0;
+
+struct SideJob {
+    pkh_side_job_fn fn;
+    unsigned char args[PKH_SIDE_JOB_ARGS];
+};
+static struct SideJob g_jobs[64];
+static int g_njobs = 0;
+
+static int side_create(void) {
+    if(g_side) return 0;
+    /* default priority, like the main stream */
+    hipError_t e = hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking);
+    if(e == hipSuccess) e = hipEventCreateWithFlags(&g_fork_ev, hipEventDisableTiming);
+    if(e == hipSuccess) e = hipEventCreateWithFlags(&g_join_ev, hipEventDisableTiming);
+    if(e != hipSuccess) {
+        (void)hipGetLastError();
+        g_side_broken = 1;
+        return -1;
     }
-    hipError_t e = hipEventRecord(g_fork_ev, (hipStream_t)pkh_stream());
+    return 0;
+}
+
+int pkh_side_prepare(void) {
+    if(!g_capturing || pkh_init() || g_side_broken || side_create()) return 0;
+    if(hipEventRecord(g_fork_ev, (hipStream_t)pkh_stream()) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    g_prepared = 1;
+    return 1;
+}
+
+pk_stream_t pkh_side_fork(void) {
+    if(pkh_init() || g_side_broken || side_create()) return NULL;
+    hipError_t e = hipSuccess;
+    if(!g_prepared) e = hipEventRecord(g_fork_ev, (hipStream_t)pkh_stream());
+    g_prepared = 0;
     if(e == hipSuccess) e = hipStreamWaitEvent(g_side, g_fork_ev, 0);
     if(e != hipSuccess) {
         pkh_status("side stream fork", (int)e);
         return NULL;
     }
     ++g_side_seq;
+    /* side work deferred under capture goes first on the side stream */
+    for(int i = 0; i < g_njobs; i++) g_jobs[i].fn(g_jobs[i].args, (pk_stream_t)g_side);
+    g_njobs = 0;
     return (pk_stream_t)g_side;
+}
+
+int pkh_side_defer(pkh_side_job_fn fn, const void* args, size_t n) {
+    if(!g_capturing || n > PKH_SIDE_JOB_ARGS || pkh_init() || g_side_broken) return 0;
+    if(g_njobs == (int)(sizeof(g_jobs) / sizeof(g_jobs[0]))) {
+        if(!pkh_side_fork()) return 0; /* issues the queued jobs */
+    }
+    g_jobs[g_njobs].fn = fn;
+    memcpy(g_jobs[g_njobs].args, args, n);
+    g_njobs++;
+    return 1;
 }
 
 uint64_t pkh_side_seq(void) { return g_side_seq; }
 uint64_t pkh_side_joined(void) { return g_side_joined; }
 
 void pkh_side_join(void) {
+    if(g_njobs) pkh_side_fork(); /* issue deferred side work first */
     if(g_side_joined == g_side_seq) return;
     hipError_t e = hipEventRecord(g_join_ev, g_side);
     if(e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)pkh_stream(), g_join_ev, 0);
