@@ -388,11 +388,13 @@ def ref_api():
     R = ref()
     if not getattr(R, "_api_ready", False):
         _declare_api(R)
-        for name in ("arena_init", "arena_destroy", "arena_ctx_push", "arena_ctx_pop"):
+        for name in ("arena_init", "arena_destroy", "arena_reset", "arena_ctx_push",
+                     "arena_ctx_pop"):
             setattr(R, name, getattr(R, "picoref_" + name))
         R.arena_init.argtypes = [ctypes.c_size_t]
         R.arena_init.restype = c_p
         R.arena_destroy.argtypes = [c_p]
+        R.arena_reset.argtypes = [c_p]
         R.arena_ctx_push.argtypes = [c_p]
         R._api_ready = True
     return R

@@ -125,5 +125,6 @@ void picoref_unary_bwd(int op, int64_t n, float* x, float* y, float* gy, float* 
  * arena_ctx_current()) */
 struct Arena* picoref_arena_init(size_t bytes) { return arena_init(bytes); }
 void picoref_arena_destroy(struct Arena* arena) { arena_destroy(arena); }
+void picoref_arena_reset(struct Arena* arena) { arena_reset(arena); }
 void picoref_arena_ctx_push(struct Arena* arena) { arena_ctx_push(arena); }
 void picoref_arena_ctx_pop(void) { arena_ctx_pop(); }
