@@ -162,6 +162,30 @@ int pk_gemm_swiglu_fwd_f32(char ta, char tb, int64_t M, int64_t N, int64_t K, fl
 int pk_fp8_scales_f32(int64_t ra, int64_t ca, const float* A, int64_t lda, int64_t rb, int64_t cb,
                       const float* B, int64_t ldb, float* scales, pk_stream_t stream);
 
+/* Narrow-operand fp8 products (no reference counterpart): the operands are
+ * quantized once into byte matrices and the product streams 1 byte per
+ * element from HBM (v_mfma_scale_f32_32x32x64_f8f6f4, scales 2^0).
+ * pk_fp8_quantized_bytes: bytes of the buffer pk_fp8_quantize_f32 fills for
+ *   R rows of K values, and its row stride (*ld, bytes) = K rounded up to 64;
+ *   rows are rounded up to a multiple of 256.
+ * pk_fp8_quantize_f32: Q[r][k] = e4m3(clamp(scale * op(X)[r][k], +-448))
+ *   (nearest even, NaN stays NaN) for r < R, k < K, and 0 in the padding up
+ *   to ldq and to R rounded up to 256 rows; op(X) = X [R, K] (trans 0) or
+ *   X^T with X [K, R] (trans 1), row stride ldx; *scale in device memory
+ *   (pk_fp8_scales_f32 writes such scales).  ldq >= K rounded up to 64, a
+ *   multiple of 16, Q 16-byte aligned.
+ * pk_gemm_fp8q_f32: C [M, N] = alpha / (scales[0] * scales[1]) * A.B^T
+ *   (+ beta * C) with A [M, K], B [N, K] e4m3 as pk_fp8_quantize_f32 writes
+ *   them (row strides lda, ldb in bytes; their padding rows and columns are
+ *   read and must be zero); accumulation in fp32.  For C = op(X).op(Y)
+ *   quantize op(X) as A and op(Y)^T as B. */
+size_t pk_fp8_quantized_bytes(int64_t R, int64_t K, int64_t* ld);
+int pk_fp8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans,
+                        const float* scale, uint8_t* Q, int64_t ldq, pk_stream_t stream);
+int pk_gemm_fp8q_f32(int64_t M, int64_t N, int64_t K, float alpha, const uint8_t* A, int64_t lda,
+                     const uint8_t* B, int64_t ldb, const float* scales, float beta, float* C,
+                     int64_t ldc, pk_stream_t stream);
+
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
  * multiplied on the bf16 matrix cores, accumulating in fp32; C and the

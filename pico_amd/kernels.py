@@ -68,6 +68,59 @@ def gemm_fp8(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None):
     return gemm_bf16(ta, tb, A, B, C, alpha, beta, ws, _name="pk_gemm_fp8_f32")
 
 
+def fp8_scales(A, B, scales):
+    """scales[0], scales[1] = largest powers of two keeping A, B within e4m3
+    (pk_fp8_scales_f32); A, B 2-D float32 tensors as stored"""
+    _f32(A, B, scales)
+    lda, ldb = _rowmajor(A, "A"), _rowmajor(B, "B")
+    check("pk_fp8_scales_f32", hip_lib().pk_fp8_scales_f32(
+        A.shape[0], A.shape[1], _ptr(A), lda, B.shape[0], B.shape[1], _ptr(B), ldb, _ptr(scales),
+        _stream()))
+    return scales
+
+
+def fp8_quantized_shape(R, K):
+    """(rows, row stride in bytes) of the buffer pk_fp8_quantize_f32 fills"""
+    ld = ctypes.c_int64(0)
+    nbytes = int(hip_lib().pk_fp8_quantized_bytes(R, K, ctypes.byref(ld)))
+    return (nbytes // ld.value if ld.value else 0), ld.value
+
+
+def fp8_quantize(X, trans, scale, out=None):
+    """e4m3(scale * op(X)) as a zero-padded uint8 [rows, ld] tensor: op(X) =
+    X (trans False) or X^T; scale a one-element float32 device tensor (or a
+    view of pk_fp8_scales_f32's output)"""
+    _f32(X, scale)
+    ldx = _rowmajor(X, "X")
+    R, Kd = (X.shape[1], X.shape[0]) if trans else (X.shape[0], X.shape[1])
+    rows, ld = fp8_quantized_shape(R, Kd)
+    if out is None:
+        out = torch.empty((rows, ld), dtype=torch.uint8, device=X.device)
+    if out.dtype != torch.uint8 or out.dim() != 2 or out.shape[0] < rows or out.shape[1] < ld \
+            or not out.is_contiguous():
+        raise ValueError(f"fp8_quantize: out must be contiguous uint8 of at least {rows}x{ld}")
+    check("pk_fp8_quantize_f32", hip_lib().pk_fp8_quantize_f32(
+        R, Kd, _ptr(X), ldx, int(bool(trans)), _ptr(scale), _ptr(out), out.stride(0), _stream()))
+    return out
+
+
+def gemm_fp8q(M, N, Kd, A8, B8, scales, C, alpha=1.0, beta=0.0):
+    """C = alpha / (scales[0] * scales[1]) * A8 . B8^T (+ beta C), A8 [M, K] and
+    B8 [N, K] as fp8_quantize writes them (pk_gemm_fp8q_f32)"""
+    _f32(C, scales)
+    ldc = _rowmajor(C, "C")
+    if tuple(C.shape) != (M, N):
+        raise ValueError(f"gemm_fp8q: C {tuple(C.shape)} is not {M}x{N}")
+    for name, Q, R in (("A8", A8, M), ("B8", B8, N)):
+        rows, ld = fp8_quantized_shape(R, Kd)
+        if Q.dtype != torch.uint8 or Q.dim() != 2 or Q.shape[0] < rows or Q.shape[1] < ld:
+            raise ValueError(f"gemm_fp8q: {name} must be uint8 of at least {rows}x{ld}")
+    check("pk_gemm_fp8q_f32", hip_lib().pk_gemm_fp8q_f32(
+        M, N, Kd, alpha, _ptr(A8), A8.stride(0), _ptr(B8), B8.stride(0), _ptr(scales), beta,
+        _ptr(C), ldc, _stream()))
+    return C
+
+
 def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False, _name=None):
     """gemm with bf16 multiplies and fp32 accumulation (fp32 tensors in and out);
     ws: optional workspace for a K split (as gemm_ex); split: hi/lo operands,

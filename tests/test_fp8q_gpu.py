@@ -1,0 +1,182 @@
+"""Narrow-operand fp8 products (pk_fp8_quantize_f32 + pk_gemm_fp8q_f32):
+outside the fp32 parity contract, pinned by what the arithmetic fixes, as the
+fp32-operand fp8 products are (tests/test_fp8_gpu.py, whose e4m3 restatement
+is reused here).
+
+* Quantization: every byte decodes (by the format's definition, written out
+  below: sign, 4-bit exponent with bias 7, 3-bit mantissa, subnormals, 0x7f /
+  0xff NaN) to e4m3_round(scale * x), and equals torch's own float8_e4m3fn
+  encoding of the clamped value; padding rows and columns are zero; the
+  transposed read equals the quantization of the transposed copy.
+* Products: a product of two e4m3 values is exact in fp32, so integers of
+  magnitude <= 16 give bit-exact results at every shape (ragged M, N, K,
+  single rows, K of one byte, K not a multiple of the 64-byte slice), and
+  uniform operands give the float64 product of the rounded operands up to
+  fp32 summation error; with the operands' scales the result is that product
+  divided by both scales.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from pico_amd import kernels as K
+from pico_amd._lib import PkError
+from tests._util import gemm_err
+from tests.test_fp8_gpu import e4m3_round
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def cu(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def e4m3_decode(b):
+    """e4m3 bytes -> float64, from the format's definition"""
+    b = np.asarray(b).astype(np.int64)
+    s, e, m = (b >> 7) & 1, (b >> 3) & 15, b & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return np.where(s == 1, -v, v)
+
+
+def test_e4m3_decode_known_bytes():
+    b = np.array([0x00, 0x80, 0x01, 0x08, 0x38, 0x3C, 0xB8, 0x7E, 0xFE, 0x7F, 0xFF, 0x07])
+    want = [0.0, -0.0, 2 ** -9, 2 ** -6, 1.0, 1.5, -1.0, 448.0, -448.0, np.nan, np.nan,
+            7 * 2 ** -9]
+    got = e4m3_decode(b)
+    assert np.array_equal(got, np.array(want), equal_nan=True)
+
+
+def one(v, dev):
+    return torch.tensor([v], dtype=torch.float32, device=dev)
+
+
+@pytest.mark.parametrize("R,Kd", [(1, 1), (70, 130), (256, 64), (300, 1000)])
+def test_quantize_bytes_match_the_format(dev, R, Kd):
+    rng = np.random.default_rng(R + Kd)
+    X = np.concatenate([rng.uniform(-500, 500, R * Kd // 2 + 1), rng.uniform(-0.05, 0.05, R * Kd)])
+    X = X[:R * Kd].astype(np.float32).reshape(R, Kd)
+    X.ravel()[:4] = [448.0, 449.0, 1e9, -3e-4][:min(4, X.size)]
+    for scale in (1.0, 4.0):
+        Q = host(K.fp8_quantize(cu(X), False, one(scale, dev)))
+        rows, ld = K.fp8_quantized_shape(R, Kd)
+        assert Q.shape == (rows, ld) and rows % 256 == 0 and ld % 64 == 0 and ld >= Kd
+        want = e4m3_round(X * np.float32(scale))
+        assert np.array_equal(e4m3_decode(Q[:R, :Kd]), want.astype(np.float64))
+        clamped = np.clip(X * np.float32(scale), -448.0, 448.0)
+        tq = torch.from_numpy(clamped).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(Q[:R, :Kd], tq)
+        assert not Q[R:].any() and not Q[:, Kd:].any()
+
+
+def test_quantize_nan_stays_nan(dev):
+    X = np.array([[np.nan, 1.0, -np.nan, 2.0]], np.float32)
+    Q = host(K.fp8_quantize(cu(X), False, one(1.0, dev)))
+    d = e4m3_decode(Q[0, :4])
+    assert np.isnan(d[0]) and np.isnan(d[2]) and d[1] == 1.0 and d[3] == 2.0
+
+
+@pytest.mark.parametrize("R,Kd", [(1, 5), (130, 70), (512, 256)])
+def test_quantize_transposed_read(dev, R, Kd):
+    X = O.uniform(R * Kd, 7).reshape(Kd, R) * 50.0  # op(X) = X^T is [R, Kd]
+    Qt = host(K.fp8_quantize(cu(X), True, one(2.0, dev)))
+    Qn = host(K.fp8_quantize(cu(np.ascontiguousarray(X.T)), False, one(2.0, dev)))
+    assert np.array_equal(Qt, Qn)
+
+
+def _product(dev, X, Y, scales=None, alpha=1.0, beta=0.0, C0=None):
+    """C = alpha * X.Y (+ beta C0) through quantize + the narrow product"""
+    M, Kd = X.shape
+    N = Y.shape[1]
+    sc = torch.ones(2, device=dev) if scales is None else scales
+    dX, dY = cu(X), cu(Y)
+    A8 = K.fp8_quantize(dX, False, sc[0:1])
+    B8 = K.fp8_quantize(dY, True, sc[1:2])
+    C = torch.full((M, N), float("nan"), device=dev) if C0 is None else cu(C0)
+    K.gemm_fp8q(M, N, Kd, A8, B8, sc, C, alpha=alpha, beta=beta)
+    return host(C)
+
+
+SHAPES = [(256, 256, 64), (512, 768, 320), (1, 1, 1), (300, 257, 65), (1000, 333, 1000),
+          (64, 4096, 128), (4096, 4096, 512), (2048, 768, 4096), (257, 511, 4095)]
+
+
+@pytest.mark.parametrize("M,N,Kd", SHAPES)
+def test_fp8q_gemm_integers_bitexact(dev, M, N, Kd):
+    rng = np.random.default_rng(M * 7 + N + Kd)
+    X = rng.integers(-16, 17, (M, Kd)).astype(np.float32)
+    Y = rng.integers(-16, 17, (Kd, N)).astype(np.float32)
+    ref = (X.astype(np.float64) @ Y.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(_product(dev, X, Y), ref)
+    # C = -X.Y + C0 = 0 exactly
+    assert not np.any(_product(dev, X, Y, alpha=-1.0, beta=1.0, C0=ref))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1024, 1024, 1024), (300, 257, 70), (4096, 768, 768)])
+def test_fp8q_gemm_equals_product_of_rounded_operands(dev, M, N, Kd):
+    X = O.uniform(M * Kd, M + 1).reshape(M, Kd)
+    Y = O.uniform(Kd * N, N + 2).reshape(Kd, N)
+    C = _product(dev, X, Y)
+    assert gemm_err(C, e4m3_round(X), e4m3_round(Y)) <= TOL
+    assert 1e-3 < gemm_err(C, X, Y) < 2 ** -3  # fp8-sized
+    # the fp32-operand fp8 product rounds the same operands: equal up to summation order
+    C2 = torch.empty(M, N, device=dev)
+    K.gemm_fp8("N", "N", cu(X), cu(Y), C2)
+    assert gemm_err(C, e4m3_round(X), e4m3_round(Y), C_ref=host(C2).astype(np.float64)) <= TOL
+
+
+def test_fp8q_gemm_with_operand_scales(dev):
+    """gradient-sized operands: quantized with pk_fp8_scales_f32's powers of two
+    and descaled in the epilogue, the result is the product of the rounded
+    scaled operands divided by the scales, and not flushed to zero"""
+    M, N, Kd = 512, 320, 448
+    X = O.uniform(M * Kd, 31).reshape(M, Kd) * 2e-5
+    Y = O.uniform(Kd * N, 32).reshape(Kd, N) * 0.02
+    sc = K.fp8_scales(cu(X), cu(Y), torch.empty(2, device=dev))
+    sa, sb = host(sc)
+    C = _product(dev, X, Y, scales=sc, alpha=0.5)
+    Xr = e4m3_round(X * sa).astype(np.float64) / sa
+    Yr = e4m3_round(Y * sb).astype(np.float64) / sb
+    assert gemm_err(C, 0.5 * Xr, Yr) <= TOL
+    assert 1e-3 < gemm_err(C, 0.5 * X, Y) < 2 ** -3
+
+
+def test_fp8q_gemm_empty_k_scales_c(dev):
+    C0 = O.uniform(40 * 30, 5).reshape(40, 30)
+    C = cu(C0)
+    K.gemm_fp8q(40, 30, 0, torch.zeros(256, 0, dtype=torch.uint8, device=dev),
+                torch.zeros(256, 0, dtype=torch.uint8, device=dev), torch.ones(2, device=dev), C,
+                beta=2.0)
+    assert np.array_equal(host(C), 2.0 * C0)
+
+
+def test_fp8q_refusals(dev):
+    from pico_amd import _lib
+
+    L = _lib.hip_lib()
+    Q = torch.zeros(256, 128, dtype=torch.uint8, device=dev)
+    C = torch.zeros(4, 4, device=dev)
+    sc = torch.ones(2, device=dev)
+    X = torch.zeros(4, 100, device=dev)
+    # row stride below K rounded up to 64
+    assert L.pk_gemm_fp8q_f32(4, 4, 100, 1.0, Q.data_ptr(), 64, Q.data_ptr(), 128, sc.data_ptr(),
+                              0.0, C.data_ptr(), 4, None) != 0
+    assert L.pk_fp8_quantize_f32(4, 100, X.data_ptr(), 100, 0, sc.data_ptr(), Q.data_ptr(), 100,
+                                 None) != 0
+    # misaligned operand
+    assert L.pk_gemm_fp8q_f32(4, 4, 64, 1.0, Q.data_ptr() + 8, 128, Q.data_ptr(), 128,
+                              sc.data_ptr(), 0.0, C.data_ptr(), 4, None) != 0
+    with pytest.raises(PkError):  # K rounded up to 64 is 128: ldq 100 refused by the library
+        from pico_amd._lib import check
+        check("pk_fp8_quantize_f32", L.pk_fp8_quantize_f32(
+            4, 100, X.data_ptr(), 100, 0, sc.data_ptr(), Q.data_ptr(), 100, None))
+    with pytest.raises(ValueError):
+        K.gemm_fp8q(4, 4, 100, Q[:, :64], Q, sc, C)
