@@ -166,25 +166,54 @@ int pk_fp8_scales_f32(int64_t ra, int64_t ca, const float* A, int64_t lda, int64
  * quantized once into byte matrices and the product streams 1 byte per
  * element from HBM (v_mfma_scale_f32_32x32x64_f8f6f4, scales 2^0).
  * pk_fp8_quantized_bytes: bytes of the buffer pk_fp8_quantize_f32 fills for
- *   R rows of K values, and its row stride (*ld, bytes) = K rounded up to 64;
+ *   R rows of K values, and its row stride (*ld, bytes) = K rounded up to 128;
  *   rows are rounded up to a multiple of 256.
  * pk_fp8_quantize_f32: Q[r][k] = e4m3(clamp(scale * op(X)[r][k], +-448))
  *   (nearest even, NaN stays NaN) for r < R, k < K, and 0 in the padding up
  *   to ldq and to R rounded up to 256 rows; op(X) = X [R, K] (trans 0) or
  *   X^T with X [K, R] (trans 1), row stride ldx; *scale in device memory
- *   (pk_fp8_scales_f32 writes such scales).  ldq >= K rounded up to 64, a
+ *   (pk_fp8_scales_f32 writes such scales).  ldq >= K rounded up to 128, a
  *   multiple of 16, Q 16-byte aligned.
  * pk_gemm_fp8q_f32: C [M, N] = alpha / (scales[0] * scales[1]) * A.B^T
  *   (+ beta * C) with A [M, K], B [N, K] e4m3 as pk_fp8_quantize_f32 writes
  *   them (row strides lda, ldb in bytes; their padding rows and columns are
  *   read and must be zero); accumulation in fp32.  For C = op(X).op(Y)
- *   quantize op(X) as A and op(Y)^T as B. */
+ *   quantize op(X) as A and op(Y)^T as B.  Row strides are K rounded up to
+ *   128 (pk_fp8_quantized_bytes), so that a product runs an even number of
+ *   64-byte slices. */
 size_t pk_fp8_quantized_bytes(int64_t R, int64_t K, int64_t* ld);
 int pk_fp8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans,
                         const float* scale, uint8_t* Q, int64_t ldq, pk_stream_t stream);
 int pk_gemm_fp8q_f32(int64_t M, int64_t N, int64_t K, float alpha, const uint8_t* A, int64_t lda,
                      const uint8_t* B, int64_t ldb, const float* scales, float beta, float* C,
                      int64_t ldc, pk_stream_t stream);
+
+/* MX8 products (no reference counterpart): OCP Microscaling MXFP8, e4m3
+ * values with one E8M0 power-of-two scale per 32 consecutive values of a row,
+ * applied by the matrix core (v_mfma_scale_f32_32x32x64_f8f6f4).  No
+ * tensor-wide maximum is needed, so an operand is quantized in one pass, and
+ * each block keeps e4m3's 3 mantissa bits whatever the other blocks' sizes.
+ * pk_mx8_bytes: bytes of an MX8 matrix of R rows of K values: Rp = R rounded
+ *   up to 256, Kp = K rounded up to 128; Rp * Kp e4m3 bytes (row stride Kp),
+ *   then the scales, Kp / 64 slices of Rp rows of 2 bytes (the scale bytes
+ *   of k 0-31 and 32-63 of the slice).
+ * pk_mx8_quantize_f32: Q = op(X) [R, K] (X [R, K] for trans 0, X^T with
+ *   X [K, R] for trans 1, row stride ldx) as an MX8 matrix: for each block
+ *   of 32 of a row with largest magnitude a, e is the smallest integer with
+ *   a * 2^-e <= 448 (0 for an all-zero block; held to [-127, 127]), the
+ *   scale byte is e + 127 and the values e4m3(clamp(x * 2^-e, +-448))
+ *   (nearest even, NaN stays NaN); padding values are 0.  Q 16-byte aligned.
+ * pk_gemm_mx8_f32: C [M, N] = alpha * A.B^T + beta * X with A [M, K] and
+ *   B [N, K] MX8 matrices; fp32 accumulation.  X [M, N] has row stride ldx
+ *   (X == C with ldx == ldc accumulates); ldx 0 adds the one row X [N] to
+ *   every row; X is not read when beta is 0.  For C = op(P).op(R) quantize
+ *   op(P) as A and op(R)^T as B. */
+size_t pk_mx8_bytes(int64_t R, int64_t K);
+int pk_mx8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, void* Q,
+                        pk_stream_t stream);
+int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                    float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                    pk_stream_t stream);
 
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and

@@ -121,6 +121,54 @@ def gemm_fp8q(M, N, Kd, A8, B8, scales, C, alpha=1.0, beta=0.0):
     return C
 
 
+def mx8_bytes(R, Kd):
+    """bytes of an MX8 matrix of R rows of Kd values (pk_mx8_bytes)"""
+    return int(hip_lib().pk_mx8_bytes(R, Kd))
+
+
+def mx8_quantize(X, trans, out=None):
+    """op(X) (X, or X^T when trans) as an MX8 matrix: e4m3 values with an E8M0
+    scale per 32 of a row (pk_mx8_quantize_f32); a uint8 tensor"""
+    _f32(X)
+    ldx = _rowmajor(X, "X")
+    R, Kd = (X.shape[1], X.shape[0]) if trans else (X.shape[0], X.shape[1])
+    nbytes = mx8_bytes(R, Kd)
+    if out is None:
+        out = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=X.device)
+    if out.dtype != torch.uint8 or out.numel() < nbytes or not out.is_contiguous():
+        raise ValueError(f"mx8_quantize: out must be contiguous uint8 of at least {nbytes} bytes")
+    check("pk_mx8_quantize_f32", hip_lib().pk_mx8_quantize_f32(
+        R, Kd, _ptr(X), ldx, int(bool(trans)), _ptr(out), _stream()))
+    return out
+
+
+def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None):
+    """C = alpha * A8 . B8^T + beta * X (pk_gemm_mx8_f32): A8 [M, Kd] and B8
+    [N, Kd] MX8 matrices as mx8_quantize writes them; X a [M, N] tensor, a
+    [N] row added to every row, or C itself"""
+    _f32(C, X)
+    ldc = _rowmajor(C, "C")
+    if tuple(C.shape) != (M, N):
+        raise ValueError(f"gemm_mx8: C {tuple(C.shape)} is not {M}x{N}")
+    for name, Q, R in (("A8", A8, M), ("B8", B8, N)):
+        if Q.dtype != torch.uint8 or Q.numel() < mx8_bytes(R, Kd):
+            raise ValueError(f"gemm_mx8: {name} must be uint8 of at least {mx8_bytes(R, Kd)} bytes")
+    ldx = 0
+    if X is None and beta != 0.0:
+        X = C
+    if X is not None:
+        if X.dim() == 1:
+            if X.shape[0] != N:
+                raise ValueError("gemm_mx8: a row X must have N values")
+        else:
+            if tuple(X.shape) != (M, N):
+                raise ValueError("gemm_mx8: X must be [M, N] or [N]")
+            ldx = _rowmajor(X, "X")
+    check("pk_gemm_mx8_f32", hip_lib().pk_gemm_mx8_f32(
+        M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _stream()))
+    return C
+
+
 def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False, _name=None):
     """gemm with bf16 multiplies and fp32 accumulation (fp32 tensors in and out);
     ws: optional workspace for a K split (as gemm_ex); split: hi/lo operands,

@@ -180,3 +180,144 @@ def test_fp8q_refusals(dev):
             4, 100, X.data_ptr(), 100, 0, sc.data_ptr(), Q.data_ptr(), 100, None))
     with pytest.raises(ValueError):
         K.gemm_fp8q(4, 4, 100, Q[:, :64], Q, sc, C)
+
+
+# ---- MX8: e4m3 with an E8M0 scale per 32 values of a row -------------------
+
+def mx8_decode(Q, R, Kd):
+    """an MX8 buffer (pk_mx8_bytes layout) -> float64 [R, Kd], plus the scale
+    bytes [Rp, Kp / 32] and the raw values [Rp, Kp]"""
+    Rp, Kp = -(-R // 256) * 256, -(-Kd // 128) * 128
+    Q = np.asarray(Q)
+    vals = Q[:Rp * Kp].reshape(Rp, Kp)
+    S = Q[Rp * Kp:Rp * Kp + Rp * Kp // 32].reshape(Kp // 64, Rp, 2)
+    S = S.transpose(1, 0, 2).reshape(Rp, Kp // 32).astype(np.int64)
+    X = e4m3_decode(vals) * np.exp2(np.repeat(S - 127, 32, axis=1).astype(np.float64))
+    return X[:R, :Kd], S, vals
+
+
+def _mixed(R, Kd, seed):
+    """rows of uniform values whose 32-value blocks have magnitudes 2^-40..2^40"""
+    rng = np.random.default_rng(seed)
+    X = rng.uniform(-1, 1, (R, Kd)).astype(np.float32)
+    nb = -(-Kd // 32)
+    mag = np.exp2(rng.integers(-40, 41, (R, nb))).astype(np.float32)
+    return (X * np.repeat(mag, 32, axis=1)[:, :Kd]).astype(np.float32)
+
+
+@pytest.mark.parametrize("R,Kd", [(1, 1), (70, 130), (256, 128), (300, 1000)])
+def test_mx8_quantize_scales_and_values(dev, R, Kd):
+    X = _mixed(R, Kd, R + Kd)
+    X.ravel()[:3] = [448.0, -449.0, 0.0][:min(3, X.size)]
+    if R > 1:
+        X[1, :] = 0.0  # all-zero blocks: scale 2^0
+    Q = host(K.mx8_quantize(cu(X), False))
+    Xd, S, vals = mx8_decode(Q, R, Kd)
+    Rp, Kp = vals.shape
+    Xp = np.zeros((Rp, Kp), np.float64)
+    Xp[:R, :Kd] = X
+    amax = np.abs(Xp).reshape(Rp, Kp // 32, 32).max(axis=2)
+    e = S - 127
+    # the defining property: the smallest power of two that brings the block within 448
+    nz = amax > 0
+    assert np.all(amax[nz] * np.exp2(-e[nz].astype(np.float64)) <= 448.0)
+    assert np.all(amax[nz] * np.exp2(-(e[nz] - 1).astype(np.float64)) > 448.0)
+    assert np.all(e[~nz] == 0)
+    # each value is e4m3 of x * 2^-e (nearest even), byte for byte as torch encodes it
+    scaled = (Xp * np.exp2(-np.repeat(e, 32, axis=1).astype(np.float64))).astype(np.float32)
+    assert np.array_equal(e4m3_decode(vals), e4m3_round(scaled).astype(np.float64))
+    tq = torch.from_numpy(np.clip(scaled, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(vals, tq.numpy())
+    assert not vals[R:].any() and not vals[:, Kd:].any()
+    # each block keeps e4m3's relative precision, whatever its magnitude
+    big = np.abs(Xp[:R, :Kd]) >= np.repeat(amax, 32, axis=1)[:R, :Kd] / 8
+    assert np.all(np.abs(Xd - X)[big] <= np.abs(X)[big] * 2.0 ** -4 + 1e-300)
+
+
+@pytest.mark.parametrize("R,Kd", [(1, 5), (130, 70), (512, 256)])
+def test_mx8_quantize_transposed_read(dev, R, Kd):
+    X = _mixed(Kd, R, 9)  # op(X) = X^T is [R, Kd]
+    Qt = host(K.mx8_quantize(cu(X), True))
+    Qn = host(K.mx8_quantize(cu(np.ascontiguousarray(X.T)), False))
+    assert np.array_equal(Qt, Qn)
+
+
+def _mx_product(dev, X, Y, alpha=1.0, beta=0.0, Xadd=None, C0=None):
+    M, Kd = X.shape
+    N = Y.shape[1]
+    A8 = K.mx8_quantize(cu(X), False)
+    B8 = K.mx8_quantize(cu(Y), True)
+    C = torch.full((M, N), float("nan"), device=dev) if C0 is None else cu(C0)
+    K.gemm_mx8(M, N, Kd, A8, B8, C, alpha=alpha, beta=beta,
+               X=None if Xadd is None else cu(Xadd))
+    return host(C), host(A8), host(B8)
+
+
+@pytest.mark.parametrize("M,N,Kd", SHAPES)
+def test_mx8_gemm_integers_bitexact(dev, M, N, Kd):
+    """integers of magnitude <= 16 have at most 4 significant bits: exact in
+    e4m3 under any power-of-two block scale, so the product is exact"""
+    rng = np.random.default_rng(M * 5 + N + Kd)
+    X = rng.integers(-16, 17, (M, Kd)).astype(np.float32)
+    Y = rng.integers(-16, 17, (Kd, N)).astype(np.float32)
+    ref = (X.astype(np.float64) @ Y.astype(np.float64)).astype(np.float32)
+    C, _, _ = _mx_product(dev, X, Y)
+    assert np.array_equal(C, ref)
+    C, _, _ = _mx_product(dev, X, Y, alpha=-1.0, beta=1.0, C0=ref)
+    assert not np.any(C)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1024, 1024, 1024), (300, 257, 70), (512, 768, 2048)])
+def test_mx8_gemm_mixed_magnitudes(dev, M, N, Kd):
+    """blocks of magnitude 2^-40..2^40: the product equals the float64 product
+    of the decoded operands within fp32 summation error, where one tensor-wide
+    scale would flush all but the largest blocks to zero"""
+    X = _mixed(M, Kd, 3 * M + Kd)
+    Y = _mixed(N, Kd, 5 * N + Kd).T.copy()
+    C, A8, B8 = _mx_product(dev, X, Y)
+    Xd, _, _ = mx8_decode(A8, M, Kd)
+    Yd, _, _ = mx8_decode(B8, N, Kd)
+    assert gemm_err(C, Xd, Yd.T) <= TOL
+    assert gemm_err(C, X, Y) < 2 ** -3
+
+
+def test_mx8_gemm_epilogue_adds_x(dev):
+    M, N, Kd = 300, 520, 200
+    X = O.uniform(M * Kd, 1).reshape(M, Kd)
+    Y = O.uniform(Kd * N, 2).reshape(Kd, N)
+    A8, B8 = K.mx8_quantize(cu(X), False), K.mx8_quantize(cu(Y), True)
+    P = torch.empty(M, N, device=dev)
+    K.gemm_mx8(M, N, Kd, A8, B8, P)
+    Pn = host(P)
+    R = O.uniform(M * N, 3).reshape(M, N)
+    b = O.uniform(N, 4)
+    for Xadd, want in ((R, 2.0 * Pn + 0.5 * R), (b, 2.0 * Pn + 0.5 * b[None, :])):
+        C = torch.full((M, N), float("nan"), device=dev)
+        K.gemm_mx8(M, N, Kd, A8, B8, C, alpha=2.0, beta=0.5, X=cu(Xadd))
+        got = host(C)
+        assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want))
+    C = cu(R)
+    K.gemm_mx8(M, N, Kd, A8, B8, C, beta=1.0)  # accumulate into C
+    assert np.max(np.abs(host(C) - (Pn + R))) <= 1e-6 * np.max(np.abs(Pn + R))
+    # beta 0: X is not read (NaN there stays out of C)
+    C = torch.empty(M, N, device=dev)
+    K.gemm_mx8(M, N, Kd, A8, B8, C, beta=0.0,
+               X=torch.full((M, N), float("nan"), device=dev))
+    assert np.array_equal(host(C), Pn)
+
+
+def test_mx8_refusals(dev):
+    from pico_amd import _lib
+
+    L = _lib.hip_lib()
+    Q = torch.zeros(K.mx8_bytes(256, 128) + 16, dtype=torch.uint8, device=dev)
+    C = torch.zeros(4, 4, device=dev)
+    X = torch.zeros(4, 100, device=dev)
+    assert L.pk_mx8_quantize_f32(4, 100, X.data_ptr(), 100, 0, Q.data_ptr() + 8, None) != 0
+    assert L.pk_mx8_quantize_f32(4, 100, X.data_ptr(), 99, 0, Q.data_ptr(), None) != 0
+    assert L.pk_gemm_mx8_f32(4, 4, 100, 1.0, Q.data_ptr() + 4, Q.data_ptr(), 0.0, None, 0,
+                             C.data_ptr(), 4, None) != 0
+    assert L.pk_gemm_mx8_f32(4, 4, 100, 1.0, Q.data_ptr(), Q.data_ptr(), 1.0, None, 0,
+                             C.data_ptr(), 4, None) != 0
+    assert L.pk_gemm_mx8_f32(4, 4, 100, 1.0, Q.data_ptr(), Q.data_ptr(), 0.0, None, 0,
+                             C.data_ptr(), 3, None) != 0
