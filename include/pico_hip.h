@@ -214,6 +214,19 @@ int pk_mx8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int t
 int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
                     float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
                     pk_stream_t stream);
+/* pk_gemm_mx8_f32 with a caller-provided device workspace: a product with
+ * too few tiles to fill the chip (a weight gradient: M, N of the order of
+ * d_model, K = tokens) splits K; the splits' sums go to the workspace as
+ * fp32 planes and a second kernel adds them in plane order (deterministic).
+ * pk_gemm_mx8_workspace returns the bytes the split needs (0: no split); a
+ * NULL or smaller workspace runs the product unsplit.  pk_gemm_mx8_plan
+ * reports the launch a shape gets with enough workspace: the C tile (256 x
+ * 256, 256 x 128, 128 x 256 or 128 x 128) and the number of K splits. */
+size_t pk_gemm_mx8_workspace(int64_t M, int64_t N, int64_t K);
+int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                       float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                       void* workspace, size_t workspace_bytes, pk_stream_t stream);
+int pk_gemm_mx8_plan(int64_t M, int64_t N, int64_t K, int* tile_m, int* tile_n, int* splits);
 
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and

@@ -38,6 +38,8 @@
 //  * Tile order as the fp32 kernel's: XCD-contiguous runs, GROUP_M tile-rows.
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "pk_common.h"
 
 namespace {
@@ -45,12 +47,10 @@ namespace {
 constexpr int NT = 256;
 constexpr int QB = 64;                        // k bytes per slice = bytes of an LDS row
 constexpr int QKPAD = 2 * QB;                 // K padding: an even number of slices
-constexpr int QT = 256;                       // rows of an operand tile (and C tile side)
-constexpr int QSTAGE = QT * QB;               // bytes of one operand's tile in one stage
 constexpr int QSTAGES = 4;
-constexpr int QLW = QSTAGE / 1024 / 4;        // 1 KB load instructions per wave per operand: 4
 constexpr int QGROUP_M = 8;
-constexpr int64_t kTileQ = 256;
+constexpr int64_t kTileQ = 256;               // row padding of the quantized operands
+constexpr int kMaxSplits = 16;
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -63,21 +63,29 @@ struct Fp8qParams {
     float* C;
     const float* X;       // C = alpha * product (+ beta * X); X == C accumulates
     const float* scales;  // per-tensor mode: device sA, sB (NULL: 1, 1)
+    float* P;             // K split: partial planes [splits][M][N], summed by fp8q_reduce_kernel
     int64_t M, N, lda, ldb, ldc, ldx;
-    int nslices;
+    int nslices;          // slices of one split (even); the last split takes what remains
+    int total_slices;     // slices of the whole K (even)
+    int splits;
     float alpha, beta;
     int tiles_m, tiles_n;
 };
 
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
 __device__ __forceinline__ int slot_of(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
 
-// the load instructions of one operand tile: lane l of instruction n fills
-// LDS slot l % 4 of row 16n + l / 4 (n = w + 4i), from the chunk that belongs there
+// the load instructions of an operand tile of ROWS rows: lane l of
+// instruction n fills LDS slot l % 4 of row 16n + l / 4 (n = w + 4i), from
+// the chunk that belongs there
+template <int ROWS>
 struct QLoad {
-    int voff[QLW];
+    static constexpr int N = ROWS / 64;  // per wave
+    int voff[N];
     __device__ __forceinline__ QLoad(int64_t ld, int w, int l) {
 #pragma unroll
-        for(int i = 0; i < QLW; ++i) {
+        for(int i = 0; i < N; ++i) {
             const int r = 16 * (w + 4 * i) + l / 4;
             voff[i] = r * (int)ld + 16 * slot_of(r, l % 4);  // slot_of is its own inverse
         }
@@ -86,11 +94,6 @@ struct QLoad {
                                               int w) const {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(tile + 1024 * (w + 4 * i)), 16, voff[i],
                                                  soff, 0, 0);
-    }
-    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, int soff, uint8_t* tile,
-                                          int w) const {
-#pragma unroll
-        for(int i = 0; i < QLW; ++i) issue_one(i, rs, soff, tile, w);
     }
 };
 
@@ -133,23 +136,32 @@ __device__ __forceinline__ void barrier_keep_loads() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// C tile TM x TN = (64 WM) x (64 WN): 2 x 2 waves of WM x WN blocks of 32 x 32.
 // MX: operands carry E8M0 scales per 32 k (one per lane's 32 bytes of an
 // MFMA operand), streamed into LDS beside the bytes and handed to the MFMA;
 // otherwise the scales are 2^0 and the tensor scales divide in the epilogue.
-template <bool MX>
-__global__ __launch_bounds__(NT, 1) void gemm_fp8q_kernel(Fp8qParams p) {
-    // a stage: each operand's 256 rows of 64 bytes, then (MX) its scales,
-    // [row][2 halves of the slice's k]
-    constexpr int OPB = QSTAGE + (MX ? QT * 2 : 0);
-    __shared__ __attribute__((aligned(16))) uint8_t lds[QSTAGES][2][OPB];
-    const int ntiles = p.tiles_m * p.tiles_n;
+// With splits > 1, workgroup b runs split b / tiles (nslices slices from
+// slice split * nslices) and writes its raw sums to plane `split` of P.
+template <bool MX, int WM, int WN>
+__global__ __launch_bounds__(NT, WM * WN <= 4 ? 2 : 1) void gemm_fp8q_kernel(Fp8qParams p) {
+    constexpr int TM = 64 * WM, TN = 64 * WN;
+    static_assert(TM % 128 == 0 && TN % 128 == 0, "scale loads cover 128 rows each");
+    constexpr int SCB = MX ? (TM + TN) * 2 : 0;  // scale bytes of a stage: [A rows | B rows][2]
+    constexpr int NSC = SCB / 256;                // scale load instructions of a stage (4 bytes a lane)
+    constexpr int STAGE = (TM + TN) * QB + SCB;
+    constexpr int OB = TM * QB, OS = (TM + TN) * QB;  // B's bytes and the scales in a stage
+    __shared__ __attribute__((aligned(16))) uint8_t lds[QSTAGES][STAGE];
+
+    const int ntiles = p.tiles_m * p.tiles_n, total = ntiles * p.splits;
     int bid = blockIdx.x;
-    if((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+    if((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+    const int split = bid / ntiles;
+    bid -= split * ntiles;
     const int group_span = QGROUP_M * p.tiles_n;
     const int first_m = (bid / group_span) * QGROUP_M;
     const int gm = min(p.tiles_m - first_m, QGROUP_M);
     const int local = bid % group_span;
-    const int64_t row0 = (int64_t)(first_m + local % gm) * QT, col0 = (int64_t)(local / gm) * QT;
+    const int64_t row0 = (int64_t)(first_m + local % gm) * TM, col0 = (int64_t)(local / gm) * TN;
 
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, lr = l & 31, lh = l >> 5;
@@ -158,96 +170,120 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8q_kernel(Fp8qParams p) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.A), (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.B), (short)0, 0x7fffffff, 0x00020000);
-    const QLoad la(p.lda, w, l), lb(p.ldb, w, l);
+    const QLoad<TM> la(p.lda, w, l);
+    const QLoad<TN> lb(p.ldb, w, l);
     const int sa = (int)(row0 * p.lda), sb = (int)(col0 * p.ldb);
-    // MX scales: wave w fetches 128 rows' (w & 1) of operand w >> 1, 256 bytes
-    // (4 per lane); the operand and half are wave-uniform
+    // this split's slices: nslices, or what remains for the last split (even,
+    // at least 2: the plan never leaves an empty split)
+    const int s0 = split * p.nslices, ns = min(p.nslices, p.total_slices - s0);
+    // MX scales: wave w fetches 128 rows (256 bytes, 4 a lane) of the stage's
+    // [A | B] scale rows: block min(w, NSC - 1), a repeat where there are fewer
+    // blocks than waves (the same bytes to the same place)
+    const int scb = min(w, (NSC > 0 ? NSC : 1) - 1);
+    const bool sc_b = scb * 128 >= TM;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(wm ? p.SB : p.SA), (short)0, 0x7fffffff, 0x00020000);
-    const int sc0 = (int)((wm ? col0 : row0) * 2 + (w & 1) * 256);
-    const int sc_stride = (int)(wm ? p.sstride_b : p.sstride_a);
-    const int ns = p.nslices;
+        const_cast<uint8_t*>(sc_b ? p.SB : p.SA), (short)0, 0x7fffffff, 0x00020000);
+    const int sc0 = (int)((sc_b ? col0 + scb * 128 - TM : row0 + scb * 128) * 2);
+    const int sc_stride = (int)(sc_b ? p.sstride_b : p.sstride_a);
     auto issue_scales = [&](int s, int st) {
         if constexpr(MX)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(&lds[st][wm][QSTAGE + (w & 1) * 256]), 4, 4 * l,
-                                                     sc0 + min(s, ns - 1) * sc_stride, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t*)(&lds[st][OS + scb * 256]), 4, 4 * l,
+                                                     sc0 + (s0 + min(s, ns - 1)) * sc_stride, 0, 0);
     };
-    // slice s into stage s % QSTAGES; past the last slice the last one is
-    // fetched again (into a stage nobody reads), which keeps every iteration's
-    // count of outstanding loads the same
+    // slice s of the split into stage s % QSTAGES; past its last slice the
+    // last one is fetched again (into a stage nobody reads), which keeps every
+    // iteration's count of outstanding loads the same
     auto issue = [&](int s) {
-        const int st = s % QSTAGES, k = min(s, ns - 1) * QB;
-        la.issue(ra, sa + k, lds[st][0], w);
-        lb.issue(rb, sb + k, lds[st][1], w);
+        const int st = s % QSTAGES, k = (s0 + min(s, ns - 1)) * QB;
+#pragma unroll
+        for(int i = 0; i < WM; ++i) la.issue_one(i, ra, sa + k, &lds[st][0], w);
+#pragma unroll
+        for(int i = 0; i < WN; ++i) lb.issue_one(i, rb, sb + k, &lds[st][OB], w);
         issue_scales(s, st);
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[WM][WN];
 #pragma unroll
-    for(int i = 0; i < 4; ++i)
+    for(int i = 0; i < WM; ++i)
 #pragma unroll
-        for(int j = 0; j < 4; ++j)
+        for(int j = 0; j < WN; ++j)
 #pragma unroll
             for(int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // this lane's scale of block i of an operand in stage st
-    auto scale_of = [&](int st, int op, int i) -> int {
-        if constexpr(MX)
-            return lds[st][op][QSTAGE + ((op ? wn : wm) * 128 + 32 * i + lr) * 2 + lh];
-        else
-            return 127;
+    // LDS rows of this lane's operand blocks within a stage
+    auto a_row = [&](int i) { return wm * (TM / 2) + 32 * i + lr; };
+    auto b_row = [&](int j) { return wn * (TN / 2) + 32 * j + lr; };
+    // this lane's scale of A block i / B block j in stage st
+    auto scale_a = [&](int st, int i) -> int {
+        if constexpr(MX) return lds[st][OS + a_row(i) * 2 + lh];
+        else return 127;
     };
-    auto read = [&](int s, i32x8 (&fa)[4], i32x8 (&fb)[4], int (&ca)[4], int (&cb)[4]) {
+    auto scale_b = [&](int st, int j) -> int {
+        if constexpr(MX) return lds[st][OS + (TM + b_row(j)) * 2 + lh];
+        else return 127;
+    };
+    auto read = [&](int s, i32x8 (&fa)[WM], i32x8 (&fb)[WN], int (&ca)[WM], int (&cb)[WN]) {
         const int st = s % QSTAGES;
 #pragma unroll
-        for(int i = 0; i < 4; ++i) {
-            fa[i] = frag(lds[st][0], wm * 128 + 32 * i + lr, lh);
-            ca[i] = scale_of(st, 0, i);
+        for(int i = 0; i < WM; ++i) {
+            fa[i] = frag(&lds[st][0], a_row(i), lh);
+            ca[i] = scale_a(st, i);
         }
 #pragma unroll
-        for(int j = 0; j < 4; ++j) {
-            fb[j] = frag(lds[st][1], wn * 128 + 32 * j + lr, lh);
-            cb[j] = scale_of(st, 1, j);
+        for(int j = 0; j < WN; ++j) {
+            fb[j] = frag(&lds[st][OB], b_row(j), lh);
+            cb[j] = scale_b(st, j);
         }
     };
-    constexpr int PER = 2 * QLW + (MX ? 1 : 0);  // loads of one slice, per wave
+    constexpr int NG = WM * WN;                 // MFMAs of a slice, per wave
+    constexpr int NR = 2 * (WM + WN);           // 128-bit fragment reads of a slice
+    constexpr int NS = MX ? WM + WN : 0;        // scale reads of a slice
+    constexpr int PER = WM + WN + (MX ? 1 : 0); // loads of a slice, per wave
     // slice s with its fragments in (fa, fb) and scales in (ca, cb): wait for
-    // slice s+1's loads and every wave's reads of slice s, then 16 groups,
-    // each one MFMA of slice s, one 128-bit LDS read of slice s+1's fragments
-    // into (ga, gb) (in the order the next slice's MFMAs use them: A0,
-    // B0..B3, A1..A3), in the first 8 one load refilling slice s's stage with
-    // slice s+QSTAGES, in the 9th its scales' load, and in the last 8 one read
-    // of slice s+1's scales.  The scheduling barriers keep that order: left
-    // alone, the compiler moves the next slice's wait above the last MFMAs.
-    auto step = [&](int s, i32x8 (&fa)[4], i32x8 (&fb)[4], int (&ca)[4], int (&cb)[4], i32x8 (&ga)[4],
-                    i32x8 (&gb)[4], int (&da)[4], int (&db)[4]) {
+    // slice s+1's loads and every wave's reads of slice s, then NG groups, each
+    // one MFMA of slice s and an even share of: the 128-bit LDS reads of slice
+    // s+1's fragments into (ga, gb) (in the order the next slice's MFMAs use
+    // them: A0, B0.., A1..), the loads refilling slice s's stage with slice
+    // s+QSTAGES, and the reads of slice s+1's scales.  The scheduling barriers
+    // keep that order: left alone, the compiler moves the next slice's wait
+    // above the last MFMAs.
+    auto step = [&](int s, i32x8 (&fa)[WM], i32x8 (&fb)[WN], int (&ca)[WM], int (&cb)[WN], i32x8 (&ga)[WM],
+                    i32x8 (&gb)[WN], int (&da)[WM], int (&db)[WN]) {
         __builtin_amdgcn_sched_barrier(0);
         wait_vm_lds<(QSTAGES - 2) * PER>();
         barrier_keep_loads();
         const int nx = (s + 1) % QSTAGES, fill = s % QSTAGES;
-        const int k = min(s + QSTAGES, ns - 1) * QB;
+        const int k = (s0 + min(s + QSTAGES, ns - 1)) * QB;
 #pragma unroll
-        for(int g = 0; g < 16; ++g) {
-            const int i = g >> 2, j = g & 3;
+        for(int g = 0; g < NG; ++g) {
+            const int i = g / WN, j = g % WN;
             acc[i][j] = mfma_fp8(fa[i], fb[j], acc[i][j], ca[i], cb[j]);
-            constexpr int order[8] = {0, 4, 5, 6, 7, 1, 2, 3};
-            const int f = order[g >> 1], h = g & 1;
-            if(f < 4) {
-                const i32x4 v = frag_half(lds[nx][0], wm * 128 + 32 * f + lr, lh, h);
-                if(h) ga[f].hi = v; else ga[f].lo = v;
-            } else {
-                const i32x4 v = frag_half(lds[nx][1], wn * 128 + 32 * (f - 4) + lr, lh, h);
-                if(h) gb[f - 4].hi = v; else gb[f - 4].lo = v;
+#pragma unroll
+            for(int r = g * NR / NG; r < (g + 1) * NR / NG; ++r) {
+                // fragment r / 2 in the order A0, B0..B(WN-1), A1..A(WM-1); half r % 2
+                const int f = r >> 1, h = r & 1;
+                const bool is_a = f == 0 || f > WN;
+                const int idx = f == 0 ? 0 : (f <= WN ? f - 1 : f - WN);
+                if(is_a) {
+                    const i32x4 v = frag_half(&lds[nx][0], a_row(idx), lh, h);
+                    if(h) ga[idx].hi = v; else ga[idx].lo = v;
+                } else {
+                    const i32x4 v = frag_half(&lds[nx][OB], b_row(idx), lh, h);
+                    if(h) gb[idx].hi = v; else gb[idx].lo = v;
+                }
             }
-            if(g < QLW)
-                la.issue_one(g, ra, sa + k, lds[fill][0], w);
-            else if(g < 2 * QLW)
-                lb.issue_one(g - QLW, rb, sb + k, lds[fill][1], w);
-            else if(g == 2 * QLW)
-                issue_scales(s + QSTAGES, fill);
-            if(g >= 8) {
-                const int q = g - 8;
-                if(q < 4) da[q] = scale_of(nx, 0, q); else db[q - 4] = scale_of(nx, 1, q - 4);
+#pragma unroll
+            for(int q = g * PER / NG; q < (g + 1) * PER / NG; ++q) {
+                if(q < WM)
+                    la.issue_one(q, ra, sa + k, &lds[fill][0], w);
+                else if(q < WM + WN)
+                    lb.issue_one(q - WM, rb, sb + k, &lds[fill][OB], w);
+                else
+                    issue_scales(s + QSTAGES, fill);
+            }
+#pragma unroll
+            for(int q = g * NS / NG; q < (g + 1) * NS / NG; ++q) {
+                if(q < WM) da[q] = scale_a(nx, q); else db[q - WM] = scale_b(nx, q - WM);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -256,45 +292,92 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8q_kernel(Fp8qParams p) {
     if(ns > 0) {
 #pragma unroll
         for(int s = 0; s < QSTAGES; ++s) issue(s);
-        i32x8 a0[4], b0[4], a1[4], b1[4];
-        int ca0[4], cb0[4], ca1[4], cb1[4];
+        i32x8 a0[WM], b0[WN], a1[WM], b1[WN];
+        // scales: MX reads them with every slice; otherwise they stay 2^0
+        int ca0[WM], cb0[WN], ca1[WM], cb1[WN];
+#pragma unroll
+        for(int i = 0; i < WM; ++i) ca0[i] = ca1[i] = 127;
+#pragma unroll
+        for(int j = 0; j < WN; ++j) cb0[j] = cb1[j] = 127;
         wait_vm_lds<(QSTAGES - 1) * PER>();
         barrier_keep_loads();
         read(0, a0, b0, ca0, cb0);
-        for(int s = 0; s < ns; s += 2) {  // ns is even: K is padded to 128 bytes
+        for(int s = 0; s < ns; s += 2) {  // ns is even: K is padded to 128 bytes, splits take pairs
             step(s, a0, b0, ca0, cb0, a1, b1, ca1, cb1);
             step(s + 1, a1, b1, ca1, cb1, a0, b0, ca0, cb0);
         }
         wait_vm_lds<0>();  // no load may land in LDS after the workgroup ends
     }
 
+    const int64_t rw = row0 + wm * (TM / 2) + 4 * lh, cw = col0 + wn * (TN / 2) + lr;
+    if(p.splits > 1) {  // raw sums into this split's plane of P (row stride N)
+        float* P = p.P + (int64_t)split * p.M * p.N;
+#pragma unroll
+        for(int i = 0; i < WM; ++i)
+#pragma unroll
+            for(int j = 0; j < WN; ++j) {
+                const int64_t col = cw + 32 * j;
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const int64_t row = rw + 32 * i + 8 * (r >> 2) + (r & 3);
+                    if(row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
     const float scale = MX || !p.scales ? p.alpha : p.alpha / (p.scales[0] * p.scales[1]);
-    const bool full = row0 + QT <= p.M && col0 + QT <= p.N;
+    const bool full = row0 + TM <= p.M && col0 + TN <= p.N;
     if(full && !p.X) {
 #pragma unroll
-        for(int i = 0; i < 4; ++i)
+        for(int i = 0; i < WM; ++i)
 #pragma unroll
-            for(int j = 0; j < 4; ++j) {
-                float* c = p.C + (row0 + wm * 128 + 32 * i + 4 * lh) * p.ldc + col0 + wn * 128 + 32 * j + lr;
+            for(int j = 0; j < WN; ++j) {
+                float* c = p.C + (rw + 32 * i) * p.ldc + cw + 32 * j;
 #pragma unroll
                 for(int r = 0; r < 16; ++r) c[(8 * (r >> 2) + (r & 3)) * p.ldc] = scale * acc[i][j][r];
             }
         return;
     }
 #pragma unroll
-    for(int i = 0; i < 4; ++i)
+    for(int i = 0; i < WM; ++i)
 #pragma unroll
-        for(int j = 0; j < 4; ++j) {
-            const int64_t col = col0 + wn * 128 + 32 * j + lr;
+        for(int j = 0; j < WN; ++j) {
+            const int64_t col = cw + 32 * j;
 #pragma unroll
             for(int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int64_t row = rw + 32 * i + 8 * (r >> 2) + (r & 3);
                 if(row >= p.M || col >= p.N) continue;
                 float v = scale * acc[i][j][r];
                 if(p.X) v += p.beta * p.X[row * p.ldx + col];
                 p.C[row * p.ldc + col] = v;
             }
         }
+}
+
+// every launch shape, instantiated here so that each gets its host stub
+template __global__ void gemm_fp8q_kernel<true, 4, 4>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<true, 4, 2>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<true, 2, 4>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<true, 2, 2>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<false, 4, 4>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<false, 4, 2>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<false, 2, 4>(Fp8qParams);
+template __global__ void gemm_fp8q_kernel<false, 2, 2>(Fp8qParams);
+
+// C = alpha * (P[0] + P[1] + ... in plane order) + beta * X: a split product's
+// planes summed in a fixed order, so the result does not depend on timing
+__global__ __launch_bounds__(NT) void fp8q_reduce_kernel(int64_t M, int64_t N, int splits, const float* __restrict__ P,
+                                                         float alpha, float beta, const float* X, int64_t ldx,
+                                                         float* C, int64_t ldc) {
+    const int64_t plane = M * N;
+    for(int64_t e = (int64_t)blockIdx.x * NT + threadIdx.x; e < plane; e += (int64_t)gridDim.x * NT) {
+        const int64_t row = e / N, col = e - row * N;
+        float v = P[e];
+        for(int s = 1; s < splits; ++s) v += P[s * plane + e];
+        v *= alpha;
+        if(X) v += beta * X[row * ldx + col];
+        C[row * ldc + col] = v;
+    }
 }
 
 // ---- quantization: Q[r][k] = e4m3(scale * op(X)[r][k]), zero padding -------
@@ -314,59 +397,135 @@ __device__ __forceinline__ int mx_exponent(float amax) {
     return min(max(E - 9 + (m > 0.875f ? 1 : 0), -127), 127);
 }
 
-// one 64 x 64 block of op(X) through LDS: read along X's contiguous dimension,
-// written as 16 e4m3 bytes per thread along k.  MX: each 32-value half row
-// (threads t, t ^ 1) takes its own scale 2^-e; its E8M0 byte e + 127 goes to
-// S[slice][row][half] (slice = the block's 64 k, rows padded to Rp).
-template <bool MX>
-__global__ __launch_bounds__(NT) void fp8_quantize_kernel(int64_t R, int64_t K, const float* __restrict__ X,
-                                                          int64_t ldx, int trans, const float* scale_p,
-                                                          uint8_t* __restrict__ Q, int64_t ldq,
-                                                          uint8_t* __restrict__ S, int64_t Rp) {
-    __shared__ float tile[64][65];
-    const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
-    const int t = threadIdx.x;
+// four e4m3 bytes of four values (clamped to +-448, nearest even)
+__device__ __forceinline__ int e4m3x4(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(a), e4m3_clamp(b), 0, false);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(c), e4m3_clamp(d), lo, true);
+}
+
+// four consecutive values of row `row` of a row-major [rows, cols] matrix
+// from column c; zero outside it.  vec: row starts 16-byte aligned.
+__device__ __forceinline__ f32x4 load4(const float* __restrict__ X, int64_t ld, int64_t rows, int64_t cols,
+                                      int64_t row, int64_t c, bool vec) {
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if(row >= rows || c >= cols) return v;
+    const float* p = X + row * ld + c;
+    if(vec && c + 4 <= cols) return *reinterpret_cast<const f32x4*>(p);
 #pragma unroll
-    for(int i = 0; i < 16; ++i) {
+    for(int q = 0; q < 4; ++q)
+        if(c + q < cols) v[q] = p[q];
+    return v;
+}
+
+// the scale byte of MX block b (32 values from k = 32b) of row r, for the
+// [slice][row][2] layout
+__device__ __forceinline__ uint8_t* scale_slot(uint8_t* S, int64_t Rp, int64_t r, int64_t b) {
+    return S + (b >> 1) * Rp * 2 + r * 2 + (b & 1);
+}
+
+// op(X) = X (rows contiguous): a wave covers 256 values of a row, 4 per
+// lane (one 1 KB load), 8 lanes per MX block (the block's largest magnitude
+// by 3 exchanges), 4 rows per wave in flight; a block of 4 waves covers 16
+// rows.  Writes every byte of [Rp, Kp] and every scale.
+template <bool MX>
+__global__ __launch_bounds__(NT) void quantize_rows_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                           int64_t ldx, bool vec, const float* scale_p,
+                                                           uint8_t* __restrict__ Q, int64_t ldq, int64_t Kp,
+                                                           uint8_t* __restrict__ S, int64_t Rp) {
+    constexpr int RW = 4;  // rows per wave
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int64_t k = (int64_t)blockIdx.x * 256 + 4 * l;
+    const int64_t r0 = ((int64_t)blockIdx.y * 4 + w) * RW;
+    f32x4 v[RW];
+#pragma unroll
+    for(int i = 0; i < RW; ++i) v[i] = load4(X, ldx, R, K, r0 + i, k, vec);
+    const float tscale = MX ? 1.0f : *scale_p;
+#pragma unroll
+    for(int i = 0; i < RW; ++i) {
+        const int64_t r = r0 + i;
+        int e = 0;
+        if constexpr(MX) {
+            float amax = fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3])));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+            e = mx_exponent(amax);
+        }
+        if(r >= Rp || k >= Kp) continue;
+        int q;
+        if constexpr(MX)
+            q = e4m3x4(ldexpf(v[i][0], -e), ldexpf(v[i][1], -e), ldexpf(v[i][2], -e), ldexpf(v[i][3], -e));
+        else
+            q = e4m3x4(v[i][0] * tscale, v[i][1] * tscale, v[i][2] * tscale, v[i][3] * tscale);
+        *reinterpret_cast<int*>(Q + r * ldq + k) = q;
+        if constexpr(MX)
+            if((l & 7) == 0) *scale_slot(S, Rp, r, k >> 5) = (uint8_t)(e + 127);
+    }
+}
+
+// op(X) = X^T (X [K, R], rows of op(X) are X's columns): a block stages a
+// 64 (k) x 128 (r) tile through LDS -- read as 16-byte pieces along X's
+// rows, written transposed -- and then each thread takes one MX block: 32
+// consecutive k of one r (tile row), 32 output bytes and its scale.
+template <bool MX>
+__global__ __launch_bounds__(NT) void quantize_cols_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                           int64_t ldx, bool vec, const float* scale_p,
+                                                           uint8_t* __restrict__ Q, int64_t ldq,
+                                                           uint8_t* __restrict__ S, int64_t Rp) {
+    __shared__ float tile[128][65];
+    const int t = threadIdx.x;
+    const int64_t k0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 128;
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
         const int idx = t + NT * i;
-        const int a = idx / 64, b = idx % 64;  // a: slow, b: fast (contiguous in X)
-        const int rr = trans ? b : a, kk = trans ? a : b;
-        const int64_t r = r0 + rr, k = k0 + kk;
-        float v = 0.0f;
-        if(r < R && k < K) v = trans ? X[k * ldx + r] : X[r * ldx + k];
-        tile[rr][kk] = v;
+        const int kk = idx >> 5, rq = (idx & 31) * 4;
+        const f32x4 v = load4(X, ldx, K, R, k0 + kk, r0 + rq, vec);
+#pragma unroll
+        for(int c = 0; c < 4; ++c) tile[rq + c][kk] = v[c];
     }
     __syncthreads();
-    const int rr = t / 4, kq = (t % 4) * 16;
-    float v[16];
+    const int rr = t >> 1, half = t & 1;
+    const int64_t r = r0 + rr;
+    if(r >= Rp) return;
+    float v[32];
 #pragma unroll
-    for(int q = 0; q < 16; ++q) v[q] = tile[rr][kq + q];
+    for(int q = 0; q < 32; ++q) v[q] = tile[rr][32 * half + q];
     int e = 0;
+    float sc = 1.0f;
     if constexpr(MX) {
         float amax = 0.0f;
 #pragma unroll
-        for(int q = 0; q < 16; ++q) amax = fmaxf(amax, fabsf(v[q]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        for(int q = 0; q < 32; ++q) amax = fmaxf(amax, fabsf(v[q]));
         e = mx_exponent(amax);
-#pragma unroll
-        for(int q = 0; q < 16; ++q) v[q] = ldexpf(v[q], -e);
-        if((t & 1) == 0) S[(int64_t)blockIdx.x * Rp * 2 + (r0 + rr) * 2 + ((t >> 1) & 1)] = (uint8_t)(e + 127);
+        *scale_slot(S, Rp, r, (k0 >> 5) + half) = (uint8_t)(e + 127);
     } else {
-        const float scale = *scale_p;
-#pragma unroll
-        for(int q = 0; q < 16; ++q) v[q] *= scale;
+        sc = *scale_p;
     }
-    i32x4 out;
+    i32x4 o[2];
 #pragma unroll
-    for(int q = 0; q < 4; ++q) {
-        int x = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(v[4 * q]), e4m3_clamp(v[4 * q + 1]), 0, false);
-        x = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(v[4 * q + 2]), e4m3_clamp(v[4 * q + 3]), x, true);
-        out[q] = x;
+    for(int q = 0; q < 8; ++q) {
+        const float* p = &v[4 * q];
+        o[q >> 2][q & 3] = MX ? e4m3x4(ldexpf(p[0], -e), ldexpf(p[1], -e), ldexpf(p[2], -e), ldexpf(p[3], -e))
+                              : e4m3x4(p[0] * sc, p[1] * sc, p[2] * sc, p[3] * sc);
     }
-    *reinterpret_cast<i32x4*>(Q + (r0 + rr) * ldq + k0 + kq) = out;
+    i32x4* dst = reinterpret_cast<i32x4*>(Q + r * ldq + k0 + 32 * half);
+    dst[0] = o[0];
+    dst[1] = o[1];
 }
 
-int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+// launch: every byte of [Rp, Kp] (row stride ldq) and, MX, every scale
+template <bool MX>
+void launch_quantize(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, const float* scale,
+                     uint8_t* Q, int64_t ldq, uint8_t* S, hipStream_t st) {
+    const int64_t Rp = round_up(R, kTileQ), Kp = round_up(K, QKPAD);
+    const bool vec = ldx % 4 == 0 && pk::aligned16(X);
+    if(trans)
+        quantize_cols_kernel<MX><<<dim3((unsigned)(Kp / 64), (unsigned)(Rp / 128)), NT, 0, st>>>(
+            R, K, X, ldx, vec, scale, Q, ldq, S, Rp);
+    else
+        quantize_rows_kernel<MX><<<dim3((unsigned)((Kp + 255) / 256), (unsigned)(Rp / 16)), NT, 0, st>>>(
+            R, K, X, ldx, vec, scale, Q, ldq, Kp, S, Rp);
+}
 
 }  // namespace
 
@@ -391,16 +550,61 @@ extern "C" int pk_fp8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t
                         "Q 16-byte aligned");
     const int64_t Rp = round_up(R, kTileQ), Kp = round_up(K, QKPAD);
     if(Rp / 64 > 65535 || Kp / 64 > INT32_MAX) return pk::fail("pk_fp8_quantize_f32: too large");
-    fp8_quantize_kernel<false><<<dim3((unsigned)(Kp / 64), (unsigned)(Rp / 64)), NT, 0, pk::as_stream(stream)>>>(
-        R, K, X, ldx, trans, scale, Q, ldq, nullptr, Rp);
+    (void)Kp;
+    launch_quantize<false>(R, K, X, ldx, trans, scale, Q, ldq, nullptr, pk::as_stream(stream));
     return pk::launch_status("pk_fp8_quantize_f32");
 }
 
 namespace {
 
-// launch checks shared by both products; fills the shapes of p
+// A launch plan: the tile (WM x WN blocks a wave) and the K split, from a
+// timing model fitted (least squares in log time) to graph-replayed launches
+// of every tile and split on MI355X over the products of a transformer step
+// and square products: each CU runs its share of the workgroups' slices at
+// the tile's cost per slice (two 128 x 128 workgroups share a CU at 0.8 of
+// the cost each), plus a fixed cost per round of workgroups, plus C's bytes
+// to HBM; a split adds its partial planes and the reduction launch.  On those
+// products the plan's pick ran within 13 % of the best tile and split.
+struct MxPlan {
+    int wm, wn, splits, per;  // per: slices of one split
+};
+
+constexpr int64_t kCUs = 256;  // MI355X
+
+MxPlan mx8_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
+    const int64_t ns = round_up(K > 0 ? K : 1, QKPAD) / QB;
+    struct Cand {
+        int wm, wn, slots;  // slots: workgroups a CU holds
+        double slice_us;    // per slice of one workgroup
+    };
+    const Cand cands[] = {{4, 4, 1, 0.80}, {4, 2, 1, 0.45}, {2, 4, 1, 0.45}, {2, 2, 2, 0.35}};
+    const double hbm = 6.0e12, round_us = 1.0, launch_us = 6.0, shared = 0.8;
+    MxPlan best{4, 4, 1, (int)ns};
+    double best_t = 1e30;
+    for(const Cand& c : cands) {
+        const int64_t tiles = ((M + 64 * c.wm - 1) / (64 * c.wm)) * ((N + 64 * c.wn - 1) / (64 * c.wn));
+        for(int S = 1; S <= (allow_split ? kMaxSplits : 1); ++S) {
+            const int64_t per = round_up((ns + S - 1) / S, 2);
+            const int64_t splits = (ns + per - 1) / per;
+            if(splits != S || (S > 1 && per < 4)) continue;
+            const int64_t wgs = tiles * splits;
+            const int64_t per_cu = (wgs + kCUs - 1) / kCUs;
+            const int64_t rounds = (wgs + kCUs * c.slots - 1) / (kCUs * c.slots);
+            double t = per_cu * per * c.slice_us * (c.slots > 1 && wgs > kCUs ? shared : 1.0) +
+                       rounds * round_us + (double)M * N * 4 / hbm * 1e6;
+            if(splits > 1) t += (splits + 1.0) * M * N * 4 / hbm * 1e6 + launch_us;
+            if(t < best_t) {
+                best_t = t;
+                best = MxPlan{c.wm, c.wn, (int)splits, (int)per};
+            }
+        }
+    }
+    return best;
+}
+
+// launch checks shared by both products; fills the shapes of p for a plan
 int fp8q_shapes(const char* name, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, const void* A,
-                const void* B, float* C, int64_t ldc, Fp8qParams& p) {
+                const void* B, float* C, int64_t ldc, const MxPlan& plan, Fp8qParams& p) {
     if(M < 0 || N < 0 || K < 0) return pk::fail("%s: negative size", name);
     if(!C || (K > 0 && (!A || !B))) return pk::fail("%s: NULL pointer", name);
     if(ldc < N) return pk::fail("%s: ldc < N", name);
@@ -410,7 +614,8 @@ int fp8q_shapes(const char* name, int64_t M, int64_t N, int64_t K, int64_t lda, 
                         "multiples of 16, 16-byte aligned", name);
     if(Mp * lda > INT32_MAX || Np * ldb > INT32_MAX)
         return pk::fail("%s: an operand spans 2^31 bytes or more", name);
-    if((Mp / kTileQ) * (Np / kTileQ) > INT32_MAX) return pk::fail("%s: too many tiles", name);
+    const int64_t tm = (M + 64 * plan.wm - 1) / (64 * plan.wm), tn = (N + 64 * plan.wn - 1) / (64 * plan.wn);
+    if(tm * tn * plan.splits > INT32_MAX) return pk::fail("%s: too many tiles", name);
     p = Fp8qParams{};
     p.A = static_cast<const uint8_t*>(A);
     p.B = static_cast<const uint8_t*>(B);
@@ -420,10 +625,37 @@ int fp8q_shapes(const char* name, int64_t M, int64_t N, int64_t K, int64_t lda, 
     p.lda = lda;
     p.ldb = ldb;
     p.ldc = ldc;
-    p.nslices = K > 0 ? (int)(Kp / QB) : 0;
-    p.tiles_m = (int)(Mp / kTileQ);
-    p.tiles_n = (int)(Np / kTileQ);
+    p.nslices = K > 0 ? plan.per : 0;
+    p.total_slices = K > 0 ? (int)(Kp / QB) : 0;
+    p.splits = K > 0 ? plan.splits : 1;
+    // every split in range and none empty: (splits - 1) * per < total <= splits * per
+    if(K > 0 && (plan.per % 2 || (int64_t)(plan.splits - 1) * plan.per >= p.total_slices ||
+                 (int64_t)plan.splits * plan.per < p.total_slices))
+        return pk::fail("%s: inconsistent K split (%d x %d slices for %d)", name, plan.splits, plan.per,
+                        p.total_slices);
+    p.tiles_m = (int)tm;
+    p.tiles_n = (int)tn;
     return PK_OK;
+}
+
+void launch_fp8q(bool mx, const MxPlan& plan, const Fp8qParams& p, hipStream_t st) {
+    const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
+    const int shape = plan.wm == 4 ? (plan.wn == 4 ? 0 : 1) : (plan.wn == 4 ? 2 : 3);
+    if(mx) {
+        switch(shape) {
+            case 0: gemm_fp8q_kernel<true, 4, 4><<<grid, NT, 0, st>>>(p); break;
+            case 1: gemm_fp8q_kernel<true, 4, 2><<<grid, NT, 0, st>>>(p); break;
+            case 2: gemm_fp8q_kernel<true, 2, 4><<<grid, NT, 0, st>>>(p); break;
+            default: gemm_fp8q_kernel<true, 2, 2><<<grid, NT, 0, st>>>(p); break;
+        }
+    } else {
+        switch(shape) {
+            case 0: gemm_fp8q_kernel<false, 4, 4><<<grid, NT, 0, st>>>(p); break;
+            case 1: gemm_fp8q_kernel<false, 4, 2><<<grid, NT, 0, st>>>(p); break;
+            case 2: gemm_fp8q_kernel<false, 2, 4><<<grid, NT, 0, st>>>(p); break;
+            default: gemm_fp8q_kernel<false, 2, 2><<<grid, NT, 0, st>>>(p); break;
+        }
+    }
 }
 
 }  // namespace
@@ -432,15 +664,16 @@ extern "C" int pk_gemm_fp8q_f32(int64_t M, int64_t N, int64_t K, float alpha, co
                                 int64_t lda, const uint8_t* B, int64_t ldb, const float* scales,
                                 float beta, float* C, int64_t ldc, pk_stream_t stream) {
     if(M > 0 && N > 0 && !scales) return pk::fail("pk_gemm_fp8q_f32: NULL scales");
+    const MxPlan plan = mx8_plan(M, N, K, false);
     Fp8qParams p;
-    if(int st = fp8q_shapes("pk_gemm_fp8q_f32", M, N, K, lda, ldb, A, B, C, ldc, p)) return st;
+    if(int st = fp8q_shapes("pk_gemm_fp8q_f32", M, N, K, lda, ldb, A, B, C, ldc, plan, p)) return st;
     if(M == 0 || N == 0) return PK_OK;
     p.scales = scales;
     p.alpha = alpha;
     p.beta = beta;
     p.X = beta != 0.0f ? C : nullptr;
     p.ldx = ldc;
-    gemm_fp8q_kernel<false><<<(unsigned)(p.tiles_m * p.tiles_n), NT, 0, pk::as_stream(stream)>>>(p);
+    launch_fp8q(false, plan, p, pk::as_stream(stream));
     return pk::launch_status("pk_gemm_fp8q_f32");
 }
 
@@ -464,17 +697,34 @@ extern "C" int pk_mx8_quantize_f32(int64_t R, int64_t K, const float* X, int64_t
     const int64_t Rp = round_up(R, kTileQ), Kp = round_up(K, QKPAD);
     if(Rp / 64 > 65535 || Kp / 64 > INT32_MAX) return pk::fail("pk_mx8_quantize_f32: too large");
     uint8_t* q = static_cast<uint8_t*>(Q);
-    fp8_quantize_kernel<true><<<dim3((unsigned)(Kp / 64), (unsigned)(Rp / 64)), NT, 0, pk::as_stream(stream)>>>(
-        R, K, X, ldx, trans, nullptr, q, Kp, q + Rp * Kp, Rp);
+    launch_quantize<true>(R, K, X, ldx, trans, nullptr, q, Kp, q + Rp * Kp, pk::as_stream(stream));
     return pk::launch_status("pk_mx8_quantize_f32");
 }
 
-extern "C" int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
-                               float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
-                               pk_stream_t stream) {
+extern "C" int pk_gemm_mx8_plan(int64_t M, int64_t N, int64_t K, int* tile_m, int* tile_n, int* splits) {
+    if(M < 0 || N < 0 || K < 0) return pk::fail("pk_gemm_mx8_plan: negative size");
+    const MxPlan plan = mx8_plan(M, N, K, true);
+    if(tile_m) *tile_m = 64 * plan.wm;
+    if(tile_n) *tile_n = 64 * plan.wn;
+    if(splits) *splits = K > 0 ? plan.splits : 1;
+    return PK_OK;
+}
+
+extern "C" size_t pk_gemm_mx8_workspace(int64_t M, int64_t N, int64_t K) {
+    if(M <= 0 || N <= 0 || K <= 0) return 0;
+    const MxPlan plan = mx8_plan(M, N, K, true);
+    return plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+}
+
+extern "C" int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                                  float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                                  void* workspace, size_t workspace_bytes, pk_stream_t stream) {
     const int64_t Kp = round_up(K > 0 ? K : 1, QKPAD), Mp = round_up(M, kTileQ), Np = round_up(N, kTileQ);
+    MxPlan plan = mx8_plan(M, N, K, true);
+    if(plan.splits > 1 && (!workspace || workspace_bytes < (size_t)plan.splits * M * N * sizeof(float)))
+        plan = mx8_plan(M, N, K, false);
     Fp8qParams p;
-    if(int st = fp8q_shapes("pk_gemm_mx8_f32", M, N, K, Kp, Kp, A, B, C, ldc, p)) return st;
+    if(int st = fp8q_shapes("pk_gemm_mx8_f32", M, N, K, Kp, Kp, A, B, C, ldc, plan, p)) return st;
     if(M == 0 || N == 0) return PK_OK;
     if(beta != 0.0f && !X) return pk::fail("pk_gemm_mx8_f32: beta != 0 needs X");
     if(beta != 0.0f && ldx != 0 && ldx < N) return pk::fail("pk_gemm_mx8_f32: ldx < N");
@@ -488,6 +738,22 @@ extern "C" int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, con
     p.beta = beta;
     p.X = beta != 0.0f ? X : nullptr;
     p.ldx = ldx;
-    gemm_fp8q_kernel<true><<<(unsigned)(p.tiles_m * p.tiles_n), NT, 0, pk::as_stream(stream)>>>(p);
+    hipStream_t st = pk::as_stream(stream);
+    if(p.splits > 1) {
+        p.P = static_cast<float*>(workspace);
+        launch_fp8q(true, plan, p, st);
+        if(int e = pk::launch_status("pk_gemm_mx8_f32")) return e;
+        const int64_t plane = M * N;
+        const unsigned blocks = (unsigned)std::min<int64_t>((plane + NT - 1) / NT, 4 * kCUs * 8);
+        fp8q_reduce_kernel<<<blocks, NT, 0, st>>>(M, N, p.splits, p.P, alpha, beta, p.X, ldx, C, ldc);
+        return pk::launch_status("pk_gemm_mx8_f32 (reduce)");
+    }
+    launch_fp8q(true, plan, p, st);
     return pk::launch_status("pk_gemm_mx8_f32");
+}
+
+extern "C" int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                               float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                               pk_stream_t stream) {
+    return pk_gemm_mx8_ex_f32(M, N, K, alpha, A, B, beta, X, ldx, C, ldc, nullptr, 0, stream);
 }

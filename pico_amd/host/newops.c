@@ -357,9 +357,11 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     n->ival[AI_B] = B;
     n->ival[AI_H] = H;
     n->ival[AI_FLASH] = flash;
-    /* the matmul precision switch covers attention's products too; the
-     * backward uses the precision the forward ran in */
-    n->ival[AI_BF16] = flash && pico_get_matmul_precision() == PICO_MATMUL_BF16;
+    /* the matmul precision switch covers attention's products too (bf16
+     * products for PICO_MATMUL_BF16 and PICO_MATMUL_FP8); the backward uses
+     * the precision the forward ran in */
+    const int prec = pico_get_matmul_precision();
+    n->ival[AI_BF16] = flash && (prec == PICO_MATMUL_BF16 || prec == PICO_MATMUL_FP8);
     n->fval[0] = 1.0f / sqrtf((float)hd);
     int st = flash ? (n->ival[AI_BF16] ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
                          B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, out->data, lse,

@@ -177,6 +177,7 @@ int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m)
         return PK_EINVAL;
     }
     if(m->ld < 1) m->ld = 1;
+    m->persist = x->is_persistent && base == x->data;
     return 0;
 }
 
@@ -199,63 +200,26 @@ int pico_get_matmul_precision(void) { return g_matmul_precision; }
 
 /* products with too few output tiles (weight gradients) split K through a
  * workspace; see pk_gemm_ex_f32.  On the side stream (side != 0) the product
- * uses the side stream's own workspace. */
-/* fp8 products scale each operand by a power of two computed from its
- * largest magnitude (pk_fp8_scales_f32), into the first FP8_SCALE_BYTES of
- * the workspace, so small values (gradients) are not flushed to zero */
-#define FP8_SCALE_BYTES 256
-
-/* the stored shape of a matrix view of logical shape [rows, cols] */
-static void stored_dims(struct PkMat m, int64_t rows, int64_t cols, int64_t* r, int64_t* c) {
-    *r = m.t == 'N' ? rows : cols;
-    *c = m.t == 'N' ? cols : rows;
-}
-
-/* scales of the kernel's operands A [M, K] and B [K, N] (logical) */
-static int fp8_scales_for(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K,
-                          float* scales, pk_stream_t st) {
-    int64_t ra, ca, rb, cb;
-    stored_dims(A, M, K, &ra, &ca);
-    stored_dims(B, K, N, &rb, &cb);
-    return pk_fp8_scales_f32(ra, ca, A.p, A.ld, rb, cb, B.p, B.ld, scales, st);
-}
-
+ * uses the side stream's own workspace.  fp8 products go through MX8
+ * operands (mx8.c). */
 static int gemm_add_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
                        char tc, int64_t ldc, float beta, const float* X, int64_t ldx,
                        pk_stream_t st, int side) {
-    const int fp8 = g_matmul_precision == PICO_MATMUL_FP8;
-    size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
-    const size_t lead = fp8 ? FP8_SCALE_BYTES : 0;
-    /* split-K scratch is optional (the product runs unsplit without it); fp8's
-     * scales are not */
-    void* ws = NULL;
-    if(fp8)
-        ws = side ? pkh_side_workspace(ws_bytes + lead) : pkh_workspace(ws_bytes + lead);
-    else if(ws_bytes)
-        ws = side ? pkh_side_workspace_opt(ws_bytes) : pkh_workspace_opt(ws_bytes);
-    float* scales = NULL;
-    if(fp8) {
-        if(!ws) return PK_EINVAL;
-        scales = (float*)ws;
-        ws = (unsigned char*)ws + lead;
-    }
-    if(!ws) ws_bytes = 0;
-    if(tc == 'N') {
-        if(fp8) {
-            int st8 = fp8_scales_for(A, B, M, N, K, scales, st);
-            if(st8) return st8;
-        }
-        return pk_gemm_add_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, X, ldx, C, ldc,
-                               g_matmul_precision, scales, ws, ws_bytes, st);
-    }
     /* C stored transposed: produce C^T [N, M] = B^T . A^T (X is C itself here) */
-    struct PkMat BT = {B.p, flip(B.t), B.ld}, AT = {A.p, flip(A.t), A.ld};
-    if(fp8) {
-        int st8 = fp8_scales_for(BT, AT, N, M, K, scales, st);
-        if(st8) return st8;
-    }
+    struct PkMat BT = {B.p, flip(B.t), B.ld, B.persist}, AT = {A.p, flip(A.t), A.ld, A.persist};
+    if(g_matmul_precision == PICO_MATMUL_FP8)
+        return tc == 'N' ? pkh_mx8_product(A, B, M, N, K, C, ldc, beta, X, ldx, st, side)
+                         : pkh_mx8_product(BT, AT, N, M, K, C, ldc, beta, C, ldc, st, side);
+    size_t ws_bytes = pk_gemm_workspace_f32(M, N, K);
+    /* split-K scratch is optional (the product runs unsplit without it) */
+    void* ws = NULL;
+    if(ws_bytes) ws = side ? pkh_side_workspace_opt(ws_bytes) : pkh_workspace_opt(ws_bytes);
+    if(!ws) ws_bytes = 0;
+    if(tc == 'N')
+        return pk_gemm_add_f32(A.t, B.t, M, N, K, 1.0f, A.p, A.ld, B.p, B.ld, beta, X, ldx, C, ldc,
+                               g_matmul_precision, NULL, ws, ws_bytes, st);
     return pk_gemm_add_f32(BT.t, AT.t, N, M, K, 1.0f, B.p, B.ld, A.p, A.ld, beta, C, ldc, C, ldc,
-                           g_matmul_precision, scales, ws, ws_bytes, st);
+                           g_matmul_precision, NULL, ws, ws_bytes, st);
 }
 
 static int gemm_on(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
@@ -320,8 +284,8 @@ static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor
         pkh_status("pico_matmul_backward", PK_EINVAL);
         return;
     }
-    struct PkMat dC = {g, 'N', N > 0 ? N : 1};
-    struct PkMat AT = {va.p, flip(va.t), va.ld};
+    struct PkMat dC = {g, 'N', N > 0 ? N : 1, 0};
+    struct PkMat AT = {va.p, flip(va.t), va.ld, va.persist};
     struct PkNode* nb = pkh_node(b);
     const int to_side = nb && b->is_persistent && !a_param && va.p != b->data;
     const int db_first = to_side && !pkh_capturing();
@@ -359,8 +323,8 @@ static int da_plain(void* ctx) {
     struct DaPlain* c = (struct DaPlain*)ctx;
     struct PkMat va, vb;
     if(matmul_views(c->a, c->b, &va, &vb)) return PK_EINVAL;
-    struct PkMat dC = {c->g, 'N', c->N > 0 ? c->N : 1};
-    struct PkMat BT = {c->b->data, flip(vb.t), vb.ld};
+    struct PkMat dC = {c->g, 'N', c->N > 0 ? c->N : 1, 0};
+    struct PkMat BT = {c->b->data, flip(vb.t), vb.ld, vb.persist};
     int st = pkh_gemm(dC, BT, c->M, c->K, c->N, c->a->grad, va.t, va.ld, pkh_grad_flag(c->a));
     if(pkh_status("pico_matmul_backward", st)) return st;
     pkh_grad_mark(c->a);
@@ -631,19 +595,15 @@ struct PicoTensor* pico_matmul_gate_up(struct PicoTensor* a, struct PicoTensor* 
     float* h = NULL;
     /* the paired product never splits K and runs on the tiled kernels; where
      * the plain product would split K or run on the small-product kernels, the
-     * plain product runs, so both ways sum k in the same order */
+     * plain product runs, so both ways sum k in the same order.  fp8 products
+     * (MX8) run the plain product too. */
     if(va.t == 'N' && vw.t == 'N' && F % 32 == 0 && M > 0 && K > 0 && F > 0 &&
-       pk_gemm_workspace_f32(M, N, K) == 0 && !pk_gemm_small_product_f32(M, N, K)) {
+       g_matmul_precision != PICO_MATMUL_FP8 && pk_gemm_workspace_f32(M, N, K) == 0 &&
+       !pk_gemm_small_product_f32(M, N, K)) {
         h = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(M * F));
         if(!h) return NULL;
-        float* scales = NULL;
-        if(g_matmul_precision == PICO_MATMUL_FP8) {
-            scales = (float*)pkh_workspace(FP8_SCALE_BYTES);
-            int st8 = scales ? fp8_scales_for(va, vw, M, N, K, scales, pkh_stream()) : PK_EINVAL;
-            if(pkh_status("pico_matmul_gate_up", st8)) return NULL;
-        }
         int st = pk_gemm_swiglu_fwd_f32('N', 'N', M, N, K, 1.0f, va.p, va.ld, vw.p, vw.ld,
-                                        out->data, N, h, F, g_matmul_precision, scales,
+                                        out->data, N, h, F, g_matmul_precision, NULL,
                                         pkh_stream());
         if(pkh_status("pico_matmul_gate_up", st)) return NULL;
     } else if(pico_matmul_gpu(a, w, out)) {
@@ -687,11 +647,12 @@ struct DaSwiglu {
 static int da_swiglu(void* ctx) {
     struct DaSwiglu* c = (struct DaSwiglu*)ctx;
     const int flags = (pkh_grad_flag(c->gate) ? PK_ACCUM : 0) | (pkh_grad_flag(c->up) ? PK_ACCUM2 : 0);
-    float* scales = NULL;
-    struct PkMat g = {c->g, 'N', c->N > 0 ? c->N : 1}, wt = {c->w->data, 'T', c->w->strides[0]};
-    if(g_matmul_precision == PICO_MATMUL_FP32 && pk_gemm_small_product_f32(c->M, c->F, c->N)) {
-        /* a small product: dh into the arena, then SwiGLU's backward row
-         * kernel, as the composed ops compute it */
+    struct PkMat g = {c->g, 'N', c->N > 0 ? c->N : 1, 0},
+                 wt = {c->w->data, 'T', c->w->strides[0], c->w->is_persistent};
+    if((g_matmul_precision == PICO_MATMUL_FP32 && pk_gemm_small_product_f32(c->M, c->F, c->N)) ||
+       g_matmul_precision == PICO_MATMUL_FP8) {
+        /* a small product, or an fp8 one (MX8): dh into the arena, then
+         * SwiGLU's backward row kernel, as the composed ops compute it */
         struct Arena* arena = pkh_need_arena();
         float* dh = arena ? (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(c->M * c->F))
                           : NULL;
@@ -705,15 +666,10 @@ static int da_swiglu(void* ctx) {
         pkh_grad_mark(c->up);
         return 0;
     }
-    if(g_matmul_precision == PICO_MATMUL_FP8) {
-        scales = (float*)pkh_workspace(FP8_SCALE_BYTES);
-        int st8 = scales ? fp8_scales_for(g, wt, c->M, c->F, c->N, scales, pkh_stream()) : PK_EINVAL;
-        if(pkh_status("pico_swiglu_matmul_add_backward", st8)) return st8;
-    }
     /* dh = g [M, N] . w^T, w [F, N] row-major */
     int st = pk_gemm_swiglu_bwd_f32('N', 'T', c->M, c->F, c->N, 1.0f, g.p, g.ld, wt.p, wt.ld,
                                     c->gate->data, c->ld, c->up->data, c->ld, c->gate->grad,
-                                    c->up->grad, c->ld, flags, g_matmul_precision, scales,
+                                    c->up->grad, c->ld, flags, g_matmul_precision, NULL,
                                     pkh_stream());
     if(pkh_status("pico_swiglu_matmul_add_backward", st)) return st;
     pkh_grad_mark(c->gate);
@@ -729,7 +685,7 @@ static void swiglu_matmul_backward(struct PicoTensor* self) {
     if(!g) return;
     if(n->ival[SM_RESID] && residual_backward(self, self->parents[3], g)) return;
     const int64_t M = gate->shape[0], F = gate->shape[1], N = w->shape[1];
-    struct PkMat vh = {(const float*)n->saved[SM_H], 'N', F > 0 ? F : 1};
+    struct PkMat vh = {(const float*)n->saved[SM_H], 'N', F > 0 ? F : 1, 0};
     struct DaSwiglu ctx = {gate, up, w, g, M, F, N, n->ival[SM_LD]};
     matmul_backward_with(vh, 0, w, g, M, F, N, da_swiglu, &ctx);
 }
@@ -776,7 +732,8 @@ struct PicoTensor* pico_swiglu_matmul_add(struct PicoTensor* gate, struct PicoTe
         st = pk_swiglu_fwd_f32(M, F, gate->data, ld, up->data, ld, h, F, pkh_stream());
         if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;
     }
-    struct PkMat vh = {h, 'N', F > 0 ? F : 1}, vw = {w->data, 'N', w->strides[0]};
+    struct PkMat vh = {h, 'N', F > 0 ? F : 1, 0},
+                 vw = {w->data, 'N', w->strides[0], w->is_persistent};
     st = gemm_add_on(vh, vw, M, N, F, out->data, 'N', N > 0 ? N : 1, c ? 1.0f : 0.0f,
                      c ? c->data : NULL, c ? c->strides[0] : 0, pkh_stream(), 0);
     if(pkh_status("pico_swiglu_matmul_add", st)) return NULL;

@@ -80,6 +80,7 @@ void pico_optim_sgd_step(struct PicoOptimSGD* o) {
             k = 0;
         }
     }
+    pkh_params_changed();
 }
 
 void pico_optim_sgd_zero_grad(struct PicoOptimSGD* o) { zero_grads(&o->params); }
@@ -216,6 +217,7 @@ void pico_optim_adamw_step(struct PicoOptimAdamW* o) {
     pkh_status("pico_optim_adamw_step",
                pk_adamw_multi_f32(o->nchunks, o->table, o->lr, o->beta1, o->beta2, o->eps, o->wd,
                                   coef, pkh_stream()));
+    pkh_params_changed();
 }
 
 void pico_optim_adamw_zero_grad(struct PicoOptimAdamW* o) { zero_grads(&o->params); }

@@ -189,12 +189,22 @@ struct PkMat {
     const float* p;
     char t;
     int64_t ld;
+    int persist; /* p is a parameter's data, read as itself (its casts can be kept) */
 };
 int pkh_mat_view(const struct PicoTensor* x, const float* base, struct PkMat* m);
 /* C (+)= A . B for logical matrices A [M,K], B [K,N]; C is stored as the
  * view `c` describes (a transposed C is produced as C^T = B^T A^T) */
 int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C, char tc,
              int64_t ldc, int flags);
+
+/* fp8 products (mx8.c): C [M, N] (not transposed) = op(A).op(B) + beta X
+ * through MX8 operands; the side flag picks the side stream's workspace */
+int pkh_mx8_product(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
+                    int64_t ldc, float beta, const float* X, int64_t ldx, pk_stream_t st,
+                    int side);
+/* parameters may have changed: casts kept from before are redone at next use */
+void pkh_params_changed(void);
+void pkh_mx8_release(void);
 
 #pragma GCC visibility pop
 

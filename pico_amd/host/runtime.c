@@ -86,6 +86,7 @@ void pico_shutdown(void) {
     if(!g_ready) return;
     pkh_side_join();
     hipStreamSynchronize(g_own_stream);
+    pkh_mx8_release();
     if(g_ws) pkh_device_free(g_ws);
     g_ws = NULL;
     g_ws_bytes = 0;
@@ -333,6 +334,7 @@ int pkh_copy_h2d(void* dst, const void* src, size_t bytes) {
     if(pkh_init()) return -1;
     if(capture_refuses("a host-to-device copy")) return -1;
     if(bytes == 0) return 0;
+    pkh_params_changed(); /* the copy may write a parameter */
     pkh_side_join();
     hipStream_t st = (hipStream_t)pkh_stream();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
@@ -353,6 +355,7 @@ int pkh_copy_d2h(void* dst, const void* src, size_t bytes) {
 
 int pkh_copy_d2d_async(void* dst, const void* src, size_t bytes) {
     if(bytes == 0) return 0;
+    pkh_params_changed(); /* the copy may write a parameter */
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
                                   (hipStream_t)pkh_stream());
     return e == hipSuccess ? 0 : pkh_status("device-to-device copy", (int)e);
@@ -377,6 +380,8 @@ int pico_graph_begin(void) {
     if(e != hipSuccess) return pkh_status("pico_graph_begin", (int)e);
     g_capturing = 1;
     g_capture_failed = 0;
+    /* kept fp8 casts are redone inside the graph, so every replay recasts */
+    pkh_params_changed();
     return 0;
 }
 
@@ -390,6 +395,7 @@ struct PicoGraph* pico_graph_end(void) {
     hipGraph_t graph = NULL;
     hipError_t e = hipStreamEndCapture((hipStream_t)pkh_stream(), &graph);
     g_capturing = 0;
+    pkh_params_changed(); /* the casts captured were never run */
     if(e != hipSuccess || g_capture_failed) {
         if(graph) hipGraphDestroy(graph);
         if(e != hipSuccess) pkh_status("pico_graph_end", (int)e);
@@ -422,6 +428,7 @@ int pico_graph_launch(struct PicoGraph* g) {
         return PK_EINVAL;
     }
     hipError_t e = hipGraphLaunch(g->exec, (hipStream_t)pkh_stream());
+    pkh_params_changed(); /* a replayed step may update parameters */
     return e == hipSuccess ? 0 : pkh_status("pico_graph_launch", (int)e);
 }
 

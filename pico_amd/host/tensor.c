@@ -73,6 +73,7 @@ struct PicoTensor* pico_create_tensor(struct Arena* arena, int64_t* shape, uint8
 /* src/tensor.c:44-84: persistent, zeroed; data and grad share one allocation */
 struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
     if(pkh_init()) return NULL;
+    pkh_params_changed(); /* a new parameter may take a freed one's address */
     if(ndim < 1) {
         PKH_ERR("pico_param needs ndim >= 1\n");
         return NULL;
@@ -122,6 +123,7 @@ struct PicoTensor* pico_param(int64_t* shape, uint8_t ndim) {
 /* src/tensor.c:136-168 */
 void pico_free(struct PicoTensor* t) {
     if(!t || t->is_persistent == 0) return;
+    pkh_params_changed();
     struct PkNode* n = pkh_node(t);
     if(!n) {
         PKH_ERR("pico_free: not a tensor of this library!\n");

@@ -142,10 +142,23 @@ def mx8_quantize(X, trans, out=None):
     return out
 
 
-def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None):
+def mx8_plan(M, N, Kd):
+    """(tile rows, tile cols, K splits) of the launch a shape gets (pk_gemm_mx8_plan)"""
+    tm, tn, sp = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    check("pk_gemm_mx8_plan", hip_lib().pk_gemm_mx8_plan(M, N, Kd, ctypes.byref(tm),
+                                                         ctypes.byref(tn), ctypes.byref(sp)))
+    return tm.value, tn.value, sp.value
+
+
+def mx8_workspace(M, N, Kd):
+    return int(hip_lib().pk_gemm_mx8_workspace(M, N, Kd))
+
+
+def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None, ws=None):
     """C = alpha * A8 . B8^T + beta * X (pk_gemm_mx8_f32): A8 [M, Kd] and B8
     [N, Kd] MX8 matrices as mx8_quantize writes them; X a [M, N] tensor, a
-    [N] row added to every row, or C itself"""
+    [N] row added to every row, or C itself; ws: workspace for a K split
+    (pk_gemm_mx8_ex_f32)"""
     _f32(C, X)
     ldc = _rowmajor(C, "C")
     if tuple(C.shape) != (M, N):
@@ -164,8 +177,13 @@ def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None):
             if tuple(X.shape) != (M, N):
                 raise ValueError("gemm_mx8: X must be [M, N] or [N]")
             ldx = _rowmajor(X, "X")
-    check("pk_gemm_mx8_f32", hip_lib().pk_gemm_mx8_f32(
-        M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _stream()))
+    if ws is None:
+        check("pk_gemm_mx8_f32", hip_lib().pk_gemm_mx8_f32(
+            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _stream()))
+    else:
+        check("pk_gemm_mx8_ex_f32", hip_lib().pk_gemm_mx8_ex_f32(
+            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _ptr(ws),
+            ws.numel() * ws.element_size(), _stream()))
     return C
 
 

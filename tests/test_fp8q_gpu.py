@@ -321,3 +321,38 @@ def test_mx8_refusals(dev):
                              C.data_ptr(), 4, None) != 0
     assert L.pk_gemm_mx8_f32(4, 4, 100, 1.0, Q.data_ptr(), Q.data_ptr(), 0.0, None, 0,
                              C.data_ptr(), 3, None) != 0
+
+
+@pytest.mark.parametrize("M,N,Kd", [(768, 768, 8192), (2048, 768, 8192), (768, 2304, 8192),
+                                    (8192, 768, 32000), (300, 200, 5000)])
+def test_mx8_gemm_k_split(dev, M, N, Kd):
+    """a split K (the planes summed in order by a second kernel, the last split
+    taking the slices that remain): integers exact, and uniform operands equal
+    to the unsplit product within fp32 summation error"""
+    tm, tn, splits = K.mx8_plan(M, N, Kd)
+    assert (tm, tn) in ((256, 256), (256, 128), (128, 256), (128, 128))
+    ws = torch.empty(K.mx8_workspace(M, N, Kd) // 4 + 1, device=dev)
+    assert (splits > 1) == (K.mx8_workspace(M, N, Kd) > 0)
+    rng = np.random.default_rng(M + N + Kd)
+    X = rng.integers(-16, 17, (M, Kd)).astype(np.float32)
+    Y = rng.integers(-16, 17, (Kd, N)).astype(np.float32)
+    A8, B8 = K.mx8_quantize(cu(X), False), K.mx8_quantize(cu(Y), True)
+    C = torch.full((M, N), float("nan"), device=dev)
+    K.gemm_mx8(M, N, Kd, A8, B8, C, ws=ws)
+    ref = (X.astype(np.float64) @ Y.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(host(C), ref)
+    # alpha, beta and a row X through the split's reduction
+    b = O.uniform(N, 12)
+    K.gemm_mx8(M, N, Kd, A8, B8, C, alpha=0.5, beta=2.0, X=cu(b), ws=ws)
+    want = (0.5 * ref.astype(np.float64) + 2.0 * b[None, :].astype(np.float64))
+    assert np.max(np.abs(host(C) - want)) <= 1e-6 * np.max(np.abs(want))
+    Xu = O.uniform(M * Kd, 13).reshape(M, Kd)
+    Yu = O.uniform(Kd * N, 14).reshape(Kd, N)
+    A8, B8 = K.mx8_quantize(cu(Xu), False), K.mx8_quantize(cu(Yu), True)
+    Cs, Cu = torch.empty(M, N, device=dev), torch.empty(M, N, device=dev)
+    K.gemm_mx8(M, N, Kd, A8, B8, Cs, ws=ws)
+    K.gemm_mx8(M, N, Kd, A8, B8, Cu)  # no workspace: unsplit
+    Xd, _, _ = mx8_decode(host(A8), M, Kd)
+    Yd, _, _ = mx8_decode(host(B8), N, Kd)
+    assert gemm_err(host(Cs), Xd, Yd.T) <= TOL
+    assert gemm_err(host(Cs), Xd, Yd.T, C_ref=host(Cu).astype(np.float64)) <= TOL

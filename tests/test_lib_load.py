@@ -77,3 +77,21 @@ def test_oracle_library_loads():
     from oracle import oracle as O
 
     assert hasattr(O.lib(), "ora_matmul_avx")
+
+
+def test_mx8_launch_plans():
+    """the MX8 product's launch plan (host logic, no GPU): a tile of the four
+    shapes, a K split only where the tiles leave most of the chip idle, and
+    workspace for exactly the split's planes"""
+    from pico_amd import kernels as K
+
+    for M, N, Kd in [(4096, 4096, 4096), (8192, 768, 768), (8192, 768, 32000), (768, 768, 8192),
+                     (768, 32000, 8192), (1, 1, 1), (300, 257, 70), (2048, 768, 8192)]:
+        tm, tn, s = K.mx8_plan(M, N, Kd)
+        assert (tm, tn) in ((256, 256), (256, 128), (128, 256), (128, 128))
+        assert 1 <= s <= 16
+        tiles = -(-M // tm) * -(-N // tn)
+        if s > 1:
+            assert tiles * s <= 2 * 256 * 2 and tiles < 256
+        assert K.mx8_workspace(M, N, Kd) == (s * M * N * 4 if s > 1 else 0)
+    assert K.mx8_plan(4096, 4096, 4096)[2] == 1
