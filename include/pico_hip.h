@@ -460,6 +460,26 @@ int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int6
                                const float* o, const float* lse, const float* dout, float* dq,
                                float* dk, float* dv, void* workspace, size_t workspace_bytes,
                                int flags, pk_stream_t stream);
+/* The same fused attention with fp8 multiplies (no reference counterpart):
+ * OCP e4m3 operands on the 32x32x64 scaled matrix cores, fp32 accumulation.
+ * q, k, v and dout enter as e4m3(x * 2^-e) per tensor, e the smallest
+ * exponent that puts the tensor's largest magnitude (times scale*log2(e)
+ * for the operand that carries the softmax scale) within 448; the products
+ * undo 2^-e exactly.  P enters as e4m3(256 P), dS with a power of two per
+ * 32 rows of a 64-row block (its largest magnitude within 448).  The softmax
+ * statistics, exponentials and accumulators stay fp32.  amax: 4 floats of
+ * device memory; the forward writes max|q|, max|k|, max|v| into amax[0..2],
+ * the backward reads them (as the forward left them) and writes max|dout|
+ * into amax[3].  Everything else as in the fp32 entry points
+ * (PK_FLASH_RECOMPUTE is refused). */
+int pk_flash_attn_fwd_fp8_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                              float scale, const float* q, const float* k, const float* v,
+                              float* o, float* lse, float* amax, pk_stream_t stream);
+int pk_flash_attn_bwd_fp8_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                              float scale, const float* q, const float* k, const float* v,
+                              const float* o, const float* lse, const float* dout, float* dq,
+                              float* dk, float* dv, float* amax, void* workspace,
+                              size_t workspace_bytes, int flags, pk_stream_t stream);
 /* the two row kernels inside the chain, exposed for tests:
  * P = softmax(scale*S) over j <= i, zero for j > i, lse per row (P may alias S) */
 int pk_causal_softmax_fwd_f32(int64_t BH, int64_t T, float scale, const float* S, float* P,

@@ -24,6 +24,7 @@
 // exponentials are exp2.
 #include <math.h>
 
+#include <algorithm>
 #include <queue>
 #include <utility>
 #include <vector>
@@ -50,6 +51,7 @@ struct FlashParams {
     int64_t ld;          // row stride of q, k, v and dq, dk, dv (>= D)
     float scale;         // softmax scale (normally 1/8)
     int flags;
+    const float* amax;   // fp8 kernels: max|q|, max|k|, max|v|, max|dO|
 };
 
 // Which block (a forward or dQ query block, a dK/dV key block) each of a
@@ -1134,6 +1136,483 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
 }
 
+// ================================================================= fp8 products
+// The same three kernels with e4m3 multiplies on v_mfma_scale_f32_32x32x64_f8f6f4
+// (fp32 accumulation), which contracts 64 values of k per instruction: one
+// MFMA is a whole 64-dim head product (S = Q.K^T, dP = dO.V^T) or a whole
+// 64-row block of a contraction over keys or queries (O += P.V, dV += P^T.dO,
+// dK += dS^T.Q, dQ += dS.K) -- 2 or 4 instructions where the bf16 kernels
+// issue 8 or 16.
+//
+// Scaling.  q, k, v and dO enter with per-tensor powers of two: amax[] holds
+// max|q|, max|k|, max|v|, max|dO| (attn_amax_kernel); a tensor x is stored as
+// e4m3(x * 2^-e) with e the smallest exponent putting its largest (scaled)
+// value within 448, and the MFMA's E8M0 operand scale 127 + e undoes the
+// division exactly, for free.  P (in [0, 1]) enters as e4m3(256 P) with
+// scale 2^-8, keeping probabilities down to 2^-17 instead of flushing those
+// below e4m3's 2^-9.  dS has no range known in advance: each 32-row half of
+// a 64-row block gets its own power of two (OCP MX style), from the largest
+// magnitude the two lanes that hold it find between them.  The softmax
+// statistics, exponentials and accumulators stay fp32.
+//
+// Operand layout.  Lane l supplies 32 bytes; the MFMA takes bytes 0-15 of
+// every lane as k-block 0 and bytes 16-31 as k-block 1, each block scaled by
+// the E8M0 scale of lane l%32 (block 0) or l%32 + 32 (block 1).  A head-dim
+// contraction (row tiles, fragments) puts dims 16h..16h+15 in bytes 0-15 and
+// 32+16h.. in bytes 16-31 of lane half h: the same for both operands, so each
+// product pairs equal dims.  A contraction over the 64 rows of an
+// accumulator pair (s[0], s[1]: rows sub*32 + acc_row(r, h)) packs s[0] into
+// bytes 0-15 and s[1] into bytes 16-31, so k-block b is sub-block b; the
+// other operand is a transposed tile whose columns are permuted to match:
+// row position 32h + 16 sub + 4 (r / 4) + r % 4 holds row sub*32 +
+// acc_row(r, h), and lane half h reads its 32 bytes from position 32h.
+// Tiles have rows of LD8 = 80 bytes (16 of padding): the 8 lanes a 128-bit
+// read serves per cycle hit 8 disjoint sets of 4 banks.
+constexpr int LD8 = HD + 16;
+constexpr int TILE8 = BLK * LD8;  // bytes
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x16 mfma64(const i32x8& a, const i32x8& b, f32x16 c, int sa, int sb) {
+    // formats 0, 0: both operands OCP e4m3
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+// the smallest e with amax * 2^-e <= 448, held to [-126, 126]; 0 for 0 (and NaN)
+__device__ __forceinline__ int fp8_exp(float amax) {
+    if(!(amax > 0.0f)) return 0;
+    if(!(amax <= 3.4028235e38f)) return 126;
+    int E;
+    const float m = frexpf(amax, &E);
+    return min(max(E - 9 + (m > 0.875f ? 1 : 0), -126), 126);
+}
+
+// four e4m3 bytes, nearest even.  No clamp: every operand here is scaled
+// into e4m3's range by a power of two taken from its exact largest magnitude
+// (or is 256 P <= 256), so nothing exceeds 448.
+__device__ __forceinline__ int pack4_fp8(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// e4m3 of (x[0..15] * mul) as 4 dwords
+__device__ __forceinline__ i32x4 pack16_fp8(const float* x, float mul) {
+    i32x4 r;
+#pragma unroll
+    for(int q = 0; q < 4; ++q) r[q] = pack4_fp8(x[4 * q] * mul, x[4 * q + 1] * mul, x[4 * q + 2] * mul,
+                                                x[4 * q + 3] * mul);
+    return r;
+}
+
+// a lane's head-dim fragment of one row (see the layout note), times mul
+__device__ __forceinline__ i32x8 load_frag_fp8(const float* __restrict__ row, int h, float mul, bool ok) {
+    i32x8 f;
+    if(!ok) {
+#pragma unroll
+        for(int q = 0; q < 8; ++q) f[q] = 0;
+        return f;
+    }
+    float x[32];
+#pragma unroll
+    for(int c = 0; c < 4; ++c) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(row + 16 * h + 4 * c);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(row + 32 + 16 * h + 4 * c);
+#pragma unroll
+        for(int e = 0; e < 4; ++e) {
+            x[4 * c + e] = a[e];
+            x[16 + 4 * c + e] = b[e];
+        }
+    }
+    f.lo = pack16_fp8(x, mul);
+    f.hi = pack16_fp8(x + 16, mul);
+    return f;
+}
+
+// row-major tile: thread t's quad (rows 4*(t/16)+i, dims 4*(t%16)..+3) times mul
+__device__ __forceinline__ void put_rows8(uint8_t* t, const f32x4 (&x)[4], float mul) {
+    const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+#pragma unroll
+    for(int i = 0; i < 4; ++i)
+        *reinterpret_cast<int*>(t + (4 * rq + i) * LD8 + 4 * c4) =
+            pack4_fp8(x[i][0] * mul, x[i][1] * mul, x[i][2] * mul, x[i][3] * mul);
+}
+
+// transposed tile with the row permutation of the layout note: dim-major,
+// rows 4*(t/16)..+3 (one acc_row run of 4) at 4 consecutive positions
+__device__ __forceinline__ void put_cols8(uint8_t* t, const f32x4 (&x)[4], float mul) {
+    const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+    const int row = 4 * rq;  // sub = row/32, g = (row/8)%4, h = (row/4)%2
+    const int pos = 32 * ((row >> 2) & 1) + 16 * (row >> 5) + 4 * ((row >> 3) & 3);
+#pragma unroll
+    for(int c = 0; c < 4; ++c)
+        *reinterpret_cast<int*>(t + (4 * c4 + c) * LD8 + pos) =
+            pack4_fp8(x[0][c] * mul, x[1][c] * mul, x[2][c] * mul, x[3][c] * mul);
+}
+
+// a row tile's head-dim fragment (row r) / a transposed tile's 64-row fragment
+__device__ __forceinline__ i32x8 tile_frag_dims(const uint8_t* t, int r, int h) {
+    i32x8 f;
+    f.lo = *reinterpret_cast<const i32x4*>(t + r * LD8 + 16 * h);
+    f.hi = *reinterpret_cast<const i32x4*>(t + r * LD8 + 32 + 16 * h);
+    return f;
+}
+__device__ __forceinline__ i32x8 tile_frag_rows(const uint8_t* t, int r, int h) {
+    i32x8 f;
+    f.lo = *reinterpret_cast<const i32x4*>(t + r * LD8 + 32 * h);
+    f.hi = *reinterpret_cast<const i32x4*>(t + r * LD8 + 32 * h + 16);
+    return f;
+}
+
+// an accumulator pair (rows of two 32-row sub-blocks) as a B operand, times mul
+__device__ __forceinline__ i32x8 pack_pair(const f32x16 (&x)[2], float mul) {
+    float a[16], b[16];
+#pragma unroll
+    for(int r = 0; r < 16; ++r) {
+        a[r] = x[0][r];
+        b[r] = x[1][r];
+    }
+    i32x8 f;
+    f.lo = pack16_fp8(a, mul);
+    f.hi = pack16_fp8(b, mul);
+    return f;
+}
+
+// the same with a power of two per sub-block (k-block): the largest magnitude
+// of each sub-block over this lane and its partner (l ^ 32), which hold its
+// 32 rows between them; returns this lane's E8M0 scale (its half's block)
+__device__ __forceinline__ i32x8 pack_pair_mx(const f32x16 (&x)[2], int h, int& scale) {
+    float am[2];
+#pragma unroll
+    for(int sb = 0; sb < 2; ++sb) {
+        float a = 0.0f;
+#pragma unroll
+        for(int r = 0; r < 16; ++r) a = fmaxf(a, fabsf(x[sb][r]));
+        am[sb] = fmaxf(a, __shfl_xor(a, 32, 64));
+    }
+    const int e0 = fp8_exp(am[0]), e1 = fp8_exp(am[1]);
+    scale = 127 + (h ? e1 : e0);
+    float a[16], b[16];
+#pragma unroll
+    for(int r = 0; r < 16; ++r) {
+        a[r] = x[0][r];
+        b[r] = x[1][r];
+    }
+    i32x8 f;
+    f.lo = pack16_fp8(a, ldexpf(1.0f, -e0));
+    f.hi = pack16_fp8(b, ldexpf(1.0f, -e1));
+    return f;
+}
+
+// the tensors' exponents from amax[] (q times qmul, k times kmul)
+struct Fp8Exps {
+    int q, k, v, o;
+};
+__device__ __forceinline__ Fp8Exps fp8_exps(const float* amax, float qmul, float kmul) {
+    return Fp8Exps{fp8_exp(amax[0] * qmul), fp8_exp(amax[1] * kmul), fp8_exp(amax[2]), fp8_exp(amax[3])};
+}
+constexpr int kPScale = 8;  // P enters as 2^8 P
+
+// ------------------------------------------------------------- fp8 forward
+__global__ __launch_bounds__(256, 2) void flash_fwd_fp8(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t sK[2][TILE8];   // [key][d]
+    __shared__ __attribute__((aligned(16))) uint8_t sVt[2][TILE8];  // [d][key position]
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
+    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+    const float qmul = p.scale * kLog2e;
+    const Fp8Exps ex = fp8_exps(p.amax, qmul, 1.0f);
+    const float kmul = ldexpf(1.0f, -ex.k), vmul = ldexpf(1.0f, -ex.v);
+
+    const i32x8 qf = load_frag_fp8(Q + qi * p.ld, lh, qmul * ldexpf(1.0f, -ex.q), qi < p.T);
+    f32x16 o[2] = {zero16(), zero16()};
+    float m = -INFINITY, lsum = 0.0f;
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
+    f32x4 rk[4], rv[4];
+    fetch_quad(K, p.ld, 0, rk, p.T);
+    fetch_quad(V, p.ld, 0, rv, p.T);
+    put_rows8(sK[0], rk, kmul);
+    put_cols8(sVt[0], rv, vmul);
+    for(int j = 0; j < nkv; ++j) {
+        const int st = j & 1;
+        __syncthreads();
+        const bool more = j + 1 < nkv;
+        if(more) {
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk, p.T);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv, p.T);
+        }
+        const int64_t kv0 = (int64_t)j * BLK;
+        if(kv0 <= q0 + 31) {
+            f32x16 s[2];
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub)
+                s[sub] = mfma64(tile_frag_dims(sK[st], sub * 32 + lq, lh), qf, zero16(), 127 + ex.k,
+                                127 + ex.q);
+            if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
+                const int lim = (int)(qi - kv0) - 4 * lh;
+#pragma unroll
+                for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) s[sub][r] = -INFINITY;
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            float ls = 0.0f;
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    s[sub][r] = __builtin_amdgcn_exp2f(s[sub][r] - mn);
+                    ls += s[sub][r];
+                }
+            ls += __shfl_xor(ls, 32, 64);
+            lsum = lsum * alpha + ls;
+            m = mn;
+#pragma unroll
+            for(int r = 0; r < 16; ++r) {
+                o[0][r] *= alpha;
+                o[1][r] *= alpha;
+            }
+            const i32x8 pf = pack_pair(s, (float)(1 << kPScale));
+#pragma unroll
+            for(int cb = 0; cb < 2; ++cb)
+                o[cb] = mfma64(tile_frag_rows(sVt[st], cb * 32 + lq, lh), pf, o[cb], 127 + ex.v, 127 - kPScale);
+        }
+        if(more) {
+            put_rows8(sK[st ^ 1], rk, kmul);
+            put_cols8(sVt[st ^ 1], rv, vmul);
+        }
+    }
+    if(qi >= p.T) return;  // a padding row of the last block
+    store_rowT(p.out + obase + qi * p.D, o, lh, 1.0f / lsum, false);
+    if(lh == 0 && p.lse_out) p.lse_out[bh * p.T + qi] = (m + log2f(lsum)) * kLn2;
+}
+
+// -------------------------------------------------------- fp8 backward: dK, dV
+__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_fp8(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t sQ[2][TILE8];   // [q][d]
+    __shared__ __attribute__((aligned(16))) uint8_t sQt[2][TILE8];  // [d][q position]
+    __shared__ __attribute__((aligned(16))) uint8_t sO[2][TILE8];   // dO [q][d]
+    __shared__ __attribute__((aligned(16))) uint8_t sOt[2][TILE8];  // dO [d][q position]
+    __shared__ float sLD[2][2 * BLK];                               // L2, then D
+    const int64_t BH = p.B * p.H;
+    const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + obase;
+    const float* cst = p.dsum + bh * 2 * p.Tp;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
+    const float kscale = p.scale * kLog2e;
+    const Fp8Exps ex = fp8_exps(p.amax, 1.0f, kscale);
+    const float qmul = ldexpf(1.0f, -ex.q), omul = ldexpf(1.0f, -ex.o);
+
+    const i32x8 kf = load_frag_fp8(K + ki * p.ld, lh, kscale * ldexpf(1.0f, -ex.k), ki < p.T);
+    const i32x8 vf = load_frag_fp8(V + ki * p.ld, lh, ldexpf(1.0f, -ex.v), ki < p.T);
+    f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
+
+    const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.Tp / BLK);
+    f32x4 rq[4], ro[4];
+    float rc = 0.0f;
+    auto fetch = [&](int j) {
+        fetch_quad(Q, p.ld, (int64_t)j * BLK, rq, p.T);
+        fetch_quad(dO, p.D, (int64_t)j * BLK, ro, p.T);
+        if(threadIdx.x < 2 * BLK) rc = cst[(int64_t)j * 2 * BLK + threadIdx.x];
+    };
+    auto put = [&](int st) {
+        put_rows8(sQ[st], rq, qmul);
+        put_cols8(sQt[st], rq, qmul);
+        put_rows8(sO[st], ro, omul);
+        put_cols8(sOt[st], ro, omul);
+        if(threadIdx.x < 2 * BLK) sLD[st][threadIdx.x] = rc;
+    };
+    fetch(j0);
+    put(0);
+    for(int j = j0; j < nq; ++j) {
+        const int st = (j - j0) & 1;
+        __syncthreads();
+        const bool more = j + 1 < nq;
+        if(more) fetch(j + 1);
+        const int64_t qs = (int64_t)j * BLK;
+        if(qs + BLK - 1 >= k0) {
+            const float* tl = sLD[st];
+            const int lim = (int)(ki - qs) - 4 * lh;  // query row qr sees key ki when qr >= lim
+            const bool diag = qs < k0 + 32;           // some query of the block precedes a key
+            f32x16 sc[2], dp[2];
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
+                sc[sub] = mfma64(tile_frag_dims(sQ[st], sub * 32 + lq, lh), kf, zero16(), 127 + ex.q,
+                                 127 + ex.k);
+                dp[sub] = mfma64(tile_frag_dims(sO[st], sub * 32 + lq, lh), vf, zero16(), 127 + ex.o,
+                                 127 + ex.v);
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const int qr = sub * 32 + acc_row(r, lh);
+                    sc[sub][r] = __builtin_amdgcn_exp2f(sc[sub][r] - tl[qr]);
+                }
+                if(diag) {
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) < lim) sc[sub][r] = 0.0f;
+                }
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const int qr = sub * 32 + acc_row(r, lh);
+                    dp[sub][r] = sc[sub][r] * (dp[sub][r] - tl[BLK + qr]);
+                }
+            }
+            const i32x8 pf = pack_pair(sc, (float)(1 << kPScale));
+            int dss;
+            const i32x8 df = pack_pair_mx(dp, lh, dss);
+#pragma unroll
+            for(int cb = 0; cb < 2; ++cb) {
+                dv[cb] = mfma64(tile_frag_rows(sOt[st], cb * 32 + lq, lh), pf, dv[cb], 127 + ex.o,
+                                127 - kPScale);
+                dk[cb] = mfma64(tile_frag_rows(sQt[st], cb * 32 + lq, lh), df, dk[cb], 127 + ex.q, dss);
+            }
+        }
+        if(more) put(st ^ 1);
+    }
+    if(ki >= p.T) return;  // a padding row of the last block
+    store_rowT(p.dv + base + ki * p.ld, dv, lh, 1.0f, (p.flags & PK_ACCUM3) != 0);
+    store_rowT(p.dk + base + ki * p.ld, dk, lh, p.scale, (p.flags & PK_ACCUM2) != 0);
+}
+
+// ------------------------------------------------------------- fp8 backward: dQ
+__global__ __launch_bounds__(256, 2) void flash_bwd_dq_fp8(FlashParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t sK[2][TILE8];   // [key][d]
+    __shared__ __attribute__((aligned(16))) uint8_t sKt[2][TILE8];  // [d][key position]
+    __shared__ __attribute__((aligned(16))) uint8_t sV[2][TILE8];   // [key][d]
+    const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
+    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const int64_t base = b * p.T * p.ld + h * HD, obase = b * p.T * p.D + h * HD;
+    const float *Q = p.q + base, *K = p.k + base, *V = p.v + base, *dO = p.dout + obase;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
+    const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
+    const float qmul = p.scale * kLog2e;
+    const Fp8Exps ex = fp8_exps(p.amax, qmul, 1.0f);
+    const float kmul = ldexpf(1.0f, -ex.k), vmul = ldexpf(1.0f, -ex.v);
+
+    const i32x8 qf = load_frag_fp8(Q + qi * p.ld, lh, qmul * ldexpf(1.0f, -ex.q), qi < p.T);
+    const i32x8 of = load_frag_fp8(dO + qi * p.D, lh, ldexpf(1.0f, -ex.o), qi < p.T);
+    const float* cst = p.dsum + bh * 2 * p.Tp + (qi / BLK) * 2 * BLK + qi % BLK;
+    const float l2 = cst[0], dd = cst[BLK];
+    f32x16 dq[2] = {zero16(), zero16()};
+
+    const int nkv = (int)((qb * ROWS + ROWS) / BLK);
+    f32x4 rk[4], rv[4];
+    fetch_quad(K, p.ld, 0, rk, p.T);
+    fetch_quad(V, p.ld, 0, rv, p.T);
+    put_rows8(sK[0], rk, kmul);
+    put_cols8(sKt[0], rk, kmul);
+    put_rows8(sV[0], rv, vmul);
+    for(int j = 0; j < nkv; ++j) {
+        const int st = j & 1;
+        __syncthreads();
+        const bool more = j + 1 < nkv;
+        if(more) {
+            fetch_quad(K, p.ld, (int64_t)(j + 1) * BLK, rk, p.T);
+            fetch_quad(V, p.ld, (int64_t)(j + 1) * BLK, rv, p.T);
+        }
+        const int64_t kv0 = (int64_t)j * BLK;
+        if(kv0 <= q0 + 31) {
+            const int lim = (int)(qi - kv0) - 4 * lh;
+            f32x16 sc[2], dp[2];
+#pragma unroll
+            for(int sub = 0; sub < 2; ++sub) {
+                sc[sub] = mfma64(tile_frag_dims(sK[st], sub * 32 + lq, lh), qf, zero16(), 127 + ex.k,
+                                 127 + ex.q);
+                dp[sub] = mfma64(tile_frag_dims(sV[st], sub * 32 + lq, lh), of, zero16(), 127 + ex.v,
+                                 127 + ex.o);
+#pragma unroll
+                for(int r = 0; r < 16; ++r) sc[sub][r] = __builtin_amdgcn_exp2f(sc[sub][r] - l2);
+                if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
+#pragma unroll
+                    for(int r = 0; r < 16; ++r)
+                        if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) sc[sub][r] = 0.0f;
+                }
+#pragma unroll
+                for(int r = 0; r < 16; ++r) dp[sub][r] = sc[sub][r] * (dp[sub][r] - dd);
+            }
+            int dss;
+            const i32x8 df = pack_pair_mx(dp, lh, dss);
+#pragma unroll
+            for(int cb = 0; cb < 2; ++cb)
+                dq[cb] = mfma64(tile_frag_rows(sKt[st], cb * 32 + lq, lh), df, dq[cb], 127 + ex.k, dss);
+        }
+        if(more) {
+            put_rows8(sK[st ^ 1], rk, kmul);
+            put_cols8(sKt[st ^ 1], rk, kmul);
+            put_rows8(sV[st ^ 1], rv, vmul);
+        }
+    }
+    if(qi >= p.T) return;  // a padding row of the last block
+    store_rowT(p.dq + base + qi * p.ld, dq, lh, p.scale, (p.flags & PK_ACCUM) != 0);
+}
+
+// amax[0..3] = max|q|, max|k|, max|v| over the heads' columns of rows
+// [0, rows) (row stride ld), max|dO| (row stride D), each taken when its
+// pointer is given; amax must be zero beforehand (attn_amax_zero).  Positive
+// floats order as their bit patterns, so an integer atomic max combines them.
+__global__ void attn_amax_zero(float* amax, int first, int n) {
+    if((int)threadIdx.x < n) amax[first + threadIdx.x] = 0.0f;
+}
+// blockIdx.y picks the tensor; a workgroup takes 32 rows, its lanes walking
+// their float4s (lane e = l + 256 j of the 32 * D/4) with all of a lane's
+// loads independent, so they are in flight together
+__global__ __launch_bounds__(256) void attn_amax_kernel(const float* q, const float* k, const float* v,
+                                                        const float* dout, int64_t rows, int64_t D, int64_t ld,
+                                                        float* amax) {
+    const int t = blockIdx.y;
+    const float* src = t == 0 ? q : t == 1 ? k : t == 2 ? v : dout;
+    if(!src) return;
+    const int64_t stride = t == 3 ? D : ld;
+    const int c4n = (int)(D / 4);
+    const int64_t r0 = (int64_t)blockIdx.x * 32;
+    const int n = (int)(std::min<int64_t>(32, rows - r0)) * c4n;
+    int row = (int)threadIdx.x / c4n, col = (int)threadIdx.x - row * c4n;
+    const int drow = 256 / c4n, dcol = 256 - drow * c4n;
+    float a = 0.0f;
+    for(int e0 = 0; e0 < n; e0 += 16 * 256) {
+        // up to 16 loads a lane, all issued before the first is used
+        f32x4 x[16];
+#pragma unroll
+        for(int j = 0; j < 16; ++j) {
+            x[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if(e0 + (int)threadIdx.x + 256 * j < n)
+                x[j] = *reinterpret_cast<const f32x4*>(src + (r0 + row) * stride + 4 * col);
+            row += drow;
+            col += dcol;
+            if(col >= c4n) {
+                col -= c4n;
+                ++row;
+            }
+        }
+#pragma unroll
+        for(int j = 0; j < 16; ++j)
+            a = fmaxf(a, fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])), fmaxf(fabsf(x[j][2]), fabsf(x[j][3]))));
+    }
+    // one atomic per workgroup: thousands on one address queue up at the cache
+    __shared__ float wmax[4];
+    a = pk::wave_max(a);
+    if((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = a;
+    __syncthreads();
+    a = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    if(threadIdx.x == 0 && a > 0.0f) atomicMax(reinterpret_cast<unsigned*>(amax + t), __float_as_uint(a));
+}
+
 int flash_check(const char* who, int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
                 const void* a, const void* b, const void* c) {
     if(B < 0 || H < 1 || T < 0) return pk::fail("%s: bad sizes", who);
@@ -1186,13 +1665,26 @@ const FlashPlan& flash_plan(int64_t BH, int64_t nqb, int slots) {
     return plan;
 }
 
-int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
+// products of a launch: fp32, bf16 or fp8 (e4m3)
+enum FlashPrec { kF32 = 0, kBF16 = 1, kFP8 = 2 };
+
+// fp8: max|.| of q, k, v (first = 0, the forward) or of dout (first = 3, the
+// backward) into amax[first..]
+void attn_amax(int first, int64_t rows, int64_t D, int64_t ld, const float* q, const float* k,
+               const float* v, const float* dout, float* amax, hipStream_t st) {
+    attn_amax_zero<<<1, 64, 0, st>>>(amax, first, first == 0 ? 3 : 1);
+    attn_amax_kernel<<<dim3((unsigned)((rows + 31) / 32), 4), 256, 0, st>>>(q, k, v, dout, rows, D, ld,
+                                                                           amax);
+}
+
+int flash_fwd_launch(const char* who, int prec, int64_t B, int64_t H, int64_t T, int64_t hd,
                      int64_t ld, float scale, const float* q, const float* k, const float* v,
-                     float* o, float* lse, pk_stream_t stream) {
+                     float* o, float* lse, float* amax, pk_stream_t stream) {
     int rc = flash_check(who, B, H, T, hd, ld, q, k, v);
     if(rc) return rc;
     if(B == 0 || T == 0) return PK_OK;
     if(!o || !pk::aligned16(o)) return pk::fail("%s: o NULL or unaligned", who);
+    if(prec == kFP8 && !amax) return pk::fail("%s: NULL amax", who);
     FlashParams p = {};
     p.q = q;
     p.k = k;
@@ -1207,10 +1699,17 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.ld = ld;
     p.scale = scale;
     const unsigned grid = (unsigned)(B * H * (p.Tp / ROWS));
-    if(bf16)
-        flash_fwd_bf16<<<grid, 256, 0, pk::as_stream(stream)>>>(p);
-    else
-        flash_fwd<<<grid, 256, 0, pk::as_stream(stream)>>>(p, flash_plan(B * H, p.Tp / ROWS, kFwdSlots));
+    hipStream_t st = pk::as_stream(stream);
+    if(prec == kFP8) {
+        attn_amax(0, B * T, p.D, ld, q, k, v, nullptr, amax, st);
+        if((rc = pk::launch_status(who))) return rc;
+        p.amax = amax;
+        flash_fwd_fp8<<<grid, 256, 0, st>>>(p);
+    } else if(prec == kBF16) {
+        flash_fwd_bf16<<<grid, 256, 0, st>>>(p);
+    } else {
+        flash_fwd<<<grid, 256, 0, st>>>(p, flash_plan(B * H, p.Tp / ROWS, kFwdSlots));
+    }
     return pk::launch_status(who);
 }
 
@@ -1219,16 +1718,24 @@ int flash_fwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
 extern "C" int pk_flash_attn_fwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
                                      float scale, const float* q, const float* k, const float* v,
                                      float* o, float* lse, pk_stream_t stream) {
-    return flash_fwd_launch("pk_flash_attn_fwd_f32", false, B, H, T, hd, ld, scale, q, k, v, o,
-                            lse, stream);
+    return flash_fwd_launch("pk_flash_attn_fwd_f32", kF32, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, nullptr, stream);
 }
 
 extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
                                           int64_t ld, float scale, const float* q, const float* k,
                                           const float* v, float* o, float* lse,
                                           pk_stream_t stream) {
-    return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", true, B, H, T, hd, ld, scale, q, k, v,
-                            o, lse, stream);
+    return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", kBF16, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, nullptr, stream);
+}
+
+extern "C" int pk_flash_attn_fwd_fp8_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                         float scale, const float* q, const float* k,
+                                         const float* v, float* o, float* lse, float* amax,
+                                         pk_stream_t stream) {
+    return flash_fwd_launch("pk_flash_attn_fwd_fp8_f32", kFP8, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, amax, stream);
 }
 
 // row constants (2*B*H*Tp floats, Tp = T rounded up to 128), then the dS tiles
@@ -1247,10 +1754,10 @@ extern "C" size_t pk_flash_attn_bwd_workspace_recompute(int64_t B, int64_t H, in
 
 namespace {
 
-int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T, int64_t hd,
+int flash_bwd_launch(const char* who, int prec, int64_t B, int64_t H, int64_t T, int64_t hd,
                      int64_t ld, float scale, const float* q, const float* k, const float* v,
                      const float* o, const float* lse, const float* dout, float* dq, float* dk,
-                     float* dv, void* workspace, size_t workspace_bytes, int flags,
+                     float* dv, float* amax, void* workspace, size_t workspace_bytes, int flags,
                      pk_stream_t stream) {
     int rc = flash_check(who, B, H, T, hd, ld, q, k, v);
     if(rc) return rc;
@@ -1260,8 +1767,9 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
        !pk::aligned16(dv))
         return pk::fail("%s: o, dout, dq, dk, dv must be 16-byte aligned", who);
     const bool recompute = (flags & PK_FLASH_RECOMPUTE) != 0;
-    if(recompute && bf16)
+    if(recompute && prec != kF32)
         return pk::fail("%s: PK_FLASH_RECOMPUTE is built for the fp32 products only", who);
+    if(prec == kFP8 && !amax) return pk::fail("%s: NULL amax", who);
     const size_t need = recompute ? pk_flash_attn_bwd_workspace_recompute(B, H, T)
                                   : pk_flash_attn_bwd_workspace(B, H, T);
     if(!workspace || workspace_bytes < need)
@@ -1290,15 +1798,24 @@ int flash_bwd_launch(const char* who, bool bf16, int64_t B, int64_t H, int64_t T
     p.scale = scale;
     p.flags = flags & (PK_ACCUM | PK_ACCUM2 | PK_ACCUM3);
     hipStream_t st = pk::as_stream(stream);
+    if(prec == kFP8) {
+        attn_amax(3, B * T, p.D, ld, nullptr, nullptr, nullptr, dout, amax, st);
+        if((rc = pk::launch_status(who))) return rc;
+        p.amax = amax;
+    }
     flash_dsum<<<pk::grid_for(B * H * p.Tp * 16, 256), 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
     const unsigned grid = (unsigned)(B * H * (p.Tp / ROWS));
-    if(bf16)
+    if(prec == kFP8)
+        flash_bwd_dkdv_fp8<<<grid, 256, 0, st>>>(p);
+    else if(prec == kBF16)
         flash_bwd_dkdv_bf16<<<grid, 256, 0, st>>>(p);
     else
         flash_bwd_dkdv<<<grid, 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
-    if(bf16)
+    if(prec == kFP8)
+        flash_bwd_dq_fp8<<<grid, 256, 0, st>>>(p);
+    else if(prec == kBF16)
         flash_bwd_dq_bf16<<<grid, 256, 0, st>>>(p);
     else if(recompute)
         flash_bwd_dq_recompute<<<grid, 256, 0, st>>>(p);
@@ -1314,8 +1831,8 @@ extern "C" int pk_flash_attn_bwd_f32(int64_t B, int64_t H, int64_t T, int64_t hd
                                      const float* o, const float* lse, const float* dout,
                                      float* dq, float* dk, float* dv, void* workspace,
                                      size_t workspace_bytes, int flags, pk_stream_t stream) {
-    return flash_bwd_launch("pk_flash_attn_bwd_f32", false, B, H, T, hd, ld, scale, q, k, v, o,
-                            lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
+    return flash_bwd_launch("pk_flash_attn_bwd_f32", kF32, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, dout, dq, dk, dv, nullptr, workspace, workspace_bytes, flags, stream);
 }
 
 extern "C" int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
@@ -1324,6 +1841,17 @@ extern "C" int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64
                                           const float* dout, float* dq, float* dk, float* dv,
                                           void* workspace, size_t workspace_bytes, int flags,
                                           pk_stream_t stream) {
-    return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", true, B, H, T, hd, ld, scale, q, k, v,
-                            o, lse, dout, dq, dk, dv, workspace, workspace_bytes, flags, stream);
+    return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", kBF16, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, dout, dq, dk, dv, nullptr, workspace, workspace_bytes, flags,
+                            stream);
+}
+
+extern "C" int pk_flash_attn_bwd_fp8_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                         float scale, const float* q, const float* k,
+                                         const float* v, const float* o, const float* lse,
+                                         const float* dout, float* dq, float* dk, float* dv,
+                                         float* amax, void* workspace, size_t workspace_bytes,
+                                         int flags, pk_stream_t stream) {
+    return flash_bwd_launch("pk_flash_attn_bwd_fp8_f32", kFP8, B, H, T, hd, ld, scale, q, k, v, o,
+                            lse, dout, dq, dk, dv, amax, workspace, workspace_bytes, flags, stream);
 }

@@ -278,7 +278,10 @@ static size_t attn_ds_cap(void) {
     }
     return (size_t)4 << 30;
 }
-enum { AI_B = 0, AI_H = 1, AI_FLASH = 2, AI_BF16 = 3 };
+/* AI_PREC: the products' precision, 0 fp32, 1 bf16, 2 fp8 (flash only); an
+ * fp8 node keeps max|q|, max|k|, max|v| for the backward in saved[AS_P] */
+enum { AI_B = 0, AI_H = 1, AI_FLASH = 2, AI_PREC = 3 };
+enum { ATTN_F32 = 0, ATTN_BF16 = 1, ATTN_FP8 = 2 };
 
 static void attn_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
@@ -287,10 +290,10 @@ static void attn_backward(struct PicoTensor* self) {
     if(!dout) return;
     int64_t B = n->ival[AI_B], H = n->ival[AI_H];
     int64_t T = q->shape[0] / B, hd = q->shape[1] / H, ld = q->strides[0];
-    const int flash = (int)n->ival[AI_FLASH], bf16 = flash && n->ival[AI_BF16];
+    const int flash = (int)n->ival[AI_FLASH], prec = flash ? (int)n->ival[AI_PREC] : ATTN_F32;
     size_t ws_bytes = flash ? pk_flash_attn_bwd_workspace(B, H, T)
                             : sizeof(float) * (size_t)(B * H * T * T);
-    const int recompute = flash && !bf16 && ws_bytes > attn_ds_cap();
+    const int recompute = flash && prec == ATTN_F32 && ws_bytes > attn_ds_cap();
     if(recompute) ws_bytes = pk_flash_attn_bwd_workspace_recompute(B, H, T);
     void* ws = pkh_workspace(ws_bytes);
     if(!ws) {
@@ -311,8 +314,13 @@ static void attn_backward(struct PicoTensor* self) {
         pkh_grad_mark(order[i]);
     }
     int st;
-    if(flash)
-        st = (bf16 ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
+    if(flash && prec == ATTN_FP8)
+        st = pk_flash_attn_bwd_fp8_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
+                                       self->data, (const float*)n->saved[AS_LSE], dout, q->grad,
+                                       k->grad, v->grad, (float*)n->saved[AS_P], ws, ws_bytes,
+                                       flags, pkh_stream());
+    else if(flash)
+        st = (prec == ATTN_BF16 ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
             B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, self->data,
             (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad, ws, ws_bytes, flags,
             pkh_stream());
@@ -349,25 +357,35 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     if(!out) return NULL;
     struct PkNode* n = pkh_node(out);
     const int flash = pk_flash_attn_supported(T, hd);
+    /* the matmul precision switch covers attention's products too; the
+     * backward uses the precision the forward ran in */
+    const int mp = pico_get_matmul_precision();
+    const int prec = !flash ? ATTN_F32
+                            : mp == PICO_MATMUL_FP8 ? ATTN_FP8
+                                                    : mp == PICO_MATMUL_BF16 ? ATTN_BF16 : ATTN_F32;
     float* lse = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T));
-    float* P = flash ? NULL : (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T));
-    if(!lse || (!flash && !P)) return NULL;
+    /* P for the unfused chain; fp8's max|q|, max|k|, max|v|, max|dout| */
+    float* P = !flash ? (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T))
+                      : prec == ATTN_FP8 ? (float*)arena_alloc_device(arena, 4 * sizeof(float))
+                                         : NULL;
+    if(!lse || ((!flash || prec == ATTN_FP8) && !P)) return NULL;
     n->saved[AS_LSE] = lse;
     n->saved[AS_P] = P;
     n->ival[AI_B] = B;
     n->ival[AI_H] = H;
     n->ival[AI_FLASH] = flash;
-    /* the matmul precision switch covers attention's products too (bf16
-     * products for PICO_MATMUL_BF16 and PICO_MATMUL_FP8); the backward uses
-     * the precision the forward ran in */
-    const int prec = pico_get_matmul_precision();
-    n->ival[AI_BF16] = flash && (prec == PICO_MATMUL_BF16 || prec == PICO_MATMUL_FP8);
+    n->ival[AI_PREC] = prec;
     n->fval[0] = 1.0f / sqrtf((float)hd);
-    int st = flash ? (n->ival[AI_BF16] ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
-                         B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, out->data, lse,
-                         pkh_stream())
-                   : pk_attn_causal_fwd_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
-                                            out->data, lse, P, pkh_stream());
+    int st;
+    if(prec == ATTN_FP8)
+        st = pk_flash_attn_fwd_fp8_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
+                                       out->data, lse, P, pkh_stream());
+    else if(flash)
+        st = (prec == ATTN_BF16 ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
+            B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, out->data, lse, pkh_stream());
+    else
+        st = pk_attn_causal_fwd_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
+                                    out->data, lse, P, pkh_stream());
     if(pkh_status("pico_attention_causal", st)) return NULL;
     pkh_set_parents(arena, out, 3, xs, attn_backward);
     return out;

@@ -496,13 +496,21 @@ def flash_supported(T, hd):
     return bool(hip_lib().pk_flash_attn_supported(T, hd))
 
 
-def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False):
+def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False, fp8_amax=None):
     """Fused causal attention; bf16=True rounds the matrix-product operands to
-    bf16 (pk_flash_attn_fwd_bf16_f32)."""
+    bf16 (pk_flash_attn_fwd_bf16_f32); fp8_amax (4 float32 on the device)
+    runs the e4m3 products (pk_flash_attn_fwd_fp8_f32) and receives max|q|,
+    max|k|, max|v| for the backward."""
     T, hd, ld = _attn_layout(B, H, q, k, v, o)
     if lse.numel() < B * H * T:
         raise ValueError("attention shape mismatch")
     scale = hd ** -0.5 if scale is None else scale
+    if fp8_amax is not None:
+        _f32(fp8_amax)
+        check("pk_flash_attn_fwd_fp8_f32", hip_lib().pk_flash_attn_fwd_fp8_f32(
+            B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
+            _ptr(fp8_amax), _stream()))
+        return
     name = "pk_flash_attn_fwd_bf16_f32" if bf16 else "pk_flash_attn_fwd_f32"
     check(name, getattr(hip_lib(), name)(
         B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
@@ -512,9 +520,10 @@ FLASH_RECOMPUTE = 16
 
 
 def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False,
-              recompute=False):
+              recompute=False, fp8_amax=None):
     """recompute: PK_FLASH_RECOMPUTE, dQ from recomputed scores (a workspace of
-    the row constants only)"""
+    the row constants only); fp8_amax: the e4m3 products, with the amax the
+    forward filled (pk_flash_attn_bwd_fp8_f32)"""
     T, hd, ld = _attn_layout(B, H, q, k, v, o, dq, dk, dv)
     if not dout.is_contiguous() or dout.shape != o.shape:
         raise ValueError("attention: dout must be contiguous like o")
@@ -525,6 +534,13 @@ def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16
     else:
         need = int(hip_lib().pk_flash_attn_bwd_workspace(B, H, T))
     ws = torch.empty(max(1, need // 4), device=q.device, dtype=torch.float32)
+    if fp8_amax is not None:
+        _f32(fp8_amax)
+        check("pk_flash_attn_bwd_fp8_f32", hip_lib().pk_flash_attn_bwd_fp8_f32(
+            B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout),
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(fp8_amax), _ptr(ws), ws.numel() * 4, flags,
+            _stream()))
+        return
     name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
     check(name, getattr(hip_lib(), name)(
         B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout),
