@@ -173,10 +173,45 @@ def sweep_section(torch, K, sizes, gemm=None):
     return out
 
 
+def mx8_section(torch, K, sizes):
+    """MX8 products (pk_gemm_mx8_f32) with both operands already cast and
+    resident, replayed from a graph, and the one-pass casts
+    (pk_mx8_quantize_f32) of a row-major and a transposed fp32 operand:
+    TFLOP/s against the 5.0 PFLOP/s dense fp8 peak, cast rates in GB/s of
+    HBM traffic (4 bytes read + 1 written per value, plus the scales)"""
+    dev = torch.device("cuda:0")
+    out = {}
+    for n in sizes:
+        gen = torch.Generator(device=dev).manual_seed(n)
+        A = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        C = torch.empty(n, n, device=dev)
+        A8, B8 = K.mx8_quantize(A, False), K.mx8_quantize(B, True)
+        reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            K.gemm_mx8(n, n, n, A8, B8, C)
+            torch.cuda.synchronize()
+        ms = _graph_time(lambda: K.gemm_mx8(n, n, n, A8, B8, C), reps, 2)
+        qms = _graph_time(lambda: K.mx8_quantize(A, False, out=A8), reps, 2)
+        qtms = _graph_time(lambda: K.mx8_quantize(B, True, out=B8), reps, 2)
+        tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        tm, tn, splits = K.mx8_plan(n, n, n)
+        out[str(n)] = {"tflops": round(tflops, 1), "frac_of_fp8_peak": round(tflops * 1e12 / MFMA_FP8_PEAK, 4),
+                       "us": round(ms * 1e3, 1), "tile": f"{tm}x{tn}", "splits": splits,
+                       "cast_us": round(qms * 1e3, 1),
+                       "cast_gbs": round(n * n * 5.03 / (qms * 1e-3) / 1e9, 1),
+                       "cast_transposed_us": round(qtms * 1e3, 1),
+                       "cast_transposed_gbs": round(n * n * 5.03 / (qtms * 1e-3) / 1e9, 1)}
+        del A, B, C, A8, B8
+    return out
+
+
 def attn_section(torch, K):
     """the fused causal attention at config 5's shapes (B 8, H 12, T 1024, hd 64),
-    fp32 and bf16 products, randn inputs; TFLOP/s by the causal count (4*hd FLOP
-    per visible (query, key) pair forward, 10*hd backward)"""
+    fp32, bf16 and fp8 products (fp8 times include the amax passes over q, k,
+    v and dout), randn inputs; TFLOP/s by the causal count (4*hd FLOP per
+    visible (query, key) pair forward, 10*hd backward)"""
     dev = torch.device("cuda:0")
     B, H, T, hd = 8, 12, 1024, 64
     D = H * hd
@@ -194,9 +229,10 @@ def attn_section(torch, K):
         K.flash_fwd(B, H, q, k, v, o, lse)
         K.flash_bwd(B, H, q, k, v, o, lse, do, dq, dk, dv)
         torch.cuda.synchronize()
-    for name, bf in (("fp32", False), ("bf16", True)):
-        fwd, _ = _events_time(lambda: K.flash_fwd(B, H, q, k, v, o, lse, bf16=bf), 20, 3)
-        bwd, _ = _events_time(lambda: K.flash_bwd(B, H, q, k, v, o, lse, do, dq, dk, dv, bf16=bf),
+    amax = torch.zeros(4, device=dev)
+    for name, kw in (("fp32", {}), ("bf16", {"bf16": True}), ("fp8", {"fp8_amax": amax})):
+        fwd, _ = _events_time(lambda: K.flash_fwd(B, H, q, k, v, o, lse, **kw), 20, 3)
+        bwd, _ = _events_time(lambda: K.flash_bwd(B, H, q, k, v, o, lse, do, dq, dk, dv, **kw),
                               20, 3)
         out[name] = {"fwd_us": round(fwd * 1e3, 1), "bwd_us": round(bwd * 1e3, 1),
                      "fwd_tflops": round(4 * hd * pairs / (fwd * 1e-3) / 1e12, 1),
@@ -800,11 +836,15 @@ def main():
         # tensors: far outside the fp32 parity contract, for experiments
         line["fp8"] = {
             "sweep": sweep_section(torch, K, [2048, 4096, 8192], K.gemm_fp8),
+            "mx8": mx8_section(torch, K, [2048, 4096, 8192]),
             "train": {name: train_section(name, args.variant_steps, 3, precision=3)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
-            "note": "pico_set_matmul_precision(PICO_MATMUL_FP8): matmul products on the fp8 "
-                    "matrix cores from fp32 tensors rounded on the way to LDS, attention fp32; "
-                    "not the headline, which is fp32"}
+            "note": "sweep: pk_gemm_fp8_f32 (fp32 operands rounded to e4m3 on the way to "
+                    "LDS, the 32x32x16 fp8 MFMA); mx8: pk_gemm_mx8_f32 over operands cast once "
+                    "to MX8 (e4m3 + a power of two per 32 values) on the 32x32x64 scaled MFMA. "
+                    "train: pico_set_matmul_precision(PICO_MATMUL_FP8) -- every product through "
+                    "MX8 (weights cast once per optimizer step, activations per product) and "
+                    "the fp8 fused attention; not the headline, which is fp32"}
     if "attn" in sections:
         line["attention"] = attn_section(torch, K)
     if "rows" in sections:
@@ -834,6 +874,12 @@ def main():
                                         for k in ("fwd_us", "bwd_us")}
     if "row_kernels" in line:
         summary["row_kernels_frac"] = {k: v["frac"] for k, v in line["row_kernels"].items()}
+    for prec in ("bf16", "fp8"):
+        t5 = line.get(prec, {}).get("train", {}).get("config5")
+        if t5:
+            summary[f"config5_{prec}_ms_per_step"] = t5["ms_per_step"]
+    if "fp8" in line and "mx8" in line["fp8"]:
+        summary["mx8_tflops"] = {n: r["tflops"] for n, r in line["fp8"]["mx8"].items()}
     line["summary"] = summary
     print(json.dumps(line), flush=True)
 
