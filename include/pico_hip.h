@@ -222,6 +222,14 @@ int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A,
  * NULL or smaller workspace runs the product unsplit.  pk_gemm_mx8_plan
  * reports the launch a shape gets with enough workspace: the C tile (256 x
  * 256, 256 x 128, 128 x 256 or 128 x 128) and the number of K splits. */
+/* pk_mx8_quantize2_f32: both MX8 casts of one row-major X [M, N] (row stride
+ * ldx) from one read of it: QR = X as an [M, N] MX8 matrix and QT = X^T as an
+ * [N, M] one (pk_mx8_bytes(M, N) and pk_mx8_bytes(N, M) bytes), byte for byte
+ * what pk_mx8_quantize_f32 writes for each.  A product's upstream gradient
+ * needs both: dY as the input gradient's A operand, dY^T as the weight
+ * gradient's B operand. */
+int pk_mx8_quantize2_f32(int64_t M, int64_t N, const float* X, int64_t ldx, void* QR, void* QT,
+                         pk_stream_t stream);
 size_t pk_gemm_mx8_workspace(int64_t M, int64_t N, int64_t K);
 int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
                        float beta, const float* X, int64_t ldx, float* C, int64_t ldc,

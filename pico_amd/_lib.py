@@ -60,6 +60,7 @@ PK_SIGNATURES = {
     "pk_mx8_quantize_f32": [c_i64, c_i64, c_p, c_i64, c_int, c_p, c_p],
     "pk_gemm_mx8_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p],
     "pk_gemm_mx8_workspace": [c_i64, c_i64, c_i64],
+    "pk_mx8_quantize2_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p],
     "pk_gemm_mx8_ex_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p,
                            c_size, c_p],
     "pk_gemm_mx8_plan": [c_i64, c_i64, c_i64, ctypes.POINTER(c_int), ctypes.POINTER(c_int),

@@ -72,7 +72,7 @@ struct Fp8qParams {
     int tiles_m, tiles_n;
 };
 
-int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+__host__ __device__ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 __device__ __forceinline__ int slot_of(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
 
@@ -513,6 +513,81 @@ __global__ __launch_bounds__(NT) void quantize_cols_kernel(int64_t R, int64_t K,
     dst[1] = o[1];
 }
 
+// Both MX8 casts of one row-major matrix X [M, N] from one read of it: QR =
+// X as [M, N] (blocks along N) and QT = X^T as [N, M] (blocks along M), equal
+// byte for byte to two calls of pk_mx8_quantize_f32.  A block stages a 64 (M)
+// x 128 (N) tile through LDS as quantize_cols_kernel does; each thread then
+// takes one MX block of QT (32 rows of X at one column) and one of QR (32
+// columns of one row of X), the latter read across the LDS tile.  The grid
+// covers the larger padded extents; a tile writes only the parts of QR and QT
+// inside their own padded shapes.
+__global__ __launch_bounds__(NT) void quantize_dual_kernel(int64_t M, int64_t N, const float* __restrict__ X,
+                                                           int64_t ldx, bool vec, uint8_t* __restrict__ QR,
+                                                           uint8_t* __restrict__ QT) {
+    __shared__ float tile[128][65];
+    const int t = threadIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.x * 64, n0 = (int64_t)blockIdx.y * 128;
+    const int64_t MpR = round_up(M, kTileQ), NpR = round_up(N, QKPAD);  // QR [MpR, NpR]
+    const int64_t NpT = round_up(N, kTileQ), MpT = round_up(M, QKPAD);  // QT [NpT, MpT]
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        const int idx = t + NT * i;
+        const int mm = idx >> 5, nq = (idx & 31) * 4;
+        const f32x4 v = load4(X, ldx, M, N, m0 + mm, n0 + nq, vec);
+#pragma unroll
+        for(int c = 0; c < 4; ++c) tile[nq + c][mm] = v[c];
+    }
+    __syncthreads();
+    // QT: row n0 + t/2 of X^T, k = m0 + 32*(t%2) .. +31
+    {
+        const int rr = t >> 1, half = t & 1;
+        const int64_t r = n0 + rr;
+        if(r < NpT && m0 < MpT) {
+            float v[32];
+#pragma unroll
+            for(int q = 0; q < 32; ++q) v[q] = tile[rr][32 * half + q];
+            float amax = 0.0f;
+#pragma unroll
+            for(int q = 0; q < 32; ++q) amax = fmaxf(amax, fabsf(v[q]));
+            const int e = mx_exponent(amax);
+            *scale_slot(QT + NpT * MpT, NpT, r, (m0 >> 5) + half) = (uint8_t)(e + 127);
+            i32x4 o[2];
+#pragma unroll
+            for(int q = 0; q < 8; ++q) {
+                const float* p = &v[4 * q];
+                o[q >> 2][q & 3] = e4m3x4(ldexpf(p[0], -e), ldexpf(p[1], -e), ldexpf(p[2], -e), ldexpf(p[3], -e));
+            }
+            i32x4* dst = reinterpret_cast<i32x4*>(QT + r * MpT + m0 + 32 * half);
+            dst[0] = o[0];
+            dst[1] = o[1];
+        }
+    }
+    // QR: row m0 + t/4 of X, k = n0 + 32*(t%4) .. +31
+    {
+        const int rr = t >> 2, blk = t & 3;
+        const int64_t r = m0 + rr, k0 = n0 + 32 * blk;
+        if(r < MpR && k0 < NpR) {
+            float v[32];
+#pragma unroll
+            for(int q = 0; q < 32; ++q) v[q] = tile[32 * blk + q][rr];
+            float amax = 0.0f;
+#pragma unroll
+            for(int q = 0; q < 32; ++q) amax = fmaxf(amax, fabsf(v[q]));
+            const int e = mx_exponent(amax);
+            *scale_slot(QR + MpR * NpR, MpR, r, k0 >> 5) = (uint8_t)(e + 127);
+            i32x4 o[2];
+#pragma unroll
+            for(int q = 0; q < 8; ++q) {
+                const float* p = &v[4 * q];
+                o[q >> 2][q & 3] = e4m3x4(ldexpf(p[0], -e), ldexpf(p[1], -e), ldexpf(p[2], -e), ldexpf(p[3], -e));
+            }
+            i32x4* dst = reinterpret_cast<i32x4*>(QR + r * NpR + k0);
+            dst[0] = o[0];
+            dst[1] = o[1];
+        }
+    }
+}
+
 // launch: every byte of [Rp, Kp] (row stride ldq) and, MX, every scale
 template <bool MX>
 void launch_quantize(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, const float* scale,
@@ -714,6 +789,21 @@ extern "C" size_t pk_gemm_mx8_workspace(int64_t M, int64_t N, int64_t K) {
     if(M <= 0 || N <= 0 || K <= 0) return 0;
     const MxPlan plan = mx8_plan(M, N, K, true);
     return plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+}
+
+extern "C" int pk_mx8_quantize2_f32(int64_t M, int64_t N, const float* X, int64_t ldx, void* QR, void* QT,
+                                    pk_stream_t stream) {
+    if(M < 0 || N < 0) return pk::fail("pk_mx8_quantize2_f32: negative size");
+    if(M == 0 || N == 0) return PK_OK;
+    if(!X || !QR || !QT) return pk::fail("pk_mx8_quantize2_f32: NULL pointer");
+    if(ldx < N) return pk::fail("pk_mx8_quantize2_f32: ldx below the row length");
+    if(!pk::aligned16(QR) || !pk::aligned16(QT)) return pk::fail("pk_mx8_quantize2_f32: Q must be 16-byte aligned");
+    const int64_t Mg = round_up(M, kTileQ), Ng = round_up(N, kTileQ);
+    if(Mg / 64 > INT32_MAX || Ng / 128 > 65535) return pk::fail("pk_mx8_quantize2_f32: too large");
+    const bool vec = ldx % 4 == 0 && pk::aligned16(X);
+    quantize_dual_kernel<<<dim3((unsigned)(Mg / 64), (unsigned)(Ng / 128)), NT, 0, pk::as_stream(stream)>>>(
+        M, N, X, ldx, vec, static_cast<uint8_t*>(QR), static_cast<uint8_t*>(QT));
+    return pk::launch_status("pk_mx8_quantize2_f32");
 }
 
 extern "C" int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,

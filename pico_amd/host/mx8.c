@@ -18,6 +18,12 @@
  * cast from an earlier epoch is redone, in place, at its next use; so within
  * a training step each weight is cast at most twice (once per layout), and a
  * captured step recasts its weights on every replay.
+ *
+ * A matmul's backward reads its upstream gradient g in both layouts: g [M, N]
+ * for the input gradient, g^T [N, M] for the weight gradient.  Both casts come
+ * from one read of g (pk_mx8_quantize2_f32), issued on the main stream before
+ * the weight gradient forks to the side stream, and live in the arena, which
+ * no later op reuses before the arena is reset.
  */
 #include <stdint.h>
 #include <string.h>
@@ -40,6 +46,28 @@ static uint64_t g_epoch = 1;
 
 void pkh_params_changed(void) { g_epoch++; }
 
+/* the upstream gradient of the matmul whose backward is running, cast both
+ * ways by one pass over it (pkh_mx8_grad_casts) into the current arena, so
+ * that its input gradient (g as [M, N]) and its weight gradient (g^T as
+ * [N, M], on the side stream) read it without casting it again */
+static struct Mx8Cast g_grad[2];
+
+int pkh_mx8_grad_casts(const float* g, int64_t M, int64_t N, pk_stream_t st) {
+    memset(g_grad, 0, sizeof(g_grad));
+    struct Arena* arena = pkh_need_arena();
+    if(!arena || M <= 0 || N <= 0) return 0;
+    void* qr = arena_alloc_device(arena, pk_mx8_bytes(M, N));
+    void* qt = qr ? arena_alloc_device(arena, pk_mx8_bytes(N, M)) : NULL;
+    if(!qt) return 0; /* the products cast g themselves */
+    int s = pk_mx8_quantize2_f32(M, N, g, N, qr, qt, st);
+    if(s) return s;
+    g_grad[0] = (struct Mx8Cast){g, M, N, N, 0, 0, qr};
+    g_grad[1] = (struct Mx8Cast){g, N, M, N, 1, 0, qt};
+    return 0;
+}
+
+void pkh_mx8_grad_casts_done(void) { memset(g_grad, 0, sizeof(g_grad)); }
+
 void pkh_mx8_release(void) {
     for(int i = 0; i < g_ncasts; i++) pkh_device_free(g_casts[i].q);
     memset(g_casts, 0, sizeof(g_casts));
@@ -52,6 +80,11 @@ void pkh_mx8_release(void) {
 static const void* kept_cast(struct PkMat m, int64_t rows, int64_t k, int trans, pk_stream_t st,
                              int side, int* status) {
     *status = 0;
+    for(int i = 0; i < 2; i++) {
+        const struct Mx8Cast* e = &g_grad[i];
+        if(e->q && e->p == m.p && e->rows == rows && e->k == k && e->ld == m.ld && e->trans == trans)
+            return e->q;
+    }
     if(!m.persist || side) return NULL;
     struct Mx8Cast* c = NULL;
     for(int i = 0; i < g_ncasts; i++) {

@@ -276,7 +276,7 @@ int pico_matmul_gpu(struct PicoTensor* a, struct PicoTensor* b, struct PicoTenso
  * chain stays on the main stream.  Either way the side stream orders dB's
  * write after every earlier write to B's grad: main-stream ones through the
  * fork, side ones by issue order. */
-static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor* b,
+static void matmul_backward_body(struct PkMat va, int a_param, struct PicoTensor* b,
                                  const float* g, int64_t M, int64_t K, int64_t N,
                                  int (*dA_fn)(void*), void* ctx) {
     struct PkMat vb;
@@ -311,6 +311,17 @@ static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor
     }
     if(pkh_status("pico_matmul_backward", st)) return;
     pkh_grad_mark(b);
+}
+
+/* fp8: both products read g, cast once for both (mx8.c) */
+static void matmul_backward_with(struct PkMat va, int a_param, struct PicoTensor* b,
+                                 const float* g, int64_t M, int64_t K, int64_t N,
+                                 int (*dA_fn)(void*), void* ctx) {
+    if(g_matmul_precision == PICO_MATMUL_FP8 &&
+       pkh_status("pico_matmul_backward", pkh_mx8_grad_casts(g, M, N, pkh_stream())))
+        return;
+    matmul_backward_body(va, a_param, b, g, M, K, N, dA_fn, ctx);
+    pkh_mx8_grad_casts_done();
 }
 
 /* dA (+)= g . B^T into a tensor's grad (the plain matmul's input gradient) */

@@ -202,6 +202,10 @@ int pkh_gemm(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, fl
 int pkh_mx8_product(struct PkMat A, struct PkMat B, int64_t M, int64_t N, int64_t K, float* C,
                     int64_t ldc, float beta, const float* X, int64_t ldx, pk_stream_t st,
                     int side);
+/* both casts of a backward's upstream gradient g [M, N] (row stride N), used
+ * by the products issued until pkh_mx8_grad_casts_done() */
+int pkh_mx8_grad_casts(const float* g, int64_t M, int64_t N, pk_stream_t st);
+void pkh_mx8_grad_casts_done(void);
 /* parameters may have changed: casts kept from before are redone at next use */
 void pkh_params_changed(void);
 void pkh_mx8_release(void);

@@ -142,6 +142,19 @@ def mx8_quantize(X, trans, out=None):
     return out
 
 
+def mx8_quantize2(X):
+    """(X as an MX8 [M, N], X^T as an MX8 [N, M]) from one read of X
+    (pk_mx8_quantize2_f32)"""
+    _f32(X)
+    ldx = _rowmajor(X, "X")
+    M, N = X.shape
+    QR = torch.empty(max(mx8_bytes(M, N), 1), dtype=torch.uint8, device=X.device)
+    QT = torch.empty(max(mx8_bytes(N, M), 1), dtype=torch.uint8, device=X.device)
+    check("pk_mx8_quantize2_f32", hip_lib().pk_mx8_quantize2_f32(
+        M, N, _ptr(X), ldx, _ptr(QR), _ptr(QT), _stream()))
+    return QR, QT
+
+
 def mx8_plan(M, N, Kd):
     """(tile rows, tile cols, K splits) of the launch a shape gets (pk_gemm_mx8_plan)"""
     tm, tn, sp = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)

@@ -356,3 +356,18 @@ def test_mx8_gemm_k_split(dev, M, N, Kd):
     Yd, _, _ = mx8_decode(host(B8), N, Kd)
     assert gemm_err(host(Cs), Xd, Yd.T) <= TOL
     assert gemm_err(host(Cs), Xd, Yd.T, C_ref=host(Cu).astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("M,N", [(1, 1), (70, 130), (256, 128), (300, 1000), (8192, 768), (130, 2304)])
+def test_mx8_dual_cast_equals_two_casts(dev, M, N):
+    """one read, both casts: byte for byte the row cast of X and the cast of
+    X^T, padding and scales included"""
+    X = _mixed(M, N, M + 3 * N)
+    dX = cu(X)
+    QR, QT = K.mx8_quantize2(dX)
+    assert np.array_equal(host(QR), host(K.mx8_quantize(dX, False)))
+    assert np.array_equal(host(QT), host(K.mx8_quantize(dX, True)))
+    # a strided view: the row stride is honoured
+    wide = cu(np.concatenate([X, X[:, :N // 2 + 1] * 3.0], axis=1))
+    QR2, QT2 = K.mx8_quantize2(wide[:, :N])
+    assert np.array_equal(host(QR2), host(QR)) and np.array_equal(host(QT2), host(QT))
