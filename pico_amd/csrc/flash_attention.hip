@@ -420,14 +420,21 @@ __global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, Flash
         __syncthreads();  // every wave has read K(j)
         if(j + 1 < nkv) blk.issue(K, p.T, p.ld, (int64_t)(j + 1) * BLK, sK, w);
     };
+    const bool half = (q0 & (BLK - 1)) == 0;
     {  // block 0: the exact max; masked when it is also the wave's last
         begin_block(0);
         f32x16 s[2] = {zero16(), zero16()};
-        dot_rows2(sK, lq, lh, qf, s[0], s[1]);
+        if(nw == 1 && half) s[0] = dot_rows(sK, 0, lq, lh, qf, s[0]);
+        else dot_rows2(sK, lq, lh, qf, s[0], s[1]);
         mid_block(0);
         if(nw == 1) mask(0, s);
         softmax_first(s);
-        pv(sV[0], s);
+        if(nw == 1 && half) {
+            o[0] = dot_cols(sV[0], 0, 0, lq, lh, s[0], o[0]);
+            o[1] = dot_cols(sV[0], 0, 1, lq, lh, s[0], o[1]);
+        } else {
+            pv(sV[0], s);
+        }
     }
     int j = 1;
     for(; j < nw - 1; ++j) {  // blocks wholly below the diagonal
@@ -443,11 +450,20 @@ __global__ __launch_bounds__(256, kFwdSlots) void flash_fwd(FlashParams p, Flash
         begin_block(j);
         f32x16 s[2];
         s[0] = s[1] = start_scores();
-        dot_rows2(sK, lq, lh, qf, s[0], s[1]);
+        // a wave whose 32 queries end before the block's second key group
+        // (q0 a multiple of 64) computes the first group only: the second is
+        // wholly masked, its probabilities exactly 0
+        if(half) s[0] = dot_rows(sK, 0, lq, lh, qf, s[0]);
+        else dot_rows2(sK, lq, lh, qf, s[0], s[1]);
         mid_block(j);
         mask(j, s);
         softmax(s);
-        pv(sV[j & 1], s);
+        if(half) {
+            o[0] = dot_cols(sV[j & 1], 0, 0, lq, lh, s[0], o[0]);
+            o[1] = dot_cols(sV[j & 1], 0, 1, lq, lh, s[0], o[1]);
+        } else {
+            pv(sV[j & 1], s);
+        }
         ++j;
     }
     for(; j < nkv; ++j) {  // the workgroup's blocks past this wave's last
@@ -645,7 +661,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv(FlashParams p) {
 // (x scale at the end) over the key blocks of 64 with key <= query: K blocks
 // stream through LDS one block ahead, the dS tiles the dK/dV kernel stored
 // are read straight into registers one block ahead.
-// Four workgroups share a CU (124 VGPRs, 34 KB of LDS), so config 5's 768
+// Four workgroups share a CU (112 VGPRs, 34 KB of LDS), so config 5's 768
 // are resident at once, placed by the dispatch plan.
 constexpr int kDqSlots = 4;
 __global__ __launch_bounds__(256, kDqSlots) void flash_bwd_dq(FlashParams p, FlashPlan plan) {
@@ -698,9 +714,18 @@ __global__ __launch_bounds__(256, kDqSlots) void flash_bwd_dq(FlashParams p, Fla
                     for(int r = 0; r < 16; ++r)
                         if(sub * 32 + 8 * (r >> 2) + (r & 3) > lim) cur[sub][r] = 0.0f;
                 }
+            }
+            // the two column chains alternate, each accumulating the keys in
+            // the order dot_cols takes them
 #pragma unroll
-                for(int cb = 0; cb < 2; ++cb)
-                    dq[cb] = dot_cols(tk, sub, cb, lq, lh, cur[sub], dq[cb]);
+            for(int sub = 0; sub < 2; ++sub) {
+                if(2 * j + sub > qg) continue;
+#pragma unroll
+                for(int r = 0; r < 16; ++r) {
+                    const float* a = tk + (sub * 32 + acc_row(r, lh)) * LDT + lq;
+                    dq[0] = mfma(a[0], cur[sub][r], dq[0]);
+                    dq[1] = mfma(a[32], cur[sub][r], dq[1]);
+                }
             }
             cur[0] = nxt[0];
             cur[1] = nxt[1];
