@@ -54,8 +54,8 @@ struct FlashParams {
     const float* amax;   // fp8 kernels: max|q|, max|k|, max|v|, max|dO|
 };
 
-// Which block (a forward or dQ query block, a dK/dV key block) each of a
-// launch's first slots*kCUs workgroups takes.  `slots` workgroups of a kernel
+// Which block (a forward or dQ query block) each of a launch's first
+// slots*kCUs workgroups takes.  `slots` workgroups of a kernel
 // share a CU, and the dispatcher places workgroup b on CU b % 256 as slot
 // b / 256 (measured: b, b+256, b+512 run on one CU, all from the start), so
 // this table decides each CU's work.  The host fills it longest-first, each
@@ -63,7 +63,10 @@ struct FlashParams {
 // 26-28 key blocks each (the plain heaviest-first order left 24-30, and the
 // launch waited on the 30s).  Later workgroups take the remaining blocks
 // heaviest first as slots free.  The table only moves work between CUs:
-// every block is computed the same way wherever it runs.
+// every block is computed the same way wherever it runs.  The dK/dV kernel
+// (two slots per CU, so a third of its workgroups start as slots free) keeps
+// the plain heaviest-first order: the table measured slower there (backward
+// 330.1 against 323.3 us at config 5).
 constexpr int kMaxSlots = 4;
 struct FlashPlan {
     uint16_t rank[kMaxSlots * kCUs];  // workgroup b < n takes rank[b]; others rank b
@@ -71,7 +74,8 @@ struct FlashPlan {
 };
 // ranks run heaviest first: rank r is block (nblk-1-r/BH) of the forward and
 // dQ (a query block seeing the most keys first), block r/BH of dK/dV (a key
-// block seen by the most queries first), of head r%BH
+// block seen by the most queries first; its rank is its workgroup index), of
+// head r%BH
 __device__ __forceinline__ int64_t plan_rank(const FlashPlan& plan) {
     return (int)blockIdx.x < plan.n ? (int64_t)plan.rank[blockIdx.x] : (int64_t)blockIdx.x;
 }
@@ -1661,14 +1665,15 @@ namespace {
 
 // The dispatch table of a launch over BH heads of nqb 128-row blocks with
 // `slots` workgroups per CU (cached per shape, per host thread).  Rank r
-// (heaviest first) streams 2*(nqb - r/BH) 64-row blocks of the other operand
-// in each of the three kernels.  Slot k of CU c is workgroup c + kCUs*k and
+// (heaviest first) streams 2*(nqb - r/BH) 64-row blocks of the other operand.  Slot k of CU c is workgroup c + kCUs*k and
 // exists when that is below the table's length.
 const FlashPlan& flash_plan(int64_t BH, int64_t nqb, int slots) {
-    thread_local int64_t cached_bh = -1, cached_nqb = -1;
-    thread_local int cached_slots = -1;
-    thread_local FlashPlan plan;
-    if(cached_bh == BH && cached_nqb == nqb && cached_slots == slots) return plan;
+    // one cached plan per slot count (each kernel has its own)
+    thread_local int64_t cached_bh[kMaxSlots + 1] = {-1, -1, -1, -1, -1},
+                         cached_nqb[kMaxSlots + 1] = {-1, -1, -1, -1, -1};
+    thread_local FlashPlan plans[kMaxSlots + 1];
+    FlashPlan& plan = plans[slots];
+    if(cached_bh[slots] == BH && cached_nqb[slots] == nqb) return plan;
     const int n = (int)std::min<int64_t>(BH * nqb, slots * kCUs);
     std::vector<int> used(kCUs, 0);
     // (work so far, cu) of the CUs with a free slot, least work first
@@ -1684,9 +1689,8 @@ const FlashPlan& flash_plan(int64_t BH, int64_t nqb, int slots) {
         if(c + kCUs * used[c] < n) free_cus.push({top.first + 2 * (nqb - r / BH), c});
     }
     plan.n = n;
-    cached_bh = BH;
-    cached_nqb = nqb;
-    cached_slots = slots;
+    cached_bh[slots] = BH;
+    cached_nqb[slots] = nqb;
     return plan;
 }
 
