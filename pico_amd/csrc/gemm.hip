@@ -1325,9 +1325,12 @@ void launch_small_edge(const SmallEdgeParams& ep, bool vec, hipStream_t st) {
 // against 59-64 tiled; 1024^3: 69-82 against 107-117).  Eight waves split K
 // when it divides (512^3: 51-53 TFLOP/s against 40-47 with four, 24-25
 // tiled); D = the most slices in flight (4, 2 or 1) that divides a wave's
-// slice count.
+// slice count.  At K = 1024 sixteen waves of two slices each (512^2 x 1024:
+// 70-74 TFLOP/s NN and TN against 60-65 with eight; at K = 512 sixteen waves
+// of one slice measured 2-5 % slower than eight).
 SmallChoice small_choice(int64_t M, int64_t N, int64_t K) {
     if(M % 32 || N % 32 || K <= 0) return {0, 0};
+    if(K == BK * 16 * 2) return {16, 2};
     const int W = K % (BK * 8) == 0 ? 8 : K % (BK * 4) == 0 ? 4 : 0;
     if(!W) return {0, 0};
     const int64_t ns = K / (BK * W);  // odd when W is 4
@@ -1337,7 +1340,9 @@ SmallChoice small_choice(int64_t M, int64_t N, int64_t K) {
 template <bool TA, bool TB>
 void launch_small(const SmallParams& sp, SmallChoice sc, hipStream_t st) {
     const unsigned grid = (unsigned)(sp.tiles_m * sp.tiles_n);
-    if(sc.W == 8) {
+    if(sc.W == 16) {
+        gemm_small_kernel<TA, TB, 16, 2><<<grid, 1024, 0, st>>>(sp);
+    } else if(sc.W == 8) {
         if(sc.D == 4) gemm_small_kernel<TA, TB, 8, 4><<<grid, 512, 0, st>>>(sp);
         else if(sc.D == 2) gemm_small_kernel<TA, TB, 8, 2><<<grid, 512, 0, st>>>(sp);
         else gemm_small_kernel<TA, TB, 8, 1><<<grid, 512, 0, st>>>(sp);

@@ -74,13 +74,15 @@ def test_gemm_integer_bitexact(dev, ta, tb, M, N, Kd):
 
 
 @pytest.mark.parametrize("ta,tb", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
-@pytest.mark.parametrize("M,N,Kd", [(512, 512, 512), (256, 256, 256), (512, 256, 1536),
-                                    (256, 512, 384), (96, 64, 128), (32, 480, 2048)])
+@pytest.mark.parametrize("M,N,Kd", [(512, 512, 512), (512, 512, 1024), (256, 256, 256),
+                                    (512, 256, 1536), (256, 512, 384), (96, 64, 128),
+                                    (32, 480, 2048)])
 def test_gemm_small_products(dev, ta, tb, M, N, Kd):
     """Outputs of at most 256 tiles of 32 x 32 (and fewer 64 x 64 tiles than
-    CUs) run one tile per workgroup with K split over its waves: eight when
-    K/256 is whole (2, 1, 6 and 8 slices of 32 per wave here, 2, 1, 2 and 4 in
-    flight), else four (3 and 1 slices, 1 in flight).  Integer operands bit for
+    CUs) run one tile per workgroup with K split over its waves: sixteen when
+    K is 1024 (two slices of 32 per wave, both in flight), eight when K/256 is
+    whole (2, 1, 6 and 8 slices per wave here, 2, 1, 2 and 4 in flight), else
+    four (3 and 1 slices, 1 in flight).  Integer operands bit for
     bit, the beta accumulate exact, a separate X (pk_gemm_add_f32), and uniform
     operands within the fp64 bound"""
     from pico_amd import _lib
