@@ -236,6 +236,31 @@ int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void*
                        void* workspace, size_t workspace_bytes, pk_stream_t stream);
 int pk_gemm_mx8_plan(int64_t M, int64_t N, int64_t K, int* tile_m, int* tile_n, int* splits);
 
+/* bf16 operands held in HBM (no reference counterpart: pico is fp32 only).
+ * A bf16 matrix of R rows and K values per row is Rp = R rounded up to 256
+ * rows of Kv = K rounded up to 64 values, 2 bytes each (row stride 2 Kv),
+ * pk_bf16q_bytes(R, K) bytes: every value of op(X) rounded to nearest even,
+ * zeros in the padding.  pk_bf16q_quantize_f32 writes op(X) (trans as in
+ * pk_mx8_quantize_f32), pk_bf16q_quantize2_f32 both X [M, N] and X^T from one
+ * read.  pk_gemm_bf16q_f32 / _ex_f32: C [M, N] = alpha * A.B^T + beta * X for
+ * bf16 A [M, K] and B [N, K], on the bf16 matrix cores with fp32
+ * accumulation, the MX8 product's kernel and contract (workspace, K split,
+ * ldx 0 for a broadcast row).  Each product of two bf16 values is exact in
+ * fp32, so the result is the fp32 product of the rounded operands up to fp32
+ * summation error. */
+size_t pk_bf16q_bytes(int64_t R, int64_t K);
+int pk_bf16q_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, void* Q,
+                          pk_stream_t stream);
+int pk_bf16q_quantize2_f32(int64_t M, int64_t N, const float* X, int64_t ldx, void* QR, void* QT,
+                           pk_stream_t stream);
+size_t pk_gemm_bf16q_workspace(int64_t M, int64_t N, int64_t K);
+int pk_gemm_bf16q_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                      float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                      pk_stream_t stream);
+int pk_gemm_bf16q_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                         float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                         void* workspace, size_t workspace_bytes, pk_stream_t stream);
+
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
  * multiplied on the bf16 matrix cores, accumulating in fp32; C and the

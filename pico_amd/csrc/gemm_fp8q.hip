@@ -55,6 +55,11 @@ constexpr int kMaxSplits = 16;
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// operand formats of the product kernel: e4m3 with per-tensor scales, MX8
+// (e4m3 with an E8M0 scale per 32 values), bf16 (2 bytes a value, no scales)
+enum QKind { kQE4M3 = 0, kQMX8 = 1, kQBF16 = 2 };
 
 struct Fp8qParams {
     const uint8_t *A, *B;
@@ -117,6 +122,28 @@ __device__ __forceinline__ f32x16 mfma_fp8(const i32x8& a, const i32x8& b, const
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
 }
 
+// one 64-byte slice of a lane's operand rows (a, b: its 32 bytes, chunks
+// lane/32 and lane/32 + 2 of the slice) into c.  fp8: one 32x32x64 MFMA.
+// bf16: the slice holds 32 values; chunk lane/32 is values 8(lane/32)..+7,
+// the lane's share of k 0-15 on the 32x32x16 bf16 MFMA, and chunk lane/32 + 2
+// its share of k 16-31 -- two MFMAs, k 0-15 first, each taking as many
+// cycles as half the fp8 one.
+template <int KIND>
+__device__ __forceinline__ f32x16 slice_mma(const i32x8& a, const i32x8& b, const f32x16& c, int sa, int sb) {
+    if constexpr(KIND == kQBF16) {
+        // the halves by shufflevector: bit-casting the .hi swizzle of an
+        // 8-int vector compiled to its .lo here (both MFMAs read k 0-15)
+        const i32x4 al = __builtin_shufflevector(a, a, 0, 1, 2, 3), ah = __builtin_shufflevector(a, a, 4, 5, 6, 7);
+        const i32x4 bl = __builtin_shufflevector(b, b, 0, 1, 2, 3), bh = __builtin_shufflevector(b, b, 4, 5, 6, 7);
+        const f32x16 r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al),
+                                                                __builtin_bit_cast(bf16x8, bl), c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah),
+                                                      __builtin_bit_cast(bf16x8, bh), r, 0, 0, 0);
+    } else {
+        return mfma_fp8(a, b, c, sa, sb);
+    }
+}
+
 // wait until at most n of this wave's vector-memory loads are outstanding and
 // its LDS reads are done
 template <int n>
@@ -142,8 +169,9 @@ __device__ __forceinline__ void barrier_keep_loads() {
 // otherwise the scales are 2^0 and the tensor scales divide in the epilogue.
 // With splits > 1, workgroup b runs split b / tiles (nslices slices from
 // slice split * nslices) and writes its raw sums to plane `split` of P.
-template <bool MX, int WM, int WN>
+template <int KIND, int WM, int WN>
 __global__ __launch_bounds__(NT, WM * WN <= 4 ? 2 : 1) void gemm_fp8q_kernel(Fp8qParams p) {
+    constexpr bool MX = KIND == kQMX8;
     constexpr int TM = 64 * WM, TN = 64 * WN;
     static_assert(TM % 128 == 0 && TN % 128 == 0, "scale loads cover 128 rows each");
     constexpr int SCB = MX ? (TM + TN) * 2 : 0;  // scale bytes of a stage: [A rows | B rows][2]
@@ -257,7 +285,7 @@ __global__ __launch_bounds__(NT, WM * WN <= 4 ? 2 : 1) void gemm_fp8q_kernel(Fp8
 #pragma unroll
         for(int g = 0; g < NG; ++g) {
             const int i = g / WN, j = g % WN;
-            acc[i][j] = mfma_fp8(fa[i], fb[j], acc[i][j], ca[i], cb[j]);
+            acc[i][j] = slice_mma<KIND>(fa[i], fb[j], acc[i][j], ca[i], cb[j]);
 #pragma unroll
             for(int r = g * NR / NG; r < (g + 1) * NR / NG; ++r) {
                 // fragment r / 2 in the order A0, B0..B(WN-1), A1..A(WM-1); half r % 2
@@ -355,14 +383,15 @@ __global__ __launch_bounds__(NT, WM * WN <= 4 ? 2 : 1) void gemm_fp8q_kernel(Fp8
 }
 
 // every launch shape, instantiated here so that each gets its host stub
-template __global__ void gemm_fp8q_kernel<true, 4, 4>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<true, 4, 2>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<true, 2, 4>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<true, 2, 2>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<false, 4, 4>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<false, 4, 2>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<false, 2, 4>(Fp8qParams);
-template __global__ void gemm_fp8q_kernel<false, 2, 2>(Fp8qParams);
+#define PK_FP8Q_SHAPES(KIND)                                              \
+    template __global__ void gemm_fp8q_kernel<KIND, 4, 4>(Fp8qParams); \
+    template __global__ void gemm_fp8q_kernel<KIND, 4, 2>(Fp8qParams); \
+    template __global__ void gemm_fp8q_kernel<KIND, 2, 4>(Fp8qParams); \
+    template __global__ void gemm_fp8q_kernel<KIND, 2, 2>(Fp8qParams);
+PK_FP8Q_SHAPES(kQE4M3)
+PK_FP8Q_SHAPES(kQMX8)
+PK_FP8Q_SHAPES(kQBF16)
+#undef PK_FP8Q_SHAPES
 
 // C = alpha * (P[0] + P[1] + ... in plane order) + beta * X: a split product's
 // planes summed in a fixed order, so the result does not depend on timing
@@ -588,6 +617,112 @@ __global__ __launch_bounds__(NT) void quantize_dual_kernel(int64_t M, int64_t N,
     }
 }
 
+// ---- bf16 operands: fp32 rounded to nearest even, 2 bytes a value ----------
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+}
+__device__ __forceinline__ uint2 bf16_quad(f32x4 v) {
+    return make_uint2(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]));
+}
+// 32 consecutive values as 64 bytes (four 16-byte stores)
+__device__ __forceinline__ void bf16_store32(uint8_t* __restrict__ dst, const float (&v)[32]) {
+#pragma unroll
+    for(int q = 0; q < 4; ++q) {
+        i32x4 o;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) o[e] = (int)bf16_pair(v[8 * q + 2 * e], v[8 * q + 2 * e + 1]);
+        reinterpret_cast<i32x4*>(dst)[q] = o;
+    }
+}
+
+// op(X) = X: as quantize_rows_kernel, 4 values (8 bytes) a lane, 4 rows a
+// wave; writes every value of [Rp, Kv] (Kv: K padded to 64 values)
+__global__ __launch_bounds__(NT) void bf16_rows_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                       int64_t ldx, bool vec, uint8_t* __restrict__ Q,
+                                                       int64_t ldq, int64_t Kv, int64_t Rp) {
+    constexpr int RW = 4;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int64_t k = (int64_t)blockIdx.x * 256 + 4 * l;
+    const int64_t r0 = ((int64_t)blockIdx.y * 4 + w) * RW;
+    f32x4 v[RW];
+#pragma unroll
+    for(int i = 0; i < RW; ++i) v[i] = load4(X, ldx, R, K, r0 + i, k, vec);
+#pragma unroll
+    for(int i = 0; i < RW; ++i) {
+        const int64_t r = r0 + i;
+        if(r >= Rp || k >= Kv) continue;
+        *reinterpret_cast<uint2*>(Q + r * ldq + 2 * k) = bf16_quad(v[i]);
+    }
+}
+
+// op(X) = X^T (X [K, R]): a 64 (k) x 128 (r) tile through LDS as in
+// quantize_cols_kernel, then 32 consecutive k of one r per thread
+__global__ __launch_bounds__(NT) void bf16_cols_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                       int64_t ldx, bool vec, uint8_t* __restrict__ Q,
+                                                       int64_t ldq, int64_t Rp) {
+    __shared__ float tile[128][65];
+    const int t = threadIdx.x;
+    const int64_t k0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 128;
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        const int idx = t + NT * i;
+        const int kk = idx >> 5, rq = (idx & 31) * 4;
+        const f32x4 v = load4(X, ldx, K, R, k0 + kk, r0 + rq, vec);
+#pragma unroll
+        for(int c = 0; c < 4; ++c) tile[rq + c][kk] = v[c];
+    }
+    __syncthreads();
+    const int rr = t >> 1, half = t & 1;
+    const int64_t r = r0 + rr;
+    if(r >= Rp) return;
+    float v[32];
+#pragma unroll
+    for(int q = 0; q < 32; ++q) v[q] = tile[rr][32 * half + q];
+    bf16_store32(Q + r * ldq + 2 * (k0 + 32 * half), v);
+}
+
+// Both bf16 casts of one row-major X [M, N] from one read, as
+// quantize_dual_kernel: QR = X [MpR, NvR], QT = X^T [NpT, MvT]
+__global__ __launch_bounds__(NT) void bf16_dual_kernel(int64_t M, int64_t N, const float* __restrict__ X,
+                                                       int64_t ldx, bool vec, uint8_t* __restrict__ QR,
+                                                       uint8_t* __restrict__ QT) {
+    __shared__ float tile[128][65];
+    const int t = threadIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.x * 64, n0 = (int64_t)blockIdx.y * 128;
+    const int64_t MpR = round_up(M, kTileQ), NvR = round_up(N, QB);  // QR rows, values a row
+    const int64_t NpT = round_up(N, kTileQ), MvT = round_up(M, QB);  // QT rows, values a row
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        const int idx = t + NT * i;
+        const int mm = idx >> 5, nq = (idx & 31) * 4;
+        const f32x4 v = load4(X, ldx, M, N, m0 + mm, n0 + nq, vec);
+#pragma unroll
+        for(int c = 0; c < 4; ++c) tile[nq + c][mm] = v[c];
+    }
+    __syncthreads();
+    {  // QT: row n0 + t/2, values m0 + 32*(t%2) .. +31
+        const int rr = t >> 1, half = t & 1;
+        const int64_t r = n0 + rr;
+        if(r < NpT && m0 < MvT) {
+            float v[32];
+#pragma unroll
+            for(int q = 0; q < 32; ++q) v[q] = tile[rr][32 * half + q];
+            bf16_store32(QT + r * 2 * MvT + 2 * (m0 + 32 * half), v);
+        }
+    }
+    {  // QR: row m0 + t/4, values n0 + 32*(t%4) .. +31
+        const int rr = t >> 2, blk = t & 3;
+        const int64_t r = m0 + rr, k0 = n0 + 32 * blk;
+        if(r < MpR && k0 < NvR) {
+            float v[32];
+#pragma unroll
+            for(int q = 0; q < 32; ++q) v[q] = tile[32 * blk + q][rr];
+            bf16_store32(QR + r * 2 * NvR + 2 * k0, v);
+        }
+    }
+}
+
 // launch: every byte of [Rp, Kp] (row stride ldq) and, MX, every scale
 template <bool MX>
 void launch_quantize(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, const float* scale,
@@ -713,24 +848,22 @@ int fp8q_shapes(const char* name, int64_t M, int64_t N, int64_t K, int64_t lda, 
     return PK_OK;
 }
 
-void launch_fp8q(bool mx, const MxPlan& plan, const Fp8qParams& p, hipStream_t st) {
+template <int KIND>
+void launch_fp8q_kind(int shape, unsigned grid, const Fp8qParams& p, hipStream_t st) {
+    switch(shape) {
+        case 0: gemm_fp8q_kernel<KIND, 4, 4><<<grid, NT, 0, st>>>(p); break;
+        case 1: gemm_fp8q_kernel<KIND, 4, 2><<<grid, NT, 0, st>>>(p); break;
+        case 2: gemm_fp8q_kernel<KIND, 2, 4><<<grid, NT, 0, st>>>(p); break;
+        default: gemm_fp8q_kernel<KIND, 2, 2><<<grid, NT, 0, st>>>(p); break;
+    }
+}
+
+void launch_fp8q(int kind, const MxPlan& plan, const Fp8qParams& p, hipStream_t st) {
     const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
     const int shape = plan.wm == 4 ? (plan.wn == 4 ? 0 : 1) : (plan.wn == 4 ? 2 : 3);
-    if(mx) {
-        switch(shape) {
-            case 0: gemm_fp8q_kernel<true, 4, 4><<<grid, NT, 0, st>>>(p); break;
-            case 1: gemm_fp8q_kernel<true, 4, 2><<<grid, NT, 0, st>>>(p); break;
-            case 2: gemm_fp8q_kernel<true, 2, 4><<<grid, NT, 0, st>>>(p); break;
-            default: gemm_fp8q_kernel<true, 2, 2><<<grid, NT, 0, st>>>(p); break;
-        }
-    } else {
-        switch(shape) {
-            case 0: gemm_fp8q_kernel<false, 4, 4><<<grid, NT, 0, st>>>(p); break;
-            case 1: gemm_fp8q_kernel<false, 4, 2><<<grid, NT, 0, st>>>(p); break;
-            case 2: gemm_fp8q_kernel<false, 2, 4><<<grid, NT, 0, st>>>(p); break;
-            default: gemm_fp8q_kernel<false, 2, 2><<<grid, NT, 0, st>>>(p); break;
-        }
-    }
+    if(kind == kQMX8) launch_fp8q_kind<kQMX8>(shape, grid, p, st);
+    else if(kind == kQBF16) launch_fp8q_kind<kQBF16>(shape, grid, p, st);
+    else launch_fp8q_kind<kQE4M3>(shape, grid, p, st);
 }
 
 }  // namespace
@@ -748,7 +881,7 @@ extern "C" int pk_gemm_fp8q_f32(int64_t M, int64_t N, int64_t K, float alpha, co
     p.beta = beta;
     p.X = beta != 0.0f ? C : nullptr;
     p.ldx = ldc;
-    launch_fp8q(false, plan, p, pk::as_stream(stream));
+    launch_fp8q(kQE4M3, plan, p, pk::as_stream(stream));
     return pk::launch_status("pk_gemm_fp8q_f32");
 }
 
@@ -806,24 +939,31 @@ extern "C" int pk_mx8_quantize2_f32(int64_t M, int64_t N, const float* X, int64_
     return pk::launch_status("pk_mx8_quantize2_f32");
 }
 
-extern "C" int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
-                                  float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
-                                  void* workspace, size_t workspace_bytes, pk_stream_t stream) {
-    const int64_t Kp = round_up(K > 0 ? K : 1, QKPAD), Mp = round_up(M, kTileQ), Np = round_up(N, kTileQ);
-    MxPlan plan = mx8_plan(M, N, K, true);
+namespace {
+
+// An MX8 or bf16 product of operands as the casts write them: Kb bytes a row
+// (Kb = K for MX8, 2K for bf16), both padded to 128 bytes; MX8 scales follow
+// the values.
+int narrow_product(int kind, const char* name, int64_t M, int64_t N, int64_t Kb, float alpha, const void* A,
+                   const void* B, float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                   void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+    const int64_t Kp = round_up(Kb > 0 ? Kb : 1, QKPAD), Mp = round_up(M, kTileQ), Np = round_up(N, kTileQ);
+    MxPlan plan = mx8_plan(M, N, Kb, true);
     if(plan.splits > 1 && (!workspace || workspace_bytes < (size_t)plan.splits * M * N * sizeof(float)))
-        plan = mx8_plan(M, N, K, false);
+        plan = mx8_plan(M, N, Kb, false);
     Fp8qParams p;
-    if(int st = fp8q_shapes("pk_gemm_mx8_f32", M, N, K, Kp, Kp, A, B, C, ldc, plan, p)) return st;
+    if(int st = fp8q_shapes(name, M, N, Kb, Kp, Kp, A, B, C, ldc, plan, p)) return st;
     if(M == 0 || N == 0) return PK_OK;
-    if(beta != 0.0f && !X) return pk::fail("pk_gemm_mx8_f32: beta != 0 needs X");
-    if(beta != 0.0f && ldx != 0 && ldx < N) return pk::fail("pk_gemm_mx8_f32: ldx < N");
-    if(Mp * Kp / 32 > INT32_MAX || Np * Kp / 32 > INT32_MAX)
-        return pk::fail("pk_gemm_mx8_f32: scales span 2^31 bytes or more");
-    p.SA = static_cast<const uint8_t*>(A) + Mp * Kp;
-    p.SB = static_cast<const uint8_t*>(B) + Np * Kp;
-    p.sstride_a = 2 * Mp;
-    p.sstride_b = 2 * Np;
+    if(beta != 0.0f && !X) return pk::fail("%s: beta != 0 needs X", name);
+    if(beta != 0.0f && ldx != 0 && ldx < N) return pk::fail("%s: ldx < N", name);
+    if(kind == kQMX8) {
+        if(Mp * Kp / 32 > INT32_MAX || Np * Kp / 32 > INT32_MAX)
+            return pk::fail("%s: scales span 2^31 bytes or more", name);
+        p.SA = static_cast<const uint8_t*>(A) + Mp * Kp;
+        p.SB = static_cast<const uint8_t*>(B) + Np * Kp;
+        p.sstride_a = 2 * Mp;
+        p.sstride_b = 2 * Np;
+    }
     p.alpha = alpha;
     p.beta = beta;
     p.X = beta != 0.0f ? X : nullptr;
@@ -831,19 +971,94 @@ extern "C" int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, 
     hipStream_t st = pk::as_stream(stream);
     if(p.splits > 1) {
         p.P = static_cast<float*>(workspace);
-        launch_fp8q(true, plan, p, st);
-        if(int e = pk::launch_status("pk_gemm_mx8_f32")) return e;
+        launch_fp8q(kind, plan, p, st);
+        if(int e = pk::launch_status(name)) return e;
         const int64_t plane = M * N;
         const unsigned blocks = (unsigned)std::min<int64_t>((plane + NT - 1) / NT, 4 * kCUs * 8);
         fp8q_reduce_kernel<<<blocks, NT, 0, st>>>(M, N, p.splits, p.P, alpha, beta, p.X, ldx, C, ldc);
-        return pk::launch_status("pk_gemm_mx8_f32 (reduce)");
+        return pk::launch_status(name);
     }
-    launch_fp8q(true, plan, p, st);
-    return pk::launch_status("pk_gemm_mx8_f32");
+    launch_fp8q(kind, plan, p, st);
+    return pk::launch_status(name);
+}
+
+}  // namespace
+
+extern "C" int pk_gemm_mx8_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                                  float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                                  void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+    return narrow_product(kQMX8, "pk_gemm_mx8_f32", M, N, K, alpha, A, B, beta, X, ldx, C, ldc, workspace,
+                          workspace_bytes, stream);
 }
 
 extern "C" int pk_gemm_mx8_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
                                float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
                                pk_stream_t stream) {
     return pk_gemm_mx8_ex_f32(M, N, K, alpha, A, B, beta, X, ldx, C, ldc, nullptr, 0, stream);
+}
+
+// ---- bf16 operands ---------------------------------------------------------
+// A bf16 matrix of R rows and K values per row: Rp = R rounded up to 256,
+// Kv = K rounded up to 64; Rp * Kv values of 2 bytes (row stride 2 Kv bytes),
+// each fp32 value rounded to nearest even, zero padding.
+extern "C" size_t pk_bf16q_bytes(int64_t R, int64_t K) {
+    if(R <= 0 || K <= 0) return 0;
+    return (size_t)(round_up(R, kTileQ) * round_up(2 * K, QKPAD));
+}
+
+extern "C" int pk_bf16q_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, void* Q,
+                                     pk_stream_t stream) {
+    if(R < 0 || K < 0) return pk::fail("pk_bf16q_quantize_f32: negative size");
+    if(R == 0 || K == 0) return PK_OK;
+    if(!X || !Q) return pk::fail("pk_bf16q_quantize_f32: NULL pointer");
+    if(ldx < (trans ? R : K)) return pk::fail("pk_bf16q_quantize_f32: ldx below the row length");
+    if(!pk::aligned16(Q)) return pk::fail("pk_bf16q_quantize_f32: Q must be 16-byte aligned");
+    const int64_t Rp = round_up(R, kTileQ), Kv = round_up(K, QB);
+    if(Rp / 16 > 65535 || Kv / 64 > INT32_MAX) return pk::fail("pk_bf16q_quantize_f32: too large");
+    const bool vec = ldx % 4 == 0 && pk::aligned16(X);
+    uint8_t* q = static_cast<uint8_t*>(Q);
+    hipStream_t st = pk::as_stream(stream);
+    if(trans)
+        bf16_cols_kernel<<<dim3((unsigned)(Kv / 64), (unsigned)(Rp / 128)), NT, 0, st>>>(R, K, X, ldx, vec, q,
+                                                                                         2 * Kv, Rp);
+    else
+        bf16_rows_kernel<<<dim3((unsigned)((Kv + 255) / 256), (unsigned)(Rp / 16)), NT, 0, st>>>(
+            R, K, X, ldx, vec, q, 2 * Kv, Kv, Rp);
+    return pk::launch_status("pk_bf16q_quantize_f32");
+}
+
+extern "C" int pk_bf16q_quantize2_f32(int64_t M, int64_t N, const float* X, int64_t ldx, void* QR, void* QT,
+                                      pk_stream_t stream) {
+    if(M < 0 || N < 0) return pk::fail("pk_bf16q_quantize2_f32: negative size");
+    if(M == 0 || N == 0) return PK_OK;
+    if(!X || !QR || !QT) return pk::fail("pk_bf16q_quantize2_f32: NULL pointer");
+    if(ldx < N) return pk::fail("pk_bf16q_quantize2_f32: ldx below the row length");
+    if(!pk::aligned16(QR) || !pk::aligned16(QT))
+        return pk::fail("pk_bf16q_quantize2_f32: Q must be 16-byte aligned");
+    const int64_t Mg = round_up(M, kTileQ), Ng = round_up(N, kTileQ);
+    if(Mg / 64 > INT32_MAX || Ng / 128 > 65535) return pk::fail("pk_bf16q_quantize2_f32: too large");
+    const bool vec = ldx % 4 == 0 && pk::aligned16(X);
+    bf16_dual_kernel<<<dim3((unsigned)(Mg / 64), (unsigned)(Ng / 128)), NT, 0, pk::as_stream(stream)>>>(
+        M, N, X, ldx, vec, static_cast<uint8_t*>(QR), static_cast<uint8_t*>(QT));
+    return pk::launch_status("pk_bf16q_quantize2_f32");
+}
+
+extern "C" size_t pk_gemm_bf16q_workspace(int64_t M, int64_t N, int64_t K) {
+    if(M <= 0 || N <= 0 || K <= 0) return 0;
+    const MxPlan plan = mx8_plan(M, N, 2 * K, true);
+    return plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+}
+
+extern "C" int pk_gemm_bf16q_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                                    float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                                    void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+    if(K < 0) return pk::fail("pk_gemm_bf16q_f32: negative size");
+    return narrow_product(kQBF16, "pk_gemm_bf16q_f32", M, N, 2 * K, alpha, A, B, beta, X, ldx, C, ldc,
+                          workspace, workspace_bytes, stream);
+}
+
+extern "C" int pk_gemm_bf16q_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                                 float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                                 pk_stream_t stream) {
+    return pk_gemm_bf16q_ex_f32(M, N, K, alpha, A, B, beta, X, ldx, C, ldc, nullptr, 0, stream);
 }

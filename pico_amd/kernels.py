@@ -126,45 +126,112 @@ def mx8_bytes(R, Kd):
     return int(hip_lib().pk_mx8_bytes(R, Kd))
 
 
-def mx8_quantize(X, trans, out=None):
-    """op(X) (X, or X^T when trans) as an MX8 matrix: e4m3 values with an E8M0
-    scale per 32 of a row (pk_mx8_quantize_f32); a uint8 tensor"""
+def bf16q_bytes(R, Kd):
+    """bytes of a bf16 operand matrix of R rows of Kd values (pk_bf16q_bytes)"""
+    return int(hip_lib().pk_bf16q_bytes(R, Kd))
+
+
+# the narrow-operand formats: (bytes, cast, dual cast, product, product with workspace)
+_NARROW = {"mx8": (mx8_bytes, "pk_mx8_quantize_f32", "pk_mx8_quantize2_f32", "pk_gemm_mx8_f32",
+                   "pk_gemm_mx8_ex_f32"),
+           "bf16q": (bf16q_bytes, "pk_bf16q_quantize_f32", "pk_bf16q_quantize2_f32", "pk_gemm_bf16q_f32",
+                     "pk_gemm_bf16q_ex_f32")}
+
+
+def _narrow_cast(fmt, X, trans, out):
+    nbytes_fn, cast = _NARROW[fmt][0], _NARROW[fmt][1]
     _f32(X)
     ldx = _rowmajor(X, "X")
     R, Kd = (X.shape[1], X.shape[0]) if trans else (X.shape[0], X.shape[1])
-    nbytes = mx8_bytes(R, Kd)
+    nbytes = nbytes_fn(R, Kd)
     if out is None:
         out = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=X.device)
     if out.dtype != torch.uint8 or out.numel() < nbytes or not out.is_contiguous():
-        raise ValueError(f"mx8_quantize: out must be contiguous uint8 of at least {nbytes} bytes")
-    check("pk_mx8_quantize_f32", hip_lib().pk_mx8_quantize_f32(
-        R, Kd, _ptr(X), ldx, int(bool(trans)), _ptr(out), _stream()))
+        raise ValueError(f"{cast}: out must be contiguous uint8 of at least {nbytes} bytes")
+    check(cast, getattr(hip_lib(), cast)(R, Kd, _ptr(X), ldx, int(bool(trans)), _ptr(out), _stream()))
     return out
+
+
+def _narrow_cast2(fmt, X):
+    nbytes_fn, cast2 = _NARROW[fmt][0], _NARROW[fmt][2]
+    _f32(X)
+    ldx = _rowmajor(X, "X")
+    M, N = X.shape
+    QR = torch.empty(max(nbytes_fn(M, N), 1), dtype=torch.uint8, device=X.device)
+    QT = torch.empty(max(nbytes_fn(N, M), 1), dtype=torch.uint8, device=X.device)
+    check(cast2, getattr(hip_lib(), cast2)(M, N, _ptr(X), ldx, _ptr(QR), _ptr(QT), _stream()))
+    return QR, QT
+
+
+def _narrow_gemm(fmt, M, N, Kd, A8, B8, C, alpha, beta, X, ws):
+    nbytes_fn, name, name_ex = _NARROW[fmt][0], _NARROW[fmt][3], _NARROW[fmt][4]
+    _f32(C, X)
+    ldc = _rowmajor(C, "C")
+    if tuple(C.shape) != (M, N):
+        raise ValueError(f"{name}: C {tuple(C.shape)} is not {M}x{N}")
+    for what, Q, R in (("A", A8, M), ("B", B8, N)):
+        if Q.dtype != torch.uint8 or Q.numel() < nbytes_fn(R, Kd):
+            raise ValueError(f"{name}: {what} must be uint8 of at least {nbytes_fn(R, Kd)} bytes")
+    ldx = 0
+    if X is None and beta != 0.0:
+        X = C
+    if X is not None:
+        if X.dim() == 1:
+            if X.shape[0] != N:
+                raise ValueError(f"{name}: a row X must have N values")
+        else:
+            if tuple(X.shape) != (M, N):
+                raise ValueError(f"{name}: X must be [M, N] or [N]")
+            ldx = _rowmajor(X, "X")
+    if ws is None:
+        check(name, getattr(hip_lib(), name)(
+            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _stream()))
+    else:
+        check(name_ex, getattr(hip_lib(), name_ex)(
+            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _ptr(ws),
+            ws.numel() * ws.element_size(), _stream()))
+    return C
+
+
+def mx8_quantize(X, trans, out=None):
+    """op(X) (X, or X^T when trans) as an MX8 matrix: e4m3 values with an E8M0
+    scale per 32 of a row (pk_mx8_quantize_f32); a uint8 tensor"""
+    return _narrow_cast("mx8", X, trans, out)
 
 
 def mx8_quantize2(X):
     """(X as an MX8 [M, N], X^T as an MX8 [N, M]) from one read of X
     (pk_mx8_quantize2_f32)"""
-    _f32(X)
-    ldx = _rowmajor(X, "X")
-    M, N = X.shape
-    QR = torch.empty(max(mx8_bytes(M, N), 1), dtype=torch.uint8, device=X.device)
-    QT = torch.empty(max(mx8_bytes(N, M), 1), dtype=torch.uint8, device=X.device)
-    check("pk_mx8_quantize2_f32", hip_lib().pk_mx8_quantize2_f32(
-        M, N, _ptr(X), ldx, _ptr(QR), _ptr(QT), _stream()))
-    return QR, QT
+    return _narrow_cast2("mx8", X)
+
+
+def bf16q_quantize(X, trans, out=None):
+    """op(X) as a bf16 operand matrix (pk_bf16q_quantize_f32); a uint8 tensor"""
+    return _narrow_cast("bf16q", X, trans, out)
+
+
+def bf16q_quantize2(X):
+    """(X as a bf16 [M, N], X^T as a bf16 [N, M]) from one read of X
+    (pk_bf16q_quantize2_f32)"""
+    return _narrow_cast2("bf16q", X)
 
 
 def mx8_plan(M, N, Kd):
-    """(tile rows, tile cols, K splits) of the launch a shape gets (pk_gemm_mx8_plan)"""
-    tm, tn, sp = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
-    check("pk_gemm_mx8_plan", hip_lib().pk_gemm_mx8_plan(M, N, Kd, ctypes.byref(tm),
-                                                         ctypes.byref(tn), ctypes.byref(sp)))
+    """(tile rows, tile columns, K splits) pk_gemm_mx8_f32 picks with a workspace"""
+    tm, tn, sp = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check("pk_gemm_mx8_plan", hip_lib().pk_gemm_mx8_plan(M, N, Kd, ctypes.byref(tm), ctypes.byref(tn),
+                                                          ctypes.byref(sp)))
     return tm.value, tn.value, sp.value
 
 
 def mx8_workspace(M, N, Kd):
+    """workspace bytes of the K split pk_gemm_mx8_f32 picks (0: none)"""
     return int(hip_lib().pk_gemm_mx8_workspace(M, N, Kd))
+
+
+def bf16q_workspace(M, N, Kd):
+    """workspace bytes of the K split pk_gemm_bf16q_f32 picks (0: none)"""
+    return int(hip_lib().pk_gemm_bf16q_workspace(M, N, Kd))
 
 
 def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None, ws=None):
@@ -172,32 +239,12 @@ def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None, ws=None):
     [N, Kd] MX8 matrices as mx8_quantize writes them; X a [M, N] tensor, a
     [N] row added to every row, or C itself; ws: workspace for a K split
     (pk_gemm_mx8_ex_f32)"""
-    _f32(C, X)
-    ldc = _rowmajor(C, "C")
-    if tuple(C.shape) != (M, N):
-        raise ValueError(f"gemm_mx8: C {tuple(C.shape)} is not {M}x{N}")
-    for name, Q, R in (("A8", A8, M), ("B8", B8, N)):
-        if Q.dtype != torch.uint8 or Q.numel() < mx8_bytes(R, Kd):
-            raise ValueError(f"gemm_mx8: {name} must be uint8 of at least {mx8_bytes(R, Kd)} bytes")
-    ldx = 0
-    if X is None and beta != 0.0:
-        X = C
-    if X is not None:
-        if X.dim() == 1:
-            if X.shape[0] != N:
-                raise ValueError("gemm_mx8: a row X must have N values")
-        else:
-            if tuple(X.shape) != (M, N):
-                raise ValueError("gemm_mx8: X must be [M, N] or [N]")
-            ldx = _rowmajor(X, "X")
-    if ws is None:
-        check("pk_gemm_mx8_f32", hip_lib().pk_gemm_mx8_f32(
-            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _stream()))
-    else:
-        check("pk_gemm_mx8_ex_f32", hip_lib().pk_gemm_mx8_ex_f32(
-            M, N, Kd, alpha, _ptr(A8), _ptr(B8), beta, _ptr(X), ldx, _ptr(C), ldc, _ptr(ws),
-            ws.numel() * ws.element_size(), _stream()))
-    return C
+    return _narrow_gemm("mx8", M, N, Kd, A8, B8, C, alpha, beta, X, ws)
+
+
+def gemm_bf16q(M, N, Kd, A16, B16, C, alpha=1.0, beta=0.0, X=None, ws=None):
+    """gemm_mx8 for bf16 operand matrices (pk_gemm_bf16q_f32 / _ex_f32)"""
+    return _narrow_gemm("bf16q", M, N, Kd, A16, B16, C, alpha, beta, X, ws)
 
 
 def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False, _name=None):
