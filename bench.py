@@ -207,6 +207,37 @@ def mx8_section(torch, K, sizes):
     return out
 
 
+def bf16q_section(torch, K, sizes):
+    """bf16 products over bf16 operands held in HBM (pk_gemm_bf16q_f32: the
+    narrow-operand kernel with two 32x32x16 bf16 MFMAs per 64-byte slice),
+    both operands cast once and resident, replayed from a graph, and the
+    one-pass casts (pk_bf16q_quantize_f32): TFLOP/s against the 2.5 PFLOP/s
+    dense bf16 peak, cast rates in GB/s (4 bytes read + 2 written per value)"""
+    dev = torch.device("cuda:0")
+    out = {}
+    for n in sizes:
+        gen = torch.Generator(device=dev).manual_seed(n)
+        A = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        C = torch.empty(n, n, device=dev)
+        A16, B16 = K.bf16q_quantize(A, False), K.bf16q_quantize(B, True)
+        reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            K.gemm_bf16q(n, n, n, A16, B16, C)
+            torch.cuda.synchronize()
+        ms = _graph_time(lambda: K.gemm_bf16q(n, n, n, A16, B16, C), reps, 2)
+        qms = _graph_time(lambda: K.bf16q_quantize(A, False, out=A16), reps, 2)
+        qtms = _graph_time(lambda: K.bf16q_quantize(B, True, out=B16), reps, 2)
+        tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        out[str(n)] = {"tflops": round(tflops, 1), "frac_of_bf16_peak": round(tflops * 1e12 / MFMA_BF16_PEAK, 4),
+                       "us": round(ms * 1e3, 1),
+                       "cast_gbs": round(n * n * 6 / (qms * 1e-3) / 1e9, 1),
+                       "cast_transposed_gbs": round(n * n * 6 / (qtms * 1e-3) / 1e9, 1)}
+        del A, B, C, A16, B16
+    return out
+
+
 def attn_section(torch, K):
     """the fused causal attention at config 5's shapes (B 8, H 12, T 1024, hd 64),
     fp32, bf16 and fp8 products (fp8 times include the amax passes over q, k,
@@ -817,11 +848,15 @@ def main():
         # fp32 tensors (pk_gemm_bf16_f32 / pico_set_matmul_precision)
         line["bf16"] = {
             "sweep": sweep_section(torch, K, [1024, 2048, 4096, 8192], K.gemm_bf16),
+            "bf16q": bf16q_section(torch, K, [2048, 4096, 8192]),
             "train": {name: train_section(name, args.variant_steps, 3, precision=1)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
             "peak_tflops": MFMA_BF16_PEAK / 1e12,
-            "note": "bf16 products of fp32 operands (rounded to nearest even), fp32 "
-                    "accumulation; not the headline, which is fp32"}
+            "note": "sweep: bf16 products of fp32 operands (rounded to nearest even on the "
+                    "way to LDS), fp32 accumulation; bf16q: bf16 operands cast once and "
+                    "resident (pk_gemm_bf16q_f32); train: pico_set_matmul_precision("
+                    "PICO_MATMUL_BF16) on the fp32-operand kernels; not the headline, which "
+                    "is fp32"}
         # three bf16 products per fp32 one (hi/lo operand split): within ~1e-5 of
         # fp32; TFLOP/s counted as fp32 products (2n^3), not bf16 instructions
         line["bf16x3"] = {
@@ -880,6 +915,8 @@ def main():
             summary[f"config5_{prec}_ms_per_step"] = t5["ms_per_step"]
     if "fp8" in line and "mx8" in line["fp8"]:
         summary["mx8_tflops"] = {n: r["tflops"] for n, r in line["fp8"]["mx8"].items()}
+    if "bf16" in line and "bf16q" in line["bf16"]:
+        summary["bf16q_tflops"] = {n: r["tflops"] for n, r in line["bf16"]["bf16q"].items()}
     line["summary"] = summary
     print(json.dumps(line), flush=True)
 
