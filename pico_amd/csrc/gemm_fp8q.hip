@@ -802,6 +802,14 @@ MxPlan mx8_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
             const int64_t rounds = (wgs + kCUs * c.slots - 1) / (kCUs * c.slots);
             double t = per_cu * per * c.slice_us * (c.slots > 1 && wgs > kCUs ? shared : 1.0) +
                        rounds * round_us + (double)M * N * 4 / hbm * 1e6;
+            // fewer workgroups than CUs: charged half again.  The fitted costs
+            // come from launches alone on the GPU, where idle CUs cost nothing;
+            // in a training step the other stream's work runs beside every
+            // product, and tiles that give each CU a workgroup measured faster
+            // there ([8192, 768] outputs on 128x128 rather than 256x128 tiles,
+            // the weight gradients on smaller tiles: config-5 fp8 step 14.76 ->
+            // 14.23-14.26 ms, same box, alternating)
+            if(wgs < kCUs) t *= 1.5;
             if(splits > 1) t += (splits + 1.0) * M * N * 4 / hbm * 1e6 + launch_us;
             if(t < best_t) {
                 best_t = t;
