@@ -1,6 +1,7 @@
 /*
  * oracle/way2_glue.c -- test infrastructure: the few helpers the "Way 2"
- * binding of INTEGRATION.md needs in pico's own sources (linked with a copy of
+ * binding (pico's own GPU op seams calling libpico_amd.so) needs in pico's own
+ * sources (linked with a copy of
  * them patched by way2_patch.py into oracle/_ref/libpico_way2.so), plus entry
  * points a test uses to make GPU tensors the way pico would and to move their
  * values.  Not part of the product.

@@ -1,10 +1,11 @@
-"""Applies the "Way 2" binding of INTEGRATION.md to a COPY of pico's sources
+"""Applies the "Way 2" binding (pico's own GPU op seams calling libpico_amd.so)
+to a COPY of pico's sources
 (test infrastructure; the result is linked into oracle/_ref/libpico_way2.so by
 oracle/Makefile's `way2` target, never into the product).
 
     python3 way2_patch.py <copy of the reference's src/>
 
-It edits, in place, exactly the seams INTEGRATION.md names, by pattern:
+It edits, in place, exactly these seams, by pattern:
 
 * src/ops.c: pico_add / pico_sub / pico_mul replace their commented-out GPU
   stub (ops.c:42-44, 86-88, 130-132) with the GPU twin of libpico_amd.so, and

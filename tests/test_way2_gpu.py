@@ -1,4 +1,4 @@
-"""Way 2 of INTEGRATION.md, end to end: pico's OWN op layer on GPU tensors.
+"""Way 2 end to end: pico's OWN op layer on GPU tensors.
 
 oracle/_ref/libpico_way2.so is the reference's src/ compiled with the Way 2
 binding applied by oracle/way2_patch.py (pico_add / pico_sub / pico_mul /
