@@ -536,7 +536,13 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const TileJob& j
                 float v = j.alpha * acc[i][jj][r];
                 float* c = j.C + row * j.ldc + col;
                 if(j.beta != 0.0f) v += j.beta * *c;
-                *c = v;
+                // 64x64 tiles (products of about 1024^2 outputs, where the
+                // launch's end is a large share of its time) store C
+                // non-temporally: 1024^3 1.1-1.6 % and 768^3 0.6-1.1 % faster,
+                // config-4 and config-5 steps unchanged (same box, alternating);
+                // for every tile they cost a config-5 step 0.05 ms
+                if constexpr(TM * TN == 1) __builtin_nontemporal_store(v, c);
+                else *c = v;
             }
         }
 }
