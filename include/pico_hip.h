@@ -526,7 +526,9 @@ int pk_causal_softmax_bwd_f32(int64_t BH, int64_t T, const float* P, const float
  * one row made in increasing i (the sequential loop's order: deterministic).
  * An id outside [0,vocab) reads as a zero row and adds nothing.  The backward
  * needs pk_embed_bwd_workspace(n) bytes of device workspace; it groups equal
- * ids with O(n^2) compares (microseconds at n ~ 10^4). */
+ * ids with a stable radix sort of (id, position) pairs (8 bits a pass), so
+ * each row's adds keep their position order, then sums each run of equal ids
+ * into its row. */
 int pk_embed_fwd_f32(int64_t n, int64_t d, int64_t vocab, const int32_t* ids, const float* table,
                      float* out, pk_stream_t stream);
 size_t pk_embed_bwd_workspace(int64_t n);
