@@ -126,10 +126,15 @@ def _device_ids(P, arena, arr):
     return d
 
 
-def test_gpt_fp8_graph_replay_matches_eager(P):
+@pytest.mark.parametrize("cfg", [
+    dict(vocab=96, d_model=64, n_layers=2, n_heads=2, d_ff=160, batch=2, seq_len=64),
+    # the benchmark's 12-layer configuration (bench.py's fp8 step)
+    pytest.param(dict(vocab=32000, d_model=768, n_layers=12, n_heads=12, d_ff=2048, batch=8,
+                      seq_len=1024), marks=[pytest.mark.slow, pytest.mark.timeout(300)]),
+])
+def test_gpt_fp8_graph_replay_matches_eager(P, cfg):
     """weights change on the device inside every replay (the captured AdamW);
     each replay recasts them, so replays equal eager steps bit for bit"""
-    cfg = dict(vocab=96, d_model=64, n_layers=2, n_heads=2, d_ff=160, batch=2, seq_len=64)
     batches = []
     for s in range(5):
         seq = O.labels(cfg["batch"] * (cfg["seq_len"] + 1), 90 + s, cfg["vocab"])
@@ -154,7 +159,7 @@ def test_gpt_fp8_graph_replay_matches_eager(P):
             return loss
 
         losses = []
-        with P.arena(1 << 28) as ar:
+        with P.arena(1 << 30) as ar:
             loss = step()
             losses.append(float(P.data(loss)[0]))
             P.reset(ar)
@@ -187,7 +192,9 @@ def test_gpt_fp8_graph_replay_matches_eager(P):
         P.lib.arena_destroy(ids_arena)
         results.append((np.array(losses), final, after))
     (l0, p0, a0), (l1, p1, a1) = results
-    assert np.all(np.isfinite(l0)) and l0[-1] < l0[0]
+    # uniform random targets: the small model fits them, the 32000-way one stays
+    # near ln(vocab) over five steps
+    assert np.all(np.isfinite(l0)) and (l0[-1] < l0[0] or cfg["vocab"] > 1000)
     assert np.array_equal(l0, l1)
     assert a0 == a1
     for x, y in zip(p0, p1):
