@@ -238,6 +238,38 @@ def bf16q_section(torch, K, sizes):
     return out
 
 
+def bf16x3q_section(torch, K, sizes):
+    """fp32 products from three bf16 ones over split-bf16 operands held in HBM
+    (pk_gemm_bf16x3q_f32: hi and lo bf16 parts of every value, cast once and
+    resident, the narrow-operand kernel with ahi.bhi + ahi.blo + alo.bhi per 16
+    values of K), replayed from a graph, and the one-pass casts
+    (pk_bf16x3q_quantize_f32): TFLOP/s counted as fp32 products (2n^3), cast
+    rates in GB/s (4 bytes read + 4 written per value)"""
+    dev = torch.device("cuda:0")
+    out = {}
+    for n in sizes:
+        gen = torch.Generator(device=dev).manual_seed(n)
+        A = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        B = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
+        C = torch.empty(n, n, device=dev)
+        A3, B3 = K.bf16x3q_quantize(A, False), K.bf16x3q_quantize(B, True)
+        reps = 20 if n <= 2048 else 8 if n <= 4096 else 4
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            K.gemm_bf16x3q(n, n, n, A3, B3, C)
+            torch.cuda.synchronize()
+        ms = _graph_time(lambda: K.gemm_bf16x3q(n, n, n, A3, B3, C), reps, 2)
+        qms = _graph_time(lambda: K.bf16x3q_quantize(A, False, out=A3), reps, 2)
+        qtms = _graph_time(lambda: K.bf16x3q_quantize(B, True, out=B3), reps, 2)
+        tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        out[str(n)] = {"tflops": round(tflops, 1), "x_fp32_peak": round(tflops * 1e12 / MFMA_FP32_PEAK, 3),
+                       "us": round(ms * 1e3, 1),
+                       "cast_gbs": round(n * n * 8 / (qms * 1e-3) / 1e9, 1),
+                       "cast_transposed_gbs": round(n * n * 8 / (qtms * 1e-3) / 1e9, 1)}
+        del A, B, C, A3, B3
+    return out
+
+
 def attn_section(torch, K):
     """the fused causal attention at config 5's shapes (B 8, H 12, T 1024, hd 64),
     fp32, bf16 and fp8 products (fp8 times include the amax passes over q, k,
@@ -861,11 +893,13 @@ def main():
         # fp32; TFLOP/s counted as fp32 products (2n^3), not bf16 instructions
         line["bf16x3"] = {
             "sweep": sweep_section(torch, K, [2048, 4096, 8192], K.gemm_bf16x3),
+            "bf16x3q": bf16x3q_section(torch, K, [2048, 4096, 8192]),
             "train": {name: train_section(name, args.variant_steps, 3, precision=2)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
             "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
                     "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "
-                    "fp32; not the headline, which is fp32"}
+                    "fp32; bf16x3q: the same products over split-bf16 operands cast once and "
+                    "resident (pk_gemm_bf16x3q_f32); not the headline, which is fp32"}
     if "fp8" in sections:
         # e4m3 operands (clamped to +-448, nearest even), fp32 accumulation and
         # tensors: far outside the fp32 parity contract, for experiments
@@ -917,6 +951,8 @@ def main():
         summary["mx8_tflops"] = {n: r["tflops"] for n, r in line["fp8"]["mx8"].items()}
     if "bf16" in line and "bf16q" in line["bf16"]:
         summary["bf16q_tflops"] = {n: r["tflops"] for n, r in line["bf16"]["bf16q"].items()}
+    if "bf16x3" in line:
+        summary["bf16x3q_tflops"] = {n: r["tflops"] for n, r in line["bf16x3"]["bf16x3q"].items()}
     line["summary"] = summary
     print(json.dumps(line), flush=True)
 

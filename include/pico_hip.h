@@ -261,6 +261,32 @@ int pk_gemm_bf16q_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const voi
                          float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
                          void* workspace, size_t workspace_bytes, pk_stream_t stream);
 
+/* Split-bf16 operands held in HBM, for fp32 products from three bf16 ones (no
+ * reference counterpart: they replace the fp32 multiplies of
+ * src/kernels/cpu_kernels.h:46-55 within the fp32 parity bound).  A value x is
+ * kept as hi = bf16(x) and lo = bf16(x - hi), both nearest even.  A matrix of
+ * R rows and K values per row is Rp = R rounded up to 256 rows of Kv = K
+ * rounded up to 32 values, each row Kv / 16 groups of 64 bytes -- a group's 16
+ * hi parts, then their 16 lo parts -- (row stride 4 Kv bytes,
+ * pk_bf16x3q_bytes(R, K) bytes), zeros in the padding.  pk_bf16x3q_quantize_f32
+ * writes op(X) (trans as in pk_mx8_quantize_f32).  pk_gemm_bf16x3q_f32 /
+ * _ex_f32: C [M, N] = alpha * A.B^T + beta * X for split A [M, K] and B [N, K]
+ * as ahi.bhi + ahi.blo + alo.bhi per 16 values of K on the bf16 matrix cores,
+ * accumulating in fp32 (the MX8 product's kernel and contract).  That is
+ * pk_gemm_bf16x3_f32's arithmetic in its order, so an unsplit product equals
+ * pk_gemm_bf16x3_f32 without a workspace bit for bit: within about 1e-5 of
+ * the fp32 product. */
+size_t pk_bf16x3q_bytes(int64_t R, int64_t K);
+int pk_bf16x3q_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, void* Q,
+                            pk_stream_t stream);
+size_t pk_gemm_bf16x3q_workspace(int64_t M, int64_t N, int64_t K);
+int pk_gemm_bf16x3q_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                        float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                        pk_stream_t stream);
+int pk_gemm_bf16x3q_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                           float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                           void* workspace, size_t workspace_bytes, pk_stream_t stream);
+
 /* The same products with bf16 multiplies (no reference counterpart: pico is
  * fp32 only): op(A) and op(B) are rounded to bf16 (nearest even) and
  * multiplied on the bf16 matrix cores, accumulating in fp32; C and the

@@ -68,6 +68,12 @@ PK_SIGNATURES = {
     "pk_gemm_bf16q_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p],
     "pk_gemm_bf16q_ex_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p,
                              c_size, c_p],
+    "pk_bf16x3q_bytes": [c_i64, c_i64],
+    "pk_bf16x3q_quantize_f32": [c_i64, c_i64, c_p, c_i64, c_int, c_p, c_p],
+    "pk_gemm_bf16x3q_workspace": [c_i64, c_i64, c_i64],
+    "pk_gemm_bf16x3q_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p],
+    "pk_gemm_bf16x3q_ex_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p,
+                               c_size, c_p],
     "pk_gemm_mx8_ex_f32": [c_i64, c_i64, c_i64, c_f, c_p, c_p, c_f, c_p, c_i64, c_p, c_i64, c_p,
                            c_size, c_p],
     "pk_gemm_mx8_plan": [c_i64, c_i64, c_i64, ctypes.POINTER(c_int), ctypes.POINTER(c_int),
@@ -143,7 +149,8 @@ _RESTYPES = {"pk_last_error": ctypes.c_char_p, "pk_rmsnorm_bwd_workspace": c_siz
              "pk_embed_bwd_workspace": c_size, "pk_gemm_noalloc_scratch_bytes": c_size,
              "pk_fp8_quantized_bytes": c_size, "pk_mx8_bytes": c_size,
              "pk_gemm_mx8_workspace": c_size, "pk_bf16q_bytes": c_size,
-             "pk_gemm_bf16q_workspace": c_size}
+             "pk_gemm_bf16q_workspace": c_size, "pk_bf16x3q_bytes": c_size,
+             "pk_gemm_bf16x3q_workspace": c_size}
 
 _hip = None
 

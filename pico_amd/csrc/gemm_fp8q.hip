@@ -58,8 +58,9 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // operand formats of the product kernel: e4m3 with per-tensor scales, MX8
-// (e4m3 with an E8M0 scale per 32 values), bf16 (2 bytes a value, no scales)
-enum QKind { kQE4M3 = 0, kQMX8 = 1, kQBF16 = 2 };
+// (e4m3 with an E8M0 scale per 32 values), bf16 (2 bytes a value, no scales),
+// split bf16 (a value as hi = bf16(x) and lo = bf16(x - hi): 4 bytes a value)
+enum QKind { kQE4M3 = 0, kQMX8 = 1, kQBF16 = 2, kQBF16X3 = 3 };
 
 struct Fp8qParams {
     const uint8_t *A, *B;
@@ -127,10 +128,23 @@ __device__ __forceinline__ f32x16 mfma_fp8(const i32x8& a, const i32x8& b, const
 // bf16: the slice holds 32 values; chunk lane/32 is values 8(lane/32)..+7,
 // the lane's share of k 0-15 on the 32x32x16 bf16 MFMA, and chunk lane/32 + 2
 // its share of k 16-31 -- two MFMAs, k 0-15 first, each taking as many
-// cycles as half the fp8 one.
+// cycles as half the fp8 one.  Split bf16: the slice holds 16 values, their
+// hi parts in chunks 0-1 and lo parts in chunks 2-3, so chunk lane/32 is the
+// lane's hi share of k 0-15 and chunk lane/32 + 2 its lo share -- three
+// MFMAs, hi.hi + hi.lo + lo.hi (lo.lo is below 2^-16 of the product), the
+// order pk_gemm_bf16x3_f32 takes them in.
 template <int KIND>
 __device__ __forceinline__ f32x16 slice_mma(const i32x8& a, const i32x8& b, const f32x16& c, int sa, int sb) {
-    if constexpr(KIND == kQBF16) {
+    if constexpr(KIND == kQBF16X3) {
+        const i32x4 ah = __builtin_shufflevector(a, a, 0, 1, 2, 3), al = __builtin_shufflevector(a, a, 4, 5, 6, 7);
+        const i32x4 bh = __builtin_shufflevector(b, b, 0, 1, 2, 3), bl = __builtin_shufflevector(b, b, 4, 5, 6, 7);
+        f32x16 r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah),
+                                                          __builtin_bit_cast(bf16x8, bh), c, 0, 0, 0);
+        r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah), __builtin_bit_cast(bf16x8, bl),
+                                                    r, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al),
+                                                      __builtin_bit_cast(bf16x8, bh), r, 0, 0, 0);
+    } else if constexpr(KIND == kQBF16) {
         // the halves by shufflevector: bit-casting the .hi swizzle of an
         // 8-int vector compiled to its .lo here (both MFMAs read k 0-15)
         const i32x4 al = __builtin_shufflevector(a, a, 0, 1, 2, 3), ah = __builtin_shufflevector(a, a, 4, 5, 6, 7);
@@ -391,6 +405,7 @@ __global__ __launch_bounds__(NT, WM * WN <= 4 ? 2 : 1) void gemm_fp8q_kernel(Fp8
 PK_FP8Q_SHAPES(kQE4M3)
 PK_FP8Q_SHAPES(kQMX8)
 PK_FP8Q_SHAPES(kQBF16)
+PK_FP8Q_SHAPES(kQBF16X3)
 #undef PK_FP8Q_SHAPES
 
 // C = alpha * (P[0] + P[1] + ... in plane order) + beta * X: a split product's
@@ -723,6 +738,84 @@ __global__ __launch_bounds__(NT) void bf16_dual_kernel(int64_t M, int64_t N, con
     }
 }
 
+// ---- split-bf16 operands: hi = bf16(x), lo = bf16(x - hi), nearest even ----
+// A row holds its values in groups of 16: the group's 16 hi parts (32 bytes),
+// then its 16 lo parts, so a 64-byte slice row is one group
+__device__ __forceinline__ uint32_t split_pair(float a, float b, uint32_t& lo) {
+    const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(a - (float)ha)) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(b - (float)hb)) << 16);
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+// one group (16 consecutive values) as its 64 bytes
+__device__ __forceinline__ void split_store16(uint8_t* __restrict__ dst, const float* v) {
+    i32x4 h[2], l[2];
+#pragma unroll
+    for(int q = 0; q < 8; ++q) {
+        uint32_t lo;
+        h[q >> 2][q & 3] = (int)split_pair(v[2 * q], v[2 * q + 1], lo);
+        l[q >> 2][q & 3] = (int)lo;
+    }
+    i32x4* d = reinterpret_cast<i32x4*>(dst);
+    d[0] = h[0];
+    d[1] = h[1];
+    d[2] = l[0];
+    d[3] = l[1];
+}
+
+// op(X) = X: as bf16_rows_kernel, 4 values a lane (8 bytes of hi and 8 of
+// lo in their group), 4 rows a wave; writes every value of [Rp, Kv]
+__global__ __launch_bounds__(NT) void split_rows_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                        int64_t ldx, bool vec, uint8_t* __restrict__ Q,
+                                                        int64_t ldq, int64_t Kv, int64_t Rp) {
+    constexpr int RW = 4;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int64_t k = (int64_t)blockIdx.x * 256 + 4 * l;
+    const int64_t r0 = ((int64_t)blockIdx.y * 4 + w) * RW;
+    f32x4 v[RW];
+#pragma unroll
+    for(int i = 0; i < RW; ++i) v[i] = load4(X, ldx, R, K, r0 + i, k, vec);
+    const int64_t at = 64 * (k >> 4) + 2 * (k & 15);
+#pragma unroll
+    for(int i = 0; i < RW; ++i) {
+        const int64_t r = r0 + i;
+        if(r >= Rp || k >= Kv) continue;
+        uint32_t l0, l1;
+        const uint2 hi = make_uint2(split_pair(v[i][0], v[i][1], l0), split_pair(v[i][2], v[i][3], l1));
+        uint8_t* row = Q + r * ldq;
+        *reinterpret_cast<uint2*>(row + at) = hi;
+        *reinterpret_cast<uint2*>(row + at + 32) = make_uint2(l0, l1);
+    }
+}
+
+// op(X) = X^T (X [K, R]): a 64 (k) x 128 (r) tile through LDS as in
+// bf16_cols_kernel, then two groups (32 consecutive k) of one r per thread
+__global__ __launch_bounds__(NT) void split_cols_kernel(int64_t R, int64_t K, const float* __restrict__ X,
+                                                        int64_t ldx, bool vec, uint8_t* __restrict__ Q,
+                                                        int64_t ldq, int64_t Kv, int64_t Rp) {
+    __shared__ float tile[128][65];
+    const int t = threadIdx.x;
+    const int64_t k0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 128;
+#pragma unroll
+    for(int i = 0; i < 8; ++i) {
+        const int idx = t + NT * i;
+        const int kk = idx >> 5, rq = (idx & 31) * 4;
+        const f32x4 v = load4(X, ldx, K, R, k0 + kk, r0 + rq, vec);
+#pragma unroll
+        for(int c = 0; c < 4; ++c) tile[rq + c][kk] = v[c];
+    }
+    __syncthreads();
+    const int rr = t >> 1, half = t & 1;
+    const int64_t r = r0 + rr, kh = k0 + 32 * half;
+    if(r >= Rp || kh >= Kv) return;  // Kv is a multiple of 32: a half is all in or all out
+    float v[32];
+#pragma unroll
+    for(int q = 0; q < 32; ++q) v[q] = tile[rr][32 * half + q];
+    uint8_t* dst = Q + r * ldq + 4 * kh;
+    split_store16(dst, v);
+    split_store16(dst + 64, v + 16);
+}
+
 // launch: every byte of [Rp, Kp] (row stride ldq) and, MX, every scale
 template <bool MX>
 void launch_quantize(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, const float* scale,
@@ -871,6 +964,7 @@ void launch_fp8q(int kind, const MxPlan& plan, const Fp8qParams& p, hipStream_t 
     const int shape = plan.wm == 4 ? (plan.wn == 4 ? 0 : 1) : (plan.wn == 4 ? 2 : 3);
     if(kind == kQMX8) launch_fp8q_kind<kQMX8>(shape, grid, p, st);
     else if(kind == kQBF16) launch_fp8q_kind<kQBF16>(shape, grid, p, st);
+    else if(kind == kQBF16X3) launch_fp8q_kind<kQBF16X3>(shape, grid, p, st);
     else launch_fp8q_kind<kQE4M3>(shape, grid, p, st);
 }
 
@@ -1069,4 +1163,55 @@ extern "C" int pk_gemm_bf16q_f32(int64_t M, int64_t N, int64_t K, float alpha, c
                                  float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
                                  pk_stream_t stream) {
     return pk_gemm_bf16q_ex_f32(M, N, K, alpha, A, B, beta, X, ldx, C, ldc, nullptr, 0, stream);
+}
+
+// ---- split-bf16 operands (three bf16 products per fp32 one) -----------------
+// A split matrix of R rows and K values per row: Rp = R rounded up to 256,
+// Kv = K rounded up to 32; each row is Kv / 16 groups of 64 bytes (16 hi parts,
+// then their 16 lo parts), row stride 4 Kv bytes, zero padding.
+extern "C" size_t pk_bf16x3q_bytes(int64_t R, int64_t K) {
+    if(R <= 0 || K <= 0) return 0;
+    return (size_t)(round_up(R, kTileQ) * round_up(4 * K, QKPAD));
+}
+
+extern "C" int pk_bf16x3q_quantize_f32(int64_t R, int64_t K, const float* X, int64_t ldx, int trans, void* Q,
+                                       pk_stream_t stream) {
+    if(R < 0 || K < 0) return pk::fail("pk_bf16x3q_quantize_f32: negative size");
+    if(R == 0 || K == 0) return PK_OK;
+    if(!X || !Q) return pk::fail("pk_bf16x3q_quantize_f32: NULL pointer");
+    if(ldx < (trans ? R : K)) return pk::fail("pk_bf16x3q_quantize_f32: ldx below the row length");
+    if(!pk::aligned16(Q)) return pk::fail("pk_bf16x3q_quantize_f32: Q must be 16-byte aligned");
+    const int64_t Rp = round_up(R, kTileQ), Kv = round_up(K, 32);
+    if(Rp / 16 > 65535 || Kv / 64 > INT32_MAX) return pk::fail("pk_bf16x3q_quantize_f32: too large");
+    const bool vec = ldx % 4 == 0 && pk::aligned16(X);
+    uint8_t* q = static_cast<uint8_t*>(Q);
+    hipStream_t st = pk::as_stream(stream);
+    if(trans)
+        split_cols_kernel<<<dim3((unsigned)((Kv + 63) / 64), (unsigned)(Rp / 128)), NT, 0, st>>>(R, K, X, ldx, vec,
+                                                                                                 q, 4 * Kv, Kv, Rp);
+    else
+        split_rows_kernel<<<dim3((unsigned)((Kv + 255) / 256), (unsigned)(Rp / 16)), NT, 0, st>>>(
+            R, K, X, ldx, vec, q, 4 * Kv, Kv, Rp);
+    return pk::launch_status("pk_bf16x3q_quantize_f32");
+}
+
+extern "C" size_t pk_gemm_bf16x3q_workspace(int64_t M, int64_t N, int64_t K) {
+    if(M <= 0 || N <= 0 || K <= 0) return 0;
+    const MxPlan plan = mx8_plan(M, N, 4 * K, true);
+    return plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+}
+
+extern "C" int pk_gemm_bf16x3q_ex_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+                                      const void* B, float beta, const float* X, int64_t ldx, float* C,
+                                      int64_t ldc, void* workspace, size_t workspace_bytes,
+                                      pk_stream_t stream) {
+    if(K < 0) return pk::fail("pk_gemm_bf16x3q_f32: negative size");
+    return narrow_product(kQBF16X3, "pk_gemm_bf16x3q_f32", M, N, 4 * K, alpha, A, B, beta, X, ldx, C, ldc,
+                          workspace, workspace_bytes, stream);
+}
+
+extern "C" int pk_gemm_bf16x3q_f32(int64_t M, int64_t N, int64_t K, float alpha, const void* A, const void* B,
+                                   float beta, const float* X, int64_t ldx, float* C, int64_t ldc,
+                                   pk_stream_t stream) {
+    return pk_gemm_bf16x3q_ex_f32(M, N, K, alpha, A, B, beta, X, ldx, C, ldc, nullptr, 0, stream);
 }

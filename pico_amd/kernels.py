@@ -131,11 +131,18 @@ def bf16q_bytes(R, Kd):
     return int(hip_lib().pk_bf16q_bytes(R, Kd))
 
 
+def bf16x3q_bytes(R, Kd):
+    """bytes of a split-bf16 operand matrix of R rows of Kd values (pk_bf16x3q_bytes)"""
+    return int(hip_lib().pk_bf16x3q_bytes(R, Kd))
+
+
 # the narrow-operand formats: (bytes, cast, dual cast, product, product with workspace)
 _NARROW = {"mx8": (mx8_bytes, "pk_mx8_quantize_f32", "pk_mx8_quantize2_f32", "pk_gemm_mx8_f32",
                    "pk_gemm_mx8_ex_f32"),
            "bf16q": (bf16q_bytes, "pk_bf16q_quantize_f32", "pk_bf16q_quantize2_f32", "pk_gemm_bf16q_f32",
-                     "pk_gemm_bf16q_ex_f32")}
+                     "pk_gemm_bf16q_ex_f32"),
+           "bf16x3q": (bf16x3q_bytes, "pk_bf16x3q_quantize_f32", None, "pk_gemm_bf16x3q_f32",
+                       "pk_gemm_bf16x3q_ex_f32")}
 
 
 def _narrow_cast(fmt, X, trans, out):
@@ -216,6 +223,12 @@ def bf16q_quantize2(X):
     return _narrow_cast2("bf16q", X)
 
 
+def bf16x3q_quantize(X, trans, out=None):
+    """op(X) as a split-bf16 operand matrix (hi and lo bf16 parts of every
+    value, pk_bf16x3q_quantize_f32); a uint8 tensor"""
+    return _narrow_cast("bf16x3q", X, trans, out)
+
+
 def mx8_plan(M, N, Kd):
     """(tile rows, tile columns, K splits) pk_gemm_mx8_f32 picks with a workspace"""
     tm, tn, sp = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
@@ -245,6 +258,17 @@ def gemm_mx8(M, N, Kd, A8, B8, C, alpha=1.0, beta=0.0, X=None, ws=None):
 def gemm_bf16q(M, N, Kd, A16, B16, C, alpha=1.0, beta=0.0, X=None, ws=None):
     """gemm_mx8 for bf16 operand matrices (pk_gemm_bf16q_f32 / _ex_f32)"""
     return _narrow_gemm("bf16q", M, N, Kd, A16, B16, C, alpha, beta, X, ws)
+
+
+def bf16x3q_workspace(M, N, Kd):
+    """workspace bytes of the K split pk_gemm_bf16x3q_f32 picks (0: none)"""
+    return int(hip_lib().pk_gemm_bf16x3q_workspace(M, N, Kd))
+
+
+def gemm_bf16x3q(M, N, Kd, A, B, C, alpha=1.0, beta=0.0, X=None, ws=None):
+    """gemm_mx8 for split-bf16 operand matrices: three bf16 products per fp32
+    one (pk_gemm_bf16x3q_f32 / _ex_f32)"""
+    return _narrow_gemm("bf16x3q", M, N, Kd, A, B, C, alpha, beta, X, ws)
 
 
 def gemm_bf16(ta, tb, A, B, C, alpha=1.0, beta=0.0, ws=None, split=False, _name=None):
