@@ -424,6 +424,14 @@ int pk_adamw_multi_f32(int64_t nchunks, const PkAdamwChunk* chunks, float lr, fl
 int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, int64_t ldz,
                         const int32_t* labels, float* loss_rows, float* dlogits, int64_t ldd,
                         float scale, const float* scale_dev, int flags, pk_stream_t stream);
+/* pk_xent_fwd_bwd_f32 (scale_dev NULL) and out[0] (+)= mean_scale * sum of the
+ * loss rows, summed as pk_reduce_sum_f32 sums them (flags bit 0: dlogits
+ * accumulate, bit 1: out accumulates).  Up to 1024 rows of at most 64
+ * classes take one launch; above that loss_rows is required and it is the
+ * two calls. */
+int pk_xent_mean_f32(int64_t R, int64_t V, const float* logits, int64_t ldz, const int32_t* labels,
+                     float* loss_rows, float* dlogits, int64_t ldd, float scale, int flags,
+                     float mean_scale, float* out, pk_stream_t stream);
 /* idx[r] = argmax_j x[r,j]: first maximum wins; a NaN is the maximum (first NaN wins) */
 int pk_argmax_f32(int64_t R, int64_t V, const float* x, int64_t ldx, int32_t* idx,
                   pk_stream_t stream);

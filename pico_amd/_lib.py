@@ -107,6 +107,7 @@ PK_SIGNATURES = {
     "pk_adamw_multi_f32": [c_i64, c_p, c_f, c_f, c_f, c_f, c_f, c_p, c_p],
     "pk_xent_fwd_bwd_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p, c_i64, c_f, c_p, c_int,
                             c_p],
+    "pk_xent_mean_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p, c_p, c_i64, c_f, c_int, c_f, c_p, c_p],
     "pk_argmax_f32": [c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "pk_rmsnorm_fwd_f32": [c_i64, c_i64, c_f, c_p, c_p, c_p, c_p, c_p],
     "pk_rmsnorm_bwd_workspace": [c_i64, c_i64],

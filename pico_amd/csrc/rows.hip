@@ -116,6 +116,53 @@ __global__ __launch_bounds__(NT) void xent_any_kernel(int64_t V, const float* __
     }
 }
 
+// Tiny problems (V <= 64, R <= 1024: a classifier head): every row in one
+// workgroup, a wave per row with one class per lane, and the rows' mean in
+// the same launch, summed as pk_reduce_sum_f32 sums.  The per-row arithmetic
+// is xent_any_kernel's (its block reductions over one wave's values and
+// zeros), so rows and gradients are the same bits.
+constexpr int kTinyRows = 1024, kTinyV = 64;
+__global__ __launch_bounds__(1024) void xent_tiny_kernel(int64_t R, int64_t V, const float* __restrict__ logits,
+                                                         int64_t ldz, const int32_t* __restrict__ labels,
+                                                         float* __restrict__ loss_rows,
+                                                         float* __restrict__ dlogits, int64_t ldd,
+                                                         float scale_in, const float* __restrict__ scale_dev,
+                                                         int accum, float mean_scale, float* __restrict__ out,
+                                                         int out_accum) {
+    __shared__ float rows[kTinyRows];
+    __shared__ float red[16];
+    const float scale = scale_dev ? scale_in * *scale_dev : scale_in;
+    const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
+    for(int64_t r = w; r < R; r += 16) {
+        const float* z = logits + r * ldz;
+        const float x = c < V ? z[c] : kNegInf;
+        const float m = pk::wave_max(x);
+        // a -inf logit adds nothing (an all -inf row: lse = -inf, as xent_any_kernel)
+        const float s = pk::wave_sum(c < V && x != kNegInf ? expf(x - m) : 0.0f);
+        const float lse = m + logf(s);
+        const int32_t y = labels[r];
+        const bool ok = y >= 0 && y < V;
+        if(c == 0) {
+            const float loss = ok ? lse - z[y] : NAN;
+            rows[r] = loss;
+            if(loss_rows) loss_rows[r] = loss;
+        }
+        if(dlogits && c < V) {
+            const float p = expf(x - lse);
+            const float g = ok ? scale * (p - (c == y ? 1.0f : 0.0f)) : 0.0f;
+            float* d = dlogits + r * ldd + c;
+            *d = accum ? *d + g : g;
+        }
+    }
+    __syncthreads();
+    const double sd = threadIdx.x < R ? (double)rows[threadIdx.x] : 0.0;
+    const float v = pk::block_sum<16>((float)sd, red);
+    if(threadIdx.x == 0) {
+        const float t = mean_scale * v;
+        out[0] = out_accum ? out[0] + t : t;
+    }
+}
+
 // ================================================================== argmax
 struct ArgBest {
     float v;
@@ -855,6 +902,27 @@ extern "C" int pk_xent_fwd_bwd_f32(int64_t R, int64_t V, const float* logits, in
                                                      scale, scale_dev, accum);
 #undef PK_XENT
     return pk::launch_status("pk_xent_fwd_bwd_f32");
+}
+
+extern "C" int pk_xent_mean_f32(int64_t R, int64_t V, const float* logits, int64_t ldz,
+                                const int32_t* labels, float* loss_rows, float* dlogits, int64_t ldd,
+                                float scale, int flags, float mean_scale, float* out,
+                                pk_stream_t stream) {
+    if(R < 0 || V < 1) return pk::fail("pk_xent_mean_f32: need R >= 0 and V >= 1");
+    if(!out) return pk::fail("pk_xent_mean_f32: NULL out");
+    if(R > 0 && R <= kTinyRows && V <= kTinyV) {
+        if(!logits || !labels) return pk::fail("pk_xent_mean_f32: NULL logits or labels");
+        if(ldz < V || (dlogits && ldd < V)) return pk::fail("pk_xent_mean_f32: row stride < V");
+        xent_tiny_kernel<<<1, 1024, 0, pk::as_stream(stream)>>>(R, V, logits, ldz, labels, loss_rows, dlogits,
+                                                                ldd, scale, nullptr, flags & PK_ACCUM,
+                                                                mean_scale, out, (flags & PK_ACCUM2) != 0);
+        return pk::launch_status("pk_xent_mean_f32");
+    }
+    if(R > 0 && !loss_rows) return pk::fail("pk_xent_mean_f32: NULL loss_rows (needed above the tiny sizes)");
+    if(int st = pk_xent_fwd_bwd_f32(R, V, logits, ldz, labels, loss_rows, dlogits, ldd, scale, nullptr,
+                                    flags & PK_ACCUM, stream))
+        return st;
+    return pk_reduce_sum_f32(R, loss_rows, mean_scale, out, (flags & PK_ACCUM2) ? PK_ACCUM : 0, stream);
 }
 
 extern "C" int pk_argmax_f32(int64_t R, int64_t V, const float* x, int64_t ldx, int32_t* idx,

@@ -81,10 +81,10 @@ struct PicoTensor* pico_softmax_xent(struct PicoTensor* logits, const int32_t* l
     n->saved[XS_LABELS] = (void*)dl;
     n->saved[XS_ROWS] = rows;
     int pre = !pkh_grad_is_live(logits);
-    int st = pk_xent_fwd_bwd_f32(R, V, logits->data, V, dl, rows, pre ? logits->grad : NULL, V,
-                                 1.0f / (float)(R > 0 ? R : 1), NULL, 0, pkh_stream());
-    if(pkh_status("pico_softmax_xent", st)) return NULL;
-    st = pk_reduce_sum_f32(R, rows, 1.0f / (float)(R > 0 ? R : 1), out->data, 0, pkh_stream());
+    /* the loss rows, their gradient and the mean (one launch for a small head) */
+    const float inv = 1.0f / (float)(R > 0 ? R : 1);
+    int st = pk_xent_mean_f32(R, V, logits->data, V, dl, rows, pre ? logits->grad : NULL, V, inv, 0, inv,
+                              out->data, pkh_stream());
     if(pkh_status("pico_softmax_xent", st)) return NULL;
     n->ival[XI_PRECOMPUTED] = pre;
     pkh_set_parents(arena, out, 1, &logits, xent_backward);

@@ -471,6 +471,20 @@ def xent_fwd_bwd(logits, labels, loss_rows=None, dlogits=None, scale=1.0, accumu
         _ptr(scale_dev), ACCUM if accumulate else 0, _stream()))
 
 
+def xent_mean(logits, labels, out, loss_rows=None, dlogits=None, scale=1.0, mean_scale=1.0,
+              accumulate=False, accumulate_out=False):
+    """xent_fwd_bwd plus out[0] (+)= mean_scale * sum(loss rows) (pk_xent_mean_f32)"""
+    R, V = logits.shape
+    if labels.dtype != torch.int32 or labels.numel() != R:
+        raise ValueError("labels must be int32 with one entry per row")
+    flags = (ACCUM if accumulate else 0) | (2 if accumulate_out else 0)
+    check("pk_xent_mean_f32", hip_lib().pk_xent_mean_f32(
+        R, V, _ptr(logits), _rowmajor(logits, "logits"), _ptr(labels), _ptr(loss_rows),
+        _ptr(dlogits), V if dlogits is None else _rowmajor(dlogits, "dlogits"), scale, flags,
+        mean_scale, _ptr(out), _stream()))
+    return out
+
+
 def argmax(x, idx):
     R, V = x.shape
     check("pk_argmax_f32", hip_lib().pk_argmax_f32(R, V, _ptr(x), _rowmajor(x, "x"), _ptr(idx),

@@ -391,6 +391,37 @@ def test_xent_golden_and_bad_labels(dev):
     assert np.isnan(r[0]) and np.isnan(r[1]) and not np.any(d[:2])
 
 
+@pytest.mark.parametrize("R,V", [(64, 10), (1, 1), (7, 37), (1024, 64), (1000, 63), (64, 16),
+                                 (1025, 10), (16, 8192)])
+def test_xent_mean_equals_rows_then_sum(dev, R, V):
+    """pk_xent_mean_f32 (one launch up to 1024 rows of 64 classes) gives the
+    rows, gradient and mean of pk_xent_fwd_bwd_f32 + pk_reduce_sum_f32 bit for
+    bit where those run the same per-row arithmetic (V not a multiple of 4, or
+    above the one-launch sizes), and within the oracle's bound otherwise"""
+    z = O.normal(R * V, R + 2 * V, 0.0, 2.0).reshape(R, V)
+    y = O.labels(R, 9, V)
+    y[0] = -1 if R > 1 else y[0]  # a bad label: NaN row, zero gradient
+    rows0, dz0, out0 = torch.empty(R, device=dev), torch.empty(R, V, device=dev), torch.empty(1, device=dev)
+    K.xent_fwd_bwd(cu(z), cu(y), rows0, dz0, scale=1.0 / R)
+    K.reduce_sum(rows0, out0, 1.0 / R)
+    rows1, dz1, out1 = torch.empty(R, device=dev), torch.empty(R, V, device=dev), torch.empty(1, device=dev)
+    K.xent_mean(cu(z), cu(y), out1, rows1, dz1, scale=1.0 / R, mean_scale=1.0 / R)
+    r0, r1, d0, d1 = host(rows0), host(rows1), host(dz0), host(dz1)
+    if V % 4 or R > 1024 or V > 64:
+        assert np.array_equal(r0, r1, equal_nan=True) and np.array_equal(d0, d1)
+        assert np.array_equal(host(out0), host(out1), equal_nan=True)
+    else:
+        ok = ~np.isnan(r0)
+        assert np.array_equal(np.isnan(r0), np.isnan(r1))
+        assert row_err(r1[ok], r0[ok]) <= TOL and max_rel(d1, d0) <= TOL
+    # accumulate: gradient and mean added onto what is there
+    K.xent_mean(cu(z), cu(y), out1, None if R <= 1024 and V <= 64 else rows1, dz1, scale=1.0 / R,
+                mean_scale=1.0 / R, accumulate=True, accumulate_out=True)
+    assert max_rel(host(dz1), 2 * d1) <= TOL
+    if R > 1:  # a NaN row makes the mean NaN
+        assert np.isnan(host(out1)[0])
+
+
 @pytest.mark.parametrize("R,V", [(6, 13), (100, 32000), (9, 7)])
 def test_argmax_bitexact(dev, R, V):
     if (R, V) == (6, 13):
