@@ -897,8 +897,9 @@ def main():
             "train": {name: train_section(name, args.variant_steps, 3, precision=2)
                       for name in args.train_configs.split(",") if name in TRAIN_CONFIGS},
             "note": "pico_set_matmul_precision(PICO_MATMUL_BF16X3): matmul products as "
-                    "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, attention "
-                    "fp32; bf16x3q: the same products over split-bf16 operands cast once and "
+                    "ahi.bhi + ahi.blo + alo.bhi in bf16, fp32 accumulation, the fused "
+                    "attention's products likewise; bf16x3q: the same products over "
+                    "split-bf16 operands cast once and "
                     "resident (pk_gemm_bf16x3q_f32); not the headline, which is fp32"}
     if "fp8" in sections:
         # e4m3 operands (clamped to +-448, nearest even), fp32 accumulation and

@@ -307,15 +307,17 @@ void pico_gpu_fail_next_workspaces(int n);
  * softmax statistics and every other op stay fp32.  Faster, and outside the
  * fp32 parity contract (relative error of order 2^-8 per operand).  An
  * attention node's backward uses the precision its forward ran in.
- * PICO_MATMUL_BF16X3: pico_matmul's products and their gradients take three
- * bf16 products per fp32 one (pk_gemm_bf16x3_f32): within about 1e-5 of
- * fp32, inside the 1e-4 parity bound; attention stays fp32.
- * PICO_MATMUL_FP8: pico_matmul's products and their gradients round both
- * operands to e4m3 (OCP FP8 E4M3, clamped to +-448, nearest even) and multiply
- * on the fp8 matrix cores, accumulating in fp32 (pk_gemm_ex_fp8_f32);
- * attention stays fp32.  Relative error of order 2^-4 per operand: far
- * outside the fp32 parity contract, for experiments.  Returns 0, or nonzero
- * for an unknown value. */
+ * PICO_MATMUL_BF16X3: pico_matmul's products, the fused attention's and
+ * their gradients take three bf16 products per fp32 one (pk_gemm_bf16x3_f32,
+ * pk_flash_attn_*_bf16x3_f32): within about 1e-5 of fp32, inside the 1e-4
+ * parity bound.
+ * PICO_MATMUL_FP8: pico_matmul's products and their gradients run on MX8
+ * operands (OCP e4m3 with a power-of-two scale per 32 values along the
+ * contraction, pk_gemm_mx8_f32; a parameter cast once per change), the fused
+ * attention on e4m3 with per-tensor power-of-two scales
+ * (pk_flash_attn_*_fp8_f32), accumulating in fp32.  Relative error of order
+ * 2^-4 per operand: far outside the fp32 parity contract, for experiments.
+ * Returns 0, or nonzero for an unknown value. */
 #define PICO_MATMUL_FP32 0
 #define PICO_MATMUL_BF16 1
 #define PICO_MATMUL_BF16X3 2

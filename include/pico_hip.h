@@ -527,6 +527,21 @@ int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int6
                                const float* o, const float* lse, const float* dout, float* dq,
                                float* dk, float* dv, void* workspace, size_t workspace_bytes,
                                int flags, pk_stream_t stream);
+/* The same fused attention with fp32 products from three bf16 ones (no
+ * reference counterpart; within the fp32 parity bound): every operand of a
+ * product -- q, k, v, dout and the probabilities and dS formed in the kernels
+ * -- as hi = bf16(x) and lo = bf16(x - hi), each product as hi.hi + hi.lo +
+ * lo.hi on the bf16 matrix cores with fp32 accumulation (lo.lo, below 2^-16 of
+ * a product, dropped); softmax statistics, exponentials and accumulators fp32.
+ * Arguments, workspace and flags as the fp32 entry points. */
+int pk_flash_attn_fwd_bf16x3_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                 float scale, const float* q, const float* k, const float* v,
+                                 float* o, float* lse, pk_stream_t stream);
+int pk_flash_attn_bwd_bf16x3_f32(int64_t B, int64_t H, int64_t T, int64_t hd, int64_t ld,
+                                 float scale, const float* q, const float* k, const float* v,
+                                 const float* o, const float* lse, const float* dout, float* dq,
+                                 float* dk, float* dv, void* workspace, size_t workspace_bytes,
+                                 int flags, pk_stream_t stream);
 /* The same fused attention with fp8 multiplies (no reference counterpart):
  * OCP e4m3 operands on the 32x32x64 scaled matrix cores, fp32 accumulation.
  * q, k, v and dout enter as e4m3(x * 2^-e) per tensor, e the smallest

@@ -133,6 +133,10 @@ PK_SIGNATURES = {
                               c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
     "pk_flash_attn_bwd_bf16_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
                                    c_p, c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
+    "pk_flash_attn_fwd_bf16x3_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
+                                     c_p, c_p],
+    "pk_flash_attn_bwd_bf16x3_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
+                                     c_p, c_p, c_p, c_p, c_p, c_p, c_size, c_int, c_p],
     "pk_flash_attn_fwd_fp8_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
                                   c_p, c_p, c_p],
     "pk_flash_attn_bwd_fp8_f32": [c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,

@@ -868,20 +868,37 @@ __device__ __forceinline__ void fetch_quad(const float* __restrict__ base, int64
     }
 }
 
+// the lo part of a split value: x - hi rounded, hi = bf16(x) (x - hi is exact
+// in fp32, so hi + lo is x to 2^-17)
+__device__ __forceinline__ __bf16 lo_part(float x, __bf16 hi) { return (__bf16)(x - (float)hi); }
+
+// SPLIT: a tile is followed (at + TILEB) by the lo parts of its values
+template <bool SPLIT = false>
 __device__ __forceinline__ void put_rows(__bf16* t, const f32x4 (&x)[4]) {
     const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
 #pragma unroll
-    for(int i = 0; i < 4; ++i)
-        *reinterpret_cast<bf16x4*>(t + (4 * rq + i) * LDB + 4 * c4) =
-            bf16x4{(__bf16)x[i][0], (__bf16)x[i][1], (__bf16)x[i][2], (__bf16)x[i][3]};
+    for(int i = 0; i < 4; ++i) {
+        const bf16x4 h = {(__bf16)x[i][0], (__bf16)x[i][1], (__bf16)x[i][2], (__bf16)x[i][3]};
+        *reinterpret_cast<bf16x4*>(t + (4 * rq + i) * LDB + 4 * c4) = h;
+        if constexpr(SPLIT)
+            *reinterpret_cast<bf16x4*>(t + TILEB + (4 * rq + i) * LDB + 4 * c4) =
+                bf16x4{lo_part(x[i][0], h[0]), lo_part(x[i][1], h[1]), lo_part(x[i][2], h[2]),
+                       lo_part(x[i][3], h[3])};
+    }
 }
 
+template <bool SPLIT = false>
 __device__ __forceinline__ void put_cols(__bf16* t, const f32x4 (&x)[4]) {
     const int rq = threadIdx.x >> 4, c4 = threadIdx.x & 15;
 #pragma unroll
-    for(int c = 0; c < 4; ++c)
-        *reinterpret_cast<bf16x4*>(t + (4 * c4 + c) * LDB + 4 * rq) =
-            bf16x4{(__bf16)x[0][c], (__bf16)x[1][c], (__bf16)x[2][c], (__bf16)x[3][c]};
+    for(int c = 0; c < 4; ++c) {
+        const bf16x4 h = {(__bf16)x[0][c], (__bf16)x[1][c], (__bf16)x[2][c], (__bf16)x[3][c]};
+        *reinterpret_cast<bf16x4*>(t + (4 * c4 + c) * LDB + 4 * rq) = h;
+        if constexpr(SPLIT)
+            *reinterpret_cast<bf16x4*>(t + TILEB + (4 * c4 + c) * LDB + 4 * rq) =
+                bf16x4{lo_part(x[0][c], h[0]), lo_part(x[1][c], h[1]), lo_part(x[2][c], h[2]),
+                       lo_part(x[3][c], h[3])};
+    }
 }
 
 // a lane's 32 head dims of one row, rounded, in the 4 MFMA steps' slots
@@ -903,14 +920,48 @@ __device__ __forceinline__ void load_frag_bf16(const float* __restrict__ row, in
     }
 }
 
+// the same fragments with their lo parts (fl) for the split products
+__device__ __forceinline__ void load_frag_split(const float* __restrict__ row, int h, bf16x8 (&f)[4],
+                                                bf16x8 (&fl)[4], float mul, bool ok) {
+    load_frag_bf16(row, h, f, mul, ok);
+#pragma unroll
+    for(int t = 0; t < 4; ++t) {
+        if(!ok) {
+            fl[t] = f[t];  // zeros
+            continue;
+        }
+        const f32x4 a = *reinterpret_cast<const f32x4*>(row + 16 * t + 8 * h);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(row + 16 * t + 8 * h + 4);
+        fl[t] = bf16x8{lo_part(a[0] * mul, f[t][0]), lo_part(a[1] * mul, f[t][1]),
+                       lo_part(a[2] * mul, f[t][2]), lo_part(a[3] * mul, f[t][3]),
+                       lo_part(b[0] * mul, f[t][4]), lo_part(b[1] * mul, f[t][5]),
+                       lo_part(b[2] * mul, f[t][6]), lo_part(b[3] * mul, f[t][7])};
+    }
+}
+
 // acc (+)= A.B over the head dims: A = row (sub*32 + lane%32) of a row-major
-// tile, B = the lane's fragments
+// tile, B = the lane's fragments.  SPLIT: hi.hi + hi.lo + lo.hi per step (bl:
+// the fragments' lo parts; the tile's at + TILEB)
+template <bool SPLIT = false>
 __device__ __forceinline__ f32x16 dot_rows16(const __bf16* t, int sub, int lq, int lh,
-                                             const bf16x8 (&bf)[4], f32x16 acc) {
+                                             const bf16x8 (&bf)[4], const bf16x8 (&bl)[SPLIT ? 4 : 1],
+                                             f32x16 acc) {
     const __bf16* row = t + (sub * 32 + lq) * LDB + 8 * lh;
 #pragma unroll
-    for(int s = 0; s < 4; ++s) acc = mfma16(*reinterpret_cast<const bf16x8*>(row + 16 * s), bf[s], acc);
+    for(int s = 0; s < 4; ++s) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(row + 16 * s);
+        acc = mfma16(a, bf[s], acc);
+        if constexpr(SPLIT) {
+            acc = mfma16(a, bl[s], acc);
+            acc = mfma16(*reinterpret_cast<const bf16x8*>(row + TILEB + 16 * s), bf[s], acc);
+        }
+    }
     return acc;
+}
+__device__ __forceinline__ f32x16 dot_rows16(const __bf16* t, int sub, int lq, int lh,
+                                             const bf16x8 (&bf)[4], f32x16 acc) {
+    const bf16x8 none[1] = {};
+    return dot_rows16<false>(t, sub, lq, lh, bf, none, acc);
 }
 
 // the accumulator rows of group g as a B operand (slot (h, j) <- register 8g + j)
@@ -921,7 +972,9 @@ __device__ __forceinline__ bf16x8 pack_group(const f32x16& x, int g) {
 }
 
 // acc (+)= X^T . W over the 32 accumulator rows of sub-block `sub`: A[i][row]
-// read from the transposed tile (row cb*32 + lane%32, the group's rows), B = w
+// read from the transposed tile (row cb*32 + lane%32, the group's rows), B = w.
+// SPLIT: w is split as it is packed, hi.hi + hi.lo + lo.hi per group
+template <bool SPLIT = false>
 __device__ __forceinline__ f32x16 dot_cols16(const __bf16* t, int sub, int cb, int lq, int lh,
                                              const f32x16& w, f32x16 acc) {
     const __bf16* row = t + (cb * 32 + lq) * LDB + sub * 32 + 4 * lh;
@@ -930,15 +983,31 @@ __device__ __forceinline__ f32x16 dot_cols16(const __bf16* t, int sub, int cb, i
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 16 * g);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 * g + 8);
         const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc = mfma16(a, pack_group(w, g), acc);
+        const bf16x8 wh = pack_group(w, g);
+        acc = mfma16(a, wh, acc);
+        if constexpr(SPLIT) {
+            bf16x8 wl;
+#pragma unroll
+            for(int j = 0; j < 8; ++j) wl[j] = lo_part(w[8 * g + j], wh[j]);
+            acc = mfma16(a, wl, acc);
+            const bf16x4 lo2 = *reinterpret_cast<const bf16x4*>(row + TILEB + 16 * g);
+            const bf16x4 hi2 = *reinterpret_cast<const bf16x4*>(row + TILEB + 16 * g + 8);
+            const bf16x8 al = {lo2[0], lo2[1], lo2[2], lo2[3], hi2[0], hi2[1], hi2[2], hi2[3]};
+            acc = mfma16(al, wh, acc);
+        }
     }
     return acc;
 }
 
 // ------------------------------------------------------------- bf16 forward
+// SPLIT (the split-bf16 products): every operand as hi and lo bf16 parts
+// (tiles of lo parts after the hi tiles, fragments ql), each product as
+// hi.hi + hi.lo + lo.hi
+template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 sVt[2][TILEB];  // [d][key]
+    constexpr int NS = SPLIT ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) __bf16 sK[2][NS * TILEB];   // [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sVt[2][NS * TILEB];  // [d][key]
     const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
@@ -948,16 +1017,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
-    bf16x8 qf[4];
-    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
+    bf16x8 qf[4], ql[SPLIT ? 4 : 1];
+    if constexpr(SPLIT) load_frag_split(Q + qi * p.ld, lh, qf, ql, p.scale * kLog2e, qi < p.T);
+    else load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
     f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY, lsum = 0.0f;
     const int nkv = (int)((qb * ROWS + ROWS) / BLK);
     f32x4 rk[4], rv[4];
     fetch_quad(K, p.ld, 0, rk, p.T);
     fetch_quad(V, p.ld, 0, rv, p.T);
-    put_rows(sK[0], rk);
-    put_cols(sVt[0], rv);
+    put_rows<SPLIT>(sK[0], rk);
+    put_cols<SPLIT>(sVt[0], rv);
     for(int j = 0; j < nkv; ++j) {
         const int st = j & 1;
         __syncthreads();
@@ -968,8 +1038,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
         }
         const int64_t kv0 = (int64_t)j * BLK;
         if(kv0 <= q0 + 31) {
-            f32x16 s[2] = {dot_rows16(sK[st], 0, lq, lh, qf, zero16()),
-                           dot_rows16(sK[st], 1, lq, lh, qf, zero16())};
+            f32x16 s[2] = {dot_rows16<SPLIT>(sK[st], 0, lq, lh, qf, ql, zero16()),
+                           dot_rows16<SPLIT>(sK[st], 1, lq, lh, qf, ql, zero16())};
             if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
                 const int lim = (int)(qi - kv0) - 4 * lh;
 #pragma unroll
@@ -1002,13 +1072,13 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
             }
 #pragma unroll
             for(int cb = 0; cb < 2; ++cb) {
-                o[cb] = dot_cols16(sVt[st], 0, cb, lq, lh, s[0], o[cb]);
-                o[cb] = dot_cols16(sVt[st], 1, cb, lq, lh, s[1], o[cb]);
+                o[cb] = dot_cols16<SPLIT>(sVt[st], 0, cb, lq, lh, s[0], o[cb]);
+                o[cb] = dot_cols16<SPLIT>(sVt[st], 1, cb, lq, lh, s[1], o[cb]);
             }
         }
         if(more) {
-            put_rows(sK[st ^ 1], rk);
-            put_cols(sVt[st ^ 1], rv);
+            put_rows<SPLIT>(sK[st ^ 1], rk);
+            put_cols<SPLIT>(sVt[st ^ 1], rv);
         }
     }
     if(qi >= p.T) return;  // a padding row of the last block
@@ -1017,11 +1087,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(FlashParams p) {
 }
 
 // ------------------------------------------------------- bf16 backward: dK, dV
-__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sQ[2][TILEB];   // [q][d]
-    __shared__ __attribute__((aligned(16))) __bf16 sQt[2][TILEB];  // [d][q]
-    __shared__ __attribute__((aligned(16))) __bf16 sO[2][TILEB];   // dO [q][d]
-    __shared__ __attribute__((aligned(16))) __bf16 sOt[2][TILEB];  // dO [d][q]
+// SPLIT: as in the forward; the tiles then take one workgroup a CU
+template <bool SPLIT>
+__global__ __launch_bounds__(256, SPLIT ? 1 : 2) void flash_bwd_dkdv_bf16(FlashParams p) {
+    constexpr int NS = SPLIT ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) __bf16 sQ[2][NS * TILEB];   // [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sQt[2][NS * TILEB];  // [d][q]
+    __shared__ __attribute__((aligned(16))) __bf16 sO[2][NS * TILEB];   // dO [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sOt[2][NS * TILEB];  // dO [d][q]
     __shared__ float sLD[2][2 * BLK];                              // L2, then D
     const int64_t BH = p.B * p.H;
     const int64_t kb = (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
@@ -1033,9 +1106,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t k0 = kb * ROWS + w * 32, ki = k0 + lq;
 
-    bf16x8 kf[4], vf[4];
-    load_frag_bf16(K + ki * p.ld, lh, kf, p.scale * kLog2e, ki < p.T);
-    load_frag_bf16(V + ki * p.ld, lh, vf, 1.0f, ki < p.T);
+    bf16x8 kf[4], vf[4], kl[SPLIT ? 4 : 1], vl[SPLIT ? 4 : 1];
+    if constexpr(SPLIT) {
+        load_frag_split(K + ki * p.ld, lh, kf, kl, p.scale * kLog2e, ki < p.T);
+        load_frag_split(V + ki * p.ld, lh, vf, vl, 1.0f, ki < p.T);
+    } else {
+        load_frag_bf16(K + ki * p.ld, lh, kf, p.scale * kLog2e, ki < p.T);
+        load_frag_bf16(V + ki * p.ld, lh, vf, 1.0f, ki < p.T);
+    }
     f32x16 dv[2] = {zero16(), zero16()}, dk[2] = {zero16(), zero16()};
 
     const int j0 = (int)(kb * ROWS / BLK), nq = (int)(p.Tp / BLK);
@@ -1047,10 +1125,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
         if(threadIdx.x < 2 * BLK) rc = cst[(int64_t)j * 2 * BLK + threadIdx.x];
     };
     auto put = [&](int st) {
-        put_rows(sQ[st], rq);
-        put_cols(sQt[st], rq);
-        put_rows(sO[st], ro);
-        put_cols(sOt[st], ro);
+        put_rows<SPLIT>(sQ[st], rq);
+        put_cols<SPLIT>(sQt[st], rq);
+        put_rows<SPLIT>(sO[st], ro);
+        put_cols<SPLIT>(sOt[st], ro);
         if(threadIdx.x < 2 * BLK) sLD[st][threadIdx.x] = rc;
     };
     fetch(j0);
@@ -1068,8 +1146,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
                 if(qs + sub * 32 + 31 < k0) continue;  // all of P would be zeros
-                f32x16 sc = dot_rows16(sQ[st], sub, lq, lh, kf, zero16());
-                f32x16 dp = dot_rows16(sO[st], sub, lq, lh, vf, zero16());
+                f32x16 sc = dot_rows16<SPLIT>(sQ[st], sub, lq, lh, kf, kl, zero16());
+                f32x16 dp = dot_rows16<SPLIT>(sO[st], sub, lq, lh, vf, vl, zero16());
 #pragma unroll
                 for(int r = 0; r < 16; ++r) {
                     const int qr = sub * 32 + acc_row(r, lh);
@@ -1087,8 +1165,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
                 }
 #pragma unroll
                 for(int cb = 0; cb < 2; ++cb) {
-                    dv[cb] = dot_cols16(sOt[st], sub, cb, lq, lh, sc, dv[cb]);
-                    dk[cb] = dot_cols16(sQt[st], sub, cb, lq, lh, dp, dk[cb]);
+                    dv[cb] = dot_cols16<SPLIT>(sOt[st], sub, cb, lq, lh, sc, dv[cb]);
+                    dk[cb] = dot_cols16<SPLIT>(sQt[st], sub, cb, lq, lh, dp, dk[cb]);
                 }
             }
         }
@@ -1100,10 +1178,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_bf16(FlashParams p) {
 }
 
 // ----------------------------------------------------------- bf16 backward: dQ
-__global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sK[2][TILEB];   // [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 sKt[2][TILEB];  // [d][key]
-    __shared__ __attribute__((aligned(16))) __bf16 sV[2][TILEB];   // [key][d]
+template <bool SPLIT>
+__global__ __launch_bounds__(256, SPLIT ? 1 : 2) void flash_bwd_dq_bf16(FlashParams p) {
+    constexpr int NS = SPLIT ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) __bf16 sK[2][NS * TILEB];   // [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 sKt[2][NS * TILEB];  // [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 sV[2][NS * TILEB];   // [key][d]
     const int64_t BH = p.B * p.H, nqb = p.Tp / ROWS;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / BH, bh = (int64_t)blockIdx.x % BH;
     const int64_t b = bh / p.H, h = bh % p.H;
@@ -1113,9 +1193,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     const int l = threadIdx.x & 63, lq = l & 31, lh = l >> 5;
     const int64_t q0 = qb * ROWS + w * 32, qi = q0 + lq;
 
-    bf16x8 qf[4], of[4];
-    load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
-    load_frag_bf16(dO + qi * p.D, lh, of, 1.0f, qi < p.T);
+    bf16x8 qf[4], of[4], ql[SPLIT ? 4 : 1], ol[SPLIT ? 4 : 1];
+    if constexpr(SPLIT) {
+        load_frag_split(Q + qi * p.ld, lh, qf, ql, p.scale * kLog2e, qi < p.T);
+        load_frag_split(dO + qi * p.D, lh, of, ol, 1.0f, qi < p.T);
+    } else {
+        load_frag_bf16(Q + qi * p.ld, lh, qf, p.scale * kLog2e, qi < p.T);
+        load_frag_bf16(dO + qi * p.D, lh, of, 1.0f, qi < p.T);
+    }
     const float* cst = p.dsum + bh * 2 * p.Tp + (qi / BLK) * 2 * BLK + qi % BLK;
     const float l2 = cst[0], dd = cst[BLK];
     f32x16 dq[2] = {zero16(), zero16()};
@@ -1124,9 +1209,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
     f32x4 rk[4], rv[4];
     fetch_quad(K, p.ld, 0, rk, p.T);
     fetch_quad(V, p.ld, 0, rv, p.T);
-    put_rows(sK[0], rk);
-    put_cols(sKt[0], rk);
-    put_rows(sV[0], rv);
+    put_rows<SPLIT>(sK[0], rk);
+    put_cols<SPLIT>(sKt[0], rk);
+    put_rows<SPLIT>(sV[0], rv);
     for(int j = 0; j < nkv; ++j) {
         const int st = j & 1;
         __syncthreads();
@@ -1140,8 +1225,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
             const int lim = (int)(qi - kv0) - 4 * lh;
 #pragma unroll
             for(int sub = 0; sub < 2; ++sub) {
-                f32x16 sc = dot_rows16(sK[st], sub, lq, lh, qf, zero16());
-                f32x16 dp = dot_rows16(sV[st], sub, lq, lh, of, zero16());
+                f32x16 sc = dot_rows16<SPLIT>(sK[st], sub, lq, lh, qf, ql, zero16());
+                f32x16 dp = dot_rows16<SPLIT>(sV[st], sub, lq, lh, of, ol, zero16());
 #pragma unroll
                 for(int r = 0; r < 16; ++r) sc[r] = __builtin_amdgcn_exp2f(sc[r] - l2);
                 if(kv0 + BLK - 1 > q0) {  // the block crosses this wave's diagonal
@@ -1152,13 +1237,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_bf16(FlashParams p) {
 #pragma unroll
                 for(int r = 0; r < 16; ++r) dp[r] = sc[r] * (dp[r] - dd);
 #pragma unroll
-                for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols16(sKt[st], sub, cb, lq, lh, dp, dq[cb]);
+                for(int cb = 0; cb < 2; ++cb) dq[cb] = dot_cols16<SPLIT>(sKt[st], sub, cb, lq, lh, dp, dq[cb]);
             }
         }
         if(more) {
-            put_rows(sK[st ^ 1], rk);
-            put_cols(sKt[st ^ 1], rk);
-            put_rows(sV[st ^ 1], rv);
+            put_rows<SPLIT>(sK[st ^ 1], rk);
+            put_cols<SPLIT>(sKt[st ^ 1], rk);
+            put_rows<SPLIT>(sV[st ^ 1], rv);
         }
     }
     if(qi >= p.T) return;  // a padding row of the last block
@@ -1694,8 +1779,9 @@ const FlashPlan& flash_plan(int64_t BH, int64_t nqb, int slots) {
     return plan;
 }
 
-// products of a launch: fp32, bf16 or fp8 (e4m3)
-enum FlashPrec { kF32 = 0, kBF16 = 1, kFP8 = 2 };
+// products of a launch: fp32, bf16, fp8 (e4m3) or split bf16 (three bf16
+// products per fp32 one)
+enum FlashPrec { kF32 = 0, kBF16 = 1, kFP8 = 2, kBF16X3 = 3 };
 
 // fp8: max|.| of q, k, v (first = 0, the forward) or of dout (first = 3, the
 // backward) into amax[first..]
@@ -1735,7 +1821,9 @@ int flash_fwd_launch(const char* who, int prec, int64_t B, int64_t H, int64_t T,
         p.amax = amax;
         flash_fwd_fp8<<<grid, 256, 0, st>>>(p);
     } else if(prec == kBF16) {
-        flash_fwd_bf16<<<grid, 256, 0, st>>>(p);
+        flash_fwd_bf16<false><<<grid, 256, 0, st>>>(p);
+    } else if(prec == kBF16X3) {
+        flash_fwd_bf16<true><<<grid, 256, 0, st>>>(p);
     } else {
         flash_fwd<<<grid, 256, 0, st>>>(p, flash_plan(B * H, p.Tp / ROWS, kFwdSlots));
     }
@@ -1756,6 +1844,14 @@ extern "C" int pk_flash_attn_fwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64
                                           const float* v, float* o, float* lse,
                                           pk_stream_t stream) {
     return flash_fwd_launch("pk_flash_attn_fwd_bf16_f32", kBF16, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, nullptr, stream);
+}
+
+extern "C" int pk_flash_attn_fwd_bf16x3_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
+                                            int64_t ld, float scale, const float* q, const float* k,
+                                            const float* v, float* o, float* lse,
+                                            pk_stream_t stream) {
+    return flash_fwd_launch("pk_flash_attn_fwd_bf16x3_f32", kBF16X3, B, H, T, hd, ld, scale, q, k, v,
                             o, lse, nullptr, stream);
 }
 
@@ -1838,14 +1934,18 @@ int flash_bwd_launch(const char* who, int prec, int64_t B, int64_t H, int64_t T,
     if(prec == kFP8)
         flash_bwd_dkdv_fp8<<<grid, 256, 0, st>>>(p);
     else if(prec == kBF16)
-        flash_bwd_dkdv_bf16<<<grid, 256, 0, st>>>(p);
+        flash_bwd_dkdv_bf16<false><<<grid, 256, 0, st>>>(p);
+    else if(prec == kBF16X3)
+        flash_bwd_dkdv_bf16<true><<<grid, 256, 0, st>>>(p);
     else
         flash_bwd_dkdv<<<grid, 256, 0, st>>>(p);
     if((rc = pk::launch_status(who))) return rc;
     if(prec == kFP8)
         flash_bwd_dq_fp8<<<grid, 256, 0, st>>>(p);
     else if(prec == kBF16)
-        flash_bwd_dq_bf16<<<grid, 256, 0, st>>>(p);
+        flash_bwd_dq_bf16<false><<<grid, 256, 0, st>>>(p);
+    else if(prec == kBF16X3)
+        flash_bwd_dq_bf16<true><<<grid, 256, 0, st>>>(p);
     else if(recompute)
         flash_bwd_dq_recompute<<<grid, 256, 0, st>>>(p);
     else
@@ -1871,6 +1971,17 @@ extern "C" int pk_flash_attn_bwd_bf16_f32(int64_t B, int64_t H, int64_t T, int64
                                           void* workspace, size_t workspace_bytes, int flags,
                                           pk_stream_t stream) {
     return flash_bwd_launch("pk_flash_attn_bwd_bf16_f32", kBF16, B, H, T, hd, ld, scale, q, k, v,
+                            o, lse, dout, dq, dk, dv, nullptr, workspace, workspace_bytes, flags,
+                            stream);
+}
+
+extern "C" int pk_flash_attn_bwd_bf16x3_f32(int64_t B, int64_t H, int64_t T, int64_t hd,
+                                            int64_t ld, float scale, const float* q, const float* k,
+                                            const float* v, const float* o, const float* lse,
+                                            const float* dout, float* dq, float* dk, float* dv,
+                                            void* workspace, size_t workspace_bytes, int flags,
+                                            pk_stream_t stream) {
+    return flash_bwd_launch("pk_flash_attn_bwd_bf16x3_f32", kBF16X3, B, H, T, hd, ld, scale, q, k, v,
                             o, lse, dout, dq, dk, dv, nullptr, workspace, workspace_bytes, flags,
                             stream);
 }

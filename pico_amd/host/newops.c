@@ -281,7 +281,7 @@ static size_t attn_ds_cap(void) {
 /* AI_PREC: the products' precision, 0 fp32, 1 bf16, 2 fp8 (flash only); an
  * fp8 node keeps max|q|, max|k|, max|v| for the backward in saved[AS_P] */
 enum { AI_B = 0, AI_H = 1, AI_FLASH = 2, AI_PREC = 3 };
-enum { ATTN_F32 = 0, ATTN_BF16 = 1, ATTN_FP8 = 2 };
+enum { ATTN_F32 = 0, ATTN_BF16 = 1, ATTN_FP8 = 2, ATTN_BF16X3 = 3 };
 
 static void attn_backward(struct PicoTensor* self) {
     struct PkNode* n = pkh_node(self);
@@ -320,7 +320,9 @@ static void attn_backward(struct PicoTensor* self) {
                                        k->grad, v->grad, (float*)n->saved[AS_P], ws, ws_bytes,
                                        flags, pkh_stream());
     else if(flash)
-        st = (prec == ATTN_BF16 ? pk_flash_attn_bwd_bf16_f32 : pk_flash_attn_bwd_f32)(
+        st = (prec == ATTN_BF16     ? pk_flash_attn_bwd_bf16_f32
+              : prec == ATTN_BF16X3 ? pk_flash_attn_bwd_bf16x3_f32
+                                    : pk_flash_attn_bwd_f32)(
             B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, self->data,
             (const float*)n->saved[AS_LSE], dout, q->grad, k->grad, v->grad, ws, ws_bytes, flags,
             pkh_stream());
@@ -360,9 +362,11 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
     /* the matmul precision switch covers attention's products too; the
      * backward uses the precision the forward ran in */
     const int mp = pico_get_matmul_precision();
-    const int prec = !flash ? ATTN_F32
-                            : mp == PICO_MATMUL_FP8 ? ATTN_FP8
-                                                    : mp == PICO_MATMUL_BF16 ? ATTN_BF16 : ATTN_F32;
+    const int prec = !flash                     ? ATTN_F32
+                     : mp == PICO_MATMUL_FP8    ? ATTN_FP8
+                     : mp == PICO_MATMUL_BF16   ? ATTN_BF16
+                     : mp == PICO_MATMUL_BF16X3 ? ATTN_BF16X3
+                                                : ATTN_F32;
     float* lse = (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T));
     /* P for the unfused chain; fp8's max|q|, max|k|, max|v|, max|dout| */
     float* P = !flash ? (float*)arena_alloc_device(arena, sizeof(float) * (size_t)(B * H * T * T))
@@ -381,7 +385,9 @@ struct PicoTensor* pico_attention_causal(struct PicoTensor* q, struct PicoTensor
         st = pk_flash_attn_fwd_fp8_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,
                                        out->data, lse, P, pkh_stream());
     else if(flash)
-        st = (prec == ATTN_BF16 ? pk_flash_attn_fwd_bf16_f32 : pk_flash_attn_fwd_f32)(
+        st = (prec == ATTN_BF16     ? pk_flash_attn_fwd_bf16_f32
+              : prec == ATTN_BF16X3 ? pk_flash_attn_fwd_bf16x3_f32
+                                    : pk_flash_attn_fwd_f32)(
             B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data, out->data, lse, pkh_stream());
     else
         st = pk_attn_causal_fwd_f32(B, H, T, hd, ld, n->fval[0], q->data, k->data, v->data,

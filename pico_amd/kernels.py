@@ -594,11 +594,12 @@ def flash_supported(T, hd):
     return bool(hip_lib().pk_flash_attn_supported(T, hd))
 
 
-def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False, fp8_amax=None):
+def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False, fp8_amax=None, bf16x3=False):
     """Fused causal attention; bf16=True rounds the matrix-product operands to
-    bf16 (pk_flash_attn_fwd_bf16_f32); fp8_amax (4 float32 on the device)
-    runs the e4m3 products (pk_flash_attn_fwd_fp8_f32) and receives max|q|,
-    max|k|, max|v| for the backward."""
+    bf16 (pk_flash_attn_fwd_bf16_f32); bf16x3=True takes each product as three
+    bf16 ones of split operands (pk_flash_attn_fwd_bf16x3_f32); fp8_amax (4
+    float32 on the device) runs the e4m3 products (pk_flash_attn_fwd_fp8_f32)
+    and receives max|q|, max|k|, max|v| for the backward."""
     T, hd, ld = _attn_layout(B, H, q, k, v, o)
     if lse.numel() < B * H * T:
         raise ValueError("attention shape mismatch")
@@ -609,7 +610,8 @@ def flash_fwd(B, H, q, k, v, o, lse, scale=None, bf16=False, fp8_amax=None):
             B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
             _ptr(fp8_amax), _stream()))
         return
-    name = "pk_flash_attn_fwd_bf16_f32" if bf16 else "pk_flash_attn_fwd_f32"
+    name = ("pk_flash_attn_fwd_bf16x3_f32" if bf16x3 else
+            "pk_flash_attn_fwd_bf16_f32" if bf16 else "pk_flash_attn_fwd_f32")
     check(name, getattr(hip_lib(), name)(
         B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _stream()))
 
@@ -618,7 +620,7 @@ FLASH_RECOMPUTE = 16
 
 
 def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16=False,
-              recompute=False, fp8_amax=None):
+              recompute=False, fp8_amax=None, bf16x3=False):
     """recompute: PK_FLASH_RECOMPUTE, dQ from recomputed scores (a workspace of
     the row constants only); fp8_amax: the e4m3 products, with the amax the
     forward filled (pk_flash_attn_bwd_fp8_f32)"""
@@ -639,7 +641,8 @@ def flash_bwd(B, H, q, k, v, o, lse, dout, dq, dk, dv, flags=0, scale=None, bf16
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(fp8_amax), _ptr(ws), ws.numel() * 4, flags,
             _stream()))
         return
-    name = "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32"
+    name = ("pk_flash_attn_bwd_bf16x3_f32" if bf16x3 else
+            "pk_flash_attn_bwd_bf16_f32" if bf16 else "pk_flash_attn_bwd_f32")
     check(name, getattr(hip_lib(), name)(
         B, H, T, hd, ld, scale, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(dout),
         _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() * 4, flags, _stream()))
