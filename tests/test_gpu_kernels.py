@@ -422,6 +422,27 @@ def test_xent_mean_equals_rows_then_sum(dev, R, V):
         assert np.isnan(host(out1)[0])
 
 
+def test_xent_mean_refusals(dev):
+    from pico_amd import _lib
+
+    L = _lib.hip_lib()
+    z = torch.zeros(2000, 10, device=dev)
+    y = torch.zeros(2000, dtype=torch.int32, device=dev)
+    out = torch.zeros(1, device=dev)
+    # no out; rows above the one-launch sizes need loss_rows; a row stride below V
+    assert L.pk_xent_mean_f32(64, 10, z.data_ptr(), 10, y.data_ptr(), None, None, 10, 1.0, 0, 1.0,
+                              None, None) != 0
+    assert L.pk_xent_mean_f32(2000, 10, z.data_ptr(), 10, y.data_ptr(), None, None, 10, 1.0, 0, 1.0,
+                              out.data_ptr(), None) != 0
+    assert L.pk_xent_mean_f32(64, 10, z.data_ptr(), 9, y.data_ptr(), None, None, 10, 1.0, 0, 1.0,
+                              out.data_ptr(), None) != 0
+    # R = 0: the mean of nothing is 0
+    out.fill_(5.0)
+    assert L.pk_xent_mean_f32(0, 10, z.data_ptr(), 10, y.data_ptr(), None, None, 10, 1.0, 0, 1.0,
+                              out.data_ptr(), None) == 0
+    assert host(out)[0] == 0.0
+
+
 @pytest.mark.parametrize("R,V", [(6, 13), (100, 32000), (9, 7)])
 def test_argmax_bitexact(dev, R, V):
     if (R, V) == (6, 13):
